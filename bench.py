@@ -1,0 +1,177 @@
+"""Benchmark of the MoE expert-FFN decode path on one MI355X.
+
+    python bench.py [--config 1] [--steps K] [--warmup W] [--gpus 1]
+
+A step is one decode token through the workload's MoE layers with all
+inputs resident in HBM.  Workloads (synthetic data):
+  0  gpt-oss-20b single MoE layer (rotating 8 distinct layer copies so the
+     256 MB Infinity Cache cannot hold the active experts)
+  1  gpt-oss-20b 24-layer MoE stack, Zipf(1.1) router bias   (default)
+  2  gpt-oss-120b 36-layer stack, 128 experts, Zipf(1.1)
+Prints one JSON line: value = expert-weight GB/s (algorithmic bytes of the
+active experts + biases + router per token / time), plus tok/s, the roofline
+of the dominant kernel (gate/up) and the CPU baseline (the oracle on the
+host's cores over a bounded sample of the same workload).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "expert-weight GB/s (% HBM peak) + MoE-layer tok/s, gpt-oss-20b shape, 1 GPU"
+HBM_PEAK_GBS = 8000.0
+
+CONFIGS = {
+    0: dict(name="config0: gpt-oss-20b single MoE layer, decode batch 1 (8 rotating layer copies)",
+            d=2880, dff=2880, ne=32, k=4, layers=8, per_step=1, zipf=None, norm=False),
+    1: dict(name="config1: gpt-oss-20b 24-layer MoE stack (attention omitted), decode batch 1, Zipf(1.1) router bias",
+            d=2880, dff=2880, ne=32, k=4, layers=24, per_step=24, zipf=1.1, norm=True),
+    2: dict(name="config2: gpt-oss-120b 36-layer MoE stack, 128 experts, decode batch 1, Zipf(1.1) router bias",
+            d=2880, dff=2880, ne=128, k=4, layers=36, per_step=36, zipf=1.1, norm=True),
+}
+
+
+def layer_bytes(c) -> dict:
+    """Algorithmic bytes one token reads per layer (active experts only)."""
+    d, dff, ne, k = c["d"], c["dff"], c["ne"], c["k"]
+    gu = k * 2 * dff * (d // 32 * 17) + k * 2 * dff * 4
+    dn = k * d * (dff // 32 * 17) + k * d * 4
+    router = ne * d * 4 + ne * 4 + (d * 4 if c["norm"] else 0)
+    return {"gate_up": gu, "down": dn, "router": router, "total": gu + dn + router}
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(host_layers, c, budget_s: float) -> dict:
+    """Oracle (C restatement of the reference path, OpenMP over rows) on the
+    host's cores, over the first layers of the same workload."""
+    import numpy as np
+    from oracle import oracle as O
+    from cpubrrr_amd import synth
+
+    threads = min(16, os.cpu_count() or 1)
+    O.set_threads(threads)
+    x = synth.token(c["d"], 0, 12345)
+    n = 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < budget_s or n == 0:
+        L = host_layers[n % len(host_layers)]
+        x, _ = O.gptoss_moe(L, x, c["norm"])
+        n += 1
+    dt = time.perf_counter() - t0
+    per_layer = dt / n
+    lb = layer_bytes(c)["total"]
+    return {"value": round(1.0 / (per_layer * c["per_step"]), 3), "unit": "tok/s", "cores": threads,
+            "kind": "port", "sample": f"{n} MoE layers ({len(host_layers)} distinct) of the same workload in "
+                                       f"{dt:.1f} s; {per_layer * 1e3:.2f} ms/layer, "
+                                       f"{lb / per_layer / 1e9:.2f} GB/s algorithmic",
+            "ms_per_layer": round(per_layer * 1e3, 3)}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", type=int, default=1, choices=sorted(CONFIGS))
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
+              "run with --gpus 1", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    from cpubrrr_amd import MoeBlock, MoeConfig, synth
+
+    c = CONFIGS[args.config]
+    d, dff, ne, k, nl = c["d"], c["dff"], c["ne"], c["k"], c["layers"]
+    cfg = MoeConfig.gptoss(d=d, n_expert=ne, top_k=k, d_ff=dff, n_layer=nl)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(0)
+    blk = MoeBlock(cfg, device=0)
+    host_keep = []
+    t0 = time.perf_counter()
+    for l in range(nl):
+        L = synth.gptoss_layer(d, dff, ne, k, seed=0, layer=l, zipf=c["zipf"])
+        blk.load_layer(l, L)
+        if l < 2:
+            host_keep.append(L)
+        del L
+    log(f"loaded {nl} layers in {time.perf_counter() - t0:.1f} s "
+        f"({MoeBlock.layer_bytes(cfg) * nl / 1e9:.2f} GB of expert weights in HBM)")
+
+    stream = torch.cuda.current_stream()
+    blk.set_stream(stream.cuda_stream)
+    x = torch.from_numpy(synth.token(d, 0, 0)).to(dev)
+
+    def step(i):
+        if c["per_step"] == nl:
+            blk.forward_device(0, nl, x.data_ptr(), 1, c["norm"])
+        else:
+            blk.forward_device(i % nl, 1, x.data_ptr(), 1, c["norm"])
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(args.steps):
+        step(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    assert torch.isfinite(x).all().item()
+
+    # per-kernel durations over the same steps (HIP events on the launch stream)
+    blk.timing(True)
+    for i in range(args.steps):
+        step(i)
+    kt = blk.kernel_times()
+    blk.timing(False)
+
+    lb = layer_bytes(c)
+    bytes_tok = lb["total"] * c["per_step"]
+    gbs = bytes_tok / (ms * 1e-3) / 1e9
+    tok_s = 1e3 / ms
+    gu_ms, gu_n = kt["gate_up"]
+    gu_avg_us = gu_ms / max(gu_n, 1) * 1e3
+    dn_ms, dn_n = kt["down"]
+    rt_ms, rt_n = kt["route"]
+    gu_ach = lb["gate_up"] / (gu_avg_us * 1e-6) / 1e9
+    out = {
+        "metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+        "config": {"workload": c["name"], "layers_per_step": c["per_step"], "d": d, "d_ff": dff,
+                   "n_expert": ne, "top_k": k, "batch": 1, "weights": "MXFP4 (GGUF type 39)"},
+        "tok_per_s": round(tok_s, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+        "bytes_per_token": bytes_tok,
+        "kernels_us": {"route": round(rt_ms / max(rt_n, 1) * 1e3, 2), "gate_up": round(gu_avg_us, 2),
+                       "down": round(dn_ms / max(dn_n, 1) * 1e3, 2)},
+        "roofline": {"bound": "hbm", "kernel": "k_gateup_mx", "achieved": round(gu_ach, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gu_ach / HBM_PEAK_GBS, 4), "traffic": None,
+                     "bytes_per_launch": lb["gate_up"]},
+    }
+    if not args.no_cpu:
+        log("timing the CPU baseline ...")
+        out["cpu_baseline"] = cpu_baseline(host_keep, c, args.cpu_seconds)
+    blk.close()
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

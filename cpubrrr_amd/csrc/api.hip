@@ -1,0 +1,477 @@
+// api.hip -- host side of the C ABI in include/cpb_moe.h.
+//
+// Owns device memory and the stream, re-lays out expert weights at load
+// time, and sequences the per-token kernels:
+//   route (rmsnorm + quant + router + top-k)  ->  gate/up (+SwiGLU + Q8 of h)
+//   ->  down (+bias + weighted combine into x).
+// Reference caller being replaced: the MoE block of forward_worker,
+// engine_gpt2.rs:845-923 (and engine_qwen2.rs:395-433).
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "cpb_moe.h"
+#include "moe_kq.h"
+#include "moe_mx.h"
+#include "route.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+#define HIP_OK(expr)                                                                   \
+    do {                                                                               \
+        hipError_t e_ = (expr);                                                        \
+        if (e_ != hipSuccess)                                                          \
+            return fail(e_ == hipErrorOutOfMemory ? CPB_ENOMEM : CPB_ENODEV, "%s: %s", \
+                        #expr, hipGetErrorString(e_));                                 \
+    } while (0)
+
+struct LayerDev {
+    cpb::u32x4* gu = nullptr;   // gate+up stream (MXFP4) or gate rows (k-quant)
+    cpb::u32x4* up = nullptr;   // k-quant up rows
+    cpb::u32x4* dn = nullptr;   // down stream
+    float *gate_b = nullptr, *up_b = nullptr, *down_b = nullptr;
+    float *router_w = nullptr, *router_b = nullptr, *norm_w = nullptr;
+    bool loaded = false;
+};
+
+}  // namespace
+
+struct cpb_moe {
+    cpb_moe_cfg cfg{};
+    int device = 0;
+    hipStream_t own = nullptr, stream = nullptr;
+    std::vector<LayerDev> layers;
+    int nb = 0, nbf = 0, parts_gu = 0, parts_dn = 0;
+    bool mx = true;
+    // activations / routing (device)
+    float* x = nullptr;
+    float* xn = nullptr;
+    int8_t *xq = nullptr, *xqn = nullptr;
+    float* xsb = nullptr;
+    int32_t* xsum = nullptr;
+    double *lstar = nullptr, *lbound = nullptr;
+    unsigned* counter = nullptr;
+    float* logits = nullptr;
+    int32_t* ids = nullptr;
+    float* wts = nullptr;
+    int32_t* fallback = nullptr;
+    int8_t *hq = nullptr, *hqn = nullptr;
+    float* hsb = nullptr;
+    int32_t* hsum = nullptr;
+    float* hbuf = nullptr;
+    // trace (device, lazily allocated)
+    float *t_gu = nullptr, *t_h = nullptr, *t_dn = nullptr;
+    int32_t *t_gu_sums = nullptr, *t_dn_sums = nullptr;
+    // staging for raw GGUF bytes at load time
+    uint8_t* staging = nullptr;
+    size_t staging_size = 0;
+    // timing
+    bool timing = false;
+    std::vector<hipEvent_t> ev_pool;
+    std::vector<std::pair<int, std::pair<hipEvent_t, hipEvent_t>>> ev_used;
+    double ms[3] = {0, 0, 0};
+    long nl[3] = {0, 0, 0};
+};
+
+namespace {
+
+template <class T>
+int dmalloc(T** p, size_t n) {
+    if (n == 0) n = 1;
+    hipError_t e = hipMalloc((void**)p, n * sizeof(T));
+    if (e != hipSuccess) return fail(CPB_ENOMEM, "hipMalloc(%zu bytes): %s", n * sizeof(T), hipGetErrorString(e));
+    return 0;
+}
+
+int check_cfg(const cpb_moe_cfg* c) {
+    if (!c) return fail(CPB_EINVAL, "cfg is NULL");
+    if (c->d <= 0 || c->d_ff <= 0 || c->n_expert <= 0 || c->n_layer <= 0 || c->max_tokens <= 0)
+        return fail(CPB_EINVAL, "non-positive shape in cfg");
+    if (c->top_k < 1 || c->top_k > 8 || c->top_k > c->n_expert)
+        return fail(CPB_EINVAL, "top_k=%d must be in [1, min(8, n_expert)]", c->top_k);
+    if (c->n_expert > 256) return fail(CPB_EINVAL, "n_expert=%d > 256 not supported", c->n_expert);
+    if (c->d < 3 * c->n_expert) return fail(CPB_EINVAL, "d=%d must be >= 3*n_expert", c->d);
+    bool mx = c->wtype_gate_up == CPB_GGUF_MXFP4;
+    if (mx) {
+        if (c->wtype_down != CPB_GGUF_MXFP4) return fail(CPB_EINVAL, "MXFP4 gate/up requires MXFP4 down");
+        if (c->d % 32 || c->d_ff % 32) return fail(CPB_EINVAL, "d and d_ff must be multiples of 32");
+        if (c->top_k != 1 && c->top_k != 2 && c->top_k != 4)
+            return fail(CPB_EINVAL, "MXFP4 path supports top_k in {1,2,4}, got %d", c->top_k);
+        if (c->d % (64 / c->top_k)) return fail(CPB_EINVAL, "d must be a multiple of 64/top_k");
+        if ((c->d / 32 + 14) / 15 > 16 || (c->d_ff / 32 + 14) / 15 > 16)
+            return fail(CPB_EINVAL, "d, d_ff must be <= 7680");
+    } else if (c->wtype_gate_up == CPB_GGUF_Q4_K) {
+        if (c->wtype_down != CPB_GGUF_Q4_K && c->wtype_down != CPB_GGUF_Q6_K)
+            return fail(CPB_EINVAL, "k-quant down must be Q4_K or Q6_K");
+        if (c->d % 256 || c->d_ff % 256) return fail(CPB_EINVAL, "d and d_ff must be multiples of 256");
+    } else {
+        return fail(CPB_EINVAL, "unsupported gate/up type %d", c->wtype_gate_up);
+    }
+    if (c->router != CPB_ROUTER_TOPK_SOFTMAX && c->router != CPB_ROUTER_SOFTMAX_TOPK)
+        return fail(CPB_EINVAL, "bad router %d", c->router);
+    if (c->act != CPB_ACT_SWIGLU_OAI && c->act != CPB_ACT_SILU) return fail(CPB_EINVAL, "bad act %d", c->act);
+    if (mx && c->act != CPB_ACT_SWIGLU_OAI) return fail(CPB_EINVAL, "MXFP4 path implements SwiGLU-OAI only");
+    if (!mx && c->act != CPB_ACT_SILU) return fail(CPB_EINVAL, "k-quant path implements SiLU only");
+    if (c->norm != CPB_NORM_GPTOSS && c->norm != CPB_NORM_QWEN) return fail(CPB_EINVAL, "bad norm %d", c->norm);
+    if (c->norm == CPB_NORM_QWEN && (c->norm_nt < 1 || c->norm_nt > 64))
+        return fail(CPB_EINVAL, "norm_nt must be in [1,64]");
+    return 0;
+}
+
+size_t row_bytes(int type, int cols) {
+    if (type == CPB_GGUF_MXFP4) return (size_t)cols / 32 * 17;
+    if (type == CPB_GGUF_Q4_K) return (size_t)cols / 256 * 144;
+    return (size_t)cols / 256 * 210;
+}
+
+int ensure_staging(cpb_moe_t* h, size_t n) {
+    if (h->staging_size >= n) return 0;
+    if (h->staging) hipFree(h->staging);
+    h->staging = nullptr;
+    h->staging_size = 0;
+    if (int r = dmalloc(&h->staging, n)) return r;
+    h->staging_size = n;
+    return 0;
+}
+
+int upload(float** dst, const float* src, size_t n, hipStream_t s) {
+    if (!src) { *dst = nullptr; return 0; }
+    if (int r = dmalloc(dst, n)) return r;
+    HIP_OK(hipMemcpyAsync(*dst, src, n * sizeof(float), hipMemcpyHostToDevice, s));
+    return 0;
+}
+
+void free_layer(LayerDev& L) {
+    hipFree(L.gu); hipFree(L.up); hipFree(L.dn);
+    hipFree(L.gate_b); hipFree(L.up_b); hipFree(L.down_b);
+    hipFree(L.router_w); hipFree(L.router_b); hipFree(L.norm_w);
+    L = LayerDev{};
+}
+
+struct Timer {
+    cpb_moe_t* h;
+    int cls;
+    hipEvent_t a = nullptr, b = nullptr;
+    Timer(cpb_moe_t* hh, int c) : h(hh), cls(c) {
+        if (!h->timing) return;
+        if (h->ev_pool.size() < 2) {
+            for (int i = 0; i < 64; i++) { hipEvent_t e; if (hipEventCreate(&e) == hipSuccess) h->ev_pool.push_back(e); }
+        }
+        if (h->ev_pool.size() < 2) return;
+        a = h->ev_pool.back(); h->ev_pool.pop_back();
+        b = h->ev_pool.back(); h->ev_pool.pop_back();
+        hipEventRecord(a, h->stream);
+    }
+    ~Timer() {
+        if (!a) return;
+        hipEventRecord(b, h->stream);
+        h->ev_used.push_back({cls, {a, b}});
+    }
+};
+
+int ensure_trace(cpb_moe_t* h) {
+    if (h->t_gu) return 0;
+    const auto& c = h->cfg;
+    size_t k = c.top_k;
+    int r;
+    if ((r = dmalloc(&h->t_gu, k * 2 * c.d_ff))) return r;
+    if ((r = dmalloc(&h->t_h, k * c.d_ff))) return r;
+    if ((r = dmalloc(&h->t_dn, k * c.d))) return r;
+    size_t gs = h->mx ? k * 2 * c.d_ff * (c.d / 32) : k * 2 * c.d_ff * (c.d / 256) * 2;
+    size_t ds = h->mx ? k * c.d * (c.d_ff / 32) : k * c.d * (c.d_ff / 256);
+    if ((r = dmalloc(&h->t_gu_sums, gs))) return r;
+    if ((r = dmalloc(&h->t_dn_sums, ds))) return r;
+    return 0;
+}
+
+// One token through one layer, x at device address dx.
+int layer_token(cpb_moe_t* h, int layer, float* dx, int apply_norm, bool trace) {
+    const auto& c = h->cfg;
+    LayerDev& L = h->layers[layer];
+    if (!L.loaded) return fail(CPB_ESTATE, "layer %d not loaded", layer);
+    cpb::RouteArgs ra{};
+    ra.x = dx; ra.norm_w = L.norm_w; ra.router_w = L.router_w; ra.router_b = L.router_b;
+    ra.d = c.d; ra.n_expert = c.n_expert; ra.top_k = c.top_k;
+    ra.norm = c.norm; ra.norm_nt = c.norm_nt; ra.apply_norm = apply_norm; ra.eps = c.rms_eps;
+    ra.qk = h->mx ? 0 : 1;
+    ra.xn = h->xn; ra.xq = h->xq; ra.xqn = h->xqn; ra.xsb = h->xsb; ra.xsum = h->xsum;
+    ra.lstar = h->lstar; ra.lbound = h->lbound; ra.counter = h->counter;
+    ra.logits = h->logits; ra.ids = h->ids; ra.wts = h->wts; ra.fallback = h->fallback;
+    {
+        Timer tm(h, 0);
+        if (cpb::launch_route(&ra, h->stream)) return fail(CPB_ENODEV, "route launch failed");
+    }
+    if (h->mx) {
+        cpb::GateUpArgs g{};
+        g.w = L.gu; g.gate_b = L.gate_b; g.up_b = L.up_b;
+        g.xq = h->xq; g.xqn = h->xqn; g.xsb = h->xsb; g.ids = h->ids;
+        g.dff = c.d_ff; g.nb = h->nb; g.nparts = h->parts_gu; g.top_k = c.top_k;
+        g.alpha = c.alpha; g.limit = c.limit;
+        g.hq = h->hq; g.hqn = h->hqn; g.hsb = h->hsb;
+        g.gu = h->t_gu; g.gu_sums = h->t_gu_sums; g.h = h->t_h;
+        {
+            Timer tm(h, 1);
+            if (cpb::launch_gateup_mx(g, trace, h->stream)) return fail(CPB_ENODEV, "gate/up launch failed");
+        }
+        cpb::DownArgs dn{};
+        dn.w = L.dn; dn.down_b = L.down_b; dn.hq = h->hq; dn.hqn = h->hqn; dn.hsb = h->hsb;
+        dn.ids = h->ids; dn.wts = h->wts;
+        dn.d = c.d; dn.dff = c.d_ff; dn.nbf = h->nbf; dn.nparts = h->parts_dn; dn.top_k = c.top_k;
+        dn.x = dx; dn.dn = h->t_dn; dn.dn_sums = h->t_dn_sums;
+        {
+            Timer tm(h, 2);
+            if (cpb::launch_down_mx(dn, trace, h->stream)) return fail(CPB_ENODEV, "down launch failed");
+        }
+    } else {
+        cpb::KqArgs k{};
+        k.gate = (const uint8_t*)L.gu; k.up = (const uint8_t*)L.up; k.down = (const uint8_t*)L.dn;
+        k.gate_type = c.wtype_gate_up; k.down_type = c.wtype_down;
+        k.xq = h->xq; k.xs = h->xsb; k.xsum = h->xsum; k.ids = h->ids; k.wts = h->wts;
+        k.d = c.d; k.dff = c.d_ff; k.top_k = c.top_k;
+        k.hbuf = h->hbuf; k.hq = h->hq; k.hs = h->hsb; k.hsum = h->hsum; k.x = dx;
+        k.gu = h->t_gu; k.gu_sums = h->t_gu_sums; k.dn = h->t_dn; k.dn_sums = h->t_dn_sums;
+        {
+            Timer tm(h, 1);
+            if (cpb::launch_gateup_kq(k, trace, h->stream)) return fail(CPB_ENODEV, "k-quant gate/up launch failed");
+        }
+        {
+            Timer tm(h, 2);
+            if (cpb::launch_down_kq(k, trace, h->stream)) return fail(CPB_ENODEV, "k-quant down launch failed");
+        }
+    }
+    return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* cpb_moe_last_error(void) { return g_err.c_str(); }
+
+int cpb_moe_layer_bytes(const cpb_moe_cfg* c, size_t* out) {
+    if (int r = check_cfg(c)) return r;
+    if (!out) return fail(CPB_EINVAL, "out is NULL");
+    if (c->wtype_gate_up == CPB_GGUF_MXFP4)
+        *out = cpb::mx_gateup_bytes(c->n_expert, c->d_ff, c->d / 32) +
+               cpb::mx_down_bytes(c->n_expert, c->d, c->d_ff / 32, c->top_k);
+    else
+        *out = (size_t)c->n_expert * (2 * c->d_ff * row_bytes(c->wtype_gate_up, c->d) +
+                                      c->d * row_bytes(c->wtype_down, c->d_ff));
+    return 0;
+}
+
+int cpb_moe_create(const cpb_moe_cfg* cfg, int device, cpb_moe_t** out) {
+    if (!out) return fail(CPB_EINVAL, "out is NULL");
+    *out = nullptr;
+    if (int r = check_cfg(cfg)) return r;
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || ndev == 0) return fail(CPB_ENODEV, "no HIP device");
+    if (device < 0 || device >= ndev) return fail(CPB_EINVAL, "device %d out of range (%d devices)", device, ndev);
+    HIP_OK(hipSetDevice(device));
+    cpb_moe_t* h = new cpb_moe_t();
+    h->cfg = *cfg;
+    h->device = device;
+    h->mx = cfg->wtype_gate_up == CPB_GGUF_MXFP4;
+    h->nb = cfg->d / 32;
+    h->nbf = cfg->d_ff / 32;
+    h->parts_gu = (h->nb + cpb::kBlkPerPart - 1) / cpb::kBlkPerPart;
+    h->parts_dn = (h->nbf + cpb::kBlkPerPart - 1) / cpb::kBlkPerPart;
+    h->layers.resize(cfg->n_layer);
+    auto bail = [&](int r) { cpb_moe_destroy(h); return r; };
+    if (hipStreamCreateWithFlags(&h->own, hipStreamNonBlocking) != hipSuccess) return bail(fail(CPB_ENODEV, "stream create failed"));
+    h->stream = h->own;
+    const size_t d = cfg->d, ff = cfg->d_ff, k = cfg->top_k, ne = cfg->n_expert, T = cfg->max_tokens;
+    int r;
+    if ((r = dmalloc(&h->x, T * d)) || (r = dmalloc(&h->xn, d)) || (r = dmalloc(&h->xq, d)) ||
+        (r = dmalloc(&h->xqn, d)) || (r = dmalloc(&h->xsb, d / 32)) || (r = dmalloc(&h->xsum, d / 32)) ||
+        (r = dmalloc(&h->lstar, ne)) || (r = dmalloc(&h->lbound, ne)) || (r = dmalloc(&h->counter, 1)) ||
+        (r = dmalloc(&h->logits, ne)) || (r = dmalloc(&h->ids, k)) || (r = dmalloc(&h->wts, k)) ||
+        (r = dmalloc(&h->fallback, 1)) || (r = dmalloc(&h->hq, k * ff)) || (r = dmalloc(&h->hqn, k * ff)) ||
+        (r = dmalloc(&h->hsb, k * ff / 32)) || (r = dmalloc(&h->hsum, k * ff / 32)) || (r = dmalloc(&h->hbuf, k * ff)))
+        return bail(r);
+    if (hipMemsetAsync(h->counter, 0, sizeof(unsigned), h->stream) != hipSuccess ||
+        hipMemsetAsync(h->fallback, 0, sizeof(int32_t), h->stream) != hipSuccess ||
+        hipStreamSynchronize(h->stream) != hipSuccess)
+        return bail(fail(CPB_ENODEV, "init memset failed"));
+    *out = h;
+    return 0;
+}
+
+int cpb_moe_load_layer(cpb_moe_t* h, int layer, const void* gate, const void* up, const void* down,
+                       const float* gate_b, const float* up_b, const float* down_b,
+                       const float* router_w, const float* router_b, const float* norm_w) {
+    if (!h) return fail(CPB_EINVAL, "handle is NULL");
+    const auto& c = h->cfg;
+    if (layer < 0 || layer >= c.n_layer) return fail(CPB_EINVAL, "layer %d out of range", layer);
+    if (!gate || !up || !down || !router_w) return fail(CPB_EINVAL, "gate/up/down/router_w must not be NULL");
+    if (c.has_bias && (!gate_b || !up_b || !down_b || !router_b))
+        return fail(CPB_EINVAL, "has_bias set but a bias pointer is NULL");
+    HIP_OK(hipSetDevice(h->device));
+    LayerDev& L = h->layers[layer];
+    free_layer(L);
+    const size_t ne = c.n_expert, d = c.d, ff = c.d_ff;
+    const size_t gbytes = ne * ff * row_bytes(c.wtype_gate_up, d);
+    const size_t dbytes = ne * d * row_bytes(c.wtype_down, ff);
+    int r;
+    if (h->mx) {
+        if ((r = ensure_staging(h, 2 * gbytes > dbytes ? 2 * gbytes : dbytes))) return r;
+        HIP_OK(hipMemcpyAsync(h->staging, gate, gbytes, hipMemcpyHostToDevice, h->stream));
+        HIP_OK(hipMemcpyAsync(h->staging + gbytes, up, gbytes, hipMemcpyHostToDevice, h->stream));
+        if ((r = dmalloc((uint8_t**)&L.gu, cpb::mx_gateup_bytes(ne, ff, d / 32)))) return r;
+        if (cpb::launch_repack_gateup(h->staging, h->staging + gbytes, L.gu, ne, ff, d / 32, h->stream))
+            return fail(CPB_ENODEV, "repack launch failed");
+        HIP_OK(hipStreamSynchronize(h->stream));
+        HIP_OK(hipMemcpyAsync(h->staging, down, dbytes, hipMemcpyHostToDevice, h->stream));
+        if ((r = dmalloc((uint8_t**)&L.dn, cpb::mx_down_bytes(ne, d, ff / 32, c.top_k)))) return r;
+        if (cpb::launch_repack_down(h->staging, L.dn, ne, d, ff / 32, c.top_k, h->stream))
+            return fail(CPB_ENODEV, "repack launch failed");
+    } else {
+        // k-quant superblocks are consumed in their native row layout
+        if ((r = dmalloc((uint8_t**)&L.gu, gbytes)) || (r = dmalloc((uint8_t**)&L.up, gbytes)) ||
+            (r = dmalloc((uint8_t**)&L.dn, dbytes)))
+            return r;
+        HIP_OK(hipMemcpyAsync(L.gu, gate, gbytes, hipMemcpyHostToDevice, h->stream));
+        HIP_OK(hipMemcpyAsync(L.up, up, gbytes, hipMemcpyHostToDevice, h->stream));
+        HIP_OK(hipMemcpyAsync(L.dn, down, dbytes, hipMemcpyHostToDevice, h->stream));
+    }
+    if (c.has_bias) {
+        if ((r = upload(&L.gate_b, gate_b, ne * ff, h->stream)) || (r = upload(&L.up_b, up_b, ne * ff, h->stream)) ||
+            (r = upload(&L.down_b, down_b, ne * d, h->stream)) || (r = upload(&L.router_b, router_b, ne, h->stream)))
+            return r;
+    }
+    if ((r = upload(&L.router_w, router_w, ne * d, h->stream))) return r;
+    if ((r = upload(&L.norm_w, norm_w, d, h->stream))) return r;
+    HIP_OK(hipStreamSynchronize(h->stream));
+    L.loaded = true;
+    return 0;
+}
+
+int cpb_moe_forward_device(cpb_moe_t* h, int layer0, int n_layers, float* d_x, int n_tok, int apply_norm) {
+    if (!h || !d_x) return fail(CPB_EINVAL, "NULL argument");
+    const auto& c = h->cfg;
+    if (layer0 < 0 || n_layers < 0 || layer0 + n_layers > c.n_layer) return fail(CPB_EINVAL, "layer range out of bounds");
+    if (n_tok < 1 || n_tok > c.max_tokens) return fail(CPB_EINVAL, "n_tok=%d outside [1, max_tokens=%d]", n_tok, c.max_tokens);
+    for (int l = layer0; l < layer0 + n_layers; l++)
+        for (int t = 0; t < n_tok; t++)
+            if (int r = layer_token(h, l, d_x + (size_t)t * c.d, apply_norm, false)) return r;
+    return 0;
+}
+
+int cpb_moe_forward(cpb_moe_t* h, int layer, float* x, int n_tok, int apply_norm, cpb_moe_trace* tr) {
+    if (!h || !x) return fail(CPB_EINVAL, "NULL argument");
+    const auto& c = h->cfg;
+    if (layer < 0 || layer >= c.n_layer) return fail(CPB_EINVAL, "layer %d out of range", layer);
+    if (n_tok < 1 || n_tok > c.max_tokens) return fail(CPB_EINVAL, "n_tok=%d outside [1, max_tokens=%d]", n_tok, c.max_tokens);
+    if (tr && n_tok != 1) return fail(CPB_EINVAL, "trace requires n_tok == 1");
+    HIP_OK(hipSetDevice(h->device));
+    const size_t d = c.d;
+    HIP_OK(hipMemcpyAsync(h->x, x, n_tok * d * sizeof(float), hipMemcpyHostToDevice, h->stream));
+    if (tr) {
+        if (int r = ensure_trace(h)) return r;
+        if (int r = layer_token(h, layer, h->x, apply_norm, true)) return r;
+    } else {
+        if (int r = cpb_moe_forward_device(h, layer, 1, h->x, n_tok, apply_norm)) return r;
+    }
+    HIP_OK(hipMemcpyAsync(x, h->x, n_tok * d * sizeof(float), hipMemcpyDeviceToHost, h->stream));
+    if (tr) {
+        const size_t k = c.top_k, ff = c.d_ff, ne = c.n_expert;
+        const bool mx = h->mx;
+        auto cp = [&](void* dst, const void* src, size_t bytes) -> int {
+            if (dst && bytes) HIP_OK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, h->stream));
+            return 0;
+        };
+        int r = 0;
+        r |= cp(tr->xn, h->xn, d * 4);
+        r |= cp(tr->xq, h->xq, d);
+        r |= cp(tr->xsb, h->xsb, (mx ? d / 32 : d / 256) * 4);
+        r |= cp(tr->xsum, h->xsum, mx ? 0 : d / 32 * 4);
+        r |= cp(tr->logits, h->logits, ne * 4);
+        r |= cp(tr->ids, h->ids, k * 4);
+        r |= cp(tr->wts, h->wts, k * 4);
+        r |= cp(tr->gu, h->t_gu, k * 2 * ff * 4);
+        r |= cp(tr->gu_sums, h->t_gu_sums, (mx ? k * 2 * ff * (d / 32) : k * 2 * ff * (d / 256) * 2) * 4);
+        r |= cp(tr->hq, h->hq, k * ff);
+        r |= cp(tr->hsb, h->hsb, (mx ? k * ff / 32 : k * ff / 256) * 4);
+        r |= cp(tr->hsum, h->hsum, mx ? 0 : k * ff / 32 * 4);
+        r |= cp(tr->dn, h->t_dn, k * d * 4);
+        r |= cp(tr->dn_sums, h->t_dn_sums, (mx ? k * d * (ff / 32) : k * d * (ff / 256)) * 4);
+        int32_t fb = 0;
+        r |= cp(&fb, h->fallback, 4);
+        HIP_OK(hipStreamSynchronize(h->stream));
+        tr->exact_router_fallbacks = fb;
+        if (r) return r;
+    }
+    HIP_OK(hipStreamSynchronize(h->stream));
+    return 0;
+}
+
+int cpb_moe_set_stream(cpb_moe_t* h, void* stream) {
+    if (!h) return fail(CPB_EINVAL, "handle is NULL");
+    h->stream = stream ? (hipStream_t)stream : h->own;
+    return 0;
+}
+
+int cpb_moe_sync(cpb_moe_t* h) {
+    if (!h) return fail(CPB_EINVAL, "handle is NULL");
+    HIP_OK(hipStreamSynchronize(h->stream));
+    return 0;
+}
+
+int cpb_moe_timing(cpb_moe_t* h, int enable) {
+    if (!h) return fail(CPB_EINVAL, "handle is NULL");
+    HIP_OK(hipStreamSynchronize(h->stream));
+    for (auto& u : h->ev_used) { h->ev_pool.push_back(u.second.first); h->ev_pool.push_back(u.second.second); }
+    h->ev_used.clear();
+    h->timing = enable != 0;
+    for (int i = 0; i < 3; i++) { h->ms[i] = 0; h->nl[i] = 0; }
+    return 0;
+}
+
+int cpb_moe_kernel_times(cpb_moe_t* h, double ms[3], long n[3]) {
+    if (!h || !ms || !n) return fail(CPB_EINVAL, "NULL argument");
+    HIP_OK(hipStreamSynchronize(h->stream));
+    for (auto& u : h->ev_used) {
+        float t = 0;
+        HIP_OK(hipEventElapsedTime(&t, u.second.first, u.second.second));
+        h->ms[u.first] += t;
+        h->nl[u.first] += 1;
+        h->ev_pool.push_back(u.second.first);
+        h->ev_pool.push_back(u.second.second);
+    }
+    h->ev_used.clear();
+    for (int i = 0; i < 3; i++) { ms[i] = h->ms[i]; n[i] = h->nl[i]; }
+    return 0;
+}
+
+void cpb_moe_destroy(cpb_moe_t* h) {
+    if (!h) return;
+    hipSetDevice(h->device);
+    if (h->stream) hipStreamSynchronize(h->stream);
+    for (auto& L : h->layers) free_layer(L);
+    void* bufs[] = {h->x, h->xn, h->xq, h->xqn, h->xsb, h->xsum, h->lstar, h->lbound, h->counter, h->logits,
+                    h->ids, h->wts, h->fallback, h->hq, h->hqn, h->hsb, h->hsum, h->hbuf, h->t_gu, h->t_h,
+                    h->t_dn, h->t_gu_sums, h->t_dn_sums, h->staging};
+    for (void* p : bufs) if (p) hipFree(p);
+    for (auto& u : h->ev_used) { hipEventDestroy(u.second.first); hipEventDestroy(u.second.second); }
+    for (auto e : h->ev_pool) hipEventDestroy(e);
+    if (h->own) hipStreamDestroy(h->own);
+    delete h;
+}
+
+}  // extern "C"

@@ -1,0 +1,49 @@
+// moe_mx.h -- launch arguments of the MXFP4 expert GEMV kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include "moe_common.h"
+
+namespace cpb {
+
+struct GateUpArgs {
+    const u32x4* w;          // stream layout of gate+up, all experts
+    const float* gate_b;     // [ne][dff] or null
+    const float* up_b;       // [ne][dff] or null
+    const int8_t* xq;        // [d]
+    const int8_t* xqn;       // [d]
+    const float* xsb;        // [d/32]
+    const int32_t* ids;      // [top_k]
+    int dff, nb, nparts, top_k;
+    float alpha, limit;
+    int8_t* hq;              // [top_k][dff]
+    int8_t* hqn;             // [top_k][dff]
+    float* hsb;              // [top_k][dff/32]
+    // trace (TRACE instantiation only)
+    float* gu;               // [top_k][2][dff]
+    int32_t* gu_sums;        // [top_k][2][dff][nb]
+    float* h;                // [top_k][dff]
+};
+
+struct DownArgs {
+    const u32x4* w;          // stream layout of down, all experts
+    const float* down_b;     // [ne][d] or null
+    const int8_t* hq;
+    const int8_t* hqn;
+    const float* hsb;
+    const int32_t* ids;
+    const float* wts;
+    int d, dff, nbf, nparts, top_k;
+    float* x;                // [d] residual, updated in place
+    float* dn;               // trace [top_k][d]
+    int32_t* dn_sums;        // trace [top_k][d][nbf]
+};
+
+size_t mx_gateup_bytes(int ne, int dff, int nb);
+size_t mx_down_bytes(int ne, int d, int nbf, int top_k);
+int launch_repack_gateup(const uint8_t* gate, const uint8_t* up, u32x4* out, int ne, int dff, int nb, hipStream_t s);
+int launch_repack_down(const uint8_t* down, u32x4* out, int ne, int d, int nbf, int top_k, hipStream_t s);
+int launch_gateup_mx(const GateUpArgs& a, bool trace, hipStream_t s);
+int launch_down_mx(const DownArgs& a, bool trace, hipStream_t s);
+
+}  // namespace cpb

@@ -1,0 +1,323 @@
+// moe_mx.hip -- gpt-oss MoE expert GEMVs over MXFP4 (gfx950), batch-1 decode.
+//
+// Reference: gate/up stage engine_gpt2.rs:870-884, SwiGLU-OAI + Q8
+// :887-906, down + weighted residual :908-922, kernel dot4_mx_i8 :194-228,
+// weight repack repack_mx :439-461.
+//
+// HBM layout ("stream layout", built at load time by k_repack_*): a matrix is
+// cut into row tiles; a tile's K (= nb 32-blocks) is cut into P k-parts of 15
+// blocks.  For each (tile, k-part) the data is 16 units x R lanes x 16 B:
+// unit 0 holds the 15 e8m0 bytes of the k-part's blocks (+1 pad byte),
+// units 1..15 hold one 32-block's 16 nibble bytes for each of the R rows.  One
+// wavefront load instruction therefore reads R*16 contiguous bytes (R = 64
+// for gate/up: 1 KB; R = 64/top_k for down: 16 lanes x 16 B per expert), and
+// a lane's whole k-part is 16 dwordx4 loads issued back to back.
+//
+//   gate/up: tile = 32 rows of gate + the same 32 rows of up of one expert
+//            (lanes 0-31 gate, 32-63 up) so SwiGLU and the per-32 Q8 of h
+//            finish inside the workgroup.
+//   down:    tile = 64/top_k rows x top_k active experts, so the weighted
+//            combine over experts (ascending slot order) finishes inside the
+//            workgroup and writes x directly.
+//
+// A workgroup has P wavefronts (one per k-part), each lane owns one row-dot
+// and accumulates its 15 blocks: int32 block sum via v_perm decode + sdot4,
+// one float conversion per block, fma with 2^(e-128)*xsb.  The P partial sums
+// are added in fixed order (deterministic).  Batch-1 decode is HBM-bound:
+// no MFMA here.
+#include "moe_common.h"
+#include "moe_mx.h"
+
+namespace cpb {
+
+// One lane's k-part: wv[0] = the 15 e8m0 bytes, wv[1..15] = nibble blocks.
+// xs: LDS activations of these 15 blocks as [15][xp 2 x u32x4][xn 2 x u32x4],
+// sb: their 15 scales.
+template <bool TRACE>
+CPB_DEV float part_dot(const u32x4* wv, const u32x4* xs, const float* sb, int32_t* sums_out, int blk0, int nb) {
+    const MxConsts k = mx_consts();
+    const uint32_t ew[4] = {wv[0][0], wv[0][1], wv[0][2], wv[0][3]};
+    float acc = 0.0f;
+#pragma unroll
+    for (int u = 0; u < kBlkPerPart; u++) {
+        const u32x4* xb = xs + u * 4;
+        int S = mx_block_sum(wv[u + 1], xb[0], xb[1], xb[2], xb[3], k);
+        uint32_t e = (ew[u >> 2] >> (8 * (u & 3))) & 0xffu;
+        acc = fmaf((float)S, e8m0_scale(e, sb[u]), acc);
+        if (TRACE && blk0 + u < nb) sums_out[u] = S;
+    }
+    return acc;
+}
+
+// LDS image of one expert's activations for one k-part: 15 blocks x
+// [xq 8 dwords | -xq 8 dwords], then 15 block scales (+1 pad): 256 dwords.
+constexpr int kXsDw = 256;
+
+// Fill one 256-dword activation image from global xq / -xq / scales.
+// `slot` runs over the image's dwords; returns the value for that slot.
+struct XsSlot {
+    const uint32_t* p;
+    bool valid;
+};
+CPB_DEV XsSlot xs_slot(const uint32_t* __restrict__ q, const uint32_t* __restrict__ qn,
+                       const float* __restrict__ sc, int blk0, int nb, int slot, bool use) {
+    // one clamped address per slot; the validity select is applied when the
+    // value is stored to LDS, after the weight loads have been issued
+    const bool isx = slot < kBlkPerPart * 16;
+    const int u = isx ? slot / 16 : slot - kBlkPerPart * 16;
+    const int j = slot & 15;
+    const int blk = blk0 + u;
+    const int bc = min(blk, nb - 1);
+    const uint32_t* base = isx ? (j < 8 ? q : qn) : (const uint32_t*)sc;
+    return XsSlot{base + (isx ? bc * 8 + (j & 7) : bc), use && blk < nb && (isx || u < kBlkPerPart)};
+}
+
+// Issue the lane's 16 weight loads in stream order (e8m0 unit first) so the
+// compiler's in-order vmcnt waits release each block as soon as it lands.
+CPB_DEV void load_part(const u32x4* p, size_t stride, u32x4* wv) {
+#pragma unroll
+    for (int u = 0; u < kUnits; u++) {
+        wv[u] = __builtin_nontemporal_load(p + (size_t)u * stride);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+CPB_DEV void wave_sync_lds() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <bool TRACE>
+__global__ __launch_bounds__(1024) void k_gateup_mx(GateUpArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int P = a.nparts;
+    const int lane = threadIdx.x & 63;
+    const int q = uniform(threadIdx.x >> 6);
+    const int tiles = a.dff / 32;
+    const int ei = blockIdx.x / tiles, t = blockIdx.x % tiles;
+    const int e = a.ids[ei];
+    uint32_t* xs = (uint32_t*)smem + q * kXsDw;
+    float* red = (float*)smem + P * kXsDw;                     // [P][64]
+    const int blk0 = q * kBlkPerPart;
+
+    // activations first: waiting for them must not wait for the weights
+    uint32_t xv[4];
+    bool ok[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        XsSlot sl = xs_slot((const uint32_t*)a.xq, (const uint32_t*)a.xqn, a.xsb, blk0, a.nb, lane + 64 * k, true);
+        xv[k] = *sl.p;
+        ok[k] = sl.valid;
+    }
+    u32x4 wv[kUnits];
+    load_part(a.w + ((((size_t)e * tiles + t) * P + q) * kUnits) * 64 + lane, 64, wv);
+#pragma unroll
+    for (int k = 0; k < 4; k++) xs[lane + 64 * k] = ok[k] ? xv[k] : 0u;
+    wave_sync_lds();
+
+    const int row = t * 32 + (lane & 31);
+    const int isup = lane >> 5;                                // lanes 0-31 gate, 32-63 up
+    int32_t* so = nullptr;
+    if (TRACE) so = a.gu_sums + (((size_t)(ei * 2 + isup) * a.dff + row) * a.nb + blk0);
+    float acc = part_dot<TRACE>(wv, (const u32x4*)xs, (const float*)xs + kBlkPerPart * 16, so, blk0, a.nb);
+
+    red[q * 64 + lane] = acc;
+    __syncthreads();
+    if (q != 0) return;
+    float v = 0.0f;
+    for (int p = 0; p < P; p++) v += red[p * 64 + lane];
+    if (isup) { if (a.up_b) v += a.up_b[(size_t)e * a.dff + row]; }
+    else      { if (a.gate_b) v += a.gate_b[(size_t)e * a.dff + row]; }
+    if (TRACE) a.gu[(size_t)(ei * 2 + isup) * a.dff + row] = v;
+    // SwiGLU-OAI (engine_gpt2.rs:887-906) in lanes 0-31: gate row r, up row r from lane r+32
+    float u = __shfl_down(v, 32);
+    float h = 0.0f;
+    if (!isup) {
+        float xg = fminf(v, a.limit);
+        float yu = fminf(fmaxf(u, -a.limit), a.limit);
+        h = (xg / (1.0f + expf(-a.alpha * xg))) * (yu + 1.0f);
+    }
+    float m = isup ? 0.0f : fabsf(h);
+#pragma unroll
+    for (int s = 16; s >= 1; s >>= 1) m = fmaxf(m, __shfl_xor(m, s));
+    float sc = fmaxf(1e-12f, m) / 127.0f;
+    if (!isup) {
+        int8_t qv = q8_round(h, sc);
+        a.hq[(size_t)ei * a.dff + row] = qv;
+        a.hqn[(size_t)ei * a.dff + row] = (int8_t)(-qv);
+        if (TRACE) a.h[(size_t)ei * a.dff + row] = h;
+    }
+    if (lane == 0) a.hsb[(size_t)ei * (a.dff / 32) + t] = sc;
+}
+
+template <bool TRACE>
+__global__ __launch_bounds__(1024) void k_down_mx(DownArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int P = a.nparts, K = a.top_k, RT = 64 / K;
+    const int lane = threadIdx.x & 63;
+    const int q = uniform(threadIdx.x >> 6);
+    const int tiles = a.d / RT, t = blockIdx.x;
+    const int ei = lane / RT, rr = lane % RT, row = t * RT + rr;
+    // expert of this lane's slot from wave-uniform (scalar) loads of ids
+    int es[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        es[k] = __builtin_amdgcn_readfirstlane(a.ids[k < K ? k : 0]);
+    }
+    const int e = ei == 0 ? es[0] : ei == 1 ? es[1] : ei == 2 ? es[2] : es[3];
+    uint32_t* xs = (uint32_t*)smem + q * K * kXsDw;           // [K][256]
+    float* red = (float*)smem + P * K * kXsDw;                 // [P][64]
+    float* vv = red + P * 64;                                  // [64]
+    const int blk0 = q * kBlkPerPart;
+
+    // activations of all K expert slots (hq is [K][dff]), before the weights
+    uint32_t xv[16];
+    bool ok[16];
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+        int i = lane + 64 * k, ex = min(i / kXsDw, K - 1);
+        XsSlot sl = xs_slot((const uint32_t*)(a.hq + (size_t)ex * a.dff), (const uint32_t*)(a.hqn + (size_t)ex * a.dff),
+                            a.hsb + (size_t)ex * a.nbf, blk0, a.nbf, i % kXsDw, i < K * kXsDw);
+        xv[k] = *sl.p;
+        ok[k] = sl.valid;
+    }
+    u32x4 wv[kUnits];
+    load_part(a.w + (((((size_t)e * tiles + t) * P + q) * kUnits) * RT) + rr, RT, wv);
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+        int i = lane + 64 * k;
+        if (i < K * kXsDw) xs[i] = ok[k] ? xv[k] : 0u;
+    }
+    wave_sync_lds();
+
+    const uint32_t* mine = xs + ei * kXsDw;
+    int32_t* so = nullptr;
+    if (TRACE) so = a.dn_sums + (((size_t)ei * a.d + row) * a.nbf + blk0);
+    float acc = part_dot<TRACE>(wv, (const u32x4*)mine, (const float*)mine + kBlkPerPart * 16, so, blk0, a.nbf);
+
+    red[q * 64 + lane] = acc;
+    __syncthreads();
+    if (q != 0) return;
+    float v = 0.0f;
+    for (int p = 0; p < P; p++) v += red[p * 64 + lane];
+    if (a.down_b) v += a.down_b[(size_t)e * a.d + row];
+    if (TRACE) a.dn[(size_t)ei * a.d + row] = v;
+    vv[lane] = v;
+    wave_sync_lds();
+    if (lane < RT) {
+        // engine_gpt2.rs:911-921: s = x[r]; s += wts[ei] * (dot + b), ei ascending
+        float s = a.x[row];
+        for (int k = 0; k < K; k++) s += a.wts[k] * vv[k * RT + lane];
+        a.x[row] = s;
+    }
+}
+
+// ---- load-time re-layout from native GGUF MXFP4 rows (17-byte blocks) ----
+// One thread per 16-byte output unit.
+__global__ void k_repack_gateup(const uint8_t* __restrict__ gate, const uint8_t* __restrict__ up,
+                                u32x4* __restrict__ out, int ne, int dff, int nb, int P) {
+    size_t tiles = dff / 32;
+    size_t total = (size_t)ne * tiles * P * kUnits * 64;
+    for (size_t idx = blockIdx.x * (size_t)blockDim.x + threadIdx.x; idx < total; idx += (size_t)gridDim.x * blockDim.x) {
+        int lane = idx % 64;
+        size_t r1 = idx / 64;
+        int u = r1 % kUnits; r1 /= kUnits;
+        int q = r1 % P; r1 /= P;
+        int t = r1 % tiles;
+        int e = (int)(r1 / tiles);
+        int row = t * 32 + (lane & 31);
+        const uint8_t* src = (lane < 32 ? gate : up) + ((size_t)e * dff + row) * nb * 17;
+        uint8_t b[16];
+        if (u > 0) {
+            int blk = q * kBlkPerPart + u - 1;
+            for (int i = 0; i < 16; i++) b[i] = blk < nb ? src[(size_t)blk * 17 + 1 + i] : 0;
+        } else {
+            for (int i = 0; i < 16; i++) {
+                int blk = q * kBlkPerPart + i;
+                b[i] = (i < kBlkPerPart && blk < nb) ? src[(size_t)blk * 17] : 0;
+            }
+        }
+        u32x4 o;
+        o[0] = b[0] | (b[1] << 8) | (b[2] << 16) | ((uint32_t)b[3] << 24);
+        o[1] = b[4] | (b[5] << 8) | (b[6] << 16) | ((uint32_t)b[7] << 24);
+        o[2] = b[8] | (b[9] << 8) | (b[10] << 16) | ((uint32_t)b[11] << 24);
+        o[3] = b[12] | (b[13] << 8) | (b[14] << 16) | ((uint32_t)b[15] << 24);
+        out[idx] = o;
+    }
+}
+
+__global__ void k_repack_down(const uint8_t* __restrict__ down, u32x4* __restrict__ out, int ne, int d, int nbf,
+                              int P, int RT) {
+    size_t tiles = d / RT;
+    size_t total = (size_t)ne * tiles * P * kUnits * RT;
+    for (size_t idx = blockIdx.x * (size_t)blockDim.x + threadIdx.x; idx < total; idx += (size_t)gridDim.x * blockDim.x) {
+        int rr = idx % RT;
+        size_t r1 = idx / RT;
+        int u = r1 % kUnits; r1 /= kUnits;
+        int q = r1 % P; r1 /= P;
+        int t = r1 % tiles;
+        int e = (int)(r1 / tiles);
+        int row = t * RT + rr;
+        const uint8_t* src = down + ((size_t)e * d + row) * nbf * 17;
+        uint8_t b[16];
+        if (u > 0) {
+            int blk = q * kBlkPerPart + u - 1;
+            for (int i = 0; i < 16; i++) b[i] = blk < nbf ? src[(size_t)blk * 17 + 1 + i] : 0;
+        } else {
+            for (int i = 0; i < 16; i++) {
+                int blk = q * kBlkPerPart + i;
+                b[i] = (i < kBlkPerPart && blk < nbf) ? src[(size_t)blk * 17] : 0;
+            }
+        }
+        u32x4 o;
+        o[0] = b[0] | (b[1] << 8) | (b[2] << 16) | ((uint32_t)b[3] << 24);
+        o[1] = b[4] | (b[5] << 8) | (b[6] << 16) | ((uint32_t)b[7] << 24);
+        o[2] = b[8] | (b[9] << 8) | (b[10] << 16) | ((uint32_t)b[11] << 24);
+        o[3] = b[12] | (b[13] << 8) | (b[14] << 16) | ((uint32_t)b[15] << 24);
+        out[idx] = o;
+    }
+}
+
+size_t mx_gateup_bytes(int ne, int dff, int nb) {
+    int P = (nb + kBlkPerPart - 1) / kBlkPerPart;
+    return (size_t)ne * (dff / 32) * P * kUnits * 64 * 16;
+}
+size_t mx_down_bytes(int ne, int d, int nbf, int top_k) {
+    int P = (nbf + kBlkPerPart - 1) / kBlkPerPart;
+    int RT = 64 / top_k;
+    return (size_t)ne * (d / RT) * P * kUnits * RT * 16;
+}
+
+int launch_repack_gateup(const uint8_t* gate, const uint8_t* up, u32x4* out, int ne, int dff, int nb, hipStream_t s) {
+    int P = (nb + kBlkPerPart - 1) / kBlkPerPart;
+    hipLaunchKernelGGL(k_repack_gateup, dim3(4096), dim3(256), 0, s, gate, up, out, ne, dff, nb, P);
+    return hipGetLastError() == hipSuccess ? 0 : -19;
+}
+int launch_repack_down(const uint8_t* down, u32x4* out, int ne, int d, int nbf, int top_k, hipStream_t s) {
+    int P = (nbf + kBlkPerPart - 1) / kBlkPerPart;
+    hipLaunchKernelGGL(k_repack_down, dim3(4096), dim3(256), 0, s, down, out, ne, d, nbf, P, 64 / top_k);
+    return hipGetLastError() == hipSuccess ? 0 : -19;
+}
+
+int launch_gateup_mx(const GateUpArgs& a, bool trace, hipStream_t s) {
+    int P = a.nparts;
+    if (P < 1 || P > 16 || a.dff % 32 != 0) return -22;
+    size_t lds = sizeof(uint32_t) * P * kXsDw + sizeof(float) * P * 64;
+    dim3 grid(a.top_k * (a.dff / 32)), block(64 * P);
+    if (trace) hipLaunchKernelGGL(k_gateup_mx<true>, grid, block, lds, s, a);
+    else hipLaunchKernelGGL(k_gateup_mx<false>, grid, block, lds, s, a);
+    return hipGetLastError() == hipSuccess ? 0 : -19;
+}
+
+int launch_down_mx(const DownArgs& a, bool trace, hipStream_t s) {
+    int P = a.nparts, K = a.top_k;
+    if (P < 1 || P > 16 || (K != 1 && K != 2 && K != 4) || a.d % (64 / K) != 0) return -22;
+    size_t lds = sizeof(uint32_t) * P * K * kXsDw + sizeof(float) * (P * 64 + 64);
+    dim3 grid(a.d / (64 / K)), block(64 * P);
+    if (trace) hipLaunchKernelGGL(k_down_mx<true>, grid, block, lds, s, a);
+    else hipLaunchKernelGGL(k_down_mx<false>, grid, block, lds, s, a);
+    return hipGetLastError() == hipSuccess ? 0 : -19;
+}
+
+}  // namespace cpb

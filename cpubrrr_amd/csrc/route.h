@@ -1,0 +1,33 @@
+// route.h -- launch arguments of the per-token routing kernel.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace cpb {
+
+struct RouteArgs {
+    const float* x;          // [d] residual input
+    const float* norm_w;     // [d] or null (ones)
+    const float* router_w;   // [ne][d]
+    const float* router_b;   // [ne] or null
+    int d, n_expert, top_k;
+    int norm, norm_nt, apply_norm;
+    float eps;
+    int qk;                  // 0: Q8 per 32 (MXFP4 experts), 1: Q8_K per 256 (k-quant experts)
+    float* xn;               // [d]
+    int8_t* xq;              // [d]
+    int8_t* xqn;             // [d]  negated xq
+    float* xsb;              // [d/32] or [d/256]
+    int32_t* xsum;           // [d/32] (qk == 1)
+    double* lstar;           // [ne] scratch
+    double* lbound;          // [ne] scratch
+    unsigned* counter;       // zero between launches
+    float* logits;           // [ne]
+    int32_t* ids;            // [top_k]
+    float* wts;              // [top_k]
+    int32_t* fallback;       // 1 when the exact serial router was needed
+};
+
+int launch_route(const RouteArgs* a, hipStream_t s);
+
+}  // namespace cpb

@@ -1,0 +1,238 @@
+"""ctypes front end of the oracle (oracle.c): the CPU restatement of the
+reference's MoE expert-FFN decode path.
+
+TEST INFRASTRUCTURE ONLY.  Imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg, where it is the checker (or the timed CPU
+baseline), never the thing measured on the GPU.  The product package
+cpubrrr_amd/ does not import it.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+_LIB = None
+
+f32p = C.POINTER(C.c_float)
+i8p = C.POINTER(C.c_int8)
+i32p = C.POINTER(C.c_int32)
+u8p = C.POINTER(C.c_uint8)
+
+
+class Trace(C.Structure):
+    _fields_ = [("xn", f32p), ("xq", i8p), ("xsb", f32p), ("xsum", i32p), ("logits", f32p),
+                ("ids", i32p), ("wts", f32p), ("gu", f32p), ("gu_sums", i32p), ("h", f32p),
+                ("hq", i8p), ("hsb", f32p), ("hsum", i32p), ("dn", f32p), ("dn_sums", i32p)]
+
+
+class GptossLayer(C.Structure):
+    _fields_ = [("d", C.c_int), ("dff", C.c_int), ("ne", C.c_int), ("k", C.c_int),
+                ("alpha", C.c_float), ("limit", C.c_float), ("eps", C.c_float),
+                ("gate", u8p), ("up", u8p), ("down", u8p),
+                ("gate_b", f32p), ("up_b", f32p), ("down_b", f32p),
+                ("router_w", f32p), ("router_b", f32p), ("norm_w", f32p)]
+
+
+class QwenLayer(C.Structure):
+    _fields_ = [("d", C.c_int), ("dff", C.c_int), ("ne", C.c_int), ("k", C.c_int), ("nt", C.c_int),
+                ("eps", C.c_float), ("gate_type", C.c_int), ("up_type", C.c_int), ("down_type", C.c_int),
+                ("gate", u8p), ("up", u8p), ("down", u8p), ("router_w", f32p), ("norm_w", f32p)]
+
+
+def lib() -> C.CDLL:
+    global _LIB
+    if _LIB is None:
+        path = HERE / "liboracle.so"
+        if not path.exists():
+            from oracle.build import build
+            build()
+        L = C.CDLL(str(path))
+        L.orc_e8m0_half.restype = C.c_float
+        L.orc_e8m0_half.argtypes = [C.c_uint8]
+        L.orc_half_to_f32.restype = C.c_float
+        L.orc_half_to_f32.argtypes = [C.c_uint16]
+        L.orc_ssq_gptoss.restype = C.c_float
+        L.orc_ssq_gptoss.argtypes = [f32p, C.c_int]
+        L.orc_rmsnorm_gptoss.argtypes = [f32p, f32p, C.c_int, C.c_float, f32p]
+        L.orc_rmsnorm_qwen.argtypes = [f32p, f32p, C.c_int, C.c_float, C.c_int, f32p]
+        L.orc_qblock32.argtypes = [f32p, C.c_int, i8p, f32p]
+        L.orc_qblock_k.argtypes = [f32p, C.c_int, i8p, f32p, i32p]
+        L.orc_router.argtypes = [f32p, f32p, f32p, C.c_int, C.c_int, f32p]
+        L.orc_topk_gptoss.argtypes = [f32p, C.c_int, C.c_int, i32p, f32p]
+        L.orc_topk_qwen.argtypes = [f32p, C.c_int, C.c_int, i32p, f32p]
+        L.orc_mx_row_dot.restype = C.c_float
+        L.orc_mx_row_dot.argtypes = [u8p, i8p, f32p, C.c_int, i32p]
+        L.orc_q4k_dot.restype = C.c_float
+        L.orc_q4k_dot.argtypes = [u8p, i8p, f32p, i32p, C.c_int, i32p]
+        L.orc_q6k_dot.restype = C.c_float
+        L.orc_q6k_dot.argtypes = [u8p, i8p, f32p, C.c_int, i32p]
+        L.orc_gptoss_moe.argtypes = [C.POINTER(GptossLayer), f32p, C.c_int, C.POINTER(Trace)]
+        L.orc_qwen_moe.argtypes = [C.POINTER(QwenLayer), f32p, C.c_int, C.POINTER(Trace)]
+        L.orc_set_threads.argtypes = [C.c_int]
+        L.orc_get_threads.restype = C.c_int
+        _LIB = L
+    return _LIB
+
+
+def _p(a: np.ndarray | None, t):
+    if a is None:
+        return C.cast(None, t)
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(t)
+
+
+def set_threads(n: int) -> None:
+    lib().orc_set_threads(int(n))
+
+
+def get_threads() -> int:
+    return int(lib().orc_get_threads())
+
+
+def e8m0_half(e: int) -> float:
+    return float(lib().orc_e8m0_half(int(e)))
+
+
+def half_to_f32(h: int) -> float:
+    return float(lib().orc_half_to_f32(int(h)))
+
+
+def ssq_gptoss(x: np.ndarray) -> np.float32:
+    x = np.ascontiguousarray(x, np.float32)
+    return np.float32(lib().orc_ssq_gptoss(_p(x, f32p), x.size))
+
+
+def rmsnorm_gptoss(x, w, eps):
+    x = np.ascontiguousarray(x, np.float32); w = np.ascontiguousarray(w, np.float32)
+    out = np.empty_like(x)
+    lib().orc_rmsnorm_gptoss(_p(x, f32p), _p(w, f32p), x.size, float(eps), _p(out, f32p))
+    return out
+
+
+def rmsnorm_qwen(x, w, eps, nt=12):
+    x = np.ascontiguousarray(x, np.float32); w = np.ascontiguousarray(w, np.float32)
+    out = np.empty_like(x)
+    lib().orc_rmsnorm_qwen(_p(x, f32p), _p(w, f32p), x.size, float(eps), int(nt), _p(out, f32p))
+    return out
+
+
+def qblock32(x):
+    x = np.ascontiguousarray(x, np.float32)
+    xq = np.empty(x.size, np.int8); xsb = np.empty(x.size // 32, np.float32)
+    lib().orc_qblock32(_p(x, f32p), x.size, _p(xq, i8p), _p(xsb, f32p))
+    return xq, xsb
+
+
+def qblock_k(x):
+    x = np.ascontiguousarray(x, np.float32)
+    xq = np.empty(x.size, np.int8); ys = np.empty(x.size // 256, np.float32)
+    xsum = np.empty(x.size // 32, np.int32)
+    lib().orc_qblock_k(_p(x, f32p), x.size, _p(xq, i8p), _p(ys, f32p), _p(xsum, i32p))
+    return xq, ys, xsum
+
+
+def router(W, b, xn):
+    W = np.ascontiguousarray(W, np.float32); xn = np.ascontiguousarray(xn, np.float32)
+    ne, d = W.shape
+    b = None if b is None else np.ascontiguousarray(b, np.float32)
+    out = np.empty(ne, np.float32)
+    lib().orc_router(_p(W, f32p), _p(b, f32p), _p(xn, f32p), ne, d, _p(out, f32p))
+    return out
+
+
+def topk_gptoss(logits, k):
+    logits = np.ascontiguousarray(logits, np.float32)
+    ids = np.empty(k, np.int32); w = np.empty(k, np.float32)
+    lib().orc_topk_gptoss(_p(logits, f32p), logits.size, k, _p(ids, i32p), _p(w, f32p))
+    return ids, w
+
+
+def topk_qwen(logits, k):
+    logits = np.ascontiguousarray(logits, np.float32)
+    ids = np.empty(k, np.int32); w = np.empty(k, np.float32)
+    lib().orc_topk_qwen(_p(logits, f32p), logits.size, k, _p(ids, i32p), _p(w, f32p))
+    return ids, w
+
+
+def mx_row_dot(row, xq, xsb):
+    row = np.ascontiguousarray(row, np.uint8); xq = np.ascontiguousarray(xq, np.int8)
+    xsb = np.ascontiguousarray(xsb, np.float32)
+    nb = xsb.size
+    sums = np.empty(nb, np.int32)
+    v = lib().orc_mx_row_dot(_p(row, u8p), _p(xq, i8p), _p(xsb, f32p), nb, _p(sums, i32p))
+    return np.float32(v), sums
+
+
+def q4k_dot(row, xq, ys, xsum):
+    row = np.ascontiguousarray(row, np.uint8); xq = np.ascontiguousarray(xq, np.int8)
+    ys = np.ascontiguousarray(ys, np.float32); xsum = np.ascontiguousarray(xsum, np.int32)
+    sums = np.empty(2 * ys.size, np.int32)
+    v = lib().orc_q4k_dot(_p(row, u8p), _p(xq, i8p), _p(ys, f32p), _p(xsum, i32p), xq.size, _p(sums, i32p))
+    return np.float32(v), sums
+
+
+def q6k_dot(row, xq, ys):
+    row = np.ascontiguousarray(row, np.uint8); xq = np.ascontiguousarray(xq, np.int8)
+    ys = np.ascontiguousarray(ys, np.float32)
+    sums = np.empty(ys.size, np.int32)
+    v = lib().orc_q6k_dot(_p(row, u8p), _p(xq, i8p), _p(ys, f32p), xq.size, _p(sums, i32p))
+    return np.float32(v), sums
+
+
+def _trace_bufs(d, dff, ne, k, mx: bool, want_sums: bool):
+    t = {
+        "xn": np.zeros(d, np.float32), "xq": np.zeros(d, np.int8),
+        "xsb": np.zeros(d // 32 if mx else d // 256, np.float32),
+        "xsum": np.zeros(d // 32, np.int32), "logits": np.zeros(ne, np.float32),
+        "ids": np.zeros(k, np.int32), "wts": np.zeros(k, np.float32),
+        "gu": np.zeros((k, 2, dff), np.float32), "h": np.zeros((k, dff), np.float32),
+        "hq": np.zeros((k, dff), np.int8),
+        "hsb": np.zeros((k, dff // 32) if mx else (k, dff // 256), np.float32),
+        "hsum": np.zeros((k, dff // 32), np.int32), "dn": np.zeros((k, d), np.float32),
+    }
+    if want_sums:
+        t["gu_sums"] = np.zeros((k, 2, dff, d // 32) if mx else (k, 2, dff, d // 256, 2), np.int32)
+        t["dn_sums"] = np.zeros((k, d, dff // 32) if mx else (k, d, dff // 256), np.int32)
+    return t
+
+
+def _mk_trace(t) -> Trace:
+    tr = Trace()
+    types = dict(Trace._fields_)
+    for name, arr in t.items():
+        setattr(tr, name, _p(arr, types[name]))
+    return tr
+
+
+def gptoss_moe(layer: dict, x: np.ndarray, apply_norm: bool, want_sums: bool = False):
+    """One gpt-oss MoE block (engine_gpt2.rs:845-923).  Returns (x_out, trace)."""
+    d, dff, ne, k = layer["d"], layer["dff"], layer["ne"], layer["k"]
+    keep = {n: np.ascontiguousarray(layer[n]) for n in
+            ("gate", "up", "down", "gate_b", "up_b", "down_b", "router_w", "router_b", "norm_w")}
+    L = GptossLayer(d, dff, ne, k, layer.get("alpha", 1.702), layer.get("limit", 7.0), layer.get("eps", 1e-5),
+                    _p(keep["gate"], u8p), _p(keep["up"], u8p), _p(keep["down"], u8p),
+                    _p(keep["gate_b"], f32p), _p(keep["up_b"], f32p), _p(keep["down_b"], f32p),
+                    _p(keep["router_w"], f32p), _p(keep["router_b"], f32p), _p(keep["norm_w"], f32p))
+    xo = np.array(x, np.float32, copy=True)
+    t = _trace_bufs(d, dff, ne, k, True, want_sums)
+    tr = _mk_trace(t)
+    lib().orc_gptoss_moe(C.byref(L), _p(xo, f32p), int(bool(apply_norm)), C.byref(tr))
+    return xo, t
+
+
+def qwen_moe(layer: dict, x: np.ndarray, apply_norm: bool, want_sums: bool = False):
+    """One Qwen3 MoE block (engine_qwen2.rs:395-433).  Returns (x_out, trace)."""
+    d, dff, ne, k = layer["d"], layer["dff"], layer["ne"], layer["k"]
+    keep = {n: np.ascontiguousarray(layer[n]) for n in ("gate", "up", "down", "router_w", "norm_w")}
+    L = QwenLayer(d, dff, ne, k, layer.get("nt", 12), layer.get("eps", 1e-6),
+                  layer.get("gate_type", 12), layer.get("up_type", 12), layer.get("down_type", 14),
+                  _p(keep["gate"], u8p), _p(keep["up"], u8p), _p(keep["down"], u8p),
+                  _p(keep["router_w"], f32p), _p(keep["norm_w"], f32p))
+    xo = np.array(x, np.float32, copy=True)
+    t = _trace_bufs(d, dff, ne, k, False, want_sums)
+    tr = _mk_trace(t)
+    lib().orc_qwen_moe(C.byref(L), _p(xo, f32p), int(bool(apply_norm)), C.byref(tr))
+    return xo, t

@@ -1,0 +1,136 @@
+"""GPU parity of the MXFP4 (gpt-oss) decode path against the oracle.
+
+Bit-exact: xn, xq, xsb (Q8 activation bytes and scales), expert ids, int32
+block sums of gate/up and (given the same hq) of down.  To tolerance: router
+logits (within the serial-sum bound), softmax weights, gate/up outputs, hq/hsb
+(SwiGLU goes through expf) and the layer output (max-abs <= 1e-3 * RMS of the
+FFN output).
+"""
+import numpy as np
+import pytest
+
+from cpubrrr_amd import MoeBlock, MoeConfig, synth
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+def check_layer(L, x, apply_norm, xo, t, *, teacher_forced_down=True):
+    xo_o, to = O.gptoss_moe(L, x, apply_norm, want_sums=True)
+    d, dff, k = L["d"], L["dff"], L["k"]
+    assert np.array_equal(t["xn"].view(np.uint32), to["xn"].view(np.uint32)), "xn"
+    assert np.array_equal(t["xq"], to["xq"]), "xq"
+    assert np.array_equal(t["xsb"].view(np.uint32), to["xsb"].view(np.uint32)), "xsb"
+    assert np.array_equal(t["ids"], to["ids"]), (t["ids"], to["ids"])
+    assert np.allclose(t["logits"], to["logits"], rtol=0, atol=2e-4 + 1e-6 * np.abs(to["logits"]).max())
+    assert np.allclose(t["wts"], to["wts"], rtol=2e-5, atol=1e-7)
+    assert np.array_equal(t["gu_sums"], to["gu_sums"]), "gate/up block sums"
+    gmax = np.abs(to["gu"]).max()
+    assert np.max(np.abs(t["gu"] - to["gu"])) <= 2e-6 * gmax, "gate/up outputs"
+    dq = t["hq"].astype(np.int32) - to["hq"].astype(np.int32)
+    assert np.abs(dq).max() <= 1 and np.count_nonzero(dq) <= max(2, dq.size // 1000), "hq"
+    assert np.allclose(t["hsb"], to["hsb"], rtol=1e-5), "hsb"
+    if teacher_forced_down:
+        # down block sums from the GPU's own hq: exact
+        nbf = dff // 32
+        for ei in range(k):
+            e = t["ids"][ei]
+            for r in range(0, d, max(1, d // 97)):
+                _, s = O.mx_row_dot(L["down"][e * d + r], t["hq"][ei], t["hsb"][ei])
+                assert np.array_equal(t["dn_sums"][ei, r], s), ("down sums", ei, r)
+    ffn_o = (xo_o - x).astype(np.float64)
+    ffn_g = (xo - x).astype(np.float64)
+    rms = np.sqrt((ffn_o ** 2).mean())
+    err = np.max(np.abs(ffn_g - ffn_o))
+    assert err <= 1e-3 * rms, (err, rms)
+    return err / rms
+
+
+def run_case(d, dff, ne, k, seed=0, layer=0, apply_norm=False, zipf=None, n_tok=1):
+    say(f"case d={d} dff={dff} ne={ne} k={k} seed={seed} layer={layer} norm={apply_norm} zipf={zipf}")
+    L = synth.gptoss_layer(d, dff, ne, k, seed=seed, layer=layer, zipf=zipf)
+    cfg = MoeConfig.gptoss(d=d, n_expert=ne, top_k=k, d_ff=dff, max_tokens=n_tok)
+    with MoeBlock(cfg) as blk:
+        blk.load_layer(0, L)
+        x = synth.token(d, seed, layer)
+        xo, t = blk.forward(0, x, apply_norm=apply_norm, trace=True)
+        rel = check_layer(L, x, apply_norm, xo, t)
+        # the untraced kernels give the same result bit for bit
+        xo2, _ = blk.forward(0, x, apply_norm=apply_norm)
+        assert np.array_equal(xo2.view(np.uint32), xo.view(np.uint32))
+    say(f"  ok rel_err={rel:.3e} fallback={t['exact_router_fallbacks']}")
+    return L, t
+
+
+def test_small_shapes(gpu):
+    run_case(480, 480, 8, 4)
+    run_case(480, 960, 8, 4, seed=1, apply_norm=True)
+    run_case(960, 480, 16, 2, seed=2)
+    run_case(512, 512, 4, 1, seed=3, apply_norm=True)
+
+
+def test_config0_layer(gpu):
+    # gpt-oss-20b layer, seed 0, input already normed
+    run_case(2880, 2880, 32, 4, seed=0, apply_norm=False)
+
+
+def test_20b_layer_zipf_norm(gpu):
+    for layer in (1, 7):
+        run_case(2880, 2880, 32, 4, seed=0, layer=layer, apply_norm=True, zipf=1.1)
+
+
+def test_router_tie_uses_exact_fallback(gpu):
+    say("case router tie")
+    d, dff, ne, k = 480, 480, 8, 4
+    L = synth.gptoss_layer(d, dff, ne, k, seed=5)
+    x = synth.token(d, 5)
+    lg = L["router_w"] @ x
+    top = np.argsort(-lg)[:2]
+    # two experts with identical router rows tie exactly; the lower index must win
+    L["router_w"][top[1]] = L["router_w"][top[0]]
+    cfg = MoeConfig.gptoss(d=d, n_expert=ne, top_k=k, d_ff=dff)
+    with MoeBlock(cfg) as blk:
+        blk.load_layer(0, L)
+        xo, t = blk.forward(0, x, apply_norm=False, trace=True)
+    assert t["exact_router_fallbacks"] == 1
+    check_layer(L, x, False, xo, t)
+
+
+def test_multi_token_equals_per_token(gpu):
+    say("case n_tok=3")
+    d = 960
+    L = synth.gptoss_layer(d, d, 16, 4, seed=4)
+    X = np.stack([synth.token(d, 4, i) for i in range(3)])
+    cfg = MoeConfig.gptoss(d=d, n_expert=16, top_k=4, d_ff=d, max_tokens=3)
+    with MoeBlock(cfg) as blk:
+        blk.load_layer(0, L)
+        Y, _ = blk.forward(0, X, apply_norm=True)
+        for i in range(3):
+            y, _ = blk.forward(0, X[i], apply_norm=True)
+            assert np.array_equal(y.view(np.uint32), Y[i].view(np.uint32))
+
+
+def test_device_stack_vs_oracle(gpu):
+    import torch
+    say("case 3-layer device stack")
+    d, ne, k, nl = 2880, 32, 4, 3
+    layers = [synth.gptoss_layer(d, d, ne, k, seed=0, layer=l, zipf=1.1) for l in range(nl)]
+    cfg = MoeConfig.gptoss(d=d, n_expert=ne, top_k=k, d_ff=d, n_layer=nl)
+    x = synth.token(d, 0, 0)
+    with MoeBlock(cfg) as blk:
+        for l in range(nl):
+            blk.load_layer(l, layers[l])
+        xd = torch.from_numpy(x.copy()).to("cuda:0")
+        torch.cuda.synchronize()
+        blk.forward_device(0, nl, xd.data_ptr(), 1, True)
+        blk.sync()
+        y = xd.cpu().numpy()
+    xr = x.copy()
+    for l in range(nl):
+        xr, _ = O.gptoss_moe(layers[l], xr, True)
+    rms = np.sqrt(((xr - x).astype(np.float64) ** 2).mean())
+    assert np.max(np.abs(y - xr)) <= 1e-3 * rms
