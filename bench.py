@@ -113,7 +113,10 @@ def main() -> int:
     log(f"loaded {nl} layers in {time.perf_counter() - t0:.1f} s "
         f"({MoeBlock.layer_bytes(cfg) * nl / 1e9:.2f} GB of expert weights in HBM)")
 
-    stream = torch.cuda.current_stream()
+    # a dedicated (non-default) stream: the library launches on it and the
+    # timing events below are recorded on it
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
     blk.set_stream(stream.cuda_stream)
     x = torch.from_numpy(synth.token(d, 0, 0)).to(dev)
 

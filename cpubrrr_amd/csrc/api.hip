@@ -10,8 +10,12 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <algorithm>
+#include <cstdlib>
 #include <cstring>
+#include <map>
 #include <string>
+#include <tuple>
 #include <vector>
 
 #include "cpb_moe.h"
@@ -81,6 +85,9 @@ struct cpb_moe {
     // staging for raw GGUF bytes at load time
     uint8_t* staging = nullptr;
     size_t staging_size = 0;
+    // captured HIP graphs of forward_device calls, keyed by their arguments
+    std::map<std::tuple<int, int, float*, int, int, hipStream_t>, hipGraphExec_t> graphs;
+    bool use_graphs = true;
     // timing
     bool timing = false;
     std::vector<hipEvent_t> ev_pool;
@@ -200,6 +207,11 @@ int ensure_trace(cpb_moe_t* h) {
     return 0;
 }
 
+void clear_graphs(cpb_moe_t* h) {
+    for (auto& g : h->graphs) hipGraphExecDestroy(g.second);
+    h->graphs.clear();
+}
+
 // One token through one layer, x at device address dx.
 int layer_token(cpb_moe_t* h, int layer, float* dx, int apply_norm, bool trace) {
     const auto& c = h->cfg;
@@ -211,16 +223,21 @@ int layer_token(cpb_moe_t* h, int layer, float* dx, int apply_norm, bool trace) 
     ra.norm = c.norm; ra.norm_nt = c.norm_nt; ra.apply_norm = apply_norm; ra.eps = c.rms_eps;
     ra.qk = h->mx ? 0 : 1;
     ra.xn = h->xn; ra.xq = h->xq; ra.xqn = h->xqn; ra.xsb = h->xsb; ra.xsum = h->xsum;
-    ra.lstar = h->lstar; ra.lbound = h->lbound; ra.counter = h->counter;
-    ra.logits = h->logits; ra.ids = h->ids; ra.wts = h->wts; ra.fallback = h->fallback;
+    ra.lstar = h->lstar; ra.lbound = h->lbound;
+    cpb::SelectArgs sa{};
+    sa.lstar = h->lstar; sa.lbound = h->lbound; sa.router_w = L.router_w; sa.router_b = L.router_b; sa.xn = h->xn;
+    sa.d = c.d; sa.n_expert = c.n_expert; sa.top_k = c.top_k;
+    sa.ids = h->ids; sa.wts = h->wts; sa.logits = h->logits; sa.fallback = h->fallback;
     {
         Timer tm(h, 0);
         if (cpb::launch_route(&ra, h->stream)) return fail(CPB_ENODEV, "route launch failed");
+        if (cpb::launch_select(&sa, h->stream)) return fail(CPB_ENODEV, "select launch failed");
     }
     if (h->mx) {
         cpb::GateUpArgs g{};
         g.w = L.gu; g.gate_b = L.gate_b; g.up_b = L.up_b;
-        g.xq = h->xq; g.xqn = h->xqn; g.xsb = h->xsb; g.ids = h->ids;
+        g.xq = h->xq; g.xqn = h->xqn; g.xsb = h->xsb;
+        g.ids = h->ids;
         g.dff = c.d_ff; g.nb = h->nb; g.nparts = h->parts_gu; g.top_k = c.top_k;
         g.alpha = c.alpha; g.limit = c.limit;
         g.hq = h->hq; g.hqn = h->hqn; g.hsb = h->hsb;
@@ -323,6 +340,8 @@ int cpb_moe_load_layer(cpb_moe_t* h, int layer, const void* gate, const void* up
     if (c.has_bias && (!gate_b || !up_b || !down_b || !router_b))
         return fail(CPB_EINVAL, "has_bias set but a bias pointer is NULL");
     HIP_OK(hipSetDevice(h->device));
+    HIP_OK(hipStreamSynchronize(h->stream));
+    clear_graphs(h);
     LayerDev& L = h->layers[layer];
     free_layer(L);
     const size_t ne = c.n_expert, d = c.d, ff = c.d_ff;
@@ -362,14 +381,42 @@ int cpb_moe_load_layer(cpb_moe_t* h, int layer, const void* gate, const void* up
     return 0;
 }
 
+static int launch_direct(cpb_moe_t* h, int layer0, int n_layers, float* d_x, int n_tok, int apply_norm) {
+    const auto& c = h->cfg;
+    for (int l = layer0; l < layer0 + n_layers; l++)
+        for (int t = 0; t < n_tok; t++)
+            if (int r = layer_token(h, l, d_x + (size_t)t * c.d, apply_norm, false)) return r;
+    return 0;
+}
+
 int cpb_moe_forward_device(cpb_moe_t* h, int layer0, int n_layers, float* d_x, int n_tok, int apply_norm) {
     if (!h || !d_x) return fail(CPB_EINVAL, "NULL argument");
     const auto& c = h->cfg;
     if (layer0 < 0 || n_layers < 0 || layer0 + n_layers > c.n_layer) return fail(CPB_EINVAL, "layer range out of bounds");
     if (n_tok < 1 || n_tok > c.max_tokens) return fail(CPB_EINVAL, "n_tok=%d outside [1, max_tokens=%d]", n_tok, c.max_tokens);
     for (int l = layer0; l < layer0 + n_layers; l++)
-        for (int t = 0; t < n_tok; t++)
-            if (int r = layer_token(h, l, d_x + (size_t)t * c.d, apply_norm, false)) return r;
+        if (!h->layers[l].loaded) return fail(CPB_ESTATE, "layer %d not loaded", l);
+    HIP_OK(hipSetDevice(h->device));
+    // per-kernel timing needs one event pair per launch: run those directly
+    if (h->timing || !h->use_graphs) return launch_direct(h, layer0, n_layers, d_x, n_tok, apply_norm);
+    // otherwise replay one captured graph per distinct call (launch overhead
+    // of ~3 kernels per layer paid once)
+    auto key = std::make_tuple(layer0, n_layers, d_x, n_tok, apply_norm, h->stream);
+    auto it = h->graphs.find(key);
+    if (it == h->graphs.end()) {
+        HIP_OK(hipStreamBeginCapture(h->stream, hipStreamCaptureModeThreadLocal));
+        int r = launch_direct(h, layer0, n_layers, d_x, n_tok, apply_norm);
+        hipGraph_t g = nullptr;
+        hipError_t ec = hipStreamEndCapture(h->stream, &g);
+        if (r) { if (g) hipGraphDestroy(g); return r; }
+        if (ec != hipSuccess) return fail(CPB_ENODEV, "graph capture failed: %s", hipGetErrorString(ec));
+        hipGraphExec_t ge = nullptr;
+        ec = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+        hipGraphDestroy(g);
+        if (ec != hipSuccess) return fail(CPB_ENODEV, "graph instantiate failed: %s", hipGetErrorString(ec));
+        it = h->graphs.emplace(key, ge).first;
+    }
+    HIP_OK(hipGraphLaunch(it->second, h->stream));
     return 0;
 }
 
@@ -463,6 +510,7 @@ void cpb_moe_destroy(cpb_moe_t* h) {
     if (!h) return;
     hipSetDevice(h->device);
     if (h->stream) hipStreamSynchronize(h->stream);
+    clear_graphs(h);
     for (auto& L : h->layers) free_layer(L);
     void* bufs[] = {h->x, h->xn, h->xq, h->xqn, h->xsb, h->xsum, h->lstar, h->lbound, h->counter, h->logits,
                     h->ids, h->wts, h->fallback, h->hq, h->hqn, h->hsb, h->hsum, h->hbuf, h->t_gu, h->t_h,

@@ -13,7 +13,7 @@ struct GateUpArgs {
     const int8_t* xq;        // [d]
     const int8_t* xqn;       // [d]
     const float* xsb;        // [d/32]
-    const int32_t* ids;      // [top_k]
+    const int32_t* ids;      // [top_k] selected experts (k_select)
     int dff, nb, nparts, top_k;
     float alpha, limit;
     int8_t* hq;              // [top_k][dff]

@@ -19,15 +19,24 @@ struct RouteArgs {
     int8_t* xqn;             // [d]  negated xq
     float* xsb;              // [d/32] or [d/256]
     int32_t* xsum;           // [d/32] (qk == 1)
-    double* lstar;           // [ne] scratch
-    double* lbound;          // [ne] scratch
-    unsigned* counter;       // zero between launches
-    float* logits;           // [ne]
+    double* lstar;           // [ne] exact fp64 logit of the reference's fp32 products
+    double* lbound;          // [ne] bound on |reference serial fp32 logit - lstar|
+};
+
+struct SelectArgs {
+    const double* lstar;
+    const double* lbound;
+    const float* router_w;   // exact fallback only
+    const float* router_b;
+    const float* xn;
+    int d, n_expert, top_k;
     int32_t* ids;            // [top_k]
     float* wts;              // [top_k]
-    int32_t* fallback;       // 1 when the exact serial router was needed
+    float* logits;           // [ne]
+    int32_t* fallback;       // [1]
 };
 
 int launch_route(const RouteArgs* a, hipStream_t s);
+int launch_select(const SelectArgs* a, hipStream_t s);
 
 }  // namespace cpb
