@@ -20,6 +20,7 @@
 
 #include "cpb_moe.h"
 #include "moe_kq.h"
+#include "decode_mx.h"
 #include "moe_mx.h"
 #include "route.h"
 
@@ -85,6 +86,14 @@ struct cpb_moe {
     // staging for raw GGUF bytes at load time
     uint8_t* staging = nullptr;
     size_t staging_size = 0;
+    // persistent decode (MXFP4, one token): per-layer pointers, phase counters
+    cpb::LayerPtrs* d_layers = nullptr;
+    unsigned* d_sync = nullptr;
+    int32_t* d_error = nullptr;
+    std::map<std::tuple<int, int, float*, int>, cpb::DecodeArgs*> decode_args;
+    bool persistent = false;  // the single-launch decode is opt-in (CPB_PERSISTENT=1)
+    bool prepare_only = false;
+    unsigned long long* d_stamps = nullptr;   // probe builds: persistent-decode phase timestamps
     // captured HIP graphs of forward_device calls, keyed by their arguments
     std::map<std::tuple<int, int, float*, int, int, hipStream_t>, hipGraphExec_t> graphs;
     bool use_graphs = true;
@@ -207,6 +216,17 @@ int ensure_trace(cpb_moe_t* h) {
     return 0;
 }
 
+// A bounded wait inside the persistent kernel expired: re-arm the phase
+// counters and report.  (Called after a stream synchronisation.)
+int check_device_error(cpb_moe_t* h) {
+    int32_t err = 0;
+    HIP_OK(hipMemcpy(&err, h->d_error, sizeof err, hipMemcpyDeviceToHost));
+    if (!err) return 0;
+    HIP_OK(hipMemset(h->d_sync, 0, sizeof(unsigned) * (3 * (size_t)h->cfg.n_layer + 1)));
+    HIP_OK(hipMemset(h->d_error, 0, sizeof(int32_t)));
+    return fail(CPB_ENODEV, "persistent decode: a phase wait timed out (workgroups not co-resident?)");
+}
+
 void clear_graphs(cpb_moe_t* h) {
     for (auto& g : h->graphs) hipGraphExecDestroy(g.second);
     h->graphs.clear();
@@ -322,6 +342,17 @@ int cpb_moe_create(const cpb_moe_cfg* cfg, int device, cpb_moe_t** out) {
         (r = dmalloc(&h->fallback, 1)) || (r = dmalloc(&h->hq, k * ff)) || (r = dmalloc(&h->hqn, k * ff)) ||
         (r = dmalloc(&h->hsb, k * ff / 32)) || (r = dmalloc(&h->hsum, k * ff / 32)) || (r = dmalloc(&h->hbuf, k * ff)))
         return bail(r);
+    if ((r = dmalloc(&h->d_layers, (size_t)cfg->n_layer)) || (r = dmalloc(&h->d_sync, 3 * (size_t)cfg->n_layer + 1)) ||
+        (r = dmalloc(&h->d_error, 1)))
+        return bail(r);
+    if (hipMemsetAsync(h->d_sync, 0, sizeof(unsigned) * (3 * (size_t)cfg->n_layer + 1), h->stream) != hipSuccess ||
+        hipMemsetAsync(h->d_error, 0, sizeof(int32_t), h->stream) != hipSuccess ||
+        hipMemsetAsync(h->d_layers, 0, sizeof(cpb::LayerPtrs) * cfg->n_layer, h->stream) != hipSuccess)
+        return bail(fail(CPB_ENODEV, "init memset failed"));
+    if (const char* v = getenv("CPB_PERSISTENT")) h->persistent = v[0] == '1';
+#ifdef CPB_DECODE_STAMPS
+    if ((r = dmalloc(&h->d_stamps, (size_t)1024 * cfg->n_layer * 8))) return bail(r);
+#endif
     if (hipMemsetAsync(h->counter, 0, sizeof(unsigned), h->stream) != hipSuccess ||
         hipMemsetAsync(h->fallback, 0, sizeof(int32_t), h->stream) != hipSuccess ||
         hipStreamSynchronize(h->stream) != hipSuccess)
@@ -376,13 +407,51 @@ int cpb_moe_load_layer(cpb_moe_t* h, int layer, const void* gate, const void* up
     }
     if ((r = upload(&L.router_w, router_w, ne * d, h->stream))) return r;
     if ((r = upload(&L.norm_w, norm_w, d, h->stream))) return r;
+    if (h->mx) {
+        cpb::LayerPtrs lp{L.gu, L.dn, L.gate_b, L.up_b, L.down_b, L.router_w, L.router_b, L.norm_w};
+        HIP_OK(hipMemcpyAsync(h->d_layers + layer, &lp, sizeof lp, hipMemcpyHostToDevice, h->stream));
+    }
     HIP_OK(hipStreamSynchronize(h->stream));
     L.loaded = true;
     return 0;
 }
 
+// Persistent single-launch decode of layers [layer0, layer0 + n_layers) for
+// one token; returns -28 / -22 when the device or shape cannot take it.
+static int launch_persistent(cpb_moe_t* h, int layer0, int n_layers, float* d_x, int apply_norm) {
+    const auto& c = h->cfg;
+    auto key = std::make_tuple(layer0, n_layers, d_x, apply_norm);
+    cpb::DecodeArgs a{};
+    a.layers = h->d_layers; a.layer0 = layer0; a.n_layers = n_layers; a.x = d_x; a.apply_norm = apply_norm;
+    a.d = c.d; a.dff = c.d_ff; a.ne = c.n_expert; a.k = c.top_k; a.nb = h->nb; a.nbf = h->nbf;
+    a.parts = std::max(h->parts_gu, h->parts_dn);
+    a.alpha = c.alpha; a.limit = c.limit; a.eps = c.rms_eps; a.norm = c.norm; a.norm_nt = c.norm_nt;
+    a.T_gu = c.top_k * (c.d_ff / 32); a.T_dn = c.d / (64 / c.top_k);
+    a.xn = h->xn; a.xq = h->xq; a.xqn = h->xqn; a.xsb = h->xsb; a.lstar = h->lstar; a.lbound = h->lbound;
+    a.ids = h->ids; a.wts = h->wts; a.logits = h->logits; a.fallback = h->fallback;
+    a.hq = h->hq; a.hqn = h->hqn; a.hsb = h->hsb; a.sync = h->d_sync; a.error = h->d_error;
+    a.stamps = h->d_stamps;
+    if (h->parts_gu != h->parts_dn) return -22;
+    auto it = h->decode_args.find(key);
+    if (it == h->decode_args.end()) {
+        // (never reached under stream capture: cpb_moe_forward_device prepares the args first)
+        cpb::DecodeArgs* dv = nullptr;
+        if (hipMalloc((void**)&dv, sizeof a) != hipSuccess) return fail(CPB_ENOMEM, "hipMalloc(decode args)");
+        if (hipMemcpy(dv, &a, sizeof a, hipMemcpyHostToDevice) != hipSuccess) { hipFree(dv); return fail(CPB_ENODEV, "args copy"); }
+        it = h->decode_args.emplace(key, dv).first;
+    }
+    if (h->prepare_only) return 0;
+    return cpb::launch_decode_mx(a, it->second, h->stream);
+}
+
 static int launch_direct(cpb_moe_t* h, int layer0, int n_layers, float* d_x, int n_tok, int apply_norm) {
     const auto& c = h->cfg;
+    if (h->mx && n_tok == 1 && h->persistent && !h->timing) {
+        const int r = launch_persistent(h, layer0, n_layers, d_x, apply_norm);
+        if (r == 0) return 0;
+        if (r != -28 && r != -22) return fail(CPB_ENODEV, "persistent decode launch failed (%d)", r);
+        h->persistent = false;          // shape/device cannot host it: per-phase kernels from now on
+    }
     for (int l = layer0; l < layer0 + n_layers; l++)
         for (int t = 0; t < n_tok; t++)
             if (int r = layer_token(h, l, d_x + (size_t)t * c.d, apply_norm, false)) return r;
@@ -399,6 +468,13 @@ int cpb_moe_forward_device(cpb_moe_t* h, int layer0, int n_layers, float* d_x, i
     HIP_OK(hipSetDevice(h->device));
     // per-kernel timing needs one event pair per launch: run those directly
     if (h->timing || !h->use_graphs) return launch_direct(h, layer0, n_layers, d_x, n_tok, apply_norm);
+    // device-side argument blocks are allocated before any stream capture
+    if (h->mx && n_tok == 1 && h->persistent) {
+        h->prepare_only = true;
+        const int r = launch_persistent(h, layer0, n_layers, d_x, apply_norm);
+        h->prepare_only = false;
+        if (r != 0 && r != -28 && r != -22) return r;
+    }
     // otherwise replay one captured graph per distinct call (launch overhead
     // of ~3 kernels per layer paid once)
     auto key = std::make_tuple(layer0, n_layers, d_x, n_tok, apply_norm, h->stream);
@@ -465,7 +541,7 @@ int cpb_moe_forward(cpb_moe_t* h, int layer, float* x, int n_tok, int apply_norm
         if (r) return r;
     }
     HIP_OK(hipStreamSynchronize(h->stream));
-    return 0;
+    return check_device_error(h);
 }
 
 int cpb_moe_set_stream(cpb_moe_t* h, void* stream) {
@@ -477,7 +553,7 @@ int cpb_moe_set_stream(cpb_moe_t* h, void* stream) {
 int cpb_moe_sync(cpb_moe_t* h) {
     if (!h) return fail(CPB_EINVAL, "handle is NULL");
     HIP_OK(hipStreamSynchronize(h->stream));
-    return 0;
+    return check_device_error(h);
 }
 
 int cpb_moe_timing(cpb_moe_t* h, int enable) {
@@ -511,6 +587,19 @@ void cpb_moe_destroy(cpb_moe_t* h) {
     hipSetDevice(h->device);
     if (h->stream) hipStreamSynchronize(h->stream);
     clear_graphs(h);
+    for (auto& kv : h->decode_args) hipFree(kv.second);
+#ifdef CPB_DECODE_STAMPS
+    if (h->d_stamps) {
+        const char* path = getenv("CPB_DECODE_STAMPS_FILE");
+        size_t n = (size_t)1024 * h->cfg.n_layer * 8;
+        std::vector<unsigned long long> st(n);
+        hipMemcpy(st.data(), h->d_stamps, n * 8, hipMemcpyDeviceToHost);
+        FILE* f = path ? fopen(path, "wb") : nullptr;
+        if (f) { fwrite(st.data(), 8, n, f); fclose(f); }
+        hipFree(h->d_stamps);
+    }
+#endif
+    hipFree(h->d_layers); hipFree(h->d_sync); hipFree(h->d_error);
     for (auto& L : h->layers) free_layer(L);
     void* bufs[] = {h->x, h->xn, h->xq, h->xqn, h->xsb, h->xsum, h->lstar, h->lbound, h->counter, h->logits,
                     h->ids, h->wts, h->fallback, h->hq, h->hqn, h->hsb, h->hsum, h->hbuf, h->t_gu, h->t_h,

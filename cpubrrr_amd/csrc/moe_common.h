@@ -4,6 +4,7 @@
 #include <stdint.h>
 
 #define CPB_DEV __device__ __forceinline__
+#define CPB_DEV_HOST_INLINE __host__ __device__ inline
 
 namespace cpb {
 
@@ -87,5 +88,29 @@ CPB_DEV float wave_max(float v) {
 
 template <class T>
 CPB_DEV T uniform(T v) { return (T)__builtin_amdgcn_readfirstlane((int)v); }
+// a wave-uniform pointer kept in SGPRs
+template <class T>
+CPB_DEV T* uniform_ptr(T* p) {
+    const uint64_t v = (uint64_t)(uintptr_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return (T*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+
+// Device-coherent access for the small buffers that workgroups hand to each
+// other inside one launch (activations, routing results, hq, x).  Relaxed
+// agent-scope atomics compile to plain loads/stores with the sc1 bit, which
+// keep them coherent across the XCDs' separate L2s without the device-wide
+// L2 writeback / invalidate that a __threadfence() costs.
+template <class T>
+CPB_DEV T ld_dev(const T* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+template <class T>
+CPB_DEV void st_dev(T* p, T v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+// Wait until every memory operation this wave issued has completed.
+CPB_DEV void drain_memory() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
 
 }  // namespace cpb

@@ -36,7 +36,7 @@ CPB_DEV void select_experts_wave(const double* __restrict__ Ls, const double* __
     double* sH = lds + NE;       // [NE] upper bounds
     int* sR = (int*)(lds + 2 * NE);          // [NE] ranks
     int* sSel = (int*)(lds + 3 * NE);        // [8] expert at rank i
-    for (int e = lane; e < NE; e += 64) { sL[e] = Ls[e]; sH[e] = Ls[e] + Bs[e]; }
+    for (int e = lane; e < NE; e += 64) { const double l = ld_dev(Ls + e); sL[e] = l; sH[e] = l + ld_dev(Bs + e); }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -73,7 +73,7 @@ CPB_DEV void select_experts_wave(const double* __restrict__ Ls, const double* __
             if (sH[e] >= tau) {
                 float acc = router_b ? router_b[e] : 0.0f;
                 const float* Wr = router_w + (size_t)e * d;
-                for (int j = 0; j < d; j++) acc = __fadd_rn(acc, __fmul_rn(Wr[j], xn[j]));
+                for (int j = 0; j < d; j++) acc = __fadd_rn(acc, __fmul_rn(Wr[j], ld_dev(xn + j)));
                 v = (double)acc;
             }
             sL[e] = v;

@@ -100,6 +100,26 @@ def test_router_tie_uses_exact_fallback(gpu):
     check_layer(L, x, False, xo, t)
 
 
+def test_persistent_matches_phased(gpu, monkeypatch):
+    # the single-launch decode and the per-phase kernels give identical bits
+    import torch
+    say("case persistent vs phased, 4 layers 20b shape")
+    d, ne, k, nl = 2880, 32, 4, 4
+    layers = [synth.gptoss_layer(d, d, ne, k, seed=3, layer=l, zipf=1.1) for l in range(nl)]
+    outs = []
+    for phased in (False, True):
+        monkeypatch.setenv("CPB_PERSISTENT", "0" if phased else "1")
+        with MoeBlock(MoeConfig.gptoss(d=d, n_expert=ne, top_k=k, d_ff=d, n_layer=nl)) as blk:
+            for l in range(nl):
+                blk.load_layer(l, layers[l])
+            x = torch.from_numpy(synth.token(d, 3, 0)).to("cuda:0")
+            for rep in range(3):
+                blk.forward_device(0, nl, x.data_ptr(), 1, True)
+            blk.sync()
+            outs.append(x.cpu().numpy())
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+
+
 def test_multi_token_equals_per_token(gpu):
     say("case n_tok=3")
     d = 960
@@ -114,9 +134,11 @@ def test_multi_token_equals_per_token(gpu):
             assert np.array_equal(y.view(np.uint32), Y[i].view(np.uint32))
 
 
-def test_device_stack_vs_oracle(gpu):
+@pytest.mark.parametrize("phased", [False, True])
+def test_device_stack_vs_oracle(gpu, phased, monkeypatch):
     import torch
-    say("case 3-layer device stack")
+    monkeypatch.setenv("CPB_PERSISTENT", "0" if phased else "1")
+    say(f"case 3-layer device stack phased={phased}")
     d, ne, k, nl = 2880, 32, 4, 3
     layers = [synth.gptoss_layer(d, d, ne, k, seed=0, layer=l, zipf=1.1) for l in range(nl)]
     cfg = MoeConfig.gptoss(d=d, n_expert=ne, top_k=k, d_ff=d, n_layer=nl)
