@@ -71,7 +71,7 @@ struct cpb_moe {
     float* xsb = nullptr;
     int32_t* xsum = nullptr;
     double *lstar = nullptr, *lbound = nullptr;
-    unsigned* counter = nullptr;
+    unsigned* counter = nullptr;          // route workgroup arrivals (zero between launches)
     float* logits = nullptr;
     int32_t* ids = nullptr;
     float* wts = nullptr;
@@ -244,14 +244,14 @@ int layer_token(cpb_moe_t* h, int layer, float* dx, int apply_norm, bool trace) 
     ra.qk = h->mx ? 0 : 1;
     ra.xn = h->xn; ra.xq = h->xq; ra.xqn = h->xqn; ra.xsb = h->xsb; ra.xsum = h->xsum;
     ra.lstar = h->lstar; ra.lbound = h->lbound;
+    ra.stamps = h->d_stamps;
     cpb::SelectArgs sa{};
     sa.lstar = h->lstar; sa.lbound = h->lbound; sa.router_w = L.router_w; sa.router_b = L.router_b; sa.xn = h->xn;
     sa.d = c.d; sa.n_expert = c.n_expert; sa.top_k = c.top_k;
     sa.ids = h->ids; sa.wts = h->wts; sa.logits = h->logits; sa.fallback = h->fallback;
     {
         Timer tm(h, 0);
-        if (cpb::launch_route(&ra, h->stream)) return fail(CPB_ENODEV, "route launch failed");
-        if (cpb::launch_select(&sa, h->stream)) return fail(CPB_ENODEV, "select launch failed");
+        if (cpb::launch_route(&ra, &sa, h->counter, h->stream)) return fail(CPB_ENODEV, "route launch failed");
     }
     if (h->mx) {
         cpb::GateUpArgs g{};

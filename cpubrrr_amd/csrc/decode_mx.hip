@@ -212,7 +212,7 @@ CPB_DEV void decode_layer(const DecodeArgs& a, int li, Selection& sel,
     __syncthreads();
     if (w == 0 && threadIdx.x < 64) {
         const int lane = threadIdx.x;
-        for (int i = lane; i < a.ne; i += 64) a.logits[i] = (float)a.lstar[i];
+        for (int i = lane; i < a.ne; i += 64) a.logits[i] = (float)ld_dev(a.lstar + i);
         if (lane < a.k) {
             a.ids[lane] = sel.ids[lane];
             a.wts[lane] = sel.wts[lane];

@@ -93,31 +93,23 @@ CPB_DEV float e8m0_times(float s, uint32_t e) {
     return e == 255u ? r * 2.0f : r;
 }
 
-// Buffer resource over [base, base + bytes): a load whose offset lies outside
-// returns zeros without touching memory, so masked loads need no branch and
-// the compiler can wait for each load by count.
-CPB_DEV __amdgpu_buffer_rsrc_t mf_rsrc(const void* base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(const_cast<void*>(base)), (short)0, (int)uniform(bytes), 0x00020000);
-}
-constexpr uint32_t kMfOff = 0x80000000u;   // an offset beyond every range
-
 // Start the weight loads of groups [gi0, gi1) of rowgroup rg (nontemporal).
 CPB_DEV void mf_issue(MfRegs& r, const uint8_t* __restrict__ rg, int nb, int gi0, int gi1) {
     const int lane = threadIdx.x & 63;
     const int n = lane & 15, g = lane >> 4;
-    const __amdgpu_buffer_rsrc_t rs = mf_rsrc(rg, (uint32_t)mf_rowgroup_bytes(nb));
+    const __amdgpu_buffer_rsrc_t rs = buf_rsrc(rg, (uint32_t)mf_rowgroup_bytes(nb));
     gi0 = uniform(gi0); gi1 = uniform(gi1); nb = uniform(nb);
 #pragma unroll
     for (int j = 0; j < kMaxGroups; j++) {
         const int gi = gi0 + j;
         const int gb = gi < gi1 ? min(16, nb - 16 * gi) : 0;
         const uint32_t go = (uint32_t)mf_group_offset(gi);
-        r.ev[j] = __builtin_amdgcn_raw_buffer_load_b128(rs, gb > 0 ? go + n * 16 : kMfOff, 0, 2);
+        r.ev[j] = __builtin_amdgcn_raw_buffer_load_b128(rs, gb > 0 ? go + n * 16 : kOffNone, 0, 2);
 #pragma unroll
         for (int w = 0; w < 4; w++) {
             const bool has = g < gb - 4 * w;
             r.wv[j][w] = __builtin_amdgcn_raw_buffer_load_b128(
-                rs, has ? go + 256 + w * 1024 + g * 256 + n * 16 : kMfOff, 0, 2);
+                rs, has ? go + 256 + w * 1024 + g * 256 + n * 16 : kOffNone, 0, 2);
         }
     }
 }

@@ -107,6 +107,17 @@ CPB_DEV T ld_dev(const T* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __H
 template <class T>
 CPB_DEV void st_dev(T* p, T v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 // Wait until every memory operation this wave issued has completed.
+// Buffer resource over [base, base + bytes) (wave-uniform base): a buffer
+// load whose offset lies outside returns zeros without touching memory, so
+// masked loads need no branch and the compiler waits for them by count.
+CPB_DEV __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(const_cast<void*>(base)), (short)0, (int)uniform(bytes), 0x00020000);
+}
+constexpr uint32_t kOffNone = 0x80000000u;   // a buffer offset beyond every range
+// 16-byte load with the cache policy of ld_dev (sc1: coherent across XCDs)
+CPB_DEV u32x4 ld_dev16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 16);
+}
 CPB_DEV void drain_memory() {
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_waitcnt(0);

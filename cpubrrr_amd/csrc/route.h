@@ -21,6 +21,7 @@ struct RouteArgs {
     int32_t* xsum;           // [d/32] (qk == 1)
     double* lstar;           // [ne] exact fp64 logit of the reference's fp32 products
     double* lbound;          // [ne] bound on |reference serial fp32 logit - lstar|
+    unsigned long long* stamps;  // probe builds (CPB_DECODE_STAMPS) only: [ne][16] phase clocks
 };
 
 struct SelectArgs {
@@ -36,7 +37,9 @@ struct SelectArgs {
     int32_t* fallback;       // [1]
 };
 
-int launch_route(const RouteArgs* a, hipStream_t s);
+// Routing and selection in one launch; `arrive` is a zero-initialised
+// counter that the launch leaves at zero.
+int launch_route(const RouteArgs* a, const SelectArgs* sa, unsigned* arrive, hipStream_t s);
 int launch_select(const SelectArgs* a, hipStream_t s);
 
 }  // namespace cpb

@@ -17,7 +17,23 @@ namespace cpb {
 CPB_DEV void norm_into(const float* __restrict__ xg, const float* __restrict__ nw, int d, float eps,
                        int norm, int nt, int apply, float* xs, float* xn, float* scratch) {
     const int tid = threadIdx.x, nth = blockDim.x;
-    for (int i = tid; i < d; i += nth) xs[i] = ld_dev(xg + i);
+    // x may have been written by other workgroups of the same launch:
+    // coherent 16-byte loads.  Thread tid owns float4 slots tid + k*nth
+    // (nth * 16 >= d for every launch: d <= 4096, nth >= 256); the norm
+    // weights of the same slots are fetched alongside, before the first wait.
+    u32x4 wn[4];
+    {
+        const __amdgpu_buffer_rsrc_t r = buf_rsrc(xg, (uint32_t)d * 4);
+        const __amdgpu_buffer_rsrc_t rw = buf_rsrc(nw, nw && apply ? (uint32_t)d * 4 : 0u);
+        u32x4 v[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) v[k] = ld_dev16(r, (uint32_t)(tid + k * nth) * 16);
+#pragma unroll
+        for (int k = 0; k < 4; k++) wn[k] = __builtin_amdgcn_raw_buffer_load_b128(rw, (uint32_t)(tid + k * nth) * 16, 0, 0);
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+            if ((tid + k * nth) * 4 < d) ((u32x4*)xs)[tid + k * nth] = v[k];
+    }
     __syncthreads();
     if (!apply) {
         for (int i = tid; i < d / 4; i += nth) ((float4*)xn)[i] = ((const float4*)xs)[i];
@@ -72,7 +88,23 @@ CPB_DEV void norm_into(const float* __restrict__ xg, const float* __restrict__ n
     }
     __syncthreads();
     const float inv = scratch[16];
-    for (int i = tid; i < d; i += nth) xn[i] = xs[i] * inv * (nw ? nw[i] : 1.0f);
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int i4 = tid + k * nth;
+        if (i4 * 4 < d) {
+            const float4 xv = ((const float4*)xs)[i4];
+            float4 o;
+            if (nw) {
+                o.x = xv.x * inv * __uint_as_float(wn[k][0]);
+                o.y = xv.y * inv * __uint_as_float(wn[k][1]);
+                o.z = xv.z * inv * __uint_as_float(wn[k][2]);
+                o.w = xv.w * inv * __uint_as_float(wn[k][3]);
+            } else {
+                o.x = xv.x * inv; o.y = xv.y * inv; o.z = xv.z * inv; o.w = xv.w * inv;
+            }
+            ((float4*)xn)[i4] = o;
+        }
+    }
     __syncthreads();
 }
 
@@ -90,6 +122,12 @@ CPB_DEV T block_sum(T v, T* red) {
     return r;
 }
 
+#ifdef CPB_DECODE_STAMPS
+#define RSTAMP(i) do { if (threadIdx.x == 0 && a.stamps) a.stamps[(size_t)e * 16 + (i)] = wall_clock64(); } while (0)
+#else
+#define RSTAMP(i) do { } while (0)
+#endif
+
 constexpr int kChunk = 16;          // router elements per thread: d <= 4096
 
 // LDS bytes route_expert needs
@@ -106,6 +144,7 @@ CPB_DEV void route_expert(const RouteArgs& a, int e, int NEg, unsigned char* sme
     float* scratch = (float*)(dred + 16);     // [64]
     const int tid = threadIdx.x, nth = blockDim.x;
     const int d = a.d;
+    RSTAMP(0);
 
     // router row chunk of this thread, loaded before anything waits on x
     const int C = ((d + 4 * nth - 1) / (4 * nth)) * 4;   // multiple of 4, C*nth >= d
@@ -119,7 +158,9 @@ CPB_DEV void route_expert(const RouteArgs& a, int e, int NEg, unsigned char* sme
     }
     const double b = a.router_b ? (double)a.router_b[e] : 0.0;
 
+    RSTAMP(1);
     norm_into(a.x, a.norm_w, d, a.eps, a.norm, a.norm_nt, a.apply_norm, xs, xn, scratch);
+    RSTAMP(2);
 
     // quantisation, distributed over the workgroups (each also publishes the
     // xn values of its blocks)
@@ -161,6 +202,7 @@ CPB_DEV void route_expert(const RouteArgs& a, int e, int NEg, unsigned char* sme
         }
     }
 
+    RSTAMP(3);
     // ---- router logit of expert e: the reference's fp32 products, exact
     // fp64 sum and prefix sums, error bound ----
     float p[kChunk];
@@ -199,6 +241,7 @@ CPB_DEV void route_expert(const RouteArgs& a, int e, int NEg, unsigned char* sme
     double sabs = 0.0;
 #pragma unroll
     for (int i = 0; i < kChunk; i++) { run += (double)p[i]; sabs += (i < C && j0 + i < d) ? fabs(run) : 0.0; }
+    RSTAMP(4);
     __syncthreads();
     const double SS = block_sum(sabs, dred);
     const double AP = block_sum(absp, dred);
@@ -212,6 +255,7 @@ CPB_DEV void route_expert(const RouteArgs& a, int e, int NEg, unsigned char* sme
         st_dev(a.lstar + e, total);
         st_dev(a.lbound + e, bound);
     }
+    RSTAMP(5);
 }
 
 

@@ -1,5 +1,5 @@
 // select.h -- top-k expert selection from certified router logits (one
-// wavefront, no LDS, no cross-workgroup synchronisation).
+// wavefront, LDS scratch, no cross-workgroup synchronisation).
 //
 // Inputs per expert e: Ls[e] = exact (fp64) sum of the reference's fp32
 // router products plus bias, Bs[e] = bound on |reference serial fp32 sum -
@@ -24,29 +24,56 @@ struct Selection {
 };
 
 // Executed by one wavefront (64 lanes).  lds: 4*NE doubles of scratch.
-// Lane l handles experts l, l+64, ...: rank_e = #{j : L_j > L_e or
+// Lane l handles experts l, l+64, ... (NE <= 256): rank_e = #{j : L_j > L_e or
 // (L_j == L_e and j < e)} from LDS broadcast reads, so every expert is ranked
-// in one pass with no dependent cross-lane steps.  Outputs ids/logit/wts in
-// rank order (written by lane 0 into `out`).
+// in one pass with no dependent cross-lane steps.  logits_out (optional)
+// receives the fp32 value of every expert's exact logit.  Outputs ids / logit
+// / wts in rank order into `out` (valid in every lane after the call).
 CPB_DEV void select_experts_wave(const double* __restrict__ Ls, const double* __restrict__ Bs, int NE, int K,
                                  const float* __restrict__ router_w, const float* __restrict__ router_b,
-                                 const float* __restrict__ xn, int d, double* lds, Selection* out) {
+                                 const float* __restrict__ xn, int d, double* lds, Selection* out,
+                                 float* logits_out = nullptr) {
     const int lane = threadIdx.x & 63;
     double* sL = lds;            // [NE] values used for ranking
     double* sH = lds + NE;       // [NE] upper bounds
     int* sR = (int*)(lds + 2 * NE);          // [NE] ranks
     int* sSel = (int*)(lds + 3 * NE);        // [8] expert at rank i
-    for (int e = lane; e < NE; e += 64) { const double l = ld_dev(Ls + e); sL[e] = l; sH[e] = l + ld_dev(Bs + e); }
+    // one coherent round trip for all values
+    double lv[4], bv[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int e = lane + 64 * k;
+        lv[k] = e < NE ? ld_dev(Ls + e) : 0.0;
+        bv[k] = e < NE ? ld_dev(Bs + e) : 0.0;
+    }
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int e = lane + 64 * k;
+        if (e < NE) {
+            sL[e] = lv[k];
+            sH[e] = lv[k] + bv[k];
+            if (logits_out) logits_out[e] = (float)lv[k];
+        }
+    }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    for (int e = lane; e < NE; e += 64) {
-        const double v = sL[e];
-        int r = 0;
+    int rk[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int e = lane + 64 * k;
+        rk[k] = NE;
+        if (64 * k < NE) {
+            const double v = lv[k];
+            int r = 0;
 #pragma unroll 16
-        for (int j = 0; j < NE; j++) { const double o = sL[j]; r += (o > v) || (o == v && j < e); }
-        sR[e] = r;
-        if (r < K) sSel[r] = e;
+            for (int j = 0; j < NE; j++) { const double o = sL[j]; r += (o > v) || (o == v && j < e); }
+            if (e < NE) {
+                rk[k] = r;
+                sR[e] = r;
+                if (r < K) sSel[r] = e;
+            }
+        }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -54,10 +81,11 @@ CPB_DEV void select_experts_wave(const double* __restrict__ Ls, const double* __
     // certification: the expert at rank r < K must lie strictly above every
     // expert ranked after it
     bool bad = false;
-    for (int e = lane; e < NE; e += 64) {
-        const int r = sR[e];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int r = rk[k];
         if (r < K) {
-            const double lo = sL[e] - (sH[e] - sL[e]);
+            const double lo = lv[k] - bv[k];
 #pragma unroll 16
             for (int j = 0; j < NE; j++) bad |= (sR[j] > r) & (sH[j] >= lo);
         }
@@ -91,14 +119,25 @@ CPB_DEV void select_experts_wave(const double* __restrict__ Ls, const double* __
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
-    if (lane == 0) {
-        // softmax over the k selected, reference order: ex_i = exp(l_i - l_0), serial sum
-        float e8[8], wsum = 0.0f;
-        for (int i = 0; i < K; i++) { out->ids[i] = sSel[i]; out->logit[i] = (float)sL[sSel[i]]; }
-        for (int i = 0; i < K; i++) { e8[i] = expf(out->logit[i] - out->logit[0]); wsum += e8[i]; }
-        for (int i = 0; i < K; i++) out->wts[i] = e8[i] / wsum;
-        out->fallback = ok ? 0 : 1;
+    // softmax over the k selected, reference order: ex_i = exp(l_i - l_0)
+    // (lane i), then the serial sum ex_0 + ex_1 + ... (every lane)
+    const int mi = lane < K ? lane : 0;
+    const int me = sSel[mi];
+    const float ml = (float)sL[me];
+    const float l0 = (float)sL[sSel[0]];
+    const float ex = expf(ml - l0);
+    float wsum = 0.0f;
+    for (int i = 0; i < K; i++) wsum += __shfl(ex, i);
+    const float wt = ex / wsum;
+    if (lane < K) {
+        out->ids[lane] = me;
+        out->logit[lane] = ml;
+        out->wts[lane] = wt;
     }
+    if (lane == 0) out->fallback = ok ? 0 : 1;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 }  // namespace cpb
