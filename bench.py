@@ -8,6 +8,7 @@ inputs resident in HBM.  Workloads (synthetic data):
      256 MB Infinity Cache cannot hold the active experts)
   1  gpt-oss-20b 24-layer MoE stack, Zipf(1.1) router bias   (default)
   2  gpt-oss-120b 36-layer stack, 128 experts, Zipf(1.1)
+  3  Qwen3-30B-A3B 48-layer MoE stack: Q4_K gate/up, Q6_K down, top-8 of 128
 Prints one JSON line: value = expert-weight GB/s (algorithmic bytes of the
 active experts + biases + router per token / time), plus tok/s, the roofline
 of the dominant kernel (gate/up) and the CPU baseline (the oracle on the
@@ -35,15 +36,25 @@ CONFIGS = {
             d=2880, dff=2880, ne=32, k=4, layers=24, per_step=24, zipf=1.1, norm=True),
     2: dict(name="config2: gpt-oss-120b 36-layer MoE stack, 128 experts, decode batch 1, Zipf(1.1) router bias",
             d=2880, dff=2880, ne=128, k=4, layers=36, per_step=36, zipf=1.1, norm=True),
+    3: dict(name="config3: Qwen3-30B-A3B 48-layer MoE stack (attention omitted), decode batch 1, Q4_K gate/up, "
+                 "Q6_K down, softmax then top-8 of 128",
+            d=2048, dff=768, ne=128, k=8, layers=48, per_step=48, zipf=None, norm=True, family="qwen"),
 }
+for _c in CONFIGS.values():
+    _c.setdefault("family", "gptoss")
 
 
 def layer_bytes(c) -> dict:
     """Algorithmic bytes one token reads per layer (active experts only)."""
     d, dff, ne, k = c["d"], c["dff"], c["ne"], c["k"]
-    gu = k * 2 * dff * (d // 32 * 17) + k * 2 * dff * 4
-    dn = k * d * (dff // 32 * 17) + k * d * 4
-    router = ne * d * 4 + ne * 4 + (d * 4 if c["norm"] else 0)
+    if c["family"] == "qwen":
+        gu = k * 2 * dff * (d // 256 * 144)                      # Q4_K gate + up rows
+        dn = k * d * (dff // 256 * 210)                          # Q6_K down rows
+        router = ne * d * 4 + (d * 4 if c["norm"] else 0)
+    else:
+        gu = k * 2 * dff * (d // 32 * 17) + k * 2 * dff * 4      # MXFP4 rows + fp32 biases
+        dn = k * d * (dff // 32 * 17) + k * d * 4
+        router = ne * d * 4 + ne * 4 + (d * 4 if c["norm"] else 0)
     return {"gate_up": gu, "down": dn, "router": router, "total": gu + dn + router}
 
 
@@ -63,9 +74,10 @@ def cpu_baseline(host_layers, c, budget_s: float) -> dict:
     x = synth.token(c["d"], 0, 12345)
     n = 0
     t0 = time.perf_counter()
+    fwd = O.qwen_moe if c["family"] == "qwen" else O.gptoss_moe
     while time.perf_counter() - t0 < budget_s or n == 0:
         L = host_layers[n % len(host_layers)]
-        x, _ = O.gptoss_moe(L, x, c["norm"])
+        x, _ = fwd(L, x, c["norm"])
         n += 1
     dt = time.perf_counter() - t0
     per_layer = dt / n
@@ -98,14 +110,21 @@ def main() -> int:
 
     c = CONFIGS[args.config]
     d, dff, ne, k, nl = c["d"], c["dff"], c["ne"], c["k"], c["layers"]
-    cfg = MoeConfig.gptoss(d=d, n_expert=ne, top_k=k, d_ff=dff, n_layer=nl)
+    qwen = c["family"] == "qwen"
+    if qwen:
+        cfg = MoeConfig.qwen3(d=d, n_expert=ne, top_k=k, d_ff=dff, n_layer=nl)
+    else:
+        cfg = MoeConfig.gptoss(d=d, n_expert=ne, top_k=k, d_ff=dff, n_layer=nl)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(0)
     blk = MoeBlock(cfg, device=0)
     host_keep = []
     t0 = time.perf_counter()
     for l in range(nl):
-        L = synth.gptoss_layer(d, dff, ne, k, seed=0, layer=l, zipf=c["zipf"])
+        if qwen:
+            L = synth.qwen_layer(d, dff, ne, k, seed=0, layer=l)
+        else:
+            L = synth.gptoss_layer(d, dff, ne, k, seed=0, layer=l, zipf=c["zipf"])
         blk.load_layer(l, L)
         if l < 2:
             host_keep.append(L)
@@ -159,12 +178,13 @@ def main() -> int:
         "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "int8", "data": "synthetic",
         "config": {"workload": c["name"], "layers_per_step": c["per_step"], "d": d, "d_ff": dff,
-                   "n_expert": ne, "top_k": k, "batch": 1, "weights": "MXFP4 (GGUF type 39)"},
+                   "n_expert": ne, "top_k": k, "batch": 1,
+                   "weights": "Q4_K gate/up + Q6_K down (GGUF types 12/14)" if qwen else "MXFP4 (GGUF type 39)"},
         "tok_per_s": round(tok_s, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
         "bytes_per_token": bytes_tok,
         "kernels_us": {"route": round(rt_ms / max(rt_n, 1) * 1e3, 2), "gate_up": round(gu_avg_us, 2),
                        "down": round(dn_ms / max(dn_n, 1) * 1e3, 2)},
-        "roofline": {"bound": "hbm", "kernel": "k_gateup_mx", "achieved": round(gu_ach, 1), "peak": HBM_PEAK_GBS,
+        "roofline": {"bound": "hbm", "kernel": "k_gateup_kq" if qwen else "k_gateup_mx", "achieved": round(gu_ach, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gu_ach / HBM_PEAK_GBS, 4), "traffic": None,
                      "bytes_per_launch": lb["gate_up"]},
     }

@@ -31,7 +31,7 @@ class MoeCfg(C.Structure):
 
 class MoeTrace(C.Structure):
     _fields_ = [("xn", f32p), ("xq", i8p), ("xsb", f32p), ("xsum", i32p), ("logits", f32p),
-                ("ids", i32p), ("wts", f32p), ("gu", f32p), ("gu_sums", i32p), ("hq", i8p),
+                ("ids", i32p), ("wts", f32p), ("gu", f32p), ("gu_sums", i32p), ("h", f32p), ("hq", i8p),
                 ("hsb", f32p), ("hsum", i32p), ("dn", f32p), ("dn_sums", i32p),
                 ("exact_router_fallbacks", C.c_int32)]
 

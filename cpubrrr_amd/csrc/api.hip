@@ -47,8 +47,8 @@ int fail(int code, const char* fmt, ...) {
     } while (0)
 
 struct LayerDev {
-    cpb::u32x4* gu = nullptr;   // gate+up stream (MXFP4) or gate rows (k-quant)
-    cpb::u32x4* up = nullptr;   // k-quant up rows
+    cpb::u32x4* gu = nullptr;   // gate+up stream layout
+    cpb::u32x4* up = nullptr;   // unused (kept null)
     cpb::u32x4* dn = nullptr;   // down stream
     float *gate_b = nullptr, *up_b = nullptr, *down_b = nullptr;
     float *router_w = nullptr, *router_b = nullptr, *norm_w = nullptr;
@@ -136,6 +136,9 @@ int check_cfg(const cpb_moe_cfg* c) {
         if (c->wtype_down != CPB_GGUF_Q4_K && c->wtype_down != CPB_GGUF_Q6_K)
             return fail(CPB_EINVAL, "k-quant down must be Q4_K or Q6_K");
         if (c->d % 256 || c->d_ff % 256) return fail(CPB_EINVAL, "d and d_ff must be multiples of 256");
+        if (c->d > 8192 || c->d_ff > 4096) return fail(CPB_EINVAL, "k-quant path supports d <= 8192, d_ff <= 4096");
+        if (c->top_k != 1 && c->top_k != 2 && c->top_k != 4 && c->top_k != 8)
+            return fail(CPB_EINVAL, "k-quant path supports top_k in {1,2,4,8}, got %d", c->top_k);
     } else {
         return fail(CPB_EINVAL, "unsupported gate/up type %d", c->wtype_gate_up);
     }
@@ -192,11 +195,11 @@ struct Timer {
         if (h->ev_pool.size() < 2) return;
         a = h->ev_pool.back(); h->ev_pool.pop_back();
         b = h->ev_pool.back(); h->ev_pool.pop_back();
-        hipEventRecord(a, h->stream);
+        cpb::armed_events() = cpb::LaunchEvents{a, b};   // taken by the one kernel launched in this scope
     }
     ~Timer() {
         if (!a) return;
-        hipEventRecord(b, h->stream);
+        cpb::armed_events() = cpb::LaunchEvents{};
         h->ev_used.push_back({cls, {a, b}});
     }
 };
@@ -210,7 +213,7 @@ int ensure_trace(cpb_moe_t* h) {
     if ((r = dmalloc(&h->t_h, k * c.d_ff))) return r;
     if ((r = dmalloc(&h->t_dn, k * c.d))) return r;
     size_t gs = h->mx ? k * 2 * c.d_ff * (c.d / 32) : k * 2 * c.d_ff * (c.d / 256) * 2;
-    size_t ds = h->mx ? k * c.d * (c.d_ff / 32) : k * c.d * (c.d_ff / 256);
+    size_t ds = h->mx ? k * c.d * (c.d_ff / 32) : k * c.d * (c.d_ff / 256) * (c.wtype_down == CPB_GGUF_Q4_K ? 2 : 1);
     if ((r = dmalloc(&h->t_gu_sums, gs))) return r;
     if ((r = dmalloc(&h->t_dn_sums, ds))) return r;
     return 0;
@@ -277,12 +280,11 @@ int layer_token(cpb_moe_t* h, int layer, float* dx, int apply_norm, bool trace) 
         }
     } else {
         cpb::KqArgs k{};
-        k.gate = (const uint8_t*)L.gu; k.up = (const uint8_t*)L.up; k.down = (const uint8_t*)L.dn;
-        k.gate_type = c.wtype_gate_up; k.down_type = c.wtype_down;
+        k.gu = L.gu; k.dn = L.dn; k.down_type = c.wtype_down;
         k.xq = h->xq; k.xs = h->xsb; k.xsum = h->xsum; k.ids = h->ids; k.wts = h->wts;
         k.d = c.d; k.dff = c.d_ff; k.top_k = c.top_k;
         k.hbuf = h->hbuf; k.hq = h->hq; k.hs = h->hsb; k.hsum = h->hsum; k.x = dx;
-        k.gu = h->t_gu; k.gu_sums = h->t_gu_sums; k.dn = h->t_dn; k.dn_sums = h->t_dn_sums;
+        k.gu_out = h->t_gu; k.gu_sums = h->t_gu_sums; k.dn_out = h->t_dn; k.dn_sums = h->t_dn_sums;
         {
             Timer tm(h, 1);
             if (cpb::launch_gateup_kq(k, trace, h->stream)) return fail(CPB_ENODEV, "k-quant gate/up launch failed");
@@ -351,7 +353,7 @@ int cpb_moe_create(const cpb_moe_cfg* cfg, int device, cpb_moe_t** out) {
         return bail(fail(CPB_ENODEV, "init memset failed"));
     if (const char* v = getenv("CPB_PERSISTENT")) h->persistent = v[0] == '1';
 #ifdef CPB_DECODE_STAMPS
-    if ((r = dmalloc(&h->d_stamps, (size_t)1024 * cfg->n_layer * 8))) return bail(r);
+    if ((r = dmalloc(&h->d_stamps, ((size_t)1 << 20) + 4096))) return bail(r);
 #endif
     if (hipMemsetAsync(h->counter, 0, sizeof(unsigned), h->stream) != hipSuccess ||
         hipMemsetAsync(h->fallback, 0, sizeof(int32_t), h->stream) != hipSuccess ||
@@ -392,13 +394,17 @@ int cpb_moe_load_layer(cpb_moe_t* h, int layer, const void* gate, const void* up
         if (cpb::launch_repack_down(h->staging, L.dn, ne, d, ff / 32, c.top_k, h->stream))
             return fail(CPB_ENODEV, "repack launch failed");
     } else {
-        // k-quant superblocks are consumed in their native row layout
-        if ((r = dmalloc((uint8_t**)&L.gu, gbytes)) || (r = dmalloc((uint8_t**)&L.up, gbytes)) ||
-            (r = dmalloc((uint8_t**)&L.dn, dbytes)))
-            return r;
-        HIP_OK(hipMemcpyAsync(L.gu, gate, gbytes, hipMemcpyHostToDevice, h->stream));
-        HIP_OK(hipMemcpyAsync(L.up, up, gbytes, hipMemcpyHostToDevice, h->stream));
-        HIP_OK(hipMemcpyAsync(L.dn, down, dbytes, hipMemcpyHostToDevice, h->stream));
+        if ((r = ensure_staging(h, 2 * gbytes > dbytes ? 2 * gbytes : dbytes))) return r;
+        HIP_OK(hipMemcpyAsync(h->staging, gate, gbytes, hipMemcpyHostToDevice, h->stream));
+        HIP_OK(hipMemcpyAsync(h->staging + gbytes, up, gbytes, hipMemcpyHostToDevice, h->stream));
+        if ((r = dmalloc((uint8_t**)&L.gu, cpb::kq_gateup_bytes(ne, ff, d)))) return r;
+        if (cpb::launch_repack_kq_gateup(h->staging, h->staging + gbytes, L.gu, ne, ff, d, h->stream))
+            return fail(CPB_ENODEV, "repack launch failed");
+        HIP_OK(hipStreamSynchronize(h->stream));
+        HIP_OK(hipMemcpyAsync(h->staging, down, dbytes, hipMemcpyHostToDevice, h->stream));
+        if ((r = dmalloc((uint8_t**)&L.dn, cpb::kq_down_bytes(ne, d, ff, c.top_k, c.wtype_down)))) return r;
+        if (cpb::launch_repack_kq_down(h->staging, L.dn, ne, d, ff, c.top_k, c.wtype_down, h->stream))
+            return fail(CPB_ENODEV, "repack launch failed");
     }
     if (c.has_bias) {
         if ((r = upload(&L.gate_b, gate_b, ne * ff, h->stream)) || (r = upload(&L.up_b, up_b, ne * ff, h->stream)) ||
@@ -533,7 +539,9 @@ int cpb_moe_forward(cpb_moe_t* h, int layer, float* x, int n_tok, int apply_norm
         r |= cp(tr->hsb, h->hsb, (mx ? k * ff / 32 : k * ff / 256) * 4);
         r |= cp(tr->hsum, h->hsum, mx ? 0 : k * ff / 32 * 4);
         r |= cp(tr->dn, h->t_dn, k * d * 4);
-        r |= cp(tr->dn_sums, h->t_dn_sums, (mx ? k * d * (ff / 32) : k * d * (ff / 256)) * 4);
+        r |= cp(tr->dn_sums, h->t_dn_sums,
+                (mx ? k * d * (ff / 32) : k * d * (ff / 256) * (c.wtype_down == CPB_GGUF_Q4_K ? 2 : 1)) * 4);
+        r |= cp(tr->h, mx ? h->t_h : h->hbuf, k * ff * 4);
         int32_t fb = 0;
         r |= cp(&fb, h->fallback, 4);
         HIP_OK(hipStreamSynchronize(h->stream));
@@ -591,7 +599,7 @@ void cpb_moe_destroy(cpb_moe_t* h) {
 #ifdef CPB_DECODE_STAMPS
     if (h->d_stamps) {
         const char* path = getenv("CPB_DECODE_STAMPS_FILE");
-        size_t n = (size_t)1024 * h->cfg.n_layer * 8;
+        size_t n = ((size_t)1 << 20) + 4096;
         std::vector<unsigned long long> st(n);
         hipMemcpy(st.data(), h->d_stamps, n * 8, hipMemcpyDeviceToHost);
         FILE* f = path ? fopen(path, "wb") : nullptr;

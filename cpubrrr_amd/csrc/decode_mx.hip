@@ -88,7 +88,7 @@ CPB_DEV void layer_tiles(const DecodeArgs& a, const LayerPtrs& Lp, const Selecti
 #pragma unroll
         for (int k = 0; k < 4; k++) {
             XsSlot sl = xs_slot((const uint32_t*)a.xq, (const uint32_t*)a.xqn, a.xsb, blk0, a.nb, lane + 64 * k, active);
-            xv[k] = *sl.p;
+            xv[k] = ld_dev(sl.p);       // written by the routing workgroups of this launch
             ok[k] = sl.valid;
         }
         u32x4 wv[kUnits];
@@ -151,7 +151,7 @@ CPB_DEV void layer_tiles(const DecodeArgs& a, const LayerPtrs& Lp, const Selecti
                 XsSlot sl = xs_slot((const uint32_t*)(a.hq + (size_t)ex * a.dff),
                                     (const uint32_t*)(a.hqn + (size_t)ex * a.dff), a.hsb + (size_t)ex * a.nbf, blk0,
                                     a.nbf, i % kXsDw, active);
-                hv[k] = *sl.p;
+                hv[k] = ld_dev(sl.p);   // written by the gate/up tiles of this launch
                 hok[k] = sl.valid;
             }
 #pragma unroll
@@ -210,6 +210,10 @@ CPB_DEV void decode_layer(const DecodeArgs& a, int li, Selection& sel,
     if (threadIdx.x < 64)
         select_experts_wave(a.lstar, a.lbound, a.ne, a.k, Lp.router_w, Lp.router_b, a.xn, a.d, (double*)smem, &sel);
     __syncthreads();
+#ifdef CPB_DECODE_STAMPS
+    if (a.stamps && li == 0 && threadIdx.x < a.k && w < 512)
+        a.stamps[((size_t)1 << 20) + 2048 + w * 4 + threadIdx.x] = (unsigned long long)sel.ids[threadIdx.x];
+#endif
     if (w == 0 && threadIdx.x < 64) {
         const int lane = threadIdx.x;
         for (int i = lane; i < a.ne; i += 64) a.logits[i] = (float)ld_dev(a.lstar + i);
@@ -219,6 +223,13 @@ CPB_DEV void decode_layer(const DecodeArgs& a, int li, Selection& sel,
             a.logits[sel.ids[lane]] = sel.logit[lane];
         }
         if (lane == 0) a.fallback[0] = sel.fallback;
+#ifdef CPB_DECODE_STAMPS
+        // probe builds: the selection each layer used (workgroup 0)
+        if (a.stamps && lane < a.k) {
+            a.stamps[(size_t)1 << 20 | (li * 16 + lane)] = (unsigned long long)sel.ids[lane];
+            a.stamps[(size_t)1 << 20 | (li * 16 + 8 + lane)] = __float_as_uint(sel.wts[lane]);
+        }
+#endif
     }
     DSTAMP(4);
     layer_tiles(a, Lp, sel, w, H, X, smem, li);

@@ -1,6 +1,7 @@
 // moe_common.h -- shared device helpers for the MoE kernels (gfx950 only).
 #pragma once
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <stdint.h>
 
 #define CPB_DEV __device__ __forceinline__
@@ -97,6 +98,35 @@ CPB_DEV T* uniform_ptr(T* p) {
     return (T*)(uintptr_t)(((uint64_t)hi << 32) | lo);
 }
 
+// Wave-wide maximum of a double through DPP row operations (no LDS
+// round trips), returned in every lane.  Inactive / out-of-row sources read
+// -inf.  Steps: quad swaps, half-row and row mirrors, then row broadcasts 15
+// and 31, leaving the total in lane 63.
+template <int CTRL, int ROWMASK>
+CPB_DEV double dpp_max_step(double v) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, CTRL, ROWMASK, 0xF, false);
+    const int hi = __builtin_amdgcn_update_dpp((int)0xFFF00000u, (int)(uint32_t)(b >> 32), CTRL, ROWMASK, 0xF, false);
+    const double o = __builtin_bit_cast(double, ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+    return fmax(v, o);
+}
+// v from lane `src` (wave-uniform) in every lane
+CPB_DEV double readlane_f64(double v, int src) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)b, src);
+    const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), src);
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+CPB_DEV double wave_max_f64(double v) {
+    v = dpp_max_step<0xB1, 0xF>(v);     // quad_perm [1,0,3,2]
+    v = dpp_max_step<0x4E, 0xF>(v);     // quad_perm [2,3,0,1]
+    v = dpp_max_step<0x141, 0xF>(v);    // row_half_mirror
+    v = dpp_max_step<0x140, 0xF>(v);    // row_mirror
+    v = dpp_max_step<0x142, 0xA>(v);    // row_bcast:15 -> rows 1, 3
+    v = dpp_max_step<0x143, 0xC>(v);    // row_bcast:31 -> rows 2, 3
+    return readlane_f64(v, 63);
+}
+
 // Device-coherent access for the small buffers that workgroups hand to each
 // other inside one launch (activations, routing results, hq, x).  Relaxed
 // agent-scope atomics compile to plain loads/stores with the sc1 bit, which
@@ -122,6 +152,28 @@ CPB_DEV void drain_memory() {
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_waitcnt(0);
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// ---- host: kernel launch with optional execution timestamps ----
+// When a caller has armed a pair of events (timing mode), the next launch goes
+// through hipExtLaunchKernelGGL, whose dispatch packet records them: they
+// bracket that kernel's execution alone, not the queue gaps around it.
+struct LaunchEvents {
+    hipEvent_t start = nullptr, stop = nullptr;
+};
+inline LaunchEvents& armed_events() {
+    static thread_local LaunchEvents ev;
+    return ev;
+}
+template <typename F, typename... Args>
+void launch(F kernel, dim3 grid, dim3 block, size_t lds, hipStream_t s, Args... args) {
+    LaunchEvents& ev = armed_events();
+    if (ev.start) {
+        hipExtLaunchKernelGGL(kernel, grid, block, (uint32_t)lds, s, ev.start, ev.stop, 0, args...);
+        ev = LaunchEvents{};
+    } else {
+        hipLaunchKernelGGL(kernel, grid, block, lds, s, args...);
+    }
 }
 
 }  // namespace cpb

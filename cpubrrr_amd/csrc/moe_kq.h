@@ -2,31 +2,39 @@
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include "moe_common.h"
 
 namespace cpb {
 
 struct KqArgs {
-    const uint8_t* gate;     // [ne][dff] Q4_K rows (native superblock layout)
-    const uint8_t* up;       // [ne][dff] Q4_K rows
-    const uint8_t* down;     // [ne][d] Q6_K or Q4_K rows
-    int gate_type, down_type;
-    const int8_t* xq;        // [d]
+    const u32x4* gu;         // gate+up stream layout (k_repack_kq_gateup)
+    const u32x4* dn;         // down stream layout (k_repack_kq_down)
+    int down_type;           // 12 (Q4_K) or 14 (Q6_K); gate/up are Q4_K
+    const int8_t* xq;        // [d]   Q8_K activations
     const float* xs;         // [d/256]
     const int32_t* xsum;     // [d/32]
     const int32_t* ids;      // [top_k]
     const float* wts;        // [top_k]
     int d, dff, top_k;
-    float* hbuf;             // [top_k][dff]
-    int8_t* hq;              // [top_k][dff]
-    float* hs;               // [top_k][dff/256]
-    int32_t* hsum;           // [top_k][dff/32]
+    float* hbuf;             // [top_k][dff] SiLU(gate) * up
+    int8_t* hq;              // [top_k][dff]      (trace only: Q8_K of hbuf)
+    float* hs;               // [top_k][dff/256]  (trace only)
+    int32_t* hsum;           // [top_k][dff/32]   (trace only)
     float* x;                // [d] residual, updated in place
     // trace
-    float* gu;               // [top_k][2][dff]
-    int32_t* gu_sums;        // [top_k][2][dff][d/256][2]
-    float* dn;               // [top_k][d]
-    int32_t* dn_sums;        // [top_k][d][dff/256]
+    float* gu_out;           // [top_k][2][dff]
+    int32_t* gu_sums;        // [top_k][2][dff][d/256][2]  (sumi, mint)
+    float* dn_out;           // [top_k][d]
+    int32_t* dn_sums;        // [top_k][d][dff/256][nsum]  nsum = 2 (Q4_K: sumi, mint) or 1 (Q6_K)
 };
+
+// bytes of the stream layouts
+size_t kq_gateup_bytes(int ne, int dff, int d);
+size_t kq_down_bytes(int ne, int d, int dff, int top_k, int down_type);
+// re-layout from native GGUF superblock rows (device buffers, stream s)
+int launch_repack_kq_gateup(const uint8_t* gate, const uint8_t* up, u32x4* out, int ne, int dff, int d, hipStream_t s);
+int launch_repack_kq_down(const uint8_t* down, u32x4* out, int ne, int d, int dff, int top_k, int down_type,
+                          hipStream_t s);
 
 int launch_gateup_kq(const KqArgs& a, bool trace, hipStream_t s);
 int launch_down_kq(const KqArgs& a, bool trace, hipStream_t s);

@@ -248,8 +248,8 @@ int launch_gateup_mx(const GateUpArgs& a, bool trace, hipStream_t s) {
     if (P < 1 || P > 16 || a.dff % 32 != 0) return -22;
     size_t lds = sizeof(uint32_t) * P * kXsDw + sizeof(float) * P * 64;
     dim3 grid(a.top_k * (a.dff / 32)), block(64 * P);
-    if (trace) hipLaunchKernelGGL(k_gateup_mx<true>, grid, block, lds, s, a);
-    else hipLaunchKernelGGL(k_gateup_mx<false>, grid, block, lds, s, a);
+    if (trace) launch(k_gateup_mx<true>, grid, block, lds, s, a);
+    else launch(k_gateup_mx<false>, grid, block, lds, s, a);
     return hipGetLastError() == hipSuccess ? 0 : -19;
 }
 
@@ -258,8 +258,8 @@ int launch_down_mx(const DownArgs& a, bool trace, hipStream_t s) {
     if (P < 1 || P > 16 || (K != 1 && K != 2 && K != 4) || a.d % (64 / K) != 0) return -22;
     size_t lds = sizeof(uint32_t) * P * K * kXsDw + sizeof(float) * (P * 64 + 64);
     dim3 grid(a.d / (64 / K)), block(64 * P);
-    if (trace) hipLaunchKernelGGL(k_down_mx<true>, grid, block, lds, s, a);
-    else hipLaunchKernelGGL(k_down_mx<false>, grid, block, lds, s, a);
+    if (trace) launch(k_down_mx<true>, grid, block, lds, s, a);
+    else launch(k_down_mx<false>, grid, block, lds, s, a);
     return hipGetLastError() == hipSuccess ? 0 : -19;
 }
 

@@ -42,7 +42,9 @@ struct XsSlot {
 CPB_DEV XsSlot xs_slot(const uint32_t* __restrict__ q, const uint32_t* __restrict__ qn,
                        const float* __restrict__ sc, int blk0, int nb, int slot, bool use) {
     // one clamped address per slot; the validity select is applied when the
-    // value is stored to LDS, after the weight loads have been issued
+    // value is stored to LDS, after the weight loads have been issued.  A
+    // consumer whose data was written earlier in the same launch must load
+    // through ld_dev (another XCD's L2 may hold a stale copy).
     const bool isx = slot < kBlkPerPart * 16;
     const int u = isx ? slot / 16 : slot - kBlkPerPart * 16;
     const int j = slot & 15;

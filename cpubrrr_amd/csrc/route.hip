@@ -23,10 +23,10 @@ namespace cpb {
 
 // Selection by one wavefront: rank, certify, softmax; publishes ids /
 // weights / logits.
-CPB_DEV void select_publish(const SelectArgs& a, unsigned char* smem) {
+CPB_DEV void select_publish(const SelectArgs& a, unsigned char* smem, unsigned long long* stamps = nullptr) {
     __shared__ Selection sel;
     select_experts_wave(a.lstar, a.lbound, a.n_expert, a.top_k, a.router_w, a.router_b, a.xn, a.d, (double*)smem, &sel,
-                        a.logits);
+                        a.logits, stamps);
     const int lane = threadIdx.x;
     if (lane < a.top_k) {
         a.ids[lane] = sel.ids[lane];
@@ -52,7 +52,7 @@ __global__ __launch_bounds__(256) void k_route(RouteArgs a, SelectArgs s, unsign
     if (threadIdx.x == 0) st_dev(arrive, 0u);
     const int e = blockIdx.x;
     RSTAMP(6);
-    select_publish(s, smem);
+    select_publish(s, smem, a.stamps ? a.stamps + (size_t)e * 16 + 8 : nullptr);
     RSTAMP(7);
 }
 
@@ -64,7 +64,7 @@ __global__ __launch_bounds__(64) void k_select(SelectArgs a) {
 
 int launch_select(const SelectArgs* a, hipStream_t s) {
     size_t lds = sizeof(double) * 4 * a->n_expert + 64;
-    hipLaunchKernelGGL(k_select, dim3(1), dim3(64), lds, s, *a);
+    launch(k_select, dim3(1), dim3(64), lds, s, *a);
     return hipGetLastError() == hipSuccess ? 0 : -19;
 }
 
@@ -74,7 +74,7 @@ int launch_route(const RouteArgs* a, const SelectArgs* sa, unsigned* arrive, hip
     size_t lds = route_lds_bytes(a->d);
     const size_t lds_sel = sizeof(double) * 4 * a->n_expert + 64;
     if (lds_sel > lds) lds = lds_sel;
-    hipLaunchKernelGGL(k_route, dim3(a->n_expert), dim3(256), lds, s, *a, *sa, arrive);
+    launch(k_route, dim3(a->n_expert), dim3(256), lds, s, *a, *sa, arrive);
     return hipGetLastError() == hipSuccess ? 0 : -19;
 }
 

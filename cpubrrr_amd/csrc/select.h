@@ -24,19 +24,23 @@ struct Selection {
 };
 
 // Executed by one wavefront (64 lanes).  lds: 4*NE doubles of scratch.
-// Lane l handles experts l, l+64, ... (NE <= 256): rank_e = #{j : L_j > L_e or
-// (L_j == L_e and j < e)} from LDS broadcast reads, so every expert is ranked
-// in one pass with no dependent cross-lane steps.  logits_out (optional)
+// Lane l holds experts l, l+64, ... (NE <= 256) in registers; the top-k come
+// from k rounds of wave-wide argmax (cross-lane shuffles, no LDS round
+// trips), the certification from one wave-wide max.  logits_out (optional)
 // receives the fp32 value of every expert's exact logit.  Outputs ids / logit
 // / wts in rank order into `out` (valid in every lane after the call).
 CPB_DEV void select_experts_wave(const double* __restrict__ Ls, const double* __restrict__ Bs, int NE, int K,
                                  const float* __restrict__ router_w, const float* __restrict__ router_b,
                                  const float* __restrict__ xn, int d, double* lds, Selection* out,
-                                 float* logits_out = nullptr) {
+                                 float* logits_out = nullptr, unsigned long long* stamps = nullptr) {
+#ifdef CPB_DECODE_STAMPS
+#define SSTAMP(i) do { if (stamps && (threadIdx.x & 63) == 0) stamps[i] = wall_clock64(); } while (0)
+#else
+#define SSTAMP(i) do { (void)stamps; } while (0)
+#endif
     const int lane = threadIdx.x & 63;
     double* sL = lds;            // [NE] values used for ranking
     double* sH = lds + NE;       // [NE] upper bounds
-    int* sR = (int*)(lds + 2 * NE);          // [NE] ranks
     int* sSel = (int*)(lds + 3 * NE);        // [8] expert at rank i
     // one coherent round trip for all values
     double lv[4], bv[4];
@@ -58,39 +62,54 @@ CPB_DEV void select_experts_wave(const double* __restrict__ Ls, const double* __
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    int rk[4];
+    SSTAMP(0);
+    // K rounds of wave-wide argmax over the register values: descending,
+    // lowest index first among equal values (the reference's strict insertion)
+    unsigned taken = 0;                    // bit k: expert lane + 64k already selected
+    for (int i = 0; i < K; i++) {
+        double best = -__builtin_inf();
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const int e = lane + 64 * k;
-        rk[k] = NE;
-        if (64 * k < NE) {
-            const double v = lv[k];
-            int r = 0;
-#pragma unroll 16
-            for (int j = 0; j < NE; j++) { const double o = sL[j]; r += (o > v) || (o == v && j < e); }
-            if (e < NE) {
-                rk[k] = r;
-                sR[e] = r;
-                if (r < K) sSel[r] = e;
-            }
+        for (int k = 0; k < 4; k++)
+            if (lane + 64 * k < NE && !((taken >> k) & 1u)) best = fmax(best, lv[k]);
+        best = wave_max_f64(best);
+        int bi = 0x7fffffff;
+#pragma unroll
+        for (int k = 3; k >= 0; k--) {
+            const uint64_t m = __ballot(lane + 64 * k < NE && !((taken >> k) & 1u) && lv[k] == best);
+            if (m) bi = 64 * k + __builtin_ctzll(m);
+        }
+        if (lane == 0) sSel[i] = bi;
+        if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
+    }
+    SSTAMP(1);
+    // certification: the expert at rank r < K must lie strictly above every
+    // expert ranked after it, i.e. lo_r > max(hi of ranks r+1..K-1, hi of
+    // every unselected expert)
+    double mu = -1e300;
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+        if (lane + 64 * k < NE && !((taken >> k) & 1u)) mu = fmax(mu, lv[k] + bv[k]);
+    mu = wave_max_f64(mu);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    bool bad = false;
+    {
+        double suffix = mu;
+        for (int i = K - 1; i >= 0; i--) {
+            const int e = __builtin_amdgcn_readfirstlane(sSel[i]);
+            const int src = e & 63, kk = e >> 6;
+            const double l = readlane_f64(kk == 0 ? lv[0] : kk == 1 ? lv[1] : kk == 2 ? lv[2] : lv[3], src);
+            const double b = readlane_f64(kk == 0 ? bv[0] : kk == 1 ? bv[1] : kk == 2 ? bv[2] : bv[3], src);
+            if (!(l - b > suffix)) bad = true;
+            suffix = fmax(suffix, l + b);
         }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // certification: the expert at rank r < K must lie strictly above every
-    // expert ranked after it
-    bool bad = false;
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const int r = rk[k];
-        if (r < K) {
-            const double lo = lv[k] - bv[k];
-#pragma unroll 16
-            for (int j = 0; j < NE; j++) bad |= (sR[j] > r) & (sH[j] >= lo);
-        }
-    }
     const bool ok = !__any(bad);
+    SSTAMP(2);
     if (!ok) {
         // candidates: intervals reaching the lowest lower bound of the selected
         double tau = 1e300;
@@ -119,6 +138,7 @@ CPB_DEV void select_experts_wave(const double* __restrict__ Ls, const double* __
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
+    SSTAMP(3);
     // softmax over the k selected, reference order: ex_i = exp(l_i - l_0)
     // (lane i), then the serial sum ex_0 + ex_1 + ... (every lane)
     const int mi = lane < K ? lane : 0;
@@ -135,6 +155,7 @@ CPB_DEV void select_experts_wave(const double* __restrict__ Ls, const double* __
         out->wts[lane] = wt;
     }
     if (lane == 0) out->fallback = ok ? 0 : 1;
+    SSTAMP(4);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");

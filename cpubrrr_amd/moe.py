@@ -138,7 +138,10 @@ class MoeBlock:
                 "hq": np.zeros((k, ff), np.int8),
                 "hsb": np.zeros((k, ff // 32) if mx else (k, ff // 256), np.float32),
                 "hsum": np.zeros((k, ff // 32), np.int32), "dn": np.zeros((k, d), np.float32),
-                "dn_sums": np.zeros((k, d, ff // 32) if mx else (k, d, ff // 256), np.int32),
+                "dn_sums": np.zeros((k, d, ff // 32) if mx else
+                                    ((k, d, ff // 256, 2) if c.wtype_down == L.GGUF_Q4_K else (k, d, ff // 256)),
+                                    np.int32),
+                "h": np.zeros((k, ff), np.float32),
             }
             tr = L.MoeTrace()
             types = dict(L.MoeTrace._fields_)

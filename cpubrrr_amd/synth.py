@@ -75,19 +75,18 @@ def gptoss_layer(d: int, dff: int, ne: int, k: int, seed: int = 0, layer: int = 
     return L
 
 
-def qwen_layer(d: int, dff: int, ne: int, k: int, seed: int = 0, layer: int = 0, zipf: float | None = None) -> dict:
-    """One Qwen3-30B-A3B-shaped MoE layer: Q4_K gate/up, Q6_K down, no biases."""
+def qwen_layer(d: int, dff: int, ne: int, k: int, seed: int = 0, layer: int = 0, down_type: int = 14) -> dict:
+    """One Qwen3-30B-A3B-shaped MoE layer: Q4_K gate/up, Q6_K (or Q4_K) down,
+    no biases (the reference's Qwen router has none, engine_qwen2.rs:400)."""
     L = {
         "d": d, "dff": dff, "ne": ne, "k": k, "nt": 12, "eps": 1e-6,
-        "gate_type": 12, "up_type": 12, "down_type": 14,
+        "gate_type": 12, "up_type": 12, "down_type": down_type,
         "gate": q4k(ne * dff, d, seed, _stream(layer, _GATE)),
         "up": q4k(ne * dff, d, seed, _stream(layer, _UP)),
-        "down": q6k(ne * d, dff, seed, _stream(layer, _DOWN)),
+        "down": (q6k if down_type == 14 else q4k)(ne * d, dff, seed, _stream(layer, _DOWN)),
         "router_w": normal((ne, d), 0.02, seed, _stream(layer, _RW)),
         "norm_w": np.ones(d, np.float32),
     }
-    if zipf:
-        L["router_b"] = zipf_bias(ne, zipf, seed, _stream(layer, _RB))
     return L
 
 

@@ -84,11 +84,12 @@ typedef struct cpb_moe_trace {
     float*   wts;       /* [k]                                             */
     float*   gu;        /* [k][2][d_ff] gate/up outputs (+bias)            */
     int32_t* gu_sums;   /* MXFP4 [k][2][d_ff][nb]; Q4_K [k][2][d_ff][d/256][2] */
+    float*   h;         /* [k][d_ff] SwiGLU-OAI / SiLU*up output before Q8  */
     int8_t*  hq;        /* [k][d_ff]                                       */
     float*   hsb;       /* [k][nbf] (MXFP4) or [k][d_ff/256] (Q8_K)        */
     int32_t* hsum;      /* [k][nbf] Q8_K only                              */
     float*   dn;        /* [k][d] down outputs (+bias)                     */
-    int32_t* dn_sums;   /* MXFP4 [k][d][nbf]; Q6_K/Q4_K [k][d][d_ff/256]   */
+    int32_t* dn_sums;   /* MXFP4 [k][d][nbf]; Q6_K [k][d][d_ff/256]; Q4_K [k][d][d_ff/256][2] */
     int32_t  exact_router_fallbacks; /* out: 1 if this call needed the exact serial router */
 } cpb_moe_trace;
 

@@ -429,7 +429,7 @@ void orc_qwen_moe(const orc_qwen_layer* L, float* x, int apply_norm, orc_trace* 
     #pragma omp parallel for schedule(static) num_threads(nth)
     for (int r = 0; r < d; r++) {
         for (int ei = 0; ei < k; ei++) {
-            int32_t* sums = tr && tr->dn_sums ? tr->dn_sums + ((size_t)ei * d + r) * nsbf : NULL;
+            int32_t* sums = tr && tr->dn_sums ? tr->dn_sums + ((size_t)ei * d + r) * nsbf * (L->down_type == 12 ? 2 : 1) : NULL;
             float v = kdot(L->down_type, L->down + ((size_t)ids[ei] * d + r) * db,
                            hq + (size_t)ei * ff, hs + (size_t)ei * nsbf, hm + (size_t)ei * (ff / 32), ff, sums);
             if (tr && tr->dn) tr->dn[(size_t)ei * d + r] = v;

@@ -182,7 +182,7 @@ def q6k_dot(row, xq, ys):
     return np.float32(v), sums
 
 
-def _trace_bufs(d, dff, ne, k, mx: bool, want_sums: bool):
+def _trace_bufs(d, dff, ne, k, mx: bool, want_sums: bool, down_pairs: bool = False):
     t = {
         "xn": np.zeros(d, np.float32), "xq": np.zeros(d, np.int8),
         "xsb": np.zeros(d // 32 if mx else d // 256, np.float32),
@@ -195,7 +195,8 @@ def _trace_bufs(d, dff, ne, k, mx: bool, want_sums: bool):
     }
     if want_sums:
         t["gu_sums"] = np.zeros((k, 2, dff, d // 32) if mx else (k, 2, dff, d // 256, 2), np.int32)
-        t["dn_sums"] = np.zeros((k, d, dff // 32) if mx else (k, d, dff // 256), np.int32)
+        t["dn_sums"] = np.zeros((k, d, dff // 32) if mx else
+                                ((k, d, dff // 256, 2) if down_pairs else (k, d, dff // 256)), np.int32)
     return t
 
 
@@ -232,7 +233,7 @@ def qwen_moe(layer: dict, x: np.ndarray, apply_norm: bool, want_sums: bool = Fal
                   _p(keep["gate"], u8p), _p(keep["up"], u8p), _p(keep["down"], u8p),
                   _p(keep["router_w"], f32p), _p(keep["norm_w"], f32p))
     xo = np.array(x, np.float32, copy=True)
-    t = _trace_bufs(d, dff, ne, k, False, want_sums)
+    t = _trace_bufs(d, dff, ne, k, False, want_sums, layer.get("down_type", 14) == 12)
     tr = _mk_trace(t)
     lib().orc_qwen_moe(C.byref(L), _p(xo, f32p), int(bool(apply_norm)), C.byref(tr))
     return xo, t
