@@ -26,6 +26,11 @@ from pathlib import Path
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
+# HBM bytes per dispatch of the roofline kernel, from rocprofv3 FETCH_SIZE /
+# WRITE_SIZE runs scaled by a 1 GiB copy (profiles/hbm_traffic_config1_phased.md);
+# None where not yet measured.
+MEASURED_TRAFFIC = {"k_gateup_mx": 35_719_000, "k_gateup_kq": None}
+
 METRIC = "expert-weight GB/s (% HBM peak) + MoE-layer tok/s, gpt-oss-20b shape, 1 GPU"
 HBM_PEAK_GBS = 8000.0
 
@@ -97,6 +102,8 @@ def main() -> int:
     ap.add_argument("--config", type=int, default=1, choices=sorted(CONFIGS))
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="also run one plain device copy of this many MiB (HBM-traffic counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
@@ -138,6 +145,16 @@ def main() -> int:
     torch.cuda.set_stream(stream)
     blk.set_stream(stream.cuda_stream)
     x = torch.from_numpy(synth.token(d, 0, 0)).to(dev)
+    if args.calib_copy_mib:
+        # a copy kernel of known size: its FETCH_SIZE / WRITE_SIZE give the
+        # counter-to-bytes factor for the kernels above
+        n = args.calib_copy_mib * (1 << 20) // 4
+        src = torch.empty(n, dtype=torch.float32, device=dev).uniform_()
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     def step(i):
         if c["per_step"] == nl:
@@ -185,7 +202,8 @@ def main() -> int:
         "kernels_us": {"route": round(rt_ms / max(rt_n, 1) * 1e3, 2), "gate_up": round(gu_avg_us, 2),
                        "down": round(dn_ms / max(dn_n, 1) * 1e3, 2)},
         "roofline": {"bound": "hbm", "kernel": "k_gateup_kq" if qwen else "k_gateup_mx", "achieved": round(gu_ach, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(gu_ach / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(gu_ach / HBM_PEAK_GBS, 4),
+                     "traffic": MEASURED_TRAFFIC["k_gateup_kq" if qwen else "k_gateup_mx"],
                      "bytes_per_launch": lb["gate_up"]},
     }
     if not args.no_cpu:
