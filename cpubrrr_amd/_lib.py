@@ -50,6 +50,7 @@ SIGNATURES = {
     "cpb_moe_layer_bytes": (C.c_int, [C.POINTER(MoeCfg), C.POINTER(C.c_size_t)]),
     "cpb_moe_timing": (C.c_int, [C.c_void_p, C.c_int]),
     "cpb_moe_kernel_times": (C.c_int, [C.c_void_p, C.POINTER(C.c_double), C.POINTER(C.c_long)]),
+    "cpb_moe_grouped_sums": (C.c_int, [C.c_void_p, C.c_int, f32p, C.c_int, C.c_int, i32p, i32p]),
     "cpb_synth_u64": (C.c_uint64, [C.c_uint64, C.c_uint64, C.c_uint64]),
     "cpb_synth_mxfp4": (None, [u8p, C.c_size_t, C.c_int, C.c_int, C.c_uint64, C.c_uint64]),
     "cpb_synth_normal": (None, [f32p, C.c_size_t, C.c_float, C.c_float, C.c_uint64, C.c_uint64]),

@@ -22,6 +22,7 @@
 #include "moe_kq.h"
 #include "decode_mx.h"
 #include "moe_mx.h"
+#include "moe_grouped.h"
 #include "route.h"
 
 namespace {
@@ -53,6 +54,7 @@ struct LayerDev {
     float *gate_b = nullptr, *up_b = nullptr, *down_b = nullptr;
     float *router_w = nullptr, *router_b = nullptr, *norm_w = nullptr;
     bool loaded = false;
+    bool mfma_exact = false;    // MXFP4 scales all in [32, 254]: the grouped matrix-core path is exact
 };
 
 }  // namespace
@@ -94,6 +96,15 @@ struct cpb_moe {
     bool persistent = false;  // the single-launch decode is opt-in (CPB_PERSISTENT=1)
     bool prepare_only = false;
     unsigned long long* d_stamps = nullptr;   // probe builds: persistent-decode phase timestamps
+    // grouped (n_tok > 1) MXFP4 path: per-token and per-pair scratch
+    bool grouped = false;
+    float *g_xn = nullptr, *g_xsb = nullptr, *g_logits = nullptr, *g_wts = nullptr, *g_hsb = nullptr, *g_dnout = nullptr;
+    int8_t *g_xq = nullptr, *g_hq = nullptr;
+    uint8_t *g_ximg = nullptr, *g_himg = nullptr;
+    double *g_lstar = nullptr, *g_lbound = nullptr;
+    int32_t *g_ids = nullptr, *g_fallback = nullptr, *g_sorted = nullptr, *g_ntiles = nullptr;
+    int4* g_tiles = nullptr;
+    unsigned* d_special = nullptr;
     // captured HIP graphs of forward_device calls, keyed by their arguments
     std::map<std::tuple<int, int, float*, int, int, hipStream_t>, hipGraphExec_t> graphs;
     bool use_graphs = true;
@@ -344,6 +355,22 @@ int cpb_moe_create(const cpb_moe_cfg* cfg, int device, cpb_moe_t** out) {
         (r = dmalloc(&h->fallback, 1)) || (r = dmalloc(&h->hq, k * ff)) || (r = dmalloc(&h->hqn, k * ff)) ||
         (r = dmalloc(&h->hsb, k * ff / 32)) || (r = dmalloc(&h->hsum, k * ff / 32)) || (r = dmalloc(&h->hbuf, k * ff)))
         return bail(r);
+    if (h->mx) {
+        if ((r = dmalloc(&h->d_special, 1))) return bail(r);
+        h->grouped = T > 1;
+        if (const char* v = getenv("CPB_GROUPED")) h->grouped = h->grouped && v[0] != '0';
+    }
+    if (h->mx && T > 1) {
+        const size_t nb = d / 32, nbf = ff / 32, np = T * k;
+        if ((r = dmalloc(&h->g_xn, T * d)) || (r = dmalloc(&h->g_xq, T * d)) || (r = dmalloc(&h->g_xsb, T * nb)) ||
+            (r = dmalloc(&h->g_ximg, T * nb * 64)) || (r = dmalloc(&h->g_lstar, T * ne)) ||
+            (r = dmalloc(&h->g_lbound, T * ne)) || (r = dmalloc(&h->g_logits, T * ne)) || (r = dmalloc(&h->g_ids, np)) ||
+            (r = dmalloc(&h->g_wts, np)) || (r = dmalloc(&h->g_fallback, T)) || (r = dmalloc(&h->g_sorted, np)) ||
+            (r = dmalloc(&h->g_tiles, np / 32 + ne + 1)) || (r = dmalloc(&h->g_ntiles, 1)) ||
+            (r = dmalloc(&h->g_hq, np * ff)) || (r = dmalloc(&h->g_hsb, np * nbf)) || (r = dmalloc(&h->g_himg, np * nbf * 64)) ||
+            (r = dmalloc(&h->g_dnout, np * d)))
+            return bail(r);
+    }
     if ((r = dmalloc(&h->d_layers, (size_t)cfg->n_layer)) || (r = dmalloc(&h->d_sync, 3 * (size_t)cfg->n_layer + 1)) ||
         (r = dmalloc(&h->d_error, 1)))
         return bail(r);
@@ -385,11 +412,16 @@ int cpb_moe_load_layer(cpb_moe_t* h, int layer, const void* gate, const void* up
         if ((r = ensure_staging(h, 2 * gbytes > dbytes ? 2 * gbytes : dbytes))) return r;
         HIP_OK(hipMemcpyAsync(h->staging, gate, gbytes, hipMemcpyHostToDevice, h->stream));
         HIP_OK(hipMemcpyAsync(h->staging + gbytes, up, gbytes, hipMemcpyHostToDevice, h->stream));
+        HIP_OK(hipMemsetAsync(h->d_special, 0, sizeof(unsigned), h->stream));
+        if (cpb::launch_count_special_exps(h->staging, 2 * gbytes / 17, h->d_special, h->stream))
+            return fail(CPB_ENODEV, "exponent scan launch failed");
         if ((r = dmalloc((uint8_t**)&L.gu, cpb::mx_gateup_bytes(ne, ff, d / 32)))) return r;
         if (cpb::launch_repack_gateup(h->staging, h->staging + gbytes, L.gu, ne, ff, d / 32, h->stream))
             return fail(CPB_ENODEV, "repack launch failed");
         HIP_OK(hipStreamSynchronize(h->stream));
         HIP_OK(hipMemcpyAsync(h->staging, down, dbytes, hipMemcpyHostToDevice, h->stream));
+        if (cpb::launch_count_special_exps(h->staging, dbytes / 17, h->d_special, h->stream))
+            return fail(CPB_ENODEV, "exponent scan launch failed");
         if ((r = dmalloc((uint8_t**)&L.dn, cpb::mx_down_bytes(ne, d, ff / 32, c.top_k)))) return r;
         if (cpb::launch_repack_down(h->staging, L.dn, ne, d, ff / 32, c.top_k, h->stream))
             return fail(CPB_ENODEV, "repack launch failed");
@@ -418,6 +450,11 @@ int cpb_moe_load_layer(cpb_moe_t* h, int layer, const void* gate, const void* up
         HIP_OK(hipMemcpyAsync(h->d_layers + layer, &lp, sizeof lp, hipMemcpyHostToDevice, h->stream));
     }
     HIP_OK(hipStreamSynchronize(h->stream));
+    if (h->mx) {
+        unsigned special = 0;
+        HIP_OK(hipMemcpy(&special, h->d_special, sizeof special, hipMemcpyDeviceToHost));
+        L.mfma_exact = special == 0;
+    }
     L.loaded = true;
     return 0;
 }
@@ -450,6 +487,29 @@ static int launch_persistent(cpb_moe_t* h, int layer0, int n_layers, float* d_x,
     return cpb::launch_decode_mx(a, it->second, h->stream);
 }
 
+// n_tok > 1 tokens through one MXFP4 layer on the matrix cores (bit-identical
+// to per-token decode); sums (test hook) receive the int32 block sums.
+static int layer_grouped(cpb_moe_t* h, int layer, float* d_x, int n_tok, int apply_norm, int32_t* gu_sums,
+                         int32_t* dn_sums) {
+    const auto& c = h->cfg;
+    const LayerDev& L = h->layers[layer];
+    cpb::GroupedArgs g{};
+    g.norm_w = L.norm_w; g.router_w = L.router_w; g.router_b = L.router_b;
+    g.gu = L.gu; g.dn = L.dn; g.gate_b = L.gate_b; g.up_b = L.up_b; g.down_b = L.down_b;
+    g.n_tok = n_tok; g.d = c.d; g.dff = c.d_ff; g.ne = c.n_expert; g.k = c.top_k; g.nb = h->nb; g.nbf = h->nbf;
+    g.parts_gu = h->parts_gu; g.parts_dn = h->parts_dn;
+    g.norm = c.norm; g.norm_nt = c.norm_nt; g.apply_norm = apply_norm;
+    g.eps = c.rms_eps; g.alpha = c.alpha; g.limit = c.limit;
+    g.max_tiles = n_tok * c.top_k / 32 + c.n_expert + 1;
+    g.x = d_x; g.xn = h->g_xn; g.xq = h->g_xq; g.xsb = h->g_xsb; g.ximg = h->g_ximg;
+    g.lstar = h->g_lstar; g.lbound = h->g_lbound; g.logits = h->g_logits; g.ids = h->g_ids; g.wts = h->g_wts;
+    g.fallback = h->g_fallback; g.sorted = h->g_sorted; g.tiles = h->g_tiles; g.ntiles = h->g_ntiles;
+    g.hq = h->g_hq; g.hsb = h->g_hsb; g.himg = h->g_himg; g.dnout = h->g_dnout;
+    g.gu_sums = gu_sums; g.dn_sums = dn_sums;
+    if (cpb::launch_grouped_layer(g, gu_sums != nullptr, h->stream)) return fail(CPB_ENODEV, "grouped layer launch failed");
+    return 0;
+}
+
 static int launch_direct(cpb_moe_t* h, int layer0, int n_layers, float* d_x, int n_tok, int apply_norm) {
     const auto& c = h->cfg;
     if (h->mx && n_tok == 1 && h->persistent && !h->timing) {
@@ -458,9 +518,14 @@ static int launch_direct(cpb_moe_t* h, int layer0, int n_layers, float* d_x, int
         if (r != -28 && r != -22) return fail(CPB_ENODEV, "persistent decode launch failed (%d)", r);
         h->persistent = false;          // shape/device cannot host it: per-phase kernels from now on
     }
-    for (int l = layer0; l < layer0 + n_layers; l++)
+    for (int l = layer0; l < layer0 + n_layers; l++) {
+        if (h->mx && n_tok > 1 && h->grouped && h->layers[l].mfma_exact) {
+            if (int r = layer_grouped(h, l, d_x, n_tok, apply_norm, nullptr, nullptr)) return r;
+            continue;
+        }
         for (int t = 0; t < n_tok; t++)
             if (int r = layer_token(h, l, d_x + (size_t)t * c.d, apply_norm, false)) return r;
+    }
     return 0;
 }
 
@@ -500,6 +565,33 @@ int cpb_moe_forward_device(cpb_moe_t* h, int layer0, int n_layers, float* d_x, i
     }
     HIP_OK(hipGraphLaunch(it->second, h->stream));
     return 0;
+}
+
+int cpb_moe_grouped_sums(cpb_moe_t* h, int layer, float* x, int n_tok, int apply_norm, int32_t* gu_sums,
+                         int32_t* dn_sums) {
+    if (!h || !x || !gu_sums || !dn_sums) return fail(CPB_EINVAL, "NULL argument");
+    const auto& c = h->cfg;
+    if (!h->mx || !h->grouped) return fail(CPB_EINVAL, "grouped path needs MXFP4 weights and max_tokens > 1");
+    if (layer < 0 || layer >= c.n_layer || !h->layers[layer].loaded) return fail(CPB_ESTATE, "layer %d not loaded", layer);
+    if (!h->layers[layer].mfma_exact) return fail(CPB_EINVAL, "layer %d has e8m0 scales outside [32, 254]", layer);
+    if (n_tok < 2 || n_tok > c.max_tokens) return fail(CPB_EINVAL, "n_tok=%d outside [2, max_tokens=%d]", n_tok, c.max_tokens);
+    HIP_OK(hipSetDevice(h->device));
+    const size_t d = c.d, np = (size_t)n_tok * c.top_k;
+    const size_t ngu = np * 2 * c.d_ff * h->nb, ndn = np * d * h->nbf;
+    int32_t *dgu = nullptr, *ddn = nullptr;
+    int r;
+    if ((r = dmalloc(&dgu, ngu)) || (r = dmalloc(&ddn, ndn))) { hipFree(dgu); return r; }
+    r = 0;
+    if (hipMemcpyAsync(h->x, x, n_tok * d * sizeof(float), hipMemcpyHostToDevice, h->stream) != hipSuccess) r = CPB_ENODEV;
+    if (!r) r = layer_grouped(h, layer, h->x, n_tok, apply_norm, dgu, ddn);
+    if (!r && (hipMemcpyAsync(x, h->x, n_tok * d * sizeof(float), hipMemcpyDeviceToHost, h->stream) != hipSuccess ||
+               hipMemcpyAsync(gu_sums, dgu, ngu * 4, hipMemcpyDeviceToHost, h->stream) != hipSuccess ||
+               hipMemcpyAsync(dn_sums, ddn, ndn * 4, hipMemcpyDeviceToHost, h->stream) != hipSuccess ||
+               hipStreamSynchronize(h->stream) != hipSuccess))
+        r = fail(CPB_ENODEV, "grouped sums copy failed");
+    hipFree(dgu);
+    hipFree(ddn);
+    return r ? r : check_device_error(h);
 }
 
 int cpb_moe_forward(cpb_moe_t* h, int layer, float* x, int n_tok, int apply_norm, cpb_moe_trace* tr) {
@@ -608,6 +700,10 @@ void cpb_moe_destroy(cpb_moe_t* h) {
     }
 #endif
     hipFree(h->d_layers); hipFree(h->d_sync); hipFree(h->d_error);
+    void* gbufs[] = {h->g_xn, h->g_xsb, h->g_logits, h->g_wts, h->g_hsb, h->g_dnout, h->g_xq, h->g_hq, h->g_ximg,
+                     h->g_himg, h->g_lstar, h->g_lbound, h->g_ids, h->g_fallback, h->g_sorted, h->g_ntiles, h->g_tiles,
+                     h->d_special};
+    for (void* p : gbufs) hipFree(p);
     for (auto& L : h->layers) free_layer(L);
     void* bufs[] = {h->x, h->xn, h->xq, h->xqn, h->xsb, h->xsum, h->lstar, h->lbound, h->counter, h->logits,
                     h->ids, h->wts, h->fallback, h->hq, h->hqn, h->hsb, h->hsum, h->hbuf, h->t_gu, h->t_h,

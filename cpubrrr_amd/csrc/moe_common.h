@@ -137,7 +137,9 @@ CPB_DEV T ld_dev(const T* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __H
 template <class T>
 CPB_DEV void st_dev(T* p, T v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 // Wait until every memory operation this wave issued has completed.
-// Buffer resource over [base, base + bytes) (wave-uniform base): a buffer
+// Buffer resource over [base, base + bytes).  base and bytes must be the same
+// in every lane (they are made wave-uniform: lane 0's values are used); lanes
+// that address different arrays need one resource over all of them.  A buffer
 // load whose offset lies outside returns zeros without touching memory, so
 // masked loads need no branch and the compiler waits for them by count.
 CPB_DEV __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uint32_t bytes) {

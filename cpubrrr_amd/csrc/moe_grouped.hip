@@ -1,0 +1,374 @@
+// moe_grouped.hip -- batched / prefill gpt-oss MoE layer (gfx950).
+//
+// Reference: the tile path engine_gpt2.rs:1120-1239, whose contract is
+// "bit-identical to per-token decode" (expert-major subscriber lists, weight
+// quads reused across tokens).  Here the tokens' (token, slot) pairs are
+// grouped by expert and each expert's gate/up and down products run on the
+// matrix cores, exactly:
+//
+//   v_mfma_scale_f32_32x32x64_f8f6f4, A = weights (fp4 e2m1, 32 rows x 64 K),
+//   B = activations (fp8 e4m3, 64 K x 32 tokens), one MXFP4 block per
+//   instruction.  A's two K halves both carry the block's 32 raw codes (the
+//   16 GGUF bytes as they are: no decode), B's first half carries 16*h and the
+//   second half l of each int8 activation x = 16*h + l (h = x >> 4, l in
+//   [0, 15]; both exact in e4m3), and the block's e8m0 byte is A's hardware
+//   scale.  Every product and partial sum is exact in fp32, so
+//       D = sum_i E2M1(c_i) * x_i * 2^(e-127) = S * 2^(e-128)
+//   with S the reference's int32 block sum (engine_gpt2.rs:194-228).  The
+//   epilogue then does what the decode kernels do with S: per 15-block k-part
+//   acc = fma(D, xsb, acc) (the same exact product S * 2^(e-128) * xsb, one
+//   rounding), parts added in order, bias, SwiGLU-OAI + Q8 (gate/up) or the
+//   slot-ordered combine (down).  Results are therefore the decode path's bit
+//   for bit.  Blocks with e8m0 < 32 or == 255 (tbl[0] = 0 and NaN in
+//   hardware, subnormal scales) are not exact this way: the caller routes
+//   such layers to the per-token kernels.
+//
+// Operand layouts (measured on gfx950): A lane l = (row l%32, K half l/32),
+// nibble n <-> K 32*half + n; B lane l = (token l%32, half hb = l/32), bytes
+// 0-15 <-> K 16*hb + j, bytes 16-31 <-> K 32 + 16*hb + j; D lane l register i
+// = (row 8*(i/4) + 4*(l/32) + i%4, token l%32); scale_a lane l = row l%32.
+// An MXFP4 block's nibble n is element n/2 (n even) or 16 + n/2 (n odd), so
+// the activation "image" of a block (64 B) puts element e's 16*h at byte
+// 32*(K/16) + K%16 and its l 16 bytes later, K = 2e (e < 16) or 2(e-16)+1.
+//
+// The weights are read in the decode kernels' stream layout (moe_mx.hip), so
+// both paths share one copy in HBM.
+#include "moe_common.h"
+#include "moe_grouped.h"
+#include "mx_dev.h"
+#include "route_dev.h"
+#include "select.h"
+
+namespace cpb {
+
+typedef int v8i_g __attribute__((ext_vector_type(8)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+constexpr int kImg = 64;          // image bytes per 32-block
+constexpr int kRouteTok = 16;     // tokens per router workgroup
+
+// exact e4m3 encodings used by the split (v = 0, an integer in [1, 15] or 16*h)
+CPB_DEV uint32_t e4m3_small(int v) {
+    if (v == 0) return 0;
+    const uint32_t s = v < 0 ? 0x80u : 0u;
+    const uint32_t a = (uint32_t)(v < 0 ? -v : v);
+    const int E = 31 - __builtin_clz(a);
+    const uint32_t m = E >= 3 ? (a >> (E - 3)) & 7u : (a << (3 - E)) & 7u;
+    return s | ((uint32_t)(E + 7) << 3) | m;
+}
+CPB_DEV int k_of_elem(int e) { return e < 16 ? 2 * e : 2 * (e - 16) + 1; }
+// byte offsets of element e's two image bytes within its block
+CPB_DEV int img_hi_off(int e) { const int K = k_of_elem(e); return (K >> 4) * 32 + (K & 15); }
+
+// ---- 1. per token: rmsnorm, Q8 per 32, fp8 image ----
+__global__ __launch_bounds__(256) void k_prep_batch(GroupedArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int t = blockIdx.x, d = a.d, tid = threadIdx.x, nth = blockDim.x;
+    float* xs = (float*)smem;
+    float* xnl = xs + d;
+    float* scratch = xnl + d;
+    norm_into(a.x + (size_t)t * d, a.norm_w, d, a.eps, a.norm, a.norm_nt, a.apply_norm, xs, xnl, scratch);
+    // Q8 per 32-block (engine_gpt2.rs:691-699): 32 lanes per block
+    const int l = tid & 31;
+    for (int bk = tid >> 5; bk < a.nb; bk += nth >> 5) {
+        const float v = xnl[bk * 32 + l];
+        float m = fabsf(v);
+#pragma unroll
+        for (int s2 = 16; s2 >= 1; s2 >>= 1) m = fmaxf(m, __shfl_xor(m, s2));
+        const float sc = fmaxf(1e-12f, m) / 127.0f;
+        const int q = q8_round(v, sc);
+        a.xn[(size_t)t * d + bk * 32 + l] = v;
+        a.xq[(size_t)t * d + bk * 32 + l] = (int8_t)q;
+        if (l == 0) a.xsb[(size_t)t * a.nb + bk] = sc;
+        const int h = q >> 4;
+        uint8_t* img = a.ximg + ((size_t)t * a.nb + bk) * kImg;
+        const int o = img_hi_off(l);
+        img[o] = (uint8_t)e4m3_small(16 * h);
+        img[o + 16] = (uint8_t)e4m3_small(q - 16 * h);
+    }
+}
+
+// ---- 2. router logits + bounds, workgroup = (expert, 16 tokens) ----
+__global__ __launch_bounds__(256) void k_router_batch(GroupedArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int e = blockIdx.x, d = a.d, tid = threadIdx.x, nth = blockDim.x;
+    float* xnl = (float*)smem;
+    double* dsc = (double*)(xnl + d + 32);
+    double* dred = dsc + 16;
+    const int C = ((d + 4 * nth - 1) / (4 * nth)) * 4;
+    const int j0 = tid * C;
+    const float* W = a.router_w + (size_t)e * d;
+    float4 wv[kChunk / 4];
+#pragma unroll
+    for (int i = 0; i < kChunk / 4; i++) wv[i] = *(const float4*)(W + min(j0 + 4 * i, d - 4));
+    const double b = a.router_b ? (double)a.router_b[e] : 0.0;
+    for (int tt = 0; tt < kRouteTok; tt++) {
+        const int t = blockIdx.y * kRouteTok + tt;
+        if (t >= a.n_tok) break;
+        for (int i = tid; i < d / 4; i += nth) ((float4*)xnl)[i] = ((const float4*)(a.xn + (size_t)t * d))[i];
+        __syncthreads();
+        double total = 0.0, bound = 0.0;
+        router_logit(wv, C, j0, xnl, d, b, dsc, dred, &total, &bound);
+        if (tid == 0) {
+            a.lstar[(size_t)t * a.ne + e] = total;
+            a.lbound[(size_t)t * a.ne + e] = bound;
+        }
+        __syncthreads();
+    }
+}
+
+// ---- 3. top-k + softmax, one wavefront per token ----
+__global__ __launch_bounds__(256) void k_select_batch(GroupedArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ Selection sel[4];
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int t = blockIdx.x * 4 + w;
+    if (t >= a.n_tok) return;
+    double* lds = (double*)smem + (size_t)w * (4 * a.ne + 8);
+    select_experts_wave(a.lstar + (size_t)t * a.ne, a.lbound + (size_t)t * a.ne, a.ne, a.k, a.router_w, a.router_b,
+                        a.xn + (size_t)t * a.d, a.d, lds, &sel[w], a.logits + (size_t)t * a.ne);
+    if (lane < a.k) {
+        a.ids[(size_t)t * a.k + lane] = sel[w].ids[lane];
+        a.wts[(size_t)t * a.k + lane] = sel[w].wts[lane];
+        a.logits[(size_t)t * a.ne + sel[w].ids[lane]] = sel[w].logit[lane];
+    }
+    if (lane == 0) a.fallback[t] = sel[w].fallback;
+}
+
+// ---- 4. group the (token, slot) pairs by expert (stable), tile table ----
+__global__ __launch_bounds__(1024) void k_group(GroupedArgs a) {
+    __shared__ int cnt_l[256], off_l[256], toff_l[256];
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
+    const int np = a.n_tok * a.k;
+    const uint64_t lt = lane ? (~0ull >> (64 - lane)) : 0ull;
+    for (int e = w; e < a.ne; e += nw) {
+        int c = 0;
+        for (int base = 0; base < np; base += 64) {
+            const int p = base + lane;
+            c += __popcll(__ballot(p < np && a.ids[p] == e));
+        }
+        if (lane == 0) cnt_l[e] = c;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int o = 0, to = 0;
+        for (int e = 0; e < a.ne; e++) {
+            off_l[e] = o;
+            toff_l[e] = to;
+            o += cnt_l[e];
+            to += (cnt_l[e] + 31) / 32;
+        }
+        *a.ntiles = to;
+    }
+    __syncthreads();
+    for (int e = w; e < a.ne; e += nw) {
+        int pos = off_l[e];
+        for (int base = 0; base < np; base += 64) {
+            const int p = base + lane;
+            const bool m = p < np && a.ids[p] == e;
+            const uint64_t bm = __ballot(m);
+            if (m) a.sorted[pos + __popcll(bm & lt)] = p;
+            pos += __popcll(bm);
+        }
+        const int c = cnt_l[e], nt = (c + 31) / 32;
+        for (int j = lane; j < nt; j += 64) a.tiles[toff_l[e] + j] = int4{e, off_l[e] + 32 * j, min(32, c - 32 * j), 0};
+    }
+}
+
+// One block of the grouped product: A = 16 raw code bytes (both K halves),
+// B = the 32-byte half-image, hardware scale = the block's e8m0 byte.
+CPB_DEV v16f mx_block_mfma(const u32x4& w, const u32x4& x0, const u32x4& x1, uint32_t e) {
+    const v8i_g A = {(int)w[0], (int)w[1], (int)w[2], (int)w[3], 0, 0, 0, 0};
+    const v8i_g B = {(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3], (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
+    const v16f Z = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(A, B, Z, 4, 0, 0, (int)e, 0, 127);
+}
+
+// ---- 5. grouped gate/up + SwiGLU-OAI + Q8 (+ image of h) ----
+// grid (max_tiles, ceil(dff/32 / 4)); wave = one 32-row tile of gate and up.
+template <bool TRACE>
+__global__ __launch_bounds__(256) void k_gateup_grouped(GroupedArgs a) {
+    if ((int)blockIdx.x >= *a.ntiles) return;
+    const int4 tl = a.tiles[blockIdx.x];
+    const int e = uniform(tl.x), start = uniform(tl.y), cnt = uniform(tl.z);
+    const int lane = threadIdx.x & 63;
+    const int T = a.dff / 32, P = a.parts_gu, nb = a.nb;
+    const int rt = blockIdx.y * 4 + uniform((int)(threadIdx.x >> 6));
+    if (rt >= T) return;
+    const int ti = lane & 31, hb = lane >> 5;
+    const bool valid = ti < cnt;
+    const int pair = a.sorted[start + (valid ? ti : 0)];
+    const int tok = pair / a.k;
+    // one resource over all tokens (a buffer base must be wave-uniform); lanes
+    // address their own token, blocks past nb read zero
+    const __amdgpu_buffer_rsrc_t rimg = buf_rsrc(a.ximg, (uint32_t)((size_t)a.n_tok * nb * kImg));
+    const __amdgpu_buffer_rsrc_t rsc = buf_rsrc(a.xsb, (uint32_t)((size_t)a.n_tok * nb * 4));
+    const uint32_t img0 = (uint32_t)tok * nb * kImg + hb * 32, sc0 = (uint32_t)tok * nb * 4;
+    const u32x4* wbase = a.gu + (((size_t)e * T + rt) * P) * kUnits * 64 + (lane & 31);
+
+    v16f tg = {}, tu = {};
+    for (int q = 0; q < P; q++) {
+        const u32x4* wp = wbase + (size_t)q * kUnits * 64;
+        const u32x4 eg = __builtin_nontemporal_load(wp), eu = __builtin_nontemporal_load(wp + 32);
+        v16f ag = {}, au = {};
+#pragma unroll
+        for (int i = 0; i < kBlkPerPart; i++) {
+            const int b = q * kBlkPerPart + i;
+            const u32x4 wg = __builtin_nontemporal_load(wp + (1 + i) * 64);
+            const u32x4 wu = __builtin_nontemporal_load(wp + (1 + i) * 64 + 32);
+            const uint32_t off = b < nb ? img0 + (uint32_t)b * kImg : kOffNone;
+            const u32x4 x0 = __builtin_amdgcn_raw_buffer_load_b128(rimg, off, 0, 0);
+            const u32x4 x1 = __builtin_amdgcn_raw_buffer_load_b128(rimg, off + 16, 0, 0);
+            const float s = __uint_as_float(
+                __builtin_amdgcn_raw_buffer_load_b32(rsc, b < nb ? sc0 + (uint32_t)b * 4 : kOffNone, 0, 0));
+            const uint32_t ebg = (eg[i >> 2] >> (8 * (i & 3))) & 0xffu;
+            const uint32_t ebu = (eu[i >> 2] >> (8 * (i & 3))) & 0xffu;
+            const v16f Dg = mx_block_mfma(wg, x0, x1, ebg);
+            const v16f Du = mx_block_mfma(wu, x0, x1, ebu);
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                ag[r] = fmaf(Dg[r], s, ag[r]);
+                au[r] = fmaf(Du[r], s, au[r]);
+            }
+            if (TRACE) {
+                // S = D * 2^(128 - e) with e the exponent of D[r]'s row (held by lane row % 32)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int rl = 8 * (r >> 2) + 4 * hb + (r & 3), row = rt * 32 + rl;
+                    const int eg_r = __shfl((int)ebg, rl), eu_r = __shfl((int)ebu, rl);
+                    if (valid && b < nb) {
+                        a.gu_sums[(((size_t)pair * 2 + 0) * a.dff + row) * nb + b] = (int)ldexpf(Dg[r], 128 - eg_r);
+                        a.gu_sums[(((size_t)pair * 2 + 1) * a.dff + row) * nb + b] = (int)ldexpf(Du[r], 128 - eu_r);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < 16; r++) { tg[r] += ag[r]; tu[r] += au[r]; }
+    }
+    // bias, SwiGLU-OAI (engine_gpt2.rs:887-906), Q8 of the 32-row block of h
+    float hv[16], m = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        const int row = rt * 32 + 8 * (r >> 2) + 4 * hb + (r & 3);
+        float vg = tg[r], vu = tu[r];
+        if (a.gate_b) vg += a.gate_b[(size_t)e * a.dff + row];
+        if (a.up_b) vu += a.up_b[(size_t)e * a.dff + row];
+        const float xg = fminf(vg, a.limit);
+        const float yu = fminf(fmaxf(vu, -a.limit), a.limit);
+        hv[r] = (xg / (1.0f + expf(-a.alpha * xg))) * (yu + 1.0f);
+        m = fmaxf(m, fabsf(hv[r]));
+    }
+    m = fmaxf(m, __shfl_xor(m, 32));
+    const float sc = fmaxf(1e-12f, m) / 127.0f;
+    if (!valid) return;
+    uint8_t* img = a.himg + ((size_t)pair * a.nbf + rt) * kImg;
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        const int el = 8 * (r >> 2) + 4 * hb + (r & 3);
+        const int qv = q8_round(hv[r], sc);
+        a.hq[(size_t)pair * a.dff + rt * 32 + el] = (int8_t)qv;
+        const int h = qv >> 4;
+        const int o = img_hi_off(el);
+        img[o] = (uint8_t)e4m3_small(16 * h);
+        img[o + 16] = (uint8_t)e4m3_small(qv - 16 * h);
+    }
+    if (hb == 0) a.hsb[(size_t)pair * a.nbf + rt] = sc;
+}
+
+// ---- 6. grouped down (+ bias) into dnout ----
+// grid (max_tiles, ceil(d/32 / 4)); wave = one 32-row tile of down.
+template <bool TRACE>
+__global__ __launch_bounds__(256) void k_down_grouped(GroupedArgs a) {
+    if ((int)blockIdx.x >= *a.ntiles) return;
+    const int4 tl = a.tiles[blockIdx.x];
+    const int e = uniform(tl.x), start = uniform(tl.y), cnt = uniform(tl.z);
+    const int lane = threadIdx.x & 63;
+    const int RTv = 64 / a.k, Tv = a.d / RTv, P = a.parts_dn, nbf = a.nbf;
+    const int rt = blockIdx.y * 4 + uniform((int)(threadIdx.x >> 6));
+    if (rt >= a.d / 32) return;
+    const int ti = lane & 31, hb = lane >> 5;
+    const bool valid = ti < cnt;
+    const int pair = a.sorted[start + (valid ? ti : 0)];
+    const size_t np = (size_t)a.n_tok * a.k;
+    const __amdgpu_buffer_rsrc_t rimg = buf_rsrc(a.himg, (uint32_t)(np * nbf * kImg));
+    const __amdgpu_buffer_rsrc_t rsc = buf_rsrc(a.hsb, (uint32_t)(np * nbf * 4));
+    const uint32_t img0 = (uint32_t)pair * nbf * kImg + hb * 32, sc0 = (uint32_t)pair * nbf * 4;
+    const int row_l = rt * 32 + (lane & 31);          // this lane's A row
+    const u32x4* wbase = a.dn + (((size_t)e * Tv + row_l / RTv) * P) * kUnits * RTv + row_l % RTv;
+
+    v16f tot = {};
+    for (int q = 0; q < P; q++) {
+        const u32x4* wp = wbase + (size_t)q * kUnits * RTv;
+        const u32x4 ev = __builtin_nontemporal_load(wp);
+        v16f acc = {};
+#pragma unroll
+        for (int i = 0; i < kBlkPerPart; i++) {
+            const int b = q * kBlkPerPart + i;
+            const u32x4 w = __builtin_nontemporal_load(wp + (1 + i) * RTv);
+            const uint32_t off = b < nbf ? img0 + (uint32_t)b * kImg : kOffNone;
+            const u32x4 x0 = __builtin_amdgcn_raw_buffer_load_b128(rimg, off, 0, 0);
+            const u32x4 x1 = __builtin_amdgcn_raw_buffer_load_b128(rimg, off + 16, 0, 0);
+            const float s = __uint_as_float(
+                __builtin_amdgcn_raw_buffer_load_b32(rsc, b < nbf ? sc0 + (uint32_t)b * 4 : kOffNone, 0, 0));
+            const uint32_t eb = (ev[i >> 2] >> (8 * (i & 3))) & 0xffu;
+            const v16f D = mx_block_mfma(w, x0, x1, eb);
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[r] = fmaf(D[r], s, acc[r]);
+            if (TRACE) {
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int rl = 8 * (r >> 2) + 4 * hb + (r & 3), row = rt * 32 + rl;
+                    const int e_r = __shfl((int)eb, rl);
+                    if (valid && b < nbf) a.dn_sums[((size_t)pair * a.d + row) * nbf + b] = (int)ldexpf(D[r], 128 - e_r);
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < 16; r++) tot[r] += acc[r];
+    }
+    if (!valid) return;
+    float* out = a.dnout + (size_t)pair * a.d + rt * 32 + 4 * hb;
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+        float4 v;
+        float* vp = (float*)&v;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const int row = rt * 32 + 8 * g + 4 * hb + c;
+            vp[c] = tot[4 * g + c] + (a.down_b ? a.down_b[(size_t)e * a.d + row] : 0.0f);
+        }
+        *(float4*)(out + 8 * g) = v;
+    }
+}
+
+// ---- 7. per token: x += sum over slots (ascending) of wts * (down + bias) ----
+__global__ __launch_bounds__(256) void k_combine_batch(GroupedArgs a) {
+    const int t = blockIdx.x;
+    for (int r = threadIdx.x; r < a.d; r += blockDim.x) {
+        float s = a.x[(size_t)t * a.d + r];                  // engine_gpt2.rs:911-921
+        for (int k = 0; k < a.k; k++) s += a.wts[(size_t)t * a.k + k] * a.dnout[((size_t)t * a.k + k) * a.d + r];
+        a.x[(size_t)t * a.d + r] = s;
+    }
+}
+
+int launch_grouped_layer(const GroupedArgs& a, bool trace, hipStream_t s) {
+    const int nt = a.n_tok;
+    launch(k_prep_batch, dim3(nt), dim3(256), sizeof(float) * (2 * a.d + 64), s, a);
+    launch(k_router_batch, dim3(a.ne, (nt + kRouteTok - 1) / kRouteTok), dim3(256),
+           sizeof(float) * (a.d + 32) + sizeof(double) * 32, s, a);
+    launch(k_select_batch, dim3((nt + 3) / 4), dim3(256), sizeof(double) * 4 * (4 * a.ne + 8), s, a);
+    launch(k_group, dim3(1), dim3(1024), 0, s, a);
+    const dim3 ggu(a.max_tiles, (a.dff / 32 + 3) / 4), gdn(a.max_tiles, (a.d / 32 + 3) / 4);
+    if (trace) {
+        launch(k_gateup_grouped<true>, ggu, dim3(256), 0, s, a);
+        launch(k_down_grouped<true>, gdn, dim3(256), 0, s, a);
+    } else {
+        launch(k_gateup_grouped<false>, ggu, dim3(256), 0, s, a);
+        launch(k_down_grouped<false>, gdn, dim3(256), 0, s, a);
+    }
+    launch(k_combine_batch, dim3(nt), dim3(256), 0, s, a);
+    return hipGetLastError() == hipSuccess ? 0 : -19;
+}
+
+}  // namespace cpb

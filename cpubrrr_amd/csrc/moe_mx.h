@@ -41,6 +41,7 @@ struct DownArgs {
 
 size_t mx_gateup_bytes(int ne, int dff, int nb);
 size_t mx_down_bytes(int ne, int d, int nbf, int top_k);
+int launch_count_special_exps(const uint8_t* raw, size_t nblocks, unsigned* out, hipStream_t s);
 int launch_repack_gateup(const uint8_t* gate, const uint8_t* up, u32x4* out, int ne, int dff, int nb, hipStream_t s);
 int launch_repack_down(const uint8_t* down, u32x4* out, int ne, int d, int nbf, int top_k, hipStream_t s);
 int launch_gateup_mx(const GateUpArgs& a, bool trace, hipStream_t s);

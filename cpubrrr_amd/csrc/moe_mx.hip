@@ -232,6 +232,21 @@ size_t mx_down_bytes(int ne, int d, int nbf, int top_k) {
     return (size_t)ne * (d / RT) * P * kUnits * RT * 16;
 }
 
+// Count MXFP4 blocks whose e8m0 byte the matrix-core path cannot scale exactly
+// (e < 32: tbl[0] = 0 and subnormal scales; e == 255: NaN in hardware).
+__global__ void k_count_special_exps(const uint8_t* __restrict__ raw, size_t nblocks, unsigned* out) {
+    unsigned c = 0;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < nblocks; i += (size_t)gridDim.x * blockDim.x) {
+        const uint8_t e = raw[i * 17];
+        c += (e < 32 || e == 255) ? 1u : 0u;
+    }
+    if (c) atomicAdd(out, c);
+}
+int launch_count_special_exps(const uint8_t* raw, size_t nblocks, unsigned* out, hipStream_t s) {
+    hipLaunchKernelGGL(k_count_special_exps, dim3(1024), dim3(256), 0, s, raw, nblocks, out);
+    return hipGetLastError() == hipSuccess ? 0 : -19;
+}
+
 int launch_repack_gateup(const uint8_t* gate, const uint8_t* up, u32x4* out, int ne, int dff, int nb, hipStream_t s) {
     int P = (nb + kBlkPerPart - 1) / kBlkPerPart;
     hipLaunchKernelGGL(k_repack_gateup, dim3(4096), dim3(256), 0, s, gate, up, out, ne, dff, nb, P);

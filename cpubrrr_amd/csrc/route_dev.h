@@ -130,6 +130,66 @@ CPB_DEV T block_sum(T v, T* red) {
 
 constexpr int kChunk = 16;          // router elements per thread: d <= 4096
 
+// Logit of one router row: the reference's fp32 products w[j]*xn[j] (xn in
+// LDS) summed exactly in fp64 with the bias, and a bound on how far the
+// reference's serial fp32 chain (acc = b; acc += w[j]*xn[j]) can lie from it:
+// u/(1-u) * (sum_k |S_k| + n*gamma_n*A) over the exact prefix sums S_k
+// (Higham, Accuracy and Stability of Numerical Algorithms, 2nd ed., 4.2).
+// wv: this thread's C (<= kChunk) consecutive weights from j0.  Every thread
+// of the workgroup calls it; thread 0 receives the results.
+CPB_DEV void router_logit(const float4* wv, int C, int j0, const float* xn, int d, double b, double* dsc,
+                          double* dred, double* out_total, double* out_bound) {
+    const int tid = threadIdx.x, nth = blockDim.x;
+    float p[kChunk];
+    double loc = 0.0, absp = 0.0;
+#pragma unroll
+    for (int i = 0; i < kChunk / 4; i++) {
+        const int j = j0 + 4 * i;
+        const int jc = min(j, d - 4);
+        const float4 xv = *(const float4*)(xn + jc);
+        const float4 w4 = wv[i];
+        const float pr[4] = {w4.x * xv.x, w4.y * xv.y, w4.z * xv.z, w4.w * xv.w};
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const bool in = 4 * i + k < C && j + k < d && j == jc;
+            p[4 * i + k] = in ? pr[k] : 0.0f;
+            loc += (double)p[4 * i + k];
+            absp += fabs((double)p[4 * i + k]);
+        }
+    }
+    // exclusive scan of the chunk sums: wave scan + wave totals
+    const int lane = tid & 63, wv_ = tid >> 6, nw = nth >> 6;
+    double inc = loc;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const double t = __shfl_up(inc, off);
+        if (lane >= off) inc += t;
+    }
+    if (lane == 63) dsc[wv_] = inc;
+    __syncthreads();
+    double woff = 0.0;
+    for (int w2 = 0; w2 < wv_; w2++) woff += dsc[w2];
+    double wtot = dsc[0];
+    for (int w2 = 1; w2 < nw; w2++) wtot += dsc[w2];
+    const double total = b + wtot;
+    double run = b + woff + (inc - loc);
+    double sabs = 0.0;
+#pragma unroll
+    for (int i = 0; i < kChunk; i++) { run += (double)p[i]; sabs += (i < C && j0 + i < d) ? fabs(run) : 0.0; }
+    __syncthreads();
+    const double SS = block_sum(sabs, dred);
+    const double AP = block_sum(absp, dred);
+    if (tid == 0) {
+        const double u = 5.9604644775390625e-08;  // 2^-24
+        const double n = (double)d;
+        const double A = fabs(b) + AP;
+        const double gam = n * u / (1.0 - n * u);
+        double bound = u / (1.0 - u) * (SS + n * gam * A);
+        *out_total = total;
+        *out_bound = bound * 1.0001 + 1e-10 * A + 1e-30;
+    }
+}
+
 // LDS bytes route_expert needs
 CPB_DEV_HOST inline size_t route_lds_bytes(int d) { return sizeof(float) * (2 * d + 32) + sizeof(double) * 32 + sizeof(float) * 64; }
 
@@ -203,55 +263,11 @@ CPB_DEV void route_expert(const RouteArgs& a, int e, int NEg, unsigned char* sme
     }
 
     RSTAMP(3);
-    // ---- router logit of expert e: the reference's fp32 products, exact
-    // fp64 sum and prefix sums, error bound ----
-    float p[kChunk];
-    double loc = 0.0, absp = 0.0;
-#pragma unroll
-    for (int i = 0; i < kChunk / 4; i++) {
-        const int j = j0 + 4 * i;
-        const int jc = min(j, d - 4);
-        const float4 xv = *(const float4*)(xn + jc);
-        const float4 w4 = wv[i];
-        const float pr[4] = {w4.x * xv.x, w4.y * xv.y, w4.z * xv.z, w4.w * xv.w};
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const bool in = 4 * i + k < C && j + k < d && j == jc;
-            p[4 * i + k] = in ? pr[k] : 0.0f;
-            loc += (double)p[4 * i + k];
-            absp += fabs((double)p[4 * i + k]);
-        }
-    }
-    // exclusive scan of the chunk sums: wave scan + wave totals
-    const int lane = tid & 63, wv_ = tid >> 6, nw = nth >> 6;
-    double inc = loc;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const double t = __shfl_up(inc, off);
-        if (lane >= off) inc += t;
-    }
-    if (lane == 63) dsc[wv_] = inc;
-    __syncthreads();
-    double woff = 0.0;
-    for (int w2 = 0; w2 < wv_; w2++) woff += dsc[w2];
-    double wtot = dsc[0];
-    for (int w2 = 1; w2 < nw; w2++) wtot += dsc[w2];
-    const double total = b + wtot;
-    double run = b + woff + (inc - loc);
-    double sabs = 0.0;
-#pragma unroll
-    for (int i = 0; i < kChunk; i++) { run += (double)p[i]; sabs += (i < C && j0 + i < d) ? fabs(run) : 0.0; }
+    // ---- router logit of expert e ----
+    double total = 0.0, bound = 0.0;
+    router_logit(wv, C, j0, xn, d, b, dsc, dred, &total, &bound);
     RSTAMP(4);
-    __syncthreads();
-    const double SS = block_sum(sabs, dred);
-    const double AP = block_sum(absp, dred);
     if (tid == 0) {
-        const double u = 5.9604644775390625e-08;  // 2^-24
-        const double n = (double)d;
-        const double A = fabs(b) + AP;
-        const double gam = n * u / (1.0 - n * u);
-        double bound = u / (1.0 - u) * (SS + n * gam * A);
-        bound = bound * 1.0001 + 1e-10 * A + 1e-30;
         st_dev(a.lstar + e, total);
         st_dev(a.lbound + e, bound);
     }

@@ -154,6 +154,20 @@ class MoeBlock:
             t["exact_router_fallbacks"] = int(tr_p.contents.exact_router_fallbacks)
         return xo, t
 
+    def grouped_sums(self, layer: int, x: np.ndarray, apply_norm: bool = True):
+        """Test hook of the grouped (n_tok > 1) MXFP4 path: returns (x_out,
+        gu_sums [n_tok*k][2][d_ff][d/32], dn_sums [n_tok*k][d][d_ff/32])."""
+        c = self.cfg
+        xo = np.array(x, np.float32, copy=True, order="C")
+        n_tok = xo.shape[0]
+        np_ = n_tok * c.top_k
+        gs = np.zeros((np_, 2, c.d_ff, c.d // 32), np.int32)
+        ds = np.zeros((np_, c.d, c.d_ff // 32), np.int32)
+        L.check(self._lib.cpb_moe_grouped_sums(self._h, layer, xo.ctypes.data_as(L.f32p), n_tok, int(bool(apply_norm)),
+                                               gs.ctypes.data_as(L.i32p), ds.ctypes.data_as(L.i32p)),
+                "cpb_moe_grouped_sums")
+        return xo, gs, ds
+
     def forward_device(self, layer0: int, n_layers: int, x_ptr: int, n_tok: int = 1, apply_norm: bool = True):
         """Asynchronous forward over layers on device memory (x_ptr: device address)."""
         L.check(self._lib.cpb_moe_forward_device(self._h, layer0, n_layers, C.c_void_p(x_ptr), n_tok,
