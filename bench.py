@@ -9,6 +9,8 @@ inputs resident in HBM.  Workloads (synthetic data):
   1  gpt-oss-20b 24-layer MoE stack, Zipf(1.1) router bias   (default)
   2  gpt-oss-120b 36-layer stack, 128 experts, Zipf(1.1)
   3  Qwen3-30B-A3B 48-layer MoE stack: Q4_K gate/up, Q6_K down, top-8 of 128
+  4  gpt-oss-20b layer, 512-token prefill: tokens grouped by expert, expert
+     GEMMs on the matrix cores (8 rotating layer copies)
 Prints one JSON line: value = expert-weight GB/s (algorithmic bytes of the
 active experts + biases + router per token / time), plus tok/s, the roofline
 of the dominant kernel (gate/up) and the CPU baseline (the oracle on the
@@ -44,9 +46,14 @@ CONFIGS = {
     3: dict(name="config3: Qwen3-30B-A3B 48-layer MoE stack (attention omitted), decode batch 1, Q4_K gate/up, "
                  "Q6_K down, softmax then top-8 of 128",
             d=2048, dff=768, ne=128, k=8, layers=48, per_step=48, zipf=None, norm=True, family="qwen"),
+    4: dict(name="config4: gpt-oss-20b MoE layer, 512-token prefill (batched), Zipf(1.1) router bias, tokens grouped "
+                 "by expert, fp8 x fp4 scaled-MFMA expert GEMMs",
+            d=2880, dff=2880, ne=32, k=4, layers=8, per_step=1, zipf=1.1, norm=True, n_tok=512),
 }
 for _c in CONFIGS.values():
     _c.setdefault("family", "gptoss")
+    _c.setdefault("n_tok", 1)
+MFMA_FP8_PEAK_TOPS = 5000.0   # MI355X dense fp8 (the f8f6f4 instructions run fp8 x fp4 at this rate)
 
 
 def layer_bytes(c) -> dict:
@@ -61,6 +68,30 @@ def layer_bytes(c) -> dict:
         dn = k * d * (dff // 32 * 17) + k * d * 4
         router = ne * d * 4 + ne * 4 + (d * 4 if c["norm"] else 0)
     return {"gate_up": gu, "down": dn, "router": router, "total": gu + dn + router}
+
+
+def batched_result(c, args, ms, n_tok) -> dict:
+    """Bench line of a batched (prefill) step: one layer over n_tok tokens."""
+    d, dff, ne, k = c["d"], c["dff"], c["ne"], c["k"]
+    expert_bytes = 3 * d * (d // 32 * 17) + 2 * dff * 4 + d * 4        # one expert's gate, up, down + biases
+    wbytes = ne * expert_bytes + ne * d * 4 + ne * 4                   # every expert holds pairs at this batch size
+    macs = n_tok * k * (2 * dff * d + d * dff)                          # useful int8 multiply-adds
+    sec = ms * 1e-3
+    gbs = wbytes / sec / 1e9
+    tops = 2 * macs / sec / 1e12
+    return {
+        "metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp8 x fp4 (exact int8 x E2M1)", "data": "synthetic",
+        "config": {"workload": c["name"], "tokens_per_step": n_tok, "d": d, "d_ff": dff, "n_expert": ne,
+                   "top_k": k, "weights": "MXFP4 (GGUF type 39)"},
+        "tok_per_s": round(n_tok / sec, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+        "roofline": {"bound": "hbm", "kernel": "whole layer (7 kernels)", "achieved": round(gbs, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "bytes_per_launch": wbytes},
+        "mfma": {"achieved": round(tops, 2), "peak": MFMA_FP8_PEAK_TOPS, "unit": "TOP/s (useful int8-equivalent)",
+                 "frac": round(tops / MFMA_FP8_PEAK_TOPS, 5), "ops_per_step": 2 * macs},
+    }
 
 
 def log(msg):
@@ -80,6 +111,7 @@ def cpu_baseline(host_layers, c, budget_s: float) -> dict:
     n = 0
     t0 = time.perf_counter()
     fwd = O.qwen_moe if c["family"] == "qwen" else O.gptoss_moe
+    # a batch of tokens is n_tok independent decodes for the reference path
     while time.perf_counter() - t0 < budget_s or n == 0:
         L = host_layers[n % len(host_layers)]
         x, _ = fwd(L, x, c["norm"])
@@ -87,7 +119,8 @@ def cpu_baseline(host_layers, c, budget_s: float) -> dict:
     dt = time.perf_counter() - t0
     per_layer = dt / n
     lb = layer_bytes(c)["total"]
-    return {"value": round(1.0 / (per_layer * c["per_step"]), 3), "unit": "tok/s", "cores": threads,
+    tok_s = 1.0 / (per_layer * c["per_step"])
+    return {"value": round(tok_s, 3), "unit": "tok/s", "cores": threads,
             "kind": "port", "sample": f"{n} MoE layers ({len(host_layers)} distinct) of the same workload in "
                                        f"{dt:.1f} s; {per_layer * 1e3:.2f} ms/layer, "
                                        f"{lb / per_layer / 1e9:.2f} GB/s algorithmic",
@@ -121,7 +154,7 @@ def main() -> int:
     if qwen:
         cfg = MoeConfig.qwen3(d=d, n_expert=ne, top_k=k, d_ff=dff, n_layer=nl)
     else:
-        cfg = MoeConfig.gptoss(d=d, n_expert=ne, top_k=k, d_ff=dff, n_layer=nl)
+        cfg = MoeConfig.gptoss(d=d, n_expert=ne, top_k=k, d_ff=dff, n_layer=nl, max_tokens=c["n_tok"])
     dev = torch.device("cuda:0")
     torch.cuda.set_device(0)
     blk = MoeBlock(cfg, device=0)
@@ -144,7 +177,11 @@ def main() -> int:
     stream = torch.cuda.Stream()
     torch.cuda.set_stream(stream)
     blk.set_stream(stream.cuda_stream)
-    x = torch.from_numpy(synth.token(d, 0, 0)).to(dev)
+    n_tok = c["n_tok"]
+    if n_tok > 1:
+        x = torch.from_numpy(np.stack([synth.token(d, 0, i) for i in range(n_tok)])).to(dev)
+    else:
+        x = torch.from_numpy(synth.token(d, 0, 0)).to(dev)
     if args.calib_copy_mib:
         # a copy kernel of known size: its FETCH_SIZE / WRITE_SIZE give the
         # counter-to-bytes factor for the kernels above
@@ -158,9 +195,9 @@ def main() -> int:
 
     def step(i):
         if c["per_step"] == nl:
-            blk.forward_device(0, nl, x.data_ptr(), 1, c["norm"])
+            blk.forward_device(0, nl, x.data_ptr(), n_tok, c["norm"])
         else:
-            blk.forward_device(i % nl, 1, x.data_ptr(), 1, c["norm"])
+            blk.forward_device(i % nl, 1, x.data_ptr(), n_tok, c["norm"])
 
     for i in range(args.warmup):
         step(i)
@@ -180,6 +217,15 @@ def main() -> int:
         step(i)
     kt = blk.kernel_times()
     blk.timing(False)
+
+    if n_tok > 1:
+        out = batched_result(c, args, ms, n_tok)
+        if not args.no_cpu:
+            log("timing the CPU baseline ...")
+            out["cpu_baseline"] = cpu_baseline(host_keep, c, args.cpu_seconds)
+        blk.close()
+        print(json.dumps(out), flush=True)
+        return 0
 
     lb = layer_bytes(c)
     bytes_tok = lb["total"] * c["per_step"]

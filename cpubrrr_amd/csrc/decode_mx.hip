@@ -273,7 +273,7 @@ int launch_decode_mx(const DecodeArgs& a, const DecodeArgs* dev_args, hipStream_
     size_t lds = route_lds_bytes(a.d);
     const size_t gu_lds = sizeof(uint32_t) * kWaves * kXsDw + sizeof(float) * kWaves * 64;
     const size_t dn_lds = sizeof(uint32_t) * kWaves * a.k * kXsDw + sizeof(float) * (kWaves * 64 + 64);
-    const size_t sel_lds = sizeof(double) * 4 * a.ne + 64;
+    const size_t sel_lds = sizeof(double) * 4 * a.ne + sizeof(float) * a.d + 64;
     lds = std::max(std::max(lds, gu_lds), std::max(dn_lds, sel_lds));
     int dev = 0, ncu = 0, per_cu = 0;
     if (hipGetDevice(&dev) != hipSuccess ||

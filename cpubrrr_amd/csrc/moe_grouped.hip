@@ -45,7 +45,7 @@ typedef int v8i_g __attribute__((ext_vector_type(8)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
 constexpr int kImg = 64;          // image bytes per 32-block
-constexpr int kRouteTok = 16;     // tokens per router workgroup
+constexpr int kRouteTok = 4;      // tokens per router workgroup
 
 // exact e4m3 encodings used by the split (v = 0, an integer in [1, 15] or 16*h)
 CPB_DEV uint32_t e4m3_small(int v) {
@@ -118,21 +118,18 @@ __global__ __launch_bounds__(256) void k_router_batch(GroupedArgs a) {
 }
 
 // ---- 3. top-k + softmax, one wavefront per token ----
-__global__ __launch_bounds__(256) void k_select_batch(GroupedArgs a) {
+__global__ __launch_bounds__(64) void k_select_batch(GroupedArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
-    __shared__ Selection sel[4];
-    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int t = blockIdx.x * 4 + w;
-    if (t >= a.n_tok) return;
-    double* lds = (double*)smem + (size_t)w * (4 * a.ne + 8);
+    __shared__ Selection sel;
+    const int lane = threadIdx.x, t = blockIdx.x;
     select_experts_wave(a.lstar + (size_t)t * a.ne, a.lbound + (size_t)t * a.ne, a.ne, a.k, a.router_w, a.router_b,
-                        a.xn + (size_t)t * a.d, a.d, lds, &sel[w], a.logits + (size_t)t * a.ne);
+                        a.xn + (size_t)t * a.d, a.d, (double*)smem, &sel, a.logits + (size_t)t * a.ne);
     if (lane < a.k) {
-        a.ids[(size_t)t * a.k + lane] = sel[w].ids[lane];
-        a.wts[(size_t)t * a.k + lane] = sel[w].wts[lane];
-        a.logits[(size_t)t * a.ne + sel[w].ids[lane]] = sel[w].logit[lane];
+        a.ids[(size_t)t * a.k + lane] = sel.ids[lane];
+        a.wts[(size_t)t * a.k + lane] = sel.wts[lane];
+        a.logits[(size_t)t * a.ne + sel.ids[lane]] = sel.logit[lane];
     }
-    if (lane == 0) a.fallback[t] = sel[w].fallback;
+    if (lane == 0) a.fallback[t] = sel.fallback;
 }
 
 // ---- 4. group the (token, slot) pairs by expert (stable), tile table ----
@@ -184,77 +181,160 @@ CPB_DEV v16f mx_block_mfma(const u32x4& w, const u32x4& x0, const u32x4& x1, uin
     return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(A, B, Z, 4, 0, 0, (int)e, 0, 127);
 }
 
-// ---- 5. grouped gate/up + SwiGLU-OAI + Q8 (+ image of h) ----
-// grid (max_tiles, ceil(dff/32 / 4)); wave = one 32-row tile of gate and up.
+// LDS staging of one k-part's activations for a 32-token tile: per block i
+// and token ti an 80-byte slot (64 B image + 16 B pad against bank
+// conflicts), then the 15 x 32 scales.
+constexpr int kSlot = 80;
+constexpr int kStageBytes = kBlkPerPart * 32 * kSlot + kBlkPerPart * 32 * 4;
+
+// Staging of blocks [q*15, q*15+15) of the images / scales of the tile's
+// tokens (src[ti] = token or pair row, -1 for padding), split into the global
+// loads (into registers, issued early) and the LDS stores (after the wait).
+// Each thread moves up to kStageVec 16-byte chunks and one scale.
+constexpr int kStageVec = (kBlkPerPart * 32 * 4 + 511) / 512;
+struct StageRegs {
+    u32x4 v[kStageVec];
+    uint32_t s;
+};
+CPB_DEV StageRegs stage_load(const uint8_t* img, const float* sc, size_t rows, int nbk, int q, const int* src) {
+    const int tid = threadIdx.x;
+    const __amdgpu_buffer_rsrc_t ri = buf_rsrc(img, (uint32_t)(rows * nbk * kImg));
+    const __amdgpu_buffer_rsrc_t rs = buf_rsrc(sc, (uint32_t)(rows * nbk * 4));
+    StageRegs g;
+#pragma unroll
+    for (int k = 0; k < kStageVec; k++) {
+        const int idx = tid + 512 * k;
+        const int i = idx >> 7, ti = (idx >> 2) & 31, c = idx & 3;
+        const int b = q * kBlkPerPart + i, r = src[ti];
+        const uint32_t off = (idx < kBlkPerPart * 128 && b < nbk && r >= 0) ? ((uint32_t)r * nbk + b) * kImg + c * 16
+                                                                            : kOffNone;
+        g.v[k] = __builtin_amdgcn_raw_buffer_load_b128(ri, off, 0, 0);
+    }
+    {
+        const int i = tid >> 5, ti = tid & 31;
+        const int b = q * kBlkPerPart + i, r = src[ti];
+        const uint32_t off = (tid < kBlkPerPart * 32 && b < nbk && r >= 0) ? ((uint32_t)r * nbk + b) * 4 : kOffNone;
+        g.s = __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0);
+    }
+    return g;
+}
+CPB_DEV void stage_store(unsigned char* st, const StageRegs& g) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int k = 0; k < kStageVec; k++) {
+        const int idx = tid + 512 * k;
+        if (idx < kBlkPerPart * 128) {
+            const int i = idx >> 7, ti = (idx >> 2) & 31, c = idx & 3;
+            *(u32x4*)(st + (i * 32 + ti) * kSlot + c * 16) = g.v[k];
+        }
+    }
+    if (tid < kBlkPerPart * 32) ((uint32_t*)(st + kBlkPerPart * 32 * kSlot))[tid] = g.s;
+}
+
+// Blocks [i0, i0 + N) of one wave's k-part: D = A(rows) x B(tokens) per
+// block, acc = fma(D, xsb, acc) in block order (the decode kernels' order).
+// w[k] = code block i0 + k of the lane's row, ex = the k-part's exponents.
+// TRACE writes the int32 block sums S = D * 2^(128 - e) of valid rows.
 template <bool TRACE>
-__global__ __launch_bounds__(256) void k_gateup_grouped(GroupedArgs a) {
+CPB_DEV v16f part_mfma(const u32x4* wv, const unsigned char* st, int lane, int q, int nbk, int32_t* trace_base,
+                       size_t trace_row_stride, bool trace_ok) {
+    const int ti = lane & 31, hb = lane >> 5;
+    const float* sl = (const float*)(st + kBlkPerPart * 32 * kSlot);
+    v16f acc = {};
+#pragma unroll
+    for (int i = 0; i < kBlkPerPart; i++) {
+        const unsigned char* xp = st + (i * 32 + ti) * kSlot + hb * 32;
+        const u32x4 x0 = *(const u32x4*)xp, x1 = *(const u32x4*)(xp + 16);
+        const float s = sl[i * 32 + ti];
+        const uint32_t eb = (wv[0][i >> 2] >> (8 * (i & 3))) & 0xffu;
+        const v16f D = mx_block_mfma(wv[1 + i], x0, x1, eb);
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[r] = fmaf(D[r], s, acc[r]);
+        if (TRACE) {
+            const int b = q * kBlkPerPart + i;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int rl = 8 * (r >> 2) + 4 * hb + (r & 3);
+                const int e_r = __shfl((int)eb, rl);
+                if (trace_ok && b < nbk) trace_base[rl * trace_row_stride + b] = (int)ldexpf(D[r], 128 - e_r);
+            }
+        }
+    }
+    return acc;
+}
+
+// Weight window of one k-part (16 units) for the lane's row: nontemporal loads.
+CPB_DEV void load_window(const u32x4* p, size_t stride, u32x4* wv) {
+#pragma unroll
+    for (int u = 0; u < kUnits; u++) wv[u] = __builtin_nontemporal_load(p + (size_t)u * stride);
+}
+
+// The k-part loop shared by the two grouped GEMMs: per k-part the workgroup
+// stages the tile's activations in LDS; each wave's next 16-unit weight
+// window is requested before the current one is consumed.  Returns the row
+// totals (k-parts added in order, as the decode kernels do).
+template <bool TRACE>
+CPB_DEV v16f grouped_parts(const u32x4* wbase, size_t stride, int P, unsigned char* smem, const uint8_t* img,
+                           const float* sc, size_t rows, int nbk, const int* src, int lane, int32_t* tb, bool trace_ok) {
+    const size_t part = (size_t)kUnits * stride;
+    u32x4 wv[kUnits], wn[kUnits];
+    load_window(wbase, stride, wv);
+    v16f tot = {};
+    for (int q = 0; q < P; q++) {
+        const StageRegs g = stage_load(img, sc, rows, nbk, q, src);
+        stage_store(smem, g);
+        __syncthreads();
+        if (q + 1 < P) load_window(wbase + (size_t)(q + 1) * part, stride, wn);
+        const v16f acc = part_mfma<TRACE>(wv, smem, lane, q, nbk, tb, nbk, trace_ok);
+#pragma unroll
+        for (int r = 0; r < 16; r++) tot[r] += acc[r];
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < kUnits; u++) wv[u] = wn[u];
+    }
+    return tot;
+}
+
+// ---- 5. grouped gate/up + SwiGLU-OAI + Q8 (+ image of h) ----
+// grid (max_tiles, ceil(dff/32 / 4)); 8 waves: wave w = row tile w/2 of this
+// group, gate (w even) or up (w odd).
+template <bool TRACE>
+__global__ __launch_bounds__(512) void k_gateup_grouped(GroupedArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ int src[32];
     if ((int)blockIdx.x >= *a.ntiles) return;
     const int4 tl = a.tiles[blockIdx.x];
     const int e = uniform(tl.x), start = uniform(tl.y), cnt = uniform(tl.z);
-    const int lane = threadIdx.x & 63;
+    const int lane = threadIdx.x & 63, w = uniform((int)(threadIdx.x >> 6));
     const int T = a.dff / 32, P = a.parts_gu, nb = a.nb;
-    const int rt = blockIdx.y * 4 + uniform((int)(threadIdx.x >> 6));
-    if (rt >= T) return;
+    const int rt = blockIdx.y * 4 + (w >> 1), isup = w & 1;
+    const bool live = rt < T;
+    if (threadIdx.x < 32) src[threadIdx.x] = (int)threadIdx.x < cnt ? a.sorted[start + threadIdx.x] / a.k : -1;
+    __syncthreads();
     const int ti = lane & 31, hb = lane >> 5;
     const bool valid = ti < cnt;
-    const int pair = a.sorted[start + (valid ? ti : 0)];
-    const int tok = pair / a.k;
-    // one resource over all tokens (a buffer base must be wave-uniform); lanes
-    // address their own token, blocks past nb read zero
-    const __amdgpu_buffer_rsrc_t rimg = buf_rsrc(a.ximg, (uint32_t)((size_t)a.n_tok * nb * kImg));
-    const __amdgpu_buffer_rsrc_t rsc = buf_rsrc(a.xsb, (uint32_t)((size_t)a.n_tok * nb * 4));
-    const uint32_t img0 = (uint32_t)tok * nb * kImg + hb * 32, sc0 = (uint32_t)tok * nb * 4;
-    const u32x4* wbase = a.gu + (((size_t)e * T + rt) * P) * kUnits * 64 + (lane & 31);
+    const int pair = valid ? a.sorted[start + ti] : 0;
+    const u32x4* wbase = a.gu + (((size_t)e * T + (live ? rt : 0)) * P) * kUnits * 64 + isup * 32 + (lane & 31);
+    int32_t* tb = TRACE ? a.gu_sums + (((size_t)pair * 2 + isup) * a.dff + rt * 32) * nb : nullptr;
 
-    v16f tg = {}, tu = {};
-    for (int q = 0; q < P; q++) {
-        const u32x4* wp = wbase + (size_t)q * kUnits * 64;
-        const u32x4 eg = __builtin_nontemporal_load(wp), eu = __builtin_nontemporal_load(wp + 32);
-        v16f ag = {}, au = {};
+    const v16f tot = grouped_parts<TRACE>(wbase, 64, P, smem, a.ximg, a.xsb, (size_t)a.n_tok, nb, src, lane, tb,
+                                          valid && live);
+    // up totals to the gate wave of the same row tile (LDS reused)
+    float* xch = (float*)smem;
+    if (isup) {
 #pragma unroll
-        for (int i = 0; i < kBlkPerPart; i++) {
-            const int b = q * kBlkPerPart + i;
-            const u32x4 wg = __builtin_nontemporal_load(wp + (1 + i) * 64);
-            const u32x4 wu = __builtin_nontemporal_load(wp + (1 + i) * 64 + 32);
-            const uint32_t off = b < nb ? img0 + (uint32_t)b * kImg : kOffNone;
-            const u32x4 x0 = __builtin_amdgcn_raw_buffer_load_b128(rimg, off, 0, 0);
-            const u32x4 x1 = __builtin_amdgcn_raw_buffer_load_b128(rimg, off + 16, 0, 0);
-            const float s = __uint_as_float(
-                __builtin_amdgcn_raw_buffer_load_b32(rsc, b < nb ? sc0 + (uint32_t)b * 4 : kOffNone, 0, 0));
-            const uint32_t ebg = (eg[i >> 2] >> (8 * (i & 3))) & 0xffu;
-            const uint32_t ebu = (eu[i >> 2] >> (8 * (i & 3))) & 0xffu;
-            const v16f Dg = mx_block_mfma(wg, x0, x1, ebg);
-            const v16f Du = mx_block_mfma(wu, x0, x1, ebu);
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                ag[r] = fmaf(Dg[r], s, ag[r]);
-                au[r] = fmaf(Du[r], s, au[r]);
-            }
-            if (TRACE) {
-                // S = D * 2^(128 - e) with e the exponent of D[r]'s row (held by lane row % 32)
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int rl = 8 * (r >> 2) + 4 * hb + (r & 3), row = rt * 32 + rl;
-                    const int eg_r = __shfl((int)ebg, rl), eu_r = __shfl((int)ebu, rl);
-                    if (valid && b < nb) {
-                        a.gu_sums[(((size_t)pair * 2 + 0) * a.dff + row) * nb + b] = (int)ldexpf(Dg[r], 128 - eg_r);
-                        a.gu_sums[(((size_t)pair * 2 + 1) * a.dff + row) * nb + b] = (int)ldexpf(Du[r], 128 - eu_r);
-                    }
-                }
-            }
-        }
-#pragma unroll
-        for (int r = 0; r < 16; r++) { tg[r] += ag[r]; tu[r] += au[r]; }
+        for (int r = 0; r < 16; r++) xch[((w >> 1) * 16 + r) * 64 + lane] = tot[r];
     }
-    // bias, SwiGLU-OAI (engine_gpt2.rs:887-906), Q8 of the 32-row block of h
+    __syncthreads();
+    if (isup || !live) return;
     float hv[16], m = 0.0f;
 #pragma unroll
     for (int r = 0; r < 16; r++) {
         const int row = rt * 32 + 8 * (r >> 2) + 4 * hb + (r & 3);
-        float vg = tg[r], vu = tu[r];
+        float vg = tot[r], vu = xch[((w >> 1) * 16 + r) * 64 + lane];
         if (a.gate_b) vg += a.gate_b[(size_t)e * a.dff + row];
         if (a.up_b) vu += a.up_b[(size_t)e * a.dff + row];
-        const float xg = fminf(vg, a.limit);
+        const float xg = fminf(vg, a.limit);                           // engine_gpt2.rs:887-906
         const float yu = fminf(fmaxf(vu, -a.limit), a.limit);
         hv[r] = (xg / (1.0f + expf(-a.alpha * xg))) * (yu + 1.0f);
         m = fmaxf(m, fabsf(hv[r]));
@@ -277,57 +357,30 @@ __global__ __launch_bounds__(256) void k_gateup_grouped(GroupedArgs a) {
 }
 
 // ---- 6. grouped down (+ bias) into dnout ----
-// grid (max_tiles, ceil(d/32 / 4)); wave = one 32-row tile of down.
+// grid (max_tiles, ceil(d/32 / 8)); 8 waves = 8 row tiles of 32 rows.
 template <bool TRACE>
-__global__ __launch_bounds__(256) void k_down_grouped(GroupedArgs a) {
+__global__ __launch_bounds__(512) void k_down_grouped(GroupedArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ int src[32];
     if ((int)blockIdx.x >= *a.ntiles) return;
     const int4 tl = a.tiles[blockIdx.x];
     const int e = uniform(tl.x), start = uniform(tl.y), cnt = uniform(tl.z);
-    const int lane = threadIdx.x & 63;
+    const int lane = threadIdx.x & 63, w = uniform((int)(threadIdx.x >> 6));
     const int RTv = 64 / a.k, Tv = a.d / RTv, P = a.parts_dn, nbf = a.nbf;
-    const int rt = blockIdx.y * 4 + uniform((int)(threadIdx.x >> 6));
-    if (rt >= a.d / 32) return;
+    const int rt = blockIdx.y * 8 + w;
+    const bool live = rt < a.d / 32;
+    if (threadIdx.x < 32) src[threadIdx.x] = (int)threadIdx.x < cnt ? a.sorted[start + threadIdx.x] : -1;
+    __syncthreads();
     const int ti = lane & 31, hb = lane >> 5;
     const bool valid = ti < cnt;
-    const int pair = a.sorted[start + (valid ? ti : 0)];
-    const size_t np = (size_t)a.n_tok * a.k;
-    const __amdgpu_buffer_rsrc_t rimg = buf_rsrc(a.himg, (uint32_t)(np * nbf * kImg));
-    const __amdgpu_buffer_rsrc_t rsc = buf_rsrc(a.hsb, (uint32_t)(np * nbf * 4));
-    const uint32_t img0 = (uint32_t)pair * nbf * kImg + hb * 32, sc0 = (uint32_t)pair * nbf * 4;
-    const int row_l = rt * 32 + (lane & 31);          // this lane's A row
+    const int pair = valid ? a.sorted[start + ti] : 0;
+    const int row_l = (live ? rt : 0) * 32 + (lane & 31);             // this lane's A row
     const u32x4* wbase = a.dn + (((size_t)e * Tv + row_l / RTv) * P) * kUnits * RTv + row_l % RTv;
+    int32_t* tb = TRACE ? a.dn_sums + ((size_t)pair * a.d + rt * 32) * nbf : nullptr;
 
-    v16f tot = {};
-    for (int q = 0; q < P; q++) {
-        const u32x4* wp = wbase + (size_t)q * kUnits * RTv;
-        const u32x4 ev = __builtin_nontemporal_load(wp);
-        v16f acc = {};
-#pragma unroll
-        for (int i = 0; i < kBlkPerPart; i++) {
-            const int b = q * kBlkPerPart + i;
-            const u32x4 w = __builtin_nontemporal_load(wp + (1 + i) * RTv);
-            const uint32_t off = b < nbf ? img0 + (uint32_t)b * kImg : kOffNone;
-            const u32x4 x0 = __builtin_amdgcn_raw_buffer_load_b128(rimg, off, 0, 0);
-            const u32x4 x1 = __builtin_amdgcn_raw_buffer_load_b128(rimg, off + 16, 0, 0);
-            const float s = __uint_as_float(
-                __builtin_amdgcn_raw_buffer_load_b32(rsc, b < nbf ? sc0 + (uint32_t)b * 4 : kOffNone, 0, 0));
-            const uint32_t eb = (ev[i >> 2] >> (8 * (i & 3))) & 0xffu;
-            const v16f D = mx_block_mfma(w, x0, x1, eb);
-#pragma unroll
-            for (int r = 0; r < 16; r++) acc[r] = fmaf(D[r], s, acc[r]);
-            if (TRACE) {
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int rl = 8 * (r >> 2) + 4 * hb + (r & 3), row = rt * 32 + rl;
-                    const int e_r = __shfl((int)eb, rl);
-                    if (valid && b < nbf) a.dn_sums[((size_t)pair * a.d + row) * nbf + b] = (int)ldexpf(D[r], 128 - e_r);
-                }
-            }
-        }
-#pragma unroll
-        for (int r = 0; r < 16; r++) tot[r] += acc[r];
-    }
-    if (!valid) return;
+    const v16f tot = grouped_parts<TRACE>(wbase, RTv, P, smem, a.himg, a.hsb, (size_t)a.n_tok * a.k, nbf, src, lane,
+                                          tb, valid && live);
+    if (!valid || !live) return;
     float* out = a.dnout + (size_t)pair * a.d + rt * 32 + 4 * hb;
 #pragma unroll
     for (int g = 0; g < 4; g++) {
@@ -357,15 +410,16 @@ int launch_grouped_layer(const GroupedArgs& a, bool trace, hipStream_t s) {
     launch(k_prep_batch, dim3(nt), dim3(256), sizeof(float) * (2 * a.d + 64), s, a);
     launch(k_router_batch, dim3(a.ne, (nt + kRouteTok - 1) / kRouteTok), dim3(256),
            sizeof(float) * (a.d + 32) + sizeof(double) * 32, s, a);
-    launch(k_select_batch, dim3((nt + 3) / 4), dim3(256), sizeof(double) * 4 * (4 * a.ne + 8), s, a);
+    launch(k_select_batch, dim3(nt), dim3(64), sizeof(double) * 4 * a.ne + sizeof(float) * a.d + 64, s, a);
     launch(k_group, dim3(1), dim3(1024), 0, s, a);
-    const dim3 ggu(a.max_tiles, (a.dff / 32 + 3) / 4), gdn(a.max_tiles, (a.d / 32 + 3) / 4);
+    const dim3 ggu(a.max_tiles, (a.dff / 32 + 3) / 4), gdn(a.max_tiles, (a.d / 32 + 7) / 8);
+    const size_t lds_gu = kStageBytes;         // >= the 16 KB epilogue exchange
     if (trace) {
-        launch(k_gateup_grouped<true>, ggu, dim3(256), 0, s, a);
-        launch(k_down_grouped<true>, gdn, dim3(256), 0, s, a);
+        launch(k_gateup_grouped<true>, ggu, dim3(512), lds_gu, s, a);
+        launch(k_down_grouped<true>, gdn, dim3(512), (size_t)kStageBytes, s, a);
     } else {
-        launch(k_gateup_grouped<false>, ggu, dim3(256), 0, s, a);
-        launch(k_down_grouped<false>, gdn, dim3(256), 0, s, a);
+        launch(k_gateup_grouped<false>, ggu, dim3(512), lds_gu, s, a);
+        launch(k_down_grouped<false>, gdn, dim3(512), (size_t)kStageBytes, s, a);
     }
     launch(k_combine_batch, dim3(nt), dim3(256), 0, s, a);
     return hipGetLastError() == hipSuccess ? 0 : -19;

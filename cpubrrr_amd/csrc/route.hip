@@ -63,7 +63,7 @@ __global__ __launch_bounds__(64) void k_select(SelectArgs a) {
 }
 
 int launch_select(const SelectArgs* a, hipStream_t s) {
-    size_t lds = sizeof(double) * 4 * a->n_expert + 64;
+    size_t lds = sizeof(double) * 4 * a->n_expert + sizeof(float) * a->d + 64;
     launch(k_select, dim3(1), dim3(64), lds, s, *a);
     return hipGetLastError() == hipSuccess ? 0 : -19;
 }
@@ -72,7 +72,7 @@ int launch_route(const RouteArgs* a, const SelectArgs* sa, unsigned* arrive, hip
     if (a->n_expert > 256 || a->n_expert < a->top_k || a->top_k > 8 || a->d % 32 != 0 || a->d > 4096)
         return -22;
     size_t lds = route_lds_bytes(a->d);
-    const size_t lds_sel = sizeof(double) * 4 * a->n_expert + 64;
+    const size_t lds_sel = sizeof(double) * 4 * a->n_expert + sizeof(float) * a->d + 64;
     if (lds_sel > lds) lds = lds_sel;
     launch(k_route, dim3(a->n_expert), dim3(256), lds, s, *a, *sa, arrive);
     return hipGetLastError() == hipSuccess ? 0 : -19;

@@ -23,7 +23,8 @@ struct Selection {
     int fallback;       // 1 when the exact serial logits were needed
 };
 
-// Executed by one wavefront (64 lanes).  lds: 4*NE doubles of scratch.
+// Executed by one wavefront (64 lanes).  lds: 4*NE doubles + d floats of
+// scratch (the floats only for the exact fallback).
 // Lane l holds experts l, l+64, ... (NE <= 256) in registers; the top-k come
 // from k rounds of wave-wide argmax (cross-lane shuffles, no LDS round
 // trips), the certification from one wave-wide max.  logits_out (optional)
@@ -115,12 +116,40 @@ CPB_DEV void select_experts_wave(const double* __restrict__ Ls, const double* __
         double tau = 1e300;
         for (int i = 0; i < K; i++) { const int e = sSel[i]; tau = fmin(tau, sL[e] - (sH[e] - sL[e])); }
         __builtin_amdgcn_wave_barrier();
+        // xn staged in LDS with coherent 16-byte loads (it may have been written
+        // by other workgroups of this launch), then each candidate lane runs the
+        // reference's serial chain with its router row fetched 64 weights ahead
+        float* xst = (float*)(lds + 4 * NE);
+        {
+            const __amdgpu_buffer_rsrc_t r = buf_rsrc(xn, (uint32_t)d * 4);
+            for (int i = lane; i < d / 4; i += 64) ((u32x4*)xst)[i] = ld_dev16(r, (uint32_t)i * 16);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         for (int e = lane; e < NE; e += 64) {
             double v = -1e300;
             if (sH[e] >= tau) {
                 float acc = router_b ? router_b[e] : 0.0f;
                 const float* Wr = router_w + (size_t)e * d;
-                for (int j = 0; j < d; j++) acc = __fadd_rn(acc, __fmul_rn(Wr[j], ld_dev(xn + j)));
+                float4 w4[16], n4[16];
+#pragma unroll
+                for (int u = 0; u < 16; u++) w4[u] = 4 * u < d ? *(const float4*)(Wr + 4 * u) : float4{0, 0, 0, 0};
+                for (int j0 = 0; j0 < d; j0 += 64) {
+                    // next chunk requested before this one is consumed
+#pragma unroll
+                    for (int u = 0; u < 16; u++)
+                        n4[u] = j0 + 64 + 4 * u < d ? *(const float4*)(Wr + j0 + 64 + 4 * u) : float4{0, 0, 0, 0};
+#pragma unroll
+                    for (int u = 0; u < 16; u++) {
+                        if (j0 + 4 * u >= d) break;
+                        const float* w = (const float*)&w4[u];
+#pragma unroll
+                        for (int c = 0; c < 4; c++) acc = __fadd_rn(acc, __fmul_rn(w[c], xst[j0 + 4 * u + c]));
+                    }
+#pragma unroll
+                    for (int u = 0; u < 16; u++) w4[u] = n4[u];
+                }
                 v = (double)acc;
             }
             sL[e] = v;
