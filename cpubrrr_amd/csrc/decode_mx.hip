@@ -31,7 +31,10 @@ namespace cpb {
 
 constexpr int kThreads = 384;           // 6 waves = 6 k-parts of 15 blocks (K <= 2880)
 constexpr int kWaves = kThreads / 64;
-constexpr long kSpinLimit = 1L << 24;   // bounded wait (~1 s)
+constexpr long kSpinLimit = 1L << 20;   // bounded wait (well under 1 s; a legitimate wait is < 100 us)
+#ifndef CPB_SPIN_SLEEP
+#define CPB_SPIN_SLEEP 2                // s_sleep units (64 cycles) between polls of a counter
+#endif
 
 // Data handed between workgroups is written with device-coherent stores
 // (st_dev); each wave waits for its stores to complete, then one atomic
@@ -48,8 +51,9 @@ CPB_DEV void wait_ge(const unsigned* c, unsigned target, int32_t* err) {
     if (threadIdx.x == 0) {
         long n = 0;
         while (ld_dev(c) < target) {
-            __builtin_amdgcn_s_sleep(1);
-            if (++n > kSpinLimit) { st_dev(err, 1); break; }
+            __builtin_amdgcn_s_sleep(CPB_SPIN_SLEEP);
+            // a wait that expired anywhere ends every later wait at once
+            if (++n > kSpinLimit || ((n & 1023) == 0 && ld_dev(err) != 0)) { st_dev(err, 1); break; }
         }
     }
     __syncthreads();
@@ -192,7 +196,17 @@ CPB_DEV void decode_layer(const DecodeArgs& a, int li, Selection& sel,
     unsigned* H = R + 1;
     unsigned* X = R + 2;
     DSTAMP(0);
+    __shared__ unsigned last_route;
     if (is_route) {
+        // warm this workgroup's router row and the norm weights into L2
+        // while the previous layer finishes
+        {
+            const int C = ((a.d + 4 * kThreads - 1) / (4 * kThreads)) * 4, j0 = threadIdx.x * C;
+            float warm = 0.0f;
+            for (int j = j0; j < j0 + C && j < a.d; j += 4) warm += Lp.router_w[(size_t)re * a.d + j];
+            if (Lp.norm_w && (int)threadIdx.x * 4 < a.d) warm += Lp.norm_w[threadIdx.x * 4];
+            asm volatile("" :: "v"(warm));
+        }
         if (li > 0) wait_ge(R - 1, (unsigned)a.T_dn, a.error);    // x of the previous layer complete
         DSTAMP(1);
         RouteArgs ra{};
@@ -202,35 +216,48 @@ CPB_DEV void decode_layer(const DecodeArgs& a, int li, Selection& sel,
         ra.xn = a.xn; ra.xq = a.xq; ra.xqn = a.xqn; ra.xsb = a.xsb; ra.xsum = nullptr;
         ra.lstar = a.lstar; ra.lbound = a.lbound;
         route_expert(ra, re, a.ne, smem);
-        signal_done(R);
+        drain_memory();
+        __syncthreads();
+        if (threadIdx.x == 0)
+            last_route = __hip_atomic_fetch_add(R, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)a.ne - 1;
+        __syncthreads();
         DSTAMP(2);
+        if (last_route) {
+            // the last routing workgroup selects once for everyone and
+            // publishes ids / weights, then bumps R past ne
+            if (threadIdx.x < 64) {
+                select_experts_wave(a.lstar, a.lbound, a.ne, a.k, Lp.router_w, Lp.router_b, a.xn, a.d, (double*)smem,
+                                    &sel, a.logits);
+                const int lane = threadIdx.x;
+                if (lane < a.k) {
+                    st_dev(a.ids + lane, sel.ids[lane]);
+                    st_dev(a.wts + lane, sel.wts[lane]);
+                    a.logits[sel.ids[lane]] = sel.logit[lane];
+                }
+                if (lane == 0) a.fallback[0] = sel.fallback;
+#ifdef CPB_DECODE_STAMPS
+                if (a.stamps && lane < a.k) {
+                    a.stamps[(size_t)1 << 20 | (li * 16 + lane)] = (unsigned long long)sel.ids[lane];
+                    a.stamps[(size_t)1 << 20 | (li * 16 + 8 + lane)] = __float_as_uint(sel.wts[lane]);
+                }
+#endif
+            }
+            signal_done(R);
+        }
     }
-    wait_ge(R, (unsigned)a.ne, a.error);
+    wait_ge(R, (unsigned)a.ne + 1, a.error);
     DSTAMP(3);
-    if (threadIdx.x < 64)
-        select_experts_wave(a.lstar, a.lbound, a.ne, a.k, Lp.router_w, Lp.router_b, a.xn, a.d, (double*)smem, &sel);
+    if (threadIdx.x < 8) {
+        // every workgroup reads the published selection
+        const int i = threadIdx.x < a.k ? threadIdx.x : 0;
+        sel.ids[threadIdx.x] = ld_dev(a.ids + i);
+        sel.wts[threadIdx.x] = ld_dev(a.wts + i);
+    }
     __syncthreads();
 #ifdef CPB_DECODE_STAMPS
     if (a.stamps && li == 0 && threadIdx.x < a.k && w < 512)
         a.stamps[((size_t)1 << 20) + 2048 + w * 4 + threadIdx.x] = (unsigned long long)sel.ids[threadIdx.x];
 #endif
-    if (w == 0 && threadIdx.x < 64) {
-        const int lane = threadIdx.x;
-        for (int i = lane; i < a.ne; i += 64) a.logits[i] = (float)ld_dev(a.lstar + i);
-        if (lane < a.k) {
-            a.ids[lane] = sel.ids[lane];
-            a.wts[lane] = sel.wts[lane];
-            a.logits[sel.ids[lane]] = sel.logit[lane];
-        }
-        if (lane == 0) a.fallback[0] = sel.fallback;
-#ifdef CPB_DECODE_STAMPS
-        // probe builds: the selection each layer used (workgroup 0)
-        if (a.stamps && lane < a.k) {
-            a.stamps[(size_t)1 << 20 | (li * 16 + lane)] = (unsigned long long)sel.ids[lane];
-            a.stamps[(size_t)1 << 20 | (li * 16 + 8 + lane)] = __float_as_uint(sel.wts[lane]);
-        }
-#endif
-    }
     DSTAMP(4);
     layer_tiles(a, Lp, sel, w, H, X, smem, li);
     __syncthreads();
@@ -280,7 +307,18 @@ int launch_decode_mx(const DecodeArgs& a, const DecodeArgs* dev_args, hipStream_
         hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_decode_mx, kThreads, lds) != hipSuccess)
         return -19;
-    if ((long)per_cu * ncu < G) return -28;
+    // The occupancy query does not model how a workgroup's waves land on a
+    // CU's 4 SIMDs: with kWaves = 6 the worst placement puts 2 waves of each
+    // workgroup on one SIMD.  Require that many waves per SIMD for every
+    // co-resident workgroup the count below relies on (register file: 512
+    // VGPRs per lane per SIMD).
+    hipFuncAttributes fa{};
+    if (hipFuncGetAttributes(&fa, (const void*)k_decode_mx) != hipSuccess) return -19;
+    const int regs = fa.numRegs > 0 ? fa.numRegs : 512;
+    const int waves_per_simd = 512 / ((regs + 7) / 8 * 8);
+    const int worst_per_wg = (kWaves + 3) / 4;
+    const int safe_per_cu = std::min(per_cu, waves_per_simd / worst_per_wg);
+    if ((long)safe_per_cu * ncu < G) return -28;
     hipLaunchKernelGGL(k_decode_mx, dim3(G), dim3(kThreads), lds, s, dev_args);
     return hipGetLastError() == hipSuccess ? 0 : -19;
 }

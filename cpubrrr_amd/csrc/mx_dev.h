@@ -17,7 +17,12 @@ CPB_DEV float part_dot(const u32x4* wv, const u32x4* xs, const float* sb, int32_
 #pragma unroll
     for (int u = 0; u < kBlkPerPart; u++) {
         const u32x4* xb = xs + u * 4;
+#ifdef CPB_PROBE_NO_DECODE
+        // probe builds only: same loads and epilogue, no decode arithmetic
+        int S = (int)(wv[u + 1][0] ^ xb[0][0]) & 7;
+#else
         int S = mx_block_sum(wv[u + 1], xb[0], xb[1], xb[2], xb[3], k);
+#endif
         uint32_t e = (ew[u >> 2] >> (8 * (u & 3))) & 0xffu;
         acc = fmaf((float)S, e8m0_scale(e, sb[u]), acc);
         if (TRACE && blk0 + u < nb) sums_out[u] = S;
