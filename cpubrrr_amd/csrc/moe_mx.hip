@@ -55,6 +55,11 @@ __global__ __launch_bounds__(1024) void k_gateup_mx(GateUpArgs a) {
     }
     u32x4 wv[kUnits];
     load_part(a.w + ((((size_t)e * tiles + t) * P + q) * kUnits) * 64 + lane, 64, wv);
+    // the epilogue's bias, requested now (behind the weights) instead of
+    // after the reduction
+    const float* bias = (lane >> 5) ? a.up_b : a.gate_b;
+    float bias_pf = 0.0f;
+    if (q == 0 && bias) bias_pf = bias[(size_t)e * a.dff + t * 32 + (lane & 31)];
 #pragma unroll
     for (int k = 0; k < 4; k++) xs[lane + 64 * k] = ok[k] ? xv[k] : 0u;
     wave_sync_lds();
@@ -70,8 +75,7 @@ __global__ __launch_bounds__(1024) void k_gateup_mx(GateUpArgs a) {
     if (q != 0) return;
     float v = 0.0f;
     for (int p = 0; p < P; p++) v += red[p * 64 + lane];
-    if (isup) { if (a.up_b) v += a.up_b[(size_t)e * a.dff + row]; }
-    else      { if (a.gate_b) v += a.gate_b[(size_t)e * a.dff + row]; }
+    if (bias) v += bias_pf;
     if (TRACE) a.gu[(size_t)(ei * 2 + isup) * a.dff + row] = v;
     // SwiGLU-OAI (engine_gpt2.rs:887-906) in lanes 0-31: gate row r, up row r from lane r+32
     float u = __shfl_down(v, 32);
@@ -127,6 +131,15 @@ __global__ __launch_bounds__(1024) void k_down_mx(DownArgs a) {
     }
     u32x4 wv[kUnits];
     load_part(a.w + (((((size_t)e * tiles + t) * P + q) * kUnits) * RT) + rr, RT, wv);
+    // the epilogue's operands (bias, residual, slot weights), requested now
+    // (behind the weights) instead of after the reduction
+    float dnb_pf = 0.0f, x_pf = 0.0f, w_pf[4];
+    if (q == 0) {
+        if (a.down_b) dnb_pf = a.down_b[(size_t)e * a.d + row];
+        if (lane < RT) x_pf = a.x[row];
+    }
+#pragma unroll
+    for (int k = 0; k < 4; k++) w_pf[k] = a.wts[k < K ? k : 0];
 #pragma unroll
     for (int k = 0; k < 16; k++) {
         int i = lane + 64 * k;
@@ -144,14 +157,16 @@ __global__ __launch_bounds__(1024) void k_down_mx(DownArgs a) {
     if (q != 0) return;
     float v = 0.0f;
     for (int p = 0; p < P; p++) v += red[p * 64 + lane];
-    if (a.down_b) v += a.down_b[(size_t)e * a.d + row];
+    if (a.down_b) v += dnb_pf;
     if (TRACE) a.dn[(size_t)ei * a.d + row] = v;
     vv[lane] = v;
     wave_sync_lds();
     if (lane < RT) {
         // engine_gpt2.rs:911-921: s = x[r]; s += wts[ei] * (dot + b), ei ascending
-        float s = a.x[row];
-        for (int k = 0; k < K; k++) s += a.wts[k] * vv[k * RT + lane];
+        float s = x_pf;
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+            if (k < K) s += w_pf[k] * vv[k * RT + lane];
         a.x[row] = s;
     }
 }
