@@ -67,6 +67,7 @@ struct cpb_moe {
     int nb = 0, nbf = 0, parts_gu = 0, parts_dn = 0;
     bool mx = true;
     // activations / routing (device)
+    float* params = nullptr;              // per-layer router / norm / bias parameters (one arena)
     float* x = nullptr;
     float* xn = nullptr;
     int8_t *xq = nullptr, *xqn = nullptr;
@@ -92,6 +93,9 @@ struct cpb_moe {
     cpb::LayerPtrs* d_layers = nullptr;
     unsigned* d_sync = nullptr;
     int32_t* d_error = nullptr;
+    unsigned* d_lsync = nullptr;          // fused gate/up + down phase counters (zero between launches)
+    bool fused = false;                   // gate/up and down in one launch (MXFP4 decode; CPB_FUSED=1 enables)
+    bool select_in_gateup = true;         // MXFP4 decode: top-k at the start of the gate/up kernel (CPB_SELECT_IN_ROUTE=1: in the route launch)
     std::map<std::tuple<int, int, float*, int>, cpb::DecodeArgs*> decode_args;
     bool persistent = false;  // the single-launch decode is opt-in (CPB_PERSISTENT=1)
     bool prepare_only = false;
@@ -141,8 +145,8 @@ int check_cfg(const cpb_moe_cfg* c) {
         if (c->top_k != 1 && c->top_k != 2 && c->top_k != 4)
             return fail(CPB_EINVAL, "MXFP4 path supports top_k in {1,2,4}, got %d", c->top_k);
         if (c->d % (64 / c->top_k)) return fail(CPB_EINVAL, "d must be a multiple of 64/top_k");
-        if ((c->d / 32 + 14) / 15 > 16 || (c->d_ff / 32 + 14) / 15 > 16)
-            return fail(CPB_EINVAL, "d, d_ff must be <= 7680");
+        if ((c->d / 32 + 14) / 15 > cpb::kMaxParts || (c->d_ff / 32 + 14) / 15 > cpb::kMaxParts)
+            return fail(CPB_EINVAL, "d, d_ff must be <= 3840");
     } else if (c->wtype_gate_up == CPB_GGUF_Q4_K) {
         if (c->wtype_down != CPB_GGUF_Q4_K && c->wtype_down != CPB_GGUF_Q6_K)
             return fail(CPB_EINVAL, "k-quant down must be Q4_K or Q6_K");
@@ -180,17 +184,39 @@ int ensure_staging(cpb_moe_t* h, size_t n) {
     return 0;
 }
 
-int upload(float** dst, const float* src, size_t n, hipStream_t s) {
+// Copy n floats into a preassigned slot of the parameter arena (null src:
+// the parameter is absent and its pointer stays null).
+int upload(float** dst, float* slot, const float* src, size_t n, hipStream_t s) {
     if (!src) { *dst = nullptr; return 0; }
-    if (int r = dmalloc(dst, n)) return r;
-    HIP_OK(hipMemcpyAsync(*dst, src, n * sizeof(float), hipMemcpyHostToDevice, s));
+    *dst = slot;
+    HIP_OK(hipMemcpyAsync(slot, src, n * sizeof(float), hipMemcpyHostToDevice, s));
     return 0;
+}
+
+// Per-layer small parameters (router rows and bias, norm weights, expert
+// biases) of every layer live in one allocation: the route and expert kernels
+// then touch a few large pages instead of one small allocation per tensor
+// per layer, which keeps their address translations warm.
+size_t align64(size_t n) { return (n + 63) / 64 * 64; }
+struct ParamSlots {
+    size_t router_w, norm_w, router_b, gate_b, up_b, down_b, per_layer;
+};
+ParamSlots param_slots(const cpb_moe_cfg& c) {
+    const size_t ne = c.n_expert, d = c.d, ff = c.d_ff;
+    ParamSlots p{};
+    size_t o = 0;
+    p.router_w = o; o += align64(ne * d);
+    p.norm_w = o; o += align64(d);
+    p.router_b = o; o += align64(ne);
+    p.gate_b = o; o += align64(ne * ff);
+    p.up_b = o; o += align64(ne * ff);
+    p.down_b = o; o += align64(ne * d);
+    p.per_layer = o;
+    return p;
 }
 
 void free_layer(LayerDev& L) {
     hipFree(L.gu); hipFree(L.up); hipFree(L.dn);
-    hipFree(L.gate_b); hipFree(L.up_b); hipFree(L.down_b);
-    hipFree(L.router_w); hipFree(L.router_b); hipFree(L.norm_w);
     L = LayerDev{};
 }
 
@@ -238,7 +264,8 @@ int check_device_error(cpb_moe_t* h) {
     if (!err) return 0;
     HIP_OK(hipMemset(h->d_sync, 0, sizeof(unsigned) * (3 * (size_t)h->cfg.n_layer + 1)));
     HIP_OK(hipMemset(h->d_error, 0, sizeof(int32_t)));
-    return fail(CPB_ENODEV, "persistent decode: a phase wait timed out (workgroups not co-resident?)");
+    HIP_OK(hipMemset(h->d_lsync, 0, sizeof(unsigned) * 2));
+    return fail(CPB_ENODEV, "a bounded in-kernel wait timed out (persistent or fused decode)");
 }
 
 void clear_graphs(cpb_moe_t* h) {
@@ -263,28 +290,44 @@ int layer_token(cpb_moe_t* h, int layer, float* dx, int apply_norm, bool trace) 
     sa.lstar = h->lstar; sa.lbound = h->lbound; sa.router_w = L.router_w; sa.router_b = L.router_b; sa.xn = h->xn;
     sa.d = c.d; sa.n_expert = c.n_expert; sa.top_k = c.top_k;
     sa.ids = h->ids; sa.wts = h->wts; sa.logits = h->logits; sa.fallback = h->fallback;
+    // MXFP4 decode: the gate/up kernel selects at its start (no
+    // cross-workgroup hand-off inside the routing launch)
+    const bool sel_in_gu = h->mx && h->select_in_gateup && !(h->fused && !trace);
     {
         Timer tm(h, 0);
-        if (cpb::launch_route(&ra, &sa, h->counter, h->stream)) return fail(CPB_ENODEV, "route launch failed");
+        if (cpb::launch_route(&ra, &sa, sel_in_gu ? nullptr : h->counter, h->stream))
+            return fail(CPB_ENODEV, "route launch failed");
     }
     if (h->mx) {
         cpb::GateUpArgs g{};
         g.w = L.gu; g.gate_b = L.gate_b; g.up_b = L.up_b;
         g.xq = h->xq; g.xqn = h->xqn; g.xsb = h->xsb;
         g.ids = h->ids;
+        g.stamps = h->d_stamps;
+        if (sel_in_gu) {
+            g.sel.lstar = h->lstar; g.sel.lbound = h->lbound; g.sel.router_w = L.router_w; g.sel.router_b = L.router_b;
+            g.sel.xn = h->xn; g.sel.ne = c.n_expert; g.sel.k = c.top_k; g.sel.d = c.d;
+            g.sel.ids = h->ids; g.sel.wts = h->wts; g.sel.logits = h->logits; g.sel.fallback = h->fallback;
+        }
         g.dff = c.d_ff; g.nb = h->nb; g.nparts = h->parts_gu; g.top_k = c.top_k;
         g.alpha = c.alpha; g.limit = c.limit;
         g.hq = h->hq; g.hqn = h->hqn; g.hsb = h->hsb;
         g.gu = h->t_gu; g.gu_sums = h->t_gu_sums; g.h = h->t_h;
-        {
-            Timer tm(h, 1);
-            if (cpb::launch_gateup_mx(g, trace, h->stream)) return fail(CPB_ENODEV, "gate/up launch failed");
-        }
         cpb::DownArgs dn{};
         dn.w = L.dn; dn.down_b = L.down_b; dn.hq = h->hq; dn.hqn = h->hqn; dn.hsb = h->hsb;
         dn.ids = h->ids; dn.wts = h->wts;
         dn.d = c.d; dn.dff = c.d_ff; dn.nbf = h->nbf; dn.nparts = h->parts_dn; dn.top_k = c.top_k;
         dn.x = dx; dn.dn = h->t_dn; dn.dn_sums = h->t_dn_sums;
+        if (!trace && h->fused && h->parts_gu == h->parts_dn) {
+            Timer tm(h, 1);
+            if (cpb::launch_layer_mx(g, dn, h->d_lsync, h->d_error, h->d_stamps, h->stream))
+                return fail(CPB_ENODEV, "gate/up + down launch failed");
+            return 0;
+        }
+        {
+            Timer tm(h, 1);
+            if (cpb::launch_gateup_mx(g, trace, h->stream)) return fail(CPB_ENODEV, "gate/up launch failed");
+        }
         {
             Timer tm(h, 2);
             if (cpb::launch_down_mx(dn, trace, h->stream)) return fail(CPB_ENODEV, "down launch failed");
@@ -353,7 +396,8 @@ int cpb_moe_create(const cpb_moe_cfg* cfg, int device, cpb_moe_t** out) {
         (r = dmalloc(&h->lstar, ne)) || (r = dmalloc(&h->lbound, ne)) || (r = dmalloc(&h->counter, 1)) ||
         (r = dmalloc(&h->logits, ne)) || (r = dmalloc(&h->ids, k)) || (r = dmalloc(&h->wts, k)) ||
         (r = dmalloc(&h->fallback, 1)) || (r = dmalloc(&h->hq, k * ff)) || (r = dmalloc(&h->hqn, k * ff)) ||
-        (r = dmalloc(&h->hsb, k * ff / 32)) || (r = dmalloc(&h->hsum, k * ff / 32)) || (r = dmalloc(&h->hbuf, k * ff)))
+        (r = dmalloc(&h->hsb, k * ff / 32)) || (r = dmalloc(&h->hsum, k * ff / 32)) || (r = dmalloc(&h->hbuf, k * ff)) ||
+        (r = dmalloc(&h->params, param_slots(*cfg).per_layer * cfg->n_layer)))
         return bail(r);
     if (h->mx) {
         if ((r = dmalloc(&h->d_special, 1))) return bail(r);
@@ -372,8 +416,12 @@ int cpb_moe_create(const cpb_moe_cfg* cfg, int device, cpb_moe_t** out) {
             return bail(r);
     }
     if ((r = dmalloc(&h->d_layers, (size_t)cfg->n_layer)) || (r = dmalloc(&h->d_sync, 3 * (size_t)cfg->n_layer + 1)) ||
-        (r = dmalloc(&h->d_error, 1)))
+        (r = dmalloc(&h->d_error, 1)) || (r = dmalloc(&h->d_lsync, 2)))
         return bail(r);
+    if (hipMemsetAsync(h->d_lsync, 0, sizeof(unsigned) * 2, h->stream) != hipSuccess)
+        return bail(fail(CPB_ENODEV, "init memset failed"));
+    if (const char* v = getenv("CPB_FUSED")) h->fused = v[0] != '0';
+    if (const char* v = getenv("CPB_SELECT_IN_ROUTE")) h->select_in_gateup = v[0] == '0';
     if (hipMemsetAsync(h->d_sync, 0, sizeof(unsigned) * (3 * (size_t)cfg->n_layer + 1), h->stream) != hipSuccess ||
         hipMemsetAsync(h->d_error, 0, sizeof(int32_t), h->stream) != hipSuccess ||
         hipMemsetAsync(h->d_layers, 0, sizeof(cpb::LayerPtrs) * cfg->n_layer, h->stream) != hipSuccess)
@@ -438,13 +486,17 @@ int cpb_moe_load_layer(cpb_moe_t* h, int layer, const void* gate, const void* up
         if (cpb::launch_repack_kq_down(h->staging, L.dn, ne, d, ff, c.top_k, c.wtype_down, h->stream))
             return fail(CPB_ENODEV, "repack launch failed");
     }
+    const ParamSlots ps = param_slots(c);
+    float* base = h->params + (size_t)layer * ps.per_layer;
     if (c.has_bias) {
-        if ((r = upload(&L.gate_b, gate_b, ne * ff, h->stream)) || (r = upload(&L.up_b, up_b, ne * ff, h->stream)) ||
-            (r = upload(&L.down_b, down_b, ne * d, h->stream)) || (r = upload(&L.router_b, router_b, ne, h->stream)))
+        if ((r = upload(&L.gate_b, base + ps.gate_b, gate_b, ne * ff, h->stream)) ||
+            (r = upload(&L.up_b, base + ps.up_b, up_b, ne * ff, h->stream)) ||
+            (r = upload(&L.down_b, base + ps.down_b, down_b, ne * d, h->stream)) ||
+            (r = upload(&L.router_b, base + ps.router_b, router_b, ne, h->stream)))
             return r;
     }
-    if ((r = upload(&L.router_w, router_w, ne * d, h->stream))) return r;
-    if ((r = upload(&L.norm_w, norm_w, d, h->stream))) return r;
+    if ((r = upload(&L.router_w, base + ps.router_w, router_w, ne * d, h->stream))) return r;
+    if ((r = upload(&L.norm_w, base + ps.norm_w, norm_w, d, h->stream))) return r;
     if (h->mx) {
         cpb::LayerPtrs lp{L.gu, L.dn, L.gate_b, L.up_b, L.down_b, L.router_w, L.router_b, L.norm_w};
         HIP_OK(hipMemcpyAsync(h->d_layers + layer, &lp, sizeof lp, hipMemcpyHostToDevice, h->stream));
@@ -699,13 +751,13 @@ void cpb_moe_destroy(cpb_moe_t* h) {
         hipFree(h->d_stamps);
     }
 #endif
-    hipFree(h->d_layers); hipFree(h->d_sync); hipFree(h->d_error);
+    hipFree(h->d_layers); hipFree(h->d_sync); hipFree(h->d_error); hipFree(h->d_lsync);
     void* gbufs[] = {h->g_xn, h->g_xsb, h->g_logits, h->g_wts, h->g_hsb, h->g_dnout, h->g_xq, h->g_hq, h->g_ximg,
                      h->g_himg, h->g_lstar, h->g_lbound, h->g_ids, h->g_fallback, h->g_sorted, h->g_ntiles, h->g_tiles,
                      h->d_special};
     for (void* p : gbufs) hipFree(p);
     for (auto& L : h->layers) free_layer(L);
-    void* bufs[] = {h->x, h->xn, h->xq, h->xqn, h->xsb, h->xsum, h->lstar, h->lbound, h->counter, h->logits,
+    void* bufs[] = {h->params, h->x, h->xn, h->xq, h->xqn, h->xsb, h->xsum, h->lstar, h->lbound, h->counter, h->logits,
                     h->ids, h->wts, h->fallback, h->hq, h->hqn, h->hsb, h->hsum, h->hbuf, h->t_gu, h->t_h,
                     h->t_dn, h->t_gu_sums, h->t_dn_sums, h->staging};
     for (void* p : bufs) if (p) hipFree(p);

@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include "moe_common.h"
+#include "select.h"
 
 namespace cpb {
 
@@ -13,12 +14,14 @@ struct GateUpArgs {
     const int8_t* xq;        // [d]
     const int8_t* xqn;       // [d]
     const float* xsb;        // [d/32]
-    const int32_t* ids;      // [top_k] selected experts (k_select)
+    const int32_t* ids;      // [top_k] selected experts, when sel.lstar is null
+    SelectIn sel;            // otherwise every workgroup selects at its start (workgroup 0 publishes ids / wts)
     int dff, nb, nparts, top_k;
     float alpha, limit;
     int8_t* hq;              // [top_k][dff]
     int8_t* hqn;             // [top_k][dff]
     float* hsb;              // [top_k][dff/32]
+    unsigned long long* stamps;  // probe builds (CPB_DECODE_STAMPS) only
     // trace (TRACE instantiation only)
     float* gu;               // [top_k][2][dff]
     int32_t* gu_sums;        // [top_k][2][dff][nb]
@@ -46,5 +49,9 @@ int launch_repack_gateup(const uint8_t* gate, const uint8_t* up, u32x4* out, int
 int launch_repack_down(const uint8_t* down, u32x4* out, int ne, int d, int nbf, int top_k, hipStream_t s);
 int launch_gateup_mx(const GateUpArgs& a, bool trace, hipStream_t s);
 int launch_down_mx(const DownArgs& a, bool trace, hipStream_t s);
+// gate/up and down of one layer in a single launch; sync: two zeroed counters
+// (left zeroed), err: set to 1 if a bounded wait expired
+int launch_layer_mx(const GateUpArgs& g, const DownArgs& a, unsigned* sync, int32_t* err, unsigned long long* stamps,
+                    hipStream_t s);
 
 }  // namespace cpb

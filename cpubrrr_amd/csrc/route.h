@@ -38,7 +38,8 @@ struct SelectArgs {
 };
 
 // Routing and selection in one launch; `arrive` is a zero-initialised
-// counter that the launch leaves at zero.
+// counter that the launch leaves at zero.  With arrive null the launch only
+// publishes lstar / lbound (a later kernel selects).
 int launch_route(const RouteArgs* a, const SelectArgs* sa, unsigned* arrive, hipStream_t s);
 int launch_select(const SelectArgs* a, hipStream_t s);
 

@@ -43,6 +43,7 @@ __global__ __launch_bounds__(256) void k_route(RouteArgs a, SelectArgs s, unsign
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ unsigned last;
     route_expert(a, blockIdx.x, gridDim.x, smem);
+    if (!arrive) return;            // the consumer kernel selects (kernel boundary orders the results)
     drain_memory();                 // this workgroup's results are visible device-wide
     __syncthreads();
     if (threadIdx.x == 0)

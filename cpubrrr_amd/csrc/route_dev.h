@@ -190,86 +190,281 @@ CPB_DEV void router_logit(const float4* wv, int C, int j0, const float* xn, int 
     }
 }
 
-// LDS bytes route_expert needs
-CPB_DEV_HOST inline size_t route_lds_bytes(int d) { return sizeof(float) * (2 * d + 32) + sizeof(double) * 32 + sizeof(float) * 64; }
+// ---- wavefront DPP helpers on doubles (no LDS round trips) ----
+// v from the DPP source lane; lanes whose source is out of the row, or whose
+// row is masked off, read 0.0
+template <int CTRL, int ROWMASK>
+CPB_DEV double dpp_f64(double v) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, CTRL, ROWMASK, 0xF, true);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), CTRL, ROWMASK, 0xF, true);
+    return __builtin_bit_cast(double, ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+}
+// inclusive prefix sum over the 64 lanes (row_shr 1,2,4,8, then row_bcast 15, 31)
+CPB_DEV double wave_scan_f64(double v) {
+    v += dpp_f64<0x111, 0xF>(v);
+    v += dpp_f64<0x112, 0xF>(v);
+    v += dpp_f64<0x114, 0xF>(v);
+    v += dpp_f64<0x118, 0xF>(v);
+    v += dpp_f64<0x142, 0xA>(v);
+    v += dpp_f64<0x143, 0xC>(v);
+    return v;
+}
+// sum over the 64 lanes, valid in lane 63 (quad swaps, half-row and row
+// mirrors, then row_bcast 15, 31)
+CPB_DEV double wave_total63_f64(double v) {
+    v += dpp_f64<0xB1, 0xF>(v);
+    v += dpp_f64<0x4E, 0xF>(v);
+    v += dpp_f64<0x141, 0xF>(v);
+    v += dpp_f64<0x140, 0xF>(v);
+    v += dpp_f64<0x142, 0xA>(v);
+    v += dpp_f64<0x143, 0xC>(v);
+    return v;
+}
+// max over each aligned group of 16 lanes (a DPP row), in every lane of it
+CPB_DEV float row_max_f32(float v) {
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false)));
+    return v;
+}
+// value of the neighbouring lane (lane ^ 1)
+CPB_DEV float pair_f32(float v) { return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false)); }
+CPB_DEV int pair_i32(int v) { return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false); }
+
+// 16-byte store with the cache policy of st_dev (sc1: visible across XCDs)
+CPB_DEV void st_dev16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, u32x4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, byte_off, 0, 16);
+}
+
+constexpr int kRouteC = 16;         // consecutive elements per thread in route_expert
+
+// LDS bytes route_expert needs (any block size; d <= 4096)
+CPB_DEV_HOST inline int route_xt_stride(int d) { return (d / 16 + 63) / 64 * 64 + 4; }
+CPB_DEV_HOST inline size_t route_lds_bytes(int d) {
+    const size_t xt = sizeof(float) * 16 * (size_t)route_xt_stride(d);
+    const size_t xr = sizeof(float) * (size_t)d;
+    return (xt > xr ? xt : xr) + sizeof(double) * 64 + 64;
+}
 
 // Workgroup-level body: expert e's logit + bound, and this workgroup's share
-// (index e of NEg) of the activation quantisation.  Any multiple of 64
-// threads with blockDim.x * kChunk >= d.
+// (blocks b with b % NEg == e) of the activation quantisation.  Any multiple
+// of 64 threads with blockDim.x * 16 >= d.
+//
+// Thread t owns x[16t .. 16t+16): its x, norm weights and router weights
+// arrive in registers from one round of loads.  The gpt-oss sum of squares
+// (16 fma chains, chain q over x[16m + q], engine_gpt2.rs:710-726) runs in 16
+// lanes of wave 0 over a transposed LDS copy (chain q's elements contiguous);
+// the Qwen one (nt serial slices, engine_qwen2.rs:457-467) over a plain copy.
+// The router logit is the exact fp64 sum of the reference's fp32 products
+// with the prefix-sum error bound of router_logit, from one DPP scan.
 CPB_DEV void route_expert(const RouteArgs& a, int e, int NEg, unsigned char* smem) {
-    float* xs = (float*)smem;                 // [d]
-    float* xn = xs + a.d;                     // [d]
-    double* dsc = (double*)(xn + a.d + 32);   // [16]
-    double* dred = dsc + 16;                  // [16]
-    float* scratch = (float*)(dred + 16);     // [64]
-    const int tid = threadIdx.x, nth = blockDim.x;
+    const int tid = threadIdx.x, nth = blockDim.x, lane = tid & 63, wv = tid >> 6, nw = nth >> 6;
     const int d = a.d;
+    const int S = route_xt_stride(d);
+    float* xl = (float*)smem;                                  // transposed (gpt-oss) or plain (Qwen) x
+    double* dred = (double*)(smem + route_lds_bytes(d) - sizeof(double) * 64 - 64);   // [64]
+    float* sinv = (float*)(dred + 64);
     RSTAMP(0);
 
-    // router row chunk of this thread, loaded before anything waits on x
-    const int C = ((d + 4 * nth - 1) / (4 * nth)) * 4;   // multiple of 4, C*nth >= d
-    const int j0 = tid * C;
-    const float* W = a.router_w + (size_t)e * d;
-    float4 wv[kChunk / 4];
+    const int j0 = tid * kRouteC;
+    const bool act = j0 < d;
+    const uint32_t off = (uint32_t)(act ? j0 : 0) * 4;
+    const __amdgpu_buffer_rsrc_t rx = buf_rsrc(a.x, (uint32_t)d * 4);
+    const __amdgpu_buffer_rsrc_t rW = buf_rsrc(a.router_w + (size_t)e * d, (uint32_t)d * 4);
+    const bool use_g = a.norm_w && a.apply_norm;
+    const __amdgpu_buffer_rsrc_t rg = buf_rsrc(a.norm_w, use_g ? (uint32_t)d * 4 : 0u);
+    u32x4 xv[4], wq[4], gq[4];
 #pragma unroll
-    for (int i = 0; i < kChunk / 4; i++) {
-        const int j = min(j0 + 4 * i, d - 4);
-        wv[i] = *(const float4*)(W + j);
-    }
+    for (int k = 0; k < 4; k++) xv[k] = ld_dev16(rx, off + 16 * k);     // may come from this launch
+#pragma unroll
+    for (int k = 0; k < 4; k++) wq[k] = __builtin_amdgcn_raw_buffer_load_b128(rW, off + 16 * k, 0, 0);
+#pragma unroll
+    for (int k = 0; k < 4; k++) gq[k] = __builtin_amdgcn_raw_buffer_load_b128(rg, off + 16 * k, 0, 0);
     const double b = a.router_b ? (double)a.router_b[e] : 0.0;
-
+    float xf[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) xf[i] = act ? __uint_as_float(xv[i >> 2][i & 3]) : 0.0f;
     RSTAMP(1);
-    norm_into(a.x, a.norm_w, d, a.eps, a.norm, a.norm_nt, a.apply_norm, xs, xn, scratch);
-    RSTAMP(2);
 
-    // quantisation, distributed over the workgroups (each also publishes the
-    // xn values of its blocks)
-    if (a.qk == 0) {
-        // Q8 per 32-block (engine_gpt2.rs:691-699): 32 lanes per block
-        const int l = tid & 31, g = nth >> 5;
-        for (int bk = e * g + (tid >> 5); bk < d / 32; bk += NEg * g) {
-            const float v = xn[bk * 32 + l];
-            float m = fabsf(v);
+    // ---- rmsnorm scale ----
+    float inv = 1.0f;
+    if (a.apply_norm) {
+        if (a.norm == 0) {
+            // chain q's element m = x[16m + q] lives in thread m, register q
+            if (act) {
 #pragma unroll
-            for (int s2 = 16; s2 >= 1; s2 >>= 1) m = fmaxf(m, __shfl_xor(m, s2));
-            const float sc = fmaxf(1e-12f, m) / 127.0f;
-            const int qv = q8_round(v, sc);
-            st_dev(a.xn + bk * 32 + l, v);
-            st_dev(a.xq + bk * 32 + l, (int8_t)qv);
-            st_dev(a.xqn + bk * 32 + l, (int8_t)(-qv));
-            if (l == 0) st_dev(a.xsb + bk, sc);
-        }
-    } else {
-        // Q8_K per 256 (engine_qwen2.rs:288-300): one wave per superblock
-        const int l = tid & 63, g = nth >> 6;
-        for (int sb = e * g + (tid >> 6); sb < d / 256; sb += NEg * g) {
-            float v[4], m = 0.0f;
+                for (int i = 0; i < 16; i++) xl[i * S + tid] = xf[i];
+            }
+            __syncthreads();
+            if (wv == 0) {
+                const int nm = d / 16;
+                float acc = 0.0f;
+                if (lane < 16) {
+                    const float* row = xl + lane * S;
+                    int m = 0;
+                    for (; m + 16 <= nm; m += 16) {
+                        float4 t[4];
 #pragma unroll
-            for (int k = 0; k < 4; k++) { v[k] = xn[sb * 256 + 64 * k + l]; m = fmaxf(m, fabsf(v[k])); }
-            const float sc = fmaxf(1e-12f, wave_max(m)) / 127.0f;
-            if (l == 0) st_dev(a.xsb + sb, sc);
+                        for (int u = 0; u < 4; u++) t[u] = *(const float4*)(row + m + 4 * u);
 #pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const int qv = q8_round(v[k], sc);
-                st_dev(a.xn + sb * 256 + 64 * k + l, v[k]);
-                st_dev(a.xq + sb * 256 + 64 * k + l, (int8_t)qv);
-                st_dev(a.xqn + sb * 256 + 64 * k + l, (int8_t)(-qv));
-                int s3 = qv;   // per-32 sums: group 2k + (l >= 32)
+                        for (int u = 0; u < 4; u++) {
+                            acc = fmaf(t[u].x, t[u].x, acc);
+                            acc = fmaf(t[u].y, t[u].y, acc);
+                            acc = fmaf(t[u].z, t[u].z, acc);
+                            acc = fmaf(t[u].w, t[u].w, acc);
+                        }
+                    }
+                    for (; m < nm; m++) { const float t = row[m]; acc = fmaf(t, t, acc); }
+                }
+                // chain q = 4v + l -> acc[v][l]; L[l] = (a0 + a1) + (a2 + a3); s = (L0 + L1) + (L2 + L3)
+                float c[16];
 #pragma unroll
-                for (int m2 = 16; m2 >= 1; m2 >>= 1) s3 += __shfl_xor(s3, m2);
-                if ((l & 31) == 0) st_dev(a.xsum + sb * 8 + 2 * k + (l >> 5), s3);
+                for (int q = 0; q < 16; q++) c[q] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, acc), q));
+                float L[4];
+#pragma unroll
+                for (int l = 0; l < 4; l++) L[l] = (c[l] + c[4 + l]) + (c[8 + l] + c[12 + l]);
+                const float s = (L[0] + L[1]) + (L[2] + L[3]);
+                if (lane == 0) *sinv = 1.0f / sqrtf(s / (float)d + a.eps);
+            }
+        } else {
+            if (act) {
+#pragma unroll
+                for (int k = 0; k < 4; k++) ((u32x4*)xl)[tid * 4 + k] = xv[k];
+            }
+            __syncthreads();
+            const int nt = a.norm_nt, base = d / nt, rem = d % nt;
+            float ps = 0.0f;
+            if (tid < nt) {
+                const int s0 = tid * base + (tid < rem ? tid : rem), sz = base + (tid < rem ? 1 : 0);
+                int i = 0;
+                for (; i + 16 <= sz; i += 16) {
+                    float t[16];
+#pragma unroll
+                    for (int u = 0; u < 16; u++) t[u] = xl[s0 + i + u];
+#pragma unroll
+                    for (int u = 0; u < 16; u++) ps += t[u] * t[u];
+                }
+                for (; i < sz; i++) { const float v = xl[s0 + i]; ps += v * v; }
+            }
+            // serial sum of the nt partials (nt <= 64: all in wave 0)
+            if (wv == 0) {
+                float tot = 0.0f;
+                for (int k = 0; k < nt; k++) tot += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ps), k));
+                if (lane == 0) *sinv = 1.0f / sqrtf(tot / (float)d + a.eps);
             }
         }
+        __syncthreads();
+        inv = *sinv;
+    }
+    RSTAMP(2);
+
+    // ---- xn = (x * inv) * w in registers ----
+    float xn[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const float g = __uint_as_float(gq[i >> 2][i & 3]);
+        xn[i] = !a.apply_norm ? xf[i] : use_g ? (xf[i] * inv) * g : xf[i] * inv;
     }
 
+    // ---- activation quantisation (this workgroup's share) ----
+    if (a.qk == 0) {
+        // Q8 per 32-block (engine_gpt2.rs:691-699): threads 2b, 2b+1 hold block b
+        float m = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) m = fmaxf(m, fabsf(xn[i]));
+        m = fmaxf(m, pair_f32(m));
+        const int blk = tid >> 1;
+        if (act && blk % NEg == e) {
+            const float sc = fmaxf(1e-12f, m) / 127.0f;
+            uint32_t qp[4] = {0, 0, 0, 0}, qn[4] = {0, 0, 0, 0};
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int qv = q8_round(xn[i], sc);
+                qp[i >> 2] |= (uint32_t)(uint8_t)qv << (8 * (i & 3));
+                qn[i >> 2] |= (uint32_t)(uint8_t)(-qv) << (8 * (i & 3));
+            }
+            const __amdgpu_buffer_rsrc_t rn = buf_rsrc(a.xn, (uint32_t)d * 4);
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+                st_dev16(rn, off + 16 * k, u32x4{__float_as_uint(xn[4 * k]), __float_as_uint(xn[4 * k + 1]),
+                                                 __float_as_uint(xn[4 * k + 2]), __float_as_uint(xn[4 * k + 3])});
+            st_dev16(buf_rsrc(a.xq, (uint32_t)d), (uint32_t)j0, u32x4{qp[0], qp[1], qp[2], qp[3]});
+            st_dev16(buf_rsrc(a.xqn, (uint32_t)d), (uint32_t)j0, u32x4{qn[0], qn[1], qn[2], qn[3]});
+            if ((tid & 1) == 0) st_dev(a.xsb + blk, sc);
+        }
+    } else {
+        // Q8_K per 256 (engine_qwen2.rs:288-300): the 16 threads of a DPP row
+        // hold one superblock; per-32 sums from thread pairs
+        float m = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) m = fmaxf(m, fabsf(xn[i]));
+        m = row_max_f32(m);
+        const int sb = tid >> 4;
+        const float sc = fmaxf(1e-12f, m) / 127.0f;
+        uint32_t qp[4] = {0, 0, 0, 0}, qn[4] = {0, 0, 0, 0};
+        int s32 = 0;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int qv = q8_round(xn[i], sc);
+            s32 += qv;
+            qp[i >> 2] |= (uint32_t)(uint8_t)qv << (8 * (i & 3));
+            qn[i >> 2] |= (uint32_t)(uint8_t)(-qv) << (8 * (i & 3));
+        }
+        s32 += pair_i32(s32);
+        if (act && sb % NEg == e) {
+            const __amdgpu_buffer_rsrc_t rn = buf_rsrc(a.xn, (uint32_t)d * 4);
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+                st_dev16(rn, off + 16 * k, u32x4{__float_as_uint(xn[4 * k]), __float_as_uint(xn[4 * k + 1]),
+                                                 __float_as_uint(xn[4 * k + 2]), __float_as_uint(xn[4 * k + 3])});
+            st_dev16(buf_rsrc(a.xq, (uint32_t)d), (uint32_t)j0, u32x4{qp[0], qp[1], qp[2], qp[3]});
+            st_dev16(buf_rsrc(a.xqn, (uint32_t)d), (uint32_t)j0, u32x4{qn[0], qn[1], qn[2], qn[3]});
+            if ((tid & 15) == 0) st_dev(a.xsb + sb, sc);
+            if ((tid & 1) == 0) st_dev(a.xsum + (tid >> 1), s32);
+        }
+    }
     RSTAMP(3);
-    // ---- router logit of expert e ----
-    double total = 0.0, bound = 0.0;
-    router_logit(wv, C, j0, xn, d, b, dsc, dred, &total, &bound);
+
+    // ---- router logit of expert e: exact fp64 sum of the reference's fp32
+    // products and the bound u/(1-u) * (sum_k |S_k| + n*gamma_n*A) ----
+    float p[16];
+    double loc = 0.0, absp = 0.0;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        p[i] = act ? __fmul_rn(__uint_as_float(wq[i >> 2][i & 3]), xn[i]) : 0.0f;
+        loc += (double)p[i];
+        absp += fabs((double)p[i]);
+    }
+    const double incl = wave_scan_f64(loc);
+    if (lane == 63) dred[wv] = incl;
+    __syncthreads();
+    double woff = 0.0, wtot = 0.0;
+    for (int w2 = 0; w2 < nw; w2++) {
+        const double t = dred[w2];
+        if (w2 < wv) woff += t;
+        wtot += t;
+    }
+    double run = b + woff + (incl - loc);
+    double sabs = 0.0;
+#pragma unroll
+    for (int i = 0; i < 16; i++) { run += (double)p[i]; sabs += act ? fabs(run) : 0.0; }
+    const double ws = wave_total63_f64(sabs);
+    const double wa = wave_total63_f64(absp);
+    if (lane == 63) { dred[16 + wv] = ws; dred[32 + wv] = wa; }
+    __syncthreads();
     RSTAMP(4);
     if (tid == 0) {
-        st_dev(a.lstar + e, total);
-        st_dev(a.lbound + e, bound);
+        double SS = 0.0, AP = 0.0;
+        for (int w2 = 0; w2 < nw; w2++) { SS += dred[16 + w2]; AP += dred[32 + w2]; }
+        const double u = 5.9604644775390625e-08;  // 2^-24
+        const double n = (double)d;
+        const double A = fabs(b) + AP;
+        const double gam = n * u / (1.0 - n * u);
+        const double bound = u / (1.0 - u) * (SS + n * gam * A);
+        st_dev(a.lstar + e, b + wtot);
+        st_dev(a.lbound + e, bound * 1.0001 + 1e-10 * A + 1e-30);
     }
     RSTAMP(5);
 }

@@ -23,6 +23,73 @@ struct Selection {
     int fallback;       // 1 when the exact serial logits were needed
 };
 
+// The exact path of the selection: recompute, in the reference's serial order
+// (acc = b; acc += W[j]*xn[j]), the logit of every expert whose interval
+// reaches the lowest lower bound of the provisional top-k, then rank those
+// exactly (descending, lowest index first).  sL / sH: LDS values and upper
+// bounds of all NE experts; sSel: LDS [K] provisional choice, overwritten;
+// xst: LDS scratch of d floats.  One wavefront.
+CPB_DEV void exact_reselect(double* sL, const double* sH, int* sSel, int NE, int K, const float* __restrict__ router_w,
+                            const float* __restrict__ router_b, const float* __restrict__ xn, int d, float* xst) {
+    const int lane = threadIdx.x & 63;
+    // candidates: intervals reaching the lowest lower bound of the selected
+    double tau = 1e300;
+    for (int i = 0; i < K; i++) { const int e = sSel[i]; tau = fmin(tau, sL[e] - (sH[e] - sL[e])); }
+    __builtin_amdgcn_wave_barrier();
+    // xn staged in LDS with coherent 16-byte loads (it may have been written
+    // by other workgroups of this launch), then each candidate lane runs the
+    // reference's serial chain with its router row fetched 64 weights ahead
+    {
+        const __amdgpu_buffer_rsrc_t r = buf_rsrc(xn, (uint32_t)d * 4);
+        for (int i = lane; i < d / 4; i += 64) ((u32x4*)xst)[i] = ld_dev16(r, (uint32_t)i * 16);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    for (int e = lane; e < NE; e += 64) {
+        double v = -1e300;
+        if (sH[e] >= tau) {
+            float acc = router_b ? router_b[e] : 0.0f;
+            const float* Wr = router_w + (size_t)e * d;
+            // kept small: this path is rare and must not raise the register
+            // budget of the kernels that embed it
+            constexpr int kU = 4;
+            float4 w4[kU], n4[kU];
+#pragma unroll
+            for (int u = 0; u < kU; u++) w4[u] = 4 * u < d ? *(const float4*)(Wr + 4 * u) : float4{0, 0, 0, 0};
+            for (int j0 = 0; j0 < d; j0 += 4 * kU) {
+                // next chunk requested before this one is consumed
+#pragma unroll
+                for (int u = 0; u < kU; u++)
+                    n4[u] = j0 + 4 * kU + 4 * u < d ? *(const float4*)(Wr + j0 + 4 * kU + 4 * u) : float4{0, 0, 0, 0};
+#pragma unroll
+                for (int u = 0; u < kU; u++) {
+                    if (j0 + 4 * u >= d) break;
+                    const float* w = (const float*)&w4[u];
+#pragma unroll
+                    for (int c = 0; c < 4; c++) acc = __fadd_rn(acc, __fmul_rn(w[c], xst[j0 + 4 * u + c]));
+                }
+#pragma unroll
+                for (int u = 0; u < kU; u++) w4[u] = n4[u];
+            }
+            v = (double)acc;
+        }
+        sL[e] = v;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    for (int e = lane; e < NE; e += 64) {
+        const double v = sL[e];
+        int r = 0;
+        for (int j = 0; j < NE; j++) { const double o = sL[j]; r += (o > v) || (o == v && j < e); }
+        if (r < K) sSel[r] = e;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // Executed by one wavefront (64 lanes).  lds: 4*NE doubles + d floats of
 // scratch (the floats only for the exact fallback).
 // Lane l holds experts l, l+64, ... (NE <= 256) in registers; the top-k come
@@ -111,62 +178,7 @@ CPB_DEV void select_experts_wave(const double* __restrict__ Ls, const double* __
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     const bool ok = !__any(bad);
     SSTAMP(2);
-    if (!ok) {
-        // candidates: intervals reaching the lowest lower bound of the selected
-        double tau = 1e300;
-        for (int i = 0; i < K; i++) { const int e = sSel[i]; tau = fmin(tau, sL[e] - (sH[e] - sL[e])); }
-        __builtin_amdgcn_wave_barrier();
-        // xn staged in LDS with coherent 16-byte loads (it may have been written
-        // by other workgroups of this launch), then each candidate lane runs the
-        // reference's serial chain with its router row fetched 64 weights ahead
-        float* xst = (float*)(lds + 4 * NE);
-        {
-            const __amdgpu_buffer_rsrc_t r = buf_rsrc(xn, (uint32_t)d * 4);
-            for (int i = lane; i < d / 4; i += 64) ((u32x4*)xst)[i] = ld_dev16(r, (uint32_t)i * 16);
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        for (int e = lane; e < NE; e += 64) {
-            double v = -1e300;
-            if (sH[e] >= tau) {
-                float acc = router_b ? router_b[e] : 0.0f;
-                const float* Wr = router_w + (size_t)e * d;
-                float4 w4[16], n4[16];
-#pragma unroll
-                for (int u = 0; u < 16; u++) w4[u] = 4 * u < d ? *(const float4*)(Wr + 4 * u) : float4{0, 0, 0, 0};
-                for (int j0 = 0; j0 < d; j0 += 64) {
-                    // next chunk requested before this one is consumed
-#pragma unroll
-                    for (int u = 0; u < 16; u++)
-                        n4[u] = j0 + 64 + 4 * u < d ? *(const float4*)(Wr + j0 + 64 + 4 * u) : float4{0, 0, 0, 0};
-#pragma unroll
-                    for (int u = 0; u < 16; u++) {
-                        if (j0 + 4 * u >= d) break;
-                        const float* w = (const float*)&w4[u];
-#pragma unroll
-                        for (int c = 0; c < 4; c++) acc = __fadd_rn(acc, __fmul_rn(w[c], xst[j0 + 4 * u + c]));
-                    }
-#pragma unroll
-                    for (int u = 0; u < 16; u++) w4[u] = n4[u];
-                }
-                v = (double)acc;
-            }
-            sL[e] = v;
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        for (int e = lane; e < NE; e += 64) {
-            const double v = sL[e];
-            int r = 0;
-            for (int j = 0; j < NE; j++) { const double o = sL[j]; r += (o > v) || (o == v && j < e); }
-            if (r < K) sSel[r] = e;
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    }
+    if (!ok) exact_reselect(sL, sH, sSel, NE, K, router_w, router_b, xn, d, (float*)(lds + 4 * NE));
     SSTAMP(3);
     // softmax over the k selected, reference order: ex_i = exp(l_i - l_0)
     // (lane i), then the serial sum ex_0 + ex_1 + ... (every lane)
@@ -188,6 +200,170 @@ CPB_DEV void select_experts_wave(const double* __restrict__ Ls, const double* __
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+
+// Selection inputs and outputs for a kernel that selects at its own start
+// (the routing kernel published lstar / lbound before this launch began, so
+// plain loads see them).
+struct SelectIn {
+    const double* lstar;     // [ne] null: ids / wts were selected elsewhere
+    const double* lbound;    // [ne]
+    const float* router_w;   // exact fallback only
+    const float* router_b;
+    const float* xn;
+    int ne, k, d;
+    int32_t* ids;            // [k]  written by workgroup 0
+    float* wts;              // [k]
+    float* logits;           // [ne]
+    int32_t* fallback;       // [1]
+};
+// LDS bytes select_topk_wave may use (its exact fallback)
+CPB_DEV_HOST_INLINE size_t select_lds_bytes(int ne, int d) { return sizeof(double) * 2 * ne + 64 + sizeof(float) * d; }
+
+// Wave-wide maximum of a 32-bit unsigned value via DPP (quad swaps, half-row
+// and row mirrors, row broadcasts 15 / 31), returned wave-uniform.
+CPB_DEV uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xA, 0xF, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xC, 0xF, false));
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+// Order-preserving map of a float onto unsigned integers (-0 < +0).
+CPB_DEV uint32_t float_key(float f) {
+    const uint32_t u = __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+CPB_DEV float key_float(uint32_t k) { return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k); }
+// fp32 bounds of a double: lo <= x <= hi
+// (finite x; one ulp outward when the nearest float lies on the wrong side)
+CPB_DEV float f32_up(double x) {
+    const float f = (float)x;
+    if (!((double)f < x)) return f;
+    const uint32_t u = __float_as_uint(f);
+    return (u & 0x7fffffffu) == 0 ? __uint_as_float(1u) : __uint_as_float(f > 0.0f ? u + 1 : u - 1);
+}
+CPB_DEV float f32_down(double x) {
+    const float f = (float)x;
+    if (!((double)f > x)) return f;
+    const uint32_t u = __float_as_uint(f);
+    return (u & 0x7fffffffu) == 0 ? __uint_as_float(0x80000001u) : __uint_as_float(f > 0.0f ? u - 1 : u + 1);
+}
+
+// Rare path of select_topk_wave (pointer and scalar
+// arguments only, so the caller needs no stack): exact_reselect over the LDS
+// image the caller wrote.
+CPB_DEV void select_exact_path(unsigned char* lds, int NE, int K, const float* router_w,
+                                                            const float* router_b, const float* xn, int d) {
+    double* sL = (double*)lds;
+    double* sH = sL + NE;
+    int* sSel = (int*)(sH + NE);
+    float* xst = (float*)(lds + sizeof(double) * 2 * NE + 64);
+    exact_reselect(sL, sH, sSel, NE, K, router_w, router_b, xn, d, xst);
+}
+
+// Top-k by one wavefront with every value in registers: lane l holds experts
+// l + 64j (j < 4).  The provisional ranking uses 32-bit keys (the logit
+// rounded to fp32, its top 24 bits, then 255 - index so that equal keys pick
+// the lowest index): K rounds of a DPP wave max.  Lane i < K collects rank i's
+// expert, fp32 logit and fp32 bounds rounded outwards.  Certification: rank i
+// must lie strictly above every later rank and every unselected expert; a
+// ranking that truncation made wrong cannot pass it, and then the exact path
+// (the reference's serial logits) decides.  Softmax over the k in the
+// reference's order.  Writes *out (LDS) from lanes < K.
+CPB_DEV void select_topk_wave(const SelectIn& s, unsigned char* lds, Selection* out) {
+    const int lane = threadIdx.x & 63;
+    const int NE = s.ne, K = s.k;
+    double lv[4], bv[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int e = lane + 64 * j;
+        lv[j] = e < NE ? s.lstar[e] : 0.0;
+        bv[j] = e < NE ? s.lbound[e] : 0.0;
+    }
+    uint32_t key[4];
+    float lf[4], lo[4], hi[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int e = lane + 64 * j;
+        lf[j] = (float)lv[j];
+        key[j] = e < NE ? ((float_key(lf[j]) & 0xFFFFFF00u) | (uint32_t)(255 - e)) : 0u;
+        lo[j] = f32_down(lv[j] - bv[j]);
+        hi[j] = e < NE ? f32_up(lv[j] + bv[j]) : -__builtin_inff();
+    }
+    int my_e = 0;
+    float my_l = 0.0f, my_lo = 0.0f, my_hi = -__builtin_inff();
+    for (int i = 0; i < K; i++) {
+        const uint32_t m = wave_max_u32(max(max(key[0], key[1]), max(key[2], key[3])));
+        const int bi = 255 - (int)(m & 0xFFu);
+        const int src = bi & 63, jj = bi >> 6;
+        // the chosen expert's values, read from its lane
+        const float vl = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+            __builtin_bit_cast(int, jj == 0 ? lf[0] : jj == 1 ? lf[1] : jj == 2 ? lf[2] : lf[3]), src));
+        const float vlo = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+            __builtin_bit_cast(int, jj == 0 ? lo[0] : jj == 1 ? lo[1] : jj == 2 ? lo[2] : lo[3]), src));
+        const float vhi = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+            __builtin_bit_cast(int, jj == 0 ? hi[0] : jj == 1 ? hi[1] : jj == 2 ? hi[2] : hi[3]), src));
+        if (lane == i) { my_e = bi; my_l = vl; my_lo = vlo; my_hi = vhi; }
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            if (lane + 64 * j == bi) { key[j] = 0u; hi[j] = -__builtin_inff(); }
+    }
+    // upper bound of every unselected expert (selected ones were set to -inf)
+    const float mu = key_float(wave_max_u32(float_key(fmaxf(fmaxf(hi[0], hi[1]), fmaxf(hi[2], hi[3])))));
+    float later = mu;
+    for (int j = 0; j < K; j++) {
+        const float hj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_hi), j));
+        if (j > lane) later = fmaxf(later, hj);
+    }
+    const bool bad = __any(lane < K && !(my_lo > later));
+    if (bad) {
+        double* sL = (double*)lds;
+        double* sH = sL + NE;
+        int* sSel = (int*)(sH + NE);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int e = lane + 64 * j;
+            if (e < NE) { sL[e] = lv[j]; sH[e] = lv[j] + bv[j]; }
+        }
+        if (lane < K) sSel[lane] = my_e;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        select_exact_path(lds, NE, K, s.router_w, s.router_b, s.xn, s.d);
+        if (lane < K) { my_e = sSel[lane]; my_l = (float)sL[my_e]; }
+    }
+    // softmax over the k selected, reference order: ex_i = exp(l_i - l_0)
+    // (lane i), then the serial sum ex_0 + ex_1 + ...
+    const float l0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_l), 0));
+    const float ex = expf(my_l - l0);
+    float wsum = 0.0f;
+    for (int i = 0; i < K; i++) wsum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ex), i));
+    const float wt = ex / wsum;
+    if (lane < K) {
+        out->ids[lane] = my_e;
+        out->logit[lane] = my_l;
+        out->wts[lane] = wt;
+    }
+    if (lane == 0) out->fallback = bad ? 1 : 0;
+    // trace outputs and the routed ids / weights for later launches
+    if (blockIdx.x == 0 && blockIdx.y == 0) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int e = lane + 64 * j;
+            if (e < NE && s.logits) s.logits[e] = lf[j];
+        }
+        __builtin_amdgcn_wave_barrier();
+        if (lane < K) {
+            s.ids[lane] = my_e;
+            s.wts[lane] = wt;
+            if (s.logits) s.logits[my_e] = my_l;     // as used (exact serial value after a fallback)
+        }
+        if (lane == 0 && s.fallback) s.fallback[0] = bad ? 1 : 0;
+    }
 }
 
 }  // namespace cpb

@@ -156,3 +156,25 @@ def test_device_stack_vs_oracle(gpu, phased, monkeypatch):
         xr, _ = O.gptoss_moe(layers[l], xr, True)
     rms = np.sqrt(((xr - x).astype(np.float64) ** 2).mean())
     assert np.max(np.abs(y - xr)) <= 1e-3 * rms
+
+
+def test_fused_layer_matches_two_launches(gpu, monkeypatch):
+    # gate/up + down in one launch (down tiles wait on a counter) and the two
+    # separate kernels give identical bits over a 4-layer stack, replayed
+    import torch
+    say("case fused vs two launches, 4 layers 20b shape")
+    d, ne, k, nl = 2880, 32, 4, 4
+    layers = [synth.gptoss_layer(d, d, ne, k, seed=6, layer=l, zipf=1.1) for l in range(nl)]
+    outs = []
+    for fused in ("1", "0"):
+        monkeypatch.setenv("CPB_PERSISTENT", "0")
+        monkeypatch.setenv("CPB_FUSED", fused)
+        with MoeBlock(MoeConfig.gptoss(d=d, n_expert=ne, top_k=k, d_ff=d, n_layer=nl)) as blk:
+            for l in range(nl):
+                blk.load_layer(l, layers[l])
+            x = torch.from_numpy(synth.token(d, 6, 0)).to("cuda:0")
+            for rep in range(3):
+                blk.forward_device(0, nl, x.data_ptr(), 1, True)
+            blk.sync()
+            outs.append(x.cpu().numpy())
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
