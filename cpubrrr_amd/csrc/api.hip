@@ -20,7 +20,6 @@
 
 #include "cpb_moe.h"
 #include "moe_kq.h"
-#include "decode_mx.h"
 #include "moe_mx.h"
 #include "moe_grouped.h"
 #include "route.h"
@@ -89,17 +88,8 @@ struct cpb_moe {
     // staging for raw GGUF bytes at load time
     uint8_t* staging = nullptr;
     size_t staging_size = 0;
-    // persistent decode (MXFP4, one token): per-layer pointers, phase counters
-    cpb::LayerPtrs* d_layers = nullptr;
-    unsigned* d_sync = nullptr;
-    int32_t* d_error = nullptr;
-    unsigned* d_lsync = nullptr;          // fused gate/up + down phase counters (zero between launches)
-    bool fused = false;                   // gate/up and down in one launch (MXFP4 decode; CPB_FUSED=1 enables)
     bool select_in_gateup = true;         // MXFP4 decode: top-k at the start of the gate/up kernel (CPB_SELECT_IN_ROUTE=1: in the route launch)
-    std::map<std::tuple<int, int, float*, int>, cpb::DecodeArgs*> decode_args;
-    bool persistent = false;  // the single-launch decode is opt-in (CPB_PERSISTENT=1)
-    bool prepare_only = false;
-    unsigned long long* d_stamps = nullptr;   // probe builds: persistent-decode phase timestamps
+    unsigned long long* d_stamps = nullptr;   // probe builds (CPB_DECODE_STAMPS): phase timestamps
     // grouped (n_tok > 1) MXFP4 path: per-token and per-pair scratch
     bool grouped = false;
     float *g_xn = nullptr, *g_xsb = nullptr, *g_logits = nullptr, *g_wts = nullptr, *g_hsb = nullptr, *g_dnout = nullptr;
@@ -256,18 +246,6 @@ int ensure_trace(cpb_moe_t* h) {
     return 0;
 }
 
-// A bounded wait inside the persistent kernel expired: re-arm the phase
-// counters and report.  (Called after a stream synchronisation.)
-int check_device_error(cpb_moe_t* h) {
-    int32_t err = 0;
-    HIP_OK(hipMemcpy(&err, h->d_error, sizeof err, hipMemcpyDeviceToHost));
-    if (!err) return 0;
-    HIP_OK(hipMemset(h->d_sync, 0, sizeof(unsigned) * (3 * (size_t)h->cfg.n_layer + 1)));
-    HIP_OK(hipMemset(h->d_error, 0, sizeof(int32_t)));
-    HIP_OK(hipMemset(h->d_lsync, 0, sizeof(unsigned) * 2));
-    return fail(CPB_ENODEV, "a bounded in-kernel wait timed out (persistent or fused decode)");
-}
-
 void clear_graphs(cpb_moe_t* h) {
     for (auto& g : h->graphs) hipGraphExecDestroy(g.second);
     h->graphs.clear();
@@ -292,7 +270,7 @@ int layer_token(cpb_moe_t* h, int layer, float* dx, int apply_norm, bool trace) 
     sa.ids = h->ids; sa.wts = h->wts; sa.logits = h->logits; sa.fallback = h->fallback;
     // MXFP4 decode: the gate/up kernel selects at its start (no
     // cross-workgroup hand-off inside the routing launch)
-    const bool sel_in_gu = h->mx && h->select_in_gateup && !(h->fused && !trace);
+    const bool sel_in_gu = h->mx && h->select_in_gateup;
     {
         Timer tm(h, 0);
         if (cpb::launch_route(&ra, &sa, sel_in_gu ? nullptr : h->counter, h->stream))
@@ -318,12 +296,6 @@ int layer_token(cpb_moe_t* h, int layer, float* dx, int apply_norm, bool trace) 
         dn.ids = h->ids; dn.wts = h->wts;
         dn.d = c.d; dn.dff = c.d_ff; dn.nbf = h->nbf; dn.nparts = h->parts_dn; dn.top_k = c.top_k;
         dn.x = dx; dn.dn = h->t_dn; dn.dn_sums = h->t_dn_sums;
-        if (!trace && h->fused && h->parts_gu == h->parts_dn) {
-            Timer tm(h, 1);
-            if (cpb::launch_layer_mx(g, dn, h->d_lsync, h->d_error, h->d_stamps, h->stream))
-                return fail(CPB_ENODEV, "gate/up + down launch failed");
-            return 0;
-        }
         {
             Timer tm(h, 1);
             if (cpb::launch_gateup_mx(g, trace, h->stream)) return fail(CPB_ENODEV, "gate/up launch failed");
@@ -391,14 +363,20 @@ int cpb_moe_create(const cpb_moe_cfg* cfg, int device, cpb_moe_t** out) {
     h->stream = h->own;
     const size_t d = cfg->d, ff = cfg->d_ff, k = cfg->top_k, ne = cfg->n_expert, T = cfg->max_tokens;
     int r;
-    if ((r = dmalloc(&h->x, T * d)) || (r = dmalloc(&h->xn, d)) || (r = dmalloc(&h->xq, d)) ||
-        (r = dmalloc(&h->xqn, d)) || (r = dmalloc(&h->xsb, d / 32)) || (r = dmalloc(&h->xsum, d / 32)) ||
+    if ((r = dmalloc(&h->x, T * d)) || (r = dmalloc(&h->xn, d)) || (r = dmalloc(&h->xq, 2 * d + 8 * (d / 32))) ||
         (r = dmalloc(&h->lstar, ne)) || (r = dmalloc(&h->lbound, ne)) || (r = dmalloc(&h->counter, 1)) ||
         (r = dmalloc(&h->logits, ne)) || (r = dmalloc(&h->ids, k)) || (r = dmalloc(&h->wts, k)) ||
-        (r = dmalloc(&h->fallback, 1)) || (r = dmalloc(&h->hq, k * ff)) || (r = dmalloc(&h->hqn, k * ff)) ||
-        (r = dmalloc(&h->hsb, k * ff / 32)) || (r = dmalloc(&h->hsum, k * ff / 32)) || (r = dmalloc(&h->hbuf, k * ff)) ||
+        (r = dmalloc(&h->fallback, 1)) || (r = dmalloc(&h->hq, 2 * k * ff + 4 * (k * ff / 32))) || (r = dmalloc(&h->hsum, k * ff / 32)) || (r = dmalloc(&h->hbuf, k * ff)) ||
         (r = dmalloc(&h->params, param_slots(*cfg).per_layer * cfg->n_layer)))
         return bail(r);
+    // xq, -xq, the x scales and the per-32 sums share one allocation, and so
+    // do hq, -hq and the hq scales (kernels read each group through one
+    // buffer resource)
+    h->xqn = h->xq + d;
+    h->xsb = (float*)(h->xq + 2 * d);
+    h->xsum = (int32_t*)(h->xq + 2 * d + 4 * (d / 32));
+    h->hqn = h->hq + k * ff;
+    h->hsb = (float*)(h->hq + 2 * k * ff);
     if (h->mx) {
         if ((r = dmalloc(&h->d_special, 1))) return bail(r);
         h->grouped = T > 1;
@@ -415,18 +393,7 @@ int cpb_moe_create(const cpb_moe_cfg* cfg, int device, cpb_moe_t** out) {
             (r = dmalloc(&h->g_dnout, np * d)))
             return bail(r);
     }
-    if ((r = dmalloc(&h->d_layers, (size_t)cfg->n_layer)) || (r = dmalloc(&h->d_sync, 3 * (size_t)cfg->n_layer + 1)) ||
-        (r = dmalloc(&h->d_error, 1)) || (r = dmalloc(&h->d_lsync, 2)))
-        return bail(r);
-    if (hipMemsetAsync(h->d_lsync, 0, sizeof(unsigned) * 2, h->stream) != hipSuccess)
-        return bail(fail(CPB_ENODEV, "init memset failed"));
-    if (const char* v = getenv("CPB_FUSED")) h->fused = v[0] != '0';
     if (const char* v = getenv("CPB_SELECT_IN_ROUTE")) h->select_in_gateup = v[0] == '0';
-    if (hipMemsetAsync(h->d_sync, 0, sizeof(unsigned) * (3 * (size_t)cfg->n_layer + 1), h->stream) != hipSuccess ||
-        hipMemsetAsync(h->d_error, 0, sizeof(int32_t), h->stream) != hipSuccess ||
-        hipMemsetAsync(h->d_layers, 0, sizeof(cpb::LayerPtrs) * cfg->n_layer, h->stream) != hipSuccess)
-        return bail(fail(CPB_ENODEV, "init memset failed"));
-    if (const char* v = getenv("CPB_PERSISTENT")) h->persistent = v[0] == '1';
 #ifdef CPB_DECODE_STAMPS
     if ((r = dmalloc(&h->d_stamps, ((size_t)1 << 20) + 4096))) return bail(r);
 #endif
@@ -497,10 +464,6 @@ int cpb_moe_load_layer(cpb_moe_t* h, int layer, const void* gate, const void* up
     }
     if ((r = upload(&L.router_w, base + ps.router_w, router_w, ne * d, h->stream))) return r;
     if ((r = upload(&L.norm_w, base + ps.norm_w, norm_w, d, h->stream))) return r;
-    if (h->mx) {
-        cpb::LayerPtrs lp{L.gu, L.dn, L.gate_b, L.up_b, L.down_b, L.router_w, L.router_b, L.norm_w};
-        HIP_OK(hipMemcpyAsync(h->d_layers + layer, &lp, sizeof lp, hipMemcpyHostToDevice, h->stream));
-    }
     HIP_OK(hipStreamSynchronize(h->stream));
     if (h->mx) {
         unsigned special = 0;
@@ -509,34 +472,6 @@ int cpb_moe_load_layer(cpb_moe_t* h, int layer, const void* gate, const void* up
     }
     L.loaded = true;
     return 0;
-}
-
-// Persistent single-launch decode of layers [layer0, layer0 + n_layers) for
-// one token; returns -28 / -22 when the device or shape cannot take it.
-static int launch_persistent(cpb_moe_t* h, int layer0, int n_layers, float* d_x, int apply_norm) {
-    const auto& c = h->cfg;
-    auto key = std::make_tuple(layer0, n_layers, d_x, apply_norm);
-    cpb::DecodeArgs a{};
-    a.layers = h->d_layers; a.layer0 = layer0; a.n_layers = n_layers; a.x = d_x; a.apply_norm = apply_norm;
-    a.d = c.d; a.dff = c.d_ff; a.ne = c.n_expert; a.k = c.top_k; a.nb = h->nb; a.nbf = h->nbf;
-    a.parts = std::max(h->parts_gu, h->parts_dn);
-    a.alpha = c.alpha; a.limit = c.limit; a.eps = c.rms_eps; a.norm = c.norm; a.norm_nt = c.norm_nt;
-    a.T_gu = c.top_k * (c.d_ff / 32); a.T_dn = c.d / (64 / c.top_k);
-    a.xn = h->xn; a.xq = h->xq; a.xqn = h->xqn; a.xsb = h->xsb; a.lstar = h->lstar; a.lbound = h->lbound;
-    a.ids = h->ids; a.wts = h->wts; a.logits = h->logits; a.fallback = h->fallback;
-    a.hq = h->hq; a.hqn = h->hqn; a.hsb = h->hsb; a.sync = h->d_sync; a.error = h->d_error;
-    a.stamps = h->d_stamps;
-    if (h->parts_gu != h->parts_dn) return -22;
-    auto it = h->decode_args.find(key);
-    if (it == h->decode_args.end()) {
-        // (never reached under stream capture: cpb_moe_forward_device prepares the args first)
-        cpb::DecodeArgs* dv = nullptr;
-        if (hipMalloc((void**)&dv, sizeof a) != hipSuccess) return fail(CPB_ENOMEM, "hipMalloc(decode args)");
-        if (hipMemcpy(dv, &a, sizeof a, hipMemcpyHostToDevice) != hipSuccess) { hipFree(dv); return fail(CPB_ENODEV, "args copy"); }
-        it = h->decode_args.emplace(key, dv).first;
-    }
-    if (h->prepare_only) return 0;
-    return cpb::launch_decode_mx(a, it->second, h->stream);
 }
 
 // n_tok > 1 tokens through one MXFP4 layer on the matrix cores (bit-identical
@@ -564,12 +499,6 @@ static int layer_grouped(cpb_moe_t* h, int layer, float* d_x, int n_tok, int app
 
 static int launch_direct(cpb_moe_t* h, int layer0, int n_layers, float* d_x, int n_tok, int apply_norm) {
     const auto& c = h->cfg;
-    if (h->mx && n_tok == 1 && h->persistent && !h->timing) {
-        const int r = launch_persistent(h, layer0, n_layers, d_x, apply_norm);
-        if (r == 0) return 0;
-        if (r != -28 && r != -22) return fail(CPB_ENODEV, "persistent decode launch failed (%d)", r);
-        h->persistent = false;          // shape/device cannot host it: per-phase kernels from now on
-    }
     for (int l = layer0; l < layer0 + n_layers; l++) {
         if (h->mx && n_tok > 1 && h->grouped && h->layers[l].mfma_exact) {
             if (int r = layer_grouped(h, l, d_x, n_tok, apply_norm, nullptr, nullptr)) return r;
@@ -591,15 +520,8 @@ int cpb_moe_forward_device(cpb_moe_t* h, int layer0, int n_layers, float* d_x, i
     HIP_OK(hipSetDevice(h->device));
     // per-kernel timing needs one event pair per launch: run those directly
     if (h->timing || !h->use_graphs) return launch_direct(h, layer0, n_layers, d_x, n_tok, apply_norm);
-    // device-side argument blocks are allocated before any stream capture
-    if (h->mx && n_tok == 1 && h->persistent) {
-        h->prepare_only = true;
-        const int r = launch_persistent(h, layer0, n_layers, d_x, apply_norm);
-        h->prepare_only = false;
-        if (r != 0 && r != -28 && r != -22) return r;
-    }
-    // otherwise replay one captured graph per distinct call (launch overhead
-    // of ~3 kernels per layer paid once)
+    // replay one captured graph per distinct call (launch overhead of ~3
+    // kernels per layer paid once)
     auto key = std::make_tuple(layer0, n_layers, d_x, n_tok, apply_norm, h->stream);
     auto it = h->graphs.find(key);
     if (it == h->graphs.end()) {
@@ -643,7 +565,7 @@ int cpb_moe_grouped_sums(cpb_moe_t* h, int layer, float* x, int n_tok, int apply
         r = fail(CPB_ENODEV, "grouped sums copy failed");
     hipFree(dgu);
     hipFree(ddn);
-    return r ? r : check_device_error(h);
+    return r;
 }
 
 int cpb_moe_forward(cpb_moe_t* h, int layer, float* x, int n_tok, int apply_norm, cpb_moe_trace* tr) {
@@ -693,7 +615,7 @@ int cpb_moe_forward(cpb_moe_t* h, int layer, float* x, int n_tok, int apply_norm
         if (r) return r;
     }
     HIP_OK(hipStreamSynchronize(h->stream));
-    return check_device_error(h);
+    return 0;
 }
 
 int cpb_moe_set_stream(cpb_moe_t* h, void* stream) {
@@ -705,7 +627,7 @@ int cpb_moe_set_stream(cpb_moe_t* h, void* stream) {
 int cpb_moe_sync(cpb_moe_t* h) {
     if (!h) return fail(CPB_EINVAL, "handle is NULL");
     HIP_OK(hipStreamSynchronize(h->stream));
-    return check_device_error(h);
+    return 0;
 }
 
 int cpb_moe_timing(cpb_moe_t* h, int enable) {
@@ -739,7 +661,6 @@ void cpb_moe_destroy(cpb_moe_t* h) {
     hipSetDevice(h->device);
     if (h->stream) hipStreamSynchronize(h->stream);
     clear_graphs(h);
-    for (auto& kv : h->decode_args) hipFree(kv.second);
 #ifdef CPB_DECODE_STAMPS
     if (h->d_stamps) {
         const char* path = getenv("CPB_DECODE_STAMPS_FILE");
@@ -751,14 +672,13 @@ void cpb_moe_destroy(cpb_moe_t* h) {
         hipFree(h->d_stamps);
     }
 #endif
-    hipFree(h->d_layers); hipFree(h->d_sync); hipFree(h->d_error); hipFree(h->d_lsync);
     void* gbufs[] = {h->g_xn, h->g_xsb, h->g_logits, h->g_wts, h->g_hsb, h->g_dnout, h->g_xq, h->g_hq, h->g_ximg,
                      h->g_himg, h->g_lstar, h->g_lbound, h->g_ids, h->g_fallback, h->g_sorted, h->g_ntiles, h->g_tiles,
                      h->d_special};
     for (void* p : gbufs) hipFree(p);
     for (auto& L : h->layers) free_layer(L);
-    void* bufs[] = {h->params, h->x, h->xn, h->xq, h->xqn, h->xsb, h->xsum, h->lstar, h->lbound, h->counter, h->logits,
-                    h->ids, h->wts, h->fallback, h->hq, h->hqn, h->hsb, h->hsum, h->hbuf, h->t_gu, h->t_h,
+    void* bufs[] = {h->params, h->x, h->xn, h->xq, h->lstar, h->lbound, h->counter, h->logits,
+                    h->ids, h->wts, h->fallback, h->hq, h->hsum, h->hbuf, h->t_gu, h->t_h,
                     h->t_dn, h->t_gu_sums, h->t_dn_sums, h->staging};
     for (void* p : bufs) if (p) hipFree(p);
     for (auto& u : h->ev_used) { hipEventDestroy(u.second.first); hipEventDestroy(u.second.second); }

@@ -15,7 +15,7 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 // 16 B unit holding the 15 e8m0 bytes, i.e. 16 dwordx4 loads per k-part.
 constexpr int kBlkPerPart = 15;
 constexpr int kUnits = 16;
-// k-parts (one wavefront each) per MXFP4 expert-GEMV workgroup: K <= 8 x 15 x 32 = 3840
+// k-parts (two wavefronts each) per MXFP4 expert-GEMV workgroup: K <= 8 x 15 x 32 = 3840
 constexpr int kMaxParts = 8;
 
 // v_perm_b32: byte i of the result = byte sel_i of {hi:lo} (0-3 lo, 4-7 hi).

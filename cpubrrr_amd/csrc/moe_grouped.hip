@@ -231,18 +231,23 @@ CPB_DEV void stage_store(unsigned char* st, const StageRegs& g) {
     if (tid < kBlkPerPart * 32) ((uint32_t*)(st + kBlkPerPart * 32 * kSlot))[tid] = g.s;
 }
 
-// Blocks [i0, i0 + N) of one wave's k-part: D = A(rows) x B(tokens) per
-// block, acc = fma(D, xsb, acc) in block order (the decode kernels' order).
+// One wave's k-part: D = A(rows) x B(tokens) per block, acc = fma(D, xsb,
+// acc) in block order.
 // w[k] = code block i0 + k of the lane's row, ex = the k-part's exponents.
 // TRACE writes the int32 block sums S = D * 2^(128 - e) of valid rows.
+// The decode kernels accumulate a k-part in two chains, blocks 0-7 and
+// 8-14 (two wavefronts per k-part), and add the chains in order: so do
+// acc0 / acc1 here.
 template <bool TRACE>
-CPB_DEV v16f part_mfma(const u32x4* wv, const unsigned char* st, int lane, int q, int nbk, int32_t* trace_base,
-                       size_t trace_row_stride, bool trace_ok) {
+CPB_DEV void part_mfma(const u32x4* wv, const unsigned char* st, int lane, int q, int nbk, int32_t* trace_base,
+                       size_t trace_row_stride, bool trace_ok, v16f& acc0, v16f& acc1) {
     const int ti = lane & 31, hb = lane >> 5;
     const float* sl = (const float*)(st + kBlkPerPart * 32 * kSlot);
-    v16f acc = {};
+    acc0 = v16f{};
+    acc1 = v16f{};
 #pragma unroll
     for (int i = 0; i < kBlkPerPart; i++) {
+        v16f& acc = i < kSubUnits ? acc0 : acc1;
         const unsigned char* xp = st + (i * 32 + ti) * kSlot + hb * 32;
         const u32x4 x0 = *(const u32x4*)xp, x1 = *(const u32x4*)(xp + 16);
         const float s = sl[i * 32 + ti];
@@ -260,7 +265,6 @@ CPB_DEV v16f part_mfma(const u32x4* wv, const unsigned char* st, int lane, int q
             }
         }
     }
-    return acc;
 }
 
 // Weight window of one k-part (16 units) for the lane's row: nontemporal loads.
@@ -285,9 +289,12 @@ CPB_DEV v16f grouped_parts(const u32x4* wbase, size_t stride, int P, unsigned ch
         stage_store(smem, g);
         __syncthreads();
         if (q + 1 < P) load_window(wbase + (size_t)(q + 1) * part, stride, wn);
-        const v16f acc = part_mfma<TRACE>(wv, smem, lane, q, nbk, tb, nbk, trace_ok);
+        v16f acc0, acc1;
+        part_mfma<TRACE>(wv, smem, lane, q, nbk, tb, nbk, trace_ok, acc0, acc1);
 #pragma unroll
-        for (int r = 0; r < 16; r++) tot[r] += acc[r];
+        for (int r = 0; r < 16; r++) tot[r] += acc0[r];
+#pragma unroll
+        for (int r = 0; r < 16; r++) tot[r] += acc1[r];
         __syncthreads();
 #pragma unroll
         for (int u = 0; u < kUnits; u++) wv[u] = wn[u];

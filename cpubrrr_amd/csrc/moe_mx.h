@@ -49,9 +49,5 @@ int launch_repack_gateup(const uint8_t* gate, const uint8_t* up, u32x4* out, int
 int launch_repack_down(const uint8_t* down, u32x4* out, int ne, int d, int nbf, int top_k, hipStream_t s);
 int launch_gateup_mx(const GateUpArgs& a, bool trace, hipStream_t s);
 int launch_down_mx(const DownArgs& a, bool trace, hipStream_t s);
-// gate/up and down of one layer in a single launch; sync: two zeroed counters
-// (left zeroed), err: set to 1 if a bounded wait expired
-int launch_layer_mx(const GateUpArgs& g, const DownArgs& a, unsigned* sync, int32_t* err, unsigned long long* stamps,
-                    hipStream_t s);
 
 }  // namespace cpb

@@ -1,38 +1,10 @@
-// mx_dev.h -- device building blocks of the MXFP4 expert GEMVs, shared by
-// the per-phase kernels (moe_mx.hip) and the persistent decode kernel
-// (decode_mx.hip).  Stream layout and lane mapping: see moe_mx.hip.
+// mx_dev.h -- device building blocks of the MXFP4 expert GEMVs (moe_mx.hip,
+// and the activation staging of the grouped path).  Stream layout and lane
+// mapping: see moe_mx.hip.
 #pragma once
 #include "moe_common.h"
 
 namespace cpb {
-
-// One lane's k-part: wv[0] = the 15 e8m0 bytes, wv[1..15] = nibble blocks.
-// xs: LDS activations of these 15 blocks as [15][xp 2 x u32x4][xn 2 x u32x4],
-// sb: their 15 scales.
-template <bool TRACE>
-CPB_DEV float part_dot(const u32x4* wv, const u32x4* xs, const float* sb, int32_t* sums_out, int blk0, int nb) {
-    const MxConsts k = mx_consts();
-    const uint32_t ew[4] = {wv[0][0], wv[0][1], wv[0][2], wv[0][3]};
-    float acc = 0.0f;
-#pragma unroll
-    for (int u = 0; u < kBlkPerPart; u++) {
-        const u32x4* xb = xs + u * 4;
-#ifdef CPB_PROBE_NO_DECODE
-        // probe builds only: same loads and epilogue, no decode arithmetic
-        int S = (int)(wv[u + 1][0] ^ xb[0][0]) & 7;
-#else
-        int S = mx_block_sum(wv[u + 1], xb[0], xb[1], xb[2], xb[3], k);
-#endif
-        uint32_t e = (ew[u >> 2] >> (8 * (u & 3))) & 0xffu;
-        acc = fmaf((float)S, e8m0_scale(e, sb[u]), acc);
-        if (TRACE && blk0 + u < nb) sums_out[u] = S;
-        // keep each block's LDS operand reads next to their use: with the
-        // weights already resident the scheduler would otherwise hoist all
-        // 15 blocks' reads (240 VGPRs)
-        __builtin_amdgcn_sched_barrier(0);
-    }
-    return acc;
-}
 
 // LDS image of one expert's activations for one k-part: 15 blocks x
 // [xq 8 dwords | -xq 8 dwords], then 15 block scales (+1 pad): 256 dwords.
@@ -59,12 +31,42 @@ CPB_DEV XsSlot xs_slot(const uint32_t* __restrict__ q, const uint32_t* __restric
     return XsSlot{base + (isx ? bc * 8 + (j & 7) : bc), use && blk < nb && (isx || u < kBlkPerPart)};
 }
 
-// Issue the lane's 16 weight loads in stream order (e8m0 unit first) so the
-// compiler's in-order vmcnt waits release each block as soon as it lands.
-CPB_DEV void load_part(const u32x4* p, size_t stride, u32x4* wv) {
+// A k-part is processed by two wavefronts: sub-part h covers blocks
+// 8h .. 8h + 7 of it (the last slot of sub-part 1 is empty).
+constexpr int kSubUnits = 8;
+
+// One lane's sub-part: wv[0] = the 15 e8m0 bytes, wv[1 .. 8] = the nibble
+// blocks ub .. ub + 7 of the k-part.  Block 15 (the second sub-part's eighth
+// slot) does not exist: its weights load as zero and its pad exponent byte is
+// zero, so it adds exactly nothing.
+template <bool TRACE>
+CPB_DEV float part_dot_sub(const u32x4* wv, int ub, const u32x4* xs, const float* sb, int32_t* sums_out, int blk0,
+                           int nb) {
+    const MxConsts k = mx_consts();
+    const uint32_t ew[4] = {wv[0][0], wv[0][1], wv[0][2], wv[0][3]};
+    float acc = 0.0f;
 #pragma unroll
-    for (int u = 0; u < kUnits; u++) {
-        wv[u] = __builtin_nontemporal_load(p + (size_t)u * stride);
+    for (int i = 0; i < kSubUnits; i++) {
+        const int u = ub + i;
+        const u32x4* xb = xs + u * 4;
+        int S = mx_block_sum(wv[i + 1], xb[0], xb[1], xb[2], xb[3], k);
+        const uint32_t e = (ew[u >> 2] >> (8 * (u & 3))) & 0xffu;
+        acc = fmaf((float)S, e8m0_scale(e, sb[u]), acc);
+        if (TRACE && u < kBlkPerPart && blk0 + u < nb) sums_out[u] = S;
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    return acc;
+}
+
+// Issue the sub-part's loads in stream order: the e8m0 unit, then units
+// 1 + ub .. 1 + ub + 7 (stride: 16-byte units between consecutive units);
+// unit 16 (beyond the k-part) is not read.
+CPB_DEV void load_sub(const u32x4* p, size_t stride, int ub, u32x4* wv) {
+    wv[0] = __builtin_nontemporal_load(p);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < kSubUnits; i++) {
+        wv[i + 1] = ub + i < kBlkPerPart ? __builtin_nontemporal_load(p + (size_t)(1 + ub + i) * stride) : u32x4{0, 0, 0, 0};
         __builtin_amdgcn_sched_barrier(0);
     }
 }

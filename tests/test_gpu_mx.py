@@ -100,26 +100,6 @@ def test_router_tie_uses_exact_fallback(gpu):
     check_layer(L, x, False, xo, t)
 
 
-def test_persistent_matches_phased(gpu, monkeypatch):
-    # the single-launch decode and the per-phase kernels give identical bits
-    import torch
-    say("case persistent vs phased, 4 layers 20b shape")
-    d, ne, k, nl = 2880, 32, 4, 4
-    layers = [synth.gptoss_layer(d, d, ne, k, seed=3, layer=l, zipf=1.1) for l in range(nl)]
-    outs = []
-    for phased in (False, True):
-        monkeypatch.setenv("CPB_PERSISTENT", "0" if phased else "1")
-        with MoeBlock(MoeConfig.gptoss(d=d, n_expert=ne, top_k=k, d_ff=d, n_layer=nl)) as blk:
-            for l in range(nl):
-                blk.load_layer(l, layers[l])
-            x = torch.from_numpy(synth.token(d, 3, 0)).to("cuda:0")
-            for rep in range(3):
-                blk.forward_device(0, nl, x.data_ptr(), 1, True)
-            blk.sync()
-            outs.append(x.cpu().numpy())
-    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
-
-
 def test_multi_token_equals_per_token(gpu):
     say("case n_tok=3")
     d = 960
@@ -134,11 +114,9 @@ def test_multi_token_equals_per_token(gpu):
             assert np.array_equal(y.view(np.uint32), Y[i].view(np.uint32))
 
 
-@pytest.mark.parametrize("phased", [False, True])
-def test_device_stack_vs_oracle(gpu, phased, monkeypatch):
+def test_device_stack_vs_oracle(gpu):
     import torch
-    monkeypatch.setenv("CPB_PERSISTENT", "0" if phased else "1")
-    say(f"case 3-layer device stack phased={phased}")
+    say("case 3-layer device stack")
     d, ne, k, nl = 2880, 32, 4, 3
     layers = [synth.gptoss_layer(d, d, ne, k, seed=0, layer=l, zipf=1.1) for l in range(nl)]
     cfg = MoeConfig.gptoss(d=d, n_expert=ne, top_k=k, d_ff=d, n_layer=nl)
@@ -158,21 +136,20 @@ def test_device_stack_vs_oracle(gpu, phased, monkeypatch):
     assert np.max(np.abs(y - xr)) <= 1e-3 * rms
 
 
-def test_fused_layer_matches_two_launches(gpu, monkeypatch):
-    # gate/up + down in one launch (down tiles wait on a counter) and the two
-    # separate kernels give identical bits over a 4-layer stack, replayed
+def test_graph_replay_matches_direct_launches(gpu):
+    # the captured HIP graph, replayed back to back, and direct launches of
+    # the same kernels give identical bits over a 4-layer stack
     import torch
-    say("case fused vs two launches, 4 layers 20b shape")
+    say("case graph replay vs direct launches, 4 layers 20b shape")
     d, ne, k, nl = 2880, 32, 4, 4
-    layers = [synth.gptoss_layer(d, d, ne, k, seed=6, layer=l, zipf=1.1) for l in range(nl)]
+    layers = [synth.gptoss_layer(d, d, ne, k, seed=3, layer=l, zipf=1.1) for l in range(nl)]
     outs = []
-    for fused in ("1", "0"):
-        monkeypatch.setenv("CPB_PERSISTENT", "0")
-        monkeypatch.setenv("CPB_FUSED", fused)
+    for direct in (False, True):
         with MoeBlock(MoeConfig.gptoss(d=d, n_expert=ne, top_k=k, d_ff=d, n_layer=nl)) as blk:
             for l in range(nl):
                 blk.load_layer(l, layers[l])
-            x = torch.from_numpy(synth.token(d, 6, 0)).to("cuda:0")
+            x = torch.from_numpy(synth.token(d, 3, 0)).to("cuda:0")
+            blk.timing(direct)
             for rep in range(3):
                 blk.forward_device(0, nl, x.data_ptr(), 1, True)
             blk.sync()
