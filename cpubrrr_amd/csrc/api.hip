@@ -92,7 +92,7 @@ struct cpb_moe {
     unsigned long long* d_stamps = nullptr;   // probe builds (CPB_DECODE_STAMPS): phase timestamps
     // grouped (n_tok > 1) MXFP4 path: per-token and per-pair scratch
     bool grouped = false;
-    float *g_xn = nullptr, *g_xsb = nullptr, *g_logits = nullptr, *g_wts = nullptr, *g_hsb = nullptr, *g_dnout = nullptr;
+    float *g_inv = nullptr, *g_xn = nullptr, *g_xsb = nullptr, *g_logits = nullptr, *g_wts = nullptr, *g_hsb = nullptr, *g_dnout = nullptr;
     int8_t *g_xq = nullptr, *g_hq = nullptr;
     uint8_t *g_ximg = nullptr, *g_himg = nullptr;
     double *g_lstar = nullptr, *g_lbound = nullptr;
@@ -384,7 +384,7 @@ int cpb_moe_create(const cpb_moe_cfg* cfg, int device, cpb_moe_t** out) {
     }
     if (h->mx && T > 1) {
         const size_t nb = d / 32, nbf = ff / 32, np = T * k;
-        if ((r = dmalloc(&h->g_xn, T * d)) || (r = dmalloc(&h->g_xq, T * d)) || (r = dmalloc(&h->g_xsb, T * nb)) ||
+        if ((r = dmalloc(&h->g_xn, T * d)) || (r = dmalloc(&h->g_inv, T)) || (r = dmalloc(&h->g_xq, T * d)) || (r = dmalloc(&h->g_xsb, T * nb)) ||
             (r = dmalloc(&h->g_ximg, T * nb * 64)) || (r = dmalloc(&h->g_lstar, T * ne)) ||
             (r = dmalloc(&h->g_lbound, T * ne)) || (r = dmalloc(&h->g_logits, T * ne)) || (r = dmalloc(&h->g_ids, np)) ||
             (r = dmalloc(&h->g_wts, np)) || (r = dmalloc(&h->g_fallback, T)) || (r = dmalloc(&h->g_sorted, np)) ||
@@ -488,7 +488,7 @@ static int layer_grouped(cpb_moe_t* h, int layer, float* d_x, int n_tok, int app
     g.norm = c.norm; g.norm_nt = c.norm_nt; g.apply_norm = apply_norm;
     g.eps = c.rms_eps; g.alpha = c.alpha; g.limit = c.limit;
     g.max_tiles = n_tok * c.top_k / 32 + c.n_expert + 1;
-    g.x = d_x; g.xn = h->g_xn; g.xq = h->g_xq; g.xsb = h->g_xsb; g.ximg = h->g_ximg;
+    g.x = d_x; g.xn = h->g_xn; g.inv = h->g_inv; g.xq = h->g_xq; g.xsb = h->g_xsb; g.ximg = h->g_ximg;
     g.lstar = h->g_lstar; g.lbound = h->g_lbound; g.logits = h->g_logits; g.ids = h->g_ids; g.wts = h->g_wts;
     g.fallback = h->g_fallback; g.sorted = h->g_sorted; g.tiles = h->g_tiles; g.ntiles = h->g_ntiles;
     g.hq = h->g_hq; g.hsb = h->g_hsb; g.himg = h->g_himg; g.dnout = h->g_dnout;
@@ -672,7 +672,7 @@ void cpb_moe_destroy(cpb_moe_t* h) {
         hipFree(h->d_stamps);
     }
 #endif
-    void* gbufs[] = {h->g_xn, h->g_xsb, h->g_logits, h->g_wts, h->g_hsb, h->g_dnout, h->g_xq, h->g_hq, h->g_ximg,
+    void* gbufs[] = {h->g_inv, h->g_xn, h->g_xsb, h->g_logits, h->g_wts, h->g_hsb, h->g_dnout, h->g_xq, h->g_hq, h->g_ximg,
                      h->g_himg, h->g_lstar, h->g_lbound, h->g_ids, h->g_fallback, h->g_sorted, h->g_ntiles, h->g_tiles,
                      h->d_special};
     for (void* p : gbufs) hipFree(p);

@@ -76,9 +76,17 @@ CPB_DEV uint32_t neg4(uint32_t v) {
     return r;
 }
 
-// Q8 round: Rust f32::round (half away from zero), clamp to +-127.
+// Q8 round: (v / sc).round() in the reference's fp32 (quotient correctly
+// rounded, then half away from zero), clamped to +-127.  The quotient from
+// the hardware reciprocal, v * rcp(sc), is within a few ulp (< 2^-16 for
+// |v / sc| <= 128) of the exact one; unless it lies within 2^-10 of a
+// half-integer both round to the same integer, and only there (about one
+// value in a thousand) the IEEE division decides.
 CPB_DEV int8_t q8_round(float v, float sc) {
-    float r = roundf(v / sc);
+    const float y = v * __builtin_amdgcn_rcpf(sc);
+    const float a = fabsf(y);
+    float r = roundf(y);
+    if (fabsf((a - floorf(a)) - 0.5f) < 0x1p-10f) r = roundf(v / sc);
     r = fminf(fmaxf(r, -127.0f), 127.0f);
     return (int8_t)r;
 }

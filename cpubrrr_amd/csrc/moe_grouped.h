@@ -26,6 +26,7 @@ struct GroupedArgs {
     // activations (device)
     float* x;                  // [n_tok][d] residual, updated in place
     float* xn;                 // [n_tok][d]
+    float* inv;                // [n_tok] rmsnorm scale (1 without the norm)
     int8_t* xq;                // [n_tok][d]
     float* xsb;                // [n_tok][nb]
     uint8_t* ximg;             // [n_tok][nb][64] fp8 image of xq (MFMA operand)

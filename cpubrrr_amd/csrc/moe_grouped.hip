@@ -68,6 +68,7 @@ __global__ __launch_bounds__(256) void k_prep_batch(GroupedArgs a) {
     float* xnl = xs + d;
     float* scratch = xnl + d;
     norm_into(a.x + (size_t)t * d, a.norm_w, d, a.eps, a.norm, a.norm_nt, a.apply_norm, xs, xnl, scratch);
+    if (tid == 0) a.inv[t] = a.apply_norm ? scratch[16] : 1.0f;
     // Q8 per 32-block (engine_gpt2.rs:691-699): 32 lanes per block
     const int l = tid & 31;
     for (int bk = tid >> 5; bk < a.nb; bk += nth >> 5) {
@@ -88,31 +89,49 @@ __global__ __launch_bounds__(256) void k_prep_batch(GroupedArgs a) {
     }
 }
 
-// ---- 2. router logits + bounds, workgroup = (expert, 16 tokens) ----
+// ---- 2. router logits + bounds, workgroup = (expert, kRouteTok tokens) ----
+// The decode route's computation (logit_phase1/2/final, 256 threads, 16
+// elements each), so every token's logits are those of per-token decode bit
+// for bit.
 __global__ __launch_bounds__(256) void k_router_batch(GroupedArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
-    const int e = blockIdx.x, d = a.d, tid = threadIdx.x, nth = blockDim.x;
-    float* xnl = (float*)smem;
-    double* dsc = (double*)(xnl + d + 32);
-    double* dred = dsc + 16;
-    const int C = ((d + 4 * nth - 1) / (4 * nth)) * 4;
-    const int j0 = tid * C;
-    const float* W = a.router_w + (size_t)e * d;
-    float4 wv[kChunk / 4];
+    const int e = blockIdx.x, d = a.d, tid = threadIdx.x, nw = blockDim.x >> 6;
+    double* dred = (double*)smem;              // [64]
+    const int j0 = tid * kRouteC;
+    const bool act = j0 < d;
+    const uint32_t off = (uint32_t)(act ? j0 : 0) * 4;
+    const __amdgpu_buffer_rsrc_t rW = buf_rsrc(a.router_w + (size_t)e * d, (uint32_t)d * 4);
+    const bool use_g = a.norm_w && a.apply_norm;
+    const __amdgpu_buffer_rsrc_t rg = buf_rsrc(a.norm_w, use_g ? (uint32_t)d * 4 : 0u);
+    float wf[16], gf[16];
 #pragma unroll
-    for (int i = 0; i < kChunk / 4; i++) wv[i] = *(const float4*)(W + min(j0 + 4 * i, d - 4));
+    for (int k = 0; k < 4; k++) {
+        const u32x4 w4 = __builtin_amdgcn_raw_buffer_load_b128(rW, off + 16 * k, 0, 0);
+        const u32x4 g4 = __builtin_amdgcn_raw_buffer_load_b128(rg, off + 16 * k, 0, 0);
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            wf[4 * k + c] = act ? __uint_as_float(w4[c]) : 0.0f;
+            gf[4 * k + c] = use_g ? __uint_as_float(g4[c]) : 1.0f;
+        }
+    }
     const double b = a.router_b ? (double)a.router_b[e] : 0.0;
     for (int tt = 0; tt < kRouteTok; tt++) {
         const int t = blockIdx.y * kRouteTok + tt;
         if (t >= a.n_tok) break;
-        for (int i = tid; i < d / 4; i += nth) ((float4*)xnl)[i] = ((const float4*)(a.xn + (size_t)t * d))[i];
-        __syncthreads();
-        double total = 0.0, bound = 0.0;
-        router_logit(wv, C, j0, xnl, d, b, dsc, dred, &total, &bound);
-        if (tid == 0) {
-            a.lstar[(size_t)t * a.ne + e] = total;
-            a.lbound[(size_t)t * a.ne + e] = bound;
+        const __amdgpu_buffer_rsrc_t rx = buf_rsrc(a.x + (size_t)t * d, (uint32_t)d * 4);
+        float xf[16];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const u32x4 x4 = __builtin_amdgcn_raw_buffer_load_b128(rx, off + 16 * k, 0, 0);
+#pragma unroll
+            for (int c = 0; c < 4; c++) xf[4 * k + c] = act ? __uint_as_float(x4[c]) : 0.0f;
         }
+        LogitThread lt;
+        logit_phase1(wf, xf, gf, lt, dred);
+        __syncthreads();
+        logit_phase2(lt, act, dred);
+        __syncthreads();
+        if (tid == 0) logit_final(dred, nw, d, b, a.inv[t], a.lstar + (size_t)t * a.ne + e, a.lbound + (size_t)t * a.ne + e);
         __syncthreads();
     }
 }
@@ -415,8 +434,7 @@ __global__ __launch_bounds__(256) void k_combine_batch(GroupedArgs a) {
 int launch_grouped_layer(const GroupedArgs& a, bool trace, hipStream_t s) {
     const int nt = a.n_tok;
     launch(k_prep_batch, dim3(nt), dim3(256), sizeof(float) * (2 * a.d + 64), s, a);
-    launch(k_router_batch, dim3(a.ne, (nt + kRouteTok - 1) / kRouteTok), dim3(256),
-           sizeof(float) * (a.d + 32) + sizeof(double) * 32, s, a);
+    launch(k_router_batch, dim3(a.ne, (nt + kRouteTok - 1) / kRouteTok), dim3(256), sizeof(double) * 64, s, a);
     launch(k_select_batch, dim3(nt), dim3(64), sizeof(double) * 4 * a.ne + sizeof(float) * a.d + 64, s, a);
     launch(k_group, dim3(1), dim3(1024), 0, s, a);
     const dim3 ggu(a.max_tiles, (a.dff / 32 + 3) / 4), gdn(a.max_tiles, (a.d / 32 + 7) / 8);

@@ -52,9 +52,7 @@ __global__ __launch_bounds__(256) void k_route(RouteArgs a, SelectArgs s, unsign
     if (!last || threadIdx.x >= 64) return;
     if (threadIdx.x == 0) st_dev(arrive, 0u);
     const int e = blockIdx.x;
-    RSTAMP(6);
     select_publish(s, smem, a.stamps ? a.stamps + (size_t)e * 16 + 8 : nullptr);
-    RSTAMP(7);
 }
 
 // Standalone selection (one wavefront), for callers that route elsewhere.

@@ -108,87 +108,18 @@ CPB_DEV void norm_into(const float* __restrict__ xg, const float* __restrict__ n
     __syncthreads();
 }
 
-template <typename T>
-CPB_DEV T block_sum(T v, T* red) {
-    // any multiple of 64 threads (<= 1024); fixed order (deterministic)
-    const int tid = threadIdx.x, nw = blockDim.x >> 6;
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
-    if ((tid & 63) == 0) red[tid >> 6] = v;
-    __syncthreads();
-    T r = red[0];
-    for (int w = 1; w < nw; w++) r += red[w];
-    __syncthreads();
-    return r;
-}
 
 #ifdef CPB_DECODE_STAMPS
-#define RSTAMP(i) do { if (threadIdx.x == 0 && a.stamps) a.stamps[(size_t)e * 16 + (i)] = wall_clock64(); } while (0)
+// timestamps kept in registers and written once at the end: a global store
+// per stamp would make every later vmcnt wait include its completion
+#define RSTAMP_DECL unsigned long long rst_[8] = {0, 0, 0, 0, 0, 0, 0, 0}
+#define RSTAMP(i) do { rst_[i] = wall_clock64(); } while (0)
+#define RSTAMP_FLUSH do { if (threadIdx.x == 0 && a.stamps) for (int i_ = 0; i_ < 8; i_++) a.stamps[(size_t)e * 16 + i_] = rst_[i_]; } while (0)
 #else
+#define RSTAMP_DECL do { } while (0)
 #define RSTAMP(i) do { } while (0)
+#define RSTAMP_FLUSH do { } while (0)
 #endif
-
-constexpr int kChunk = 16;          // router elements per thread: d <= 4096
-
-// Logit of one router row: the reference's fp32 products w[j]*xn[j] (xn in
-// LDS) summed exactly in fp64 with the bias, and a bound on how far the
-// reference's serial fp32 chain (acc = b; acc += w[j]*xn[j]) can lie from it:
-// u/(1-u) * (sum_k |S_k| + n*gamma_n*A) over the exact prefix sums S_k
-// (Higham, Accuracy and Stability of Numerical Algorithms, 2nd ed., 4.2).
-// wv: this thread's C (<= kChunk) consecutive weights from j0.  Every thread
-// of the workgroup calls it; thread 0 receives the results.
-CPB_DEV void router_logit(const float4* wv, int C, int j0, const float* xn, int d, double b, double* dsc,
-                          double* dred, double* out_total, double* out_bound) {
-    const int tid = threadIdx.x, nth = blockDim.x;
-    float p[kChunk];
-    double loc = 0.0, absp = 0.0;
-#pragma unroll
-    for (int i = 0; i < kChunk / 4; i++) {
-        const int j = j0 + 4 * i;
-        const int jc = min(j, d - 4);
-        const float4 xv = *(const float4*)(xn + jc);
-        const float4 w4 = wv[i];
-        const float pr[4] = {w4.x * xv.x, w4.y * xv.y, w4.z * xv.z, w4.w * xv.w};
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const bool in = 4 * i + k < C && j + k < d && j == jc;
-            p[4 * i + k] = in ? pr[k] : 0.0f;
-            loc += (double)p[4 * i + k];
-            absp += fabs((double)p[4 * i + k]);
-        }
-    }
-    // exclusive scan of the chunk sums: wave scan + wave totals
-    const int lane = tid & 63, wv_ = tid >> 6, nw = nth >> 6;
-    double inc = loc;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const double t = __shfl_up(inc, off);
-        if (lane >= off) inc += t;
-    }
-    if (lane == 63) dsc[wv_] = inc;
-    __syncthreads();
-    double woff = 0.0;
-    for (int w2 = 0; w2 < wv_; w2++) woff += dsc[w2];
-    double wtot = dsc[0];
-    for (int w2 = 1; w2 < nw; w2++) wtot += dsc[w2];
-    const double total = b + wtot;
-    double run = b + woff + (inc - loc);
-    double sabs = 0.0;
-#pragma unroll
-    for (int i = 0; i < kChunk; i++) { run += (double)p[i]; sabs += (i < C && j0 + i < d) ? fabs(run) : 0.0; }
-    __syncthreads();
-    const double SS = block_sum(sabs, dred);
-    const double AP = block_sum(absp, dred);
-    if (tid == 0) {
-        const double u = 5.9604644775390625e-08;  // 2^-24
-        const double n = (double)d;
-        const double A = fabs(b) + AP;
-        const double gam = n * u / (1.0 - n * u);
-        double bound = u / (1.0 - u) * (SS + n * gam * A);
-        *out_total = total;
-        *out_bound = bound * 1.0001 + 1e-10 * A + 1e-30;
-    }
-}
 
 // ---- wavefront DPP helpers on doubles (no LDS round trips) ----
 // v from the DPP source lane; lanes whose source is out of the row, or whose
@@ -241,11 +172,73 @@ CPB_DEV void st_dev16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, u32x4 v) {
 constexpr int kRouteC = 16;         // consecutive elements per thread in route_expert
 
 // LDS bytes route_expert needs (any block size; d <= 4096)
-CPB_DEV_HOST inline int route_xt_stride(int d) { return (d / 16 + 63) / 64 * 64 + 4; }
+// transposed x: 16 rows of d/16 values, padded so the 16 lanes' 16-byte
+// reads spread over the banks and the look-ahead reads stay inside
+CPB_DEV_HOST inline int route_xt_stride(int d) { return (d / 16 + 32 + 63) / 64 * 64 + 4; }
 CPB_DEV_HOST inline size_t route_lds_bytes(int d) {
     const size_t xt = sizeof(float) * 16 * (size_t)route_xt_stride(d);
     const size_t xr = sizeof(float) * (size_t)d;
     return (xt > xr ? xt : xr) + sizeof(double) * 64 + 64;
+}
+
+// ---- router logit from unscaled products, shared by the decode route and
+// the batched router so both produce the same bits ----
+// Thread t (of a workgroup of nw waves) owns 16 consecutive elements.
+// Phase 1: P_j = W_j * x_j * g_j in fp64, this thread's sum, the wave's
+// inclusive scan; the wave total goes to dred[wv].  Phase 2 (after a
+// barrier): prefix sums for the bound; wave totals to dred[16 + wv] and
+// dred[32 + wv].  Final (after a barrier, one thread): logit and bound for
+// the norm scale inv.
+struct LogitThread {
+    double P[16];
+    double loc, absp, incl;
+};
+CPB_DEV void logit_phase1(const float* wf, const float* xf, const float* gf, LogitThread& L, double* dred) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    L.loc = 0.0;
+    L.absp = 0.0;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        L.P[i] = (double)wf[i] * ((double)xf[i] * (double)gf[i]);
+        L.loc += L.P[i];
+        L.absp += fabs(L.P[i]);
+    }
+    L.incl = wave_scan_f64(L.loc);
+    if (lane == 63) dred[wv] = L.incl;
+}
+CPB_DEV void logit_phase2(const LogitThread& L, bool act, double* dred) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    double woff = 0.0;
+    for (int w2 = 0; w2 < wv; w2++) woff += dred[w2];
+    double run = woff + (L.incl - L.loc);
+    double sabs = 0.0;
+#pragma unroll
+    for (int i = 0; i < 16; i++) { run += L.P[i]; sabs += act ? fabs(run) : 0.0; }
+    const double ws = wave_total63_f64(sabs);
+    const double wa = wave_total63_f64(L.absp);
+    if (lane == 63) { dred[16 + wv] = ws; dred[32 + wv] = wa; }
+    (void)nw;
+}
+// The reference computes xn_j = fl(fl(x_j * inv) * g_j), p_j = fl(W_j * xn_j)
+// and the serial fp32 chain acc = b; acc += p_j.  With t_j = inv * P_j
+// (exact), |p_j - t_j| <= g3 |t_j|, and the chain lies within
+// u/(1-u) (sum_k |S_k| + n gamma_n A) of b + sum p_j (Higham, Accuracy and
+// Stability of Numerical Algorithms, 2nd ed., 4.2), where sum_k |S_k| <=
+// n|b| + inv sum_k |P-prefix_k| + n g3 inv A' and A <= |b| + (1 + g3) inv A',
+// A' = sum |P_j|.  n = d elements.
+CPB_DEV void logit_final(const double* dred, int nw, int d, double b, float inv, double* lstar, double* lbound) {
+    double wtot = 0.0, SS = 0.0, AP = 0.0;
+    for (int w2 = 0; w2 < nw; w2++) { wtot += dred[w2]; SS += dred[16 + w2]; AP += dred[32 + w2]; }
+    const double u = 5.9604644775390625e-08;  // 2^-24
+    const double n = (double)d;
+    const double g3 = 3.0 * u / (1.0 - 3.0 * u);
+    const double gam = n * u / (1.0 - n * u);
+    const double sc = (double)inv;
+    const double IA = sc * AP;
+    const double ab = fabs(b);
+    const double bound = u / (1.0 - u) * (n * ab + sc * SS + n * g3 * IA + n * gam * (ab + (1.0 + g3) * IA)) + g3 * IA;
+    *lstar = b + sc * wtot;
+    *lbound = bound * 1.0001 + 1e-10 * (ab + IA) + 1e-30;
 }
 
 // Workgroup-level body: expert e's logit + bound, and this workgroup's share
@@ -255,17 +248,20 @@ CPB_DEV_HOST inline size_t route_lds_bytes(int d) {
 // Thread t owns x[16t .. 16t+16): its x, norm weights and router weights
 // arrive in registers from one round of loads.  The gpt-oss sum of squares
 // (16 fma chains, chain q over x[16m + q], engine_gpt2.rs:710-726) runs in 16
-// lanes of wave 0 over a transposed LDS copy (chain q's elements contiguous);
-// the Qwen one (nt serial slices, engine_qwen2.rs:457-467) over a plain copy.
-// The router logit is the exact fp64 sum of the reference's fp32 products
-// with the prefix-sum error bound of router_logit, from one DPP scan.
+// lanes of wave 0 over a transposed LDS copy (chain q's elements
+// contiguous); the Qwen one (nt serial slices, engine_qwen2.rs:457-467) over
+// a plain copy.
+// The router logit is the fp64 sum of the unscaled products W_j * x_j * g_j
+// (one DPP scan, computed beside the sum-of-squares chain), scaled by the norm
+// scale once that is known; its bound covers every rounding of the
+// reference's fp32 path (see the bound below).
 CPB_DEV void route_expert(const RouteArgs& a, int e, int NEg, unsigned char* smem) {
     const int tid = threadIdx.x, nth = blockDim.x, lane = tid & 63, wv = tid >> 6, nw = nth >> 6;
     const int d = a.d;
-    const int S = route_xt_stride(d);
     float* xl = (float*)smem;                                  // transposed (gpt-oss) or plain (Qwen) x
     double* dred = (double*)(smem + route_lds_bytes(d) - sizeof(double) * 64 - 64);   // [64]
     float* sinv = (float*)(dred + 64);
+    RSTAMP_DECL;
     RSTAMP(0);
 
     const int j0 = tid * kRouteC;
@@ -283,61 +279,82 @@ CPB_DEV void route_expert(const RouteArgs& a, int e, int NEg, unsigned char* sme
 #pragma unroll
     for (int k = 0; k < 4; k++) gq[k] = __builtin_amdgcn_raw_buffer_load_b128(rg, off + 16 * k, 0, 0);
     const double b = a.router_b ? (double)a.router_b[e] : 0.0;
-    float xf[16];
+    float xf[16], gf[16], wf[16];
 #pragma unroll
-    for (int i = 0; i < 16; i++) xf[i] = act ? __uint_as_float(xv[i >> 2][i & 3]) : 0.0f;
+    for (int i = 0; i < 16; i++) {
+        xf[i] = act ? __uint_as_float(xv[i >> 2][i & 3]) : 0.0f;
+        gf[i] = use_g ? __uint_as_float(gq[i >> 2][i & 3]) : 1.0f;
+        wf[i] = act ? __uint_as_float(wq[i >> 2][i & 3]) : 0.0f;
+    }
     RSTAMP(1);
 
+    // ---- router logit, unscaled (the norm scale is applied at the end), so
+    // it runs beside the sum-of-squares chain instead of after it ----
+    LogitThread lt;
+    logit_phase1(wf, xf, gf, lt, dred);
+
     // ---- rmsnorm scale ----
-    float inv = 1.0f;
+    const int S = route_xt_stride(d);
     if (a.apply_norm) {
         if (a.norm == 0) {
-            // chain q's element m = x[16m + q] lives in thread m, register q
+            // chain q's element m = x[16m + q] lives in thread m, register q:
+            // transposed into LDS (chain q's elements contiguous)
             if (act) {
 #pragma unroll
                 for (int i = 0; i < 16; i++) xl[i * S + tid] = xf[i];
             }
-            __syncthreads();
-            if (wv == 0) {
-                const int nm = d / 16;
-                float acc = 0.0f;
-                if (lane < 16) {
-                    const float* row = xl + lane * S;
-                    int m = 0;
-                    for (; m + 16 <= nm; m += 16) {
-                        float4 t[4];
+            // zero padding past d/16: fma(0, 0, acc) leaves acc (>= 0) unchanged
+            for (int c = d / 16 + tid; c < S; c += nth) {
 #pragma unroll
-                        for (int u = 0; u < 4; u++) t[u] = *(const float4*)(row + m + 4 * u);
+                for (int i = 0; i < 16; i++) xl[i * S + c] = 0.0f;
+            }
+        } else if (act) {
 #pragma unroll
-                        for (int u = 0; u < 4; u++) {
-                            acc = fmaf(t[u].x, t[u].x, acc);
-                            acc = fmaf(t[u].y, t[u].y, acc);
-                            acc = fmaf(t[u].z, t[u].z, acc);
-                            acc = fmaf(t[u].w, t[u].w, acc);
-                        }
+            for (int k = 0; k < 4; k++) ((u32x4*)xl)[tid * 4 + k] = xv[k];
+        }
+    }
+    __syncthreads();
+    if (a.apply_norm && wv == 0) {
+        if (a.norm == 0) {
+            // lane q of wave 0 streams its row, every read issued ahead of
+            // the fma chain that consumes it
+            const int nm = d / 16;                   // <= 256
+            float acc = 0.0f;
+            const float* row = xl + (lane & 15) * S;
+            constexpr int G = 32;                    // values per group (8 reads)
+            float4 cur[G / 4], nxt[G / 4];
+#pragma unroll
+            for (int u = 0; u < G / 4; u++) cur[u] = *(const float4*)(row + 4 * u);
+            for (int m = 0; m < nm; m += G) {
+#pragma unroll
+                for (int u = 0; u < G / 4; u++) nxt[u] = *(const float4*)(row + m + G + 4 * u);
+#pragma unroll
+                for (int u = 0; u < G / 4; u++) {
+                    if (m + 4 * u < nm) {            // the padding reads as zero
+                        acc = fmaf(cur[u].x, cur[u].x, acc);
+                        acc = fmaf(cur[u].y, cur[u].y, acc);
+                        acc = fmaf(cur[u].z, cur[u].z, acc);
+                        acc = fmaf(cur[u].w, cur[u].w, acc);
                     }
-                    for (; m < nm; m++) { const float t = row[m]; acc = fmaf(t, t, acc); }
                 }
-                // chain q = 4v + l -> acc[v][l]; L[l] = (a0 + a1) + (a2 + a3); s = (L0 + L1) + (L2 + L3)
-                float c[16];
 #pragma unroll
-                for (int q = 0; q < 16; q++) c[q] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, acc), q));
-                float L[4];
-#pragma unroll
-                for (int l = 0; l < 4; l++) L[l] = (c[l] + c[4 + l]) + (c[8 + l] + c[12 + l]);
-                const float s = (L[0] + L[1]) + (L[2] + L[3]);
-                if (lane == 0) *sinv = 1.0f / sqrtf(s / (float)d + a.eps);
+                for (int u = 0; u < G / 4; u++) cur[u] = nxt[u];
             }
+            // chain q = 4v + l -> acc[v][l]; L[l] = (a0 + a1) + (a2 + a3); s = (L0 + L1) + (L2 + L3)
+            float c16[16];
+#pragma unroll
+            for (int q = 0; q < 16; q++) c16[q] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, acc), q));
+            float L[4];
+#pragma unroll
+            for (int l = 0; l < 4; l++) L[l] = (c16[l] + c16[4 + l]) + (c16[8 + l] + c16[12 + l]);
+            const float ssq = (L[0] + L[1]) + (L[2] + L[3]);
+            if (lane == 0) *sinv = 1.0f / sqrtf(ssq / (float)d + a.eps);
         } else {
-            if (act) {
-#pragma unroll
-                for (int k = 0; k < 4; k++) ((u32x4*)xl)[tid * 4 + k] = xv[k];
-            }
-            __syncthreads();
+            // nt serial slices, then a serial sum of the partials (nt <= 64)
             const int nt = a.norm_nt, base = d / nt, rem = d % nt;
             float ps = 0.0f;
-            if (tid < nt) {
-                const int s0 = tid * base + (tid < rem ? tid : rem), sz = base + (tid < rem ? 1 : 0);
+            if (lane < nt) {
+                const int s0 = lane * base + (lane < rem ? lane : rem), sz = base + (lane < rem ? 1 : 0);
                 int i = 0;
                 for (; i + 16 <= sz; i += 16) {
                     float t[16];
@@ -348,27 +365,29 @@ CPB_DEV void route_expert(const RouteArgs& a, int e, int NEg, unsigned char* sme
                 }
                 for (; i < sz; i++) { const float v = xl[s0 + i]; ps += v * v; }
             }
-            // serial sum of the nt partials (nt <= 64: all in wave 0)
-            if (wv == 0) {
-                float tot = 0.0f;
-                for (int k = 0; k < nt; k++) tot += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ps), k));
-                if (lane == 0) *sinv = 1.0f / sqrtf(tot / (float)d + a.eps);
-            }
+            float tot = 0.0f;
+            for (int k = 0; k < nt; k++) tot += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ps), k));
+            if (lane == 0) *sinv = 1.0f / sqrtf(tot / (float)d + a.eps);
         }
-        __syncthreads();
-        inv = *sinv;
     }
+    // meanwhile (waves 1.., and wave 0 after its chain): prefix sums of the
+    // unscaled products for the error bound
+    logit_phase2(lt, act, dred);
+    __syncthreads();
+    const float inv = a.apply_norm ? *sinv : 1.0f;
     RSTAMP(2);
+    if (tid == 0) {
+        double ls = 0.0, lb = 0.0;
+        logit_final(dred, nw, d, b, inv, &ls, &lb);
+        st_dev(a.lstar + e, ls);
+        st_dev(a.lbound + e, lb);
+    }
 
-    // ---- xn = (x * inv) * w in registers ----
+    // ---- xn = (x * inv) * w, and this workgroup's share of the activation
+    // quantisation ----
     float xn[16];
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-        const float g = __uint_as_float(gq[i >> 2][i & 3]);
-        xn[i] = !a.apply_norm ? xf[i] : use_g ? (xf[i] * inv) * g : xf[i] * inv;
-    }
-
-    // ---- activation quantisation (this workgroup's share) ----
+    for (int i = 0; i < 16; i++) xn[i] = !a.apply_norm ? xf[i] : use_g ? (xf[i] * inv) * gf[i] : xf[i] * inv;
     if (a.qk == 0) {
         // Q8 per 32-block (engine_gpt2.rs:691-699): threads 2b, 2b+1 hold block b
         float m = 0.0f;
@@ -426,47 +445,8 @@ CPB_DEV void route_expert(const RouteArgs& a, int e, int NEg, unsigned char* sme
         }
     }
     RSTAMP(3);
-
-    // ---- router logit of expert e: exact fp64 sum of the reference's fp32
-    // products and the bound u/(1-u) * (sum_k |S_k| + n*gamma_n*A) ----
-    float p[16];
-    double loc = 0.0, absp = 0.0;
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-        p[i] = act ? __fmul_rn(__uint_as_float(wq[i >> 2][i & 3]), xn[i]) : 0.0f;
-        loc += (double)p[i];
-        absp += fabs((double)p[i]);
-    }
-    const double incl = wave_scan_f64(loc);
-    if (lane == 63) dred[wv] = incl;
-    __syncthreads();
-    double woff = 0.0, wtot = 0.0;
-    for (int w2 = 0; w2 < nw; w2++) {
-        const double t = dred[w2];
-        if (w2 < wv) woff += t;
-        wtot += t;
-    }
-    double run = b + woff + (incl - loc);
-    double sabs = 0.0;
-#pragma unroll
-    for (int i = 0; i < 16; i++) { run += (double)p[i]; sabs += act ? fabs(run) : 0.0; }
-    const double ws = wave_total63_f64(sabs);
-    const double wa = wave_total63_f64(absp);
-    if (lane == 63) { dred[16 + wv] = ws; dred[32 + wv] = wa; }
-    __syncthreads();
-    RSTAMP(4);
-    if (tid == 0) {
-        double SS = 0.0, AP = 0.0;
-        for (int w2 = 0; w2 < nw; w2++) { SS += dred[16 + w2]; AP += dred[32 + w2]; }
-        const double u = 5.9604644775390625e-08;  // 2^-24
-        const double n = (double)d;
-        const double A = fabs(b) + AP;
-        const double gam = n * u / (1.0 - n * u);
-        const double bound = u / (1.0 - u) * (SS + n * gam * A);
-        st_dev(a.lstar + e, b + wtot);
-        st_dev(a.lbound + e, bound * 1.0001 + 1e-10 * A + 1e-30);
-    }
     RSTAMP(5);
+    RSTAMP_FLUSH;
 }
 
 
