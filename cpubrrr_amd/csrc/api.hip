@@ -88,7 +88,7 @@ struct cpb_moe {
     // staging for raw GGUF bytes at load time
     uint8_t* staging = nullptr;
     size_t staging_size = 0;
-    bool select_in_gateup = true;         // MXFP4 decode: top-k at the start of the gate/up kernel (CPB_SELECT_IN_ROUTE=1: in the route launch)
+    bool select_in_gateup = true;         // top-k at the start of the gate/up kernel (CPB_SELECT_IN_ROUTE=1: in the route launch)
     unsigned long long* d_stamps = nullptr;   // probe builds (CPB_DECODE_STAMPS): phase timestamps
     // grouped (n_tok > 1) MXFP4 path: per-token and per-pair scratch
     bool grouped = false;
@@ -268,9 +268,9 @@ int layer_token(cpb_moe_t* h, int layer, float* dx, int apply_norm, bool trace) 
     sa.lstar = h->lstar; sa.lbound = h->lbound; sa.router_w = L.router_w; sa.router_b = L.router_b; sa.xn = h->xn;
     sa.d = c.d; sa.n_expert = c.n_expert; sa.top_k = c.top_k;
     sa.ids = h->ids; sa.wts = h->wts; sa.logits = h->logits; sa.fallback = h->fallback;
-    // MXFP4 decode: the gate/up kernel selects at its start (no
-    // cross-workgroup hand-off inside the routing launch)
-    const bool sel_in_gu = h->mx && h->select_in_gateup;
+    // the gate/up kernel selects at its start (no cross-workgroup hand-off
+    // inside the routing launch)
+    const bool sel_in_gu = h->select_in_gateup;
     {
         Timer tm(h, 0);
         if (cpb::launch_route(&ra, &sa, sel_in_gu ? nullptr : h->counter, h->stream))
@@ -308,6 +308,11 @@ int layer_token(cpb_moe_t* h, int layer, float* dx, int apply_norm, bool trace) 
         cpb::KqArgs k{};
         k.gu = L.gu; k.dn = L.dn; k.down_type = c.wtype_down;
         k.xq = h->xq; k.xs = h->xsb; k.xsum = h->xsum; k.ids = h->ids; k.wts = h->wts;
+        if (sel_in_gu) {
+            k.sel.lstar = h->lstar; k.sel.lbound = h->lbound; k.sel.router_w = L.router_w; k.sel.router_b = L.router_b;
+            k.sel.xn = h->xn; k.sel.ne = c.n_expert; k.sel.k = c.top_k; k.sel.d = c.d;
+            k.sel.ids = h->ids; k.sel.wts = h->wts; k.sel.logits = h->logits; k.sel.fallback = h->fallback;
+        }
         k.d = c.d; k.dff = c.d_ff; k.top_k = c.top_k;
         k.hbuf = h->hbuf; k.hq = h->hq; k.hs = h->hsb; k.hsum = h->hsum; k.x = dx;
         k.gu_out = h->t_gu; k.gu_sums = h->t_gu_sums; k.dn_out = h->t_dn; k.dn_sums = h->t_dn_sums;

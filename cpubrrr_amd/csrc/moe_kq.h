@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include "moe_common.h"
+#include "select.h"
 
 namespace cpb {
 
@@ -13,8 +14,9 @@ struct KqArgs {
     const int8_t* xq;        // [d]   Q8_K activations
     const float* xs;         // [d/256]
     const int32_t* xsum;     // [d/32]
-    const int32_t* ids;      // [top_k]
+    const int32_t* ids;      // [top_k]  (selected by the gate/up kernel when sel.lstar is set)
     const float* wts;        // [top_k]
+    SelectIn sel;            // when set, every gate/up workgroup selects at its start and workgroup 0 publishes ids / wts
     int d, dff, top_k;
     float* hbuf;             // [top_k][dff] SiLU(gate) * up
     int8_t* hq;              // [top_k][dff]      (trace only: Q8_K of hbuf)

@@ -28,6 +28,8 @@
 #include "moe_common.h"
 #include "moe_kq.h"
 
+#include <algorithm>
+
 namespace cpb {
 
 constexpr int kQ4Units = 9;
@@ -132,7 +134,6 @@ __global__ __launch_bounds__(1024) void k_gateup_kq(KqArgs a) {
     const int lane = threadIdx.x & 63, q = uniform((int)(threadIdx.x >> 6));
     const int nth = blockDim.x;
     const int ei = blockIdx.x / T, t = blockIdx.x % T;
-    const int e = uniform(a.ids[ei]);
     int8_t* xl = (int8_t*)smem;                                  // [nsb][kXsPad]
     int32_t* xsl = (int32_t*)(smem + nsb * kXsPad);              // [nsb * 8]
     float* ysl = (float*)(xsl + nsb * 8);                        // [nsb]
@@ -147,6 +148,18 @@ __global__ __launch_bounds__(1024) void k_gateup_kq(KqArgs a) {
     for (int k = 0; k < 2; k++) xv[k] = __builtin_amdgcn_raw_buffer_load_b128(rx, (uint32_t)(threadIdx.x + k * nth) * 16, 0, 0);
     const uint32_t sv = __builtin_amdgcn_raw_buffer_load_b32(rs, threadIdx.x * 4, 0, 0);
     const uint32_t yv = __builtin_amdgcn_raw_buffer_load_b32(ry, threadIdx.x * 4, 0, 0);
+
+    // expert of this tile: selected here by wave 0 from the certified logits
+    // (its LDS scratch is used before the activations are stored)
+    int e;
+    if (a.sel.lstar) {
+        __shared__ Selection ssel;
+        if (q == 0) select_topk_wave(a.sel, smem, &ssel);
+        __syncthreads();
+        e = uniform(ssel.ids[ei]);
+    } else {
+        e = uniform(a.ids[ei]);
+    }
 
     // weights: this lane's (row, superblock); idle lanes (s >= nsb) read superblock 0
     const int s = 2 * q + (lane >> 5), r = lane & 31;
@@ -355,7 +368,8 @@ int launch_repack_kq_down(const uint8_t* down, u32x4* out, int ne, int d, int df
 int launch_gateup_kq(const KqArgs& a, bool trace, hipStream_t s) {
     const int nsb = a.d / 256;
     const int waves = (nsb + 1) / 2;
-    const size_t lds = (size_t)nsb * kXsPad + nsb * 8 * 4 + 32 * 4 + (size_t)nsb * 32 * 4;
+    size_t lds = (size_t)nsb * kXsPad + nsb * 8 * 4 + 32 * 4 + (size_t)nsb * 32 * 4;
+    if (a.sel.lstar) lds = std::max(lds, select_lds_bytes(a.sel.ne, a.sel.d));
     const dim3 grid(a.top_k * (a.dff / 16)), block(64 * waves);
     if (trace) launch(k_gateup_kq<true>, grid, block, lds, s, a);
     else launch(k_gateup_kq<false>, grid, block, lds, s, a);
