@@ -73,7 +73,6 @@ struct cpb_moe {
     float* xsb = nullptr;
     int32_t* xsum = nullptr;
     double *lstar = nullptr, *lbound = nullptr;
-    unsigned* counter = nullptr;          // route workgroup arrivals (zero between launches)
     float* logits = nullptr;
     int32_t* ids = nullptr;
     float* wts = nullptr;
@@ -88,7 +87,6 @@ struct cpb_moe {
     // staging for raw GGUF bytes at load time
     uint8_t* staging = nullptr;
     size_t staging_size = 0;
-    bool select_in_gateup = true;         // top-k at the start of the gate/up kernel (CPB_SELECT_IN_ROUTE=1: in the route launch)
     unsigned long long* d_stamps = nullptr;   // probe builds (CPB_DECODE_STAMPS): phase timestamps
     // grouped (n_tok > 1) MXFP4 path: per-token and per-pair scratch
     bool grouped = false;
@@ -264,17 +262,11 @@ int layer_token(cpb_moe_t* h, int layer, float* dx, int apply_norm, bool trace) 
     ra.xn = h->xn; ra.xq = h->xq; ra.xqn = h->xqn; ra.xsb = h->xsb; ra.xsum = h->xsum;
     ra.lstar = h->lstar; ra.lbound = h->lbound;
     ra.stamps = h->d_stamps;
-    cpb::SelectArgs sa{};
-    sa.lstar = h->lstar; sa.lbound = h->lbound; sa.router_w = L.router_w; sa.router_b = L.router_b; sa.xn = h->xn;
-    sa.d = c.d; sa.n_expert = c.n_expert; sa.top_k = c.top_k;
-    sa.ids = h->ids; sa.wts = h->wts; sa.logits = h->logits; sa.fallback = h->fallback;
-    // the gate/up kernel selects at its start (no cross-workgroup hand-off
-    // inside the routing launch)
-    const bool sel_in_gu = h->select_in_gateup;
+    // the route launch publishes certified logits; the gate/up kernel
+    // selects at its start (no cross-workgroup hand-off inside a launch)
     {
         Timer tm(h, 0);
-        if (cpb::launch_route(&ra, &sa, sel_in_gu ? nullptr : h->counter, h->stream))
-            return fail(CPB_ENODEV, "route launch failed");
+        if (cpb::launch_route(&ra, h->stream)) return fail(CPB_ENODEV, "route launch failed");
     }
     if (h->mx) {
         cpb::GateUpArgs g{};
@@ -282,7 +274,7 @@ int layer_token(cpb_moe_t* h, int layer, float* dx, int apply_norm, bool trace) 
         g.xq = h->xq; g.xqn = h->xqn; g.xsb = h->xsb;
         g.ids = h->ids;
         g.stamps = h->d_stamps;
-        if (sel_in_gu) {
+        {
             g.sel.lstar = h->lstar; g.sel.lbound = h->lbound; g.sel.router_w = L.router_w; g.sel.router_b = L.router_b;
             g.sel.xn = h->xn; g.sel.ne = c.n_expert; g.sel.k = c.top_k; g.sel.d = c.d;
             g.sel.ids = h->ids; g.sel.wts = h->wts; g.sel.logits = h->logits; g.sel.fallback = h->fallback;
@@ -308,7 +300,7 @@ int layer_token(cpb_moe_t* h, int layer, float* dx, int apply_norm, bool trace) 
         cpb::KqArgs k{};
         k.gu = L.gu; k.dn = L.dn; k.down_type = c.wtype_down;
         k.xq = h->xq; k.xs = h->xsb; k.xsum = h->xsum; k.ids = h->ids; k.wts = h->wts;
-        if (sel_in_gu) {
+        {
             k.sel.lstar = h->lstar; k.sel.lbound = h->lbound; k.sel.router_w = L.router_w; k.sel.router_b = L.router_b;
             k.sel.xn = h->xn; k.sel.ne = c.n_expert; k.sel.k = c.top_k; k.sel.d = c.d;
             k.sel.ids = h->ids; k.sel.wts = h->wts; k.sel.logits = h->logits; k.sel.fallback = h->fallback;
@@ -369,7 +361,7 @@ int cpb_moe_create(const cpb_moe_cfg* cfg, int device, cpb_moe_t** out) {
     const size_t d = cfg->d, ff = cfg->d_ff, k = cfg->top_k, ne = cfg->n_expert, T = cfg->max_tokens;
     int r;
     if ((r = dmalloc(&h->x, T * d)) || (r = dmalloc(&h->xn, d)) || (r = dmalloc(&h->xq, 2 * d + 8 * (d / 32))) ||
-        (r = dmalloc(&h->lstar, ne)) || (r = dmalloc(&h->lbound, ne)) || (r = dmalloc(&h->counter, 1)) ||
+        (r = dmalloc(&h->lstar, ne)) || (r = dmalloc(&h->lbound, ne)) ||
         (r = dmalloc(&h->logits, ne)) || (r = dmalloc(&h->ids, k)) || (r = dmalloc(&h->wts, k)) ||
         (r = dmalloc(&h->fallback, 1)) || (r = dmalloc(&h->hq, 2 * k * ff + 4 * (k * ff / 32))) || (r = dmalloc(&h->hsum, k * ff / 32)) || (r = dmalloc(&h->hbuf, k * ff)) ||
         (r = dmalloc(&h->params, param_slots(*cfg).per_layer * cfg->n_layer)))
@@ -398,12 +390,10 @@ int cpb_moe_create(const cpb_moe_cfg* cfg, int device, cpb_moe_t** out) {
             (r = dmalloc(&h->g_dnout, np * d)))
             return bail(r);
     }
-    if (const char* v = getenv("CPB_SELECT_IN_ROUTE")) h->select_in_gateup = v[0] == '0';
 #ifdef CPB_DECODE_STAMPS
     if ((r = dmalloc(&h->d_stamps, ((size_t)1 << 20) + 4096))) return bail(r);
 #endif
-    if (hipMemsetAsync(h->counter, 0, sizeof(unsigned), h->stream) != hipSuccess ||
-        hipMemsetAsync(h->fallback, 0, sizeof(int32_t), h->stream) != hipSuccess ||
+    if (hipMemsetAsync(h->fallback, 0, sizeof(int32_t), h->stream) != hipSuccess ||
         hipStreamSynchronize(h->stream) != hipSuccess)
         return bail(fail(CPB_ENODEV, "init memset failed"));
     *out = h;
@@ -682,7 +672,7 @@ void cpb_moe_destroy(cpb_moe_t* h) {
                      h->d_special};
     for (void* p : gbufs) hipFree(p);
     for (auto& L : h->layers) free_layer(L);
-    void* bufs[] = {h->params, h->x, h->xn, h->xq, h->lstar, h->lbound, h->counter, h->logits,
+    void* bufs[] = {h->params, h->x, h->xn, h->xq, h->lstar, h->lbound, h->logits,
                     h->ids, h->wts, h->fallback, h->hq, h->hsum, h->hbuf, h->t_gu, h->t_h,
                     h->t_dn, h->t_gu_sums, h->t_dn_sums, h->staging};
     for (void* p : bufs) if (p) hipFree(p);

@@ -136,17 +136,24 @@ __global__ __launch_bounds__(256) void k_router_batch(GroupedArgs a) {
     }
 }
 
-// ---- 3. top-k + softmax, one wavefront per token ----
+// ---- 3. top-k + softmax, one wavefront per token (the decode kernels'
+// selection, so ids and weights are per-token decode's bit for bit) ----
 __global__ __launch_bounds__(64) void k_select_batch(GroupedArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ Selection sel;
     const int lane = threadIdx.x, t = blockIdx.x;
-    select_experts_wave(a.lstar + (size_t)t * a.ne, a.lbound + (size_t)t * a.ne, a.ne, a.k, a.router_w, a.router_b,
-                        a.xn + (size_t)t * a.d, a.d, (double*)smem, &sel, a.logits + (size_t)t * a.ne);
+    SelectIn si{};
+    si.lstar = a.lstar + (size_t)t * a.ne;
+    si.lbound = a.lbound + (size_t)t * a.ne;
+    si.router_w = a.router_w;
+    si.router_b = a.router_b;
+    si.xn = a.xn + (size_t)t * a.d;
+    si.ne = a.ne; si.k = a.k; si.d = a.d;
+    si.logits = a.logits + (size_t)t * a.ne;      // written by every workgroup: one per token
+    select_topk_wave(si, smem, &sel, true);
     if (lane < a.k) {
         a.ids[(size_t)t * a.k + lane] = sel.ids[lane];
         a.wts[(size_t)t * a.k + lane] = sel.wts[lane];
-        a.logits[(size_t)t * a.ne + sel.ids[lane]] = sel.logit[lane];
     }
     if (lane == 0) a.fallback[t] = sel.fallback;
 }
@@ -435,7 +442,7 @@ int launch_grouped_layer(const GroupedArgs& a, bool trace, hipStream_t s) {
     const int nt = a.n_tok;
     launch(k_prep_batch, dim3(nt), dim3(256), sizeof(float) * (2 * a.d + 64), s, a);
     launch(k_router_batch, dim3(a.ne, (nt + kRouteTok - 1) / kRouteTok), dim3(256), sizeof(double) * 64, s, a);
-    launch(k_select_batch, dim3(nt), dim3(64), sizeof(double) * 4 * a.ne + sizeof(float) * a.d + 64, s, a);
+    launch(k_select_batch, dim3(nt), dim3(64), select_lds_bytes(a.ne, a.d), s, a);
     launch(k_group, dim3(1), dim3(1024), 0, s, a);
     const dim3 ggu(a.max_tiles, (a.dff / 32 + 3) / 4), gdn(a.max_tiles, (a.d / 32 + 7) / 8);
     const size_t lds_gu = kStageBytes;         // >= the 16 KB epilogue exchange

@@ -19,28 +19,13 @@ struct RouteArgs {
     int8_t* xqn;             // [d]  negated xq
     float* xsb;              // [d/32] or [d/256]
     int32_t* xsum;           // [d/32] (qk == 1)
-    double* lstar;           // [ne] exact fp64 logit of the reference's fp32 products
+    double* lstar;           // [ne] fp64 logit (route_dev.h)
     double* lbound;          // [ne] bound on |reference serial fp32 logit - lstar|
     unsigned long long* stamps;  // probe builds (CPB_DECODE_STAMPS) only: [ne][16] phase clocks
 };
 
-struct SelectArgs {
-    const double* lstar;
-    const double* lbound;
-    const float* router_w;   // exact fallback only
-    const float* router_b;
-    const float* xn;
-    int d, n_expert, top_k;
-    int32_t* ids;            // [top_k]
-    float* wts;              // [top_k]
-    float* logits;           // [ne]
-    int32_t* fallback;       // [1]
-};
-
-// Routing and selection in one launch; `arrive` is a zero-initialised
-// counter that the launch leaves at zero.  With arrive null the launch only
-// publishes lstar / lbound (a later kernel selects).
-int launch_route(const RouteArgs* a, const SelectArgs* sa, unsigned* arrive, hipStream_t s);
-int launch_select(const SelectArgs* a, hipStream_t s);
+// Routing: expert e's certified logit (lstar / lbound) and the activation
+// quantisation, one workgroup per expert.
+int launch_route(const RouteArgs* a, hipStream_t s);
 
 }  // namespace cpb

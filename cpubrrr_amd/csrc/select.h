@@ -1,9 +1,8 @@
 // select.h -- top-k expert selection from certified router logits (one
-// wavefront, LDS scratch, no cross-workgroup synchronisation).
+// wavefront, registers; LDS only on the exact path).
 //
-// Inputs per expert e: Ls[e] = exact (fp64) sum of the reference's fp32
-// router products plus bias, Bs[e] = bound on |reference serial fp32 sum -
-// Ls[e]| (k_route).  The reference selects by descending value with the
+// Inputs per expert e: Ls[e] = fp64 logit, Bs[e] = bound on |reference serial
+// fp32 logit - Ls[e]| (k_route).  The reference selects by descending value with the
 // lowest index winning ties (engine_gpt2.rs:852-867 insertion with strict
 // comparisons; engine_qwen2.rs:403-410 stable sort), then takes a softmax
 // over the k selected logits.  If every selected expert's interval lies
@@ -36,12 +35,11 @@ CPB_DEV void exact_reselect(double* sL, const double* sH, int* sSel, int NE, int
     double tau = 1e300;
     for (int i = 0; i < K; i++) { const int e = sSel[i]; tau = fmin(tau, sL[e] - (sH[e] - sL[e])); }
     __builtin_amdgcn_wave_barrier();
-    // xn staged in LDS with coherent 16-byte loads (it may have been written
-    // by other workgroups of this launch), then each candidate lane runs the
+    // xn staged in LDS, then each candidate lane runs the
     // reference's serial chain with its router row fetched 64 weights ahead
     {
         const __amdgpu_buffer_rsrc_t r = buf_rsrc(xn, (uint32_t)d * 4);
-        for (int i = lane; i < d / 4; i += 64) ((u32x4*)xst)[i] = ld_dev16(r, (uint32_t)i * 16);
+        for (int i = lane; i < d / 4; i += 64) ((u32x4*)xst)[i] = __builtin_amdgcn_raw_buffer_load_b128(r, (uint32_t)i * 16, 0, 0);
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -89,119 +87,6 @@ CPB_DEV void exact_reselect(double* sL, const double* sH, int* sSel, int NE, int
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
-
-// Executed by one wavefront (64 lanes).  lds: 4*NE doubles + d floats of
-// scratch (the floats only for the exact fallback).
-// Lane l holds experts l, l+64, ... (NE <= 256) in registers; the top-k come
-// from k rounds of wave-wide argmax (cross-lane shuffles, no LDS round
-// trips), the certification from one wave-wide max.  logits_out (optional)
-// receives the fp32 value of every expert's exact logit.  Outputs ids / logit
-// / wts in rank order into `out` (valid in every lane after the call).
-CPB_DEV void select_experts_wave(const double* __restrict__ Ls, const double* __restrict__ Bs, int NE, int K,
-                                 const float* __restrict__ router_w, const float* __restrict__ router_b,
-                                 const float* __restrict__ xn, int d, double* lds, Selection* out,
-                                 float* logits_out = nullptr, unsigned long long* stamps = nullptr) {
-#ifdef CPB_DECODE_STAMPS
-#define SSTAMP(i) do { if (stamps && (threadIdx.x & 63) == 0) stamps[i] = wall_clock64(); } while (0)
-#else
-#define SSTAMP(i) do { (void)stamps; } while (0)
-#endif
-    const int lane = threadIdx.x & 63;
-    double* sL = lds;            // [NE] values used for ranking
-    double* sH = lds + NE;       // [NE] upper bounds
-    int* sSel = (int*)(lds + 3 * NE);        // [8] expert at rank i
-    // one coherent round trip for all values
-    double lv[4], bv[4];
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const int e = lane + 64 * k;
-        lv[k] = e < NE ? ld_dev(Ls + e) : 0.0;
-        bv[k] = e < NE ? ld_dev(Bs + e) : 0.0;
-    }
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const int e = lane + 64 * k;
-        if (e < NE) {
-            sL[e] = lv[k];
-            sH[e] = lv[k] + bv[k];
-            if (logits_out) logits_out[e] = (float)lv[k];
-        }
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    SSTAMP(0);
-    // K rounds of wave-wide argmax over the register values: descending,
-    // lowest index first among equal values (the reference's strict insertion)
-    unsigned taken = 0;                    // bit k: expert lane + 64k already selected
-    for (int i = 0; i < K; i++) {
-        double best = -__builtin_inf();
-#pragma unroll
-        for (int k = 0; k < 4; k++)
-            if (lane + 64 * k < NE && !((taken >> k) & 1u)) best = fmax(best, lv[k]);
-        best = wave_max_f64(best);
-        int bi = 0x7fffffff;
-#pragma unroll
-        for (int k = 3; k >= 0; k--) {
-            const uint64_t m = __ballot(lane + 64 * k < NE && !((taken >> k) & 1u) && lv[k] == best);
-            if (m) bi = 64 * k + __builtin_ctzll(m);
-        }
-        if (lane == 0) sSel[i] = bi;
-        if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
-    }
-    SSTAMP(1);
-    // certification: the expert at rank r < K must lie strictly above every
-    // expert ranked after it, i.e. lo_r > max(hi of ranks r+1..K-1, hi of
-    // every unselected expert)
-    double mu = -1e300;
-#pragma unroll
-    for (int k = 0; k < 4; k++)
-        if (lane + 64 * k < NE && !((taken >> k) & 1u)) mu = fmax(mu, lv[k] + bv[k]);
-    mu = wave_max_f64(mu);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    bool bad = false;
-    {
-        double suffix = mu;
-        for (int i = K - 1; i >= 0; i--) {
-            const int e = __builtin_amdgcn_readfirstlane(sSel[i]);
-            const int src = e & 63, kk = e >> 6;
-            const double l = readlane_f64(kk == 0 ? lv[0] : kk == 1 ? lv[1] : kk == 2 ? lv[2] : lv[3], src);
-            const double b = readlane_f64(kk == 0 ? bv[0] : kk == 1 ? bv[1] : kk == 2 ? bv[2] : bv[3], src);
-            if (!(l - b > suffix)) bad = true;
-            suffix = fmax(suffix, l + b);
-        }
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    const bool ok = !__any(bad);
-    SSTAMP(2);
-    if (!ok) exact_reselect(sL, sH, sSel, NE, K, router_w, router_b, xn, d, (float*)(lds + 4 * NE));
-    SSTAMP(3);
-    // softmax over the k selected, reference order: ex_i = exp(l_i - l_0)
-    // (lane i), then the serial sum ex_0 + ex_1 + ... (every lane)
-    const int mi = lane < K ? lane : 0;
-    const int me = sSel[mi];
-    const float ml = (float)sL[me];
-    const float l0 = (float)sL[sSel[0]];
-    const float ex = expf(ml - l0);
-    float wsum = 0.0f;
-    for (int i = 0; i < K; i++) wsum += __shfl(ex, i);
-    const float wt = ex / wsum;
-    if (lane < K) {
-        out->ids[lane] = me;
-        out->logit[lane] = ml;
-        out->wts[lane] = wt;
-    }
-    if (lane == 0) out->fallback = ok ? 0 : 1;
-    SSTAMP(4);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
 
 // Selection inputs and outputs for a kernel that selects at its own start
 // (the routing kernel published lstar / lbound before this launch began, so
@@ -274,7 +159,7 @@ CPB_DEV void select_exact_path(unsigned char* lds, int NE, int K, const float* r
 // ranking that truncation made wrong cannot pass it, and then the exact path
 // (the reference's serial logits) decides.  Softmax over the k in the
 // reference's order.  Writes *out (LDS) from lanes < K.
-CPB_DEV void select_topk_wave(const SelectIn& s, unsigned char* lds, Selection* out) {
+CPB_DEV void select_topk_wave(const SelectIn& s, unsigned char* lds, Selection* out, bool publish_logits = false) {
     const int lane = threadIdx.x & 63;
     const int NE = s.ne, K = s.k;
     double lv[4], bv[4];
@@ -349,8 +234,17 @@ CPB_DEV void select_topk_wave(const SelectIn& s, unsigned char* lds, Selection* 
         out->wts[lane] = wt;
     }
     if (lane == 0) out->fallback = bad ? 1 : 0;
-    // trace outputs and the routed ids / weights for later launches
-    if (blockIdx.x == 0 && blockIdx.y == 0) {
+    // trace outputs and the routed ids / weights for later launches (by one
+    // workgroup, or by this one when it alone selects for its token)
+    if (publish_logits) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int e = lane + 64 * j;
+            if (e < NE) s.logits[e] = lf[j];
+        }
+        __builtin_amdgcn_wave_barrier();
+        if (lane < K) s.logits[my_e] = my_l;
+    } else if (blockIdx.x == 0 && blockIdx.y == 0) {
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const int e = lane + 64 * j;
