@@ -36,7 +36,7 @@
 namespace cpb {
 
 template <bool TRACE>
-__global__ __launch_bounds__(128 * kMaxParts) void k_gateup_mx(GateUpArgs a) {
+__global__ __launch_bounds__(128 * kMaxParts) __attribute__((amdgpu_waves_per_eu(6))) void k_gateup_mx(GateUpArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     const int P = a.nparts, W = 2 * P;
     const int lane = threadIdx.x & 63;

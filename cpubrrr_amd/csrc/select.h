@@ -15,6 +15,9 @@
 
 namespace cpb {
 
+// candidates whose exact serial logits are computed side by side
+constexpr int kExactGroup = 4;
+
 struct Selection {
     int ids[8];
     float logit[8];     // fp32 logits of the selected experts, in rank order
@@ -27,56 +30,72 @@ struct Selection {
 // reaches the lowest lower bound of the provisional top-k, then rank those
 // exactly (descending, lowest index first).  sL / sH: LDS values and upper
 // bounds of all NE experts; sSel: LDS [K] provisional choice, overwritten;
-// xst: LDS scratch of d floats.  One wavefront.
+// pst: LDS scratch of kExactGroup * (d + 4) floats.  One wavefront.
 CPB_DEV void exact_reselect(double* sL, const double* sH, int* sSel, int NE, int K, const float* __restrict__ router_w,
-                            const float* __restrict__ router_b, const float* __restrict__ xn, int d, float* xst) {
+                            const float* __restrict__ router_b, const float* __restrict__ xn, int d, float* pst) {
     const int lane = threadIdx.x & 63;
     // candidates: intervals reaching the lowest lower bound of the selected
     double tau = 1e300;
     for (int i = 0; i < K; i++) { const int e = sSel[i]; tau = fmin(tau, sL[e] - (sH[e] - sL[e])); }
-    __builtin_amdgcn_wave_barrier();
-    // xn staged in LDS, then each candidate lane runs the
-    // reference's serial chain with its router row fetched 64 weights ahead
-    {
-        const __amdgpu_buffer_rsrc_t r = buf_rsrc(xn, (uint32_t)d * 4);
-        for (int i = lane; i < d / 4; i += 64) ((u32x4*)xst)[i] = __builtin_amdgcn_raw_buffer_load_b128(r, (uint32_t)i * 16, 0, 0);
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    for (int e = lane; e < NE; e += 64) {
-        double v = -1e300;
-        if (sH[e] >= tau) {
-            float acc = router_b ? router_b[e] : 0.0f;
-            const float* Wr = router_w + (size_t)e * d;
-            // kept small: this path is rare and must not raise the register
-            // budget of the kernels that embed it
-            constexpr int kU = 4;
-            float4 w4[kU], n4[kU];
-#pragma unroll
-            for (int u = 0; u < kU; u++) w4[u] = 4 * u < d ? *(const float4*)(Wr + 4 * u) : float4{0, 0, 0, 0};
-            for (int j0 = 0; j0 < d; j0 += 4 * kU) {
-                // next chunk requested before this one is consumed
-#pragma unroll
-                for (int u = 0; u < kU; u++)
-                    n4[u] = j0 + 4 * kU + 4 * u < d ? *(const float4*)(Wr + j0 + 4 * kU + 4 * u) : float4{0, 0, 0, 0};
-#pragma unroll
-                for (int u = 0; u < kU; u++) {
-                    if (j0 + 4 * u >= d) break;
-                    const float* w = (const float*)&w4[u];
-#pragma unroll
-                    for (int c = 0; c < 4; c++) acc = __fadd_rn(acc, __fmul_rn(w[c], xst[j0 + 4 * u + c]));
-                }
-#pragma unroll
-                for (int u = 0; u < kU; u++) w4[u] = n4[u];
-            }
-            v = (double)acc;
+    // the others can never reach the top k
+    for (int e = lane; e < NE; e += 64)
+        if (!(sH[e] >= tau)) sL[e] = -1e300;
+    const __amdgpu_buffer_rsrc_t rx = buf_rsrc(xn, (uint32_t)d * 4);
+    const int stride = d + 4;                      // spreads the chain lanes over the LDS banks
+    // candidates in groups of kExactGroup: the wave writes each candidate's
+    // fp32 products W[j]*xn[j] to LDS (coalesced row loads), then lane c runs
+    // candidate c's serial chain acc = b; acc += p_j over them
+    int e_next = 0;
+    for (;;) {
+        static_assert(kExactGroup == 4, "group of four named candidates");
+        int g0 = 0, g1 = 0, g2 = 0, g3 = 0, ng = 0;
+        for (; e_next < NE && ng < kExactGroup; e_next++) {
+            if (!(sH[e_next] >= tau)) continue;
+            if (ng == 0) g0 = e_next; else if (ng == 1) g1 = e_next; else if (ng == 2) g2 = e_next; else g3 = e_next;
+            ng++;
         }
-        sL[e] = v;
+        if (ng == 0) break;
+        for (int c = 0; c < ng; c++) {
+            const int ec = c == 0 ? g0 : c == 1 ? g1 : c == 2 ? g2 : g3;
+            const __amdgpu_buffer_rsrc_t rw = buf_rsrc(router_w + (size_t)ec * d, (uint32_t)d * 4);
+            for (int j = 4 * lane; j < d; j += 256) {
+                const u32x4 w4 = __builtin_amdgcn_raw_buffer_load_b128(rw, (uint32_t)j * 4, 0, 0);
+                const u32x4 x4 = __builtin_amdgcn_raw_buffer_load_b128(rx, (uint32_t)j * 4, 0, 0);
+                float4 p4;
+                p4.x = __fmul_rn(__uint_as_float(w4[0]), __uint_as_float(x4[0]));
+                p4.y = __fmul_rn(__uint_as_float(w4[1]), __uint_as_float(x4[1]));
+                p4.z = __fmul_rn(__uint_as_float(w4[2]), __uint_as_float(x4[2]));
+                p4.w = __fmul_rn(__uint_as_float(w4[3]), __uint_as_float(x4[3]));
+                *(float4*)(pst + c * stride + j) = p4;
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (lane < ng) {
+            const int e = lane == 0 ? g0 : lane == 1 ? g1 : lane == 2 ? g2 : g3;
+            const float* pr = pst + lane * stride;
+            float acc = router_b ? router_b[e] : 0.0f;
+            int j = 0;
+            for (; j + 32 <= d; j += 32) {
+                float4 v[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++) v[u] = *(const float4*)(pr + j + 4 * u);
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    acc = __fadd_rn(acc, v[u].x);
+                    acc = __fadd_rn(acc, v[u].y);
+                    acc = __fadd_rn(acc, v[u].z);
+                    acc = __fadd_rn(acc, v[u].w);
+                }
+            }
+            for (; j < d; j++) acc = __fadd_rn(acc, pr[j]);
+            sL[e] = (double)acc;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     for (int e = lane; e < NE; e += 64) {
         const double v = sL[e];
         int r = 0;
@@ -104,7 +123,7 @@ struct SelectIn {
     int32_t* fallback;       // [1]
 };
 // LDS bytes select_topk_wave may use (its exact fallback)
-CPB_DEV_HOST_INLINE size_t select_lds_bytes(int ne, int d) { return sizeof(double) * 2 * ne + 64 + sizeof(float) * d; }
+CPB_DEV_HOST_INLINE size_t select_lds_bytes(int ne, int d) { return sizeof(double) * 2 * ne + 64 + sizeof(float) * kExactGroup * (d + 4); }
 
 // Wave-wide maximum of a 32-bit unsigned value via DPP (quad swaps, half-row
 // and row mirrors, row broadcasts 15 / 31), returned wave-uniform.
