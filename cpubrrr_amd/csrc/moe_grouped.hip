@@ -299,9 +299,11 @@ CPB_DEV void load_window(const u32x4* p, size_t stride, u32x4* wv) {
     for (int u = 0; u < kUnits; u++) wv[u] = __builtin_nontemporal_load(p + (size_t)u * stride);
 }
 
-// The k-part loop shared by the two grouped GEMMs: per k-part the workgroup
-// stages the tile's activations in LDS; each wave's next 16-unit weight
-// window is requested before the current one is consumed.  Returns the row
+// The k-part loop shared by the two grouped GEMMs.  Two LDS staging buffers
+// alternate: the next k-part's activations and weight window are requested
+// before the current one is computed, so their latency hides behind the
+// MFMAs, and one barrier per k-part suffices (buffer q & 1 is rewritten two
+// iterations after it was read, past the next barrier).  Returns the row
 // totals (k-parts added in order, as the decode kernels do).
 template <bool TRACE>
 CPB_DEV v16f grouped_parts(const u32x4* wbase, size_t stride, int P, unsigned char* smem, const uint8_t* img,
@@ -309,22 +311,26 @@ CPB_DEV v16f grouped_parts(const u32x4* wbase, size_t stride, int P, unsigned ch
     const size_t part = (size_t)kUnits * stride;
     u32x4 wv[kUnits], wn[kUnits];
     load_window(wbase, stride, wv);
+    StageRegs g = stage_load(img, sc, rows, nbk, 0, src);
     v16f tot = {};
     for (int q = 0; q < P; q++) {
-        const StageRegs g = stage_load(img, sc, rows, nbk, q, src);
-        stage_store(smem, g);
+        unsigned char* st = smem + (q & 1) * kStageBytes;
+        stage_store(st, g);
         __syncthreads();
-        if (q + 1 < P) load_window(wbase + (size_t)(q + 1) * part, stride, wn);
+        if (q + 1 < P) {
+            load_window(wbase + (size_t)(q + 1) * part, stride, wn);
+            g = stage_load(img, sc, rows, nbk, q + 1, src);
+        }
         v16f acc0, acc1;
-        part_mfma<TRACE>(wv, smem, lane, q, nbk, tb, nbk, trace_ok, acc0, acc1);
+        part_mfma<TRACE>(wv, st, lane, q, nbk, tb, nbk, trace_ok, acc0, acc1);
 #pragma unroll
         for (int r = 0; r < 16; r++) tot[r] += acc0[r];
 #pragma unroll
         for (int r = 0; r < 16; r++) tot[r] += acc1[r];
-        __syncthreads();
 #pragma unroll
         for (int u = 0; u < kUnits; u++) wv[u] = wn[u];
     }
+    __syncthreads();             // callers reuse the LDS
     return tot;
 }
 
@@ -445,13 +451,13 @@ int launch_grouped_layer(const GroupedArgs& a, bool trace, hipStream_t s) {
     launch(k_select_batch, dim3(nt), dim3(64), select_lds_bytes(a.ne, a.d), s, a);
     launch(k_group, dim3(1), dim3(1024), 0, s, a);
     const dim3 ggu(a.max_tiles, (a.dff / 32 + 3) / 4), gdn(a.max_tiles, (a.d / 32 + 7) / 8);
-    const size_t lds_gu = kStageBytes;         // >= the 16 KB epilogue exchange
+    const size_t lds = 2 * kStageBytes;        // two staging buffers (>= the 16 KB epilogue exchange)
     if (trace) {
-        launch(k_gateup_grouped<true>, ggu, dim3(512), lds_gu, s, a);
-        launch(k_down_grouped<true>, gdn, dim3(512), (size_t)kStageBytes, s, a);
+        launch(k_gateup_grouped<true>, ggu, dim3(512), lds, s, a);
+        launch(k_down_grouped<true>, gdn, dim3(512), lds, s, a);
     } else {
-        launch(k_gateup_grouped<false>, ggu, dim3(512), lds_gu, s, a);
-        launch(k_down_grouped<false>, gdn, dim3(512), (size_t)kStageBytes, s, a);
+        launch(k_gateup_grouped<false>, ggu, dim3(512), lds, s, a);
+        launch(k_down_grouped<false>, gdn, dim3(512), lds, s, a);
     }
     launch(k_combine_batch, dim3(nt), dim3(256), 0, s, a);
     return hipGetLastError() == hipSuccess ? 0 : -19;
