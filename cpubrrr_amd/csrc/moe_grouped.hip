@@ -334,19 +334,37 @@ CPB_DEV v16f grouped_parts(const u32x4* wbase, size_t stride, int P, unsigned ch
     return tot;
 }
 
+// XCD-aware work order of the grouped GEMMs.  Work item w = (row group
+// w / ntiles, token tile w % ntiles); the workgroups of a launch are dealt to
+// the 8 XCDs round robin (workgroup L runs on XCD L % 8, in order of L), so
+// XCD x takes the contiguous range of items [x * per, (x + 1) * per): the
+// token tiles of one expert and row group then run back to back on one XCD
+// and re-read that weight slice from its L2 instead of HBM.  Returns false for
+// workgroups past the last item.
+CPB_DEV bool grouped_item(int ntiles, int ngroups, int* tile, int* group) {
+    const int L = blockIdx.x, total = ntiles * ngroups;
+    const int per = (total + 7) / 8;
+    const int slot = L >> 3, w = (L & 7) * per + slot;
+    if (slot >= per || w >= total) return false;
+    *group = w / ntiles;
+    *tile = w % ntiles;
+    return true;
+}
+
 // ---- 5. grouped gate/up + SwiGLU-OAI + Q8 (+ image of h) ----
-// grid (max_tiles, ceil(dff/32 / 4)); 8 waves: wave w = row tile w/2 of this
-// group, gate (w even) or up (w odd).
+// one workgroup per (token tile, group of 4 row tiles) (grouped_item); 8
+// waves: wave w = row tile w/2 of the group, gate (w even) or up (w odd).
 template <bool TRACE>
 __global__ __launch_bounds__(512) void k_gateup_grouped(GroupedArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ int src[32];
-    if ((int)blockIdx.x >= *a.ntiles) return;
-    const int4 tl = a.tiles[blockIdx.x];
+    const int T = a.dff / 32, P = a.parts_gu, nb = a.nb;
+    int tile, grp;
+    if (!grouped_item(uniform(*a.ntiles), (T + 3) / 4, &tile, &grp)) return;
+    const int4 tl = a.tiles[tile];
     const int e = uniform(tl.x), start = uniform(tl.y), cnt = uniform(tl.z);
     const int lane = threadIdx.x & 63, w = uniform((int)(threadIdx.x >> 6));
-    const int T = a.dff / 32, P = a.parts_gu, nb = a.nb;
-    const int rt = blockIdx.y * 4 + (w >> 1), isup = w & 1;
+    const int rt = grp * 4 + (w >> 1), isup = w & 1;
     const bool live = rt < T;
     if (threadIdx.x < 32) src[threadIdx.x] = (int)threadIdx.x < cnt ? a.sorted[start + threadIdx.x] / a.k : -1;
     __syncthreads();
@@ -396,17 +414,18 @@ __global__ __launch_bounds__(512) void k_gateup_grouped(GroupedArgs a) {
 }
 
 // ---- 6. grouped down (+ bias) into dnout ----
-// grid (max_tiles, ceil(d/32 / 8)); 8 waves = 8 row tiles of 32 rows.
+// one workgroup per (token tile, group of 8 row tiles of 32 rows) (grouped_item).
 template <bool TRACE>
 __global__ __launch_bounds__(512) void k_down_grouped(GroupedArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ int src[32];
-    if ((int)blockIdx.x >= *a.ntiles) return;
-    const int4 tl = a.tiles[blockIdx.x];
+    int tile, grp;
+    if (!grouped_item(uniform(*a.ntiles), (a.d / 32 + 7) / 8, &tile, &grp)) return;
+    const int4 tl = a.tiles[tile];
     const int e = uniform(tl.x), start = uniform(tl.y), cnt = uniform(tl.z);
     const int lane = threadIdx.x & 63, w = uniform((int)(threadIdx.x >> 6));
     const int RTv = 64 / a.k, Tv = a.d / RTv, P = a.parts_dn, nbf = a.nbf;
-    const int rt = blockIdx.y * 8 + w;
+    const int rt = grp * 8 + w;
     const bool live = rt < a.d / 32;
     if (threadIdx.x < 32) src[threadIdx.x] = (int)threadIdx.x < cnt ? a.sorted[start + threadIdx.x] : -1;
     __syncthreads();
@@ -450,7 +469,10 @@ int launch_grouped_layer(const GroupedArgs& a, bool trace, hipStream_t s) {
     launch(k_router_batch, dim3(a.ne, (nt + kRouteTok - 1) / kRouteTok), dim3(256), sizeof(double) * 64, s, a);
     launch(k_select_batch, dim3(nt), dim3(64), select_lds_bytes(a.ne, a.d), s, a);
     launch(k_group, dim3(1), dim3(1024), 0, s, a);
-    const dim3 ggu(a.max_tiles, (a.dff / 32 + 3) / 4), gdn(a.max_tiles, (a.d / 32 + 7) / 8);
+    // one workgroup per (token tile, row group), dealt out by grouped_item:
+    // 8 slots per XCD round, enough for the largest tile count
+    const int ngu = a.max_tiles * ((a.dff / 32 + 3) / 4), ndn = a.max_tiles * ((a.d / 32 + 7) / 8);
+    const dim3 ggu((ngu + 7) / 8 * 8), gdn((ndn + 7) / 8 * 8);
     const size_t lds = 2 * kStageBytes;        // two staging buffers (>= the 16 KB epilogue exchange)
     if (trace) {
         launch(k_gateup_grouped<true>, ggu, dim3(512), lds, s, a);
