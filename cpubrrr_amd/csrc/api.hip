@@ -69,7 +69,8 @@ struct cpb_moe {
     float* params = nullptr;              // per-layer router / norm / bias parameters (one arena)
     float* x = nullptr;
     float* xn = nullptr;
-    int8_t *xq = nullptr, *xqn = nullptr;
+    int8_t* xq = nullptr;
+    uint8_t* ximg = nullptr;
     float* xsb = nullptr;
     int32_t* xsum = nullptr;
     double *lstar = nullptr, *lbound = nullptr;
@@ -259,7 +260,7 @@ int layer_token(cpb_moe_t* h, int layer, float* dx, int apply_norm, bool trace) 
     ra.d = c.d; ra.n_expert = c.n_expert; ra.top_k = c.top_k;
     ra.norm = c.norm; ra.norm_nt = c.norm_nt; ra.apply_norm = apply_norm; ra.eps = c.rms_eps;
     ra.qk = h->mx ? 0 : 1;
-    ra.xn = h->xn; ra.xq = h->xq; ra.xqn = h->xqn; ra.xsb = h->xsb; ra.xsum = h->xsum;
+    ra.xn = h->xn; ra.xq = h->xq; ra.ximg = h->ximg; ra.xsb = h->xsb; ra.xsum = h->xsum;
     ra.lstar = h->lstar; ra.lbound = h->lbound;
     ra.stamps = h->d_stamps;
     // the route launch publishes certified logits; the gate/up kernel
@@ -271,7 +272,7 @@ int layer_token(cpb_moe_t* h, int layer, float* dx, int apply_norm, bool trace) 
     if (h->mx) {
         cpb::GateUpArgs g{};
         g.w = L.gu; g.gate_b = L.gate_b; g.up_b = L.up_b;
-        g.xq = h->xq; g.xqn = h->xqn; g.xsb = h->xsb;
+        g.ximg = h->ximg; g.xsb = h->xsb;
         g.ids = h->ids;
         g.stamps = h->d_stamps;
         {
@@ -360,18 +361,17 @@ int cpb_moe_create(const cpb_moe_cfg* cfg, int device, cpb_moe_t** out) {
     h->stream = h->own;
     const size_t d = cfg->d, ff = cfg->d_ff, k = cfg->top_k, ne = cfg->n_expert, T = cfg->max_tokens;
     int r;
-    if ((r = dmalloc(&h->x, T * d)) || (r = dmalloc(&h->xn, d)) || (r = dmalloc(&h->xq, 2 * d + 8 * (d / 32))) ||
+    if ((r = dmalloc(&h->x, T * d)) || (r = dmalloc(&h->xn, d)) || (r = dmalloc(&h->xq, 3 * d + 8 * (d / 32))) ||
         (r = dmalloc(&h->lstar, ne)) || (r = dmalloc(&h->lbound, ne)) ||
         (r = dmalloc(&h->logits, ne)) || (r = dmalloc(&h->ids, k)) || (r = dmalloc(&h->wts, k)) ||
         (r = dmalloc(&h->fallback, 1)) || (r = dmalloc(&h->hq, 2 * k * ff + 4 * (k * ff / 32))) || (r = dmalloc(&h->hsum, k * ff / 32)) || (r = dmalloc(&h->hbuf, k * ff)) ||
         (r = dmalloc(&h->params, param_slots(*cfg).per_layer * cfg->n_layer)))
         return bail(r);
-    // xq, -xq, the x scales and the per-32 sums share one allocation, and so
-    // do hq, -hq and the hq scales (kernels read each group through one
-    // buffer resource)
-    h->xqn = h->xq + d;
-    h->xsb = (float*)(h->xq + 2 * d);
-    h->xsum = (int32_t*)(h->xq + 2 * d + 4 * (d / 32));
+    // xq, its matrix-core image (2 bytes per element), the x scales and the
+    // per-32 sums share one allocation, and so do hq, -hq and the hq scales
+    h->ximg = (uint8_t*)(h->xq + d);
+    h->xsb = (float*)(h->xq + 3 * d);
+    h->xsum = (int32_t*)(h->xq + 3 * d + 4 * (d / 32));
     h->hqn = h->hq + k * ff;
     h->hsb = (float*)(h->hq + 2 * k * ff);
     if (h->mx) {

@@ -20,6 +20,38 @@ constexpr int kMaxParts = 8;
 
 // v_perm_b32: byte i of the result = byte sel_i of {hi:lo} (0-3 lo, 4-7 hi).
 CPB_DEV uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) { return __builtin_amdgcn_perm(hi, lo, sel); }
+
+// e4m3 encoding of a small integer v (0, or |v| with at most 4 significant
+// bits and below 2^9: exact)
+constexpr uint32_t e4m3_int(int v) {
+    if (v == 0) return 0;
+    uint32_t s = v < 0 ? 0x80u : 0u, a = (uint32_t)(v < 0 ? -v : v);
+    int E = 0;
+    while ((a >> (E + 1)) != 0) E++;
+    uint32_t m = E >= 3 ? (a >> (E - 3)) & 7u : (a << (3 - E)) & 7u;
+    return s | ((uint32_t)(E + 7) << 3) | m;
+}
+// table dword of entries 4c .. 4c+3 of f
+template <typename F>
+constexpr uint32_t table4(F f, int c) {
+    return f(4 * c) | (f(4 * c + 1) << 8) | (f(4 * c + 2) << 16) | (f(4 * c + 3) << 24);
+}
+constexpr uint32_t img_h_entry(int i) { return e4m3_int(32 * (i < 8 ? i : i - 16)); }   // nibble i = h & 15
+constexpr uint32_t img_l_entry(int i) { return e4m3_int(2 * i); }                        // nibble i = l
+// 16-entry byte-wise table lookup: entry (nibble of each byte at bit `sh`)
+template <int SH>
+CPB_DEV uint32_t nib_lookup(uint32_t v, uint32_t t0, uint32_t t1, uint32_t t2, uint32_t t3) {
+    const uint32_t i7 = (v >> SH) & 0x07070707u;
+    const uint32_t lo = perm(t1, t0, i7), hi = perm(t3, t2, i7);
+    return perm(hi, lo, ((v >> (SH + 1)) & 0x04040404u) | 0x03020100u);
+}
+// e4m3 of 32*h and of 2*l for the four int8 bytes x = 16*h + l of v
+CPB_DEV uint32_t img_hi(uint32_t v) {
+    return nib_lookup<4>(v, table4(img_h_entry, 0), table4(img_h_entry, 1), table4(img_h_entry, 2), table4(img_h_entry, 3));
+}
+CPB_DEV uint32_t img_lo(uint32_t v) {
+    return nib_lookup<0>(v, table4(img_l_entry, 0), table4(img_l_entry, 1), table4(img_l_entry, 2), table4(img_l_entry, 3));
+}
 CPB_DEV int sdot4(uint32_t a, uint32_t b, int c) { return __builtin_amdgcn_sdot4((int)a, (int)b, c, false); }
 
 // Lane-invariant constants of the decode, held in VGPRs so that the

@@ -11,8 +11,7 @@ struct GateUpArgs {
     const u32x4* w;          // stream layout of gate+up, all experts
     const float* gate_b;     // [ne][dff] or null
     const float* up_b;       // [ne][dff] or null
-    const int8_t* xq;        // [d]
-    const int8_t* xqn;       // [d]
+    const uint8_t* ximg;     // [d/32][64] fp8 activation image (mx_dev.h)
     const float* xsb;        // [d/32]
     const int32_t* ids;      // [top_k] selected experts, when sel.lstar is null
     SelectIn sel;            // otherwise every workgroup selects at its start (workgroup 0 publishes ids / wts)

@@ -21,12 +21,14 @@
 //            workgroup and writes x directly.
 //
 // A workgroup has 2P wavefronts, two per k-part: wave 2q + h accumulates
-// blocks 0-7 (h = 0) or 8-14 (h = 1) of k-part q.  Each lane owns one row-dot:
-// int32 block sum via v_perm decode + sdot4, one float conversion per block,
-// fma with 2^(e-128)*xsb.  The 2P partial sums are added in fixed order
-// (deterministic).  Eight blocks per lane (rather than a whole k-part) halve
-// the decode work that follows the last weight bytes to land, which is what
-// bounds these single-burst kernels.  Batch-1 decode is HBM-bound: no MFMA.
+// blocks 0-7 (h = 0) or 8-14 (h = 1) of k-part q.  Each lane owns one row-dot
+// and a block's int32 sum S becomes one fma with 2^(e-128)*xsb; the 2P partial
+// sums are added in fixed order (deterministic).  Eight blocks per lane
+// (rather than a whole k-part) halve the work that follows the last weight
+// bytes to land, which is what bounds these single-burst kernels.  The block
+// sums come from the matrix cores in gate/up (exact fp8 x fp4 products of the
+// routing kernel's activation image, part_dot_sub_mfma) and from the v_perm
+// decode + sdot4 in down; both give the same S.
 #include "moe_common.h"
 #include "moe_mx.h"
 #include "mx_dev.h"
@@ -44,16 +46,18 @@ __global__ __launch_bounds__(128 * kMaxParts) __attribute__((amdgpu_waves_per_eu
     const int ub = kSubUnits * hh;
     const int tiles = a.dff / 32;
     const int ei = blockIdx.x / tiles, t = blockIdx.x % tiles;
-    uint32_t* xs = (uint32_t*)smem + w * kXsDw;
-    float* red = (float*)smem + W * kXsDw;                     // [W][64]
+    float* red = (float*)smem;                                 // [W][64]
     const int blk0 = q * kBlkPerPart;
-    uint32_t xv[4];
-    bool ok[4];
+    // activations: the two windows' A operands and the 8 block scales
+    const __amdgpu_buffer_rsrc_t ri = buf_rsrc(a.ximg, (uint32_t)(a.nb * kImgBytes));
+    WinAct xw[2];
+    xw[0] = load_win_act(ri, blk0 + ub, ub, a.nb);
+    xw[1] = load_win_act(ri, blk0 + ub + 4, ub + 4, a.nb);
+    float xsc[kSubUnits];
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-        XsSlot sl = xs_slot((const uint32_t*)a.xq, (const uint32_t*)a.xqn, a.xsb, blk0, a.nb, lane + 64 * k, true);
-        xv[k] = *sl.p;
-        ok[k] = sl.valid;
+    for (int i = 0; i < kSubUnits; i++) {
+        const int u = ub + i;
+        xsc[i] = (u < kBlkPerPart && blk0 + u < a.nb) ? a.xsb[blk0 + u] : 0.0f;
     }
     int e;
     if (a.sel.lstar) {
@@ -69,14 +73,11 @@ __global__ __launch_bounds__(128 * kMaxParts) __attribute__((amdgpu_waves_per_eu
     const float* bias = (lane >> 5) ? a.up_b : a.gate_b;
     float bias_pf = 0.0f;
     if (w == 0 && bias) bias_pf = bias[(size_t)e * a.dff + t * 32 + (lane & 31)];
-#pragma unroll
-    for (int k = 0; k < 4; k++) xs[lane + 64 * k] = ok[k] ? xv[k] : 0u;
-    wave_sync_lds();
     const int row = t * 32 + (lane & 31);
     const int isup = lane >> 5;
     int32_t* so = nullptr;
     if (TRACE) so = a.gu_sums + (((size_t)(ei * 2 + isup) * a.dff + row) * a.nb + blk0);
-    const float acc = part_dot_sub<TRACE>(wv, ub, (const u32x4*)xs, (const float*)xs + kBlkPerPart * 16, so, blk0, a.nb);
+    const float acc = part_dot_sub_mfma<TRACE>(wv, ub, xw, xsc, so, blk0, a.nb);
     red[w * 64 + lane] = acc;
     __syncthreads();
     if (w != 0) return;
@@ -275,7 +276,7 @@ int launch_repack_down(const uint8_t* down, u32x4* out, int ne, int d, int nbf, 
 int launch_gateup_mx(const GateUpArgs& a, bool trace, hipStream_t s) {
     const int P = a.nparts;
     if (P < 1 || P > kMaxParts || a.dff % 32 != 0) return -22;
-    size_t lds = sizeof(uint32_t) * 2 * P * kXsDw + sizeof(float) * 2 * P * 64;
+    size_t lds = sizeof(float) * 2 * P * 64;
     if (a.sel.lstar) lds = std::max(lds, select_lds_bytes(a.sel.ne, a.sel.d));
     dim3 grid(a.top_k * (a.dff / 32)), block(128 * P);
     if (trace) launch(k_gateup_mx<true>, grid, block, lds, s, a);

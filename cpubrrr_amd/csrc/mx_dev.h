@@ -77,4 +77,140 @@ CPB_DEV void wave_sync_lds() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+
+// ---- matrix-core block sums of one sub-part ----
+//
+// v_mfma_scale_f32_16x16x128_f8f6f4 with A = activations (fp8 e4m3, 16 x 128)
+// and B = weights (fp4 e2m1, 128 x 16): a "window" is 4 consecutive blocks
+// (128 K) of 16 weight rows.  An int8 activation x is split exactly as
+// x = 16*h + l (h = x >> 4 in [-8, 7], l in [0, 15]) and A row m = 2*bo + p
+// holds 32*h (p = 0) or 2*l (p = 1) of window block bo at that block's K and
+// zeros elsewhere (rows 8-15 are zero).  Both are exact in e4m3, every product
+// with an e2m1 weight and every partial sum is an integer below 2^16, so
+//     D[2*bo][n] + D[2*bo + 1][n] = sum_i 2*E2M1(w_ni) * x_i = S
+// exactly: the reference's int32 block sum (engine_gpt2.rs:194-228, KVI =
+// 2*E2M1 at :152) as a float, bit for bit what the v_perm + sdot4 decode gives.
+//
+// Operand layouts (gfx950): A lane (m = l%16, g = l/16) holds K 16g..16g+15 in
+// bytes 0-15 and K 64+16g.. in bytes 16-31; B lane (n = l%16, g) holds K
+// 32g..32g+31 as nibbles, low nibble first (= block g's 16 GGUF bytes as they
+// are); D lane l holds column l%16, rows 4*(l/16)..+3.  A GGUF block's byte i
+// holds elements i (low nibble) and i + 16, so K offset k inside a block is
+// element k/2 + 16*(k%2): the activation image (below) is stored in K order.
+//
+// The stream layout gives lane r row r of a 64-row tile and one block per
+// register; B needs rows 16t..16t+15 x the window's 4 blocks in one register.
+// That is a 4 x 4 transpose of (16-lane group, register), two rounds of
+// permlane swaps per dword; the four row groups' sums come back to lane = row
+// the same way.
+//
+// Activation image: per 32-block 64 bytes, [32*h of the 32 elements in K
+// order | 2*l in K order], fp8 e4m3 (written by the routing kernel).
+constexpr int kImgBytes = 64;
+
+typedef int v8i_mx __attribute__((ext_vector_type(8)));
+typedef float v4f_mx __attribute__((ext_vector_type(4)));
+typedef uint32_t u2_mx __attribute__((ext_vector_type(2)));
+
+// a.upper 32 lanes <-> b.lower 32 lanes
+CPB_DEV void swap32(uint32_t& a, uint32_t& b) {
+    const u2_mx r = __builtin_amdgcn_permlane32_swap(a, b, false, false);
+    a = r[0];
+    b = r[1];
+}
+// a's 16-lane groups 1, 3 <-> b's groups 0, 2
+CPB_DEV void swap16(uint32_t& a, uint32_t& b) {
+    const u2_mx r = __builtin_amdgcn_permlane16_swap(a, b, false, false);
+    a = r[0];
+    b = r[1];
+}
+CPB_DEV void swap32f(float& a, float& b) {
+    uint32_t x = __float_as_uint(a), y = __float_as_uint(b);
+    swap32(x, y);
+    a = __uint_as_float(x);
+    b = __uint_as_float(y);
+}
+CPB_DEV void swap16f(float& a, float& b) {
+    uint32_t x = __float_as_uint(a), y = __float_as_uint(b);
+    swap16(x, y);
+    a = __uint_as_float(x);
+    b = __uint_as_float(y);
+}
+
+// Window activations of this lane: 16 bytes for its low and high K halves.
+struct WinAct {
+    u32x4 lo, hi;
+};
+// Issue the loads of a window's A operand: blocks wb .. wb+3 (absolute block
+// indices), u0 = index of block wb inside its k-part; blocks beyond the k-part
+// or the row (nb) read as zero (out-of-range buffer offset).
+CPB_DEV WinAct load_win_act(__amdgpu_buffer_rsrc_t img, int wb, int u0, int nb) {
+    const int lane = threadIdx.x & 63;
+    const int m = lane & 15, g = lane >> 4, bo = m >> 1, p = m & 1;
+    const int bl = g >> 1, bh = 2 + (g >> 1);
+    const uint32_t sub = (uint32_t)(p * 32 + (g & 1) * 16);
+    const bool lo_ok = m < 8 && bo == bl && u0 + bl < kBlkPerPart && wb + bl < nb;
+    const bool hi_ok = m < 8 && bo == bh && u0 + bh < kBlkPerPart && wb + bh < nb;
+    WinAct r;
+    r.lo = __builtin_amdgcn_raw_buffer_load_b128(img, lo_ok ? (uint32_t)(wb + bl) * kImgBytes + sub : kOffNone, 0, 0);
+    r.hi = __builtin_amdgcn_raw_buffer_load_b128(img, hi_ok ? (uint32_t)(wb + bh) * kImgBytes + sub : kOffNone, 0, 0);
+    return r;
+}
+
+// Block sums of one window: r[0..3] = the lane's row, blocks 0-3 of the
+// window (transposed in place); S[0..3] = the row's four block sums.
+CPB_DEV void window_sums(u32x4* r, const WinAct& x, float* S) {
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        uint32_t a0 = r[0][c], a1 = r[1][c], a2 = r[2][c], a3 = r[3][c];
+        swap32(a0, a2);
+        swap32(a1, a3);
+        swap16(a0, a1);
+        swap16(a2, a3);
+        r[0][c] = a0; r[1][c] = a1; r[2][c] = a2; r[3][c] = a3;
+    }
+    const v8i_mx A = {(int)x.lo[0], (int)x.lo[1], (int)x.lo[2], (int)x.lo[3],
+                      (int)x.hi[0], (int)x.hi[1], (int)x.hi[2], (int)x.hi[3]};
+    float sa[4], sb[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const v8i_mx B = {(int)r[t][0], (int)r[t][1], (int)r[t][2], (int)r[t][3], 0, 0, 0, 0};
+        const v4f_mx D = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, B, v4f_mx{0, 0, 0, 0}, 0, 4, 0, 127, 0, 127);
+        // lanes 0-15: blocks 0, 1 of row 16t + n; lanes 16-31: blocks 2, 3
+        sa[t] = D[0] + D[1];
+        sb[t] = D[2] + D[3];
+    }
+    swap32f(sa[0], sa[2]);
+    swap32f(sa[1], sa[3]);
+    swap16f(sa[0], sa[1]);
+    swap32f(sb[0], sb[2]);
+    swap32f(sb[1], sb[3]);
+    swap16f(sb[0], sb[1]);
+    S[0] = sa[0];
+    S[1] = sb[0];
+    S[2] = sa[1];
+    S[3] = sb[1];
+}
+
+// One lane's sub-part on the matrix cores: wv as from load_sub, x[0..1] the
+// windows' activations, sc[0..7] the blocks' activation scales.  The fma
+// chain is part_dot_sub's, so the result is the same bit for bit.
+template <bool TRACE>
+CPB_DEV float part_dot_sub_mfma(u32x4* wv, int ub, const WinAct* x, const float* sc, int32_t* sums_out, int blk0,
+                                int nb) {
+    const uint32_t ew[4] = {wv[0][0], wv[0][1], wv[0][2], wv[0][3]};
+    float S[kSubUnits];
+    window_sums(wv + 1, x[0], S);
+    window_sums(wv + 5, x[1], S + 4);
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kSubUnits; i++) {
+        const int u = ub + i;
+        const uint32_t e = (ew[u >> 2] >> (8 * (u & 3))) & 0xffu;
+        acc = fmaf(S[i], e8m0_scale(e, sc[i]), acc);
+        if (TRACE && u < kBlkPerPart && blk0 + u < nb) sums_out[u] = (int32_t)S[i];
+    }
+    return acc;
+}
+
 }  // namespace cpb

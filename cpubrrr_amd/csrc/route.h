@@ -16,7 +16,7 @@ struct RouteArgs {
     int qk;                  // 0: Q8 per 32 (MXFP4 experts), 1: Q8_K per 256 (k-quant experts)
     float* xn;               // [d]
     int8_t* xq;              // [d]
-    int8_t* xqn;             // [d]  negated xq
+    uint8_t* ximg;           // [d/32][64] fp8 activation image of xq (qk == 0; layout in mx_dev.h)
     float* xsb;              // [d/32] or [d/256]
     int32_t* xsum;           // [d/32] (qk == 1)
     double* lstar;           // [ne] fp64 logit (route_dev.h)

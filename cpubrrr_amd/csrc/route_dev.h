@@ -397,20 +397,32 @@ CPB_DEV void route_expert(const RouteArgs& a, int e, int NEg, unsigned char* sme
         const int blk = tid >> 1;
         if (act && blk % NEg == e) {
             const float sc = fmaxf(1e-12f, m) / 127.0f;
-            uint32_t qp[4] = {0, 0, 0, 0}, qn[4] = {0, 0, 0, 0};
+            uint32_t qp[4] = {0, 0, 0, 0};
 #pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const int qv = q8_round(xn[i], sc);
-                qp[i >> 2] |= (uint32_t)(uint8_t)qv << (8 * (i & 3));
-                qn[i >> 2] |= (uint32_t)(uint8_t)(-qv) << (8 * (i & 3));
-            }
+            for (int i = 0; i < 16; i++) qp[i >> 2] |= (uint32_t)(uint8_t)q8_round(xn[i], sc) << (8 * (i & 3));
             const __amdgpu_buffer_rsrc_t rn = buf_rsrc(a.xn, (uint32_t)d * 4);
 #pragma unroll
             for (int k = 0; k < 4; k++)
                 st_dev16(rn, off + 16 * k, u32x4{__float_as_uint(xn[4 * k]), __float_as_uint(xn[4 * k + 1]),
                                                  __float_as_uint(xn[4 * k + 2]), __float_as_uint(xn[4 * k + 3])});
             st_dev16(buf_rsrc(a.xq, (uint32_t)d), (uint32_t)j0, u32x4{qp[0], qp[1], qp[2], qp[3]});
-            st_dev16(buf_rsrc(a.xqn, (uint32_t)d), (uint32_t)j0, u32x4{qn[0], qn[1], qn[2], qn[3]});
+            // the block's matrix-core image: this thread writes K 16*par .. +15
+            // of both halves (both threads of the pair are active here)
+            const int par = tid & 1;
+            const uint32_t r0 = (uint32_t)pair_i32((int)(par ? qp[0] : qp[2]));
+            const uint32_t r1 = (uint32_t)pair_i32((int)(par ? qp[1] : qp[3]));
+            const uint32_t L0 = par ? r0 : qp[0], L1 = par ? r1 : qp[1];
+            const uint32_t H0 = par ? qp[2] : r0, H1 = par ? qp[3] : r1;
+            uint32_t ih[4], il[4];
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) {
+                const uint32_t v = perm(jj < 2 ? H0 : H1, jj < 2 ? L0 : L1, (jj & 1) ? 0x07030602u : 0x05010400u);
+                ih[jj] = img_hi(v);
+                il[jj] = img_lo(v);
+            }
+            const __amdgpu_buffer_rsrc_t rim = buf_rsrc(a.ximg, (uint32_t)d * 2);
+            st_dev16(rim, (uint32_t)(blk * 64 + 16 * par), u32x4{ih[0], ih[1], ih[2], ih[3]});
+            st_dev16(rim, (uint32_t)(blk * 64 + 32 + 16 * par), u32x4{il[0], il[1], il[2], il[3]});
             if ((tid & 1) == 0) st_dev(a.xsb + blk, sc);
         }
     } else {
@@ -422,14 +434,13 @@ CPB_DEV void route_expert(const RouteArgs& a, int e, int NEg, unsigned char* sme
         m = row_max_f32(m);
         const int sb = tid >> 4;
         const float sc = fmaxf(1e-12f, m) / 127.0f;
-        uint32_t qp[4] = {0, 0, 0, 0}, qn[4] = {0, 0, 0, 0};
+        uint32_t qp[4] = {0, 0, 0, 0};
         int s32 = 0;
 #pragma unroll
         for (int i = 0; i < 16; i++) {
             const int qv = q8_round(xn[i], sc);
             s32 += qv;
             qp[i >> 2] |= (uint32_t)(uint8_t)qv << (8 * (i & 3));
-            qn[i >> 2] |= (uint32_t)(uint8_t)(-qv) << (8 * (i & 3));
         }
         s32 += pair_i32(s32);
         if (act && sb % NEg == e) {
@@ -439,7 +450,6 @@ CPB_DEV void route_expert(const RouteArgs& a, int e, int NEg, unsigned char* sme
                 st_dev16(rn, off + 16 * k, u32x4{__float_as_uint(xn[4 * k]), __float_as_uint(xn[4 * k + 1]),
                                                  __float_as_uint(xn[4 * k + 2]), __float_as_uint(xn[4 * k + 3])});
             st_dev16(buf_rsrc(a.xq, (uint32_t)d), (uint32_t)j0, u32x4{qp[0], qp[1], qp[2], qp[3]});
-            st_dev16(buf_rsrc(a.xqn, (uint32_t)d), (uint32_t)j0, u32x4{qn[0], qn[1], qn[2], qn[3]});
             if ((tid & 15) == 0) st_dev(a.xsb + sb, sc);
             if ((tid & 1) == 0) st_dev(a.xsum + (tid >> 1), s32);
         }
