@@ -262,7 +262,8 @@ int layer_token(cpb_moe_t* h, int layer, float* dx, int apply_norm, bool trace) 
     ra.qk = h->mx ? 0 : 1;
     ra.xn = h->xn; ra.xq = h->xq; ra.ximg = h->ximg; ra.xsb = h->xsb; ra.xsum = h->xsum;
     ra.lstar = h->lstar; ra.lbound = h->lbound;
-    ra.stamps = h->d_stamps;
+    unsigned long long* stamps = h->d_stamps ? h->d_stamps + (size_t)(layer % 60) * 16384 : nullptr;
+    ra.stamps = stamps;
     // the route launch publishes certified logits; the gate/up kernel
     // selects at its start (no cross-workgroup hand-off inside a launch)
     {
@@ -274,7 +275,7 @@ int layer_token(cpb_moe_t* h, int layer, float* dx, int apply_norm, bool trace) 
         g.w = L.gu; g.gate_b = L.gate_b; g.up_b = L.up_b;
         g.ximg = h->ximg; g.xsb = h->xsb;
         g.ids = h->ids;
-        g.stamps = h->d_stamps;
+        g.stamps = stamps;
         {
             g.sel.lstar = h->lstar; g.sel.lbound = h->lbound; g.sel.router_w = L.router_w; g.sel.router_b = L.router_b;
             g.sel.xn = h->xn; g.sel.ne = c.n_expert; g.sel.k = c.top_k; g.sel.d = c.d;
@@ -288,7 +289,7 @@ int layer_token(cpb_moe_t* h, int layer, float* dx, int apply_norm, bool trace) 
         dn.w = L.dn; dn.down_b = L.down_b; dn.hq = h->hq; dn.hqn = h->hqn; dn.hsb = h->hsb;
         dn.ids = h->ids; dn.wts = h->wts;
         dn.d = c.d; dn.dff = c.d_ff; dn.nbf = h->nbf; dn.nparts = h->parts_dn; dn.top_k = c.top_k;
-        dn.x = dx; dn.dn = h->t_dn; dn.dn_sums = h->t_dn_sums;
+        dn.x = dx; dn.dn = h->t_dn; dn.dn_sums = h->t_dn_sums; dn.stamps = stamps;
         {
             Timer tm(h, 1);
             if (cpb::launch_gateup_mx(g, trace, h->stream)) return fail(CPB_ENODEV, "gate/up launch failed");

@@ -37,6 +37,7 @@ struct DownArgs {
     const float* wts;
     int d, dff, nbf, nparts, top_k;
     float* x;                // [d] residual, updated in place
+    unsigned long long* stamps;  // probe builds (CPB_DECODE_STAMPS) only
     float* dn;               // trace [top_k][d]
     int32_t* dn_sums;        // trace [top_k][d][nbf]
 };

@@ -32,6 +32,7 @@
 #include "moe_common.h"
 #include "moe_mx.h"
 #include "mx_dev.h"
+#include "route_dev.h"
 
 #include <algorithm>
 
@@ -46,6 +47,8 @@ __global__ __launch_bounds__(128 * kMaxParts) __attribute__((amdgpu_waves_per_eu
     const int ub = kSubUnits * hh;
     const int tiles = a.dff / 32;
     const int ei = blockIdx.x / tiles, t = blockIdx.x % tiles;
+    RSTAMP_DECL;
+    RSTAMP(0);
     float* red = (float*)smem;                                 // [W][64]
     const int blk0 = q * kBlkPerPart;
     // activations: the two windows' A operands and the 8 block scales
@@ -62,25 +65,43 @@ __global__ __launch_bounds__(128 * kMaxParts) __attribute__((amdgpu_waves_per_eu
     int e;
     if (a.sel.lstar) {
         __shared__ Selection ssel;
+#ifdef CPB_DECODE_STAMPS
+        __shared__ unsigned long long last_start, last_pre;
+        if (w == W - 1 && lane == 0) last_start = wall_clock64();
+#endif
         if (w == 0) select_topk_wave(a.sel, smem, &ssel);
-        __syncthreads();
-        e = ssel.ids[ei];
+        RSTAMP(5);
+#ifdef CPB_DECODE_STAMPS
+        if (w == W - 1 && lane == 0) last_pre = wall_clock64();
+#endif
+        // LDS-only barrier: the activation loads above need not have landed
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+#ifdef CPB_DECODE_STAMPS
+        rst_[6] = last_start;
+        rst_[7] = last_pre;
+#endif
+        // a plain LDS read: merged with the global read below into one flat
+        // load it would queue behind the CU's outstanding weight loads
+        e = uniform(((const __attribute__((address_space(3))) int*)ssel.ids)[ei]);
     } else {
         e = a.ids[ei];
     }
+    RSTAMP(1);
     u32x4 wv[1 + kSubUnits];
     load_sub(a.w + ((((size_t)e * tiles + t) * P + q) * kUnits) * 64 + lane, 64, ub, wv);
     const float* bias = (lane >> 5) ? a.up_b : a.gate_b;
     float bias_pf = 0.0f;
-    if (w == 0 && bias) bias_pf = bias[(size_t)e * a.dff + t * 32 + (lane & 31)];
+    if (w == 0 && bias) bias_pf = ((const __attribute__((address_space(1))) float*)bias)[(size_t)e * a.dff + t * 32 + (lane & 31)];
     const int row = t * 32 + (lane & 31);
     const int isup = lane >> 5;
     int32_t* so = nullptr;
     if (TRACE) so = a.gu_sums + (((size_t)(ei * 2 + isup) * a.dff + row) * a.nb + blk0);
     const float acc = part_dot_sub_mfma<TRACE>(wv, ub, xw, xsc, so, blk0, a.nb);
+    RSTAMP(2);
     red[w * 64 + lane] = acc;
     __syncthreads();
     if (w != 0) return;
+    RSTAMP(3);
     float v = 0.0f;
     for (int p = 0; p < W; p++) v += red[p * 64 + lane];
     if (bias) v += bias_pf;
@@ -104,6 +125,8 @@ __global__ __launch_bounds__(128 * kMaxParts) __attribute__((amdgpu_waves_per_eu
         if (TRACE) a.h[(size_t)ei * a.dff + row] = h;
     }
     if (lane == 0) a.hsb[(size_t)ei * (a.dff / 32) + t] = sc;
+    RSTAMP(4);
+    RSTAMP_FLUSH_TO(a.stamps ? a.stamps + 1024 + (size_t)blockIdx.x * 8 : nullptr);
 }
 
 template <bool TRACE>
@@ -118,6 +141,8 @@ __global__ __launch_bounds__(128 * kMaxParts) void k_down_mx(DownArgs a) {
     int es[4];
 #pragma unroll
     for (int k = 0; k < 4; k++) es[k] = __builtin_amdgcn_readfirstlane(a.ids[k < K ? k : 0]);
+    RSTAMP_DECL;
+    RSTAMP(0);
     const int e = ei == 0 ? es[0] : ei == 1 ? es[1] : ei == 2 ? es[2] : es[3];
     uint32_t* xs = (uint32_t*)smem + w * K * kXsDw;            // [K][256]
     float* red = (float*)smem + W * K * kXsDw;                 // [W][64]
@@ -152,9 +177,11 @@ __global__ __launch_bounds__(128 * kMaxParts) void k_down_mx(DownArgs a) {
     int32_t* so = nullptr;
     if (TRACE) so = a.dn_sums + (((size_t)ei * a.d + row) * a.nbf + blk0);
     const float acc = part_dot_sub<TRACE>(wv, ub, (const u32x4*)mine, (const float*)mine + kBlkPerPart * 16, so, blk0, a.nbf);
+    RSTAMP(1);
     red[w * 64 + lane] = acc;
     __syncthreads();
     if (w != 0) return;
+    RSTAMP(2);
     float v = 0.0f;
     for (int p = 0; p < W; p++) v += red[p * 64 + lane];
     if (a.down_b) v += dnb_pf;
@@ -169,6 +196,8 @@ __global__ __launch_bounds__(128 * kMaxParts) void k_down_mx(DownArgs a) {
             if (k < K) s += w_pf[k] * vv[k * RT + lane];
         a.x[row] = s;
     }
+    RSTAMP(3);
+    RSTAMP_FLUSH_TO(a.stamps ? a.stamps + 8192 + (size_t)blockIdx.x * 8 : nullptr);
 }
 
 // ---- load-time re-layout from native GGUF MXFP4 rows (17-byte blocks) ----

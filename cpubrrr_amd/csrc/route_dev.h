@@ -114,11 +114,13 @@ CPB_DEV void norm_into(const float* __restrict__ xg, const float* __restrict__ n
 // per stamp would make every later vmcnt wait include its completion
 #define RSTAMP_DECL unsigned long long rst_[8] = {0, 0, 0, 0, 0, 0, 0, 0}
 #define RSTAMP(i) do { rst_[i] = wall_clock64(); } while (0)
-#define RSTAMP_FLUSH do { if (threadIdx.x == 0 && a.stamps) for (int i_ = 0; i_ < 8; i_++) a.stamps[(size_t)e * 16 + i_] = rst_[i_]; } while (0)
+#define RSTAMP_FLUSH_TO(p_) do { if (threadIdx.x == 0 && (p_)) for (int i_ = 0; i_ < 8; i_++) (p_)[i_] = rst_[i_]; } while (0)
+#define RSTAMP_FLUSH RSTAMP_FLUSH_TO(a.stamps ? a.stamps + (size_t)e * 16 : nullptr)
 #else
 #define RSTAMP_DECL do { } while (0)
 #define RSTAMP(i) do { } while (0)
 #define RSTAMP_FLUSH do { } while (0)
+#define RSTAMP_FLUSH_TO(p_) do { } while (0)
 #endif
 
 // ---- wavefront DPP helpers on doubles (no LDS round trips) ----
