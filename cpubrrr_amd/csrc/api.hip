@@ -78,7 +78,8 @@ struct cpb_moe {
     int32_t* ids = nullptr;
     float* wts = nullptr;
     int32_t* fallback = nullptr;
-    int8_t *hq = nullptr, *hqn = nullptr;
+    int8_t* hq = nullptr;
+    uint8_t* himg = nullptr;
     float* hsb = nullptr;
     int32_t* hsum = nullptr;
     float* hbuf = nullptr;
@@ -283,10 +284,10 @@ int layer_token(cpb_moe_t* h, int layer, float* dx, int apply_norm, bool trace) 
         }
         g.dff = c.d_ff; g.nb = h->nb; g.nparts = h->parts_gu; g.top_k = c.top_k;
         g.alpha = c.alpha; g.limit = c.limit;
-        g.hq = h->hq; g.hqn = h->hqn; g.hsb = h->hsb;
+        g.hq = h->hq; g.himg = h->himg; g.hsb = h->hsb;
         g.gu = h->t_gu; g.gu_sums = h->t_gu_sums; g.h = h->t_h;
         cpb::DownArgs dn{};
-        dn.w = L.dn; dn.down_b = L.down_b; dn.hq = h->hq; dn.hqn = h->hqn; dn.hsb = h->hsb;
+        dn.w = L.dn; dn.down_b = L.down_b; dn.himg = h->himg; dn.hsb = h->hsb;
         dn.ids = h->ids; dn.wts = h->wts;
         dn.d = c.d; dn.dff = c.d_ff; dn.nbf = h->nbf; dn.nparts = h->parts_dn; dn.top_k = c.top_k;
         dn.x = dx; dn.dn = h->t_dn; dn.dn_sums = h->t_dn_sums; dn.stamps = stamps;
@@ -365,16 +366,16 @@ int cpb_moe_create(const cpb_moe_cfg* cfg, int device, cpb_moe_t** out) {
     if ((r = dmalloc(&h->x, T * d)) || (r = dmalloc(&h->xn, d)) || (r = dmalloc(&h->xq, 3 * d + 8 * (d / 32))) ||
         (r = dmalloc(&h->lstar, ne)) || (r = dmalloc(&h->lbound, ne)) ||
         (r = dmalloc(&h->logits, ne)) || (r = dmalloc(&h->ids, k)) || (r = dmalloc(&h->wts, k)) ||
-        (r = dmalloc(&h->fallback, 1)) || (r = dmalloc(&h->hq, 2 * k * ff + 4 * (k * ff / 32))) || (r = dmalloc(&h->hsum, k * ff / 32)) || (r = dmalloc(&h->hbuf, k * ff)) ||
+        (r = dmalloc(&h->fallback, 1)) || (r = dmalloc(&h->hq, 3 * k * ff + 4 * (k * ff / 32))) || (r = dmalloc(&h->hsum, k * ff / 32)) || (r = dmalloc(&h->hbuf, k * ff)) ||
         (r = dmalloc(&h->params, param_slots(*cfg).per_layer * cfg->n_layer)))
         return bail(r);
     // xq, its matrix-core image (2 bytes per element), the x scales and the
-    // per-32 sums share one allocation, and so do hq, -hq and the hq scales
+    // per-32 sums share one allocation, and so do hq, its image and the hq scales
     h->ximg = (uint8_t*)(h->xq + d);
     h->xsb = (float*)(h->xq + 3 * d);
     h->xsum = (int32_t*)(h->xq + 3 * d + 4 * (d / 32));
-    h->hqn = h->hq + k * ff;
-    h->hsb = (float*)(h->hq + 2 * k * ff);
+    h->himg = (uint8_t*)(h->hq + k * ff);
+    h->hsb = (float*)(h->hq + 3 * k * ff);
     if (h->mx) {
         if ((r = dmalloc(&h->d_special, 1))) return bail(r);
         h->grouped = T > 1;

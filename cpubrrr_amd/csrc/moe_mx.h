@@ -18,7 +18,7 @@ struct GateUpArgs {
     int dff, nb, nparts, top_k;
     float alpha, limit;
     int8_t* hq;              // [top_k][dff]
-    int8_t* hqn;             // [top_k][dff]
+    uint8_t* himg;           // [top_k][dff/32][64] fp8 image of hq (mx_dev.h)
     float* hsb;              // [top_k][dff/32]
     unsigned long long* stamps;  // probe builds (CPB_DECODE_STAMPS) only
     // trace (TRACE instantiation only)
@@ -30,9 +30,8 @@ struct GateUpArgs {
 struct DownArgs {
     const u32x4* w;          // stream layout of down, all experts
     const float* down_b;     // [ne][d] or null
-    const int8_t* hq;
-    const int8_t* hqn;
-    const float* hsb;
+    const uint8_t* himg;     // [top_k][dff/32][64]
+    const float* hsb;        // [top_k][dff/32]
     const int32_t* ids;
     const float* wts;
     int d, dff, nbf, nparts, top_k;

@@ -121,7 +121,13 @@ __global__ __launch_bounds__(128 * kMaxParts) __attribute__((amdgpu_waves_per_eu
     if (!isup) {
         const int8_t qv = q8_round(h, sc);
         a.hq[(size_t)ei * a.dff + row] = qv;
-        a.hqn[(size_t)ei * a.dff + row] = (int8_t)(-qv);
+        // h's matrix-core image for the down kernel: element j = row % 32 of
+        // block t sits at K offset 2j (j < 16) or 2(j - 16) + 1
+        const int j = lane & 31, kpos = j < 16 ? 2 * j : 2 * (j - 16) + 1;
+        uint8_t* im = a.himg + ((size_t)ei * (a.dff / 32) + t) * kImgBytes;
+        const uint32_t qb = (uint32_t)(uint8_t)qv;
+        im[kpos] = (uint8_t)img_hi(qb);
+        im[32 + kpos] = (uint8_t)img_lo(qb);
         if (TRACE) a.h[(size_t)ei * a.dff + row] = h;
     }
     if (lane == 0) a.hsb[(size_t)ei * (a.dff / 32) + t] = sc;
@@ -144,19 +150,24 @@ __global__ __launch_bounds__(128 * kMaxParts) void k_down_mx(DownArgs a) {
     RSTAMP_DECL;
     RSTAMP(0);
     const int e = ei == 0 ? es[0] : ei == 1 ? es[1] : ei == 2 ? es[2] : es[3];
-    uint32_t* xs = (uint32_t*)smem + w * K * kXsDw;            // [K][256]
-    float* red = (float*)smem + W * K * kXsDw;                 // [W][64]
+    float* red = (float*)smem;                                 // [W][64]
     float* vv = red + W * 64;                                  // [64]
     const int blk0 = q * kBlkPerPart;
-    uint32_t xv[16];
-    bool ok[16];
+    // activations: for each window and 16-lane group (whose rows all belong
+    // to expert slot 16g / RT) this lane's A fragment; the slot's scales
+    const __amdgpu_buffer_rsrc_t ri = buf_rsrc(a.himg, (uint32_t)(K * a.nbf * kImgBytes));
+    u32x4 xa[2][4];
 #pragma unroll
-    for (int k = 0; k < 16; k++) {
-        int i = lane + 64 * k, ex = min(i / kXsDw, K - 1);
-        XsSlot sl = xs_slot((const uint32_t*)(a.hq + (size_t)ex * a.dff), (const uint32_t*)(a.hqn + (size_t)ex * a.dff),
-                            a.hsb + (size_t)ex * a.nbf, blk0, a.nbf, i % kXsDw, i < K * kXsDw);
-        xv[k] = *sl.p;
-        ok[k] = sl.valid;
+    for (int h = 0; h < 2; h++)
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+            xa[h][g] = load_act_frag(ri, (uint32_t)(((16 * g) / RT) * a.nbf * kImgBytes), blk0 + ub + 4 * h, ub + 4 * h,
+                                     a.nbf);
+    float xsc[kSubUnits];
+#pragma unroll
+    for (int i = 0; i < kSubUnits; i++) {
+        const int u = ub + i;
+        xsc[i] = (u < kBlkPerPart && blk0 + u < a.nbf) ? a.hsb[(size_t)ei * a.nbf + blk0 + u] : 0.0f;
     }
     u32x4 wv[1 + kSubUnits];
     load_sub(a.w + (((((size_t)e * tiles + t) * P + q) * kUnits) * RT) + rr, RT, ub, wv);
@@ -167,16 +178,9 @@ __global__ __launch_bounds__(128 * kMaxParts) void k_down_mx(DownArgs a) {
     }
 #pragma unroll
     for (int k = 0; k < 4; k++) w_pf[k] = a.wts[k < K ? k : 0];
-#pragma unroll
-    for (int k = 0; k < 16; k++) {
-        int i = lane + 64 * k;
-        if (i < K * kXsDw) xs[i] = ok[k] ? xv[k] : 0u;
-    }
-    wave_sync_lds();
-    const uint32_t* mine = xs + ei * kXsDw;
     int32_t* so = nullptr;
     if (TRACE) so = a.dn_sums + (((size_t)ei * a.d + row) * a.nbf + blk0);
-    const float acc = part_dot_sub<TRACE>(wv, ub, (const u32x4*)mine, (const float*)mine + kBlkPerPart * 16, so, blk0, a.nbf);
+    const float acc = part_dot_sub_mfma4<TRACE>(wv, ub, xa, xsc, so, blk0, a.nbf);
     RSTAMP(1);
     red[w * 64 + lane] = acc;
     __syncthreads();
@@ -316,7 +320,7 @@ int launch_gateup_mx(const GateUpArgs& a, bool trace, hipStream_t s) {
 int launch_down_mx(const DownArgs& a, bool trace, hipStream_t s) {
     const int P = a.nparts, K = a.top_k;
     if (P < 1 || P > kMaxParts || (K != 1 && K != 2 && K != 4) || a.d % (64 / K) != 0) return -22;
-    const size_t lds = sizeof(uint32_t) * 2 * P * K * kXsDw + sizeof(float) * (2 * P * 64 + 64);
+    const size_t lds = sizeof(float) * (2 * P * 64 + 64);
     dim3 grid(a.d / (64 / K)), block(128 * P);
     if (trace) launch(k_down_mx<true>, grid, block, lds, s, a);
     else launch(k_down_mx<false>, grid, block, lds, s, a);

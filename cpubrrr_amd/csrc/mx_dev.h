@@ -157,9 +157,31 @@ CPB_DEV WinAct load_win_act(__amdgpu_buffer_rsrc_t img, int wb, int u0, int nb) 
     return r;
 }
 
+// One 16-byte A fragment per lane: lane (m, g) with m < 8 holds part p = m%2
+// of window block bo = m/2 at K half (g%2) of that block, i.e. the low half
+// of A when bo = g/2 (m < 4) or the high half when bo = 2 + g/2 (4 <= m < 8);
+// every other fragment is zero.  img: the image of one activation vector;
+// blocks beyond the k-part or the row (nb) read as zero (out-of-range offset).
+CPB_DEV u32x4 load_act_frag(__amdgpu_buffer_rsrc_t img, uint32_t base, int wb, int u0, int nb) {
+    const int lane = threadIdx.x & 63;
+    const int m = lane & 15, g = lane >> 4;
+    const int bi = (m < 4 ? 0 : 2) + (g >> 1);   // block of the window this lane could hold
+    const bool ok = m < 8 && (m >> 1) == bi && u0 + bi < kBlkPerPart && wb + bi < nb;
+    const uint32_t off = base + (uint32_t)(wb + bi) * kImgBytes + (uint32_t)((m & 1) * 32 + (g & 1) * 16);
+    return __builtin_amdgcn_raw_buffer_load_b128(img, ok ? off : kOffNone, 0, 0);
+}
+CPB_DEV v8i_mx act_operand(const u32x4& x) {
+    const bool lo = (threadIdx.x & 15) < 4;
+    const u32x4 z = {0, 0, 0, 0};
+    const u32x4 l = lo ? x : z, h = lo ? z : x;
+    return v8i_mx{(int)l[0], (int)l[1], (int)l[2], (int)l[3], (int)h[0], (int)h[1], (int)h[2], (int)h[3]};
+}
+
 // Block sums of one window: r[0..3] = the lane's row, blocks 0-3 of the
-// window (transposed in place); S[0..3] = the row's four block sums.
-CPB_DEV void window_sums(u32x4* r, const WinAct& x, float* S) {
+// window (transposed in place); a(t) = the A operand for rows 16t..16t+15
+// (lane group t); S[0..3] = the row's four block sums.
+template <typename AFn>
+CPB_DEV void window_sums(u32x4* r, AFn a, float* S) {
 #pragma unroll
     for (int c = 0; c < 4; c++) {
         uint32_t a0 = r[0][c], a1 = r[1][c], a2 = r[2][c], a3 = r[3][c];
@@ -169,13 +191,11 @@ CPB_DEV void window_sums(u32x4* r, const WinAct& x, float* S) {
         swap16(a2, a3);
         r[0][c] = a0; r[1][c] = a1; r[2][c] = a2; r[3][c] = a3;
     }
-    const v8i_mx A = {(int)x.lo[0], (int)x.lo[1], (int)x.lo[2], (int)x.lo[3],
-                      (int)x.hi[0], (int)x.hi[1], (int)x.hi[2], (int)x.hi[3]};
     float sa[4], sb[4];
 #pragma unroll
     for (int t = 0; t < 4; t++) {
         const v8i_mx B = {(int)r[t][0], (int)r[t][1], (int)r[t][2], (int)r[t][3], 0, 0, 0, 0};
-        const v4f_mx D = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, B, v4f_mx{0, 0, 0, 0}, 0, 4, 0, 127, 0, 127);
+        const v4f_mx D = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a(t), B, v4f_mx{0, 0, 0, 0}, 0, 4, 0, 127, 0, 127);
         // lanes 0-15: blocks 0, 1 of row 16t + n; lanes 16-31: blocks 2, 3
         sa[t] = D[0] + D[1];
         sb[t] = D[2] + D[3];
@@ -192,16 +212,11 @@ CPB_DEV void window_sums(u32x4* r, const WinAct& x, float* S) {
     S[3] = sb[1];
 }
 
-// One lane's sub-part on the matrix cores: wv as from load_sub, x[0..1] the
-// windows' activations, sc[0..7] the blocks' activation scales.  The fma
-// chain is part_dot_sub's, so the result is the same bit for bit.
+// The fma chain of part_dot_sub over block sums S[0..7] of blocks ub .. ub+7
+// (so the result is the same bit for bit).
 template <bool TRACE>
-CPB_DEV float part_dot_sub_mfma(u32x4* wv, int ub, const WinAct* x, const float* sc, int32_t* sums_out, int blk0,
-                                int nb) {
-    const uint32_t ew[4] = {wv[0][0], wv[0][1], wv[0][2], wv[0][3]};
-    float S[kSubUnits];
-    window_sums(wv + 1, x[0], S);
-    window_sums(wv + 5, x[1], S + 4);
+CPB_DEV float sub_chain(const u32x4& ew4, int ub, const float* S, const float* sc, int32_t* sums_out, int blk0, int nb) {
+    const uint32_t ew[4] = {ew4[0], ew4[1], ew4[2], ew4[3]};
     float acc = 0.0f;
 #pragma unroll
     for (int i = 0; i < kSubUnits; i++) {
@@ -211,6 +226,33 @@ CPB_DEV float part_dot_sub_mfma(u32x4* wv, int ub, const WinAct* x, const float*
         if (TRACE && u < kBlkPerPart && blk0 + u < nb) sums_out[u] = (int32_t)S[i];
     }
     return acc;
+}
+
+// One lane's sub-part on the matrix cores, one activation vector for all 64
+// rows (gate/up): wv as from load_sub, x[0..1] the windows' activations,
+// sc[0..7] the blocks' activation scales.
+template <bool TRACE>
+CPB_DEV float part_dot_sub_mfma(u32x4* wv, int ub, const WinAct* x, const float* sc, int32_t* sums_out, int blk0,
+                                int nb) {
+    float S[kSubUnits];
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const v8i_mx A = {(int)x[h].lo[0], (int)x[h].lo[1], (int)x[h].lo[2], (int)x[h].lo[3],
+                          (int)x[h].hi[0], (int)x[h].hi[1], (int)x[h].hi[2], (int)x[h].hi[3]};
+        window_sums(wv + 1 + 4 * h, [&](int) { return A; }, S + 4 * h);
+    }
+    return sub_chain<TRACE>(wv[0], ub, S, sc, sums_out, blk0, nb);
+}
+
+// The same with a different activation vector per 16-row lane group
+// (down: xa[h][t] = window h's fragment of the vector of lane group t).
+template <bool TRACE>
+CPB_DEV float part_dot_sub_mfma4(u32x4* wv, int ub, const u32x4 (*xa)[4], const float* sc, int32_t* sums_out,
+                                 int blk0, int nb) {
+    float S[kSubUnits];
+#pragma unroll
+    for (int h = 0; h < 2; h++) window_sums(wv + 1 + 4 * h, [&](int t) { return act_operand(xa[h][t]); }, S + 4 * h);
+    return sub_chain<TRACE>(wv[0], ub, S, sc, sums_out, blk0, nb);
 }
 
 }  // namespace cpb
