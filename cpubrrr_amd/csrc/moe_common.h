@@ -54,73 +54,49 @@ CPB_DEV uint32_t img_lo(uint32_t v) {
 }
 CPB_DEV int sdot4(uint32_t a, uint32_t b, int c) { return __builtin_amdgcn_sdot4((int)a, (int)b, c, false); }
 
-// Lane-invariant constants of the decode, held in VGPRs so that the
-// shift-mask-or steps compile to v_and_or_b32 (gfx9 VOP3 takes no literal).
-struct MxConsts {
-    uint32_t m7, m4, sel, tlo, thi;
-};
-CPB_DEV MxConsts mx_consts() {
-    MxConsts k;
-    asm volatile("v_mov_b32 %0, 0x07070707" : "=v"(k.m7));
-    asm volatile("v_mov_b32 %0, 0x04040404" : "=v"(k.m4));
-    asm volatile("v_mov_b32 %0, 0x03020100" : "=v"(k.sel));
-    asm volatile("v_mov_b32 %0, 0x03020100" : "=v"(k.tlo));
-    asm volatile("v_mov_b32 %0, 0x0C080604" : "=v"(k.thi));
-    return k;
-}
-
-// Int32 block sum S = sum_i KVI[c_i] * x_i of one MXFP4 block (16 nibble
-// bytes `q`; element j<16 = low nibble of byte j, 16+j = high nibble) against
-// 32 int8 activations given as 8 dwords `xp` and their negations `xn`.
-// The 3-bit magnitude goes through a v_perm table of doubled E2M1
-// magnitudes {0,1,2,3,4,6,8,12}; the sign bit (code bit 3) picks x or -x
-// per byte with a second v_perm, so the dot is a plain sdot4.
-CPB_DEV int mx_block_sum(const u32x4& q, const u32x4& xp0, const u32x4& xp1, const u32x4& xn0,
-                         const u32x4& xn1, const MxConsts& k) {
-    const uint32_t w[4] = {q[0], q[1], q[2], q[3]};
-    const uint32_t p[8] = {xp0[0], xp0[1], xp0[2], xp0[3], xp1[0], xp1[1], xp1[2], xp1[3]};
-    const uint32_t n[8] = {xn0[0], xn0[1], xn0[2], xn0[3], xn1[0], xn1[1], xn1[2], xn1[3]};
-    int S = 0;
-#pragma unroll
-    for (int c = 0; c < 4; c++) {
-        uint32_t lo = w[c];
-        uint32_t ma = perm(k.thi, k.tlo, lo & k.m7);
-        uint32_t mb = perm(k.thi, k.tlo, (lo >> 4) & k.m7);
-        uint32_t sa = ((lo >> 1) & k.m4) | k.sel;
-        uint32_t sb = ((lo >> 5) & k.m4) | k.sel;
-        uint32_t xa = perm(n[c], p[c], sa);
-        uint32_t xb = perm(n[4 + c], p[4 + c], sb);
-        S = sdot4(ma, xa, S);
-        S = sdot4(mb, xb, S);
-    }
-    return S;
-}
-
 // 2^(e-128) * xsb exactly as the reference computes tbl[e] * xsb, with tbl
 // from 2f32.powi(e-128) (tbl[0] = 0: the powi intermediate overflows).
 CPB_DEV float e8m0_scale(uint32_t e, float xsb) { return e == 0 ? 0.0f : ldexpf(xsb, (int)e - 128); }
 
-// bytewise int8 negation of a dword (-(-128) is never produced: |q| <= 127)
-CPB_DEV uint32_t neg4(uint32_t v) {
-    uint32_t r = 0;
-#pragma unroll
-    for (int i = 0; i < 4; i++) r |= ((uint32_t)(uint8_t)(-(int8_t)(v >> (8 * i)))) << (8 * i);
-    return r;
-}
 
 // Q8 round: (v / sc).round() in the reference's fp32 (quotient correctly
 // rounded, then half away from zero), clamped to +-127.  The quotient from
 // the hardware reciprocal, v * rcp(sc), is within a few ulp (< 2^-16 for
 // |v / sc| <= 128) of the exact one; unless it lies within 2^-10 of a
-// half-integer both round to the same integer, and only there (about one
-// value in a thousand) the IEEE division decides.
+// half-integer both round to the same integer (and round-to-nearest-even of
+// it agrees with half-away-from-zero), and only there (about one value in a
+// thousand) the IEEE division decides.
+CPB_DEV bool q8_near_half(float y) { return fabsf(__builtin_amdgcn_fractf(fabsf(y)) - 0.5f) < 0x1p-10f; }
+CPB_DEV int8_t q8_clamp(float r) { return (int8_t)(int)fminf(fmaxf(r, -127.0f), 127.0f); }
 CPB_DEV int8_t q8_round(float v, float sc) {
     const float y = v * __builtin_amdgcn_rcpf(sc);
-    const float a = fabsf(y);
-    float r = roundf(y);
-    if (fabsf((a - floorf(a)) - 0.5f) < 0x1p-10f) r = roundf(v / sc);
-    r = fminf(fmaxf(r, -127.0f), 127.0f);
-    return (int8_t)r;
+    float r = __builtin_rintf(y);
+    if (q8_near_half(y)) r = roundf(v / sc);
+    return q8_clamp(r);
+}
+// q8_round of 16 values with one (rarely taken) branch for the exact path;
+// the bytes packed little-endian into q[0..3].
+CPB_DEV void q8_round16(const float* v, float sc, uint32_t* q) {
+    const float rs = __builtin_amdgcn_rcpf(sc);
+    float r[16];
+    bool near = false;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const float y = v[i] * rs;
+        r[i] = __builtin_rintf(y);
+        near = near || q8_near_half(y);
+    }
+    if (near) {
+#pragma unroll
+        for (int i = 0; i < 16; i++)
+            if (q8_near_half(v[i] * rs)) r[i] = roundf(v[i] / sc);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        q[k] = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) q[k] |= (uint32_t)(uint8_t)q8_clamp(r[4 * k + i]) << (8 * i);
+    }
 }
 
 CPB_DEV float wave_max(float v) {

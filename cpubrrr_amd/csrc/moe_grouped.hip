@@ -90,9 +90,9 @@ __global__ __launch_bounds__(256) void k_prep_batch(GroupedArgs a) {
 }
 
 // ---- 2. router logits + bounds, workgroup = (expert, kRouteTok tokens) ----
-// The decode route's computation (logit_phase1/2/final, 256 threads, 16
-// elements each), so every token's logits are those of per-token decode bit
-// for bit.
+// The decode route's computation (logit_phase1/2/final, 16 elements per
+// thread, element wave w = elements 1024w ..), so every token's logits are
+// those of per-token decode bit for bit.
 __global__ __launch_bounds__(256) void k_router_batch(GroupedArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     const int e = blockIdx.x, d = a.d, tid = threadIdx.x, nw = blockDim.x >> 6;
@@ -127,9 +127,8 @@ __global__ __launch_bounds__(256) void k_router_batch(GroupedArgs a) {
             for (int c = 0; c < 4; c++) xf[4 * k + c] = act ? __uint_as_float(x4[c]) : 0.0f;
         }
         LogitThread lt;
-        logit_phase1(wf, xf, gf, lt, dred);
-        __syncthreads();
-        logit_phase2(lt, act, dred);
+        logit_phase1(wf, xf, gf, lt, dred, tid >> 6);
+        logit_phase2(lt, act, dred, tid >> 6);
         __syncthreads();
         if (tid == 0) logit_final(dred, nw, d, b, a.inv[t], a.lstar + (size_t)t * a.ne + e, a.lbound + (size_t)t * a.ne + e);
         __syncthreads();

@@ -26,9 +26,9 @@
 // sums are added in fixed order (deterministic).  Eight blocks per lane
 // (rather than a whole k-part) halve the work that follows the last weight
 // bytes to land, which is what bounds these single-burst kernels.  The block
-// sums come from the matrix cores in gate/up (exact fp8 x fp4 products of the
-// routing kernel's activation image, part_dot_sub_mfma) and from the v_perm
-// decode + sdot4 in down; both give the same S.
+// sums come from the matrix cores (mx_dev.h): exact fp8 x fp4 products of an
+// fp8 image of the Q8 activations (written by the routing kernel for x, by
+// the gate/up epilogue for h) with the stream's nibbles as they are.
 #include "moe_common.h"
 #include "moe_mx.h"
 #include "mx_dev.h"

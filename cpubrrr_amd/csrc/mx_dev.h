@@ -1,62 +1,14 @@
-// mx_dev.h -- device building blocks of the MXFP4 expert GEMVs (moe_mx.hip,
-// and the activation staging of the grouped path).  Stream layout and lane
-// mapping: see moe_mx.hip.
+// mx_dev.h -- device building blocks of the MXFP4 expert GEMVs (moe_mx.hip;
+// the grouped path shares the sub-part split and the image encoding).  Stream
+// layout and lane mapping: see moe_mx.hip.
 #pragma once
 #include "moe_common.h"
 
 namespace cpb {
 
-// LDS image of one expert's activations for one k-part: 15 blocks x
-// [xq 8 dwords | -xq 8 dwords], then 15 block scales (+1 pad): 256 dwords.
-constexpr int kXsDw = 256;
-
-// Fill one 256-dword activation image from global xq / -xq / scales.
-// `slot` runs over the image's dwords; returns the value for that slot.
-struct XsSlot {
-    const uint32_t* p;
-    bool valid;
-};
-CPB_DEV XsSlot xs_slot(const uint32_t* __restrict__ q, const uint32_t* __restrict__ qn,
-                       const float* __restrict__ sc, int blk0, int nb, int slot, bool use) {
-    // one clamped address per slot; the validity select is applied when the
-    // value is stored to LDS, after the weight loads have been issued.  A
-    // consumer whose data was written earlier in the same launch must load
-    // through ld_dev (another XCD's L2 may hold a stale copy).
-    const bool isx = slot < kBlkPerPart * 16;
-    const int u = isx ? slot / 16 : slot - kBlkPerPart * 16;
-    const int j = slot & 15;
-    const int blk = blk0 + u;
-    const int bc = min(blk, nb - 1);
-    const uint32_t* base = isx ? (j < 8 ? q : qn) : (const uint32_t*)sc;
-    return XsSlot{base + (isx ? bc * 8 + (j & 7) : bc), use && blk < nb && (isx || u < kBlkPerPart)};
-}
-
 // A k-part is processed by two wavefronts: sub-part h covers blocks
 // 8h .. 8h + 7 of it (the last slot of sub-part 1 is empty).
 constexpr int kSubUnits = 8;
-
-// One lane's sub-part: wv[0] = the 15 e8m0 bytes, wv[1 .. 8] = the nibble
-// blocks ub .. ub + 7 of the k-part.  Block 15 (the second sub-part's eighth
-// slot) does not exist: its weights load as zero and its pad exponent byte is
-// zero, so it adds exactly nothing.
-template <bool TRACE>
-CPB_DEV float part_dot_sub(const u32x4* wv, int ub, const u32x4* xs, const float* sb, int32_t* sums_out, int blk0,
-                           int nb) {
-    const MxConsts k = mx_consts();
-    const uint32_t ew[4] = {wv[0][0], wv[0][1], wv[0][2], wv[0][3]};
-    float acc = 0.0f;
-#pragma unroll
-    for (int i = 0; i < kSubUnits; i++) {
-        const int u = ub + i;
-        const u32x4* xb = xs + u * 4;
-        int S = mx_block_sum(wv[i + 1], xb[0], xb[1], xb[2], xb[3], k);
-        const uint32_t e = (ew[u >> 2] >> (8 * (u & 3))) & 0xffu;
-        acc = fmaf((float)S, e8m0_scale(e, sb[u]), acc);
-        if (TRACE && u < kBlkPerPart && blk0 + u < nb) sums_out[u] = S;
-        __builtin_amdgcn_sched_barrier(0);
-    }
-    return acc;
-}
 
 // Issue the sub-part's loads in stream order: the e8m0 unit, then units
 // 1 + ub .. 1 + ub + 7 (stride: 16-byte units between consecutive units);
@@ -89,7 +41,7 @@ CPB_DEV void wave_sync_lds() {
 // with an e2m1 weight and every partial sum is an integer below 2^16, so
 //     D[2*bo][n] + D[2*bo + 1][n] = sum_i 2*E2M1(w_ni) * x_i = S
 // exactly: the reference's int32 block sum (engine_gpt2.rs:194-228, KVI =
-// 2*E2M1 at :152) as a float, bit for bit what the v_perm + sdot4 decode gives.
+// 2*E2M1 at :152) as a float, bit for bit.
 //
 // Operand layouts (gfx950): A lane (m = l%16, g = l/16) holds K 16g..16g+15 in
 // bytes 0-15 and K 64+16g.. in bytes 16-31; B lane (n = l%16, g) holds K
@@ -212,8 +164,8 @@ CPB_DEV void window_sums(u32x4* r, AFn a, float* S) {
     S[3] = sb[1];
 }
 
-// The fma chain of part_dot_sub over block sums S[0..7] of blocks ub .. ub+7
-// (so the result is the same bit for bit).
+// A sub-part's fma chain over block sums S[0..7] of blocks ub .. ub+7: one
+// fma with 2^(e-128) * xsb per block, in block order.
 template <bool TRACE>
 CPB_DEV float sub_chain(const u32x4& ew4, int ub, const float* S, const float* sc, int32_t* sums_out, int blk0, int nb) {
     const uint32_t ew[4] = {ew4[0], ew4[1], ew4[2], ew4[3]};

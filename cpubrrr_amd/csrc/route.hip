@@ -17,7 +17,7 @@ namespace cpb {
 
 // Workgroup e: expert e's certified logit and its share of the activation
 // quantisation.
-__global__ __launch_bounds__(256) void k_route(RouteArgs a) {
+__global__ __launch_bounds__(320) void k_route(RouteArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     route_expert(a, blockIdx.x, gridDim.x, smem);
 }
@@ -25,7 +25,7 @@ __global__ __launch_bounds__(256) void k_route(RouteArgs a) {
 int launch_route(const RouteArgs* a, hipStream_t s) {
     if (a->n_expert > 256 || a->n_expert < a->top_k || a->top_k > 8 || a->d % 32 != 0 || a->d > 4096)
         return -22;
-    launch(k_route, dim3(a->n_expert), dim3(256), route_lds_bytes(a->d), s, *a);
+    launch(k_route, dim3(a->n_expert), dim3(route_threads(a->d)), route_lds_bytes(a->d), s, *a);
     return hipGetLastError() == hipSuccess ? 0 : -19;
 }
 

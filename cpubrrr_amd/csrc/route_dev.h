@@ -185,18 +185,18 @@ CPB_DEV_HOST inline size_t route_lds_bytes(int d) {
 
 // ---- router logit from unscaled products, shared by the decode route and
 // the batched router so both produce the same bits ----
-// Thread t (of a workgroup of nw waves) owns 16 consecutive elements.
-// Phase 1: P_j = W_j * x_j * g_j in fp64, this thread's sum, the wave's
-// inclusive scan; the wave total goes to dred[wv].  Phase 2 (after a
-// barrier): prefix sums for the bound; wave totals to dred[16 + wv] and
-// dred[32 + wv].  Final (after a barrier, one thread): logit and bound for
-// the norm scale inv.
+// Each thread of an element wave owns 16 consecutive elements; element wave
+// ws covers elements 1024*ws .. 1024*ws + 1023.  Phase 1: P_j = W_j * x_j *
+// g_j in fp64, this thread's sum, the wave's inclusive scan (wave total to
+// dred[ws]).  Phase 2 (no barrier needed): the wave-local prefix sums for the
+// bound, sum |prefix| to dred[16 + ws] and sum |P_j| to dred[32 + ws].  Final
+// (after a barrier, one thread): logit and bound for the norm scale inv.
 struct LogitThread {
     double P[16];
     double loc, absp, incl;
 };
-CPB_DEV void logit_phase1(const float* wf, const float* xf, const float* gf, LogitThread& L, double* dred) {
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+CPB_DEV void logit_phase1(const float* wf, const float* xf, const float* gf, LogitThread& L, double* dred, int ws) {
+    const int lane = threadIdx.x & 63;
     L.loc = 0.0;
     L.absp = 0.0;
 #pragma unroll
@@ -206,20 +206,17 @@ CPB_DEV void logit_phase1(const float* wf, const float* xf, const float* gf, Log
         L.absp += fabs(L.P[i]);
     }
     L.incl = wave_scan_f64(L.loc);
-    if (lane == 63) dred[wv] = L.incl;
+    if (lane == 63) dred[ws] = L.incl;
 }
-CPB_DEV void logit_phase2(const LogitThread& L, bool act, double* dred) {
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    double woff = 0.0;
-    for (int w2 = 0; w2 < wv; w2++) woff += dred[w2];
-    double run = woff + (L.incl - L.loc);
+CPB_DEV void logit_phase2(const LogitThread& L, bool act, double* dred, int ws) {
+    const int lane = threadIdx.x & 63;
+    double run = L.incl - L.loc;
     double sabs = 0.0;
 #pragma unroll
     for (int i = 0; i < 16; i++) { run += L.P[i]; sabs += act ? fabs(run) : 0.0; }
-    const double ws = wave_total63_f64(sabs);
-    const double wa = wave_total63_f64(L.absp);
-    if (lane == 63) { dred[16 + wv] = ws; dred[32 + wv] = wa; }
-    (void)nw;
+    const double s1 = wave_total63_f64(sabs);
+    const double s2 = wave_total63_f64(L.absp);
+    if (lane == 63) { dred[16 + ws] = s1; dred[32 + ws] = s2; }
 }
 // The reference computes xn_j = fl(fl(x_j * inv) * g_j), p_j = fl(W_j * xn_j)
 // and the serial fp32 chain acc = b; acc += p_j.  With t_j = inv * P_j
@@ -227,14 +224,22 @@ CPB_DEV void logit_phase2(const LogitThread& L, bool act, double* dred) {
 // u/(1-u) (sum_k |S_k| + n gamma_n A) of b + sum p_j (Higham, Accuracy and
 // Stability of Numerical Algorithms, 2nd ed., 4.2), where sum_k |S_k| <=
 // n|b| + inv sum_k |P-prefix_k| + n g3 inv A' and A <= |b| + (1 + g3) inv A',
-// A' = sum |P_j|.  n = d elements.
-CPB_DEV void logit_final(const double* dred, int nw, int d, double b, float inv, double* lstar, double* lbound) {
+// A' = sum |P_j|.  n = d elements.  A prefix inside element wave w is the
+// wave's offset O_w (the earlier waves' totals) plus a wave-local prefix, so
+// sum_k |P-prefix_k| <= sum_w (n_w |O_w| + sum_wave-local |prefix|), n_w =
+// the wave's element count.  gamma_n = nu/(1-nu) <= nu (1 + 2nu) (nu <= 1/2).
+CPB_DEV void logit_final(const double* dred, int nws, int d, double b, float inv, double* lstar, double* lbound) {
     double wtot = 0.0, SS = 0.0, AP = 0.0;
-    for (int w2 = 0; w2 < nw; w2++) { wtot += dred[w2]; SS += dred[16 + w2]; AP += dred[32 + w2]; }
+    for (int w2 = 0; w2 < nws; w2++) {
+        const int nw2 = min(max(d - 1024 * w2, 0), 1024);
+        SS += (double)nw2 * fabs(wtot) + dred[16 + w2];
+        wtot += dred[w2];
+        AP += dred[32 + w2];
+    }
     const double u = 5.9604644775390625e-08;  // 2^-24
     const double n = (double)d;
     const double g3 = 3.0 * u / (1.0 - 3.0 * u);
-    const double gam = n * u / (1.0 - n * u);
+    const double gam = n * u * (1.0 + 2.0 * n * u);
     const double sc = (double)inv;
     const double IA = sc * AP;
     const double ab = fabs(b);
@@ -244,82 +249,82 @@ CPB_DEV void logit_final(const double* dred, int nw, int d, double b, float inv,
 }
 
 // Workgroup-level body: expert e's logit + bound, and this workgroup's share
-// (blocks b with b % NEg == e) of the activation quantisation.  Any multiple
-// of 64 threads with blockDim.x * 16 >= d.
+// (blocks b with b % NEg == e) of the activation quantisation.  Wave 0 runs
+// the rmsnorm sum of squares; waves 1.. are element waves (route_threads(d)
+// threads in all).
 //
-// Thread t owns x[16t .. 16t+16): its x, norm weights and router weights
-// arrive in registers from one round of loads.  The gpt-oss sum of squares
-// (16 fma chains, chain q over x[16m + q], engine_gpt2.rs:710-726) runs in 16
-// lanes of wave 0 over a transposed LDS copy (chain q's elements
-// contiguous); the Qwen one (nt serial slices, engine_qwen2.rs:457-467) over
-// a plain copy.
-// The router logit is the fp64 sum of the unscaled products W_j * x_j * g_j
-// (one DPP scan, computed beside the sum-of-squares chain), scaled by the norm
-// scale once that is known; its bound covers every rounding of the
-// reference's fp32 path (see the bound below).
+// Thread 64 + t owns x[16t .. 16t+16): its x, norm weights and router weights
+// arrive in registers from one round of loads and x goes to LDS.  The gpt-oss
+// sum of squares (16 fma chains, chain q over x[16m + q],
+// engine_gpt2.rs:710-726) runs in 16 lanes of wave 0 over a transposed copy
+// (chain q's elements contiguous); the Qwen one (nt serial slices,
+// engine_qwen2.rs:457-467) over a plain copy.  Meanwhile the element waves
+// compute the router logit as the fp64 sum of the unscaled products W_j * x_j
+// * g_j (scaled by the norm scale once that is known; its bound covers every
+// rounding of the reference's fp32 path, see logit_final).
+CPB_DEV_HOST_INLINE int route_threads(int d) { return 64 + (d / 16 + 63) / 64 * 64; }
 CPB_DEV void route_expert(const RouteArgs& a, int e, int NEg, unsigned char* smem) {
-    const int tid = threadIdx.x, nth = blockDim.x, lane = tid & 63, wv = tid >> 6, nw = nth >> 6;
+    const int tid = threadIdx.x, nth = blockDim.x, lane = tid & 63, wv = tid >> 6;
     const int d = a.d;
+    const int et = tid - 64, ws = wv - 1, nws = (nth >> 6) - 1;     // element thread / wave
     float* xl = (float*)smem;                                  // transposed (gpt-oss) or plain (Qwen) x
     double* dred = (double*)(smem + route_lds_bytes(d) - sizeof(double) * 64 - 64);   // [64]
     float* sinv = (float*)(dred + 64);
     RSTAMP_DECL;
     RSTAMP(0);
 
-    const int j0 = tid * kRouteC;
-    const bool act = j0 < d;
+    const int j0 = et * kRouteC;
+    const bool act = et >= 0 && j0 < d;
     const uint32_t off = (uint32_t)(act ? j0 : 0) * 4;
     const __amdgpu_buffer_rsrc_t rx = buf_rsrc(a.x, (uint32_t)d * 4);
     const __amdgpu_buffer_rsrc_t rW = buf_rsrc(a.router_w + (size_t)e * d, (uint32_t)d * 4);
     const bool use_g = a.norm_w && a.apply_norm;
     const __amdgpu_buffer_rsrc_t rg = buf_rsrc(a.norm_w, use_g ? (uint32_t)d * 4 : 0u);
-    u32x4 xv[4], wq[4], gq[4];
-#pragma unroll
-    for (int k = 0; k < 4; k++) xv[k] = ld_dev16(rx, off + 16 * k);     // may come from this launch
-#pragma unroll
-    for (int k = 0; k < 4; k++) wq[k] = __builtin_amdgcn_raw_buffer_load_b128(rW, off + 16 * k, 0, 0);
-#pragma unroll
-    for (int k = 0; k < 4; k++) gq[k] = __builtin_amdgcn_raw_buffer_load_b128(rg, off + 16 * k, 0, 0);
-    const double b = a.router_b ? (double)a.router_b[e] : 0.0;
     float xf[16], gf[16], wf[16];
+    u32x4 xv[4] = {};
+    if (wv > 0) {
+        u32x4 wq[4], gq[4];
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-        xf[i] = act ? __uint_as_float(xv[i >> 2][i & 3]) : 0.0f;
-        gf[i] = use_g ? __uint_as_float(gq[i >> 2][i & 3]) : 1.0f;
-        wf[i] = act ? __uint_as_float(wq[i >> 2][i & 3]) : 0.0f;
+        for (int k = 0; k < 4; k++) xv[k] = ld_dev16(rx, off + 16 * k);     // may come from this launch
+#pragma unroll
+        for (int k = 0; k < 4; k++) wq[k] = __builtin_amdgcn_raw_buffer_load_b128(rW, off + 16 * k, 0, 0);
+#pragma unroll
+        for (int k = 0; k < 4; k++) gq[k] = __builtin_amdgcn_raw_buffer_load_b128(rg, off + 16 * k, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            xf[i] = act ? __uint_as_float(xv[i >> 2][i & 3]) : 0.0f;
+            gf[i] = use_g ? __uint_as_float(gq[i >> 2][i & 3]) : 1.0f;
+            wf[i] = act ? __uint_as_float(wq[i >> 2][i & 3]) : 0.0f;
+        }
     }
+    const double b = a.router_b ? (double)a.router_b[e] : 0.0;
     RSTAMP(1);
 
-    // ---- router logit, unscaled (the norm scale is applied at the end), so
-    // it runs beside the sum-of-squares chain instead of after it ----
-    LogitThread lt;
-    logit_phase1(wf, xf, gf, lt, dred);
-
-    // ---- rmsnorm scale ----
+    // ---- x into LDS for the sum of squares ----
     const int S = route_xt_stride(d);
-    if (a.apply_norm) {
+    if (a.apply_norm && wv > 0) {
         if (a.norm == 0) {
-            // chain q's element m = x[16m + q] lives in thread m, register q:
-            // transposed into LDS (chain q's elements contiguous)
+            // chain q's element m = x[16m + q] lives in element thread m,
+            // register q: transposed (chain q's elements contiguous)
             if (act) {
 #pragma unroll
-                for (int i = 0; i < 16; i++) xl[i * S + tid] = xf[i];
+                for (int i = 0; i < 16; i++) xl[i * S + et] = xf[i];
             }
             // zero padding past d/16: fma(0, 0, acc) leaves acc (>= 0) unchanged
-            for (int c = d / 16 + tid; c < S; c += nth) {
+            for (int c = d / 16 + et; c < S; c += nth - 64) {
 #pragma unroll
                 for (int i = 0; i < 16; i++) xl[i * S + c] = 0.0f;
             }
         } else if (act) {
 #pragma unroll
-            for (int k = 0; k < 4; k++) ((u32x4*)xl)[tid * 4 + k] = xv[k];
+            for (int k = 0; k < 4; k++) ((u32x4*)xl)[et * 4 + k] = xv[k];
         }
     }
     __syncthreads();
-    if (a.apply_norm && wv == 0) {
-        if (a.norm == 0) {
-            // lane q of wave 0 streams its row, every read issued ahead of
-            // the fma chain that consumes it
+    if (wv == 0) {
+        if (a.apply_norm && a.norm == 0) {
+            // lane q streams its row, every read issued ahead of the fma
+            // chain that consumes it
             const int nm = d / 16;                   // <= 256
             float acc = 0.0f;
             const float* row = xl + (lane & 15) * S;
@@ -351,7 +356,7 @@ CPB_DEV void route_expert(const RouteArgs& a, int e, int NEg, unsigned char* sme
             for (int l = 0; l < 4; l++) L[l] = (c16[l] + c16[4 + l]) + (c16[8 + l] + c16[12 + l]);
             const float ssq = (L[0] + L[1]) + (L[2] + L[3]);
             if (lane == 0) *sinv = 1.0f / sqrtf(ssq / (float)d + a.eps);
-        } else {
+        } else if (a.apply_norm) {
             // nt serial slices, then a serial sum of the partials (nt <= 64)
             const int nt = a.norm_nt, base = d / nt, rem = d % nt;
             float ps = 0.0f;
@@ -371,18 +376,26 @@ CPB_DEV void route_expert(const RouteArgs& a, int e, int NEg, unsigned char* sme
             for (int k = 0; k < nt; k++) tot += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ps), k));
             if (lane == 0) *sinv = 1.0f / sqrtf(tot / (float)d + a.eps);
         }
+        RSTAMP(6);
+    } else {
+        // ---- router logit, unscaled, beside the sum-of-squares chain ----
+        LogitThread lt;
+        logit_phase1(wf, xf, gf, lt, dred, ws);
+        logit_phase2(lt, act, dred, ws);
     }
-    // meanwhile (waves 1.., and wave 0 after its chain): prefix sums of the
-    // unscaled products for the error bound
-    logit_phase2(lt, act, dred);
     __syncthreads();
     const float inv = a.apply_norm ? *sinv : 1.0f;
     RSTAMP(2);
     if (tid == 0) {
         double ls = 0.0, lb = 0.0;
-        logit_final(dred, nw, d, b, inv, &ls, &lb);
+        logit_final(dred, nws, d, b, inv, &ls, &lb);
         st_dev(a.lstar + e, ls);
         st_dev(a.lbound + e, lb);
+        RSTAMP(4);
+    }
+    if (wv == 0) {
+        RSTAMP_FLUSH;
+        return;
     }
 
     // ---- xn = (x * inv) * w, and this workgroup's share of the activation
@@ -390,18 +403,18 @@ CPB_DEV void route_expert(const RouteArgs& a, int e, int NEg, unsigned char* sme
     float xn[16];
 #pragma unroll
     for (int i = 0; i < 16; i++) xn[i] = !a.apply_norm ? xf[i] : use_g ? (xf[i] * inv) * gf[i] : xf[i] * inv;
+    RSTAMP(7);
     if (a.qk == 0) {
         // Q8 per 32-block (engine_gpt2.rs:691-699): threads 2b, 2b+1 hold block b
         float m = 0.0f;
 #pragma unroll
         for (int i = 0; i < 16; i++) m = fmaxf(m, fabsf(xn[i]));
         m = fmaxf(m, pair_f32(m));
-        const int blk = tid >> 1;
+        const int blk = et >> 1;
         if (act && blk % NEg == e) {
             const float sc = fmaxf(1e-12f, m) / 127.0f;
-            uint32_t qp[4] = {0, 0, 0, 0};
-#pragma unroll
-            for (int i = 0; i < 16; i++) qp[i >> 2] |= (uint32_t)(uint8_t)q8_round(xn[i], sc) << (8 * (i & 3));
+            uint32_t qp[4];
+            q8_round16(xn, sc, qp);
             const __amdgpu_buffer_rsrc_t rn = buf_rsrc(a.xn, (uint32_t)d * 4);
 #pragma unroll
             for (int k = 0; k < 4; k++)
@@ -410,7 +423,7 @@ CPB_DEV void route_expert(const RouteArgs& a, int e, int NEg, unsigned char* sme
             st_dev16(buf_rsrc(a.xq, (uint32_t)d), (uint32_t)j0, u32x4{qp[0], qp[1], qp[2], qp[3]});
             // the block's matrix-core image: this thread writes K 16*par .. +15
             // of both halves (both threads of the pair are active here)
-            const int par = tid & 1;
+            const int par = et & 1;
             const uint32_t r0 = (uint32_t)pair_i32((int)(par ? qp[0] : qp[2]));
             const uint32_t r1 = (uint32_t)pair_i32((int)(par ? qp[1] : qp[3]));
             const uint32_t L0 = par ? r0 : qp[0], L1 = par ? r1 : qp[1];
@@ -425,7 +438,7 @@ CPB_DEV void route_expert(const RouteArgs& a, int e, int NEg, unsigned char* sme
             const __amdgpu_buffer_rsrc_t rim = buf_rsrc(a.ximg, (uint32_t)d * 2);
             st_dev16(rim, (uint32_t)(blk * 64 + 16 * par), u32x4{ih[0], ih[1], ih[2], ih[3]});
             st_dev16(rim, (uint32_t)(blk * 64 + 32 + 16 * par), u32x4{il[0], il[1], il[2], il[3]});
-            if ((tid & 1) == 0) st_dev(a.xsb + blk, sc);
+            if ((et & 1) == 0) st_dev(a.xsb + blk, sc);
         }
     } else {
         // Q8_K per 256 (engine_qwen2.rs:288-300): the 16 threads of a DPP row
@@ -434,16 +447,13 @@ CPB_DEV void route_expert(const RouteArgs& a, int e, int NEg, unsigned char* sme
 #pragma unroll
         for (int i = 0; i < 16; i++) m = fmaxf(m, fabsf(xn[i]));
         m = row_max_f32(m);
-        const int sb = tid >> 4;
+        const int sb = et >> 4;
         const float sc = fmaxf(1e-12f, m) / 127.0f;
-        uint32_t qp[4] = {0, 0, 0, 0};
+        uint32_t qp[4];
+        q8_round16(xn, sc, qp);
         int s32 = 0;
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const int qv = q8_round(xn[i], sc);
-            s32 += qv;
-            qp[i >> 2] |= (uint32_t)(uint8_t)qv << (8 * (i & 3));
-        }
+        for (int i = 0; i < 16; i++) s32 += (int)(int8_t)(qp[i >> 2] >> (8 * (i & 3)));
         s32 += pair_i32(s32);
         if (act && sb % NEg == e) {
             const __amdgpu_buffer_rsrc_t rn = buf_rsrc(a.xn, (uint32_t)d * 4);
@@ -452,13 +462,10 @@ CPB_DEV void route_expert(const RouteArgs& a, int e, int NEg, unsigned char* sme
                 st_dev16(rn, off + 16 * k, u32x4{__float_as_uint(xn[4 * k]), __float_as_uint(xn[4 * k + 1]),
                                                  __float_as_uint(xn[4 * k + 2]), __float_as_uint(xn[4 * k + 3])});
             st_dev16(buf_rsrc(a.xq, (uint32_t)d), (uint32_t)j0, u32x4{qp[0], qp[1], qp[2], qp[3]});
-            if ((tid & 15) == 0) st_dev(a.xsb + sb, sc);
-            if ((tid & 1) == 0) st_dev(a.xsum + (tid >> 1), s32);
+            if ((et & 15) == 0) st_dev(a.xsb + sb, sc);
+            if ((et & 1) == 0) st_dev(a.xsum + (et >> 1), s32);
         }
     }
-    RSTAMP(3);
-    RSTAMP(5);
-    RSTAMP_FLUSH;
 }
 
 
