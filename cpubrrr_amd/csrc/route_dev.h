@@ -298,6 +298,17 @@ CPB_DEV void route_expert(const RouteArgs& a, int e, int NEg, unsigned char* sme
         }
     }
     const double b = a.router_b ? (double)a.router_b[e] : 0.0;
+    // Q8 (qk == 0): element thread et quantises element et % 32 of this
+    // workgroup's block slot et / 32 (the blocks b with b % NEg == e); its
+    // x and norm weight are fetched now
+    const int nbq = d / 32, qslots = (nth - 64) / 32;
+    const int qb0 = et >> 5, qj = et & 31;
+    float qx = 0.0f, qg = 1.0f;
+    if (a.qk == 0 && wv > 0 && e + NEg * qb0 < nbq) {
+        const int j = (e + NEg * qb0) * 32 + qj;
+        qx = ld_dev(a.x + j);
+        if (use_g) qg = a.norm_w[j];
+    }
     RSTAMP(1);
 
     // ---- x into LDS for the sum of squares ----
@@ -400,49 +411,35 @@ CPB_DEV void route_expert(const RouteArgs& a, int e, int NEg, unsigned char* sme
 
     // ---- xn = (x * inv) * w, and this workgroup's share of the activation
     // quantisation ----
-    float xn[16];
-#pragma unroll
-    for (int i = 0; i < 16; i++) xn[i] = !a.apply_norm ? xf[i] : use_g ? (xf[i] * inv) * gf[i] : xf[i] * inv;
-    RSTAMP(7);
     if (a.qk == 0) {
-        // Q8 per 32-block (engine_gpt2.rs:691-699): threads 2b, 2b+1 hold block b
-        float m = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 16; i++) m = fmaxf(m, fabsf(xn[i]));
-        m = fmaxf(m, pair_f32(m));
-        const int blk = et >> 1;
-        if (act && blk % NEg == e) {
-            const float sc = fmaxf(1e-12f, m) / 127.0f;
-            uint32_t qp[4];
-            q8_round16(xn, sc, qp);
-            const __amdgpu_buffer_rsrc_t rn = buf_rsrc(a.xn, (uint32_t)d * 4);
-#pragma unroll
-            for (int k = 0; k < 4; k++)
-                st_dev16(rn, off + 16 * k, u32x4{__float_as_uint(xn[4 * k]), __float_as_uint(xn[4 * k + 1]),
-                                                 __float_as_uint(xn[4 * k + 2]), __float_as_uint(xn[4 * k + 3])});
-            st_dev16(buf_rsrc(a.xq, (uint32_t)d), (uint32_t)j0, u32x4{qp[0], qp[1], qp[2], qp[3]});
-            // the block's matrix-core image: this thread writes K 16*par .. +15
-            // of both halves (both threads of the pair are active here)
-            const int par = et & 1;
-            const uint32_t r0 = (uint32_t)pair_i32((int)(par ? qp[0] : qp[2]));
-            const uint32_t r1 = (uint32_t)pair_i32((int)(par ? qp[1] : qp[3]));
-            const uint32_t L0 = par ? r0 : qp[0], L1 = par ? r1 : qp[1];
-            const uint32_t H0 = par ? qp[2] : r0, H1 = par ? qp[3] : r1;
-            uint32_t ih[4], il[4];
-#pragma unroll
-            for (int jj = 0; jj < 4; jj++) {
-                const uint32_t v = perm(jj < 2 ? H0 : H1, jj < 2 ? L0 : L1, (jj & 1) ? 0x07030602u : 0x05010400u);
-                ih[jj] = img_hi(v);
-                il[jj] = img_lo(v);
+        // Q8 per 32-block (engine_gpt2.rs:691-699): 32 lanes per block, the
+        // block maximum over the lane group, then each lane's xq byte, its two
+        // image bytes (K offset 2j or 2(j - 16) + 1 for element j) and xn
+        for (int qb = qb0; e + NEg * qb < nbq; qb += qslots) {
+            const int blk = e + NEg * qb, j = blk * 32 + qj;
+            if (qb != qb0) {
+                qx = ld_dev(a.x + j);
+                qg = use_g ? a.norm_w[j] : 1.0f;
             }
-            const __amdgpu_buffer_rsrc_t rim = buf_rsrc(a.ximg, (uint32_t)d * 2);
-            st_dev16(rim, (uint32_t)(blk * 64 + 16 * par), u32x4{ih[0], ih[1], ih[2], ih[3]});
-            st_dev16(rim, (uint32_t)(blk * 64 + 32 + 16 * par), u32x4{il[0], il[1], il[2], il[3]});
-            if ((et & 1) == 0) st_dev(a.xsb + blk, sc);
+            const float xnv = !a.apply_norm ? qx : use_g ? (qx * inv) * qg : qx * inv;
+            float m = row_max_f32(fabsf(xnv));
+            m = fmaxf(m, __shfl_xor(m, 16));
+            const float sc = fmaxf(1e-12f, m) / 127.0f;
+            const int8_t qv = q8_round(xnv, sc);
+            a.xn[j] = xnv;
+            a.xq[j] = qv;
+            const int kpos = qj < 16 ? 2 * qj : 2 * (qj - 16) + 1;
+            const uint32_t qb8 = (uint32_t)(uint8_t)qv;
+            a.ximg[blk * 64 + kpos] = (uint8_t)img_hi(qb8);
+            a.ximg[blk * 64 + 32 + kpos] = (uint8_t)img_lo(qb8);
+            if (qj == 0) a.xsb[blk] = sc;
         }
     } else {
         // Q8_K per 256 (engine_qwen2.rs:288-300): the 16 threads of a DPP row
         // hold one superblock; per-32 sums from thread pairs
+        float xn[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) xn[i] = !a.apply_norm ? xf[i] : use_g ? (xf[i] * inv) * gf[i] : xf[i] * inv;
         float m = 0.0f;
 #pragma unroll
         for (int i = 0; i < 16; i++) m = fmaxf(m, fabsf(xn[i]));
