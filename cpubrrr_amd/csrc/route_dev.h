@@ -171,11 +171,56 @@ CPB_DEV void st_dev16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, u32x4 v) {
     __builtin_amdgcn_raw_buffer_store_b128(v, r, byte_off, 0, 16);
 }
 
+// ---- LDS streaming for the sum-of-squares chain ----
+// The compiler's wait insertion drains every LDS read before any use inside
+// the loop below; these issue eight 16-byte reads and wait for all but the
+// newest eight explicitly, so one group's reads overlap the previous group's
+// fma chain.  (LDS reads of a wave complete in order.)
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+CPB_DEV uint32_t lds_addr(const float* p) {
+    return (uint32_t)(size_t)(const __attribute__((address_space(3))) float*)p;
+}
+CPB_DEV void lds_read8(f32x4 (&o)[8], uint32_t a) {
+    asm volatile(
+        "ds_read_b128 %0, %8\n\t"
+        "ds_read_b128 %1, %8 offset:16\n\t"
+        "ds_read_b128 %2, %8 offset:32\n\t"
+        "ds_read_b128 %3, %8 offset:48\n\t"
+        "ds_read_b128 %4, %8 offset:64\n\t"
+        "ds_read_b128 %5, %8 offset:80\n\t"
+        "ds_read_b128 %6, %8 offset:96\n\t"
+        "ds_read_b128 %7, %8 offset:112"
+        : "=&v"(o[0]), "=&v"(o[1]), "=&v"(o[2]), "=&v"(o[3]), "=&v"(o[4]), "=&v"(o[5]), "=&v"(o[6]), "=&v"(o[7])
+        : "v"(a)
+        : "memory");
+}
+// o (read before the newest eight LDS reads) has landed
+CPB_DEV void lds_wait_older8(f32x4 (&o)[8]) {
+    asm volatile("s_waitcnt lgkmcnt(8)"
+                 : "+v"(o[0]), "+v"(o[1]), "+v"(o[2]), "+v"(o[3]), "+v"(o[4]), "+v"(o[5]), "+v"(o[6]), "+v"(o[7])
+                 :
+                 : "memory");
+}
+CPB_DEV void lds_wait_all() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+CPB_DEV float sumsq_chain(const f32x4 (&g)[8], float acc) {
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+        acc = fmaf(g[u][0], g[u][0], acc);
+        acc = fmaf(g[u][1], g[u][1], acc);
+        acc = fmaf(g[u][2], g[u][2], acc);
+        acc = fmaf(g[u][3], g[u][3], acc);
+    }
+    return acc;
+}
+
+
 constexpr int kRouteC = 16;         // consecutive elements per thread in route_expert
 
 // LDS bytes route_expert needs (any block size; d <= 4096)
-// transposed x: 16 rows of d/16 values, padded so the 16 lanes' 16-byte
-// reads spread over the banks and the look-ahead reads stay inside
+// transposed x: 16 rows of d/16 values, zero padded to at least d/16 + 32
+// (whole 32-value groups of the chain read zeros past d/16) and offset so
+// the 16 lanes' 16-byte reads spread over the banks; the chain's one-group
+// look-ahead past the last row lands in the reduction area behind it
 CPB_DEV_HOST inline int route_xt_stride(int d) { return (d / 16 + 32 + 63) / 64 * 64 + 4; }
 CPB_DEV_HOST inline size_t route_lds_bytes(int d) {
     const size_t xt = sizeof(float) * 16 * (size_t)route_xt_stride(d);
@@ -332,32 +377,31 @@ CPB_DEV void route_expert(const RouteArgs& a, int e, int NEg, unsigned char* sme
         }
     }
     __syncthreads();
+    RSTAMP(3);
     if (wv == 0) {
         if (a.apply_norm && a.norm == 0) {
-            // lane q streams its row, every read issued ahead of the fma
-            // chain that consumes it
+            // lane q streams its row: the next group's reads are issued before
+            // the current group's fmas (software pipelined; the scheduling
+            // barriers keep the compiler from regrouping them).  The zero
+            // padding past d/16 leaves acc unchanged (fma(0, 0, acc) = acc,
+            // acc >= 0), so whole groups run without a bound check.
             const int nm = d / 16;                   // <= 256
             float acc = 0.0f;
-            const float* row = xl + (lane & 15) * S;
-            constexpr int G = 32;                    // values per group (8 reads)
-            float4 cur[G / 4], nxt[G / 4];
-#pragma unroll
-            for (int u = 0; u < G / 4; u++) cur[u] = *(const float4*)(row + 4 * u);
-            for (int m = 0; m < nm; m += G) {
-#pragma unroll
-                for (int u = 0; u < G / 4; u++) nxt[u] = *(const float4*)(row + m + G + 4 * u);
-#pragma unroll
-                for (int u = 0; u < G / 4; u++) {
-                    if (m + 4 * u < nm) {            // the padding reads as zero
-                        acc = fmaf(cur[u].x, cur[u].x, acc);
-                        acc = fmaf(cur[u].y, cur[u].y, acc);
-                        acc = fmaf(cur[u].z, cur[u].z, acc);
-                        acc = fmaf(cur[u].w, cur[u].w, acc);
-                    }
-                }
-#pragma unroll
-                for (int u = 0; u < G / 4; u++) cur[u] = nxt[u];
+            uint32_t ra = lds_addr(xl + (lane & 15) * S);
+            f32x4 ga[8], gb[8];                      // ping-pong groups of 32 values
+            lds_read8(ga, ra);
+            for (int m = 0;; m += 64) {
+                lds_read8(gb, ra + 128);
+                lds_wait_older8(ga);
+                acc = sumsq_chain(ga, acc);
+                if (m + 32 >= nm) break;
+                lds_read8(ga, ra + 256);
+                lds_wait_older8(gb);
+                acc = sumsq_chain(gb, acc);
+                if (m + 64 >= nm) break;
+                ra += 256;
             }
+            lds_wait_all();
             // chain q = 4v + l -> acc[v][l]; L[l] = (a0 + a1) + (a2 + a3); s = (L0 + L1) + (L2 + L3)
             float c16[16];
 #pragma unroll
