@@ -47,6 +47,10 @@ __global__ __launch_bounds__(128 * kMaxParts) __attribute__((amdgpu_waves_per_eu
     const int ub = kSubUnits * hh;
     const int tiles = a.dff / 32;
     const int ei = blockIdx.x / tiles, t = blockIdx.x % tiles;
+    // every argument the prologue needs, loaded in one batch up front (else
+    // the selection's fields arrive in a second kernarg round trip)
+    asm volatile("" ::"s"(a.sel.lstar), "s"(a.sel.lbound), "s"(a.sel.ne), "s"(a.sel.k), "s"(a.ximg), "s"(a.xsb),
+                 "s"(a.nb), "s"(a.w));
     RSTAMP_DECL;
     RSTAMP(0);
     float* red = (float*)smem;                                 // [W][64]
@@ -57,10 +61,14 @@ __global__ __launch_bounds__(128 * kMaxParts) __attribute__((amdgpu_waves_per_eu
     xw[0] = load_win_act(ri, blk0 + ub, ub, a.nb);
     xw[1] = load_win_act(ri, blk0 + ub + 4, ub + 4, a.nb);
     float xsc[kSubUnits];
+    {
+        const __amdgpu_buffer_rsrc_t rs = buf_rsrc(a.xsb, (uint32_t)(a.nb * 4));
 #pragma unroll
-    for (int i = 0; i < kSubUnits; i++) {
-        const int u = ub + i;
-        xsc[i] = (u < kBlkPerPart && blk0 + u < a.nb) ? a.xsb[blk0 + u] : 0.0f;
+        for (int i = 0; i < kSubUnits; i++) {
+            const int u = ub + i;
+            const bool ok = u < kBlkPerPart && blk0 + u < a.nb;
+            xsc[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, ok ? (uint32_t)(blk0 + u) * 4 : kOffNone, 0, 0));
+        }
     }
     int e;
     if (a.sel.lstar) {
@@ -69,7 +77,7 @@ __global__ __launch_bounds__(128 * kMaxParts) __attribute__((amdgpu_waves_per_eu
         __shared__ unsigned long long last_start, last_pre;
         if (w == W - 1 && lane == 0) last_start = wall_clock64();
 #endif
-        if (w == 0) select_topk_wave(a.sel, smem, &ssel);
+        if (w == 0) select_topk_wave(a.sel, smem, &ssel, false, a.stamps ? a.stamps + 4096 + (size_t)blockIdx.x * 4 : nullptr);
         RSTAMP(5);
 #ifdef CPB_DECODE_STAMPS
         if (w == W - 1 && lane == 0) last_pre = wall_clock64();

@@ -169,6 +169,11 @@ CPB_DEV void select_exact_path(unsigned char* lds, int NE, int K, const float* r
     exact_reselect(sL, sH, sSel, NE, K, router_w, router_b, xn, d, xst);
 }
 
+// One wavefront's LDS writes visible to its later LDS reads (a wave's LDS
+// operations complete in order; unlike a fence this does not wait for the
+// wave's outstanding global loads).
+CPB_DEV void wave_lds_order() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
 // Top-k by one wavefront with every value in registers: lane l holds experts
 // l + 64j (j < 4).  The provisional ranking uses 32-bit keys (the logit
 // rounded to fp32, its top 24 bits, then 255 - index so that equal keys pick
@@ -178,10 +183,57 @@ CPB_DEV void select_exact_path(unsigned char* lds, int NE, int K, const float* r
 // ranking that truncation made wrong cannot pass it, and then the exact path
 // (the reference's serial logits) decides.  Softmax over the k in the
 // reference's order.  Writes *out (LDS) from lanes < K.
-CPB_DEV void select_topk_wave(const SelectIn& s, unsigned char* lds, Selection* out, bool publish_logits = false) {
+#ifdef CPB_DECODE_STAMPS
+#define SSTAMP(i) do { if (st && (threadIdx.x & 63) == 0) st[i] = wall_clock64(); } while (0)
+#else
+#define SSTAMP(i) do { } while (0)
+#endif
+CPB_DEV void select_topk_wave(const SelectIn& s, unsigned char* lds, Selection* out, bool publish_logits = false,
+                              unsigned long long* st = nullptr) {
     const int lane = threadIdx.x & 63;
+    SSTAMP(0);
     const int NE = s.ne, K = s.k;
     double lv[4], bv[4];
+    float lf[4];
+    int my_e = 0;
+    float my_l = 0.0f;
+    bool bad;
+    if (NE <= 64) {
+        // one expert per lane; rank = number of larger keys, read back from
+        // LDS (no serial rounds); rank r < K is selection slot r
+        const bool valid = lane < NE;
+        lv[0] = valid ? s.lstar[lane] : 0.0;
+        bv[0] = valid ? s.lbound[lane] : 0.0;
+        lv[1] = lv[2] = lv[3] = bv[1] = bv[2] = bv[3] = 0.0;
+        lf[0] = (float)lv[0];
+        lf[1] = lf[2] = lf[3] = 0.0f;
+        const uint32_t key = valid ? ((float_key(lf[0]) & 0xFFFFFF00u) | (uint32_t)(255 - lane)) : 0u;
+        const float lo = f32_down(lv[0] - bv[0]);
+        const float hi = valid ? f32_up(lv[0] + bv[0]) : -__builtin_inff();
+        SSTAMP(1);
+        uint32_t* skey = (uint32_t*)lds;                  // [64]
+        int* sE = (int*)(skey + 64);                      // [8] by rank
+        float* sLf = (float*)(sE + 8);                    // [8]
+        float* sHi = sLf + 8;                             // [8]
+        skey[lane] = key;
+        wave_lds_order();
+        int rank = 0;
+        for (int j = 0; j < NE; j += 4) {
+            const u32x4 k4 = *(const u32x4*)(skey + j);
+            rank += (k4[0] > key) + (k4[1] > key) + (k4[2] > key) + (k4[3] > key);
+        }
+        const bool sel = valid && rank < K;
+        if (sel) { sE[rank] = lane; sLf[rank] = lf[0]; sHi[rank] = hi; }
+        // upper bound of every unselected expert
+        const float mu = key_float(wave_max_u32(float_key(sel ? -__builtin_inff() : hi)));
+        wave_lds_order();
+        float later = mu;
+        if (sel)
+            for (int j = rank + 1; j < K; j++) later = fmaxf(later, sHi[j]);
+        bad = __any(sel && !(lo > later));
+        if (lane < K) { my_e = sE[lane]; my_l = sLf[lane]; }
+        wave_lds_order();
+    } else {
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         const int e = lane + 64 * j;
@@ -189,7 +241,7 @@ CPB_DEV void select_topk_wave(const SelectIn& s, unsigned char* lds, Selection* 
         bv[j] = e < NE ? s.lbound[e] : 0.0;
     }
     uint32_t key[4];
-    float lf[4], lo[4], hi[4];
+    float lo[4], hi[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         const int e = lane + 64 * j;
@@ -198,8 +250,8 @@ CPB_DEV void select_topk_wave(const SelectIn& s, unsigned char* lds, Selection* 
         lo[j] = f32_down(lv[j] - bv[j]);
         hi[j] = e < NE ? f32_up(lv[j] + bv[j]) : -__builtin_inff();
     }
-    int my_e = 0;
-    float my_l = 0.0f, my_lo = 0.0f, my_hi = -__builtin_inff();
+    SSTAMP(1);
+    float my_lo = 0.0f, my_hi = -__builtin_inff();
     for (int i = 0; i < K; i++) {
         const uint32_t m = wave_max_u32(max(max(key[0], key[1]), max(key[2], key[3])));
         const int bi = 255 - (int)(m & 0xFFu);
@@ -223,7 +275,9 @@ CPB_DEV void select_topk_wave(const SelectIn& s, unsigned char* lds, Selection* 
         const float hj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_hi), j));
         if (j > lane) later = fmaxf(later, hj);
     }
-    const bool bad = __any(lane < K && !(my_lo > later));
+    bad = __any(lane < K && !(my_lo > later));
+    }
+    SSTAMP(2);
     if (bad) {
         double* sL = (double*)lds;
         double* sH = sL + NE;
@@ -253,6 +307,7 @@ CPB_DEV void select_topk_wave(const SelectIn& s, unsigned char* lds, Selection* 
         out->wts[lane] = wt;
     }
     if (lane == 0) out->fallback = bad ? 1 : 0;
+    SSTAMP(3);
     // trace outputs and the routed ids / weights for later launches (by one
     // workgroup, or by this one when it alone selects for its token)
     if (publish_logits) {
