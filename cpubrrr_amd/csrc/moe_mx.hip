@@ -53,9 +53,13 @@ __global__ __launch_bounds__(128 * kMaxParts) __attribute__((amdgpu_waves_per_eu
                  "s"(a.nb), "s"(a.w));
     RSTAMP_DECL;
     RSTAMP(0);
+    SelectPre pre{0.0, 0.0};
+    if (a.sel.lstar && w == 0) pre = select_preload(a.sel);
     float* red = (float*)smem;                                 // [W][64]
     const int blk0 = q * kBlkPerPart;
-    // activations: the two windows' A operands and the 8 block scales
+    // activations: the two windows' A operands and the 8 block scales (issued
+    // before the weights: requests queued behind a CU's weight stream would
+    // land after it)
     const __amdgpu_buffer_rsrc_t ri = buf_rsrc(a.ximg, (uint32_t)(a.nb * kImgBytes));
     WinAct xw[2];
     xw[0] = load_win_act(ri, blk0 + ub, ub, a.nb);
@@ -73,21 +77,10 @@ __global__ __launch_bounds__(128 * kMaxParts) __attribute__((amdgpu_waves_per_eu
     int e;
     if (a.sel.lstar) {
         __shared__ Selection ssel;
-#ifdef CPB_DECODE_STAMPS
-        __shared__ unsigned long long last_start, last_pre;
-        if (w == W - 1 && lane == 0) last_start = wall_clock64();
-#endif
-        if (w == 0) select_topk_wave(a.sel, smem, &ssel, false, a.stamps ? a.stamps + 4096 + (size_t)blockIdx.x * 4 : nullptr);
+        if (w == 0) select_topk_wave(a.sel, smem, &ssel, false, a.stamps ? a.stamps + 4096 + (size_t)blockIdx.x * 4 : nullptr, &pre);
         RSTAMP(5);
-#ifdef CPB_DECODE_STAMPS
-        if (w == W - 1 && lane == 0) last_pre = wall_clock64();
-#endif
-        // LDS-only barrier: the activation loads above need not have landed
+        // barrier on LDS only (s_barrier without a wait for the activation loads)
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-#ifdef CPB_DECODE_STAMPS
-        rst_[6] = last_start;
-        rst_[7] = last_pre;
-#endif
         // a plain LDS read: merged with the global read below into one flat
         // load it would queue behind the CU's outstanding weight loads
         e = uniform(((const __attribute__((address_space(3))) int*)ssel.ids)[ei]);
@@ -110,21 +103,32 @@ __global__ __launch_bounds__(128 * kMaxParts) __attribute__((amdgpu_waves_per_eu
     __syncthreads();
     if (w != 0) return;
     RSTAMP(3);
+    float pr[2 * kMaxParts];
+#pragma unroll
+    for (int p = 0; p < 2 * kMaxParts; p++) pr[p] = p < W ? red[p * 64 + lane] : 0.0f;
     float v = 0.0f;
-    for (int p = 0; p < W; p++) v += red[p * 64 + lane];
+#pragma unroll
+    for (int p = 0; p < 2 * kMaxParts; p++)
+        if (p < W) v += pr[p];
     if (bias) v += bias_pf;
     if (TRACE) a.gu[(size_t)(ei * 2 + isup) * a.dff + row] = v;
     // SwiGLU-OAI (engine_gpt2.rs:887-906) in lanes 0-31: gate row r, up row r from lane r+32
-    const float u = __shfl_down(v, 32);
+    float vd = v, u = v;
+    swap32f(vd, u);                      // lanes 0-31: u = v of lane + 32
     float h = 0.0f;
     if (!isup) {
         const float xg = fminf(v, a.limit);
         const float yu = fminf(fmaxf(u, -a.limit), a.limit);
         h = (xg / (1.0f + expf(-a.alpha * xg))) * (yu + 1.0f);
     }
-    float m = isup ? 0.0f : fabsf(h);
-#pragma unroll
-    for (int s = 16; s >= 1; s >>= 1) m = fmaxf(m, __shfl_xor(m, s));
+    // block maximum over the 32 gate lanes: DPP within 16-lane rows, then the
+    // partner row by a permlane swap (no LDS round trips)
+    float m = row_max_f32(isup ? 0.0f : fabsf(h));
+    {
+        float ma = m, mb = m;
+        swap16f(ma, mb);
+        m = fmaxf(m, (lane & 16) ? ma : mb);
+    }
     const float sc = fmaxf(1e-12f, m) / 127.0f;
     if (!isup) {
         const int8_t qv = q8_round(h, sc);
@@ -194,8 +198,13 @@ __global__ __launch_bounds__(128 * kMaxParts) void k_down_mx(DownArgs a) {
     __syncthreads();
     if (w != 0) return;
     RSTAMP(2);
+    float pr[2 * kMaxParts];
+#pragma unroll
+    for (int p = 0; p < 2 * kMaxParts; p++) pr[p] = p < W ? red[p * 64 + lane] : 0.0f;
     float v = 0.0f;
-    for (int p = 0; p < W; p++) v += red[p * 64 + lane];
+#pragma unroll
+    for (int p = 0; p < 2 * kMaxParts; p++)
+        if (p < W) v += pr[p];
     if (a.down_b) v += dnb_pf;
     if (TRACE) a.dn[(size_t)ei * a.d + row] = v;
     vv[lane] = v;

@@ -188,8 +188,20 @@ CPB_DEV void wave_lds_order() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"
 #else
 #define SSTAMP(i) do { } while (0)
 #endif
+// The intervals of a <= 64-expert selection, one per lane, loaded ahead (a
+// caller issues these before its other loads so that the selection does not
+// wait for them: a wave's loads complete in order).
+struct SelectPre {
+    double lv, bv;
+};
+CPB_DEV SelectPre select_preload(const SelectIn& s) {
+    const int lane = threadIdx.x & 63;
+    const bool ok = s.ne <= 64 && lane < s.ne;
+    return SelectPre{ok ? s.lstar[lane] : 0.0, ok ? s.lbound[lane] : 0.0};
+}
+
 CPB_DEV void select_topk_wave(const SelectIn& s, unsigned char* lds, Selection* out, bool publish_logits = false,
-                              unsigned long long* st = nullptr) {
+                              unsigned long long* st = nullptr, const SelectPre* pre = nullptr) {
     const int lane = threadIdx.x & 63;
     SSTAMP(0);
     const int NE = s.ne, K = s.k;
@@ -202,8 +214,8 @@ CPB_DEV void select_topk_wave(const SelectIn& s, unsigned char* lds, Selection* 
         // one expert per lane; rank = number of larger keys, read back from
         // LDS (no serial rounds); rank r < K is selection slot r
         const bool valid = lane < NE;
-        lv[0] = valid ? s.lstar[lane] : 0.0;
-        bv[0] = valid ? s.lbound[lane] : 0.0;
+        lv[0] = pre ? pre->lv : valid ? s.lstar[lane] : 0.0;
+        bv[0] = pre ? pre->bv : valid ? s.lbound[lane] : 0.0;
         lv[1] = lv[2] = lv[3] = bv[1] = bv[2] = bv[3] = 0.0;
         lf[0] = (float)lv[0];
         lf[1] = lf[2] = lf[3] = 0.0f;
