@@ -156,12 +156,8 @@ __global__ __launch_bounds__(128 * kMaxParts) void k_down_mx(DownArgs a) {
     const int ub = kSubUnits * hh;
     const int tiles = a.d / RT, t = blockIdx.x;
     const int ei = lane / RT, rr = lane % RT, row = t * RT + rr;
-    int es[4];
-#pragma unroll
-    for (int k = 0; k < 4; k++) es[k] = __builtin_amdgcn_readfirstlane(a.ids[k < K ? k : 0]);
     RSTAMP_DECL;
     RSTAMP(0);
-    const int e = ei == 0 ? es[0] : ei == 1 ? es[1] : ei == 2 ? es[2] : es[3];
     float* red = (float*)smem;                                 // [W][64]
     float* vv = red + W * 64;                                  // [64]
     const int blk0 = q * kBlkPerPart;
@@ -176,11 +172,22 @@ __global__ __launch_bounds__(128 * kMaxParts) void k_down_mx(DownArgs a) {
             xa[h][g] = load_act_frag(ri, (uint32_t)(((16 * g) / RT) * a.nbf * kImgBytes), blk0 + ub + 4 * h, ub + 4 * h,
                                      a.nbf);
     float xsc[kSubUnits];
+    {
+        const __amdgpu_buffer_rsrc_t rs = buf_rsrc(a.hsb, (uint32_t)(K * a.nbf * 4));
 #pragma unroll
-    for (int i = 0; i < kSubUnits; i++) {
-        const int u = ub + i;
-        xsc[i] = (u < kBlkPerPart && blk0 + u < a.nbf) ? a.hsb[(size_t)ei * a.nbf + blk0 + u] : 0.0f;
+        for (int i = 0; i < kSubUnits; i++) {
+            const int u = ub + i;
+            const bool ok = u < kBlkPerPart && blk0 + u < a.nbf;
+            xsc[i] = __uint_as_float(
+                __builtin_amdgcn_raw_buffer_load_b32(rs, ok ? (uint32_t)(ei * a.nbf + blk0 + u) * 4 : kOffNone, 0, 0));
+        }
     }
+    // the routed experts (written by the gate/up launch; scalar loads, which
+    // the activation requests above need not wait for)
+    int es[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) es[k] = __builtin_amdgcn_readfirstlane(a.ids[k < K ? k : 0]);
+    const int e = ei == 0 ? es[0] : ei == 1 ? es[1] : ei == 2 ? es[2] : es[3];
     u32x4 wv[1 + kSubUnits];
     load_sub(a.w + (((((size_t)e * tiles + t) * P + q) * kUnits) * RT) + rr, RT, ub, wv);
     float dnb_pf = 0.0f, x_pf = 0.0f, w_pf[4];
