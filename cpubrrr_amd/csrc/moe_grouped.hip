@@ -39,6 +39,8 @@
 #include "route_dev.h"
 #include "select.h"
 
+#include <algorithm>
+
 namespace cpb {
 
 typedef int v8i_g __attribute__((ext_vector_type(8)));
@@ -149,7 +151,7 @@ __global__ __launch_bounds__(64) void k_select_batch(GroupedArgs a) {
     si.xn = a.xn + (size_t)t * a.d;
     si.ne = a.ne; si.k = a.k; si.d = a.d;
     si.logits = a.logits + (size_t)t * a.ne;      // written by every workgroup: one per token
-    select_topk_wave(si, smem, &sel, true);
+    select_topk_wave<4, 2>(si, smem, &sel, true);
     if (lane < a.k) {
         a.ids[(size_t)t * a.k + lane] = sel.ids[lane];
         a.wts[(size_t)t * a.k + lane] = sel.wts[lane];
@@ -158,40 +160,58 @@ __global__ __launch_bounds__(64) void k_select_batch(GroupedArgs a) {
 }
 
 // ---- 4. group the (token, slot) pairs by expert (stable), tile table ----
+// The pairs' expert ids are staged in LDS as bytes (ne <= 256) in chunks of
+// kGroupChunk, so the per-expert ballot scans read LDS, not global memory.
+constexpr int kGroupChunk = 16384;
 __global__ __launch_bounds__(1024) void k_group(GroupedArgs a) {
-    __shared__ int cnt_l[256], off_l[256], toff_l[256];
-    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
+    __shared__ int cnt_l[256], off_l[256], toff_l[256], pos_l[256];
+    __shared__ uint8_t ids_l[kGroupChunk];
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, nw = blockDim.x >> 6;
     const int np = a.n_tok * a.k;
     const uint64_t lt = lane ? (~0ull >> (64 - lane)) : 0ull;
-    for (int e = w; e < a.ne; e += nw) {
-        int c = 0;
-        for (int base = 0; base < np; base += 64) {
-            const int p = base + lane;
-            c += __popcll(__ballot(p < np && a.ids[p] == e));
-        }
-        if (lane == 0) cnt_l[e] = c;
-    }
+    for (int e = tid; e < a.ne; e += blockDim.x) cnt_l[e] = 0;
     __syncthreads();
-    if (threadIdx.x == 0) {
+    // counts: LDS atomics
+    for (int p = tid; p < np; p += blockDim.x) atomicAdd(&cnt_l[a.ids[p]], 1);
+    __syncthreads();
+    if (w == 0) {
+        // exclusive prefix sums of the counts and of the tile counts, 64 experts per round
         int o = 0, to = 0;
-        for (int e = 0; e < a.ne; e++) {
-            off_l[e] = o;
-            toff_l[e] = to;
-            o += cnt_l[e];
-            to += (cnt_l[e] + 31) / 32;
+        for (int base = 0; base < a.ne; base += 64) {
+            const int e = base + lane;
+            const int c = e < a.ne ? cnt_l[e] : 0, t = (c + 31) / 32;
+            int ic = c, it = t;
+#pragma unroll
+            for (int s2 = 1; s2 < 64; s2 <<= 1) {
+                const int uc = __shfl_up(ic, s2), ut = __shfl_up(it, s2);
+                if (lane >= s2) { ic += uc; it += ut; }
+            }
+            if (e < a.ne) { off_l[e] = o + ic - c; pos_l[e] = o + ic - c; toff_l[e] = to + it - t; }
+            o += __shfl(ic, 63);
+            to += __shfl(it, 63);
         }
-        *a.ntiles = to;
+        if (lane == 0) *a.ntiles = to;
     }
     __syncthreads();
-    for (int e = w; e < a.ne; e += nw) {
-        int pos = off_l[e];
-        for (int base = 0; base < np; base += 64) {
-            const int p = base + lane;
-            const bool m = p < np && a.ids[p] == e;
-            const uint64_t bm = __ballot(m);
-            if (m) a.sorted[pos + __popcll(bm & lt)] = p;
-            pos += __popcll(bm);
+    // stable scatter, chunk by chunk (pairs in ascending order)
+    for (int c0 = 0; c0 < np; c0 += kGroupChunk) {
+        const int n = min(kGroupChunk, np - c0);
+        for (int p = tid; p < n; p += blockDim.x) ids_l[p] = (uint8_t)a.ids[c0 + p];
+        __syncthreads();
+        for (int e = w; e < a.ne; e += nw) {
+            int pos = pos_l[e];
+            for (int base = 0; base < n; base += 64) {
+                const int p = base + lane;
+                const bool m = p < n && ids_l[p] == e;
+                const uint64_t bm = __ballot(m);
+                if (m) a.sorted[pos + __popcll(bm & lt)] = c0 + p;
+                pos += __popcll(bm);
+            }
+            if (lane == 0) pos_l[e] = pos;
         }
+        __syncthreads();
+    }
+    for (int e = w; e < a.ne; e += nw) {
         const int c = cnt_l[e], nt = (c + 31) / 32;
         for (int j = lane; j < nt; j += 64) a.tiles[toff_l[e] + j] = int4{e, off_l[e] + 32 * j, min(32, c - 32 * j), 0};
     }
@@ -256,78 +276,89 @@ CPB_DEV void stage_store(unsigned char* st, const StageRegs& g) {
     if (tid < kBlkPerPart * 32) ((uint32_t*)(st + kBlkPerPart * 32 * kSlot))[tid] = g.s;
 }
 
-// One wave's k-part: D = A(rows) x B(tokens) per block, acc = fma(D, xsb,
-// acc) in block order.
-// w[k] = code block i0 + k of the lane's row, ex = the k-part's exponents.
+// Weight operand of one k-part for the lane's row: unit u (0 = the e8m0
+// bytes, 1..15 = blocks) sits at byte off + u * ustride of the expert's
+// stream; rs covers the expert's whole stream (out-of-range offsets read 0).
+struct WeightStream {
+    __amdgpu_buffer_rsrc_t rs;
+    uint32_t off, ustride, pstride;      // bytes: lane's unit 0 of k-part 0, unit step, k-part step
+};
+CPB_DEV u32x4 wload(const WeightStream& ws, int q, int u) {
+    return __builtin_amdgcn_raw_buffer_load_b128(ws.rs, ws.off + (uint32_t)q * ws.pstride + (uint32_t)u * ws.ustride, 0, 0);
+}
+
+// The k-part loop shared by the two grouped GEMMs.  Per k-part, D = A(rows)
+// x B(tokens) per block on the matrix cores and acc = fma(D, xsb, acc) in
+// block order, in two chains (blocks 0-7 and 8-14, as the decode kernels'
+// two wavefronts per k-part), the chains added to the total in order.
+//
+// Software pipeline: block i + 1's MFMA is issued before block i's sixteen
+// fmas (two D register sets), so the matrix core and the VALU run side by
+// side; each weight register is refilled with the next k-part's unit right
+// after its MFMA has been issued (one k-part of lead time, 16 units of
+// registers instead of 32).  Two LDS staging buffers alternate for the
+// activations: the next k-part's are requested (into registers) before the
+// current one is multiplied, and one barrier per k-part suffices (buffer q & 1
+// is rewritten two iterations after it was read, past the next barrier).
 // TRACE writes the int32 block sums S = D * 2^(128 - e) of valid rows.
-// The decode kernels accumulate a k-part in two chains, blocks 0-7 and
-// 8-14 (two wavefronts per k-part), and add the chains in order: so do
-// acc0 / acc1 here.
 template <bool TRACE>
-CPB_DEV void part_mfma(const u32x4* wv, const unsigned char* st, int lane, int q, int nbk, int32_t* trace_base,
-                       size_t trace_row_stride, bool trace_ok, v16f& acc0, v16f& acc1) {
+CPB_DEV v16f grouped_parts(const WeightStream& ws, int P, unsigned char* smem, const uint8_t* img, const float* sc,
+                           size_t rows, int nbk, const int* src, int lane, int32_t* tb, bool trace_ok) {
     const int ti = lane & 31, hb = lane >> 5;
-    const float* sl = (const float*)(st + kBlkPerPart * 32 * kSlot);
-    acc0 = v16f{};
-    acc1 = v16f{};
+    u32x4 wv[kUnits];
 #pragma unroll
-    for (int i = 0; i < kBlkPerPart; i++) {
-        v16f& acc = i < kSubUnits ? acc0 : acc1;
-        const unsigned char* xp = st + (i * 32 + ti) * kSlot + hb * 32;
-        const u32x4 x0 = *(const u32x4*)xp, x1 = *(const u32x4*)(xp + 16);
-        const float s = sl[i * 32 + ti];
-        const uint32_t eb = (wv[0][i >> 2] >> (8 * (i & 3))) & 0xffu;
-        const v16f D = mx_block_mfma(wv[1 + i], x0, x1, eb);
-#pragma unroll
-        for (int r = 0; r < 16; r++) acc[r] = fmaf(D[r], s, acc[r]);
-        if (TRACE) {
-            const int b = q * kBlkPerPart + i;
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int rl = 8 * (r >> 2) + 4 * hb + (r & 3);
-                const int e_r = __shfl((int)eb, rl);
-                if (trace_ok && b < nbk) trace_base[rl * trace_row_stride + b] = (int)ldexpf(D[r], 128 - e_r);
-            }
-        }
-    }
-}
-
-// Weight window of one k-part (16 units) for the lane's row: nontemporal loads.
-CPB_DEV void load_window(const u32x4* p, size_t stride, u32x4* wv) {
-#pragma unroll
-    for (int u = 0; u < kUnits; u++) wv[u] = __builtin_nontemporal_load(p + (size_t)u * stride);
-}
-
-// The k-part loop shared by the two grouped GEMMs.  Two LDS staging buffers
-// alternate: the next k-part's activations and weight window are requested
-// before the current one is computed, so their latency hides behind the
-// MFMAs, and one barrier per k-part suffices (buffer q & 1 is rewritten two
-// iterations after it was read, past the next barrier).  Returns the row
-// totals (k-parts added in order, as the decode kernels do).
-template <bool TRACE>
-CPB_DEV v16f grouped_parts(const u32x4* wbase, size_t stride, int P, unsigned char* smem, const uint8_t* img,
-                           const float* sc, size_t rows, int nbk, const int* src, int lane, int32_t* tb, bool trace_ok) {
-    const size_t part = (size_t)kUnits * stride;
-    u32x4 wv[kUnits], wn[kUnits];
-    load_window(wbase, stride, wv);
+    for (int u = 0; u < kUnits; u++) wv[u] = wload(ws, 0, u);
     StageRegs g = stage_load(img, sc, rows, nbk, 0, src);
     v16f tot = {};
     for (int q = 0; q < P; q++) {
         unsigned char* st = smem + (q & 1) * kStageBytes;
         stage_store(st, g);
         __syncthreads();
-        if (q + 1 < P) {
-            load_window(wbase + (size_t)(q + 1) * part, stride, wn);
-            g = stage_load(img, sc, rows, nbk, q + 1, src);
+        // past the last k-part the refills read out of range (zeros, no traffic)
+        const int qn = q + 1 < P ? q + 1 : 0x7fff;
+        const u32x4 ex = wv[0];
+        wv[0] = wload(ws, qn, 0);
+        if (q + 1 < P) g = stage_load(img, sc, rows, nbk, q + 1, src);
+        const unsigned char* xp = st + ti * kSlot + hb * 32;
+        const float* sl = (const float*)(st + kBlkPerPart * 32 * kSlot) + ti;
+        v16f acc = {}, Dc, Dn;
+        float sc_c, sc_n;
+        {
+            const u32x4 x0 = *(const u32x4*)xp, x1 = *(const u32x4*)(xp + 16);
+            sc_c = sl[0];
+            Dc = mx_block_mfma(wv[1], x0, x1, ex[0] & 0xffu);
+            wv[1] = wload(ws, qn, 1);
         }
-        v16f acc0, acc1;
-        part_mfma<TRACE>(wv, st, lane, q, nbk, tb, nbk, trace_ok, acc0, acc1);
 #pragma unroll
-        for (int r = 0; r < 16; r++) tot[r] += acc0[r];
+        for (int i = 0; i < kBlkPerPart; i++) {
+            if (i + 1 < kBlkPerPart) {
+                const int j = i + 1;
+                const u32x4 x0 = *(const u32x4*)(xp + j * 32 * kSlot), x1 = *(const u32x4*)(xp + j * 32 * kSlot + 16);
+                sc_n = sl[j * 32];
+                Dn = mx_block_mfma(wv[1 + j], x0, x1, (ex[j >> 2] >> (8 * (j & 3))) & 0xffu);
+                wv[1 + j] = wload(ws, qn, 1 + j);
+            }
+            if (TRACE) {
+                const int b = q * kBlkPerPart + i;
+                const uint32_t eb = (ex[i >> 2] >> (8 * (i & 3))) & 0xffu;
 #pragma unroll
-        for (int r = 0; r < 16; r++) tot[r] += acc1[r];
+                for (int r = 0; r < 16; r++) {
+                    const int rl = 8 * (r >> 2) + 4 * hb + (r & 3);
+                    const int e_r = __shfl((int)eb, rl);
+                    if (trace_ok && b < nbk) tb[rl * (size_t)nbk + b] = (int)ldexpf(Dc[r], 128 - e_r);
+                }
+            }
 #pragma unroll
-        for (int u = 0; u < kUnits; u++) wv[u] = wn[u];
+            for (int r = 0; r < 16; r++) acc[r] = fmaf(Dc[r], sc_c, acc[r]);
+            if (i == kSubUnits - 1 || i == kBlkPerPart - 1) {
+                // end of a chain: into the total, in order
+#pragma unroll
+                for (int r = 0; r < 16; r++) tot[r] += acc[r];
+                acc = v16f{};
+            }
+            Dc = Dn;
+            sc_c = sc_n;
+        }
     }
     __syncthreads();             // callers reuse the LDS
     return tot;
@@ -370,10 +401,17 @@ __global__ __launch_bounds__(512) void k_gateup_grouped(GroupedArgs a) {
     const int ti = lane & 31, hb = lane >> 5;
     const bool valid = ti < cnt;
     const int pair = valid ? a.sorted[start + ti] : 0;
-    const u32x4* wbase = a.gu + (((size_t)e * T + (live ? rt : 0)) * P) * kUnits * 64 + isup * 32 + (lane & 31);
+    WeightStream ws;
+    {
+        const size_t ex_units = (size_t)T * P * kUnits * 64;         // one expert's gate/up stream
+        ws.rs = buf_rsrc(a.gu + (size_t)e * ex_units, (uint32_t)(ex_units * 16));
+        ws.off = (uint32_t)((((size_t)(live ? rt : T) * P) * kUnits * 64 + isup * 32 + (lane & 31)) * 16);
+        ws.ustride = 64 * 16;
+        ws.pstride = kUnits * 64 * 16;
+    }
     int32_t* tb = TRACE ? a.gu_sums + (((size_t)pair * 2 + isup) * a.dff + rt * 32) * nb : nullptr;
 
-    const v16f tot = grouped_parts<TRACE>(wbase, 64, P, smem, a.ximg, a.xsb, (size_t)a.n_tok, nb, src, lane, tb,
+    const v16f tot = grouped_parts<TRACE>(ws, P, smem, a.ximg, a.xsb, (size_t)a.n_tok, nb, src, lane, tb,
                                           valid && live);
     // up totals to the gate wave of the same row tile (LDS reused)
     float* xch = (float*)smem;
@@ -431,11 +469,18 @@ __global__ __launch_bounds__(512) void k_down_grouped(GroupedArgs a) {
     const int ti = lane & 31, hb = lane >> 5;
     const bool valid = ti < cnt;
     const int pair = valid ? a.sorted[start + ti] : 0;
-    const int row_l = (live ? rt : 0) * 32 + (lane & 31);             // this lane's A row
-    const u32x4* wbase = a.dn + (((size_t)e * Tv + row_l / RTv) * P) * kUnits * RTv + row_l % RTv;
+    const int row_l = rt * 32 + (lane & 31);                          // this lane's A row
+    WeightStream ws;
+    {
+        const size_t ex_units = (size_t)Tv * P * kUnits * RTv;      // one expert's down stream
+        ws.rs = buf_rsrc(a.dn + (size_t)e * ex_units, (uint32_t)(ex_units * 16));
+        ws.off = live ? (uint32_t)(((size_t)(row_l / RTv) * P * kUnits * RTv + row_l % RTv) * 16) : kOffNone;
+        ws.ustride = RTv * 16;
+        ws.pstride = kUnits * RTv * 16;
+    }
     int32_t* tb = TRACE ? a.dn_sums + ((size_t)pair * a.d + rt * 32) * nbf : nullptr;
 
-    const v16f tot = grouped_parts<TRACE>(wbase, RTv, P, smem, a.himg, a.hsb, (size_t)a.n_tok * a.k, nbf, src, lane,
+    const v16f tot = grouped_parts<TRACE>(ws, P, smem, a.himg, a.hsb, (size_t)a.n_tok * a.k, nbf, src, lane,
                                           tb, valid && live);
     if (!valid || !live) return;
     float* out = a.dnout + (size_t)pair * a.d + rt * 32 + 4 * hb;
@@ -453,12 +498,33 @@ __global__ __launch_bounds__(512) void k_down_grouped(GroupedArgs a) {
 }
 
 // ---- 7. per token: x += sum over slots (ascending) of wts * (down + bias) ----
+// one thread per 4 consecutive elements (d % 4 == 0), the same fp32 operations
+// in the same order as a scalar loop
 __global__ __launch_bounds__(256) void k_combine_batch(GroupedArgs a) {
-    const int t = blockIdx.x;
-    for (int r = threadIdx.x; r < a.d; r += blockDim.x) {
-        float s = a.x[(size_t)t * a.d + r];                  // engine_gpt2.rs:911-921
-        for (int k = 0; k < a.k; k++) s += a.wts[(size_t)t * a.k + k] * a.dnout[((size_t)t * a.k + k) * a.d + r];
-        a.x[(size_t)t * a.d + r] = s;
+    const int d4 = a.d / 4, K = a.k;
+    const size_t n4 = (size_t)a.n_tok * d4;
+    const float4* __restrict__ dn = (const float4*)a.dnout;
+    float4* __restrict__ x = (float4*)a.x;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n4; i += (size_t)gridDim.x * blockDim.x) {
+        const size_t t = i / d4, r4 = i % d4;
+        float4 v[4];
+        float wk[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            v[k] = k < K ? dn[(t * K + k) * d4 + r4] : float4{0, 0, 0, 0};
+            wk[k] = k < K ? a.wts[t * K + k] : 0.0f;
+        }
+        float4 s = x[i];                                     // engine_gpt2.rs:911-921
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            if (k < K) {
+                s.x += wk[k] * v[k].x;
+                s.y += wk[k] * v[k].y;
+                s.z += wk[k] * v[k].z;
+                s.w += wk[k] * v[k].w;
+            }
+        }
+        x[i] = s;
     }
 }
 
@@ -480,7 +546,7 @@ int launch_grouped_layer(const GroupedArgs& a, bool trace, hipStream_t s) {
         launch(k_gateup_grouped<false>, ggu, dim3(512), lds, s, a);
         launch(k_down_grouped<false>, gdn, dim3(512), lds, s, a);
     }
-    launch(k_combine_batch, dim3(nt), dim3(256), 0, s, a);
+    launch(k_combine_batch, dim3((unsigned)std::min<size_t>(((size_t)nt * (a.d / 4) + 255) / 256, 2048)), dim3(256), 0, s, a);
     return hipGetLastError() == hipSuccess ? 0 : -19;
 }
 

@@ -171,37 +171,6 @@ CPB_DEV void st_dev16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, u32x4 v) {
     __builtin_amdgcn_raw_buffer_store_b128(v, r, byte_off, 0, 16);
 }
 
-// ---- LDS streaming for the sum-of-squares chain ----
-// The compiler's wait insertion drains every LDS read before any use inside
-// the loop below; these issue eight 16-byte reads and wait for all but the
-// newest eight explicitly, so one group's reads overlap the previous group's
-// fma chain.  (LDS reads of a wave complete in order.)
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-CPB_DEV uint32_t lds_addr(const float* p) {
-    return (uint32_t)(size_t)(const __attribute__((address_space(3))) float*)p;
-}
-CPB_DEV void lds_read8(f32x4 (&o)[8], uint32_t a) {
-    asm volatile(
-        "ds_read_b128 %0, %8\n\t"
-        "ds_read_b128 %1, %8 offset:16\n\t"
-        "ds_read_b128 %2, %8 offset:32\n\t"
-        "ds_read_b128 %3, %8 offset:48\n\t"
-        "ds_read_b128 %4, %8 offset:64\n\t"
-        "ds_read_b128 %5, %8 offset:80\n\t"
-        "ds_read_b128 %6, %8 offset:96\n\t"
-        "ds_read_b128 %7, %8 offset:112"
-        : "=&v"(o[0]), "=&v"(o[1]), "=&v"(o[2]), "=&v"(o[3]), "=&v"(o[4]), "=&v"(o[5]), "=&v"(o[6]), "=&v"(o[7])
-        : "v"(a)
-        : "memory");
-}
-// o (read before the newest eight LDS reads) has landed
-CPB_DEV void lds_wait_older8(f32x4 (&o)[8]) {
-    asm volatile("s_waitcnt lgkmcnt(8)"
-                 : "+v"(o[0]), "+v"(o[1]), "+v"(o[2]), "+v"(o[3]), "+v"(o[4]), "+v"(o[5]), "+v"(o[6]), "+v"(o[7])
-                 :
-                 : "memory");
-}
-CPB_DEV void lds_wait_all() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 CPB_DEV float sumsq_chain(const f32x4 (&g)[8], float acc) {
 #pragma unroll
     for (int u = 0; u < 8; u++) {

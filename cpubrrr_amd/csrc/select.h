@@ -17,6 +17,22 @@ namespace cpb {
 
 // candidates whose exact serial logits are computed side by side
 constexpr int kExactGroup = 4;
+// LDS floats per candidate's product row: d plus the chain's look-ahead slack
+// (64 floats), a multiple of 4 (16-byte reads) that spreads the chain lanes
+// over the banks
+CPB_DEV_HOST_INLINE int exact_stride(int d) { return d + 68; }
+// acc += v in order, 32 products, fp32 round to nearest (the reference's
+// serial chain)
+CPB_DEV float serial_add32(const f32x4 (&v)[8], float acc) {
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+        acc = __fadd_rn(acc, v[u][0]);
+        acc = __fadd_rn(acc, v[u][1]);
+        acc = __fadd_rn(acc, v[u][2]);
+        acc = __fadd_rn(acc, v[u][3]);
+    }
+    return acc;
+}
 
 struct Selection {
     int ids[8];
@@ -30,7 +46,8 @@ struct Selection {
 // reaches the lowest lower bound of the provisional top-k, then rank those
 // exactly (descending, lowest index first).  sL / sH: LDS values and upper
 // bounds of all NE experts; sSel: LDS [K] provisional choice, overwritten;
-// pst: LDS scratch of kExactGroup * (d + 4) floats.  One wavefront.
+// pst: LDS scratch of kExactGroup * exact_stride(d) floats.  One wavefront.
+template <int CAND, int CHUNK>
 CPB_DEV void exact_reselect(double* sL, const double* sH, int* sSel, int NE, int K, const float* __restrict__ router_w,
                             const float* __restrict__ router_b, const float* __restrict__ xn, int d, float* pst) {
     const int lane = threadIdx.x & 63;
@@ -41,52 +58,112 @@ CPB_DEV void exact_reselect(double* sL, const double* sH, int* sSel, int NE, int
     for (int e = lane; e < NE; e += 64)
         if (!(sH[e] >= tau)) sL[e] = -1e300;
     const __amdgpu_buffer_rsrc_t rx = buf_rsrc(xn, (uint32_t)d * 4);
-    const int stride = d + 4;                      // spreads the chain lanes over the LDS banks
+    const int stride = exact_stride(d);
     // candidates in groups of kExactGroup: the wave writes each candidate's
     // fp32 products W[j]*xn[j] to LDS (coalesced row loads), then lane c runs
     // candidate c's serial chain acc = b; acc += p_j over them
     int e_next = 0;
     for (;;) {
         static_assert(kExactGroup == 4, "group of four named candidates");
-        int g0 = 0, g1 = 0, g2 = 0, g3 = 0, ng = 0;
+        int g[kExactGroup] = {0, 0, 0, 0}, ng = 0;
         for (; e_next < NE && ng < kExactGroup; e_next++) {
             if (!(sH[e_next] >= tau)) continue;
-            if (ng == 0) g0 = e_next; else if (ng == 1) g1 = e_next; else if (ng == 2) g2 = e_next; else g3 = e_next;
+            if (ng == 0) g[0] = e_next; else if (ng == 1) g[1] = e_next; else if (ng == 2) g[2] = e_next; else g[3] = e_next;
             ng++;
         }
         if (ng == 0) break;
-        for (int c = 0; c < ng; c++) {
-            const int ec = c == 0 ? g0 : c == 1 ? g1 : c == 2 ? g2 : g3;
-            const __amdgpu_buffer_rsrc_t rw = buf_rsrc(router_w + (size_t)ec * d, (uint32_t)d * 4);
-            for (int j = 4 * lane; j < d; j += 256) {
-                const u32x4 w4 = __builtin_amdgcn_raw_buffer_load_b128(rw, (uint32_t)j * 4, 0, 0);
-                const u32x4 x4 = __builtin_amdgcn_raw_buffer_load_b128(rx, (uint32_t)j * 4, 0, 0);
-                float4 p4;
-                p4.x = __fmul_rn(__uint_as_float(w4[0]), __uint_as_float(x4[0]));
-                p4.y = __fmul_rn(__uint_as_float(w4[1]), __uint_as_float(x4[1]));
-                p4.z = __fmul_rn(__uint_as_float(w4[2]), __uint_as_float(x4[2]));
-                p4.w = __fmul_rn(__uint_as_float(w4[3]), __uint_as_float(x4[3]));
-                *(float4*)(pst + c * stride + j) = p4;
+        if constexpr (CAND == 1) {
+            // one 16-byte load pair per lane in flight (few registers)
+            for (int c = 0; c < ng; c++) {
+                const int ec = c == 0 ? g[0] : c == 1 ? g[1] : c == 2 ? g[2] : g[3];
+                const __amdgpu_buffer_rsrc_t rw = buf_rsrc(router_w + (size_t)ec * d, (uint32_t)d * 4);
+                for (int j = 4 * lane; j < d; j += 256) {
+                    const u32x4 w4 = __builtin_amdgcn_raw_buffer_load_b128(rw, (uint32_t)j * 4, 0, 0);
+                    const u32x4 x4 = __builtin_amdgcn_raw_buffer_load_b128(rx, (uint32_t)j * 4, 0, 0);
+                    float4 p4;
+                    p4.x = __fmul_rn(__uint_as_float(w4[0]), __uint_as_float(x4[0]));
+                    p4.y = __fmul_rn(__uint_as_float(w4[1]), __uint_as_float(x4[1]));
+                    p4.z = __fmul_rn(__uint_as_float(w4[2]), __uint_as_float(x4[2]));
+                    p4.w = __fmul_rn(__uint_as_float(w4[3]), __uint_as_float(x4[3]));
+                    *(float4*)(pst + c * stride + j) = p4;
+                }
+            }
+        } else {
+            // CAND candidates' rows (CHUNK 16-byte loads per lane each) in flight per round
+            for (int c0 = 0; c0 < ng; c0 += CAND) {
+                for (int j0 = 0; j0 < d; j0 += 256 * CHUNK) {
+                    u32x4 x4[CHUNK], w4[CAND][CHUNK];
+    #pragma unroll
+                    for (int k = 0; k < CHUNK; k++) {
+                        const int j = j0 + 256 * k + 4 * lane;
+                        x4[k] = __builtin_amdgcn_raw_buffer_load_b128(rx, j < d ? (uint32_t)j * 4 : kOffNone, 0, 0);
+                    }
+    #pragma unroll
+                    for (int ci = 0; ci < CAND; ci++) {
+                        const int c = c0 + ci;
+                        const int ec = c == 0 ? g[0] : c == 1 ? g[1] : c == 2 ? g[2] : g[3];
+                        const __amdgpu_buffer_rsrc_t rw = buf_rsrc(router_w + (size_t)ec * d, c < ng ? (uint32_t)d * 4 : 0u);
+    #pragma unroll
+                        for (int k = 0; k < CHUNK; k++) {
+                            const int j = j0 + 256 * k + 4 * lane;
+                            w4[ci][k] = __builtin_amdgcn_raw_buffer_load_b128(rw, j < d ? (uint32_t)j * 4 : kOffNone, 0, 0);
+                        }
+                    }
+    #pragma unroll
+                    for (int ci = 0; ci < CAND; ci++) {
+                        const int c = c0 + ci;
+    #pragma unroll
+                        for (int k = 0; k < CHUNK; k++) {
+                            const int j = j0 + 256 * k + 4 * lane;
+                            if (c < ng && j < d) {
+                                float4 p4;
+                                p4.x = __fmul_rn(__uint_as_float(w4[ci][k][0]), __uint_as_float(x4[k][0]));
+                                p4.y = __fmul_rn(__uint_as_float(w4[ci][k][1]), __uint_as_float(x4[k][1]));
+                                p4.z = __fmul_rn(__uint_as_float(w4[ci][k][2]), __uint_as_float(x4[k][2]));
+                                p4.w = __fmul_rn(__uint_as_float(w4[ci][k][3]), __uint_as_float(x4[k][3]));
+                                *(float4*)(pst + c * stride + j) = p4;
+                            }
+                        }
+                    }
+                }
             }
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         if (lane < ng) {
-            const int e = lane == 0 ? g0 : lane == 1 ? g1 : lane == 2 ? g2 : g3;
+            const int e = lane == 0 ? g[0] : lane == 1 ? g[1] : lane == 2 ? g[2] : g[3];
             const float* pr = pst + lane * stride;
             float acc = router_b ? router_b[e] : 0.0f;
             int j = 0;
-            for (; j + 32 <= d; j += 32) {
-                float4 v[8];
+            if constexpr (CAND > 1) {
+                // full groups of 32 products streamed from LDS (the next
+                // group's reads issued before the current group's adds; the
+                // look-ahead reads at most 64 floats past d, inside the
+                // stride's slack).  64 registers: the wide variant only.
+                const int nfull = d / 32;
+                uint32_t ra = lds_addr(pr);
+                f32x4 ga[8], gb[8];
+                lds_read8(ga, ra);
+                for (int m = 0;; m += 2) {
+                    lds_read8(gb, ra + 128);
+                    lds_wait_older8(ga);
+                    if (m >= nfull) break;
+                    acc = serial_add32(ga, acc);
+                    lds_read8(ga, ra + 256);
+                    lds_wait_older8(gb);
+                    if (m + 1 >= nfull) break;
+                    acc = serial_add32(gb, acc);
+                    ra += 256;
+                }
+                lds_wait_all();
+                j = nfull * 32;
+            } else {
+                for (; j + 32 <= d; j += 32) {
+                    f32x4 v[8];
 #pragma unroll
-                for (int u = 0; u < 8; u++) v[u] = *(const float4*)(pr + j + 4 * u);
-#pragma unroll
-                for (int u = 0; u < 8; u++) {
-                    acc = __fadd_rn(acc, v[u].x);
-                    acc = __fadd_rn(acc, v[u].y);
-                    acc = __fadd_rn(acc, v[u].z);
-                    acc = __fadd_rn(acc, v[u].w);
+                    for (int u = 0; u < 8; u++) v[u] = *(const f32x4*)(pr + j + 4 * u);
+                    acc = serial_add32(v, acc);
                 }
             }
             for (; j < d; j++) acc = __fadd_rn(acc, pr[j]);
@@ -123,7 +200,7 @@ struct SelectIn {
     int32_t* fallback;       // [1]
 };
 // LDS bytes select_topk_wave may use (its exact fallback)
-CPB_DEV_HOST_INLINE size_t select_lds_bytes(int ne, int d) { return sizeof(double) * 2 * ne + 64 + sizeof(float) * kExactGroup * (d + 4); }
+CPB_DEV_HOST_INLINE size_t select_lds_bytes(int ne, int d) { return sizeof(double) * 2 * ne + 64 + sizeof(float) * kExactGroup * exact_stride(d); }
 
 // Wave-wide maximum of a 32-bit unsigned value via DPP (quad swaps, half-row
 // and row mirrors, row broadcasts 15 / 31), returned wave-uniform.
@@ -160,13 +237,14 @@ CPB_DEV float f32_down(double x) {
 // Rare path of select_topk_wave (pointer and scalar
 // arguments only, so the caller needs no stack): exact_reselect over the LDS
 // image the caller wrote.
+template <int CAND, int CHUNK>
 CPB_DEV void select_exact_path(unsigned char* lds, int NE, int K, const float* router_w,
                                                             const float* router_b, const float* xn, int d) {
     double* sL = (double*)lds;
     double* sH = sL + NE;
     int* sSel = (int*)(sH + NE);
     float* xst = (float*)(lds + sizeof(double) * 2 * NE + 64);
-    exact_reselect(sL, sH, sSel, NE, K, router_w, router_b, xn, d, xst);
+    exact_reselect<CAND, CHUNK>(sL, sH, sSel, NE, K, router_w, router_b, xn, d, xst);
 }
 
 // One wavefront's LDS writes visible to its later LDS reads (a wave's LDS
@@ -200,6 +278,10 @@ CPB_DEV SelectPre select_preload(const SelectIn& s) {
     return SelectPre{ok ? s.lstar[lane] : 0.0, ok ? s.lbound[lane] : 0.0};
 }
 
+// EXACT_CAND / EXACT_CHUNK: router rows (and 16-byte loads per lane of each)
+// in flight on the exact path; EXACT_CAND > 1 also streams the serial chains'
+// LDS reads ahead (registers: the decode kernels keep both small)
+template <int EXACT_CAND = 1, int EXACT_CHUNK = 1>
 CPB_DEV void select_topk_wave(const SelectIn& s, unsigned char* lds, Selection* out, bool publish_logits = false,
                               unsigned long long* st = nullptr, const SelectPre* pre = nullptr) {
     const int lane = threadIdx.x & 63;
@@ -303,7 +385,7 @@ CPB_DEV void select_topk_wave(const SelectIn& s, unsigned char* lds, Selection* 
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        select_exact_path(lds, NE, K, s.router_w, s.router_b, s.xn, s.d);
+        select_exact_path<EXACT_CAND, EXACT_CHUNK>(lds, NE, K, s.router_w, s.router_b, s.xn, s.d);
         if (lane < K) { my_e = sSel[lane]; my_l = (float)sL[my_e]; }
     }
     // softmax over the k selected, reference order: ex_i = exp(l_i - l_0)
