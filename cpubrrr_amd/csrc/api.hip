@@ -311,6 +311,7 @@ int layer_token(cpb_moe_t* h, int layer, float* dx, int apply_norm, bool trace) 
         k.d = c.d; k.dff = c.d_ff; k.top_k = c.top_k;
         k.hbuf = h->hbuf; k.hq = h->hq; k.hs = h->hsb; k.hsum = h->hsum; k.x = dx;
         k.gu_out = h->t_gu; k.gu_sums = h->t_gu_sums; k.dn_out = h->t_dn; k.dn_sums = h->t_dn_sums;
+        k.stamps = stamps;
         {
             Timer tm(h, 1);
             if (cpb::launch_gateup_kq(k, trace, h->stream)) return fail(CPB_ENODEV, "k-quant gate/up launch failed");

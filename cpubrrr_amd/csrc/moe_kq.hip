@@ -27,6 +27,7 @@
 // spans 16 gate/up workgroups) from hbuf with the reference's operations.
 #include "moe_common.h"
 #include "moe_kq.h"
+#include "route_dev.h"
 
 #include <algorithm>
 
@@ -134,6 +135,8 @@ __global__ __launch_bounds__(1024) void k_gateup_kq(KqArgs a) {
     const int lane = threadIdx.x & 63, q = uniform((int)(threadIdx.x >> 6));
     const int nth = blockDim.x;
     const int ei = blockIdx.x / T, t = blockIdx.x % T;
+    RSTAMP_DECL;
+    RSTAMP(0);
     int8_t* xl = (int8_t*)smem;                                  // [nsb][kXsPad]
     int32_t* xsl = (int32_t*)(smem + nsb * kXsPad);              // [nsb * 8]
     float* ysl = (float*)(xsl + nsb * 8);                        // [nsb]
@@ -161,6 +164,7 @@ __global__ __launch_bounds__(1024) void k_gateup_kq(KqArgs a) {
         e = uniform(a.ids[ei]);
     }
 
+    RSTAMP(1);
     // weights: this lane's (row, superblock); idle lanes (s >= nsb) read superblock 0
     const int s = 2 * q + (lane >> 5), r = lane & 31;
     const bool live = s < nsb;
@@ -184,7 +188,10 @@ __global__ __launch_bounds__(1024) void k_gateup_kq(KqArgs a) {
         int32_t* so = TRACE ? a.gu_sums + ((((size_t)ei * 2 + isup) * a.dff + row) * nsb + s) * 2 : nullptr;
         part[s * 32 + r] = q4k_term<TRACE>(u, xl + s * kXsPad, xsl + s * 8, ysl[s], so);
     }
+    RSTAMP(2);
     __syncthreads();
+    RSTAMP(3);
+    RSTAMP_FLUSH_TO(a.stamps ? a.stamps + 2048 + (size_t)blockIdx.x * 8 : nullptr);
     if (threadIdx.x >= 32) return;
     float v = 0.0f;                                              // sumf, superblocks in order
     for (int k = 0; k < nsb; k++) v += part[k * 32 + r];
@@ -211,7 +218,10 @@ __global__ __launch_bounds__(1024) void k_down_kq(KqArgs a) {
     float* hsl = (float*)(h16 + K * a.dff / 16);                  // [K*nsbf]
     float* part = hsl + K * nsbf;                                 // [nsbf][64]
     float* vv = part + nsbf * 64;                                 // [64]
+    float4* hst = (float4*)(((size_t)(vv + 64) + 15) & ~(size_t)15);   // [K*dff/32][8] h chunks (one-chunk case)
 
+    RSTAMP_DECL;
+    RSTAMP(0);
     int es[8];
 #pragma unroll
     for (int k = 0; k < 8; k++) es[k] = uniform(a.ids[k < K ? k : 0]);
@@ -219,26 +229,62 @@ __global__ __launch_bounds__(1024) void k_down_kq(KqArgs a) {
 #pragma unroll
     for (int k = 1; k < 8; k++) if (ei == k) e = es[k];
 
-    // weights of (slot ei, row, superblock q) first
+    // this thread's 32-value chunk of h first (one chunk per thread when
+    // K*dff/32 <= the block size, as for every supported shape but the
+    // largest), then the weights of (slot ei, row, superblock q): the chunk
+    // lands before the weight stream, so the Q8_K below runs while the
+    // weights are in flight (a wave's loads complete in order)
+    const int nch = K * a.dff / 32;
+    const bool one_chunk = nch <= nth;
+    float4 hv[8];
+    {
+        const int c = one_chunk && (int)threadIdx.x < nch ? (int)threadIdx.x : 0;
+        const float4* src = (const float4*)(a.hbuf + (size_t)c * 32);
+#pragma unroll
+        for (int k = 0; k < 8; k++) hv[k] = src[k];
+    }
+    __builtin_amdgcn_sched_barrier(0);          // the chunk's loads stay ahead of the weights'
     const u32x4* wp = a.dn + ((((size_t)e * T + t) * nsbf + q) * U) * RT + rr;
     u32x4 u[U];
 #pragma unroll
-    for (int k = 0; k < U; k++) u[k] = __builtin_nontemporal_load(wp + k * RT);
+    for (int k = 0; k < U; k++) {
+        // Q6_K's last unit holds only the fp16 d: a 4-byte load (a partly dead
+        // 16-byte destination lets later instructions reuse its registers,
+        // which then wait for the whole weight stream)
+        if (TYPE == 14 && k == kQ6Units - 1) u[k] = u32x4{__builtin_nontemporal_load((const uint32_t*)(wp + k * RT)), 0, 0, 0};
+        else u[k] = __builtin_nontemporal_load(wp + k * RT);
+    }
+    __builtin_amdgcn_sched_barrier(0);
 
     // Q8_K of hbuf (engine_qwen2.rs:288-300): chunk c = 32 values; a 256-block
-    // is 8 chunks.  Pass 1: chunk amax.
-    const int nch = K * a.dff / 32;
-    for (int c = threadIdx.x; c < nch; c += nth) {
-        const float4* src = (const float4*)(a.hbuf + (size_t)c * 32);
+    // is 8 chunks.  Pass 1: chunk amax (the one-chunk case straight-line, so
+    // that it waits for the chunk's loads only, not the weights behind them).
+    auto chunk_max = [&](int c) {
         float m = 0.0f;
 #pragma unroll
         for (int k = 0; k < 8; k++) {
-            const float4 v = src[k];
+            const float4 v = hv[k];
             m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
         }
         cmax[c] = m;
+    };
+    if (one_chunk) {
+        if ((int)threadIdx.x < nch) {
+            chunk_max(threadIdx.x);
+#pragma unroll
+            for (int k = 0; k < 8; k++) hst[threadIdx.x * 8 + k] = hv[k];
+        }
+    } else {
+        for (int c = threadIdx.x; c < nch; c += nth) {
+            const float4* src = (const float4*)(a.hbuf + (size_t)c * 32);
+#pragma unroll
+            for (int k = 0; k < 8; k++) hv[k] = src[k];
+            chunk_max(c);
+        }
     }
+    RSTAMP(1);
     __syncthreads();
+    RSTAMP(2);
     // pass 2: scale per 256 (amax seeded 1e-12), round, sums per 32 and 16
     for (int c = threadIdx.x; c < nch; c += nth) {
         const int blk = c / 8;
@@ -246,13 +292,17 @@ __global__ __launch_bounds__(1024) void k_down_kq(KqArgs a) {
 #pragma unroll
         for (int k = 0; k < 8; k++) amax = fmaxf(amax, cmax[blk * 8 + k]);
         const float sc = amax / 127.0f;
-        const float4* src = (const float4*)(a.hbuf + (size_t)c * 32);
+        {
+            const float4* src = one_chunk ? hst + c * 8 : (const float4*)(a.hbuf + (size_t)c * 32);
+#pragma unroll
+            for (int k = 0; k < 8; k++) hv[k] = src[k];
+        }
         const int slot = c / (a.dff / 32), cc = c % (a.dff / 32);   // expert slot, chunk within it
         int8_t* dst = hql + slot * hstride + (cc / 8) * kXsPad + (cc % 8) * 32;
         int s16[2] = {0, 0};
 #pragma unroll
         for (int k = 0; k < 8; k++) {
-            const float4 v = src[k];
+            const float4 v = hv[k];
             const int q0 = q8_round(v.x, sc), q1 = q8_round(v.y, sc), q2 = q8_round(v.z, sc), q3 = q8_round(v.w, sc);
             s16[k / 4] += q0 + q1 + q2 + q3;
             *(uint32_t*)(dst + 4 * k) = (uint32_t)(uint8_t)q0 | ((uint32_t)(uint8_t)q1 << 8) |
@@ -283,7 +333,10 @@ __global__ __launch_bounds__(1024) void k_down_kq(KqArgs a) {
             tv = q6k_term<TRACE>(u, xs, h16 + (ei * nsbf + q) * 16, ys, so);
         part[q * 64 + lane] = tv;
     }
+    RSTAMP(3);
     __syncthreads();
+    RSTAMP(4);
+    RSTAMP_FLUSH_TO(a.stamps ? a.stamps + 8192 + (size_t)blockIdx.x * 8 : nullptr);
     if (q != 0) return;
     float v = 0.0f;
     for (int k = 0; k < nsbf; k++) v += part[k * 64 + lane];
@@ -379,7 +432,8 @@ int launch_gateup_kq(const KqArgs& a, bool trace, hipStream_t s) {
 int launch_down_kq(const KqArgs& a, bool trace, hipStream_t s) {
     const int K = a.top_k, nsbf = a.dff / 256, RT = 64 / K;
     const size_t lds = (size_t)K * nsbf * kXsPad + (size_t)K * a.dff / 32 * 4 * 2 + (size_t)K * a.dff / 16 * 4 +
-                       (size_t)K * nsbf * 4 + (size_t)nsbf * 64 * 4 + 64 * 4;
+                       (size_t)K * nsbf * 4 + (size_t)nsbf * 64 * 4 + 64 * 4 +
+                       (K * a.dff / 32 <= 64 * nsbf ? (size_t)K * a.dff / 32 * 128 + 16 : 0);
     const dim3 grid(a.d / RT), block(64 * nsbf);
     if (a.down_type == 12) {
         if (trace) launch((k_down_kq<12, true>), grid, block, lds, s, a);
