@@ -142,7 +142,11 @@ __global__ __launch_bounds__(1024) void k_gateup_kq(KqArgs a) {
     float* ysl = (float*)(xsl + nsb * 8);                        // [nsb]
     float* part = ysl + 32;                                      // [nsb][32]
 
-    // activations first (buffer loads; out of range reads zero)
+    // the selection's intervals (more than 64 experts: one per thread), then
+    // the activations (buffer loads; out of range reads zero)
+    const bool ranked = a.sel.lstar && a.sel.ne > 64 && a.sel.ne <= (int)blockDim.x;
+    SelectPre pre{0.0, 0.0};
+    if (ranked) pre = select_preload_wg(a.sel);
     const __amdgpu_buffer_rsrc_t rx = buf_rsrc(a.xq, (uint32_t)a.d);
     const __amdgpu_buffer_rsrc_t rs = buf_rsrc(a.xsum, (uint32_t)a.d / 8);
     const __amdgpu_buffer_rsrc_t ry = buf_rsrc(a.xs, (uint32_t)nsb * 4);
@@ -157,7 +161,10 @@ __global__ __launch_bounds__(1024) void k_gateup_kq(KqArgs a) {
     int e;
     if (a.sel.lstar) {
         __shared__ Selection ssel;
-        if (q == 0) select_topk_wave(a.sel, smem, &ssel);
+        // more than 64 experts: every thread ranks one expert first
+        if (ranked) select_rank_wg(a.sel, smem, blockIdx.x == 0 ? a.sel.logits : nullptr, pre);
+        if (q == 0) select_topk_wave(a.sel, smem, &ssel, false, a.stamps ? a.stamps + 12288 + (size_t)blockIdx.x * 4 : nullptr,
+                                     nullptr, ranked);
         __syncthreads();
         e = uniform(ssel.ids[ei]);
     } else {
@@ -422,7 +429,7 @@ int launch_gateup_kq(const KqArgs& a, bool trace, hipStream_t s) {
     const int nsb = a.d / 256;
     const int waves = (nsb + 1) / 2;
     size_t lds = (size_t)nsb * kXsPad + nsb * 8 * 4 + 32 * 4 + (size_t)nsb * 32 * 4;
-    if (a.sel.lstar) lds = std::max(lds, select_lds_bytes(a.sel.ne, a.sel.d));
+    if (a.sel.lstar) lds = std::max(lds, std::max(select_lds_bytes(a.sel.ne, a.sel.d), select_ranked_bytes));
     const dim3 grid(a.top_k * (a.dff / 16)), block(64 * waves);
     if (trace) launch(k_gateup_kq<true>, grid, block, lds, s, a);
     else launch(k_gateup_kq<false>, grid, block, lds, s, a);

@@ -278,21 +278,121 @@ CPB_DEV SelectPre select_preload(const SelectIn& s) {
     return SelectPre{ok ? s.lstar[lane] : 0.0, ok ? s.lbound[lane] : 0.0};
 }
 
+// Workgroup pre-pass of the selection for up to 256 experts (one thread per
+// expert; blockDim.x >= ne): every thread ranks its expert's 32-bit key
+// against all keys in LDS (rank = number of larger keys), the top k write
+// their id, fp32 logit and outward-rounded bounds to LDS by rank, the others
+// fold their upper bound into an LDS maximum.  Thread e also publishes its
+// fp32 logit when logits_out is set.  Ends with a barrier; select_topk_wave
+// (called with ranked = true by one wavefront) then certifies and finishes
+// from the LDS state.  LDS: the first select_ranked_bytes bytes of lds.
+constexpr size_t select_ranked_bytes = 256 * 4 + 8 * 4 * 4 + 16 + 256 * 4;
+// Thread e's interval, loaded by the caller ahead of its other loads (a
+// wavefront's loads complete in order).
+CPB_DEV SelectPre select_preload_wg(const SelectIn& s) {
+    const int tid = threadIdx.x;
+    const bool ok = tid < s.ne;
+    return SelectPre{ok ? s.lstar[tid] : 0.0, ok ? s.lbound[tid] : 0.0};
+}
+CPB_DEV void select_rank_wg(const SelectIn& s, unsigned char* lds, float* logits_out, const SelectPre& pre) {
+    const int tid = threadIdx.x, NE = s.ne, K = s.k;
+    uint32_t* skey = (uint32_t*)lds;                   // [256]
+    int* sE = (int*)(skey + 256);                      // [8] by rank
+    float* sLf = (float*)(sE + 8);                     // [8]
+    float* sLo = sLf + 8;                              // [8]
+    float* sHi = sLo + 8;                              // [8]
+    uint32_t* smu = (uint32_t*)(sHi + 8);              // max key of the unselected upper bounds
+    const bool valid = tid < NE;
+    const double lv = pre.lv, bv = pre.bv;
+    const float lf = (float)lv;
+    const uint32_t key = valid ? ((float_key(lf) & 0xFFFFFF00u) | (uint32_t)(255 - tid)) : 0u;
+    if (tid < ((NE + 31) & ~31)) skey[tid] = key;      // zero keys (never larger) pad to a multiple of 32
+    if (tid == 0) *smu = float_key(-__builtin_inff());
+    if (valid && logits_out) logits_out[tid] = lf;
+    __syncthreads();
+    // rank: with at least twice as many threads as experts, thread e + NE
+    // counts the larger keys among the second half of the (32-padded) keys
+    // and thread e the first half; else thread e counts all
+    const int NEp = (NE + 31) & ~31;
+    const bool split = (int)blockDim.x >= 2 * NE && NEp >= 64;
+    const int half = (NEp / 2 + 31) & ~31;
+    int* srank = (int*)(smu + 1);                      // [NE] second-half counts
+    int rank = 0;
+    if (tid < (split ? 2 * NE : NE)) {
+        const int ee = tid < NE ? tid : tid - NE;
+        const uint32_t kk = tid < NE ? key : skey[ee];
+        const int j0 = split && tid >= NE ? half : 0, j1 = split && tid < NE ? half : NEp;
+        // 32 keys per round: eight 16-byte LDS reads in flight, then the compares
+        for (int j = j0; j < j1; j += 32) {
+            u32x4 k4[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) k4[u] = *(const u32x4*)(skey + j + 4 * u);
+#pragma unroll
+            for (int u = 0; u < 8; u++) rank += (k4[u][0] > kk) + (k4[u][1] > kk) + (k4[u][2] > kk) + (k4[u][3] > kk);
+        }
+        if (split && tid >= NE) srank[ee] = rank;
+    }
+    if (split) __syncthreads();
+    uint32_t mu_key = 0u;                              // this thread's unselected upper bound (0: none)
+    if (valid) {
+        if (split) rank += srank[tid];
+        const float hi = f32_up(lv + bv);
+        if (rank < K) { sE[rank] = tid; sLf[rank] = lf; sLo[rank] = f32_down(lv - bv); sHi[rank] = hi; }
+        else mu_key = float_key(hi);
+    }
+    // one LDS atomic per wavefront (same-address LDS atomics serialise)
+    const uint32_t wm = wave_max_u32(mu_key);
+    if ((tid & 63) == 0 && wm) atomicMax(smu, wm);
+    __syncthreads();
+}
+
 // EXACT_CAND / EXACT_CHUNK: router rows (and 16-byte loads per lane of each)
 // in flight on the exact path; EXACT_CAND > 1 also streams the serial chains'
 // LDS reads ahead (registers: the decode kernels keep both small)
+// ranked: select_rank_wg ran first (the logits were published there); the
+// wave certifies its LDS ranking and, on the rare exact path, reloads the
+// intervals.
 template <int EXACT_CAND = 1, int EXACT_CHUNK = 1>
 CPB_DEV void select_topk_wave(const SelectIn& s, unsigned char* lds, Selection* out, bool publish_logits = false,
-                              unsigned long long* st = nullptr, const SelectPre* pre = nullptr) {
+                              unsigned long long* st = nullptr, const SelectPre* pre = nullptr, bool ranked = false) {
     const int lane = threadIdx.x & 63;
     SSTAMP(0);
     const int NE = s.ne, K = s.k;
-    double lv[4], bv[4];
-    float lf[4];
+    double lv[4] = {0.0, 0.0, 0.0, 0.0}, bv[4] = {0.0, 0.0, 0.0, 0.0};
+    float lf[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     int my_e = 0;
     float my_l = 0.0f;
     bool bad;
-    if (NE <= 64) {
+    if (ranked) {
+        const int* sE = (const int*)(lds + 256 * 4);
+        const float* sLf = (const float*)(sE + 8);
+        const float* sLo = sLf + 8;
+        const float* sHi = sLo + 8;
+        const uint32_t mu = *(const uint32_t*)(sHi + 8);
+        float later = key_float(mu), my_lo = 0.0f;
+        const f32x4 h0 = *(const f32x4*)sHi, h1 = *(const f32x4*)(sHi + 4);
+        const float hs[8] = {h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
+#pragma unroll
+        for (int j = 1; j < 8; j++)
+            if (j > lane && j < K) later = fmaxf(later, hs[j]);
+        if (lane < K) {
+            my_e = sE[lane];
+            my_l = sLf[lane];
+            my_lo = sLo[lane];
+        }
+        SSTAMP(1);
+        bad = __any(lane < K && !(my_lo > later));
+        wave_lds_order();
+        if (bad) {
+            // the exact path needs every interval (LDS state above is consumed)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int e = lane + 64 * j;
+                lv[j] = e < NE ? s.lstar[e] : 0.0;
+                bv[j] = e < NE ? s.lbound[e] : 0.0;
+            }
+        }
+    } else if (NE <= 64) {
         // one expert per lane; rank = number of larger keys, read back from
         // LDS (no serial rounds); rank r < K is selection slot r
         const bool valid = lane < NE;
@@ -311,10 +411,14 @@ CPB_DEV void select_topk_wave(const SelectIn& s, unsigned char* lds, Selection* 
         float* sHi = sLf + 8;                             // [8]
         skey[lane] = key;
         wave_lds_order();
+        // 32 keys per round: eight 16-byte LDS reads in flight, then the compares
         int rank = 0;
-        for (int j = 0; j < NE; j += 4) {
-            const u32x4 k4 = *(const u32x4*)(skey + j);
-            rank += (k4[0] > key) + (k4[1] > key) + (k4[2] > key) + (k4[3] > key);
+        for (int j = 0; j < NE; j += 32) {
+            u32x4 k4[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) k4[u] = *(const u32x4*)(skey + j + 4 * u);
+#pragma unroll
+            for (int u = 0; u < 8; u++) rank += (k4[u][0] > key) + (k4[u][1] > key) + (k4[u][2] > key) + (k4[u][3] > key);
         }
         const bool sel = valid && rank < K;
         if (sel) { sE[rank] = lane; sLf[rank] = lf[0]; sHi[rank] = hi; }
@@ -413,10 +517,12 @@ CPB_DEV void select_topk_wave(const SelectIn& s, unsigned char* lds, Selection* 
         __builtin_amdgcn_wave_barrier();
         if (lane < K) s.logits[my_e] = my_l;
     } else if (blockIdx.x == 0 && blockIdx.y == 0) {
+        if (!ranked) {
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int e = lane + 64 * j;
-            if (e < NE && s.logits) s.logits[e] = lf[j];
+            for (int j = 0; j < 4; j++) {
+                const int e = lane + 64 * j;
+                if (e < NE && s.logits) s.logits[e] = lf[j];
+            }
         }
         __builtin_amdgcn_wave_barrier();
         if (lane < K) {
