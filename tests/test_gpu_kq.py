@@ -113,3 +113,27 @@ def test_qwen_stack_device(gpu):
         xr, _ = O.qwen_moe(layers[l], xr, True)
     rms = np.sqrt(((xr - x).astype(np.float64) ** 2).mean())
     assert np.max(np.abs(y - xr)) <= 1e-3 * rms
+
+
+def test_qwen_router_tie_128_experts(gpu):
+    # 128 experts: the workgroup-ranked selection.  The experts ranked 8th and
+    # 9th get identical router rows, so their logits tie exactly at the top-8
+    # boundary: the certification must fail, the exact serial logits decide,
+    # and the lower index wins (engine_qwen2.rs:403-410)
+    say("case qwen router tie, 128 experts")
+    d, dff, ne, k = 1024, 256, 128, 8
+    L = synth.qwen_layer(d, dff, ne, k, seed=7)
+    x = synth.token(d, 7)
+    _, to = O.qwen_moe(L, x, True, want_sums=True)
+    order = np.argsort(-to["logits"].astype(np.float64), kind="stable")
+    a, b = order[k - 1], order[k]
+    L["router_w"][max(a, b)] = L["router_w"][min(a, b)]
+    cfg = MoeConfig.qwen3(d=d, n_expert=ne, top_k=k, d_ff=dff)
+    with MoeBlock(cfg) as blk:
+        blk.load_layer(0, L)
+        xo, t = blk.forward(0, x, apply_norm=True, trace=True)
+        assert t["exact_router_fallbacks"] == 1
+        assert min(a, b) in t["ids"] and max(a, b) not in t["ids"], (a, b, t["ids"])
+        check_qwen(L, x, True, xo, t)
+        xo2, _ = blk.forward(0, x, apply_norm=True)
+        assert np.array_equal(xo2.view(np.uint32), xo.view(np.uint32))
