@@ -38,15 +38,22 @@
 
 namespace cpb {
 
+// A workgroup covers kTilesPerWG row tiles of one expert (tile pair tp:
+// tiles kTilesPerWG*tp + j), every wave streaming its sub-part of each: 180
+// workgroups of ~196 KB for a gpt-oss layer (no CU holds two, which a 360 x
+// 98 KB split forces on 104 of 256 CUs), and one activation fetch serves both
+// tiles.  Wave j then runs tile j's epilogue.
+constexpr int kTilesPerWG = 2;
+
 template <bool TRACE>
-__global__ __launch_bounds__(128 * kMaxParts) __attribute__((amdgpu_waves_per_eu(6))) void k_gateup_mx(GateUpArgs a) {
+__global__ __launch_bounds__(128 * kMaxParts) __attribute__((amdgpu_waves_per_eu(3))) void k_gateup_mx(GateUpArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     const int P = a.nparts, W = 2 * P;
     const int lane = threadIdx.x & 63;
     const int w = uniform(threadIdx.x >> 6), q = w >> 1, hh = w & 1;
     const int ub = kSubUnits * hh;
-    const int tiles = a.dff / 32;
-    const int ei = blockIdx.x / tiles, t = blockIdx.x % tiles;
+    const int tiles = a.dff / 32, pairs = (tiles + kTilesPerWG - 1) / kTilesPerWG;
+    const int ei = blockIdx.x / pairs, tp = blockIdx.x % pairs;
     // every argument the prologue needs, loaded in one batch up front (else
     // the selection's fields arrive in a second kernarg round trip)
     asm volatile("" ::"s"(a.sel.lstar), "s"(a.sel.lbound), "s"(a.sel.ne), "s"(a.sel.k), "s"(a.ximg), "s"(a.xsb),
@@ -55,7 +62,7 @@ __global__ __launch_bounds__(128 * kMaxParts) __attribute__((amdgpu_waves_per_eu
     RSTAMP(0);
     SelectPre pre{0.0, 0.0};
     if (a.sel.lstar && w == 0) pre = select_preload(a.sel);
-    float* red = (float*)smem;                                 // [W][64]
+    float* red = (float*)smem;                                 // [kTilesPerWG][W][64]
     const int blk0 = q * kBlkPerPart;
     // activations: the two windows' A operands and the 8 block scales (issued
     // before the weights: requests queued behind a CU's weight stream would
@@ -88,24 +95,35 @@ __global__ __launch_bounds__(128 * kMaxParts) __attribute__((amdgpu_waves_per_eu
         e = a.ids[ei];
     }
     RSTAMP(1);
-    u32x4 wv[1 + kSubUnits];
-    load_sub(a.w + ((((size_t)e * tiles + t) * P + q) * kUnits) * 64 + lane, 64, ub, wv);
+    // both tiles' sub-parts requested back to back (a missing second tile of
+    // an odd tile count reads the first again; its result is dropped)
+    u32x4 wv[kTilesPerWG][1 + kSubUnits];
+#pragma unroll
+    for (int j = 0; j < kTilesPerWG; j++) {
+        const int t = min(kTilesPerWG * tp + j, tiles - 1);
+        load_sub(a.w + ((((size_t)e * tiles + t) * P + q) * kUnits) * 64 + lane, 64, ub, wv[j]);
+    }
     const float* bias = (lane >> 5) ? a.up_b : a.gate_b;
+    const int tw = kTilesPerWG * tp + w;                       // the tile whose epilogue wave w runs (w < kTilesPerWG)
     float bias_pf = 0.0f;
-    if (w == 0 && bias) bias_pf = ((const __attribute__((address_space(1))) float*)bias)[(size_t)e * a.dff + t * 32 + (lane & 31)];
-    const int row = t * 32 + (lane & 31);
+    if (w < kTilesPerWG && tw < tiles && bias)
+        bias_pf = ((const __attribute__((address_space(1))) float*)bias)[(size_t)e * a.dff + tw * 32 + (lane & 31)];
     const int isup = lane >> 5;
-    int32_t* so = nullptr;
-    if (TRACE) so = a.gu_sums + (((size_t)(ei * 2 + isup) * a.dff + row) * a.nb + blk0);
-    const float acc = part_dot_sub_mfma<TRACE>(wv, ub, xw, xsc, so, blk0, a.nb);
+#pragma unroll
+    for (int j = 0; j < kTilesPerWG; j++) {
+        const int t = kTilesPerWG * tp + j;
+        int32_t* so = nullptr;
+        if (TRACE && t < tiles) so = a.gu_sums + (((size_t)(ei * 2 + isup) * a.dff + t * 32 + (lane & 31)) * a.nb + blk0);
+        red[(j * W + w) * 64 + lane] = part_dot_sub_mfma<TRACE>(wv[j], ub, xw, xsc, so, blk0, a.nb);
+    }
     RSTAMP(2);
-    red[w * 64 + lane] = acc;
     __syncthreads();
-    if (w != 0) return;
+    if (w >= kTilesPerWG || tw >= tiles) return;
     RSTAMP(3);
+    const int t = tw, row = t * 32 + (lane & 31);
     float pr[2 * kMaxParts];
 #pragma unroll
-    for (int p = 0; p < 2 * kMaxParts; p++) pr[p] = p < W ? red[p * 64 + lane] : 0.0f;
+    for (int p = 0; p < 2 * kMaxParts; p++) pr[p] = p < W ? red[(w * W + p) * 64 + lane] : 0.0f;
     float v = 0.0f;
 #pragma unroll
     for (int p = 0; p < 2 * kMaxParts; p++)
@@ -333,9 +351,9 @@ int launch_repack_down(const uint8_t* down, u32x4* out, int ne, int d, int nbf, 
 int launch_gateup_mx(const GateUpArgs& a, bool trace, hipStream_t s) {
     const int P = a.nparts;
     if (P < 1 || P > kMaxParts || a.dff % 32 != 0) return -22;
-    size_t lds = sizeof(float) * 2 * P * 64;
+    size_t lds = sizeof(float) * kTilesPerWG * 2 * P * 64;
     if (a.sel.lstar) lds = std::max(lds, select_lds_bytes(a.sel.ne, a.sel.d));
-    dim3 grid(a.top_k * (a.dff / 32)), block(128 * P);
+    dim3 grid(a.top_k * ((a.dff / 32 + kTilesPerWG - 1) / kTilesPerWG)), block(128 * P);
     if (trace) launch(k_gateup_mx<true>, grid, block, lds, s, a);
     else launch(k_gateup_mx<false>, grid, block, lds, s, a);
     return hipGetLastError() == hipSuccess ? 0 : -19;

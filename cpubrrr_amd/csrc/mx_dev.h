@@ -175,7 +175,7 @@ CPB_DEV float sub_chain(const u32x4& ew4, int ub, const float* S, const float* s
         const int u = ub + i;
         const uint32_t e = (ew[u >> 2] >> (8 * (u & 3))) & 0xffu;
         acc = fmaf(S[i], e8m0_scale(e, sc[i]), acc);
-        if (TRACE && u < kBlkPerPart && blk0 + u < nb) sums_out[u] = (int32_t)S[i];
+        if (TRACE && sums_out && u < kBlkPerPart && blk0 + u < nb) sums_out[u] = (int32_t)S[i];
     }
     return acc;
 }
