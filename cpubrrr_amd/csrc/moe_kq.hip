@@ -159,12 +159,14 @@ __global__ __launch_bounds__(1024) void k_gateup_kq(KqArgs a) {
     // expert of this tile: selected here by wave 0 from the certified logits
     // (its LDS scratch is used before the activations are stored)
     int e;
+    __shared__ Selection ssel;
     if (a.sel.lstar) {
-        __shared__ Selection ssel;
         // more than 64 experts: every thread ranks one expert first
         if (ranked) select_rank_wg(a.sel, smem, blockIdx.x == 0 ? a.sel.logits : nullptr, pre);
+        // ids only; workgroup 0 publishes the softmax weights once its
+        // weight loads are in flight
         if (q == 0) select_topk_wave(a.sel, smem, &ssel, false, a.stamps ? a.stamps + 12288 + (size_t)blockIdx.x * 4 : nullptr,
-                                     nullptr, ranked);
+                                     nullptr, ranked, true);
         __syncthreads();
         e = uniform(ssel.ids[ei]);
     } else {
@@ -180,6 +182,7 @@ __global__ __launch_bounds__(1024) void k_gateup_kq(KqArgs a) {
     u32x4 u[kQ4Units];
 #pragma unroll
     for (int k = 0; k < kQ4Units; k++) u[k] = __builtin_nontemporal_load(wp + k * 32);
+    if (a.sel.lstar && blockIdx.x == 0 && q == 0) select_publish(a.sel, &ssel);
 
 #pragma unroll
     for (int k = 0; k < 2; k++) {

@@ -82,9 +82,13 @@ __global__ __launch_bounds__(128 * kMaxParts) __attribute__((amdgpu_waves_per_eu
         }
     }
     int e;
+    __shared__ Selection ssel;
     if (a.sel.lstar) {
-        __shared__ Selection ssel;
-        if (w == 0) select_topk_wave(a.sel, smem, &ssel, false, a.stamps ? a.stamps + 4096 + (size_t)blockIdx.x * 4 : nullptr, &pre);
+        // ids only; workgroup 0 publishes the softmax weights once its weight
+        // loads are in flight
+        if (w == 0)
+            select_topk_wave(a.sel, smem, &ssel, false, a.stamps ? a.stamps + 4096 + (size_t)blockIdx.x * 4 : nullptr, &pre,
+                             false, true);
         RSTAMP(5);
         // barrier on LDS only (s_barrier without a wait for the activation loads)
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
@@ -103,6 +107,7 @@ __global__ __launch_bounds__(128 * kMaxParts) __attribute__((amdgpu_waves_per_eu
         const int t = min(kTilesPerWG * tp + j, tiles - 1);
         load_sub(a.w + ((((size_t)e * tiles + t) * P + q) * kUnits) * 64 + lane, 64, ub, wv[j]);
     }
+    if (a.sel.lstar && blockIdx.x == 0 && w == 0) select_publish(a.sel, &ssel);
     const float* bias = (lane >> 5) ? a.up_b : a.gate_b;
     const int tw = kTilesPerWG * tp + w;                       // the tile whose epilogue wave w runs (w < kTilesPerWG)
     float bias_pf = 0.0f;

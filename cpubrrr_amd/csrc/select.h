@@ -352,9 +352,15 @@ CPB_DEV void select_rank_wg(const SelectIn& s, unsigned char* lds, float* logits
 // ranked: select_rank_wg ran first (the logits were published there); the
 // wave certifies its LDS ranking and, on the rare exact path, reloads the
 // intervals.
+// defer: write only ids, logits and the fallback flag to *out (what the
+// caller needs to start its weight loads); the softmax weights and the
+// published ids / weights follow from select_publish, which workgroup 0 runs
+// once its loads are in flight.
+CPB_DEV void select_publish(const SelectIn& s, const Selection* out);
 template <int EXACT_CAND = 1, int EXACT_CHUNK = 1>
 CPB_DEV void select_topk_wave(const SelectIn& s, unsigned char* lds, Selection* out, bool publish_logits = false,
-                              unsigned long long* st = nullptr, const SelectPre* pre = nullptr, bool ranked = false) {
+                              unsigned long long* st = nullptr, const SelectPre* pre = nullptr, bool ranked = false,
+                              bool defer = false) {
     const int lane = threadIdx.x & 63;
     SSTAMP(0);
     const int NE = s.ne, K = s.k;
@@ -426,8 +432,14 @@ CPB_DEV void select_topk_wave(const SelectIn& s, unsigned char* lds, Selection* 
         const float mu = key_float(wave_max_u32(float_key(sel ? -__builtin_inff() : hi)));
         wave_lds_order();
         float later = mu;
-        if (sel)
-            for (int j = rank + 1; j < K; j++) later = fmaxf(later, sHi[j]);
+        {
+            // the later ranks' upper bounds in two 16-byte reads
+            const f32x4 h0 = *(const f32x4*)sHi, h1 = *(const f32x4*)(sHi + 4);
+            const float hs[8] = {h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
+#pragma unroll
+            for (int j = 1; j < 8; j++)
+                if (sel && j > rank && j < K) later = fmaxf(later, hs[j]);
+        }
         bad = __any(sel && !(lo > later));
         if (lane < K) { my_e = sE[lane]; my_l = sLf[lane]; }
         wave_lds_order();
@@ -492,6 +504,22 @@ CPB_DEV void select_topk_wave(const SelectIn& s, unsigned char* lds, Selection* 
         select_exact_path<EXACT_CAND, EXACT_CHUNK>(lds, NE, K, s.router_w, s.router_b, s.xn, s.d);
         if (lane < K) { my_e = sSel[lane]; my_l = (float)sL[my_e]; }
     }
+    if (defer) {
+        if (lane < K) {
+            out->ids[lane] = my_e;
+            out->logit[lane] = my_l;
+        }
+        if (lane == 0) out->fallback = bad ? 1 : 0;
+        if (blockIdx.x == 0 && blockIdx.y == 0 && s.logits && !ranked) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int e = lane + 64 * j;
+                if (e < NE) s.logits[e] = lf[j];
+            }
+        }
+        SSTAMP(3);
+        return;
+    }
     // softmax over the k selected, reference order: ex_i = exp(l_i - l_0)
     // (lane i), then the serial sum ex_0 + ex_1 + ...
     const float l0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_l), 0));
@@ -532,6 +560,26 @@ CPB_DEV void select_topk_wave(const SelectIn& s, unsigned char* lds, Selection* 
         }
         if (lane == 0 && s.fallback) s.fallback[0] = bad ? 1 : 0;
     }
+}
+
+// Softmax over the k experts of a deferred selection (reference order, as in
+// select_topk_wave) and the routed ids / weights / used logits for later
+// launches.  One wavefront of workgroup 0.
+CPB_DEV void select_publish(const SelectIn& s, const Selection* out) {
+    const int lane = threadIdx.x & 63, K = s.k;
+    const int my_e = lane < K ? out->ids[lane] : 0;
+    const float my_l = lane < K ? out->logit[lane] : 0.0f;
+    const float l0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_l), 0));
+    const float ex = expf(my_l - l0);
+    float wsum = 0.0f;
+    for (int i = 0; i < K; i++) wsum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ex), i));
+    const float wt = ex / wsum;
+    if (lane < K) {
+        s.ids[lane] = my_e;
+        s.wts[lane] = wt;
+        if (s.logits) s.logits[my_e] = my_l;     // as used (exact serial value after a fallback)
+    }
+    if (lane == 0 && s.fallback) s.fallback[0] = out->fallback;
 }
 
 }  // namespace cpb
