@@ -532,7 +532,7 @@ int launch_grouped_layer(const GroupedArgs& a, bool trace, hipStream_t s) {
     const int nt = a.n_tok;
     launch(k_prep_batch, dim3(nt), dim3(256), sizeof(float) * (2 * a.d + 64), s, a);
     launch(k_router_batch, dim3(a.ne, (nt + kRouteTok - 1) / kRouteTok), dim3(256), sizeof(double) * 64, s, a);
-    launch(k_select_batch, dim3(nt), dim3(64), select_lds_bytes(a.ne, a.d), s, a);
+    launch(k_select_batch, dim3(nt), dim3(64), select_lds_bytes(a.ne, a.d, kExactGroupWide), s, a);
     launch(k_group, dim3(1), dim3(1024), 0, s, a);
     // one workgroup per (token tile, row group), dealt out by grouped_item:
     // 8 slots per XCD round, enough for the largest tile count

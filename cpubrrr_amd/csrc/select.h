@@ -15,8 +15,11 @@
 
 namespace cpb {
 
-// candidates whose exact serial logits are computed side by side
+// candidates whose exact serial logits are computed side by side: four in
+// the decode kernels (their LDS budget), eight in the batched selection
 constexpr int kExactGroup = 4;
+constexpr int kExactGroupWide = 8;
+CPB_DEV_HOST_INLINE constexpr int exact_group(int cand) { return cand > 1 ? kExactGroupWide : kExactGroup; }
 // LDS floats per candidate's product row: d plus the chain's look-ahead slack
 // (64 floats), a multiple of 4 (16-byte reads) that spreads the chain lanes
 // over the banks
@@ -46,11 +49,14 @@ struct Selection {
 // reaches the lowest lower bound of the provisional top-k, then rank those
 // exactly (descending, lowest index first).  sL / sH: LDS values and upper
 // bounds of all NE experts; sSel: LDS [K] provisional choice, overwritten;
-// pst: LDS scratch of kExactGroup * exact_stride(d) floats.  One wavefront.
+// pst: LDS scratch of exact_group(CAND) * exact_stride(d) floats and as many
+// ints.  One wavefront.
 template <int CAND, int CHUNK>
 CPB_DEV void exact_reselect(double* sL, const double* sH, int* sSel, int NE, int K, const float* __restrict__ router_w,
                             const float* __restrict__ router_b, const float* __restrict__ xn, int d, float* pst) {
     const int lane = threadIdx.x & 63;
+    constexpr int NG = exact_group(CAND);
+    int* sCand = (int*)(pst + NG * exact_stride(d));   // [NG]
     // candidates: intervals reaching the lowest lower bound of the selected
     double tau = 1e300;
     for (int i = 0; i < K; i++) { const int e = sSel[i]; tau = fmin(tau, sL[e] - (sH[e] - sL[e])); }
@@ -64,18 +70,21 @@ CPB_DEV void exact_reselect(double* sL, const double* sH, int* sSel, int NE, int
     // candidate c's serial chain acc = b; acc += p_j over them
     int e_next = 0;
     for (;;) {
-        static_assert(kExactGroup == 4, "group of four named candidates");
-        int g[kExactGroup] = {0, 0, 0, 0}, ng = 0;
-        for (; e_next < NE && ng < kExactGroup; e_next++) {
+        // the group's candidates (wave-uniform scan), their ids in LDS
+        int ng = 0;
+        for (; e_next < NE && ng < NG; e_next++) {
             if (!(sH[e_next] >= tau)) continue;
-            if (ng == 0) g[0] = e_next; else if (ng == 1) g[1] = e_next; else if (ng == 2) g[2] = e_next; else g[3] = e_next;
+            if (lane == 0) sCand[ng] = e_next;
             ng++;
         }
         if (ng == 0) break;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         if constexpr (CAND == 1) {
             // one 16-byte load pair per lane in flight (few registers)
             for (int c = 0; c < ng; c++) {
-                const int ec = c == 0 ? g[0] : c == 1 ? g[1] : c == 2 ? g[2] : g[3];
+                const int ec = sCand[c];
                 const __amdgpu_buffer_rsrc_t rw = buf_rsrc(router_w + (size_t)ec * d, (uint32_t)d * 4);
                 for (int j = 4 * lane; j < d; j += 256) {
                     const u32x4 w4 = __builtin_amdgcn_raw_buffer_load_b128(rw, (uint32_t)j * 4, 0, 0);
@@ -101,7 +110,7 @@ CPB_DEV void exact_reselect(double* sL, const double* sH, int* sSel, int NE, int
     #pragma unroll
                     for (int ci = 0; ci < CAND; ci++) {
                         const int c = c0 + ci;
-                        const int ec = c == 0 ? g[0] : c == 1 ? g[1] : c == 2 ? g[2] : g[3];
+                        const int ec = sCand[c < ng ? c : 0];
                         const __amdgpu_buffer_rsrc_t rw = buf_rsrc(router_w + (size_t)ec * d, c < ng ? (uint32_t)d * 4 : 0u);
     #pragma unroll
                         for (int k = 0; k < CHUNK; k++) {
@@ -132,7 +141,7 @@ CPB_DEV void exact_reselect(double* sL, const double* sH, int* sSel, int NE, int
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         if (lane < ng) {
-            const int e = lane == 0 ? g[0] : lane == 1 ? g[1] : lane == 2 ? g[2] : g[3];
+            const int e = sCand[lane];
             const float* pr = pst + lane * stride;
             float acc = router_b ? router_b[e] : 0.0f;
             int j = 0;
@@ -200,7 +209,9 @@ struct SelectIn {
     int32_t* fallback;       // [1]
 };
 // LDS bytes select_topk_wave may use (its exact fallback)
-CPB_DEV_HOST_INLINE size_t select_lds_bytes(int ne, int d) { return sizeof(double) * 2 * ne + 64 + sizeof(float) * kExactGroup * exact_stride(d); }
+CPB_DEV_HOST_INLINE size_t select_lds_bytes(int ne, int d, int group = kExactGroup) {
+    return sizeof(double) * 2 * ne + 64 + sizeof(float) * group * exact_stride(d) + sizeof(int) * group;
+}
 
 // Wave-wide maximum of a 32-bit unsigned value via DPP (quad swaps, half-row
 // and row mirrors, row broadcasts 15 / 31), returned wave-uniform.
