@@ -83,6 +83,13 @@ def test_20b_layer_zipf_norm(gpu):
         run_case(2880, 2880, 32, 4, seed=0, layer=layer, apply_norm=True, zipf=1.1)
 
 
+def test_128_experts(gpu):
+    # more than 64 experts (the gpt-oss-120b router width): the selection's
+    # serial-round path, with and without the norm and a skewed router
+    run_case(480, 480, 128, 4, seed=8)
+    run_case(960, 480, 128, 4, seed=9, apply_norm=True, zipf=1.1)
+
+
 def test_router_tie_uses_exact_fallback(gpu):
     say("case router tie")
     d, dff, ne, k = 480, 480, 8, 4
