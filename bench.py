@@ -98,33 +98,64 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
+def _host_info() -> dict:
+    """nproc, the cores this process may run on, and the CPU model."""
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = os.cpu_count() or 1
+    return {"nproc": os.cpu_count() or 1, "usable": usable, "model": model}
+
+
 def cpu_baseline(host_layers, c, budget_s: float) -> dict:
     """Oracle (C restatement of the reference path, OpenMP over rows) on the
-    host's cores, over the first layers of the same workload."""
+    host's cores, over the first layers of the same workload: threaded over
+    every core this process may use (capped by OMP_NUM_THREADS, the host's
+    per-GPU CPU share on the GPU boxes), and single-threaded."""
     import numpy as np
     from oracle import oracle as O
     from cpubrrr_amd import synth
 
-    threads = min(16, os.cpu_count() or 1)
-    O.set_threads(threads)
-    x = synth.token(c["d"], 0, 12345)
-    n = 0
-    t0 = time.perf_counter()
+    info = _host_info()
+    threads = info["usable"]
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        threads = min(threads, int(os.environ["OMP_NUM_THREADS"]))
     fwd = O.qwen_moe if c["family"] == "qwen" else O.gptoss_moe
-    # a batch of tokens is n_tok independent decodes for the reference path
-    while time.perf_counter() - t0 < budget_s or n == 0:
-        L = host_layers[n % len(host_layers)]
-        x, _ = fwd(L, x, c["norm"])
-        n += 1
-    dt = time.perf_counter() - t0
-    per_layer = dt / n
     lb = layer_bytes(c)["total"]
+
+    def run(nth, budget):
+        O.set_threads(nth)
+        x = synth.token(c["d"], 0, 12345)
+        n = 0
+        t0 = time.perf_counter()
+        # a batch of tokens is n_tok independent decodes for the reference path
+        while time.perf_counter() - t0 < budget or n == 0:
+            L = host_layers[n % len(host_layers)]
+            x, _ = fwd(L, x, c["norm"])
+            n += 1
+        return n, time.perf_counter() - t0
+
+    n, dt = run(threads, budget_s)
+    n1, dt1 = run(1, budget_s / 2)
+    per_layer, per_layer1 = dt / n, dt1 / n1
     tok_s = 1.0 / (per_layer * c["per_step"])
     return {"value": round(tok_s, 3), "unit": "tok/s", "cores": threads,
             "kind": "port", "sample": f"{n} MoE layers ({len(host_layers)} distinct) of the same workload in "
-                                       f"{dt:.1f} s; {per_layer * 1e3:.2f} ms/layer, "
+                                       f"{dt:.1f} s on {threads} threads; {per_layer * 1e3:.2f} ms/layer, "
                                        f"{lb / per_layer / 1e9:.2f} GB/s algorithmic",
-            "ms_per_layer": round(per_layer * 1e3, 3)}
+            "ms_per_layer": round(per_layer * 1e3, 3),
+            "single_thread": {"value": round(1.0 / (per_layer1 * c["per_step"]), 3), "unit": "tok/s",
+                              "ms_per_layer": round(per_layer1 * 1e3, 3), "layers": n1},
+            "host": {"nproc": info["nproc"], "usable_cores": info["usable"], "cpu_model": info["model"],
+                     "omp_num_threads": os.environ.get("OMP_NUM_THREADS")}}
 
 
 def main() -> int:
@@ -166,7 +197,7 @@ def main() -> int:
         else:
             L = synth.gptoss_layer(d, dff, ne, k, seed=0, layer=l, zipf=c["zipf"])
         blk.load_layer(l, L)
-        if l < 2:
+        if l < 8:
             host_keep.append(L)
         del L
     log(f"loaded {nl} layers in {time.perf_counter() - t0:.1f} s "

@@ -41,6 +41,8 @@ SIGNATURES = {
     "cpb_moe_create": (C.c_int, [C.POINTER(MoeCfg), C.c_int, C.POINTER(C.c_void_p)]),
     "cpb_moe_load_layer": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p,
                                      f32p, f32p, f32p, f32p, f32p, f32p]),
+    "cpb_moe_load_layer_typed": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p,
+                                           C.c_void_p, f32p, f32p, f32p, f32p, f32p, f32p]),
     "cpb_moe_forward": (C.c_int, [C.c_void_p, C.c_int, f32p, C.c_int, C.c_int, C.POINTER(MoeTrace)]),
     "cpb_moe_forward_device": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_int]),
     "cpb_moe_set_stream": (C.c_int, [C.c_void_p, C.c_void_p]),

@@ -52,6 +52,7 @@ struct LayerDev {
     cpb::u32x4* dn = nullptr;   // down stream
     float *gate_b = nullptr, *up_b = nullptr, *down_b = nullptr;
     float *router_w = nullptr, *router_b = nullptr, *norm_w = nullptr;
+    int gu_type = 0, down_type = 0;   // GGUF type ids of this layer's gate/up and down tensors
     bool loaded = false;
     bool mfma_exact = false;    // MXFP4 scales all in [32, 254]: the grouped matrix-core path is exact
 };
@@ -99,8 +100,11 @@ struct cpb_moe {
     int32_t *g_ids = nullptr, *g_fallback = nullptr, *g_sorted = nullptr, *g_ntiles = nullptr;
     int4* g_tiles = nullptr;
     unsigned* d_special = nullptr;
-    // captured HIP graphs of forward_device calls, keyed by their arguments
-    std::map<std::tuple<int, int, float*, int, int, hipStream_t>, hipGraphExec_t> graphs;
+    // captured HIP graphs of forward_device calls, keyed by their arguments,
+    // with the call counter of their last use (least recently used evicted
+    // beyond kMaxGraphs)
+    std::map<std::tuple<int, int, float*, int, int, hipStream_t>, std::pair<hipGraphExec_t, unsigned long long>> graphs;
+    unsigned long long graph_clock = 0;
     bool use_graphs = true;
     // timing
     bool timing = false;
@@ -231,24 +235,49 @@ struct Timer {
     }
 };
 
+// Trace buffers, allocated on the first traced call: all of them or none
+// (a failed allocation frees the ones already made, so no later call sees a
+// partial set).  Down sums are sized for two per superblock, the larger of
+// Q4_K's {sumi, mint} and Q6_K's {sumi}, since the type is per layer.
+void free_trace(cpb_moe_t* h) {
+    void* p[] = {h->t_gu, h->t_h, h->t_dn, h->t_gu_sums, h->t_dn_sums};
+    for (void* q : p) if (q) hipFree(q);
+    h->t_gu = h->t_h = h->t_dn = nullptr;
+    h->t_gu_sums = h->t_dn_sums = nullptr;
+}
 int ensure_trace(cpb_moe_t* h) {
-    if (h->t_gu) return 0;
+    if (h->t_gu && h->t_h && h->t_dn && h->t_gu_sums && h->t_dn_sums) return 0;
+    free_trace(h);
     const auto& c = h->cfg;
     size_t k = c.top_k;
-    int r;
-    if ((r = dmalloc(&h->t_gu, k * 2 * c.d_ff))) return r;
-    if ((r = dmalloc(&h->t_h, k * c.d_ff))) return r;
-    if ((r = dmalloc(&h->t_dn, k * c.d))) return r;
     size_t gs = h->mx ? k * 2 * c.d_ff * (c.d / 32) : k * 2 * c.d_ff * (c.d / 256) * 2;
-    size_t ds = h->mx ? k * c.d * (c.d_ff / 32) : k * c.d * (c.d_ff / 256) * (c.wtype_down == CPB_GGUF_Q4_K ? 2 : 1);
-    if ((r = dmalloc(&h->t_gu_sums, gs))) return r;
-    if ((r = dmalloc(&h->t_dn_sums, ds))) return r;
+    size_t ds = h->mx ? k * c.d * (c.d_ff / 32) : k * c.d * (c.d_ff / 256) * 2;
+    int r;
+    if ((r = dmalloc(&h->t_gu, k * 2 * c.d_ff)) || (r = dmalloc(&h->t_h, k * c.d_ff)) || (r = dmalloc(&h->t_dn, k * c.d)) ||
+        (r = dmalloc(&h->t_gu_sums, gs)) || (r = dmalloc(&h->t_dn_sums, ds))) {
+        free_trace(h);
+        return r;
+    }
     return 0;
 }
 
 void clear_graphs(cpb_moe_t* h) {
-    for (auto& g : h->graphs) hipGraphExecDestroy(g.second);
+    for (auto& g : h->graphs) hipGraphExecDestroy(g.second.first);
     h->graphs.clear();
+}
+
+// A caller that passes a new x pointer or token count on every call would
+// otherwise grow the cache without bound.
+constexpr size_t kMaxGraphs = 16;
+void evict_lru_graph(cpb_moe_t* h) {
+    auto old = h->graphs.begin();
+    for (auto it = h->graphs.begin(); it != h->graphs.end(); ++it)
+        if (it->second.second < old->second.second) old = it;
+    // the graph may still be executing on the stream: destroying an exec
+    // that is in flight is not allowed
+    hipStreamSynchronize(h->stream);
+    hipGraphExecDestroy(old->second.first);
+    h->graphs.erase(old);
 }
 
 // One token through one layer, x at device address dx.
@@ -301,7 +330,7 @@ int layer_token(cpb_moe_t* h, int layer, float* dx, int apply_norm, bool trace) 
         }
     } else {
         cpb::KqArgs k{};
-        k.gu = L.gu; k.dn = L.dn; k.down_type = c.wtype_down;
+        k.gu = L.gu; k.dn = L.dn; k.down_type = L.down_type;
         k.xq = h->xq; k.xs = h->xsb; k.xsum = h->xsum; k.ids = h->ids; k.wts = h->wts;
         {
             k.sel.lstar = h->lstar; k.sel.lbound = h->lbound; k.sel.router_w = L.router_w; k.sel.router_b = L.router_b;
@@ -407,8 +436,30 @@ int cpb_moe_load_layer(cpb_moe_t* h, int layer, const void* gate, const void* up
                        const float* gate_b, const float* up_b, const float* down_b,
                        const float* router_w, const float* router_b, const float* norm_w) {
     if (!h) return fail(CPB_EINVAL, "handle is NULL");
+    return cpb_moe_load_layer_typed(h, layer, h->cfg.wtype_gate_up, h->cfg.wtype_gate_up, h->cfg.wtype_down, gate, up,
+                                    down, gate_b, up_b, down_b, router_w, router_b, norm_w);
+}
+
+int cpb_moe_load_layer_typed(cpb_moe_t* h, int layer, int gate_type, int up_type, int down_type, const void* gate,
+                             const void* up, const void* down, const float* gate_b, const float* up_b,
+                             const float* down_b, const float* router_w, const float* router_b,
+                             const float* norm_w) {
+    if (!h) return fail(CPB_EINVAL, "handle is NULL");
     const auto& c = h->cfg;
     if (layer < 0 || layer >= c.n_layer) return fail(CPB_EINVAL, "layer %d out of range", layer);
+    // per-tensor type dispatch (engine_qwen2.rs:202-233 reads each matrix's
+    // GGUF type): the MXFP4 kernels take type 39 only; the k-quant kernels
+    // take Q4_K gate/up and a Q4_K or Q6_K down, chosen per layer
+    if (h->mx) {
+        if (gate_type != CPB_GGUF_MXFP4 || up_type != CPB_GGUF_MXFP4 || down_type != CPB_GGUF_MXFP4)
+            return fail(CPB_EINVAL, "layer %d: MXFP4 handle needs type 39 for gate/up/down, got %d/%d/%d", layer,
+                        gate_type, up_type, down_type);
+    } else {
+        if (gate_type != CPB_GGUF_Q4_K || up_type != CPB_GGUF_Q4_K)
+            return fail(CPB_EINVAL, "layer %d: k-quant gate/up must be Q4_K (12), got %d/%d", layer, gate_type, up_type);
+        if (down_type != CPB_GGUF_Q4_K && down_type != CPB_GGUF_Q6_K)
+            return fail(CPB_EINVAL, "layer %d: k-quant down must be Q4_K (12) or Q6_K (14), got %d", layer, down_type);
+    }
     if (!gate || !up || !down || !router_w) return fail(CPB_EINVAL, "gate/up/down/router_w must not be NULL");
     if (c.has_bias && (!gate_b || !up_b || !down_b || !router_b))
         return fail(CPB_EINVAL, "has_bias set but a bias pointer is NULL");
@@ -418,8 +469,8 @@ int cpb_moe_load_layer(cpb_moe_t* h, int layer, const void* gate, const void* up
     LayerDev& L = h->layers[layer];
     free_layer(L);
     const size_t ne = c.n_expert, d = c.d, ff = c.d_ff;
-    const size_t gbytes = ne * ff * row_bytes(c.wtype_gate_up, d);
-    const size_t dbytes = ne * d * row_bytes(c.wtype_down, ff);
+    const size_t gbytes = ne * ff * row_bytes(gate_type, d);
+    const size_t dbytes = ne * d * row_bytes(down_type, ff);
     int r;
     if (h->mx) {
         if ((r = ensure_staging(h, 2 * gbytes > dbytes ? 2 * gbytes : dbytes))) return r;
@@ -447,8 +498,8 @@ int cpb_moe_load_layer(cpb_moe_t* h, int layer, const void* gate, const void* up
             return fail(CPB_ENODEV, "repack launch failed");
         HIP_OK(hipStreamSynchronize(h->stream));
         HIP_OK(hipMemcpyAsync(h->staging, down, dbytes, hipMemcpyHostToDevice, h->stream));
-        if ((r = dmalloc((uint8_t**)&L.dn, cpb::kq_down_bytes(ne, d, ff, c.top_k, c.wtype_down)))) return r;
-        if (cpb::launch_repack_kq_down(h->staging, L.dn, ne, d, ff, c.top_k, c.wtype_down, h->stream))
+        if ((r = dmalloc((uint8_t**)&L.dn, cpb::kq_down_bytes(ne, d, ff, c.top_k, down_type)))) return r;
+        if (cpb::launch_repack_kq_down(h->staging, L.dn, ne, d, ff, c.top_k, down_type, h->stream))
             return fail(CPB_ENODEV, "repack launch failed");
     }
     const ParamSlots ps = param_slots(c);
@@ -468,6 +519,8 @@ int cpb_moe_load_layer(cpb_moe_t* h, int layer, const void* gate, const void* up
         HIP_OK(hipMemcpy(&special, h->d_special, sizeof special, hipMemcpyDeviceToHost));
         L.mfma_exact = special == 0;
     }
+    L.gu_type = gate_type;
+    L.down_type = down_type;
     L.loaded = true;
     return 0;
 }
@@ -518,11 +571,17 @@ int cpb_moe_forward_device(cpb_moe_t* h, int layer0, int n_layers, float* d_x, i
     HIP_OK(hipSetDevice(h->device));
     // per-kernel timing needs one event pair per launch: run those directly
     if (h->timing || !h->use_graphs) return launch_direct(h, layer0, n_layers, d_x, n_tok, apply_norm);
+    // a caller capturing this stream into a graph of its own gets the
+    // kernels themselves in that graph
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    HIP_OK(hipStreamIsCapturing(h->stream, &cap));
+    if (cap != hipStreamCaptureStatusNone) return launch_direct(h, layer0, n_layers, d_x, n_tok, apply_norm);
     // replay one captured graph per distinct call (launch overhead of ~3
     // kernels per layer paid once)
     auto key = std::make_tuple(layer0, n_layers, d_x, n_tok, apply_norm, h->stream);
     auto it = h->graphs.find(key);
     if (it == h->graphs.end()) {
+        if (h->graphs.size() >= kMaxGraphs) evict_lru_graph(h);
         HIP_OK(hipStreamBeginCapture(h->stream, hipStreamCaptureModeThreadLocal));
         int r = launch_direct(h, layer0, n_layers, d_x, n_tok, apply_norm);
         hipGraph_t g = nullptr;
@@ -533,9 +592,10 @@ int cpb_moe_forward_device(cpb_moe_t* h, int layer0, int n_layers, float* d_x, i
         ec = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
         hipGraphDestroy(g);
         if (ec != hipSuccess) return fail(CPB_ENODEV, "graph instantiate failed: %s", hipGetErrorString(ec));
-        it = h->graphs.emplace(key, ge).first;
+        it = h->graphs.emplace(key, std::make_pair(ge, 0ull)).first;
     }
-    HIP_OK(hipGraphLaunch(it->second, h->stream));
+    it->second.second = ++h->graph_clock;
+    HIP_OK(hipGraphLaunch(it->second.first, h->stream));
     return 0;
 }
 
@@ -604,7 +664,7 @@ int cpb_moe_forward(cpb_moe_t* h, int layer, float* x, int n_tok, int apply_norm
         r |= cp(tr->hsum, h->hsum, mx ? 0 : k * ff / 32 * 4);
         r |= cp(tr->dn, h->t_dn, k * d * 4);
         r |= cp(tr->dn_sums, h->t_dn_sums,
-                (mx ? k * d * (ff / 32) : k * d * (ff / 256) * (c.wtype_down == CPB_GGUF_Q4_K ? 2 : 1)) * 4);
+                (mx ? k * d * (ff / 32) : k * d * (ff / 256) * (h->layers[layer].down_type == CPB_GGUF_Q4_K ? 2 : 1)) * 4);
         r |= cp(tr->h, mx ? h->t_h : h->hbuf, k * ff * 4);
         int32_t fb = 0;
         r |= cp(&fb, h->fallback, 4);
@@ -618,7 +678,26 @@ int cpb_moe_forward(cpb_moe_t* h, int layer, float* x, int n_tok, int apply_norm
 
 int cpb_moe_set_stream(cpb_moe_t* h, void* stream) {
     if (!h) return fail(CPB_EINVAL, "handle is NULL");
-    h->stream = stream ? (hipStream_t)stream : h->own;
+    hipStream_t ns = stream ? (hipStream_t)stream : h->own;
+    if (ns == h->stream) return 0;
+    HIP_OK(hipSetDevice(h->device));
+    // every launch shares the handle's scratch: work on the new stream waits
+    // for what is still queued on the old one (not across a graph capture,
+    // where the capturing caller orders its own work)
+    hipStreamCaptureStatus c0 = hipStreamCaptureStatusNone, c1 = hipStreamCaptureStatusNone;
+    HIP_OK(hipStreamIsCapturing(h->stream, &c0));
+    HIP_OK(hipStreamIsCapturing(ns, &c1));
+    if (c0 != hipStreamCaptureStatusNone || c1 != hipStreamCaptureStatusNone) {
+        h->stream = ns;
+        return 0;
+    }
+    hipEvent_t ev = nullptr;
+    HIP_OK(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+    hipError_t e = hipEventRecord(ev, h->stream);
+    if (e == hipSuccess) e = hipStreamWaitEvent(ns, ev, 0);
+    hipEventDestroy(ev);
+    if (e != hipSuccess) return fail(CPB_ENODEV, "stream switch: %s", hipGetErrorString(e));
+    h->stream = ns;
     return 0;
 }
 

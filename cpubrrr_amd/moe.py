@@ -79,6 +79,7 @@ class MoeBlock:
         ccfg = cfg.c()
         L.check(self._lib.cpb_moe_create(C.byref(ccfg), device, C.byref(h)), "cpb_moe_create")
         self._h = h
+        self._down_type = {}
 
     def close(self) -> None:
         if getattr(self, "_h", None):
@@ -102,7 +103,8 @@ class MoeBlock:
         return n.value
 
     def load_layer(self, layer: int, t: dict) -> None:
-        """t: gate/up/down (native GGUF bytes), gate_b/up_b/down_b, router_w/router_b, norm_w."""
+        """t: gate/up/down (native GGUF bytes), gate_b/up_b/down_b, router_w/router_b, norm_w;
+        optional gate_type/up_type/down_type (GGUF type ids, default: the config's)."""
         keep = {k: (np.ascontiguousarray(t[k]) if t.get(k) is not None else None)
                 for k in ("gate", "up", "down", "gate_b", "up_b", "down_b", "router_w", "router_b", "norm_w")}
         for k in ("gate_b", "up_b", "down_b", "router_w", "router_b", "norm_w"):
@@ -111,11 +113,16 @@ class MoeBlock:
         if not self.cfg.has_bias:
             for k in ("gate_b", "up_b", "down_b", "router_b"):
                 keep[k] = None
-        rc = self._lib.cpb_moe_load_layer(
-            self._h, layer, keep["gate"].ctypes.data, keep["up"].ctypes.data, keep["down"].ctypes.data,
+        c = self.cfg
+        gt = int(t.get("gate_type", c.wtype_gate_up))
+        ut = int(t.get("up_type", c.wtype_gate_up))
+        dt = int(t.get("down_type", c.wtype_down))
+        rc = self._lib.cpb_moe_load_layer_typed(
+            self._h, layer, gt, ut, dt, keep["gate"].ctypes.data, keep["up"].ctypes.data, keep["down"].ctypes.data,
             _fp(keep["gate_b"]), _fp(keep["up_b"]), _fp(keep["down_b"]), _fp(keep["router_w"]),
             _fp(keep["router_b"]), _fp(keep["norm_w"]))
-        L.check(rc, "cpb_moe_load_layer")
+        L.check(rc, "cpb_moe_load_layer_typed")
+        self._down_type[layer] = dt
 
     def forward(self, layer: int, x: np.ndarray, apply_norm: bool = True, trace: bool = False):
         """x: [d] or [n_tok, d] fp32, updated like the reference's residual.
@@ -139,7 +146,8 @@ class MoeBlock:
                 "hsb": np.zeros((k, ff // 32) if mx else (k, ff // 256), np.float32),
                 "hsum": np.zeros((k, ff // 32), np.int32), "dn": np.zeros((k, d), np.float32),
                 "dn_sums": np.zeros((k, d, ff // 32) if mx else
-                                    ((k, d, ff // 256, 2) if c.wtype_down == L.GGUF_Q4_K else (k, d, ff // 256)),
+                                    ((k, d, ff // 256, 2) if self._down_type.get(layer, c.wtype_down) == L.GGUF_Q4_K
+                                     else (k, d, ff // 256)),
                                     np.int32),
                 "h": np.zeros((k, ff), np.float32),
             }

@@ -111,6 +111,17 @@ int cpb_moe_load_layer(cpb_moe_t* h, int layer,
                        const float* gate_b, const float* up_b, const float* down_b,
                        const float* router_w, const float* router_b, const float* norm_w);
 
+/* The same with each tensor's GGUF type id given explicitly, as a GGUF file
+ * records it per tensor (engine_qwen2.rs:202-233 dispatches every matrix on
+ * its own type; Q4_K_M Qwen3 files mix Q4_K and Q6_K ffn_down across layers).
+ * MXFP4 handles take 39 for all three; k-quant handles take Q4_K (12) gate/up
+ * and a Q4_K (12) or Q6_K (14) down, per layer.  Other types: CPB_EINVAL.
+ * cpb_moe_load_layer is this call with cfg.wtype_gate_up / wtype_down.   */
+int cpb_moe_load_layer_typed(cpb_moe_t* h, int layer, int gate_type, int up_type, int down_type,
+                             const void* gate, const void* up, const void* down,
+                             const float* gate_b, const float* up_b, const float* down_b,
+                             const float* router_w, const float* router_b, const float* norm_w);
+
 /* One MoE block on host memory: x[n_tok][d] <- x + MoE(norm(x)).
  * Replaces engine_gpt2.rs:845-923 (n_tok == 1), :1120-1239 (n_tok > 1),
  * engine_qwen2.rs:395-433.  apply_norm = 0 feeds x itself to the router and
@@ -121,12 +132,17 @@ int cpb_moe_forward(cpb_moe_t* h, int layer, float* x, int n_tok, int apply_norm
 
 /* Same on device memory, asynchronous on the handle's stream, over layers
  * [layer0, layer0 + n_layers).  d_x is a device pointer [n_tok][d].  The
- * layer loop of forward_worker (engine_gpt2.rs:767-930, MoE part only).    */
+ * layer loop of forward_worker (engine_gpt2.rs:767-930, MoE part only).
+ * Each distinct (layer0, n_layers, d_x, n_tok, apply_norm, stream) is
+ * captured once into a HIP graph and replayed (at most 16 kept, least
+ * recently used evicted).  If the stream is already being captured by the
+ * caller, the kernels are launched into the caller's capture instead.      */
 int cpb_moe_forward_device(cpb_moe_t* h, int layer0, int n_layers, float* d_x, int n_tok,
                            int apply_norm);
 
 /* Use `stream` (a hipStream_t) for all further work of this handle; NULL
- * restores the handle's own stream. */
+ * restores the handle's own stream.  Ordered: work issued on the new stream
+ * waits for everything already queued on the old one. */
 int cpb_moe_set_stream(cpb_moe_t* h, void* stream);
 int cpb_moe_sync(cpb_moe_t* h);
 void cpb_moe_destroy(cpb_moe_t* h);

@@ -137,3 +137,33 @@ def test_qwen_router_tie_128_experts(gpu):
         check_qwen(L, x, True, xo, t)
         xo2, _ = blk.forward(0, x, apply_norm=True)
         assert np.array_equal(xo2.view(np.uint32), xo.view(np.uint32))
+
+
+def test_qwen_mixed_down_types_per_layer(gpu):
+    # Q4_K_M files mix Q6_K and Q4_K ffn_down across layers; each layer's
+    # tensors carry their own GGUF type (engine_qwen2.rs:202-233)
+    import torch
+    say("case qwen mixed down types: layer 0 Q6_K, layer 1 Q4_K")
+    d, dff, ne, k = 1024, 512, 32, 8
+    layers = [synth.qwen_layer(d, dff, ne, k, seed=13, layer=0, down_type=14),
+              synth.qwen_layer(d, dff, ne, k, seed=13, layer=1, down_type=12)]
+    cfg = MoeConfig.qwen3(d=d, n_expert=ne, top_k=k, d_ff=dff, n_layer=2, down_type=14)
+    x0 = synth.token(d, 13, 0)
+    with MoeBlock(cfg) as blk:
+        # a type the k-quant kernels do not take is rejected, not misread
+        bad = dict(layers[1], down_type=39)
+        with pytest.raises(Exception) as ei:
+            blk.load_layer(1, bad)
+        assert getattr(ei.value, "code", None) == -22
+        x = x0.copy()
+        for l, L in enumerate(layers):
+            blk.load_layer(l, L)
+            xo, t = blk.forward(l, x, apply_norm=True, trace=True)
+            check_qwen(L, x, True, xo, t)
+            x = xo
+        xd = torch.from_numpy(x0.copy()).to("cuda:0")
+        torch.cuda.synchronize()
+        blk.forward_device(0, 2, xd.data_ptr(), 1, True)
+        blk.sync()
+        y = xd.cpu().numpy()
+    assert np.array_equal(y.view(np.uint32), x.view(np.uint32))

@@ -162,3 +162,43 @@ def test_graph_replay_matches_direct_launches(gpu):
             blk.sync()
             outs.append(x.cpu().numpy())
     assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+
+
+def test_caller_graph_capture_and_stream_switch(gpu):
+    # forward_device on a stream the caller is capturing puts the kernels in
+    # the caller's graph; replays (with eager work between them) match eager
+    # calls bit for bit.  A stream switch orders the new stream after the old.
+    import torch
+    say("case caller graph capture + stream switch")
+    d, ne, k, nl = 960, 16, 4, 2
+    layers = [synth.gptoss_layer(d, d, ne, k, seed=21, layer=l, zipf=1.1) for l in range(nl)]
+    with MoeBlock(MoeConfig.gptoss(d=d, n_expert=ne, top_k=k, d_ff=d, n_layer=nl)) as blk:
+        for l in range(nl):
+            blk.load_layer(l, layers[l])
+        x0 = torch.from_numpy(synth.token(d, 21, 0)).to("cuda:0")
+        ref = x0.clone()
+        for _ in range(3):
+            blk.forward_device(0, nl, ref.data_ptr(), 1, True)
+        blk.sync()
+        s = torch.cuda.Stream()
+        blk.set_stream(s.cuda_stream)
+        xg = x0.clone()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            blk.forward_device(0, nl, xg.data_ptr(), 1, True)
+        for rep in range(3):
+            xg.copy_(x0)
+            torch.cuda.synchronize()
+            for _ in range(rep + 1):
+                g.replay()
+            torch.cuda.synchronize()
+            want = x0.clone()
+            blk.set_stream(None)
+            for _ in range(rep + 1):
+                blk.forward_device(0, nl, want.data_ptr(), 1, True)
+            blk.sync()
+            blk.set_stream(s.cuda_stream)
+            assert torch.equal(xg.view(torch.int32), want.view(torch.int32)), rep
+        assert torch.equal(want.view(torch.int32), ref.view(torch.int32))
+        blk.set_stream(None)

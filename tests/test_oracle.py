@@ -116,6 +116,82 @@ def test_rmsnorm_qwen_vs_f64():
     assert np.max(np.abs(out - ref)) <= 4e-7 * np.max(np.abs(ref))
 
 
+def test_rmsnorm_qwen_slice_order_known_answer():
+    # engine_qwen2.rs:243-250, 457-467: NT static slices, each summed serially,
+    # then the NT partials summed serially.  x = [2^12, 1, 1, ...] (d = 24):
+    # in fp32, 2^24 + 1 rounds back to 2^24 (tie to even), so a serial sum
+    # stays at 2^24 while 12 slices of 2 keep 11 partials of 2:
+    # tot = 2^24 + 22 exactly.  A serial sum (nt = 1) gives 2^24.
+    d = 24
+    x = np.ones(d, np.float32)
+    x[0] = 4096.0
+    w = np.ones(d, np.float32)
+    for nt, tot in ((12, 2.0 ** 24 + 22), (1, 2.0 ** 24), (24, 2.0 ** 24)):
+        inv = f32(1.0) / np.sqrt(f32(f32(tot) / f32(d)) + f32(1e-6), dtype=np.float32)
+        out = O.rmsnorm_qwen(x, w, 1e-6, nt)
+        assert out[1] == f32(f32(1.0) * inv), (nt, out[1], inv)
+        assert out[0] == f32(f32(4096.0) * inv), nt
+    # (nt = 24: one element per slice, the partials summed serially as above)
+    # the slice order and the serial order give different scales
+    outs = {nt: O.rmsnorm_qwen(x, w, 1e-6, nt)[1] for nt in (1, 12)}
+    assert outs[1] != outs[12]
+    # uneven slices (d % nt != 0): the first d % nt slices take one more element
+    d = 26
+    x = np.ones(d, np.float32)
+    x[0] = 4096.0
+    w = np.ones(d, np.float32)
+    # slices: 2 of 3 elements, 10 of 2 -> slice 0 = 2^24 (both ones lost), slice 1 = 3,
+    # slices 2..11 = 2: tot = 2^24 + 3 + 20 -> rounds: 2^24 + 3 -> 2^24 + 4 (tie to even), + 20
+    tot = f32(2.0 ** 24)
+    for part in [3.0] + [2.0] * 10:
+        tot = f32(tot + f32(part))
+    assert tot == f32(2.0 ** 24 + 24)
+    inv = f32(1.0) / np.sqrt(f32(tot / f32(d)) + f32(1e-6), dtype=np.float32)
+    assert O.rmsnorm_qwen(x, w, 1e-6, 12)[1] == inv
+
+
+def _pack_q4k_scales(sc, mn):
+    """Pack 8 six-bit scales and mins into the 12 Q4_K scale bytes, written
+    from the format's description (ggml's quantize_row_q4_K packing): bytes
+    0-3 hold sc[0..3] plus the top 2 bits of sc[4..7]; bytes 4-7 hold
+    mn[0..3] plus the top 2 bits of mn[4..7]; bytes 8-11 hold the low nibbles
+    of sc[4..7] (low) and mn[4..7] (high)."""
+    q = [0] * 12
+    for j in range(4):
+        q[j] = sc[j] | ((sc[j + 4] >> 4) << 6)
+        q[j + 4] = mn[j] | ((mn[j + 4] >> 4) << 6)
+        q[j + 8] = (sc[j + 4] & 0xF) | ((mn[j + 4] & 0xF) << 4)
+    return q
+
+
+def test_q4k_scale_unpack_hand_built():
+    # engine_qwen2.rs:57-74 (get_scale_min_k4): a superblock with hand-packed
+    # scales/mins, d = dmin = 1.0, every quant nibble = 1, x = 1 on one
+    # sub-block only: sumi = 32 * sc_j and mint = mn_j * xsum_j recover each
+    # sub-block's 6-bit scale and min.
+    r = np.random.default_rng(7)
+    for trial in range(20):
+        sc = [int(v) for v in r.integers(0, 64, 8)]
+        mn = [int(v) for v in r.integers(0, 64, 8)]
+        if trial == 0:
+            sc, mn = [63] * 8, [63] * 8
+        if trial == 1:
+            sc, mn = [1, 2, 4, 8, 16, 32, 48, 63], [63, 32, 16, 8, 4, 2, 1, 0]
+        blk = np.zeros(144, np.uint8)
+        blk[0:2] = [0x00, 0x3C]          # fp16 1.0
+        blk[2:4] = [0x00, 0x3C]
+        blk[4:16] = _pack_q4k_scales(sc, mn)
+        blk[16:] = 0x11
+        for j in range(8):
+            xq = np.zeros(256, np.int8)
+            xq[32 * j:32 * j + 32] = 1
+            xsum = np.zeros(8, np.int32)
+            xsum[j] = 32
+            v, s = O.q4k_dot(blk, xq, np.ones(1, np.float32), xsum)
+            assert s[0] == 32 * sc[j] and s[1] == 32 * mn[j], (trial, j, s, sc[j], mn[j])
+            assert v == f32(32 * sc[j]) - f32(32 * mn[j])
+
+
 # ---------------------------------------------------------------- router / top-k
 def test_router_serial_order_and_bound():
     ne, d = 8, 2880
