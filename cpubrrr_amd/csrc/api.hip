@@ -46,6 +46,62 @@ int fail(int code, const char* fmt, ...) {
                         #expr, hipGetErrorString(e_));                                 \
     } while (0)
 
+// Per-call device scratch of the decode (n_tok = 1) kernels: activations,
+// routing results and h.  Carved from one block, either the handle's own
+// allocation or the library's static no-allocation scratch.
+struct DecodeBufs {
+    float* xn = nullptr;                       // [d]
+    int8_t* xq = nullptr;                      // [d], then its image [2d], xsb, xsum
+    uint8_t* ximg = nullptr;
+    float* xsb = nullptr;
+    int32_t* xsum = nullptr;
+    double *lstar = nullptr, *lbound = nullptr;  // [E]
+    float* logits = nullptr;                   // [E]
+    int32_t* ids = nullptr;                    // [k]
+    float* wts = nullptr;                      // [k]
+    int32_t* fallback = nullptr;               // [1]
+    int8_t* hq = nullptr;                      // [k*ff], then its image [2*k*ff], hsb
+    uint8_t* himg = nullptr;
+    float* hsb = nullptr;
+    int32_t* hsum = nullptr;                   // [k*ff/32]
+    float* hbuf = nullptr;                     // [k*ff]
+};
+
+// Lay out the decode scratch for cfg from base (null: sizing only); returns
+// the bytes used.  Every piece starts on a 256-byte boundary.
+size_t carve_decode(const cpb_moe_cfg& c, unsigned char* base, DecodeBufs* b) {
+    const size_t d = c.d, ff = c.d_ff, k = c.top_k, ne = c.n_expert;
+    size_t o = 0;
+    auto take = [&](size_t bytes) -> unsigned char* {
+        unsigned char* p = base ? base + o : nullptr;
+        o += (bytes + 255) / 256 * 256;
+        return p;
+    };
+    DecodeBufs t;
+    t.xn = (float*)take(4 * d);
+    t.xq = (int8_t*)take(3 * d + 8 * (d / 32));
+    t.lstar = (double*)take(8 * ne);
+    t.lbound = (double*)take(8 * ne);
+    t.logits = (float*)take(4 * ne);
+    t.ids = (int32_t*)take(4 * k);
+    t.wts = (float*)take(4 * k);
+    t.fallback = (int32_t*)take(4);
+    t.hq = (int8_t*)take(3 * k * ff + 4 * (k * ff / 32));
+    t.hsum = (int32_t*)take(4 * (k * ff / 32));
+    t.hbuf = (float*)take(4 * k * ff);
+    if (base) {
+        // xq, its matrix-core image (2 bytes per element), the x scales and
+        // the per-32 sums share one piece, and so do hq, its image and the hq scales
+        t.ximg = (uint8_t*)(t.xq + d);
+        t.xsb = (float*)(t.xq + 3 * d);
+        t.xsum = (int32_t*)(t.xq + 3 * d + 4 * (d / 32));
+        t.himg = (uint8_t*)(t.hq + k * ff);
+        t.hsb = (float*)(t.hq + 3 * k * ff);
+    }
+    if (b) *b = t;
+    return o;
+}
+
 struct LayerDev {
     cpb::u32x4* gu = nullptr;   // gate+up stream layout
     cpb::u32x4* up = nullptr;   // unused (kept null)
@@ -69,21 +125,8 @@ struct cpb_moe {
     // activations / routing (device)
     float* params = nullptr;              // per-layer router / norm / bias parameters (one arena)
     float* x = nullptr;
-    float* xn = nullptr;
-    int8_t* xq = nullptr;
-    uint8_t* ximg = nullptr;
-    float* xsb = nullptr;
-    int32_t* xsum = nullptr;
-    double *lstar = nullptr, *lbound = nullptr;
-    float* logits = nullptr;
-    int32_t* ids = nullptr;
-    float* wts = nullptr;
-    int32_t* fallback = nullptr;
-    int8_t* hq = nullptr;
-    uint8_t* himg = nullptr;
-    float* hsb = nullptr;
-    int32_t* hsum = nullptr;
-    float* hbuf = nullptr;
+    unsigned char* dec_base = nullptr;    // the handle's decode scratch (one allocation)
+    DecodeBufs b;
     // trace (device, lazily allocated)
     float *t_gu = nullptr, *t_h = nullptr, *t_dn = nullptr;
     int32_t *t_gu_sums = nullptr, *t_dn_sums = nullptr;
@@ -281,7 +324,7 @@ void evict_lru_graph(cpb_moe_t* h) {
 }
 
 // One token through one layer, x at device address dx.
-int layer_token(cpb_moe_t* h, int layer, float* dx, int apply_norm, bool trace) {
+int layer_token(cpb_moe_t* h, const DecodeBufs& B, int layer, float* dx, int apply_norm, bool trace) {
     const auto& c = h->cfg;
     LayerDev& L = h->layers[layer];
     if (!L.loaded) return fail(CPB_ESTATE, "layer %d not loaded", layer);
@@ -290,8 +333,8 @@ int layer_token(cpb_moe_t* h, int layer, float* dx, int apply_norm, bool trace) 
     ra.d = c.d; ra.n_expert = c.n_expert; ra.top_k = c.top_k;
     ra.norm = c.norm; ra.norm_nt = c.norm_nt; ra.apply_norm = apply_norm; ra.eps = c.rms_eps;
     ra.qk = h->mx ? 0 : 1;
-    ra.xn = h->xn; ra.xq = h->xq; ra.ximg = h->ximg; ra.xsb = h->xsb; ra.xsum = h->xsum;
-    ra.lstar = h->lstar; ra.lbound = h->lbound;
+    ra.xn = B.xn; ra.xq = B.xq; ra.ximg = B.ximg; ra.xsb = B.xsb; ra.xsum = B.xsum;
+    ra.lstar = B.lstar; ra.lbound = B.lbound;
     unsigned long long* stamps = h->d_stamps ? h->d_stamps + (size_t)(layer % 60) * 16384 : nullptr;
     ra.stamps = stamps;
     // the route launch publishes certified logits; the gate/up kernel
@@ -303,21 +346,21 @@ int layer_token(cpb_moe_t* h, int layer, float* dx, int apply_norm, bool trace) 
     if (h->mx) {
         cpb::GateUpArgs g{};
         g.w = L.gu; g.gate_b = L.gate_b; g.up_b = L.up_b;
-        g.ximg = h->ximg; g.xsb = h->xsb;
-        g.ids = h->ids;
+        g.ximg = B.ximg; g.xsb = B.xsb;
+        g.ids = B.ids;
         g.stamps = stamps;
         {
-            g.sel.lstar = h->lstar; g.sel.lbound = h->lbound; g.sel.router_w = L.router_w; g.sel.router_b = L.router_b;
-            g.sel.xn = h->xn; g.sel.ne = c.n_expert; g.sel.k = c.top_k; g.sel.d = c.d;
-            g.sel.ids = h->ids; g.sel.wts = h->wts; g.sel.logits = h->logits; g.sel.fallback = h->fallback;
+            g.sel.lstar = B.lstar; g.sel.lbound = B.lbound; g.sel.router_w = L.router_w; g.sel.router_b = L.router_b;
+            g.sel.xn = B.xn; g.sel.ne = c.n_expert; g.sel.k = c.top_k; g.sel.d = c.d;
+            g.sel.ids = B.ids; g.sel.wts = B.wts; g.sel.logits = B.logits; g.sel.fallback = B.fallback;
         }
         g.dff = c.d_ff; g.nb = h->nb; g.nparts = h->parts_gu; g.top_k = c.top_k;
         g.alpha = c.alpha; g.limit = c.limit;
-        g.hq = h->hq; g.himg = h->himg; g.hsb = h->hsb;
+        g.hq = B.hq; g.himg = B.himg; g.hsb = B.hsb;
         g.gu = h->t_gu; g.gu_sums = h->t_gu_sums; g.h = h->t_h;
         cpb::DownArgs dn{};
-        dn.w = L.dn; dn.down_b = L.down_b; dn.himg = h->himg; dn.hsb = h->hsb;
-        dn.ids = h->ids; dn.wts = h->wts;
+        dn.w = L.dn; dn.down_b = L.down_b; dn.himg = B.himg; dn.hsb = B.hsb;
+        dn.ids = B.ids; dn.wts = B.wts;
         dn.d = c.d; dn.dff = c.d_ff; dn.nbf = h->nbf; dn.nparts = h->parts_dn; dn.top_k = c.top_k;
         dn.x = dx; dn.dn = h->t_dn; dn.dn_sums = h->t_dn_sums; dn.stamps = stamps;
         {
@@ -331,14 +374,14 @@ int layer_token(cpb_moe_t* h, int layer, float* dx, int apply_norm, bool trace) 
     } else {
         cpb::KqArgs k{};
         k.gu = L.gu; k.dn = L.dn; k.down_type = L.down_type;
-        k.xq = h->xq; k.xs = h->xsb; k.xsum = h->xsum; k.ids = h->ids; k.wts = h->wts;
+        k.xq = B.xq; k.xs = B.xsb; k.xsum = B.xsum; k.ids = B.ids; k.wts = B.wts;
         {
-            k.sel.lstar = h->lstar; k.sel.lbound = h->lbound; k.sel.router_w = L.router_w; k.sel.router_b = L.router_b;
-            k.sel.xn = h->xn; k.sel.ne = c.n_expert; k.sel.k = c.top_k; k.sel.d = c.d;
-            k.sel.ids = h->ids; k.sel.wts = h->wts; k.sel.logits = h->logits; k.sel.fallback = h->fallback;
+            k.sel.lstar = B.lstar; k.sel.lbound = B.lbound; k.sel.router_w = L.router_w; k.sel.router_b = L.router_b;
+            k.sel.xn = B.xn; k.sel.ne = c.n_expert; k.sel.k = c.top_k; k.sel.d = c.d;
+            k.sel.ids = B.ids; k.sel.wts = B.wts; k.sel.logits = B.logits; k.sel.fallback = B.fallback;
         }
         k.d = c.d; k.dff = c.d_ff; k.top_k = c.top_k;
-        k.hbuf = h->hbuf; k.hq = h->hq; k.hs = h->hsb; k.hsum = h->hsum; k.x = dx;
+        k.hbuf = B.hbuf; k.hq = B.hq; k.hs = B.hsb; k.hsum = B.hsum; k.x = dx;
         k.gu_out = h->t_gu; k.gu_sums = h->t_gu_sums; k.dn_out = h->t_dn; k.dn_sums = h->t_dn_sums;
         k.stamps = stamps;
         {
@@ -393,19 +436,10 @@ int cpb_moe_create(const cpb_moe_cfg* cfg, int device, cpb_moe_t** out) {
     h->stream = h->own;
     const size_t d = cfg->d, ff = cfg->d_ff, k = cfg->top_k, ne = cfg->n_expert, T = cfg->max_tokens;
     int r;
-    if ((r = dmalloc(&h->x, T * d)) || (r = dmalloc(&h->xn, d)) || (r = dmalloc(&h->xq, 3 * d + 8 * (d / 32))) ||
-        (r = dmalloc(&h->lstar, ne)) || (r = dmalloc(&h->lbound, ne)) ||
-        (r = dmalloc(&h->logits, ne)) || (r = dmalloc(&h->ids, k)) || (r = dmalloc(&h->wts, k)) ||
-        (r = dmalloc(&h->fallback, 1)) || (r = dmalloc(&h->hq, 3 * k * ff + 4 * (k * ff / 32))) || (r = dmalloc(&h->hsum, k * ff / 32)) || (r = dmalloc(&h->hbuf, k * ff)) ||
+    if ((r = dmalloc(&h->x, T * d)) || (r = dmalloc(&h->dec_base, carve_decode(*cfg, nullptr, nullptr))) ||
         (r = dmalloc(&h->params, param_slots(*cfg).per_layer * cfg->n_layer)))
         return bail(r);
-    // xq, its matrix-core image (2 bytes per element), the x scales and the
-    // per-32 sums share one allocation, and so do hq, its image and the hq scales
-    h->ximg = (uint8_t*)(h->xq + d);
-    h->xsb = (float*)(h->xq + 3 * d);
-    h->xsum = (int32_t*)(h->xq + 3 * d + 4 * (d / 32));
-    h->himg = (uint8_t*)(h->hq + k * ff);
-    h->hsb = (float*)(h->hq + 3 * k * ff);
+    carve_decode(*cfg, h->dec_base, &h->b);
     if (h->mx) {
         if ((r = dmalloc(&h->d_special, 1))) return bail(r);
         h->grouped = T > 1;
@@ -425,7 +459,7 @@ int cpb_moe_create(const cpb_moe_cfg* cfg, int device, cpb_moe_t** out) {
 #ifdef CPB_DECODE_STAMPS
     if ((r = dmalloc(&h->d_stamps, ((size_t)1 << 20) + 4096))) return bail(r);
 #endif
-    if (hipMemsetAsync(h->fallback, 0, sizeof(int32_t), h->stream) != hipSuccess ||
+    if (hipMemsetAsync(h->b.fallback, 0, sizeof(int32_t), h->stream) != hipSuccess ||
         hipStreamSynchronize(h->stream) != hipSuccess)
         return bail(fail(CPB_ENODEV, "init memset failed"));
     *out = h;
@@ -556,7 +590,7 @@ static int launch_direct(cpb_moe_t* h, int layer0, int n_layers, float* d_x, int
             continue;
         }
         for (int t = 0; t < n_tok; t++)
-            if (int r = layer_token(h, l, d_x + (size_t)t * c.d, apply_norm, false)) return r;
+            if (int r = layer_token(h, h->b, l, d_x + (size_t)t * c.d, apply_norm, false)) return r;
     }
     return 0;
 }
@@ -637,7 +671,7 @@ int cpb_moe_forward(cpb_moe_t* h, int layer, float* x, int n_tok, int apply_norm
     HIP_OK(hipMemcpyAsync(h->x, x, n_tok * d * sizeof(float), hipMemcpyHostToDevice, h->stream));
     if (tr) {
         if (int r = ensure_trace(h)) return r;
-        if (int r = layer_token(h, layer, h->x, apply_norm, true)) return r;
+        if (int r = layer_token(h, h->b, layer, h->x, apply_norm, true)) return r;
     } else {
         if (int r = cpb_moe_forward_device(h, layer, 1, h->x, n_tok, apply_norm)) return r;
     }
@@ -650,24 +684,24 @@ int cpb_moe_forward(cpb_moe_t* h, int layer, float* x, int n_tok, int apply_norm
             return 0;
         };
         int r = 0;
-        r |= cp(tr->xn, h->xn, d * 4);
-        r |= cp(tr->xq, h->xq, d);
-        r |= cp(tr->xsb, h->xsb, (mx ? d / 32 : d / 256) * 4);
-        r |= cp(tr->xsum, h->xsum, mx ? 0 : d / 32 * 4);
-        r |= cp(tr->logits, h->logits, ne * 4);
-        r |= cp(tr->ids, h->ids, k * 4);
-        r |= cp(tr->wts, h->wts, k * 4);
+        r |= cp(tr->xn, h->b.xn, d * 4);
+        r |= cp(tr->xq, h->b.xq, d);
+        r |= cp(tr->xsb, h->b.xsb, (mx ? d / 32 : d / 256) * 4);
+        r |= cp(tr->xsum, h->b.xsum, mx ? 0 : d / 32 * 4);
+        r |= cp(tr->logits, h->b.logits, ne * 4);
+        r |= cp(tr->ids, h->b.ids, k * 4);
+        r |= cp(tr->wts, h->b.wts, k * 4);
         r |= cp(tr->gu, h->t_gu, k * 2 * ff * 4);
         r |= cp(tr->gu_sums, h->t_gu_sums, (mx ? k * 2 * ff * (d / 32) : k * 2 * ff * (d / 256) * 2) * 4);
-        r |= cp(tr->hq, h->hq, k * ff);
-        r |= cp(tr->hsb, h->hsb, (mx ? k * ff / 32 : k * ff / 256) * 4);
-        r |= cp(tr->hsum, h->hsum, mx ? 0 : k * ff / 32 * 4);
+        r |= cp(tr->hq, h->b.hq, k * ff);
+        r |= cp(tr->hsb, h->b.hsb, (mx ? k * ff / 32 : k * ff / 256) * 4);
+        r |= cp(tr->hsum, h->b.hsum, mx ? 0 : k * ff / 32 * 4);
         r |= cp(tr->dn, h->t_dn, k * d * 4);
         r |= cp(tr->dn_sums, h->t_dn_sums,
                 (mx ? k * d * (ff / 32) : k * d * (ff / 256) * (h->layers[layer].down_type == CPB_GGUF_Q4_K ? 2 : 1)) * 4);
-        r |= cp(tr->h, mx ? h->t_h : h->hbuf, k * ff * 4);
+        r |= cp(tr->h, mx ? h->t_h : h->b.hbuf, k * ff * 4);
         int32_t fb = 0;
-        r |= cp(&fb, h->fallback, 4);
+        r |= cp(&fb, h->b.fallback, 4);
         HIP_OK(hipStreamSynchronize(h->stream));
         tr->exact_router_fallbacks = fb;
         if (r) return r;
@@ -754,8 +788,7 @@ void cpb_moe_destroy(cpb_moe_t* h) {
                      h->d_special};
     for (void* p : gbufs) hipFree(p);
     for (auto& L : h->layers) free_layer(L);
-    void* bufs[] = {h->params, h->x, h->xn, h->xq, h->lstar, h->lbound, h->logits,
-                    h->ids, h->wts, h->fallback, h->hq, h->hsum, h->hbuf, h->t_gu, h->t_h,
+    void* bufs[] = {h->params, h->x, h->dec_base, h->t_gu, h->t_h,
                     h->t_dn, h->t_gu_sums, h->t_dn_sums, h->staging};
     for (void* p : bufs) if (p) hipFree(p);
     for (auto& u : h->ev_used) { hipEventDestroy(u.second.first); hipEventDestroy(u.second.second); }
