@@ -45,6 +45,7 @@ SIGNATURES = {
                                            C.c_void_p, f32p, f32p, f32p, f32p, f32p, f32p]),
     "cpb_moe_forward": (C.c_int, [C.c_void_p, C.c_int, f32p, C.c_int, C.c_int, C.POINTER(MoeTrace)]),
     "cpb_moe_forward_device": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_int]),
+    "cpb_moe_forward_device_noalloc": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_int]),
     "cpb_moe_set_stream": (C.c_int, [C.c_void_p, C.c_void_p]),
     "cpb_moe_sync": (C.c_int, [C.c_void_p]),
     "cpb_moe_destroy": (None, [C.c_void_p]),

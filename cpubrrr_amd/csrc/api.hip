@@ -14,6 +14,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <map>
+#include <mutex>
 #include <string>
 #include <tuple>
 #include <vector>
@@ -23,6 +24,13 @@
 #include "moe_mx.h"
 #include "moe_grouped.h"
 #include "route.h"
+
+// Static decode scratch of the no-allocation entry point
+// (cpb_moe_forward_device_noalloc): one copy per GPU, held until the process
+// ends.  Host code must use the address hipGetSymbolAddress gives for the
+// current device (kept per device below), never this name.
+constexpr size_t kScratchBytes = 256 * 1024;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 namespace {
 
@@ -126,6 +134,7 @@ struct cpb_moe {
     float* params = nullptr;              // per-layer router / norm / bias parameters (one arena)
     float* x = nullptr;
     unsigned char* dec_base = nullptr;    // the handle's decode scratch (one allocation)
+    unsigned char* noalloc_base = nullptr;  // this device's static scratch (device address)
     DecodeBufs b;
     // trace (device, lazily allocated)
     float *t_gu = nullptr, *t_h = nullptr, *t_dn = nullptr;
@@ -211,6 +220,24 @@ size_t row_bytes(int type, int cols) {
     return (size_t)cols / 256 * 210;
 }
 
+// Device address of the static scratch on the current device, looked up once
+// per device (each GPU holds its own copy at its own address).
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+unsigned char* g_scratch_addr[kMaxDevices] = {};
+int scratch_address(int device, unsigned char** out) {
+    if (device < 0 || device >= kMaxDevices) return fail(CPB_EINVAL, "device %d beyond %d", device, kMaxDevices);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_addr[device]) {
+        void* p = nullptr;
+        hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) return fail(CPB_ENODEV, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+        g_scratch_addr[device] = (unsigned char*)p;
+    }
+    *out = g_scratch_addr[device];
+    return 0;
+}
+
 int ensure_staging(cpb_moe_t* h, size_t n) {
     if (h->staging_size >= n) return 0;
     if (h->staging) hipFree(h->staging);
@@ -261,8 +288,8 @@ struct Timer {
     cpb_moe_t* h;
     int cls;
     hipEvent_t a = nullptr, b = nullptr;
-    Timer(cpb_moe_t* hh, int c) : h(hh), cls(c) {
-        if (!h->timing) return;
+    Timer(cpb_moe_t* hh, int c, bool allow = true) : h(hh), cls(c) {
+        if (!h->timing || !allow) return;
         if (h->ev_pool.size() < 2) {
             for (int i = 0; i < 64; i++) { hipEvent_t e; if (hipEventCreate(&e) == hipSuccess) h->ev_pool.push_back(e); }
         }
@@ -324,7 +351,8 @@ void evict_lru_graph(cpb_moe_t* h) {
 }
 
 // One token through one layer, x at device address dx.
-int layer_token(cpb_moe_t* h, const DecodeBufs& B, int layer, float* dx, int apply_norm, bool trace) {
+int layer_token(cpb_moe_t* h, const DecodeBufs& B, int layer, float* dx, int apply_norm, bool trace,
+                bool timed = true) {
     const auto& c = h->cfg;
     LayerDev& L = h->layers[layer];
     if (!L.loaded) return fail(CPB_ESTATE, "layer %d not loaded", layer);
@@ -340,7 +368,7 @@ int layer_token(cpb_moe_t* h, const DecodeBufs& B, int layer, float* dx, int app
     // the route launch publishes certified logits; the gate/up kernel
     // selects at its start (no cross-workgroup hand-off inside a launch)
     {
-        Timer tm(h, 0);
+        Timer tm(h, 0, timed);
         if (cpb::launch_route(&ra, h->stream)) return fail(CPB_ENODEV, "route launch failed");
     }
     if (h->mx) {
@@ -364,11 +392,11 @@ int layer_token(cpb_moe_t* h, const DecodeBufs& B, int layer, float* dx, int app
         dn.d = c.d; dn.dff = c.d_ff; dn.nbf = h->nbf; dn.nparts = h->parts_dn; dn.top_k = c.top_k;
         dn.x = dx; dn.dn = h->t_dn; dn.dn_sums = h->t_dn_sums; dn.stamps = stamps;
         {
-            Timer tm(h, 1);
+            Timer tm(h, 1, timed);
             if (cpb::launch_gateup_mx(g, trace, h->stream)) return fail(CPB_ENODEV, "gate/up launch failed");
         }
         {
-            Timer tm(h, 2);
+            Timer tm(h, 2, timed);
             if (cpb::launch_down_mx(dn, trace, h->stream)) return fail(CPB_ENODEV, "down launch failed");
         }
     } else {
@@ -385,11 +413,11 @@ int layer_token(cpb_moe_t* h, const DecodeBufs& B, int layer, float* dx, int app
         k.gu_out = h->t_gu; k.gu_sums = h->t_gu_sums; k.dn_out = h->t_dn; k.dn_sums = h->t_dn_sums;
         k.stamps = stamps;
         {
-            Timer tm(h, 1);
+            Timer tm(h, 1, timed);
             if (cpb::launch_gateup_kq(k, trace, h->stream)) return fail(CPB_ENODEV, "k-quant gate/up launch failed");
         }
         {
-            Timer tm(h, 2);
+            Timer tm(h, 2, timed);
             if (cpb::launch_down_kq(k, trace, h->stream)) return fail(CPB_ENODEV, "k-quant down launch failed");
         }
     }
@@ -440,6 +468,7 @@ int cpb_moe_create(const cpb_moe_cfg* cfg, int device, cpb_moe_t** out) {
         (r = dmalloc(&h->params, param_slots(*cfg).per_layer * cfg->n_layer)))
         return bail(r);
     carve_decode(*cfg, h->dec_base, &h->b);
+    if ((r = scratch_address(device, &h->noalloc_base))) return bail(r);
     if (h->mx) {
         if ((r = dmalloc(&h->d_special, 1))) return bail(r);
         h->grouped = T > 1;
@@ -630,6 +659,30 @@ int cpb_moe_forward_device(cpb_moe_t* h, int layer0, int n_layers, float* d_x, i
     }
     it->second.second = ++h->graph_clock;
     HIP_OK(hipGraphLaunch(it->second.first, h->stream));
+    return 0;
+}
+
+int cpb_moe_forward_device_noalloc(cpb_moe_t* h, int layer0, int n_layers, float* d_x, int n_tok, int apply_norm) {
+    if (!h || !d_x) return fail(CPB_EINVAL, "NULL argument");
+    const auto& c = h->cfg;
+    if (layer0 < 0 || n_layers < 0 || layer0 + n_layers > c.n_layer) return fail(CPB_EINVAL, "layer range out of bounds");
+    if (n_tok < 1 || n_tok > c.max_tokens) return fail(CPB_EINVAL, "n_tok=%d outside [1, max_tokens=%d]", n_tok, c.max_tokens);
+    const size_t need = carve_decode(c, nullptr, nullptr);
+    if (need > kScratchBytes)
+        return fail(CPB_EINVAL, "this shape needs %zu bytes of decode scratch; the static scratch holds %zu", need,
+                    kScratchBytes);
+    for (int l = layer0; l < layer0 + n_layers; l++)
+        if (!h->layers[l].loaded) return fail(CPB_ESTATE, "layer %d not loaded", l);
+    if (!h->noalloc_base) return fail(CPB_ESTATE, "static scratch address not set up");
+    HIP_OK(hipSetDevice(h->device));
+    // the decode kernels, one token at a time, launched directly (no graph:
+    // instantiating one allocates); every scratch element they read is
+    // written earlier in the same call, so nothing needs clearing first
+    DecodeBufs B;
+    carve_decode(c, h->noalloc_base, &B);
+    for (int l = layer0; l < layer0 + n_layers; l++)
+        for (int t = 0; t < n_tok; t++)
+            if (int r = layer_token(h, B, l, d_x + (size_t)t * c.d, apply_norm, false, false)) return r;
     return 0;
 }
 

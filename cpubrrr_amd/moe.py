@@ -181,6 +181,12 @@ class MoeBlock:
         L.check(self._lib.cpb_moe_forward_device(self._h, layer0, n_layers, C.c_void_p(x_ptr), n_tok,
                                                  int(bool(apply_norm))), "cpb_moe_forward_device")
 
+    def forward_device_noalloc(self, layer0: int, n_layers: int, x_ptr: int, n_tok: int = 1, apply_norm: bool = True):
+        """forward_device without any allocation: per-call scratch in the library's
+        static per-GPU array (calls overlapping on one GPU race)."""
+        L.check(self._lib.cpb_moe_forward_device_noalloc(self._h, layer0, n_layers, C.c_void_p(x_ptr), n_tok,
+                                                         int(bool(apply_norm))), "cpb_moe_forward_device_noalloc")
+
     def set_stream(self, stream_ptr: int | None) -> None:
         L.check(self._lib.cpb_moe_set_stream(self._h, C.c_void_p(stream_ptr or 0)), "cpb_moe_set_stream")
 

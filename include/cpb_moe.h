@@ -140,6 +140,18 @@ int cpb_moe_forward(cpb_moe_t* h, int layer, float* x, int n_tok, int apply_norm
 int cpb_moe_forward_device(cpb_moe_t* h, int layer0, int n_layers, float* d_x, int n_tok,
                            int apply_norm);
 
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): cpb_moe_forward_device with no allocation of any kind.
+ * The per-call scratch (activations, routing, h) lives in a static 256 KiB
+ * device array per GPU instead of the handle's buffers; shapes whose scratch
+ * exceeds it get CPB_EINVAL.  Kernels are launched directly on the handle's
+ * stream (no graph is captured; per-kernel timing is not recorded).  All
+ * calls on one GPU share that array: calls that overlap on one GPU (from any
+ * handle or thread) race.  Results equal cpb_moe_forward_device's bit for bit. */
+int cpb_moe_forward_device_noalloc(cpb_moe_t* h, int layer0, int n_layers, float* d_x, int n_tok,
+                                   int apply_norm);
+
 /* Use `stream` (a hipStream_t) for all further work of this handle; NULL
  * restores the handle's own stream.  Ordered: work issued on the new stream
  * waits for everything already queued on the old one. */

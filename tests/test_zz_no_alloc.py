@@ -1,0 +1,61 @@
+"""The no-allocation entry point (cpb_moe_forward_device_noalloc, static
+per-GPU scratch) against cpb_moe_forward_device, bit for bit, on two calls in
+a row (the second with a smaller input), for both weight families, and its
+size limit.  Runs last: it shares one device array across handles."""
+import numpy as np
+import pytest
+
+from cpubrrr_amd import MoeBlock, MoeConfig, synth
+from cpubrrr_amd import _lib as L
+
+pytestmark = pytest.mark.gpu
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+def _pair(blk, X, n_tok, nl, norm):
+    import torch
+    a = torch.from_numpy(np.ascontiguousarray(X[:n_tok])).to("cuda:0")
+    b = a.clone()
+    torch.cuda.synchronize()
+    blk.forward_device(0, nl, a.data_ptr(), n_tok, norm)
+    blk.sync()
+    blk.forward_device_noalloc(0, nl, b.data_ptr(), n_tok, norm)
+    blk.sync()
+    return a.cpu().numpy(), b.cpu().numpy()
+
+
+def test_noalloc_matches_forward_device_mx(gpu):
+    say("case noalloc gpt-oss: n_tok 4 then 2, 2 layers")
+    d, ne, k, nl = 960, 16, 4, 2
+    layers = [synth.gptoss_layer(d, d, ne, k, seed=31, layer=l, zipf=1.1) for l in range(nl)]
+    X = np.stack([synth.token(d, 31, i) for i in range(4)])
+    with MoeBlock(MoeConfig.gptoss(d=d, n_expert=ne, top_k=k, d_ff=d, n_layer=nl, max_tokens=4)) as blk:
+        for l in range(nl):
+            blk.load_layer(l, layers[l])
+        for n_tok in (4, 2):
+            want, got = _pair(blk, X, n_tok, nl, True)
+            assert np.array_equal(want.view(np.uint32), got.view(np.uint32)), n_tok
+
+
+def test_noalloc_matches_forward_device_qwen(gpu):
+    say("case noalloc qwen: n_tok 3 then 1")
+    d, dff, ne, k = 1024, 512, 32, 8
+    L0 = synth.qwen_layer(d, dff, ne, k, seed=32)
+    X = np.stack([synth.token(d, 32, i) for i in range(3)])
+    with MoeBlock(MoeConfig.qwen3(d=d, n_expert=ne, top_k=k, d_ff=dff, max_tokens=3)) as blk:
+        blk.load_layer(0, L0)
+        for n_tok in (3, 1):
+            want, got = _pair(blk, X, n_tok, 1, True)
+            assert np.array_equal(want.view(np.uint32), got.view(np.uint32)), n_tok
+
+
+def test_noalloc_rejects_shapes_beyond_scratch(gpu):
+    say("case noalloc size limit")
+    cfg = MoeConfig.qwen3(d=8192, n_expert=8, top_k=8, d_ff=4096)
+    with MoeBlock(cfg) as blk:
+        with pytest.raises(L.CpbError) as ei:
+            blk.forward_device_noalloc(0, 1, 0x1000, 1, True)
+        assert ei.value.code == L.CPB_EINVAL and "static scratch" in str(ei.value)
