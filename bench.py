@@ -29,9 +29,10 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 # HBM bytes per dispatch of the roofline kernel, from rocprofv3 FETCH_SIZE /
-# WRITE_SIZE runs scaled by a 1 GiB copy (profiles/hbm_traffic_config1_phased.md);
+# WRITE_SIZE runs scaled by a 1 GiB copy (profiles/hbm_traffic_config1_phased.md,
+# profiles/hbm_traffic_config3_qwen.md);
 # None where not yet measured.
-MEASURED_TRAFFIC = {"k_gateup_mx": 35_815_144, "k_gateup_kq": None}
+MEASURED_TRAFFIC = {"k_gateup_mx": 35_815_144, "k_gateup_kq": 14_404_042}
 
 METRIC = "expert-weight GB/s (% HBM peak) + MoE-layer tok/s, gpt-oss-20b shape, 1 GPU"
 HBM_PEAK_GBS = 8000.0
