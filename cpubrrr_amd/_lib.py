@@ -1,5 +1,5 @@
-"""ctypes binding of libcpb_moe.so (the C ABI in include/cpb_moe.h and
-include/cpb_synth.h).  Loading fails loudly when the library is missing: there
+"""ctypes binding of libcpb_moe.so (the C ABI in include/cpb_moe.h,
+include/cpb_gguf.h and include/cpb_synth.h).  Loading fails loudly when the library is missing: there
 is no CPU fallback for the HIP path."""
 from __future__ import annotations
 
@@ -36,6 +36,19 @@ class MoeTrace(C.Structure):
                 ("exact_router_fallbacks", C.c_int32)]
 
 
+class GgufTensor(C.Structure):
+    _fields_ = [("name", C.c_char_p), ("type", C.c_int32), ("n_dims", C.c_int32), ("dims", C.c_uint64 * 4),
+                ("n_elements", C.c_uint64), ("offset", C.c_uint64), ("n_bytes", C.c_uint64), ("data", C.c_void_p)]
+
+
+class GgufHparams(C.Structure):
+    _fields_ = [("arch", C.c_char * 32), ("n_embd", C.c_int64), ("n_layer", C.c_int64), ("n_head", C.c_int64),
+                ("n_head_kv", C.c_int64), ("head_dim", C.c_int64), ("n_expert", C.c_int64),
+                ("n_expert_used", C.c_int64), ("n_ff_exp", C.c_int64), ("sliding_window", C.c_int64),
+                ("n_vocab", C.c_int64), ("context_length", C.c_int64), ("rope_freq_base", C.c_double),
+                ("rms_eps", C.c_double)]
+
+
 # every symbol the public headers declare, with its ctypes signature
 SIGNATURES = {
     "cpb_moe_create": (C.c_int, [C.POINTER(MoeCfg), C.c_int, C.POINTER(C.c_void_p)]),
@@ -54,6 +67,19 @@ SIGNATURES = {
     "cpb_moe_timing": (C.c_int, [C.c_void_p, C.c_int]),
     "cpb_moe_kernel_times": (C.c_int, [C.c_void_p, C.POINTER(C.c_double), C.POINTER(C.c_long)]),
     "cpb_moe_grouped_sums": (C.c_int, [C.c_void_p, C.c_int, f32p, C.c_int, C.c_int, i32p, i32p]),
+    "cpb_moe_config": (C.c_int, [C.c_void_p, C.POINTER(MoeCfg)]),
+    "cpb_gguf_open": (C.c_int, [C.c_char_p, C.POINTER(C.c_void_p)]),
+    "cpb_gguf_close": (None, [C.c_void_p]),
+    "cpb_gguf_version": (C.c_int, [C.c_void_p, C.POINTER(C.c_uint32), C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
+    "cpb_gguf_n_tensors": (C.c_int, [C.c_void_p, C.POINTER(C.c_int64)]),
+    "cpb_gguf_tensor_at": (C.c_int, [C.c_void_p, C.c_int64, C.POINTER(GgufTensor)]),
+    "cpb_gguf_find": (C.c_int, [C.c_void_p, C.c_char_p, C.POINTER(GgufTensor)]),
+    "cpb_gguf_meta_i64": (C.c_int, [C.c_void_p, C.c_char_p, C.POINTER(C.c_int64)]),
+    "cpb_gguf_meta_f64": (C.c_int, [C.c_void_p, C.c_char_p, C.POINTER(C.c_double)]),
+    "cpb_gguf_meta_str": (C.c_int, [C.c_void_p, C.c_char_p, C.POINTER(C.c_char_p)]),
+    "cpb_gguf_hparams_get": (C.c_int, [C.c_void_p, C.POINTER(GgufHparams)]),
+    "cpb_gguf_write_manifest": (C.c_int, [C.c_void_p, C.c_char_p]),
+    "cpb_moe_load_gguf_layer": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int]),
     "cpb_synth_u64": (C.c_uint64, [C.c_uint64, C.c_uint64, C.c_uint64]),
     "cpb_synth_mxfp4": (None, [u8p, C.c_size_t, C.c_int, C.c_int, C.c_uint64, C.c_uint64]),
     "cpb_synth_normal": (None, [f32p, C.c_size_t, C.c_float, C.c_float, C.c_uint64, C.c_uint64]),

@@ -35,7 +35,7 @@ COMMON = [
 ]
 
 SOURCES = ["route.hip", "moe_mx.hip", "moe_kq.hip", "moe_grouped.hip", "api.hip"]
-HOST_SOURCES = ["synth.cpp"]
+HOST_SOURCES = ["synth.cpp", "gguf.cpp"]
 
 
 def _run(cmd: list[str]) -> None:
@@ -54,7 +54,7 @@ def build(verbose: bool = False) -> Path:
     for s in SOURCES:
         jobs.append([HIPCC, *COMMON, "-c", str(CSRC / s), "-o", str(BUILD / (s + ".o"))])
     for s in HOST_SOURCES:
-        jobs.append(["g++", "-O3", "-std=c++17", "-fPIC", f"-I{ROOT / 'include'}", "-c", str(CSRC / s),
+        jobs.append(["g++", "-O3", "-std=c++17", "-fPIC", "-Wall", f"-I{ROOT / 'include'}", f"-I{CSRC}", "-c", str(CSRC / s),
                      "-o", str(BUILD / (s + ".o"))])
     with cf.ThreadPoolExecutor(max_workers=min(8, os.cpu_count() or 4)) as ex:
         for f in [ex.submit(_run, j) for j in jobs]:

@@ -20,6 +20,7 @@
 #include <vector>
 
 #include "cpb_moe.h"
+#include "cpb_internal.h"
 #include "moe_kq.h"
 #include "moe_mx.h"
 #include "moe_grouped.h"
@@ -33,9 +34,10 @@ constexpr size_t kScratchBytes = 256 * 1024;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 namespace {
-
 thread_local std::string g_err;
+}  // namespace
 
+namespace cpb {
 int fail(int code, const char* fmt, ...) {
     char buf[512];
     va_list ap;
@@ -45,6 +47,10 @@ int fail(int code, const char* fmt, ...) {
     g_err = buf;
     return code;
 }
+}  // namespace cpb
+
+namespace {
+using cpb::fail;
 
 #define HIP_OK(expr)                                                                   \
     do {                                                                               \
@@ -760,6 +766,12 @@ int cpb_moe_forward(cpb_moe_t* h, int layer, float* x, int n_tok, int apply_norm
         if (r) return r;
     }
     HIP_OK(hipStreamSynchronize(h->stream));
+    return 0;
+}
+
+int cpb_moe_config(const cpb_moe_t* h, cpb_moe_cfg* out) {
+    if (!h || !out) return fail(CPB_EINVAL, "NULL argument");
+    *out = h->cfg;
     return 0;
 }
 

@@ -184,6 +184,12 @@ __global__ __launch_bounds__(128 * kMaxParts) void k_down_mx(DownArgs a) {
     float* red = (float*)smem;                                 // [W][64]
     float* vv = red + W * 64;                                  // [64]
     const int blk0 = q * kBlkPerPart;
+    // the routed experts (written by the gate/up launch) first: the weight
+    // addresses wait on them; scalar loads, which the activation requests
+    // below need not wait for
+    int es[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) es[k] = __builtin_amdgcn_readfirstlane(a.ids[k < K ? k : 0]);
     // activations: for each window and 16-lane group (whose rows all belong
     // to expert slot 16g / RT) this lane's A fragment; the slot's scales
     const __amdgpu_buffer_rsrc_t ri = buf_rsrc(a.himg, (uint32_t)(K * a.nbf * kImgBytes));
@@ -205,14 +211,14 @@ __global__ __launch_bounds__(128 * kMaxParts) void k_down_mx(DownArgs a) {
                 __builtin_amdgcn_raw_buffer_load_b32(rs, ok ? (uint32_t)(ei * a.nbf + blk0 + u) * 4 : kOffNone, 0, 0));
         }
     }
-    // the routed experts (written by the gate/up launch; scalar loads, which
-    // the activation requests above need not wait for)
-    int es[4];
-#pragma unroll
-    for (int k = 0; k < 4; k++) es[k] = __builtin_amdgcn_readfirstlane(a.ids[k < K ? k : 0]);
     const int e = ei == 0 ? es[0] : ei == 1 ? es[1] : ei == 2 ? es[2] : es[3];
+#ifdef CPB_DECODE_STAMPS
+    asm volatile("" ::"v"(e));
+#endif
+    RSTAMP(4);
     u32x4 wv[1 + kSubUnits];
     load_sub(a.w + (((((size_t)e * tiles + t) * P + q) * kUnits) * RT) + rr, RT, ub, wv);
+    RSTAMP(5);
     float dnb_pf = 0.0f, x_pf = 0.0f, w_pf[4];
     if (w == 0) {
         if (a.down_b) dnb_pf = a.down_b[(size_t)e * a.d + row];

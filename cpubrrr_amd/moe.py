@@ -124,6 +124,12 @@ class MoeBlock:
         L.check(rc, "cpb_moe_load_layer_typed")
         self._down_type[layer] = dt
 
+    def load_gguf_layer(self, gguf, layer: int) -> None:
+        """Layer `layer` straight from a mapped GGUF file (cpubrrr_amd.gguf.GgufFile):
+        tensors by the reference's names, types and shapes checked."""
+        L.check(self._lib.cpb_moe_load_gguf_layer(self._h, gguf.handle, layer), "cpb_moe_load_gguf_layer")
+        self._down_type[layer] = gguf.tensor(f"blk.{layer}.ffn_down_exps.weight")["type"]
+
     def forward(self, layer: int, x: np.ndarray, apply_norm: bool = True, trace: bool = False):
         """x: [d] or [n_tok, d] fp32, updated like the reference's residual.
         Returns (x_out, trace_dict or None)."""

@@ -160,6 +160,9 @@ int cpb_moe_sync(cpb_moe_t* h);
 void cpb_moe_destroy(cpb_moe_t* h);
 const char* cpb_moe_last_error(void);
 
+/* The configuration the handle was created with. */
+int cpb_moe_config(const cpb_moe_t* h, cpb_moe_cfg* out);
+
 /* Device bytes held for one layer's re-laid-out expert weights (for sizing). */
 int cpb_moe_layer_bytes(const cpb_moe_cfg* cfg, size_t* out);
 
