@@ -194,9 +194,7 @@ int check_cfg(const cpb_moe_cfg* c) {
     if (mx) {
         if (c->wtype_down != CPB_GGUF_MXFP4) return fail(CPB_EINVAL, "MXFP4 gate/up requires MXFP4 down");
         if (c->d % 32 || c->d_ff % 32) return fail(CPB_EINVAL, "d and d_ff must be multiples of 32");
-        if (c->top_k != 1 && c->top_k != 2 && c->top_k != 4)
-            return fail(CPB_EINVAL, "MXFP4 path supports top_k in {1,2,4}, got %d", c->top_k);
-        if (c->d % (64 / c->top_k)) return fail(CPB_EINVAL, "d must be a multiple of 64/top_k");
+        if (c->d % cpb::mx_down_rt(c->top_k)) return fail(CPB_EINVAL, "d must be a multiple of %d", cpb::mx_down_rt(c->top_k));
         if ((c->d / 32 + 14) / 15 > cpb::kMaxParts || (c->d_ff / 32 + 14) / 15 > cpb::kMaxParts)
             return fail(CPB_EINVAL, "d, d_ff must be <= 3840");
     } else if (c->wtype_gate_up == CPB_GGUF_Q4_K) {

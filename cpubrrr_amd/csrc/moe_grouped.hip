@@ -35,6 +35,7 @@
 // both paths share one copy in HBM.
 #include "moe_common.h"
 #include "moe_grouped.h"
+#include "moe_mx.h"
 #include "mx_dev.h"
 #include "route_dev.h"
 #include "select.h"
@@ -461,7 +462,7 @@ __global__ __launch_bounds__(512) void k_down_grouped(GroupedArgs a) {
     const int4 tl = a.tiles[tile];
     const int e = uniform(tl.x), start = uniform(tl.y), cnt = uniform(tl.z);
     const int lane = threadIdx.x & 63, w = uniform((int)(threadIdx.x >> 6));
-    const int RTv = 64 / a.k, Tv = a.d / RTv, P = a.parts_dn, nbf = a.nbf;
+    const int RTv = mx_down_rt(a.k), Tv = a.d / RTv, P = a.parts_dn, nbf = a.nbf;
     const int rt = grp * 8 + w;
     const bool live = rt < a.d / 32;
     if (threadIdx.x < 32) src[threadIdx.x] = (int)threadIdx.x < cnt ? a.sorted[start + threadIdx.x] : -1;
@@ -507,16 +508,16 @@ __global__ __launch_bounds__(256) void k_combine_batch(GroupedArgs a) {
     float4* __restrict__ x = (float4*)a.x;
     for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n4; i += (size_t)gridDim.x * blockDim.x) {
         const size_t t = i / d4, r4 = i % d4;
-        float4 v[4];
-        float wk[4];
+        float4 v[8];
+        float wk[8];
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
+        for (int k = 0; k < 8; k++) {
             v[k] = k < K ? dn[(t * K + k) * d4 + r4] : float4{0, 0, 0, 0};
             wk[k] = k < K ? a.wts[t * K + k] : 0.0f;
         }
         float4 s = x[i];                                     // engine_gpt2.rs:911-921
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
+        for (int k = 0; k < 8; k++) {
             if (k < K) {
                 s.x += wk[k] * v[k].x;
                 s.y += wk[k] * v[k].y;

@@ -41,6 +41,11 @@ struct DownArgs {
     int32_t* dn_sums;        // trace [top_k][d][nbf]
 };
 
+// Rows per down row tile of the stream layout: 64 / top_k lanes of one
+// expert slot per 16-lane group for top_k in {1, 2, 4}; otherwise 16 rows,
+// with the slots run four at a time (a 5th..8th slot in a second pass).
+CPB_DEV_HOST_INLINE int mx_down_rt(int top_k) { return (top_k == 1 || top_k == 2) ? 64 / top_k : 16; }
+
 size_t mx_gateup_bytes(int ne, int dff, int nb);
 size_t mx_down_bytes(int ne, int d, int nbf, int top_k);
 int launch_count_special_exps(const uint8_t* raw, size_t nblocks, unsigned* out, hipStream_t s);

@@ -173,84 +173,99 @@ __global__ __launch_bounds__(128 * kMaxParts) __attribute__((amdgpu_waves_per_eu
 template <bool TRACE>
 __global__ __launch_bounds__(128 * kMaxParts) void k_down_mx(DownArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
-    const int P = a.nparts, W = 2 * P, K = a.top_k, RT = 64 / K;
+    const int P = a.nparts, W = 2 * P, K = a.top_k, RT = mx_down_rt(K);
+    // slots per pass (lane groups of RT rows) and passes: one pass of K
+    // slots for K in {1, 2, 4}; passes of four 16-row slots otherwise
+    const int SP = 64 / RT, NP = (K + SP - 1) / SP;
     const int lane = threadIdx.x & 63;
     const int w = uniform(threadIdx.x >> 6), q = w >> 1, hh = w & 1;
     const int ub = kSubUnits * hh;
     const int tiles = a.d / RT, t = blockIdx.x;
-    const int ei = lane / RT, rr = lane % RT, row = t * RT + rr;
+    const int gi = lane / RT, rr = lane % RT, row = t * RT + rr;
     RSTAMP_DECL;
     RSTAMP(0);
-    float* red = (float*)smem;                                 // [W][64]
-    float* vv = red + W * 64;                                  // [64]
+    float* red = (float*)smem;                                 // [NP][W][64]
+    float* vv = red + NP * W * 64;                             // [NP][64]
     const int blk0 = q * kBlkPerPart;
     // the routed experts (written by the gate/up launch) first: the weight
     // addresses wait on them; scalar loads, which the activation requests
     // below need not wait for
-    int es[4];
+    int es[8];
 #pragma unroll
-    for (int k = 0; k < 4; k++) es[k] = __builtin_amdgcn_readfirstlane(a.ids[k < K ? k : 0]);
-    // activations: for each window and 16-lane group (whose rows all belong
-    // to expert slot 16g / RT) this lane's A fragment; the slot's scales
+    for (int k = 0; k < 8; k++) es[k] = __builtin_amdgcn_readfirstlane(a.ids[k < K ? k : 0]);
+    float w_pf[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) w_pf[k] = a.wts[k < K ? k : 0];
+    float x_pf = 0.0f;
+    if (w == 0 && lane < RT) x_pf = a.x[row];
     const __amdgpu_buffer_rsrc_t ri = buf_rsrc(a.himg, (uint32_t)(K * a.nbf * kImgBytes));
-    u32x4 xa[2][4];
+    const __amdgpu_buffer_rsrc_t rs = buf_rsrc(a.hsb, (uint32_t)(K * a.nbf * 4));
+    float dnb_pf[2] = {0.0f, 0.0f};
+    for (int pass = 0; pass < NP; pass++) {
+        // slot of lane group g in this pass; a slot beyond K reads zero
+        // activations (its rows' results are dropped)
+        const int s0 = pass * SP, slot = s0 + gi;
+        // activations: for each window and 16-lane group (whose rows all
+        // belong to one slot) this lane's A fragment; the slot's scales
+        u32x4 xa[2][4];
 #pragma unroll
-    for (int h = 0; h < 2; h++)
+        for (int h = 0; h < 2; h++)
 #pragma unroll
-        for (int g = 0; g < 4; g++)
-            xa[h][g] = load_act_frag(ri, (uint32_t)(((16 * g) / RT) * a.nbf * kImgBytes), blk0 + ub + 4 * h, ub + 4 * h,
-                                     a.nbf);
-    float xsc[kSubUnits];
-    {
-        const __amdgpu_buffer_rsrc_t rs = buf_rsrc(a.hsb, (uint32_t)(K * a.nbf * 4));
+            for (int g = 0; g < 4; g++) {
+                const int sg = s0 + (16 * g) / RT;
+                xa[h][g] = sg < K ? load_act_frag(ri, (uint32_t)(sg * a.nbf * kImgBytes), blk0 + ub + 4 * h, ub + 4 * h,
+                                                  a.nbf)
+                                  : u32x4{0, 0, 0, 0};
+            }
+        float xsc[kSubUnits];
 #pragma unroll
         for (int i = 0; i < kSubUnits; i++) {
             const int u = ub + i;
-            const bool ok = u < kBlkPerPart && blk0 + u < a.nbf;
+            const bool ok = slot < K && u < kBlkPerPart && blk0 + u < a.nbf;
             xsc[i] = __uint_as_float(
-                __builtin_amdgcn_raw_buffer_load_b32(rs, ok ? (uint32_t)(ei * a.nbf + blk0 + u) * 4 : kOffNone, 0, 0));
+                __builtin_amdgcn_raw_buffer_load_b32(rs, ok ? (uint32_t)(slot * a.nbf + blk0 + u) * 4 : kOffNone, 0, 0));
         }
-    }
-    const int e = ei == 0 ? es[0] : ei == 1 ? es[1] : ei == 2 ? es[2] : es[3];
-#ifdef CPB_DECODE_STAMPS
-    asm volatile("" ::"v"(e));
-#endif
-    RSTAMP(4);
-    u32x4 wv[1 + kSubUnits];
-    load_sub(a.w + (((((size_t)e * tiles + t) * P + q) * kUnits) * RT) + rr, RT, ub, wv);
-    RSTAMP(5);
-    float dnb_pf = 0.0f, x_pf = 0.0f, w_pf[4];
-    if (w == 0) {
-        if (a.down_b) dnb_pf = a.down_b[(size_t)e * a.d + row];
-        if (lane < RT) x_pf = a.x[row];
-    }
+        int e = es[0];
 #pragma unroll
-    for (int k = 0; k < 4; k++) w_pf[k] = a.wts[k < K ? k : 0];
-    int32_t* so = nullptr;
-    if (TRACE) so = a.dn_sums + (((size_t)ei * a.d + row) * a.nbf + blk0);
-    const float acc = part_dot_sub_mfma4<TRACE>(wv, ub, xa, xsc, so, blk0, a.nbf);
+        for (int k = 1; k < 8; k++)
+            if (slot == k) e = es[k];
+#ifdef CPB_DECODE_STAMPS
+        asm volatile("" ::"v"(e));
+#endif
+        if (pass == 0) RSTAMP(4);
+        u32x4 wv[1 + kSubUnits];
+        load_sub(a.w + (((((size_t)e * tiles + t) * P + q) * kUnits) * RT) + rr, RT, ub, wv);
+        if (pass == 0) RSTAMP(5);
+        if (w == 0 && a.down_b && slot < K) dnb_pf[pass] = a.down_b[(size_t)e * a.d + row];
+        int32_t* so = nullptr;
+        if (TRACE && slot < K) so = a.dn_sums + (((size_t)slot * a.d + row) * a.nbf + blk0);
+        const float acc = part_dot_sub_mfma4<TRACE>(wv, ub, xa, xsc, so, blk0, a.nbf);
+        red[(pass * W + w) * 64 + lane] = acc;
+    }
     RSTAMP(1);
-    red[w * 64 + lane] = acc;
     __syncthreads();
     if (w != 0) return;
     RSTAMP(2);
-    float pr[2 * kMaxParts];
+    for (int pass = 0; pass < NP; pass++) {
+        float pr[2 * kMaxParts];
 #pragma unroll
-    for (int p = 0; p < 2 * kMaxParts; p++) pr[p] = p < W ? red[p * 64 + lane] : 0.0f;
-    float v = 0.0f;
+        for (int p = 0; p < 2 * kMaxParts; p++) pr[p] = p < W ? red[(pass * W + p) * 64 + lane] : 0.0f;
+        float v = 0.0f;
 #pragma unroll
-    for (int p = 0; p < 2 * kMaxParts; p++)
-        if (p < W) v += pr[p];
-    if (a.down_b) v += dnb_pf;
-    if (TRACE) a.dn[(size_t)ei * a.d + row] = v;
-    vv[lane] = v;
+        for (int p = 0; p < 2 * kMaxParts; p++)
+            if (p < W) v += pr[p];
+        const int slot = pass * SP + gi;
+        if (a.down_b) v += dnb_pf[pass];
+        if (TRACE && slot < K) a.dn[(size_t)slot * a.d + row] = v;
+        vv[pass * 64 + lane] = v;
+    }
     wave_sync_lds();
     if (lane < RT) {
         // engine_gpt2.rs:911-921: s = x[r]; s += wts[ei] * (dot + b), ei ascending
         float s = x_pf;
 #pragma unroll
-        for (int k = 0; k < 4; k++)
-            if (k < K) s += w_pf[k] * vv[k * RT + lane];
+        for (int k = 0; k < 8; k++)
+            if (k < K) s += w_pf[k] * vv[(k / SP) * 64 + (k % SP) * RT + lane];
         a.x[row] = s;
     }
     RSTAMP(3);
@@ -329,7 +344,7 @@ size_t mx_gateup_bytes(int ne, int dff, int nb) {
 }
 size_t mx_down_bytes(int ne, int d, int nbf, int top_k) {
     int P = (nbf + kBlkPerPart - 1) / kBlkPerPart;
-    int RT = 64 / top_k;
+    int RT = mx_down_rt(top_k);
     return (size_t)ne * (d / RT) * P * kUnits * RT * 16;
 }
 
@@ -355,7 +370,7 @@ int launch_repack_gateup(const uint8_t* gate, const uint8_t* up, u32x4* out, int
 }
 int launch_repack_down(const uint8_t* down, u32x4* out, int ne, int d, int nbf, int top_k, hipStream_t s) {
     int P = (nbf + kBlkPerPart - 1) / kBlkPerPart;
-    hipLaunchKernelGGL(k_repack_down, dim3(4096), dim3(256), 0, s, down, out, ne, d, nbf, P, 64 / top_k);
+    hipLaunchKernelGGL(k_repack_down, dim3(4096), dim3(256), 0, s, down, out, ne, d, nbf, P, mx_down_rt(top_k));
     return hipGetLastError() == hipSuccess ? 0 : -19;
 }
 
@@ -371,10 +386,11 @@ int launch_gateup_mx(const GateUpArgs& a, bool trace, hipStream_t s) {
 }
 
 int launch_down_mx(const DownArgs& a, bool trace, hipStream_t s) {
-    const int P = a.nparts, K = a.top_k;
-    if (P < 1 || P > kMaxParts || (K != 1 && K != 2 && K != 4) || a.d % (64 / K) != 0) return -22;
-    const size_t lds = sizeof(float) * (2 * P * 64 + 64);
-    dim3 grid(a.d / (64 / K)), block(128 * P);
+    const int P = a.nparts, K = a.top_k, RT = mx_down_rt(K);
+    if (P < 1 || P > kMaxParts || K < 1 || K > 8 || a.d % RT != 0) return -22;
+    const int NP = (K + 64 / RT - 1) / (64 / RT);
+    const size_t lds = sizeof(float) * (NP * 2 * P * 64 + NP * 64);
+    dim3 grid(a.d / RT), block(128 * P);
     if (trace) launch(k_down_mx<true>, grid, block, lds, s, a);
     else launch(k_down_mx<false>, grid, block, lds, s, a);
     return hipGetLastError() == hipSuccess ? 0 : -19;

@@ -37,7 +37,7 @@ def _create(cfg):
 
 
 @pytest.mark.parametrize("mut", [
-    dict(top_k=0), dict(top_k=9), dict(top_k=3), dict(d=2880 + 16), dict(n_expert=1000),
+    dict(top_k=0), dict(top_k=9), dict(top_k=3, n_expert=2), dict(d=2880 + 16), dict(n_expert=1000),
     dict(act=L.ACT_SILU), dict(wtype_down=L.GGUF_Q6_K), dict(max_tokens=0), dict(router=7),
 ])
 def test_bad_configs_rejected(mut):

@@ -31,6 +31,8 @@ def per_token(blk, X, apply_norm):
     (960, 480, 16, 2, 70, 1, False, None),
     (512, 1024, 4, 1, 33, 2, True, None),
     (2880, 2880, 32, 4, 64, 3, True, 1.1),
+    (960, 960, 32, 8, 45, 4, True, 1.1),
+    (480, 480, 8, 3, 29, 5, False, None),
 ])
 def test_grouped_equals_per_token(gpu, d, dff, ne, k, n_tok, seed, norm, zipf):
     say(f"case grouped d={d} dff={dff} ne={ne} k={k} n_tok={n_tok} seed={seed} norm={norm} zipf={zipf}")

@@ -202,3 +202,12 @@ def test_caller_graph_capture_and_stream_switch(gpu):
             assert torch.equal(xg.view(torch.int32), want.view(torch.int32)), rep
         assert torch.equal(want.view(torch.int32), ref.view(torch.int32))
         blk.set_stream(None)
+
+
+def test_other_top_k(gpu):
+    # top_k outside {1, 2, 4} (the reference takes any topk <= 8,
+    # engine_gpt2.rs:853-866): 16-row down tiles, slots four at a time
+    run_case(960, 480, 16, 3, seed=22, apply_norm=True)
+    run_case(960, 960, 32, 8, seed=23, apply_norm=True, zipf=1.1)
+    run_case(512, 1024, 8, 6, seed=24)
+    run_case(2880, 2880, 32, 8, seed=25, apply_norm=True, zipf=1.1)
