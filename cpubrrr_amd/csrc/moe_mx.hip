@@ -170,8 +170,99 @@ __global__ __launch_bounds__(128 * kMaxParts) __attribute__((amdgpu_waves_per_eu
     RSTAMP_FLUSH_TO(a.stamps ? a.stamps + 1024 + (size_t)blockIdx.x * 8 : nullptr);
 }
 
+// top_k in {1, 2, 4}: one tile of 64 / top_k rows x top_k slots.
 template <bool TRACE>
 __global__ __launch_bounds__(128 * kMaxParts) void k_down_mx(DownArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int P = a.nparts, W = 2 * P, K = a.top_k, RT = 64 / K;
+    const int lane = threadIdx.x & 63;
+    const int w = uniform(threadIdx.x >> 6), q = w >> 1, hh = w & 1;
+    const int ub = kSubUnits * hh;
+    const int tiles = a.d / RT, t = blockIdx.x;
+    const int ei = lane / RT, rr = lane % RT, row = t * RT + rr;
+    RSTAMP_DECL;
+    RSTAMP(0);
+    float* red = (float*)smem;                                 // [W][64]
+    float* vv = red + W * 64;                                  // [64]
+    const int blk0 = q * kBlkPerPart;
+    // the routed experts (written by the gate/up launch) first: the weight
+    // addresses wait on them; scalar loads, which the activation requests
+    // below need not wait for
+    int es[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) es[k] = __builtin_amdgcn_readfirstlane(a.ids[k < K ? k : 0]);
+    // activations: for each window and 16-lane group (whose rows all belong
+    // to expert slot 16g / RT) this lane's A fragment; the slot's scales
+    const __amdgpu_buffer_rsrc_t ri = buf_rsrc(a.himg, (uint32_t)(K * a.nbf * kImgBytes));
+    u32x4 xa[2][4];
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+            xa[h][g] = load_act_frag(ri, (uint32_t)(((16 * g) / RT) * a.nbf * kImgBytes), blk0 + ub + 4 * h, ub + 4 * h,
+                                     a.nbf);
+    float xsc[kSubUnits];
+    {
+        const __amdgpu_buffer_rsrc_t rs = buf_rsrc(a.hsb, (uint32_t)(K * a.nbf * 4));
+#pragma unroll
+        for (int i = 0; i < kSubUnits; i++) {
+            const int u = ub + i;
+            const bool ok = u < kBlkPerPart && blk0 + u < a.nbf;
+            xsc[i] = __uint_as_float(
+                __builtin_amdgcn_raw_buffer_load_b32(rs, ok ? (uint32_t)(ei * a.nbf + blk0 + u) * 4 : kOffNone, 0, 0));
+        }
+    }
+    const int e = ei == 0 ? es[0] : ei == 1 ? es[1] : ei == 2 ? es[2] : es[3];
+#ifdef CPB_DECODE_STAMPS
+    asm volatile("" ::"v"(e));
+#endif
+    RSTAMP(4);
+    u32x4 wv[1 + kSubUnits];
+    load_sub(a.w + (((((size_t)e * tiles + t) * P + q) * kUnits) * RT) + rr, RT, ub, wv);
+    RSTAMP(5);
+    float dnb_pf = 0.0f, x_pf = 0.0f, w_pf[4];
+    if (w == 0) {
+        if (a.down_b) dnb_pf = a.down_b[(size_t)e * a.d + row];
+        if (lane < RT) x_pf = a.x[row];
+    }
+#pragma unroll
+    for (int k = 0; k < 4; k++) w_pf[k] = a.wts[k < K ? k : 0];
+    int32_t* so = nullptr;
+    if (TRACE) so = a.dn_sums + (((size_t)ei * a.d + row) * a.nbf + blk0);
+    const float acc = part_dot_sub_mfma4<TRACE>(wv, ub, xa, xsc, so, blk0, a.nbf);
+    RSTAMP(1);
+    red[w * 64 + lane] = acc;
+    __syncthreads();
+    if (w != 0) return;
+    RSTAMP(2);
+    float pr[2 * kMaxParts];
+#pragma unroll
+    for (int p = 0; p < 2 * kMaxParts; p++) pr[p] = p < W ? red[p * 64 + lane] : 0.0f;
+    float v = 0.0f;
+#pragma unroll
+    for (int p = 0; p < 2 * kMaxParts; p++)
+        if (p < W) v += pr[p];
+    if (a.down_b) v += dnb_pf;
+    if (TRACE) a.dn[(size_t)ei * a.d + row] = v;
+    vv[lane] = v;
+    wave_sync_lds();
+    if (lane < RT) {
+        // engine_gpt2.rs:911-921: s = x[r]; s += wts[ei] * (dot + b), ei ascending
+        float s = x_pf;
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+            if (k < K) s += w_pf[k] * vv[k * RT + lane];
+        a.x[row] = s;
+    }
+    RSTAMP(3);
+    RSTAMP_FLUSH_TO(a.stamps ? a.stamps + 8192 + (size_t)blockIdx.x * 8 : nullptr);
+}
+
+// Any top_k <= 8: 16-row tiles, expert slots four at a time (one pass for
+// top_k <= 4, two above), each pass a full sub-part stream and block sums as
+// in k_down_mx; the combine runs over all slots in ascending order.
+template <bool TRACE>
+__global__ __launch_bounds__(128 * kMaxParts) void k_down_mx_slots(DownArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     const int P = a.nparts, W = 2 * P, K = a.top_k, RT = mx_down_rt(K);
     // slots per pass (lane groups of RT rows) and passes: one pass of K
@@ -391,8 +482,13 @@ int launch_down_mx(const DownArgs& a, bool trace, hipStream_t s) {
     const int NP = (K + 64 / RT - 1) / (64 / RT);
     const size_t lds = sizeof(float) * (NP * 2 * P * 64 + NP * 64);
     dim3 grid(a.d / RT), block(128 * P);
-    if (trace) launch(k_down_mx<true>, grid, block, lds, s, a);
-    else launch(k_down_mx<false>, grid, block, lds, s, a);
+    if (K == 1 || K == 2 || K == 4) {
+        if (trace) launch(k_down_mx<true>, grid, block, lds, s, a);
+        else launch(k_down_mx<false>, grid, block, lds, s, a);
+    } else {
+        if (trace) launch(k_down_mx_slots<true>, grid, block, lds, s, a);
+        else launch(k_down_mx_slots<false>, grid, block, lds, s, a);
+    }
     return hipGetLastError() == hipSuccess ? 0 : -19;
 }
 
