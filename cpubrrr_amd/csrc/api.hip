@@ -156,6 +156,8 @@ struct cpb_moe {
     uint8_t *g_ximg = nullptr, *g_himg = nullptr;
     double *g_lstar = nullptr, *g_lbound = nullptr;
     int32_t *g_ids = nullptr, *g_fallback = nullptr, *g_sorted = nullptr, *g_ntiles = nullptr;
+    int32_t *g_xsum = nullptr, *g_hsum = nullptr;   // k-quant grouped path
+    float* g_hbuf = nullptr;
     int4* g_tiles = nullptr;
     unsigned* d_special = nullptr;
     // captured HIP graphs of forward_device calls, keyed by their arguments,
@@ -473,20 +475,22 @@ int cpb_moe_create(const cpb_moe_cfg* cfg, int device, cpb_moe_t** out) {
         return bail(r);
     carve_decode(*cfg, h->dec_base, &h->b);
     if ((r = scratch_address(device, &h->noalloc_base))) return bail(r);
-    if (h->mx) {
-        if ((r = dmalloc(&h->d_special, 1))) return bail(r);
-        h->grouped = T > 1;
-        if (const char* v = getenv("CPB_GROUPED")) h->grouped = h->grouped && v[0] != '0';
-    }
-    if (h->mx && T > 1) {
+    if (h->mx && (r = dmalloc(&h->d_special, 1))) return bail(r);
+    h->grouped = T > 1;
+    if (const char* v = getenv("CPB_GROUPED")) h->grouped = h->grouped && v[0] != '0';
+    if (T > 1) {
+        // grouped (batched) path: per-token and per-pair buffers; MXFP4 uses
+        // the fp8 images, the k-quant path the per-32 sums and fp32 h
         const size_t nb = d / 32, nbf = ff / 32, np = T * k;
         if ((r = dmalloc(&h->g_xn, T * d)) || (r = dmalloc(&h->g_inv, T)) || (r = dmalloc(&h->g_xq, T * d)) || (r = dmalloc(&h->g_xsb, T * nb)) ||
-            (r = dmalloc(&h->g_ximg, T * nb * 64)) || (r = dmalloc(&h->g_lstar, T * ne)) ||
+            (r = dmalloc(&h->g_lstar, T * ne)) ||
             (r = dmalloc(&h->g_lbound, T * ne)) || (r = dmalloc(&h->g_logits, T * ne)) || (r = dmalloc(&h->g_ids, np)) ||
             (r = dmalloc(&h->g_wts, np)) || (r = dmalloc(&h->g_fallback, T)) || (r = dmalloc(&h->g_sorted, np)) ||
             (r = dmalloc(&h->g_tiles, np / 32 + ne + 1)) || (r = dmalloc(&h->g_ntiles, 1)) ||
-            (r = dmalloc(&h->g_hq, np * ff)) || (r = dmalloc(&h->g_hsb, np * nbf)) || (r = dmalloc(&h->g_himg, np * nbf * 64)) ||
-            (r = dmalloc(&h->g_dnout, np * d)))
+            (r = dmalloc(&h->g_hq, np * ff)) || (r = dmalloc(&h->g_hsb, np * nbf)) || (r = dmalloc(&h->g_dnout, np * d)))
+            return bail(r);
+        if (h->mx && ((r = dmalloc(&h->g_ximg, T * nb * 64)) || (r = dmalloc(&h->g_himg, np * nbf * 64)))) return bail(r);
+        if (!h->mx && ((r = dmalloc(&h->g_xsum, T * nb)) || (r = dmalloc(&h->g_hsum, np * nbf)) || (r = dmalloc(&h->g_hbuf, np * ff))))
             return bail(r);
     }
 #ifdef CPB_DECODE_STAMPS
@@ -610,6 +614,8 @@ static int layer_grouped(cpb_moe_t* h, int layer, float* d_x, int n_tok, int app
     g.lstar = h->g_lstar; g.lbound = h->g_lbound; g.logits = h->g_logits; g.ids = h->g_ids; g.wts = h->g_wts;
     g.fallback = h->g_fallback; g.sorted = h->g_sorted; g.tiles = h->g_tiles; g.ntiles = h->g_ntiles;
     g.hq = h->g_hq; g.hsb = h->g_hsb; g.himg = h->g_himg; g.dnout = h->g_dnout;
+    g.kq = h->mx ? 0 : 1; g.down_type = L.down_type;
+    g.xsum = h->g_xsum; g.hbuf = h->g_hbuf; g.hsum = h->g_hsum;
     g.gu_sums = gu_sums; g.dn_sums = dn_sums;
     if (cpb::launch_grouped_layer(g, gu_sums != nullptr, h->stream)) return fail(CPB_ENODEV, "grouped layer launch failed");
     return 0;
@@ -618,7 +624,7 @@ static int layer_grouped(cpb_moe_t* h, int layer, float* d_x, int n_tok, int app
 static int launch_direct(cpb_moe_t* h, int layer0, int n_layers, float* d_x, int n_tok, int apply_norm) {
     const auto& c = h->cfg;
     for (int l = layer0; l < layer0 + n_layers; l++) {
-        if (h->mx && n_tok > 1 && h->grouped && h->layers[l].mfma_exact) {
+        if (n_tok > 1 && h->grouped && (h->mx ? h->layers[l].mfma_exact : c.d <= 4096)) {
             if (int r = layer_grouped(h, l, d_x, n_tok, apply_norm, nullptr, nullptr)) return r;
             continue;
         }
@@ -694,13 +700,16 @@ int cpb_moe_grouped_sums(cpb_moe_t* h, int layer, float* x, int n_tok, int apply
                          int32_t* dn_sums) {
     if (!h || !x || !gu_sums || !dn_sums) return fail(CPB_EINVAL, "NULL argument");
     const auto& c = h->cfg;
-    if (!h->mx || !h->grouped) return fail(CPB_EINVAL, "grouped path needs MXFP4 weights and max_tokens > 1");
+    if (!h->grouped) return fail(CPB_EINVAL, "grouped path needs max_tokens > 1");
     if (layer < 0 || layer >= c.n_layer || !h->layers[layer].loaded) return fail(CPB_ESTATE, "layer %d not loaded", layer);
-    if (!h->layers[layer].mfma_exact) return fail(CPB_EINVAL, "layer %d has e8m0 scales outside [32, 254]", layer);
+    if (h->mx && !h->layers[layer].mfma_exact) return fail(CPB_EINVAL, "layer %d has e8m0 scales outside [32, 254]", layer);
+    if (!h->mx && c.d > 4096) return fail(CPB_EINVAL, "k-quant grouped path takes d <= 4096");
     if (n_tok < 2 || n_tok > c.max_tokens) return fail(CPB_EINVAL, "n_tok=%d outside [2, max_tokens=%d]", n_tok, c.max_tokens);
     HIP_OK(hipSetDevice(h->device));
     const size_t d = c.d, np = (size_t)n_tok * c.top_k;
-    const size_t ngu = np * 2 * c.d_ff * h->nb, ndn = np * d * h->nbf;
+    const size_t ngu = h->mx ? np * 2 * c.d_ff * h->nb : np * 2 * c.d_ff * (d / 256) * 2;
+    const size_t ndn = h->mx ? np * d * h->nbf
+                             : np * d * (c.d_ff / 256) * (h->layers[layer].down_type == CPB_GGUF_Q4_K ? 2 : 1);
     int32_t *dgu = nullptr, *ddn = nullptr;
     int r;
     if ((r = dmalloc(&dgu, ngu)) || (r = dmalloc(&ddn, ndn))) { hipFree(dgu); return r; }
@@ -846,7 +855,8 @@ void cpb_moe_destroy(cpb_moe_t* h) {
         hipFree(h->d_stamps);
     }
 #endif
-    void* gbufs[] = {h->g_inv, h->g_xn, h->g_xsb, h->g_logits, h->g_wts, h->g_hsb, h->g_dnout, h->g_xq, h->g_hq, h->g_ximg,
+    void* gbufs[] = {h->g_xsum, h->g_hsum, h->g_hbuf,
+                     h->g_inv, h->g_xn, h->g_xsb, h->g_logits, h->g_wts, h->g_hsb, h->g_dnout, h->g_xq, h->g_hq, h->g_ximg,
                      h->g_himg, h->g_lstar, h->g_lbound, h->g_ids, h->g_fallback, h->g_sorted, h->g_ntiles, h->g_tiles,
                      h->d_special};
     for (void* p : gbufs) hipFree(p);

@@ -43,13 +43,41 @@ struct GroupedArgs {
     float* hsb;                // [n_tok*k][nbf]
     uint8_t* himg;             // [n_tok*k][nbf][64]
     float* dnout;              // [n_tok*k][d] down rows + bias
+    // k-quant (Qwen3) layers: Q8_K activations and h, weights of down_type
+    int kq;                    // 1: Q4_K gate/up, Q4_K / Q6_K down (int8 matrix cores)
+    int down_type;             // 12 or 14
+    int32_t* xsum;             // [n_tok][d/32] sums of xq per 32 (xsb: per-256 scales)
+    float* hbuf;               // [n_tok*k][dff] SiLU(gate) * up
+    int32_t* hsum;             // [n_tok*k][dff/32] (hsb: per-256 scales of hq)
     // trace (optional, small shapes): int32 block sums, pair-major
-    int32_t* gu_sums;          // [n_tok*k][2][dff][nb]
-    int32_t* dn_sums;          // [n_tok*k][d][nbf]
+    int32_t* gu_sums;          // MXFP4 [n_tok*k][2][dff][nb]; Q4_K [n_tok*k][2][dff][d/256][2]
+    int32_t* dn_sums;          // MXFP4 [n_tok*k][d][nbf]; Q4_K [..][d][dff/256][2]; Q6_K [..][d][dff/256]
 };
 
+// XCD-aware work order of the grouped GEMMs.  Work item w = (row group
+// w / ntiles, token tile w % ntiles); the workgroups of a launch are dealt to
+// the 8 XCDs round robin (workgroup L runs on XCD L % 8, in order of L), so
+// XCD x takes the contiguous range of items [x * per, (x + 1) * per): the
+// token tiles of one expert and row group then run back to back on one XCD
+// and re-read that weight slice from its L2 instead of HBM.  Returns false for
+// workgroups past the last item.
+CPB_DEV inline bool grouped_item(int ntiles, int ngroups, int* tile, int* group) {
+    const int L = blockIdx.x, total = ntiles * ngroups;
+    const int per = (total + 7) / 8;
+    const int slot = L >> 3, w = (L & 7) * per + slot;
+    if (slot >= per || w >= total) return false;
+    *group = w / ntiles;
+    *tile = w % ntiles;
+    return true;
+}
+
 // All stages of one layer on stream s.  Shapes validated by the caller
-// (MXFP4, top_k in {1,2,4}, d and dff multiples of 32).
+// (MXFP4: d and dff multiples of 32; k-quants: multiples of 256).
 int launch_grouped_layer(const GroupedArgs& a, bool trace, hipStream_t s);
+
+// k-quant stages (moe_grouped_kq.hip): per-token rmsnorm + Q8_K, and the
+// expert GEMMs on int8 matrix cores (gate/up + SiLU * up, Q8_K of h, down)
+int launch_prep_kq(const GroupedArgs& a, hipStream_t s);
+int launch_kq_gemms(const GroupedArgs& a, bool trace, hipStream_t s);
 
 }  // namespace cpb

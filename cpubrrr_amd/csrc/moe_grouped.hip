@@ -365,23 +365,6 @@ CPB_DEV v16f grouped_parts(const WeightStream& ws, int P, unsigned char* smem, c
     return tot;
 }
 
-// XCD-aware work order of the grouped GEMMs.  Work item w = (row group
-// w / ntiles, token tile w % ntiles); the workgroups of a launch are dealt to
-// the 8 XCDs round robin (workgroup L runs on XCD L % 8, in order of L), so
-// XCD x takes the contiguous range of items [x * per, (x + 1) * per): the
-// token tiles of one expert and row group then run back to back on one XCD
-// and re-read that weight slice from its L2 instead of HBM.  Returns false for
-// workgroups past the last item.
-CPB_DEV bool grouped_item(int ntiles, int ngroups, int* tile, int* group) {
-    const int L = blockIdx.x, total = ntiles * ngroups;
-    const int per = (total + 7) / 8;
-    const int slot = L >> 3, w = (L & 7) * per + slot;
-    if (slot >= per || w >= total) return false;
-    *group = w / ntiles;
-    *tile = w % ntiles;
-    return true;
-}
-
 // ---- 5. grouped gate/up + SwiGLU-OAI + Q8 (+ image of h) ----
 // one workgroup per (token tile, group of 4 row tiles) (grouped_item); 8
 // waves: wave w = row tile w/2 of the group, gate (w even) or up (w odd).
@@ -531,10 +514,19 @@ __global__ __launch_bounds__(256) void k_combine_batch(GroupedArgs a) {
 
 int launch_grouped_layer(const GroupedArgs& a, bool trace, hipStream_t s) {
     const int nt = a.n_tok;
-    launch(k_prep_batch, dim3(nt), dim3(256), sizeof(float) * (2 * a.d + 64), s, a);
+    if (a.kq) {
+        if (launch_prep_kq(a, s)) return -19;
+    } else {
+        launch(k_prep_batch, dim3(nt), dim3(256), sizeof(float) * (2 * a.d + 64), s, a);
+    }
     launch(k_router_batch, dim3(a.ne, (nt + kRouteTok - 1) / kRouteTok), dim3(256), sizeof(double) * 64, s, a);
     launch(k_select_batch, dim3(nt), dim3(64), select_lds_bytes(a.ne, a.d, kExactGroupWide), s, a);
     launch(k_group, dim3(1), dim3(1024), 0, s, a);
+    if (a.kq) {
+        if (launch_kq_gemms(a, trace, s)) return -19;
+        launch(k_combine_batch, dim3((unsigned)std::min<size_t>(((size_t)nt * (a.d / 4) + 255) / 256, 2048)), dim3(256), 0, s, a);
+        return hipGetLastError() == hipSuccess ? 0 : -19;
+    }
     // one workgroup per (token tile, row group), dealt out by grouped_item:
     // 8 slots per XCD round, enough for the largest tile count
     const int ngu = a.max_tiles * ((a.dff / 32 + 3) / 4), ndn = a.max_tiles * ((a.d / 32 + 7) / 8);

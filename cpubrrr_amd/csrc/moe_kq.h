@@ -7,6 +7,16 @@
 
 namespace cpb {
 
+// 16-byte units per superblock in the stream layouts (Q4_K: 144 B = 9 units;
+// Q6_K: 210 B padded to 14, the fp16 d alone in unit 13)
+constexpr int kQ4Units = 9;
+constexpr int kQ6Units = 14;
+CPB_DEV_HOST_INLINE int kq_units(int type) { return type == 12 ? kQ4Units : kQ6Units; }
+CPB_DEV_HOST_INLINE int kq_sb_bytes(int type) { return type == 12 ? 144 : 210; }
+
+// engine_qwen2.rs:40-51 converts IEEE binary16 exactly; so does the hardware.
+CPB_DEV inline float half_bits(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (uint16_t)h); }
+
 struct KqArgs {
     const u32x4* gu;         // gate+up stream layout (k_repack_kq_gateup)
     const u32x4* dn;         // down stream layout (k_repack_kq_down)

@@ -33,14 +33,7 @@
 
 namespace cpb {
 
-constexpr int kQ4Units = 9;
-constexpr int kQ6Units = 14;
-CPB_DEV_HOST_INLINE int kq_units(int type) { return type == 12 ? kQ4Units : kQ6Units; }
-CPB_DEV_HOST_INLINE int kq_sb_bytes(int type) { return type == 12 ? 144 : 210; }
 constexpr int kXsPad = 272;      // LDS bytes per 256-activation superblock (256 + 16: bank spread)
-
-// engine_qwen2.rs:40-51 converts IEEE binary16 exactly; so does the hardware.
-CPB_DEV float half_bits(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (uint16_t)h); }
 
 // Q4_K superblock term of one row (engine_qwen2.rs:84-114).  u: the 9 units
 // (u[0] = d, dmin, 12 packed scale/min bytes; u[1..8] = qs[128]); xs: the 256

@@ -169,14 +169,20 @@ class MoeBlock:
         return xo, t
 
     def grouped_sums(self, layer: int, x: np.ndarray, apply_norm: bool = True):
-        """Test hook of the grouped (n_tok > 1) MXFP4 path: returns (x_out,
-        gu_sums [n_tok*k][2][d_ff][d/32], dn_sums [n_tok*k][d][d_ff/32])."""
+        """Test hook of the grouped (n_tok > 1) path: returns (x_out, gu_sums,
+        dn_sums), pair-major; MXFP4: [n_tok*k][2][d_ff][d/32] and
+        [n_tok*k][d][d_ff/32]; k-quants: the decode trace's superblock sums."""
         c = self.cfg
         xo = np.array(x, np.float32, copy=True, order="C")
         n_tok = xo.shape[0]
         np_ = n_tok * c.top_k
-        gs = np.zeros((np_, 2, c.d_ff, c.d // 32), np.int32)
-        ds = np.zeros((np_, c.d, c.d_ff // 32), np.int32)
+        if c.mx:
+            gs = np.zeros((np_, 2, c.d_ff, c.d // 32), np.int32)
+            ds = np.zeros((np_, c.d, c.d_ff // 32), np.int32)
+        else:
+            gs = np.zeros((np_, 2, c.d_ff, c.d // 256, 2), np.int32)
+            q4 = self._down_type.get(layer, c.wtype_down) == L.GGUF_Q4_K
+            ds = np.zeros((np_, c.d, c.d_ff // 256, 2) if q4 else (np_, c.d, c.d_ff // 256), np.int32)
         L.check(self._lib.cpb_moe_grouped_sums(self._h, layer, xo.ctypes.data_as(L.f32p), n_tok, int(bool(apply_norm)),
                                                gs.ctypes.data_as(L.i32p), ds.ctypes.data_as(L.i32p)),
                 "cpb_moe_grouped_sums")

@@ -173,11 +173,13 @@ int cpb_moe_layer_bytes(const cpb_moe_cfg* cfg, size_t* out);
 int cpb_moe_timing(cpb_moe_t* h, int enable);
 int cpb_moe_kernel_times(cpb_moe_t* h, double ms[3], long n[3]);
 
-/* Test hook of the grouped (n_tok > 1) MXFP4 path, no counterpart in the
+/* Test hook of the grouped (n_tok > 1) path, no counterpart in the
  * reference: one layer on host x[n_tok][d] like cpb_moe_forward, also
- * returning every int32 block sum of the matrix-core products, pair-major
- * (pair = token * top_k + slot):
- *   gu_sums [n_tok*top_k][2][d_ff][d/32], dn_sums [n_tok*top_k][d][d_ff/32].
+ * returning every integer block sum of the matrix-core products, pair-major
+ * (pair = token * top_k + slot), in the per-token trace's layouts:
+ *   MXFP4:  gu_sums [pairs][2][d_ff][d/32], dn_sums [pairs][d][d_ff/32];
+ *   Q4_K gate/up: gu_sums [pairs][2][d_ff][d/256][2] {sumi, mint};
+ *   down: Q6_K [pairs][d][d_ff/256] {acc}, Q4_K [pairs][d][d_ff/256][2].
  * Lets tests check them bit for bit against the per-token trace.           */
 int cpb_moe_grouped_sums(cpb_moe_t* h, int layer, float* x, int n_tok, int apply_norm,
                          int32_t* gu_sums, int32_t* dn_sums);
