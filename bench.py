@@ -11,6 +11,8 @@ inputs resident in HBM.  Workloads (synthetic data):
   3  Qwen3-30B-A3B 48-layer MoE stack: Q4_K gate/up, Q6_K down, top-8 of 128
   4  gpt-oss-20b layer, 512-token prefill: tokens grouped by expert, expert
      GEMMs on the matrix cores (8 rotating layer copies)
+  5  Qwen3-30B-A3B layer, 512-token prefill on the int8 matrix cores (not a
+     BASELINE config; the batched k-quant path beside config 4)
 Prints one JSON line: value = expert-weight GB/s (algorithmic bytes of the
 active experts + biases + router per token / time), plus tok/s, the roofline
 of the dominant kernel (gate/up) and the CPU baseline (the oracle on the
@@ -32,7 +34,8 @@ sys.path.insert(0, str(ROOT))
 # WRITE_SIZE runs scaled by a 1 GiB copy (profiles/hbm_traffic_config1_phased.md,
 # profiles/hbm_traffic_config3_qwen.md);
 # None where not yet measured.
-MEASURED_TRAFFIC = {"k_gateup_mx": 35_815_144, "k_gateup_kq": 14_404_042}
+MEASURED_TRAFFIC = {"k_gateup_mx": 35_815_144, "k_gateup_kq": 14_404_042,
+                    "k_gateup_grouped": 484_748_900}
 
 METRIC = "expert-weight GB/s (% HBM peak) + MoE-layer tok/s, gpt-oss-20b shape, 1 GPU"
 HBM_PEAK_GBS = 8000.0
@@ -50,11 +53,14 @@ CONFIGS = {
     4: dict(name="config4: gpt-oss-20b MoE layer, 512-token prefill (batched), Zipf(1.1) router bias, tokens grouped "
                  "by expert, fp8 x fp4 scaled-MFMA expert GEMMs",
             d=2880, dff=2880, ne=32, k=4, layers=8, per_step=1, zipf=1.1, norm=True, n_tok=512),
+    5: dict(name="config5: Qwen3-30B-A3B MoE layer, 512-token prefill (batched), Q4_K gate/up + Q6_K down, tokens "
+                 "grouped by expert, int8 MFMA expert GEMMs",
+            d=2048, dff=768, ne=128, k=8, layers=8, per_step=1, zipf=None, norm=True, n_tok=512, family="qwen"),
 }
 for _c in CONFIGS.values():
     _c.setdefault("family", "gptoss")
     _c.setdefault("n_tok", 1)
-MFMA_FP8_PEAK_TOPS = 5000.0   # MI355X dense fp8 (the f8f6f4 instructions run fp8 x fp4 at this rate)
+MFMA_FP8_PEAK_TOPS = 5000.0   # MI355X dense fp8 / int8 (the f8f6f4 instructions run fp8 x fp4 at this rate)
 
 
 def layer_bytes(c) -> dict:
@@ -71,26 +77,46 @@ def layer_bytes(c) -> dict:
     return {"gate_up": gu, "down": dn, "router": router, "total": gu + dn + router}
 
 
-def batched_result(c, args, ms, n_tok) -> dict:
-    """Bench line of a batched (prefill) step: one layer over n_tok tokens."""
+def batched_result(c, args, ms, n_tok, kt) -> dict:
+    """Bench line of a batched (prefill) step: one layer over n_tok tokens.
+    The roofline is the gate/up GEMM's (the dominant kernel): every expert's
+    gate/up weights are read (all experts hold pairs at this batch size)."""
     d, dff, ne, k = c["d"], c["dff"], c["ne"], c["k"]
-    expert_bytes = 3 * d * (d // 32 * 17) + 2 * dff * 4 + d * 4        # one expert's gate, up, down + biases
-    wbytes = ne * expert_bytes + ne * d * 4 + ne * 4                   # every expert holds pairs at this batch size
+    qwen = c["family"] == "qwen"
+    if qwen:
+        gu_w = ne * 2 * dff * (d // 256 * 144)
+        dn_w = ne * d * (dff // 256 * 210)
+        wbytes = gu_w + dn_w + ne * d * 4
+    else:
+        gu_w = ne * 2 * dff * (d // 32 * 17) + ne * 2 * dff * 4          # MXFP4 rows + biases
+        dn_w = ne * d * (dff // 32 * 17) + ne * d * 4
+        wbytes = gu_w + dn_w + ne * d * 4 + ne * 4
     macs = n_tok * k * (2 * dff * d + d * dff)                          # useful int8 multiply-adds
     sec = ms * 1e-3
     gbs = wbytes / sec / 1e9
     tops = 2 * macs / sec / 1e12
+    gu_ms, gu_n = kt["gate_up"]
+    dn_ms, dn_n = kt["down"]
+    gu_us = gu_ms / max(gu_n, 1) * 1e3
+    dn_us = dn_ms / max(dn_n, 1) * 1e3
+    gu_gbs = gu_w / (gu_us * 1e-6) / 1e9
+    gu_tops = 2 * n_tok * k * 2 * dff * d / (gu_us * 1e-6) / 1e12
+    kern = "k_gateup_kq_grouped" if qwen else "k_gateup_grouped"
     return {
         "metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "fp8 x fp4 (exact int8 x E2M1)", "data": "synthetic",
+        "vs_baseline": None, "dtype": "int8" if qwen else "fp8 x fp4 (exact int8 x E2M1)", "data": "synthetic",
         "config": {"workload": c["name"], "tokens_per_step": n_tok, "d": d, "d_ff": dff, "n_expert": ne,
-                   "top_k": k, "weights": "MXFP4 (GGUF type 39)"},
+                   "top_k": k,
+                   "weights": "Q4_K gate/up + Q6_K down (GGUF types 12/14)" if qwen else "MXFP4 (GGUF type 39)"},
         "tok_per_s": round(n_tok / sec, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
-        "roofline": {"bound": "hbm", "kernel": "whole layer (7 kernels)", "achieved": round(gbs, 1),
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "bytes_per_launch": wbytes},
-        "mfma": {"achieved": round(tops, 2), "peak": MFMA_FP8_PEAK_TOPS, "unit": "TOP/s (useful int8-equivalent)",
+        "kernels_us": {"gate_up_gemm": round(gu_us, 2), "down_gemm": round(dn_us, 2)},
+        "roofline": {"bound": "hbm", "kernel": kern, "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": MEASURED_TRAFFIC.get(kern), "bytes_per_launch": gu_w,
+                     "mfma_int8_equiv": {"achieved": round(gu_tops, 2), "peak": MFMA_FP8_PEAK_TOPS,
+                                         "unit": "TOP/s", "frac": round(gu_tops / MFMA_FP8_PEAK_TOPS, 5)}},
+        "mfma": {"achieved": round(tops, 2), "peak": MFMA_FP8_PEAK_TOPS, "unit": "TOP/s (useful int8-equivalent, whole layer)",
                  "frac": round(tops / MFMA_FP8_PEAK_TOPS, 5), "ops_per_step": 2 * macs},
     }
 
@@ -184,7 +210,7 @@ def main() -> int:
     d, dff, ne, k, nl = c["d"], c["dff"], c["ne"], c["k"], c["layers"]
     qwen = c["family"] == "qwen"
     if qwen:
-        cfg = MoeConfig.qwen3(d=d, n_expert=ne, top_k=k, d_ff=dff, n_layer=nl)
+        cfg = MoeConfig.qwen3(d=d, n_expert=ne, top_k=k, d_ff=dff, n_layer=nl, max_tokens=c["n_tok"])
     else:
         cfg = MoeConfig.gptoss(d=d, n_expert=ne, top_k=k, d_ff=dff, n_layer=nl, max_tokens=c["n_tok"])
     dev = torch.device("cuda:0")
@@ -251,7 +277,7 @@ def main() -> int:
     blk.timing(False)
 
     if n_tok > 1:
-        out = batched_result(c, args, ms, n_tok)
+        out = batched_result(c, args, ms, n_tok, kt)
         if not args.no_cpu:
             log("timing the CPU baseline ...")
             out["cpu_baseline"] = cpu_baseline(host_keep, c, args.cpu_seconds)

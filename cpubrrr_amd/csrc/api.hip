@@ -617,7 +617,18 @@ static int layer_grouped(cpb_moe_t* h, int layer, float* d_x, int n_tok, int app
     g.kq = h->mx ? 0 : 1; g.down_type = L.down_type;
     g.xsum = h->g_xsum; g.hbuf = h->g_hbuf; g.hsum = h->g_hsum;
     g.gu_sums = gu_sums; g.dn_sums = dn_sums;
-    if (cpb::launch_grouped_layer(g, gu_sums != nullptr, h->stream)) return fail(CPB_ENODEV, "grouped layer launch failed");
+    // timing mode: events around the two expert GEMMs (classes gate/up, down)
+    cpb::LaunchEvents ev[2];
+    Timer t1(h, 1), t2(h, 2);
+    const bool timed = t1.a && t2.a;
+    if (timed) {
+        ev[0] = cpb::LaunchEvents{t1.a, t1.b};
+        ev[1] = cpb::LaunchEvents{t2.a, t2.b};
+    }
+    cpb::armed_events() = cpb::LaunchEvents{};
+    const int r = cpb::launch_grouped_layer(g, gu_sums != nullptr, h->stream, timed ? ev : nullptr);
+    cpb::armed_events() = cpb::LaunchEvents{};
+    if (r) return fail(CPB_ENODEV, "grouped layer launch failed");
     return 0;
 }
 

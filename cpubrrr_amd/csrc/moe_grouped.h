@@ -73,11 +73,13 @@ CPB_DEV inline bool grouped_item(int ntiles, int ngroups, int* tile, int* group)
 
 // All stages of one layer on stream s.  Shapes validated by the caller
 // (MXFP4: d and dff multiples of 32; k-quants: multiples of 256).
-int launch_grouped_layer(const GroupedArgs& a, bool trace, hipStream_t s);
+// ev (optional): event pairs armed for the gate/up GEMM (ev[0]) and the down
+// GEMM (ev[1]) launches (timing mode).
+int launch_grouped_layer(const GroupedArgs& a, bool trace, hipStream_t s, const LaunchEvents* ev = nullptr);
 
 // k-quant stages (moe_grouped_kq.hip): per-token rmsnorm + Q8_K, and the
 // expert GEMMs on int8 matrix cores (gate/up + SiLU * up, Q8_K of h, down)
 int launch_prep_kq(const GroupedArgs& a, hipStream_t s);
-int launch_kq_gemms(const GroupedArgs& a, bool trace, hipStream_t s);
+int launch_kq_gemms(const GroupedArgs& a, bool trace, hipStream_t s, const LaunchEvents* ev = nullptr);
 
 }  // namespace cpb

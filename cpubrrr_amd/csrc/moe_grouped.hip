@@ -512,7 +512,7 @@ __global__ __launch_bounds__(256) void k_combine_batch(GroupedArgs a) {
     }
 }
 
-int launch_grouped_layer(const GroupedArgs& a, bool trace, hipStream_t s) {
+int launch_grouped_layer(const GroupedArgs& a, bool trace, hipStream_t s, const LaunchEvents* ev) {
     const int nt = a.n_tok;
     if (a.kq) {
         if (launch_prep_kq(a, s)) return -19;
@@ -523,7 +523,7 @@ int launch_grouped_layer(const GroupedArgs& a, bool trace, hipStream_t s) {
     launch(k_select_batch, dim3(nt), dim3(64), select_lds_bytes(a.ne, a.d, kExactGroupWide), s, a);
     launch(k_group, dim3(1), dim3(1024), 0, s, a);
     if (a.kq) {
-        if (launch_kq_gemms(a, trace, s)) return -19;
+        if (launch_kq_gemms(a, trace, s, ev)) return -19;
         launch(k_combine_batch, dim3((unsigned)std::min<size_t>(((size_t)nt * (a.d / 4) + 255) / 256, 2048)), dim3(256), 0, s, a);
         return hipGetLastError() == hipSuccess ? 0 : -19;
     }
@@ -532,13 +532,12 @@ int launch_grouped_layer(const GroupedArgs& a, bool trace, hipStream_t s) {
     const int ngu = a.max_tiles * ((a.dff / 32 + 3) / 4), ndn = a.max_tiles * ((a.d / 32 + 7) / 8);
     const dim3 ggu((ngu + 7) / 8 * 8), gdn((ndn + 7) / 8 * 8);
     const size_t lds = 2 * kStageBytes;        // two staging buffers (>= the 16 KB epilogue exchange)
-    if (trace) {
-        launch(k_gateup_grouped<true>, ggu, dim3(512), lds, s, a);
-        launch(k_down_grouped<true>, gdn, dim3(512), lds, s, a);
-    } else {
-        launch(k_gateup_grouped<false>, ggu, dim3(512), lds, s, a);
-        launch(k_down_grouped<false>, gdn, dim3(512), lds, s, a);
-    }
+    if (ev) armed_events() = ev[0];
+    if (trace) launch(k_gateup_grouped<true>, ggu, dim3(512), lds, s, a);
+    else launch(k_gateup_grouped<false>, ggu, dim3(512), lds, s, a);
+    if (ev) armed_events() = ev[1];
+    if (trace) launch(k_down_grouped<true>, gdn, dim3(512), lds, s, a);
+    else launch(k_down_grouped<false>, gdn, dim3(512), lds, s, a);
     launch(k_combine_batch, dim3((unsigned)std::min<size_t>(((size_t)nt * (a.d / 4) + 255) / 256, 2048)), dim3(256), 0, s, a);
     return hipGetLastError() == hipSuccess ? 0 : -19;
 }

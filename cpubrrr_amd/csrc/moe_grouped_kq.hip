@@ -378,13 +378,15 @@ int launch_prep_kq(const GroupedArgs& a, hipStream_t s) {
     return hipGetLastError() == hipSuccess ? 0 : -19;
 }
 
-int launch_kq_gemms(const GroupedArgs& a, bool trace, hipStream_t s) {
+int launch_kq_gemms(const GroupedArgs& a, bool trace, hipStream_t s, const LaunchEvents* ev) {
     const int ngu = a.max_tiles * ((a.dff / 32 + 1) / 2), ndn = a.max_tiles * ((a.d / 32 + 3) / 4);
     const dim3 ggu((ngu + 7) / 8 * 8), gdn((ndn + 7) / 8 * 8);
     const int np = a.n_tok * a.k, nq = np * (a.dff / 256);
+    if (ev) armed_events() = ev[0];
     if (trace) launch(k_gateup_kq_grouped<true>, ggu, dim3(256), 0, s, a);
     else launch(k_gateup_kq_grouped<false>, ggu, dim3(256), 0, s, a);
     launch(k_quant_h_batch, dim3((nq + 3) / 4), dim3(256), 0, s, a);
+    if (ev) armed_events() = ev[1];
     if (a.down_type == 12) {
         if (trace) launch(k_down_kq_grouped<12, true>, gdn, dim3(256), 0, s, a);
         else launch(k_down_kq_grouped<12, false>, gdn, dim3(256), 0, s, a);
