@@ -209,6 +209,8 @@ int check_cfg(const cpb_moe_cfg* c) {
     } else {
         return fail(CPB_EINVAL, "unsupported gate/up type %d", c->wtype_gate_up);
     }
+    if ((size_t)c->max_tokens * c->top_k > 16384)
+        return fail(CPB_EINVAL, "max_tokens * top_k = %lld exceeds 16384", (long long)c->max_tokens * c->top_k);
     if (c->router != CPB_ROUTER_TOPK_SOFTMAX && c->router != CPB_ROUTER_SOFTMAX_TOPK)
         return fail(CPB_EINVAL, "bad router %d", c->router);
     if (c->act != CPB_ACT_SWIGLU_OAI && c->act != CPB_ACT_SILU) return fail(CPB_EINVAL, "bad act %d", c->act);

@@ -161,58 +161,86 @@ __global__ __launch_bounds__(64) void k_select_batch(GroupedArgs a) {
 }
 
 // ---- 4. group the (token, slot) pairs by expert (stable), tile table ----
-// The pairs' expert ids are staged in LDS as bytes (ne <= 256) in chunks of
-// kGroupChunk, so the per-expert ballot scans read LDS, not global memory.
-constexpr int kGroupChunk = 16384;
+// One workgroup of 16 waves; wave w takes a contiguous run of pairs.  Per
+// 64-pair group a wave ranks its lanes among those of the same expert with one
+// ballot per distinct expert present (not per expert of the layer), keeping
+// a running per-wave count per expert in LDS; the waves' counts are then
+// scanned (expert major, wave minor), so the order is stable: by expert, then
+// by pair index.  Pair ranks stay in registers (np <= kGroupMax).
+constexpr int kGroupWaves = 16, kGroupMax = kGroupWaves * 64 * 16;
 __global__ __launch_bounds__(1024) void k_group(GroupedArgs a) {
-    __shared__ int cnt_l[256], off_l[256], toff_l[256], pos_l[256];
-    __shared__ uint8_t ids_l[kGroupChunk];
-    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, nw = blockDim.x >> 6;
-    const int np = a.n_tok * a.k;
+    __shared__ int wcnt[kGroupWaves][256];
+    __shared__ int off_l[256], toff_l[256], cnt_l[256];
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int np = a.n_tok * a.k, ne = a.ne;
     const uint64_t lt = lane ? (~0ull >> (64 - lane)) : 0ull;
-    for (int e = tid; e < a.ne; e += blockDim.x) cnt_l[e] = 0;
+    for (int i = tid; i < kGroupWaves * 256; i += blockDim.x) (&wcnt[0][0])[i] = 0;
+    const int per = (np + kGroupWaves * 64 - 1) / (kGroupWaves * 64) * 64;     // pairs per wave, whole groups
+    const int p0 = w * per;
+    // this lane's pairs (up to 16 groups) and experts
+    int ex[16], rk[16];
+#pragma unroll
+    for (int g = 0; g < 16; g++) {
+        const int p = p0 + 64 * g + lane;
+        ex[g] = (64 * g < per && p < np) ? a.ids[p] : -1;
+    }
     __syncthreads();
-    // counts: LDS atomics
-    for (int p = tid; p < np; p += blockDim.x) atomicAdd(&cnt_l[a.ids[p]], 1);
+#pragma unroll
+    for (int g = 0; g < 16; g++) {
+        rk[g] = 0;
+        if (64 * g >= per) continue;
+        uint64_t active = __ballot(ex[g] >= 0);
+        while (active) {
+            const int leader = __builtin_ctzll(active);
+            const int e0 = __builtin_amdgcn_readlane(ex[g], leader);
+            const uint64_t m = __ballot(ex[g] == e0);
+            const int base = wcnt[w][e0];
+            if (ex[g] == e0) rk[g] = base + __popcll(m & lt);
+            __builtin_amdgcn_wave_barrier();
+            if (lane == leader) wcnt[w][e0] = base + __popcll(m);
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            active &= ~m;
+        }
+    }
     __syncthreads();
+    // per expert: total, exclusive prefix over experts (counts and 32-pair tiles)
     if (w == 0) {
-        // exclusive prefix sums of the counts and of the tile counts, 64 experts per round
         int o = 0, to = 0;
-        for (int base = 0; base < a.ne; base += 64) {
+        for (int base = 0; base < ne; base += 64) {
             const int e = base + lane;
-            const int c = e < a.ne ? cnt_l[e] : 0, t = (c + 31) / 32;
+            int c = 0;
+            if (e < ne)
+                for (int v = 0; v < kGroupWaves; v++) c += wcnt[v][e];
+            const int t = (c + 31) / 32;
             int ic = c, it = t;
 #pragma unroll
             for (int s2 = 1; s2 < 64; s2 <<= 1) {
                 const int uc = __shfl_up(ic, s2), ut = __shfl_up(it, s2);
                 if (lane >= s2) { ic += uc; it += ut; }
             }
-            if (e < a.ne) { off_l[e] = o + ic - c; pos_l[e] = o + ic - c; toff_l[e] = to + it - t; }
+            if (e < ne) { off_l[e] = o + ic - c; toff_l[e] = to + it - t; cnt_l[e] = c; }
             o += __shfl(ic, 63);
             to += __shfl(it, 63);
         }
         if (lane == 0) *a.ntiles = to;
     }
     __syncthreads();
-    // stable scatter, chunk by chunk (pairs in ascending order)
-    for (int c0 = 0; c0 < np; c0 += kGroupChunk) {
-        const int n = min(kGroupChunk, np - c0);
-        for (int p = tid; p < n; p += blockDim.x) ids_l[p] = (uint8_t)a.ids[c0 + p];
-        __syncthreads();
-        for (int e = w; e < a.ne; e += nw) {
-            int pos = pos_l[e];
-            for (int base = 0; base < n; base += 64) {
-                const int p = base + lane;
-                const bool m = p < n && ids_l[p] == e;
-                const uint64_t bm = __ballot(m);
-                if (m) a.sorted[pos + __popcll(bm & lt)] = c0 + p;
-                pos += __popcll(bm);
-            }
-            if (lane == 0) pos_l[e] = pos;
+    // wave offsets within each expert: in place, expert-parallel
+    for (int e = tid; e < ne; e += blockDim.x) {
+        int run = off_l[e];
+        for (int v = 0; v < kGroupWaves; v++) {
+            const int c = wcnt[v][e];
+            wcnt[v][e] = run;
+            run += c;
         }
-        __syncthreads();
     }
-    for (int e = w; e < a.ne; e += nw) {
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < 16; g++)
+        if (ex[g] >= 0) a.sorted[wcnt[w][ex[g]] + rk[g]] = p0 + 64 * g + lane;
+    for (int e = w; e < ne; e += kGroupWaves) {
         const int c = cnt_l[e], nt = (c + 31) / 32;
         for (int j = lane; j < nt; j += 64) a.tiles[toff_l[e] + j] = int4{e, off_l[e] + 32 * j, min(32, c - 32 * j), 0};
     }
