@@ -103,6 +103,18 @@ typedef struct orc_qwen_layer {
 /* engine_qwen2.rs:395-433 */
 void orc_qwen_moe(const orc_qwen_layer* L, float* x, int apply_norm, orc_trace* tr);
 
+/* ---- two-stage LM head (head.c; engine_gpt2.rs:237-342, 464-494, 937-1002) -- */
+uint16_t orc_f32_to_bf16(float v);
+float    orc_bf16_to_f32(uint16_t v);
+uint16_t orc_q4_scale_search(const float* vals, float* idq);
+void  orc_q4_quant_row(const uint16_t* w, int cols, uint8_t* nib, uint16_t* sc);
+void  orc_q8_quant_row(const uint16_t* w, int cols, int8_t* q, float* s);
+float orc_q4_row_dot(const uint8_t* nib, const uint16_t* sc, const int8_t* xq, const float* xsb, int nb);
+float orc_q8_row_dot(const int8_t* q, const float* s, const int8_t* xq, const float* xsb, int cols);
+void  orc_head(const uint16_t* w, int V, int d, const float* x, const float* norm_w, float eps, int nt, int cand,
+               int32_t* cand_ids, float* cand_screen, float* cand_logits, int8_t* xq_out, float* xsb_out,
+               int32_t* chosen);
+
 /* ---- configuration --------------------------------------------------------*/
 void orc_set_threads(int n);   /* OpenMP threads for the row loops (0 = default) */
 int  orc_get_threads(void);

@@ -71,6 +71,21 @@ def lib() -> C.CDLL:
         L.orc_q6k_dot.argtypes = [u8p, i8p, f32p, C.c_int, i32p]
         L.orc_gptoss_moe.argtypes = [C.POINTER(GptossLayer), f32p, C.c_int, C.POINTER(Trace)]
         L.orc_qwen_moe.argtypes = [C.POINTER(QwenLayer), f32p, C.c_int, C.POINTER(Trace)]
+        u16p = C.POINTER(C.c_uint16)
+        L.orc_f32_to_bf16.restype = C.c_uint16
+        L.orc_f32_to_bf16.argtypes = [C.c_float]
+        L.orc_bf16_to_f32.restype = C.c_float
+        L.orc_bf16_to_f32.argtypes = [C.c_uint16]
+        L.orc_q4_scale_search.restype = C.c_uint16
+        L.orc_q4_scale_search.argtypes = [f32p, f32p]
+        L.orc_q4_quant_row.argtypes = [u16p, C.c_int, u8p, u16p]
+        L.orc_q8_quant_row.argtypes = [u16p, C.c_int, i8p, f32p]
+        L.orc_q4_row_dot.restype = C.c_float
+        L.orc_q4_row_dot.argtypes = [u8p, u16p, i8p, f32p, C.c_int]
+        L.orc_q8_row_dot.restype = C.c_float
+        L.orc_q8_row_dot.argtypes = [i8p, f32p, i8p, f32p, C.c_int]
+        L.orc_head.argtypes = [u16p, C.c_int, C.c_int, f32p, f32p, C.c_float, C.c_int, C.c_int, i32p, f32p, f32p,
+                               i8p, f32p, i32p]
         L.orc_set_threads.argtypes = [C.c_int]
         L.orc_get_threads.restype = C.c_int
         _LIB = L
@@ -237,3 +252,61 @@ def qwen_moe(layer: dict, x: np.ndarray, apply_norm: bool, want_sums: bool = Fal
     tr = _mk_trace(t)
     lib().orc_qwen_moe(C.byref(L), _p(xo, f32p), int(bool(apply_norm)), C.byref(tr))
     return xo, t
+
+
+# ---- two-stage LM head (oracle/head.c) ----
+u16p = C.POINTER(C.c_uint16)
+
+
+def f32_to_bf16(v: float) -> int:
+    return int(lib().orc_f32_to_bf16(float(v)))
+
+
+def q4_scale_search(vals):
+    vals = np.ascontiguousarray(vals, np.float32)
+    idq = C.c_float()
+    db = lib().orc_q4_scale_search(_p(vals, f32p), C.byref(idq))
+    return int(db), np.float32(idq.value)
+
+
+def q4_quant_row(w_bf16):
+    w = np.ascontiguousarray(w_bf16, np.uint16)
+    nib = np.empty(w.size // 2, np.uint8); sc = np.empty(w.size // 32, np.uint16)
+    lib().orc_q4_quant_row(_p(w, u16p), w.size, _p(nib, u8p), _p(sc, u16p))
+    return nib, sc
+
+
+def q8_quant_row(w_bf16):
+    w = np.ascontiguousarray(w_bf16, np.uint16)
+    q = np.empty(w.size, np.int8); s = np.empty(w.size // 32, np.float32)
+    lib().orc_q8_quant_row(_p(w, u16p), w.size, _p(q, i8p), _p(s, f32p))
+    return q, s
+
+
+def q4_row_dot(nib, sc, xq, xsb):
+    nib = np.ascontiguousarray(nib, np.uint8); sc = np.ascontiguousarray(sc, np.uint16)
+    xq = np.ascontiguousarray(xq, np.int8); xsb = np.ascontiguousarray(xsb, np.float32)
+    return np.float32(lib().orc_q4_row_dot(_p(nib, u8p), _p(sc, u16p), _p(xq, i8p), _p(xsb, f32p), xsb.size))
+
+
+def q8_row_dot(q, s, xq, xsb):
+    q = np.ascontiguousarray(q, np.int8); s = np.ascontiguousarray(s, np.float32)
+    xq = np.ascontiguousarray(xq, np.int8); xsb = np.ascontiguousarray(xsb, np.float32)
+    return np.float32(lib().orc_q8_row_dot(_p(q, i8p), _p(s, f32p), _p(xq, i8p), _p(xsb, f32p), q.size))
+
+
+def head(w_bf16, x, norm_w, eps, nt=12, cand=8):
+    """engine_gpt2.rs:937-1002 (greedy).  Returns dict: chosen, cand_ids,
+    cand_screen, cand_logits, xq, xsb."""
+    w = np.ascontiguousarray(w_bf16, np.uint16)
+    V, d = w.shape
+    x = np.ascontiguousarray(x, np.float32); norm_w = np.ascontiguousarray(norm_w, np.float32)
+    out = {"cand_ids": np.zeros(nt * cand, np.int32), "cand_screen": np.zeros(nt * cand, np.float32),
+           "cand_logits": np.zeros(nt * cand, np.float32), "xq": np.zeros(d, np.int8),
+           "xsb": np.zeros(d // 32, np.float32)}
+    ch = C.c_int32()
+    lib().orc_head(_p(w, u16p), V, d, _p(x, f32p), _p(norm_w, f32p), float(eps), nt, cand,
+                   _p(out["cand_ids"], i32p), _p(out["cand_screen"], f32p), _p(out["cand_logits"], f32p),
+                   _p(out["xq"], i8p), _p(out["xsb"], f32p), C.byref(ch))
+    out["chosen"] = int(ch.value)
+    return out

@@ -1,0 +1,182 @@
+"""Pins the head restatement (oracle/head.c) against independent numpy
+float32 restatements and closed forms: bf16 rounding, the Q4 scale search
+(engine_gpt2.rs:274-300), Q4 / Q8 row quantisation and dots (:240-272,
+:314-342, :466-494, :169-191) and the two-stage head's candidate and greedy
+logic (:937-1002).  CPU only."""
+import numpy as np
+
+from oracle import oracle as O
+
+rng = np.random.default_rng(99)
+f32 = np.float32
+
+
+def fma32(a, b, c):
+    """a * b + c with one rounding to fp32 (round to nearest even), exactly"""
+    from fractions import Fraction
+    exact = Fraction(float(a)) * Fraction(float(b)) + Fraction(float(c))
+    cand = np.float32(float(exact))
+    best = None
+    for v in (np.nextafter(cand, np.float32(-np.inf)), cand, np.nextafter(cand, np.float32(np.inf))):
+        err = abs(Fraction(float(v)) - exact)
+        key = (err, int(np.float32(v).view(np.uint32)) & 1)
+        if best is None or key < best[0]:
+            best = (key, v)
+    return np.float32(best[1])
+
+
+def bf16_np(v):
+    """round-to-nearest-even of fp32 into its top 16 bits (numpy, vectorised)"""
+    b = np.asarray(v, np.float32).view(np.uint32).astype(np.uint64)
+    return (((b + 0x7FFF + ((b >> 16) & 1)) >> 16) & 0xFFFF).astype(np.uint16)
+
+
+def from_bf16(h):
+    return (np.asarray(h, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def test_bf16_rounding():
+    vals = np.concatenate([rng.standard_normal(2000).astype(np.float32),
+                           np.array([1.0, -1.0, 0.0, 1.00390625, 1.01171875, 3.0e38, 1e-40], np.float32)])
+    # exact ties: low 16 bits = 0x8000 round to even
+    ties = (rng.integers(0, 1 << 15, 200).astype(np.uint32) << 16 | 0x8000).view(np.float32) + np.float32(0)
+    vals = np.concatenate([vals, ties[np.isfinite(ties)]])
+    got = np.array([O.f32_to_bf16(v) for v in vals], np.uint16)
+    assert np.array_equal(got, bf16_np(vals))
+    # bf16 of exactly representable values is exact
+    r = from_bf16(rng.integers(0, 0x7F80, 500).astype(np.uint16))
+    assert np.array_equal(from_bf16(np.array([O.f32_to_bf16(v) for v in r], np.uint16)), r)
+
+
+def scale_search_np(vals):
+    vals = np.asarray(vals, np.float32)
+    amax, vmax = f32(0), f32(0)
+    for v in vals:
+        if abs(v) > amax:
+            amax, vmax = abs(v), v
+    if amax == 0:
+        return 0, f32(0)
+    best_err, best_db = np.float32(np.finfo(np.float32).max), 0
+    for t in range(17):
+        nmax = f32(7.0) + f32(t) * f32(0.0625)
+        db = int(bf16_np(vmax / -nmax))
+        d = from_bf16(np.uint16(db))
+        if d == 0:
+            continue
+        idq = f32(1.0) / d
+        err = f32(0)
+        for v in vals:
+            c = int(np.clip(np.floor(v * idq + f32(8.5)), 0, 15))
+            e = v - f32(c - 8) * d
+            err = f32(err + f32(e * e))
+        if err < best_err:
+            best_err, best_db = err, db
+    d = from_bf16(np.uint16(best_db))
+    return best_db, (f32(1.0) / d if d != 0 else f32(0))
+
+
+def test_q4_scale_search_and_codes():
+    for trial in range(60):
+        vals = from_bf16(bf16_np(rng.standard_normal(32).astype(np.float32) * f32(10 ** rng.uniform(-3, 1))))
+        if trial == 0:
+            vals[:] = 0
+        if trial == 1:
+            vals = from_bf16(bf16_np(np.linspace(-1, 2, 32)))
+        db, idq = O.q4_scale_search(vals)
+        db2, idq2 = scale_search_np(vals)
+        assert db == db2 and idq == idq2, trial
+    # the row quantiser: codes from the chosen scale; block of zeros -> code 8
+    w = bf16_np(rng.standard_normal(256).astype(np.float32) * 0.02)
+    w[32:64] = 0
+    nib, sc = O.q4_quant_row(w)
+    for b in range(8):
+        vals = from_bf16(w[b * 32:(b + 1) * 32])
+        db, idq = scale_search_np(vals)
+        assert sc[b] == db
+        c = np.clip(np.floor(vals * idq + f32(8.5)), 0, 15).astype(np.uint8)
+        assert np.array_equal(nib[b * 16:(b + 1) * 16], c[:16] | (c[16:] << 4)), b
+    assert np.all(nib[16:32] == 0x88) and sc[1] == 0
+
+
+def test_q8_quant_row_closed_form():
+    w = bf16_np(rng.standard_normal(512).astype(np.float32) * 0.05)
+    q, s = O.q8_quant_row(w)
+    v = from_bf16(w).reshape(-1, 32)
+    amax = np.maximum(np.abs(v).max(1), f32(1e-12))
+    assert np.array_equal(s, (amax / f32(127.0)).astype(np.float32))
+    ratio = v / s[:, None]
+    want = np.clip(np.sign(ratio) * np.floor(np.abs(ratio) + 0.5), -127, 127).astype(np.int8)
+    assert np.array_equal(q, want.reshape(-1))
+
+
+def _xq(d):
+    x = rng.standard_normal(d).astype(np.float32)
+    return O.qblock32(x)
+
+
+def test_q4_and_q8_row_dots():
+    d = 2880
+    xq, xsb = _xq(d)
+    w = bf16_np(rng.standard_normal(d).astype(np.float32) * 0.02)
+    nib, sc = O.q4_quant_row(w)
+    # numpy float32 restatement of the lane order (lane j: elements 4j..4j+3, 16+4j..)
+    a = [f32(0)] * 4
+    nb16 = nib.reshape(-1, 16)
+    codes = np.stack([nb16 & 15, nb16 >> 4], 1)                          # [block][half][16]
+    for b in range(d // 32):
+        sv = from_bf16(sc[b]) * xsb[b]
+        for j in range(4):
+            e = np.arange(4 * j, 4 * j + 4)
+            t = int(((codes[b, 0, e].astype(int) - 8) * xq[b * 32 + e]).sum() +
+                    ((codes[b, 1, e].astype(int) - 8) * xq[b * 32 + 16 + e]).sum())
+            a[j] = fma32(f32(t), sv, a[j])
+    want = f32(f32(a[0] + a[1]) + f32(a[2] + a[3]))
+    assert O.q4_row_dot(nib, sc, xq, xsb) == want
+    # and against float64 of the dequantised row
+    deq = ((codes.reshape(-1, 32).astype(np.float64) - 8)
+           * from_bf16(sc)[:, None].astype(np.float64)).reshape(-1)
+    ref = float((deq * xq.astype(np.float64) * np.repeat(xsb, 32)).sum())
+    assert abs(float(want) - ref) <= 1e-5 * float(np.abs(deq * xq * np.repeat(xsb, 32)).sum())
+    q, s = O.q8_quant_row(w)
+    ref8 = float((q.astype(np.float64) * np.repeat(s, 32) * xq * np.repeat(xsb, 32)).sum())
+    got8 = float(O.q8_row_dot(q, s, xq, xsb))
+    assert abs(got8 - ref8) <= 1e-5 * float(np.abs(q * np.repeat(s, 32) * xq * np.repeat(xsb, 32)).sum())
+    # the exact lane / accumulator order of dot_q8_i8 (even blocks -> acc0, odd -> acc1)
+    a0, a1 = [f32(0)] * 4, [f32(0)] * 4
+    for b in range(d // 32):
+        sv = f32(s[b] * xsb[b])
+        for j in range(4):
+            e = np.r_[np.arange(4 * j, 4 * j + 4), np.arange(16 + 4 * j, 16 + 4 * j + 4)]
+            t = int((q[b * 32 + e].astype(int) * xq[b * 32 + e]).sum())
+            if b % 2 == 0:
+                a0[j] = fma32(f32(t), sv, a0[j])
+            else:
+                a1[j] = fma32(f32(t), sv, a1[j])
+    v = [f32(a0[j] + a1[j]) for j in range(4)]
+    assert O.q8_row_dot(q, s, xq, xsb) == f32(f32(v[0] + v[1]) + f32(v[2] + v[3]))
+    # odd block count: the last block goes into the first accumulator
+    assert np.isfinite(O.q8_row_dot(q[:96], s[:3], xq[:96], xsb[:3]))
+
+
+def test_head_candidates_and_greedy():
+    V, d, nt, cand = 1024, 512, 12, 8
+    w = bf16_np(rng.standard_normal((V, d)).astype(np.float32) * 0.02)
+    x = rng.standard_normal(d).astype(np.float32)
+    nw = (1 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+    out = O.head(w, x, nw, 1e-5, nt, cand)
+    xq, xsb = out["xq"], out["xsb"]
+    xn = O.rmsnorm_gptoss(x, nw, 1e-5)
+    xq2, xsb2 = O.qblock32(xn)
+    assert np.array_equal(xq, xq2) and np.array_equal(xsb, xsb2)
+    screen = np.array([O.q4_row_dot(*O.q4_quant_row(w[r]), xq, xsb) for r in range(V)], np.float32)
+    nq = V // 4
+    ids = []
+    for wid in range(nt):
+        r0, r1 = 4 * (nq * wid // nt), 4 * (nq * (wid + 1) // nt)
+        order = np.argsort(-screen[r0:r1].astype(np.float64), kind="stable")[:cand]
+        ids += list(r0 + order)
+    assert np.array_equal(out["cand_ids"], np.array(ids, np.int32))
+    assert np.array_equal(out["cand_screen"], screen[ids])
+    logits = np.array([O.q8_row_dot(*O.q8_quant_row(w[r]), xq, xsb) for r in ids], np.float32)
+    assert np.array_equal(out["cand_logits"], logits)
+    assert out["chosen"] == ids[int(np.argmax(logits))]       # first maximum
