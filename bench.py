@@ -13,6 +13,8 @@ inputs resident in HBM.  Workloads (synthetic data):
      GEMMs on the matrix cores (8 rotating layer copies)
   5  Qwen3-30B-A3B layer, 512-token prefill on the int8 matrix cores (not a
      BASELINE config; the batched k-quant path beside config 4)
+  6  gpt-oss two-stage LM head, 201088 x 2880 (not a BASELINE config): Q4
+     screen of every row, exact Q8 refine of 96 candidates, greedy
 Prints one JSON line: value = expert-weight GB/s (algorithmic bytes of the
 active experts + biases + router per token / time), plus tok/s, the roofline
 of the dominant kernel (gate/up) and the CPU baseline (the oracle on the
@@ -56,6 +58,9 @@ CONFIGS = {
     5: dict(name="config5: Qwen3-30B-A3B MoE layer, 512-token prefill (batched), Q4_K gate/up + Q6_K down, tokens "
                  "grouped by expert, int8 MFMA expert GEMMs",
             d=2048, dff=768, ne=128, k=8, layers=8, per_step=1, zipf=None, norm=True, n_tok=512, family="qwen"),
+    6: dict(name="config6: gpt-oss two-stage LM head (output.weight 201088 x 2880 bf16 -> Q4 screen + Q8 refine of "
+                 "12 x 8 candidates + greedy), one token",
+            d=2880, dff=0, ne=0, k=0, layers=1, per_step=1, zipf=None, norm=True, family="head", vocab=201088),
 }
 for _c in CONFIGS.values():
     _c.setdefault("family", "gptoss")
@@ -185,6 +190,56 @@ def cpu_baseline(host_layers, c, budget_s: float) -> dict:
                      "omp_num_threads": os.environ.get("OMP_NUM_THREADS")}}
 
 
+def bench_head(args, c) -> int:
+    """config 6: the LM head on one token; value = Q4 screen bytes / time."""
+    import numpy as np
+    import torch
+
+    from cpubrrr_amd import LmHead
+
+    d, V = c["d"], c["vocab"]
+    r = np.random.default_rng(0)
+    w32 = (r.standard_normal((V, d)) * 0.02).astype(np.float32)
+    w = ((w32.view(np.uint32).astype(np.uint64) + 0x7FFF + ((w32.view(np.uint32) >> 16) & 1)) >> 16).astype(np.uint16)
+    del w32
+    nw = np.ones(d, np.float32)
+    torch.cuda.set_device(0)
+    hd = LmHead(d, V)
+    t0 = time.perf_counter()
+    hd.load(w, nw)
+    log(f"head quantised in {time.perf_counter() - t0:.1f} s")
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
+    hd.set_stream(stream.cuda_stream)
+    x = torch.from_numpy((r.standard_normal(d) * 3).astype(np.float32)).to("cuda:0")
+    ch = torch.zeros(1, dtype=torch.int32, device="cuda:0")
+    for _ in range(args.warmup):
+        hd.forward_device(x.data_ptr(), ch.data_ptr())
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(args.steps):
+        hd.forward_device(x.data_ptr(), ch.data_ptr())
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    nb = d // 32
+    screen_bytes = V * nb * (16 + 2)                   # nibbles + bf16 scales of every row
+    refine_bytes = 96 * (d + nb * 4)
+    gbs = (screen_bytes + refine_bytes) / (ms * 1e-3) / 1e9
+    out = {"metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+           "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "dtype": "int8 x Q4 / Q8", "data": "synthetic",
+           "config": {"workload": c["name"], "d": d, "n_vocab": V, "n_slices": 12, "n_cand": 8},
+           "tok_per_s": round(1e3 / ms, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+           "roofline": {"bound": "hbm", "kernel": "whole head (norm, screen, top-k, refine)", "achieved": round(gbs, 1),
+                        "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                        "bytes_per_launch": screen_bytes + refine_bytes}}
+    hd.close()
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -207,6 +262,8 @@ def main() -> int:
     from cpubrrr_amd import MoeBlock, MoeConfig, synth
 
     c = CONFIGS[args.config]
+    if c["family"] == "head":
+        return bench_head(args, c)
     d, dff, ne, k, nl = c["d"], c["dff"], c["ne"], c["k"], c["layers"]
     qwen = c["family"] == "qwen"
     if qwen:

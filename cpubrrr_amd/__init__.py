@@ -6,5 +6,6 @@ package is its Python host mirror (`MoeBlock`) and workload synthesiser.
 from .moe import MoeBlock, MoeConfig  # noqa: F401
 from . import synth  # noqa: F401
 from .gguf import GgufFile  # noqa: F401
+from .head import LmHead  # noqa: F401
 
-__all__ = ["MoeBlock", "MoeConfig", "synth", "GgufFile"]
+__all__ = ["MoeBlock", "MoeConfig", "synth", "GgufFile", "LmHead"]

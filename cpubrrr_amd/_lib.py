@@ -1,5 +1,5 @@
 """ctypes binding of libcpb_moe.so (the C ABI in include/cpb_moe.h,
-include/cpb_gguf.h and include/cpb_synth.h).  Loading fails loudly when the library is missing: there
+include/cpb_gguf.h, include/cpb_head.h and include/cpb_synth.h).  Loading fails loudly when the library is missing: there
 is no CPU fallback for the HIP path."""
 from __future__ import annotations
 
@@ -49,6 +49,16 @@ class GgufHparams(C.Structure):
                 ("rms_eps", C.c_double)]
 
 
+class HeadCfg(C.Structure):
+    _fields_ = [("d", C.c_int), ("n_vocab", C.c_int), ("n_slices", C.c_int), ("n_cand", C.c_int),
+                ("rms_eps", C.c_float)]
+
+
+class HeadTrace(C.Structure):
+    _fields_ = [("cand_ids", i32p), ("cand_screen", f32p), ("cand_logits", f32p), ("xq", i8p), ("xsb", f32p),
+                ("screen", f32p)]
+
+
 # every symbol the public headers declare, with its ctypes signature
 SIGNATURES = {
     "cpb_moe_create": (C.c_int, [C.POINTER(MoeCfg), C.c_int, C.POINTER(C.c_void_p)]),
@@ -80,6 +90,14 @@ SIGNATURES = {
     "cpb_gguf_hparams_get": (C.c_int, [C.c_void_p, C.POINTER(GgufHparams)]),
     "cpb_gguf_write_manifest": (C.c_int, [C.c_void_p, C.c_char_p]),
     "cpb_moe_load_gguf_layer": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int]),
+    "cpb_head_create": (C.c_int, [C.POINTER(HeadCfg), C.c_int, C.POINTER(C.c_void_p)]),
+    "cpb_head_load": (C.c_int, [C.c_void_p, C.POINTER(C.c_uint16), f32p]),
+    "cpb_head_forward": (C.c_int, [C.c_void_p, f32p, i32p, C.POINTER(HeadTrace)]),
+    "cpb_head_forward_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p]),
+    "cpb_head_set_stream": (C.c_int, [C.c_void_p, C.c_void_p]),
+    "cpb_head_sync": (C.c_int, [C.c_void_p]),
+    "cpb_head_destroy": (None, [C.c_void_p]),
+    "cpb_head_bytes": (C.c_int, [C.POINTER(HeadCfg), C.POINTER(C.c_size_t)]),
     "cpb_synth_u64": (C.c_uint64, [C.c_uint64, C.c_uint64, C.c_uint64]),
     "cpb_synth_mxfp4": (None, [u8p, C.c_size_t, C.c_int, C.c_int, C.c_uint64, C.c_uint64]),
     "cpb_synth_normal": (None, [f32p, C.c_size_t, C.c_float, C.c_float, C.c_uint64, C.c_uint64]),

@@ -19,4 +19,5 @@ fn main() {
     println!("cargo:rerun-if-env-changed=ROCM_PATH");
     println!("cargo:rerun-if-changed=../../include/cpb_moe.h");
     println!("cargo:rerun-if-changed=../../include/cpb_gguf.h");
+    println!("cargo:rerun-if-changed=../../include/cpb_head.h");
 }

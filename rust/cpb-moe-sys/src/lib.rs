@@ -1,4 +1,5 @@
-//! Raw declarations of libcpb_moe's C ABI (include/cpb_moe.h, include/cpb_gguf.h).
+//! Raw declarations of libcpb_moe's C ABI (include/cpb_moe.h, include/cpb_gguf.h,
+//! include/cpb_head.h).
 //!
 //! The MoE block of cpubrrr's engines (src/bin/engine_gpt2.rs:845-923,
 //! src/bin/engine_qwen2.rs:395-433) becomes `cpb_moe_forward` (host x) or
@@ -124,6 +125,34 @@ pub struct cpb_gguf_hparams {
     pub rms_eps: f64,
 }
 
+/// Two-stage LM head configuration (include/cpb_head.h).
+#[repr(C)]
+#[derive(Clone, Copy, Debug, Default)]
+pub struct cpb_head_cfg {
+    pub d: c_int,
+    pub n_vocab: c_int,
+    pub n_slices: c_int,
+    pub n_cand: c_int,
+    pub rms_eps: f32,
+}
+
+/// Opaque head handle.
+#[repr(C)]
+pub struct cpb_head_t {
+    _private: [u8; 0],
+}
+
+#[repr(C)]
+#[derive(Clone, Copy, Debug)]
+pub struct cpb_head_trace {
+    pub cand_ids: *mut i32,
+    pub cand_screen: *mut f32,
+    pub cand_logits: *mut f32,
+    pub xq: *mut i8,
+    pub xsb: *mut f32,
+    pub screen: *mut f32,
+}
+
 #[link(name = "cpb_moe")]
 extern "C" {
     // ---- include/cpb_moe.h ----
@@ -166,4 +195,14 @@ extern "C" {
     pub fn cpb_gguf_hparams_get(g: *const cpb_gguf_t, out: *mut cpb_gguf_hparams) -> c_int;
     pub fn cpb_gguf_write_manifest(g: *const cpb_gguf_t, path: *const c_char) -> c_int;
     pub fn cpb_moe_load_gguf_layer(h: *mut cpb_moe_t, g: *const cpb_gguf_t, layer: c_int) -> c_int;
+
+    // ---- include/cpb_head.h ----
+    pub fn cpb_head_create(cfg: *const cpb_head_cfg, device: c_int, out: *mut *mut cpb_head_t) -> c_int;
+    pub fn cpb_head_load(h: *mut cpb_head_t, out_w: *const u16, out_norm: *const f32) -> c_int;
+    pub fn cpb_head_forward(h: *mut cpb_head_t, x: *const f32, chosen: *mut i32, trace: *mut cpb_head_trace) -> c_int;
+    pub fn cpb_head_forward_device(h: *mut cpb_head_t, d_x: *const f32, d_chosen: *mut i32) -> c_int;
+    pub fn cpb_head_set_stream(h: *mut cpb_head_t, stream: *mut c_void) -> c_int;
+    pub fn cpb_head_sync(h: *mut cpb_head_t) -> c_int;
+    pub fn cpb_head_destroy(h: *mut cpb_head_t);
+    pub fn cpb_head_bytes(cfg: *const cpb_head_cfg, out: *mut usize) -> c_int;
 }
