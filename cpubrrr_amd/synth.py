@@ -93,3 +93,30 @@ def qwen_layer(d: int, dff: int, ne: int, k: int, seed: int = 0, layer: int = 0,
 def token(d: int, seed: int = 0, index: int = 0) -> np.ndarray:
     """fp32 N(0,1) activation (BASELINE: input after RMSNorm for config 0)."""
     return normal(d, 1.0, seed, 1_000_000 + index)
+
+
+def bf16(a: np.ndarray) -> np.ndarray:
+    """fp32 -> bf16 bits, round to nearest even (the GGUF BF16 tensor type)."""
+    b = np.asarray(a, np.float32).view(np.uint32).astype(np.uint64)
+    return (((b + 0x7FFF + ((b >> 16) & 1)) >> 16) & 0xFFFF).astype(np.uint16)
+
+
+def attn_layer(d: int, nh: int, nkv: int, hd: int, seed: int = 0, layer: int = 0, swa: int = 128) -> dict:
+    """One gpt-oss attention block: bf16 q/k/v/o weights N(0, 0.02), fp32
+    biases N(0, 0.01), sinks N(0, 1), attn_norm near 1 (the reference loads
+    these from the GGUF: attn_q/k/v/out.weight BF16, .bias, attn_sinks,
+    attn_norm, engine_gpt2.rs:1293-1305)."""
+    base = 1_000 + layer * 16
+    return {
+        "d": d, "nh": nh, "nkv": nkv, "hd": hd, "swa": swa, "eps": 1e-5,
+        "attn_norm": 1.0 + normal(d, 0.05, seed, base + 0),
+        "wq": bf16(normal((nh * hd, d), 0.02, seed, base + 1)),
+        "wk": bf16(normal((nkv * hd, d), 0.02, seed, base + 2)),
+        "wv": bf16(normal((nkv * hd, d), 0.02, seed, base + 3)),
+        "wo": bf16(normal((d, nh * hd), 0.02, seed, base + 4)),
+        "bq": normal(nh * hd, 0.01, seed, base + 5),
+        "bk": normal(nkv * hd, 0.01, seed, base + 6),
+        "bv": normal(nkv * hd, 0.01, seed, base + 7),
+        "bo": normal(d, 0.01, seed, base + 8),
+        "sinks": normal(nh, 1.0, seed, base + 9),
+    }

@@ -21,7 +21,7 @@ def build() -> Path:
     march = ["-march=x86-64-v3"] if platform.machine() == "x86_64" else []
     tmp = LIB.with_suffix(".so.tmp")
     cmd = ["gcc", "-O3", *march, "-ffp-contract=off", "-fno-fast-math", "-fopenmp", "-fPIC", "-shared",
-           "-std=c11", "-Wall", "-o", str(tmp), str(HERE / "oracle.c"), str(HERE / "head.c"), "-lm"]
+           "-std=c11", "-Wall", "-o", str(tmp), str(HERE / "oracle.c"), str(HERE / "head.c"), str(HERE / "attn.c"), "-lm"]
     subprocess.run(cmd, check=True)
     os.replace(tmp, LIB)
     return LIB

@@ -115,6 +115,25 @@ void  orc_head(const uint16_t* w, int V, int d, const float* x, const float* nor
                int32_t* cand_ids, float* cand_screen, float* cand_logits, int8_t* xq_out, float* xsb_out,
                int32_t* chosen);
 
+/* ---- attention block, decode (attn.c; engine_gpt2.rs:535-590, 772-843) ---- */
+typedef struct orc_attn_layer_t {
+    int d, nh, nkv, hd, swa;
+    float eps;
+    const float* attn_norm;                       /* [d] */
+    const int8_t* wq; const float* sq;            /* Q8 rows [nh*hd][d], scales [nh*hd][d/32] */
+    const int8_t* wk; const float* sk;            /* [nkv*hd][d] */
+    const int8_t* wv; const float* sv;            /* [nkv*hd][d] */
+    const int8_t* wo; const float* so;            /* [d][nh*hd] */
+    const float *bq, *bk, *bv, *bo, *sinks;       /* [nh*hd] [nkv*hd] [nkv*hd] [d] [nh] */
+} orc_attn_layer_t;
+typedef struct orc_attn_trace {
+    int8_t* xq; float* xsb; float* q; float* k; float* v; float* ao; int8_t* aq; float* asb;
+} orc_attn_trace;
+void orc_rope_table(int hd, int max_seq, float base, float* tab);
+/* x [d] updated in place; kc / vc: this layer's cache [max_seq][nkv][hd] */
+void orc_attn_layer(const orc_attn_layer_t* L, int il, int pos, float* x, float* kc, float* vc, const float* rope_tab,
+                    orc_attn_trace* tr);
+
 /* ---- configuration --------------------------------------------------------*/
 void orc_set_threads(int n);   /* OpenMP threads for the row loops (0 = default) */
 int  orc_get_threads(void);

@@ -310,3 +310,60 @@ def head(w_bf16, x, norm_w, eps, nt=12, cand=8):
                    _p(out["xq"], i8p), _p(out["xsb"], f32p), C.byref(ch))
     out["chosen"] = int(ch.value)
     return out
+
+
+# ---- attention block, decode (oracle/attn.c) ----
+class AttnLayerC(C.Structure):
+    _fields_ = [("d", C.c_int), ("nh", C.c_int), ("nkv", C.c_int), ("hd", C.c_int), ("swa", C.c_int),
+                ("eps", C.c_float), ("attn_norm", f32p),
+                ("wq", i8p), ("sq", f32p), ("wk", i8p), ("sk", f32p), ("wv", i8p), ("sv", f32p),
+                ("wo", i8p), ("so", f32p), ("bq", f32p), ("bk", f32p), ("bv", f32p), ("bo", f32p),
+                ("sinks", f32p)]
+
+
+class AttnTraceC(C.Structure):
+    _fields_ = [("xq", i8p), ("xsb", f32p), ("q", f32p), ("k", f32p), ("v", f32p), ("ao", f32p), ("aq", i8p),
+                ("asb", f32p)]
+
+
+def rope_table(hd, max_seq, base):
+    tab = np.zeros(max_seq * hd, np.float32)
+    lib().orc_rope_table.argtypes = [C.c_int, C.c_int, C.c_float, f32p]
+    lib().orc_rope_table(hd, max_seq, float(base), _p(tab, f32p))
+    return tab
+
+
+def q8_rows(w_bf16):
+    """Q8Mat::from_bf16 of a [rows][cols] bf16 matrix: (q int8 [rows][cols], s [rows][cols/32])."""
+    w = np.ascontiguousarray(w_bf16, np.uint16)
+    q = np.empty(w.shape, np.int8)
+    s = np.empty((w.shape[0], w.shape[1] // 32), np.float32)
+    for r in range(w.shape[0]):
+        q[r], s[r] = q8_quant_row(w[r])
+    return q, s
+
+
+def attn_layer(L: dict, il: int, pos: int, x, kc, vc, tab):
+    """One decode step of the attention block (engine_gpt2.rs:772-843).
+    L: d, nh, nkv, hd, swa, eps, attn_norm, q8 weights wq/sq/wk/sk/wv/sv/wo/so
+    (see q8_rows), biases bq/bk/bv/bo, sinks.  kc / vc: this layer's cache
+    [max_seq][nkv][hd] (updated at pos).  Returns (x_out, trace)."""
+    keep = {k: np.ascontiguousarray(L[k]) for k in ("attn_norm", "wq", "sq", "wk", "sk", "wv", "sv", "wo", "so",
+                                                     "bq", "bk", "bv", "bo", "sinks")}
+    S = AttnLayerC(L["d"], L["nh"], L["nkv"], L["hd"], L["swa"], L["eps"], _p(keep["attn_norm"], f32p),
+                   _p(keep["wq"], i8p), _p(keep["sq"], f32p), _p(keep["wk"], i8p), _p(keep["sk"], f32p),
+                   _p(keep["wv"], i8p), _p(keep["sv"], f32p), _p(keep["wo"], i8p), _p(keep["so"], f32p),
+                   _p(keep["bq"], f32p), _p(keep["bk"], f32p), _p(keep["bv"], f32p), _p(keep["bo"], f32p),
+                   _p(keep["sinks"], f32p))
+    d, nh, nkv, hd = L["d"], L["nh"], L["nkv"], L["hd"]
+    t = {"xq": np.zeros(d, np.int8), "xsb": np.zeros(d // 32, np.float32), "q": np.zeros(nh * hd, np.float32),
+         "k": np.zeros(nkv * hd, np.float32), "v": np.zeros(nkv * hd, np.float32),
+         "ao": np.zeros(nh * hd, np.float32), "aq": np.zeros(nh * hd, np.int8),
+         "asb": np.zeros(nh * hd // 32, np.float32)}
+    tr = AttnTraceC(*[_p(t[n], ty) for n, ty in AttnTraceC._fields_])
+    xo = np.array(x, np.float32, copy=True)
+    lib().orc_attn_layer.argtypes = [C.POINTER(AttnLayerC), C.c_int, C.c_int, f32p, f32p, f32p, f32p,
+                                     C.POINTER(AttnTraceC)]
+    assert kc.flags["C_CONTIGUOUS"] and vc.flags["C_CONTIGUOUS"]
+    lib().orc_attn_layer(C.byref(S), il, pos, _p(xo, f32p), _p(kc, f32p), _p(vc, f32p), _p(tab, f32p), C.byref(tr))
+    return xo, t
