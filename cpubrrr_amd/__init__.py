@@ -7,5 +7,6 @@ from .moe import MoeBlock, MoeConfig  # noqa: F401
 from . import synth  # noqa: F401
 from .gguf import GgufFile  # noqa: F401
 from .head import LmHead  # noqa: F401
+from .attn import Attention  # noqa: F401
 
-__all__ = ["MoeBlock", "MoeConfig", "synth", "GgufFile", "LmHead"]
+__all__ = ["MoeBlock", "MoeConfig", "synth", "GgufFile", "LmHead", "Attention"]

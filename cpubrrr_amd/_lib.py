@@ -1,5 +1,5 @@
 """ctypes binding of libcpb_moe.so (the C ABI in include/cpb_moe.h,
-include/cpb_gguf.h, include/cpb_head.h and include/cpb_synth.h).  Loading fails loudly when the library is missing: there
+include/cpb_gguf.h, include/cpb_head.h, include/cpb_attn.h and include/cpb_synth.h).  Loading fails loudly when the library is missing: there
 is no CPU fallback for the HIP path."""
 from __future__ import annotations
 
@@ -59,6 +59,17 @@ class HeadTrace(C.Structure):
                 ("screen", f32p)]
 
 
+class AttnCfg(C.Structure):
+    _fields_ = [("d", C.c_int), ("n_head", C.c_int), ("n_head_kv", C.c_int), ("head_dim", C.c_int),
+                ("n_layer", C.c_int), ("max_seq", C.c_int), ("sliding_window", C.c_int), ("rope_base", C.c_float),
+                ("rms_eps", C.c_float)]
+
+
+class AttnTrace(C.Structure):
+    _fields_ = [("xq", i8p), ("xsb", f32p), ("q", f32p), ("k", f32p), ("v", f32p), ("ao", f32p), ("aq", i8p),
+                ("asb", f32p)]
+
+
 # every symbol the public headers declare, with its ctypes signature
 SIGNATURES = {
     "cpb_moe_create": (C.c_int, [C.POINTER(MoeCfg), C.c_int, C.POINTER(C.c_void_p)]),
@@ -98,6 +109,15 @@ SIGNATURES = {
     "cpb_head_sync": (C.c_int, [C.c_void_p]),
     "cpb_head_destroy": (None, [C.c_void_p]),
     "cpb_head_bytes": (C.c_int, [C.POINTER(HeadCfg), C.POINTER(C.c_size_t)]),
+    "cpb_attn_create": (C.c_int, [C.POINTER(AttnCfg), C.c_int, C.POINTER(C.c_void_p)]),
+    "cpb_attn_load_layer": (C.c_int, [C.c_void_p, C.c_int, f32p, C.POINTER(C.c_uint16), C.POINTER(C.c_uint16), C.POINTER(C.c_uint16), C.POINTER(C.c_uint16),
+                                      f32p, f32p, f32p, f32p, f32p]),
+    "cpb_attn_forward": (C.c_int, [C.c_void_p, C.c_int, C.c_int, f32p, C.POINTER(AttnTrace)]),
+    "cpb_attn_forward_device": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_void_p]),
+    "cpb_attn_reset": (C.c_int, [C.c_void_p]),
+    "cpb_attn_set_stream": (C.c_int, [C.c_void_p, C.c_void_p]),
+    "cpb_attn_sync": (C.c_int, [C.c_void_p]),
+    "cpb_attn_destroy": (None, [C.c_void_p]),
     "cpb_synth_u64": (C.c_uint64, [C.c_uint64, C.c_uint64, C.c_uint64]),
     "cpb_synth_mxfp4": (None, [u8p, C.c_size_t, C.c_int, C.c_int, C.c_uint64, C.c_uint64]),
     "cpb_synth_normal": (None, [f32p, C.c_size_t, C.c_float, C.c_float, C.c_uint64, C.c_uint64]),
@@ -121,6 +141,14 @@ def lib() -> C.CDLL:
     if _LIB is None:
         if not LIB_PATH.exists():
             raise RuntimeError(f"{LIB_PATH} is not built; run `python -m cpubrrr_amd.build` (hipcc, gfx950)")
+        # One HIP runtime per process: PyTorch-ROCm ships its own
+        # libamdhip64.so.7.  Loaded after ours, torch would bind to the system
+        # runtime already in the process and find no device; loaded first, the
+        # library binds to torch's copy.  So torch (when installed) goes first.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         L = C.CDLL(str(LIB_PATH))
         for name, (res, args) in SIGNATURES.items():
             fn = getattr(L, name)

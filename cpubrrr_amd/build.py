@@ -34,7 +34,7 @@ COMMON = [
     "-Wno-unused-command-line-argument",
 ]
 
-SOURCES = ["route.hip", "moe_mx.hip", "moe_kq.hip", "moe_grouped.hip", "moe_grouped_kq.hip", "head.hip", "api.hip"]
+SOURCES = ["route.hip", "moe_mx.hip", "moe_kq.hip", "moe_grouped.hip", "moe_grouped_kq.hip", "head.hip", "attn.hip", "api.hip"]
 HOST_SOURCES = ["synth.cpp", "gguf.cpp"]
 
 

@@ -1,5 +1,5 @@
 //! Raw declarations of libcpb_moe's C ABI (include/cpb_moe.h, include/cpb_gguf.h,
-//! include/cpb_head.h).
+//! include/cpb_head.h, include/cpb_attn.h).
 //!
 //! The MoE block of cpubrrr's engines (src/bin/engine_gpt2.rs:845-923,
 //! src/bin/engine_qwen2.rs:395-433) becomes `cpb_moe_forward` (host x) or
@@ -153,6 +153,40 @@ pub struct cpb_head_trace {
     pub screen: *mut f32,
 }
 
+/// Attention block configuration (include/cpb_attn.h).
+#[repr(C)]
+#[derive(Clone, Copy, Debug, Default)]
+pub struct cpb_attn_cfg {
+    pub d: c_int,
+    pub n_head: c_int,
+    pub n_head_kv: c_int,
+    pub head_dim: c_int,
+    pub n_layer: c_int,
+    pub max_seq: c_int,
+    pub sliding_window: c_int,
+    pub rope_base: f32,
+    pub rms_eps: f32,
+}
+
+/// Opaque attention handle.
+#[repr(C)]
+pub struct cpb_attn_t {
+    _private: [u8; 0],
+}
+
+#[repr(C)]
+#[derive(Clone, Copy, Debug)]
+pub struct cpb_attn_trace {
+    pub xq: *mut i8,
+    pub xsb: *mut f32,
+    pub q: *mut f32,
+    pub k: *mut f32,
+    pub v: *mut f32,
+    pub ao: *mut f32,
+    pub aq: *mut i8,
+    pub asb: *mut f32,
+}
+
 #[link(name = "cpb_moe")]
 extern "C" {
     // ---- include/cpb_moe.h ----
@@ -205,4 +239,17 @@ extern "C" {
     pub fn cpb_head_sync(h: *mut cpb_head_t) -> c_int;
     pub fn cpb_head_destroy(h: *mut cpb_head_t);
     pub fn cpb_head_bytes(cfg: *const cpb_head_cfg, out: *mut usize) -> c_int;
+
+    // ---- include/cpb_attn.h ----
+    pub fn cpb_attn_create(cfg: *const cpb_attn_cfg, device: c_int, out: *mut *mut cpb_attn_t) -> c_int;
+    pub fn cpb_attn_load_layer(h: *mut cpb_attn_t, layer: c_int, attn_norm: *const f32, wq: *const u16,
+                               wk: *const u16, wv: *const u16, wo: *const u16, bq: *const f32, bk: *const f32,
+                               bv: *const f32, bo: *const f32, sinks: *const f32) -> c_int;
+    pub fn cpb_attn_forward(h: *mut cpb_attn_t, layer: c_int, pos: c_int, x: *mut f32,
+                            trace: *mut cpb_attn_trace) -> c_int;
+    pub fn cpb_attn_forward_device(h: *mut cpb_attn_t, layer: c_int, pos: c_int, d_x: *mut f32) -> c_int;
+    pub fn cpb_attn_reset(h: *mut cpb_attn_t) -> c_int;
+    pub fn cpb_attn_set_stream(h: *mut cpb_attn_t, stream: *mut c_void) -> c_int;
+    pub fn cpb_attn_sync(h: *mut cpb_attn_t) -> c_int;
+    pub fn cpb_attn_destroy(h: *mut cpb_attn_t);
 }

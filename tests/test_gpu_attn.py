@@ -1,0 +1,119 @@
+"""GPU parity of the attention block (attn.hip) against the oracle
+(oracle/attn.c, pinned in tests/test_oracle_attn.py), one decode step at a
+time over a sequence, each step fed the same x on both sides:
+Q8 activations, q after bias + RoPE and the k / v cache rows bit for bit (the
+projections follow the reference's lane order and the RoPE table is built
+with the same fp32 formula); the heads' outputs to 2e-5 relative (expf and
+the order of the softmax sums differ), their Q8 codes within one step on the
+rare value that the last ulp moves across a rounding boundary, and x bit for
+bit (where a code moved, against the oracle's o-projection of the GPU's own
+codes).  Covers the sliding window of even layers, the
+full-causal odd layers, an odd block count, the gpt-oss shape, reset and
+the device entry point."""
+import numpy as np
+import pytest
+
+from cpubrrr_amd import Attention, synth
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+def oracle_layer(L):
+    Lq = dict(L)
+    for n in ("q", "k", "v", "o"):
+        Lq["w" + n], Lq["s" + n] = O.q8_rows(L["w" + n])
+    return Lq
+
+
+def check_seq(d, nh, nkv, swa, n_pos, layers=(0, 1), seed=0, max_seq=None, xs=2.0):
+    say(f"case attn d={d} nh={nh} nkv={nkv} swa={swa} n_pos={n_pos} layers={layers} seed={seed}")
+    hd = 64
+    max_seq = max_seq or n_pos
+    Ls = {il: synth.attn_layer(d, nh, nkv, hd, seed=seed, layer=il, swa=swa) for il in layers}
+    Lq = {il: oracle_layer(L) for il, L in Ls.items()}
+    tab = O.rope_table(hd, max_seq, 150000.0)
+    r = np.random.default_rng(seed)
+    forced = 0
+    with Attention(d, nh, nkv, max(layers) + 1, max_seq, swa, 150000.0, 1e-5) as at:
+        for il, L in Ls.items():
+            at.load_layer(il, L)
+        for il in layers:
+            kc = np.zeros((max_seq, nkv, hd), np.float32)
+            vc = np.zeros((max_seq, nkv, hd), np.float32)
+            for pos in range(n_pos):
+                x = (r.standard_normal(d) * xs).astype(np.float32)
+                xg, t = at.forward(il, pos, x, trace=True)
+                xo, o = O.attn_layer(Lq[il], il, pos, x, kc, vc, tab)
+                assert np.array_equal(t["xq"], o["xq"]), (il, pos)
+                assert np.array_equal(t["xsb"].view(np.uint32), o["xsb"].view(np.uint32)), (il, pos)
+                assert np.array_equal(t["q"].view(np.uint32), o["q"].view(np.uint32)), (il, pos)
+                assert np.array_equal(t["k"].view(np.uint32), o["k"].view(np.uint32)), (il, pos)
+                assert np.array_equal(t["v"].view(np.uint32), o["v"].view(np.uint32)), (il, pos)
+                assert np.allclose(t["ao"], o["ao"], rtol=2e-5, atol=1e-6), (il, pos)
+                dq = np.abs(t["aq"].astype(int) - o["aq"].astype(int))
+                assert dq.max() <= 1 and (dq != 0).sum() <= max(2, dq.size // 500), (il, pos)
+                if dq.any() or not np.array_equal(t["asb"], o["asb"]):
+                    # teacher-forced o-projection: the oracle's Q8 rows on the GPU's codes
+                    L = Lq[il]
+                    xo = x.copy()
+                    for row in range(d):
+                        xo[row] += O.q8_row_dot(L["wo"][row], L["so"][row], t["aq"], t["asb"]) + L["bo"][row]
+                    forced += 1
+                assert np.array_equal(xg.view(np.uint32), xo.view(np.uint32)), (il, pos)
+    say(f"  steps with a teacher-forced o-projection: {forced}")
+
+
+def test_small_odd_blocks():
+    # d = 288: 9 activation blocks (odd tail in the Q8 dot); window 4
+    check_seq(288, 8, 2, 4, 12, seed=1)
+
+
+def test_small_gqa_window_wrap():
+    check_seq(256, 16, 4, 8, 40, layers=(0, 1, 2), seed=2, max_seq=64)
+
+
+def test_gptoss_shape():
+    # gpt-oss-20b: d 2880, 64 q heads, 8 kv heads, window 128; past the window
+    check_seq(2880, 64, 8, 128, 136, seed=3, max_seq=160, xs=1.0)
+
+
+def test_reset_and_device_entry():
+    import torch
+    d, nh, nkv, hd = 256, 8, 2, 64
+    L = synth.attn_layer(d, nh, nkv, hd, seed=4, layer=0, swa=4)
+    r = np.random.default_rng(4)
+    xs = [(r.standard_normal(d) * 2).astype(np.float32) for _ in range(6)]
+    with Attention(d, nh, nkv, 1, 16, 4, 150000.0, 1e-5) as at:
+        at.load_layer(0, L)
+        first = [at.forward(0, p, x)[0] for p, x in enumerate(xs)]
+        at.reset()
+        stream = torch.cuda.current_stream().cuda_stream
+        at.set_stream(stream)
+        dev = []
+        for p, x in enumerate(xs):
+            xt = torch.from_numpy(x).cuda()
+            at.forward_device(0, p, xt.data_ptr())
+            at.sync()
+            dev.append(xt.cpu().numpy())
+        at.set_stream(None)
+    for a, b in zip(first, dev):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_errors():
+    from cpubrrr_amd import _lib as Lb
+    with Attention(256, 8, 2, 2, 16, 4) as at:
+        x = np.zeros(256, np.float32)
+        with pytest.raises(RuntimeError):
+            at.forward(0, 0, x)                   # layer not loaded
+        at.load_layer(0, synth.attn_layer(256, 8, 2, 64, seed=5))
+        with pytest.raises(RuntimeError):
+            at.forward(0, 16, x)                  # pos >= max_seq
+    with pytest.raises(RuntimeError):
+        Attention(256, 8, 3, 1)                   # n_head not a multiple of n_head_kv
+    assert Lb.CPB_EINVAL == -22

@@ -12,7 +12,7 @@ from cpubrrr_amd import _lib as L
 
 ROOT = Path(__file__).resolve().parent.parent
 RS = (ROOT / "rust" / "cpb-moe-sys" / "src" / "lib.rs").read_text()
-HEADERS = [(ROOT / "include" / h).read_text() for h in ("cpb_moe.h", "cpb_gguf.h", "cpb_head.h")]
+HEADERS = [(ROOT / "include" / h).read_text() for h in ("cpb_moe.h", "cpb_gguf.h", "cpb_head.h", "cpb_attn.h")]
 
 
 def c_functions():
@@ -76,7 +76,8 @@ def _rust_layout(struct):
 def test_struct_layouts():
     for rust, cty in (("cpb_moe_cfg", L.MoeCfg), ("cpb_moe_trace", L.MoeTrace),
                       ("cpb_gguf_tensor", L.GgufTensor), ("cpb_gguf_hparams", L.GgufHparams),
-                      ("cpb_head_cfg", L.HeadCfg), ("cpb_head_trace", L.HeadTrace)):
+                      ("cpb_head_cfg", L.HeadCfg), ("cpb_head_trace", L.HeadTrace),
+                      ("cpb_attn_cfg", L.AttnCfg), ("cpb_attn_trace", L.AttnTrace)):
         want = [(name, getattr(cty, name).offset) for name, _ in cty._fields_]
         assert _rust_layout(rust) == want, rust
 
@@ -85,7 +86,8 @@ def test_ctypes_mirrors_follow_the_headers():
     # the ctypes structs (used above as the C layout) list the header's fields in order
     for h, name, cty in ((HEADERS[0], "cpb_moe_cfg", L.MoeCfg), (HEADERS[0], "cpb_moe_trace", L.MoeTrace),
                          (HEADERS[1], "cpb_gguf_tensor", L.GgufTensor), (HEADERS[1], "cpb_gguf_hparams", L.GgufHparams),
-                         (HEADERS[2], "cpb_head_cfg", L.HeadCfg), (HEADERS[2], "cpb_head_trace", L.HeadTrace)):
+                         (HEADERS[2], "cpb_head_cfg", L.HeadCfg), (HEADERS[2], "cpb_head_trace", L.HeadTrace),
+                         (HEADERS[3], "cpb_attn_cfg", L.AttnCfg), (HEADERS[3], "cpb_attn_trace", L.AttnTrace)):
         body = re.search(r"typedef struct %s \{(.*?)\} %s;" % (name, name), h, re.S).group(1)
         body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
         names = []
