@@ -61,6 +61,10 @@ CONFIGS = {
     6: dict(name="config6: gpt-oss two-stage LM head (output.weight 201088 x 2880 bf16 -> Q4 screen + Q8 refine of "
                  "12 x 8 candidates + greedy), one token",
             d=2880, dff=0, ne=0, k=0, layers=1, per_step=1, zipf=None, norm=True, family="head", vocab=201088),
+    7: dict(name="config7: gpt-oss-20b attention, 24 layers (even: window 128, odd: full causal), decode one token "
+                 "at position 1024 with the KV cache filled, Q8 projections",
+            d=2880, dff=0, ne=0, k=0, layers=24, per_step=24, zipf=None, norm=True, family="attn", n_head=64,
+            n_head_kv=8, swa=128, pos=1024),
 }
 for _c in CONFIGS.values():
     _c.setdefault("family", "gptoss")
@@ -236,8 +240,134 @@ def bench_head(args, c) -> int:
                         "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
                         "bytes_per_launch": screen_bytes + refine_bytes}}
     hd.close()
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline_head(w, nw, x.cpu().numpy(), args.cpu_seconds)
     print(json.dumps(out), flush=True)
     return 0
+
+
+def attn_bytes(c) -> dict:
+    """Algorithmic bytes of one token through one attention layer: the Q8
+    weights of q / k / v / o (codes + fp32 scale per 32) and the cache rows
+    the layer reads (window on even layers, every position on odd ones)."""
+    d, nq, nkv = c["d"], c["n_head"] * 64, c["n_head_kv"] * 64
+    w = ((nq + 2 * nkv) * d + d * nq) * (1 + 4 / 32)
+    vec = 4 * (d + nq + 2 * nkv + d + c["n_head"])
+    pos = c["pos"]
+    kv_even = 2 * min(c["swa"], pos + 1) * nkv * 4
+    kv_odd = 2 * (pos + 1) * nkv * 4
+    return {"weights": int(w + vec), "kv_even": kv_even, "kv_odd": kv_odd,
+            "per_token": int(c["layers"] * (w + vec) + c["layers"] // 2 * (kv_even + kv_odd))}
+
+
+def bench_attn(args, c) -> int:
+    """config 7: one token through the 24 attention layers; value = bytes / time."""
+    import numpy as np
+    import torch
+
+    from cpubrrr_amd import Attention, synth
+
+    d, nh, nkv, nl, pos = c["d"], c["n_head"], c["n_head_kv"], c["layers"], c["pos"]
+    torch.cuda.set_device(0)
+    at = Attention(d, nh, nkv, nl, max_seq=pos + 1, sliding_window=c["swa"], rope_base=150000.0, rms_eps=1e-5)
+    t0 = time.perf_counter()
+    host0 = None
+    for il in range(nl):
+        L = synth.attn_layer(d, nh, nkv, 64, seed=0, layer=il, swa=c["swa"])
+        at.load_layer(il, L)
+        if il == 0:
+            host0 = L
+    log(f"attention weights quantised in {time.perf_counter() - t0:.1f} s")
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
+    at.set_stream(stream.cuda_stream)
+    x = torch.from_numpy(synth.token(d, 0, 7)).to("cuda:0")
+    # fill the cache: positions 0 .. pos-1 through every layer
+    for p in range(pos):
+        for il in range(nl):
+            at.forward_device(il, p, x.data_ptr())
+        x.mul_(0.5)      # keep the residual bounded while the cache fills
+    torch.cuda.synchronize()
+    x0 = x.clone()
+
+    def step():
+        x.copy_(x0)
+        for il in range(nl):
+            at.forward_device(il, pos, x.data_ptr())
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(args.steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    ab = attn_bytes(c)
+    gbs = ab["per_token"] / (ms * 1e-3) / 1e9
+    out = {"metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+           "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "dtype": "int8 x Q8 (fp32 softmax)", "data": "synthetic",
+           "config": {"workload": c["name"], "d": d, "n_head": nh, "n_head_kv": nkv, "layers": nl, "pos": pos,
+                      "sliding_window": c["swa"]},
+           "tok_per_s": round(1e3 / ms, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+           "roofline": {"bound": "hbm", "kernel": "whole block (norm, qkv, core, o-proj) x 24 layers",
+                        "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "bytes_per_launch": ab["per_token"]}}
+    at.close()
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline_attn(host0, c, args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def cpu_baseline_attn(L, c, budget_s: float) -> dict:
+    """The oracle's attention step (single-threaded C, the reference's fp32
+    order) at the same shape and position, on random cache contents."""
+    import numpy as np
+    from oracle import oracle as O
+
+    pos, nkv = c["pos"], c["n_head_kv"]
+    Lq = dict(L)
+    for n in ("q", "k", "v", "o"):
+        Lq["w" + n], Lq["s" + n] = O.q8_rows(L["w" + n])
+    tab = O.rope_table(64, pos + 1, 150000.0)
+    r = np.random.default_rng(1)
+    kc = r.standard_normal((pos + 1, nkv, 64)).astype(np.float32)
+    vc = r.standard_normal((pos + 1, nkv, 64)).astype(np.float32)
+    x = r.standard_normal(c["d"]).astype(np.float32)
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < budget_s or n < 2:
+        O.attn_layer(Lq, n % 2, pos, x, kc, vc, tab)       # alternate window / full layers
+        n += 1
+    per_layer = (time.perf_counter() - t0) / n
+    return {"value": round(1.0 / (per_layer * c["per_step"]), 3), "unit": "tok/s", "cores": 1, "kind": "port",
+            "sample": f"{n} attention layer steps (alternating window / full) at pos {pos} in "
+                      f"{per_layer * n:.1f} s on 1 thread; {per_layer * 1e3:.2f} ms/layer",
+            "ms_per_layer": round(per_layer * 1e3, 3)}
+
+
+def cpu_baseline_head(w, nw, x, budget_s: float) -> dict:
+    """The oracle's head (C, OpenMP over the Q4 screen rows) on the same
+    weights and hidden state."""
+    from oracle import oracle as O
+
+    info = _host_info()
+    threads = info["usable"]
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        threads = min(threads, int(os.environ["OMP_NUM_THREADS"]))
+    O.set_threads(threads)
+    pre = O.q4_quant_rows(w)                  # load time, outside the sample
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < budget_s or n == 0:
+        O.head(w, x, nw, 1e-5, pre=pre)
+        n += 1
+    per = (time.perf_counter() - t0) / n
+    return {"value": round(1.0 / per, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"{n} head evaluations (Q4 rows quantised beforehand, as at the reference's load) in "
+                      f"{per * n:.1f} s on {threads} threads; {per * 1e3:.1f} ms each",
+            "ms_per_token": round(per * 1e3, 2)}
 
 
 def main() -> int:
@@ -264,6 +394,8 @@ def main() -> int:
     c = CONFIGS[args.config]
     if c["family"] == "head":
         return bench_head(args, c)
+    if c["family"] == "attn":
+        return bench_attn(args, c)
     d, dff, ne, k, nl = c["d"], c["dff"], c["ne"], c["k"], c["layers"]
     qwen = c["family"] == "qwen"
     if qwen:

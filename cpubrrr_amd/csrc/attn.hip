@@ -5,20 +5,22 @@
 // :169-191, qblock32 :691-699, rmsnorm_quant_par :730-738.
 //
 // Kernels per token and layer:
-//   k_attn_norm  rmsnorm (16-lane sum of squares) + Q8 per 32 of x;
-//   k_attn_qkv   q / k / v rows: the reference's Q8 dot (8 fp32 chains per
+//   k_attn_qkv   rmsnorm (16-lane sum of squares) + Q8 per 32 of x, then the
+//                q / k / v rows: the reference's Q8 dot (8 fp32 chains per
 //                row, one lane each), bias, RoPE from the table, cache write;
-//   k_attn_core  per q-head: scores over the window, softmax with the sink,
-//                weighted sum of v, Q8 of the head's 64 outputs;
+//   k_attn_core  per (kv-head, chunk of 64 positions): scores of the group's
+//                q-heads, chunk max / sum / weighted v; the last workgroup of
+//                a kv-head merges the chunks with the sink and quantises;
 //   k_attn_oproj x[r] += wo[r] . ao + bo[r].
 // The projections, RoPE and the cache rows are the reference's operations in
 // its order (bit for bit given the same RoPE table, which the host computes
-// once with the reference's formula); the softmax goes through expf and a
-// fixed-order tree sum, so its outputs match to tolerance.
+// once with the reference's formula); the softmax is merged over chunks
+// (flash-decoding) and goes through expf, so the heads' outputs match to
+// tolerance.
 //
-// Q8 weights are re-laid out at load time into tiles of 8 rows: per (tile,
-// 32-block) 8 rows x 32 int8 (256 B) and 8 fp32 scales, so a wavefront (8
-// rows x 8 chains) reads 512 contiguous bytes per step.
+// Weights: the chain-major Q8 stream described at q8c_dot, built on the GPU
+// at load time from the bf16 tensors.  KV cache: [layer][kv-head][position]
+// [64] fp32, so a chunk of positions of one head is one contiguous 16 KiB run.
 #include <hip/hip_runtime.h>
 
 #include <cfloat>
@@ -33,33 +35,77 @@
 namespace cpb {
 
 constexpr int kAttnHd = 64;
+constexpr int kAttnChunk = 128;    // cache positions per core workgroup
+constexpr int kAttnMaxGroup = 8;   // q-heads per kv-head
+
+// ---- cross-lane reductions on DPP + readlane (no LDS round trips) ----
+template <int CTRL>
+CPB_DEV float dppf(float v) { return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false)); }
+CPB_DEV float lanef(float v, int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l)); }
+CPB_DEV float row_sum_f32(float v) {
+    v += dppf<0xB1>(v);          // lane ^ 1
+    v += dppf<0x4E>(v);          // lane ^ 2
+    v += dppf<0x141>(v);         // mirror within 8
+    v += dppf<0x140>(v);         // mirror within 16
+    return v;
+}
+CPB_DEV float wave_max_f32(float v) {
+    const float r = row_max_f32(v);
+    return fmaxf(fmaxf(lanef(r, 0), lanef(r, 16)), fmaxf(lanef(r, 32), lanef(r, 48)));
+}
+CPB_DEV float wave_sum_f32(float v) {
+    const float r = row_sum_f32(v);
+    return (lanef(r, 0) + lanef(r, 16)) + (lanef(r, 32) + lanef(r, 48));
+}
+// max over each half wave (lanes 0-31, 32-63)
+CPB_DEV float half_max_f32(float v) {
+    const float r = row_max_f32(v);
+    const float lo = fmaxf(lanef(r, 0), lanef(r, 16)), hi = fmaxf(lanef(r, 32), lanef(r, 48));
+    return (threadIdx.x & 32) ? hi : lo;
+}
+
+// Chain-major Q8 stream.  dot_q8_i8 (:169-191) runs 8 fp32 chains per row:
+// chain c = 4h + j accumulates, over the blocks b = h, h+2, h+4, ... in order,
+// the integer dot of block b's bytes 4j..4j+3 and 16+4j..16+4j+3 times
+// scale(b) * xscale(b).  Lane 8r + c of a wave runs chain c of tile row r.
+// Per 8-row tile the codes are stored by pairs of chain steps: entry (tile,
+// sp) is 64 lanes x 16 bytes, lane l's 16 bytes = (lo, hi) of its chain at
+// steps 2sp and 2sp + 1 (step s = block 2s + h).  Scales: [tile][s][r][h].
+// Blocks are padded to a multiple of 4 with zero codes and zero scales
+// (their products are +0 and leave every chain unchanged).
+CPB_DEV_HOST_INLINE int q8c_nbp(int nb) { return (nb + 3) & ~3; }
+CPB_DEV_HOST_INLINE size_t q8c_code_bytes(int rows, int cols) { return (size_t)rows / 8 * q8c_nbp(cols / 32) / 4 * 1024; }
+CPB_DEV_HOST_INLINE size_t q8c_scale_bytes(int rows, int cols) { return (size_t)rows / 8 * q8c_nbp(cols / 32) / 2 * 64; }
 
 struct AttnLayerDev {
-    const int8_t *wq, *wk, *wv, *wo;    // Q8 tile streams
-    const float *sq, *sk, *sv, *so;     // scales [tile][block][8]
+    const u32x4 *wq, *wk, *wv, *wo;     // chain-major Q8 codes
+    const float *sq, *sk, *sv, *so;     // scales [tile][step][8][2]
     const float *bq, *bk, *bv, *bo, *sinks, *norm;
 };
 
 struct AttnArgs {
-    int d, nh, nkv, nb, nbo, pos, start, max_seq;
+    int d, nh, nkv, nb, nbo, pos, start, max_seq, nsplit;
     float eps;
     AttnLayerDev L;
     float* x;            // [d] residual (in place)
-    float* kc;           // this layer's cache [max_seq][nkv][64]
+    float* kc;           // this layer's cache [nkv][max_seq][64]
     float* vc;
     const float* rope;   // [max_seq][32][2]
-    int8_t* xq;          // [d]
-    float* xsb;          // [d/32]
     float* q;            // [nh*64]
     float* ao;           // [nh*64]
     int8_t* aq;          // [nh*64]
     float* asb;          // [nh*64/32]
+    int8_t* xq;          // [d] (trace copy of the activations)
+    float* xsb;          // [d/32]
+    float* part;         // [nh][nsplit][66]: max, sum, 64 weighted values
+    int* count;          // [nkv] arrivals of the core workgroups (0 between launches)
 };
 
-// ---- load time: Q8Mat::from_bf16 into the 8-row tile stream ----
-__global__ void k_q8_tiles(const uint16_t* __restrict__ w, int rows, int cols, int8_t* __restrict__ q,
-                           float* __restrict__ s) {
-    const int nb = cols / 32;
+// ---- load time: Q8Mat::from_bf16 (:476-489) into the chain-major stream ----
+// one thread per (row, block); the stream must be zeroed beforehand (padding)
+__global__ void k_q8c_quant(const uint16_t* __restrict__ w, int rows, int cols, u32x4* __restrict__ q,
+                            float* __restrict__ s) {
+    const int nb = cols / 32, nbp = q8c_nbp(nb), nsp = nbp / 4, ns = nbp / 2;
     const size_t total = (size_t)rows * nb;
     for (size_t idx = blockIdx.x * (size_t)blockDim.x + threadIdx.x; idx < total; idx += (size_t)gridDim.x * blockDim.x) {
         const int row = (int)(idx / nb), b = (int)(idx % nb);
@@ -70,8 +116,6 @@ __global__ void k_q8_tiles(const uint16_t* __restrict__ w, int rows, int cols, i
             amax = fmaxf(amax, fabsf(vals[i]));
         }
         const float sc = amax / 127.0f;
-        const size_t tb = (size_t)(row / 8) * nb + b;
-        s[tb * 8 + row % 8] = sc;
         uint32_t wd[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
         for (int i = 0; i < 32; i++) {
@@ -79,122 +123,254 @@ __global__ void k_q8_tiles(const uint16_t* __restrict__ w, int rows, int cols, i
             r = r < -127.0f ? -127.0f : r > 127.0f ? 127.0f : r;
             wd[i >> 2] |= (uint32_t)(uint8_t)(int8_t)r << (8 * (i & 3));
         }
-        uint32_t* dst = (uint32_t*)(q + tb * 256 + (row % 8) * 32);
+        const int tile = row >> 3, r = row & 7, h = b & 1, st = b >> 1, sp = st >> 1, k = st & 1;
+        s[(((size_t)tile * ns + st) * 8 + r) * 2 + h] = sc;
+        uint32_t* base = (uint32_t*)(q + ((size_t)tile * nsp + sp) * 64 + r * 8 + h * 4);
 #pragma unroll
-        for (int k = 0; k < 8; k++) dst[k] = wd[k];
+        for (int j = 0; j < 4; j++) {
+            base[j * 4 + k * 2] = wd[j];            // lane 8r + 4h + j: bytes 4j..4j+3
+            base[j * 4 + k * 2 + 1] = wd[4 + j];    // and 16+4j..16+4j+3
+        }
     }
 }
 
-// dot_q8_i8 (:169-191) of tile row r (lane >> 3) against activations xl / sl
-// (LDS): lane chain c = lane & 7 -> accumulator h = c >> 2 (even / odd
-// blocks, an odd last block into the first), lane part j = c & 3; returns
-// the row's value in every lane of its group of 8.
-CPB_DEV float q8_tile_dot(const int8_t* __restrict__ w, const float* __restrict__ s, int tile, int nb,
-                          const uint32_t* xl, const float* sl) {
+// ---- staging of 8-row tiles into LDS ----
+// A workgroup copies the codes and scales of its (one or two) tiles to LDS
+// with every thread's 16-byte loads issued before any is waited for, so the
+// whole tile stream is in flight at once; the chains then run from LDS.
+constexpr int kStageBatch = 16;       // 16-byte loads per thread per batch (x 256 threads)
+struct TileSet {
+    const u32x4* w[2];
+    const float* s[2];
+    int nt, nsp;                      // tiles, step pairs per tile
+};
+struct StageRegs {
+    u32x4 r[kStageBatch];
+    float4 sc[2];
+};
+CPB_DEV void stage_issue(const TileSet& t, int b0, StageRegs& g, bool scales) {
+    const int per = t.nsp * 64, total = t.nt * per, tid = threadIdx.x;
+#pragma unroll
+    for (int k = 0; k < kStageBatch; k++) {
+        const int i = b0 + k * 256 + tid;
+        if (i < total) {
+            const int ti = i >= per;
+            g.r[k] = __builtin_nontemporal_load(t.w[ti] + (i - ti * per));
+        }
+    }
+    if (scales) {
+        const int sper = t.nsp * 2 * 4, stotal = t.nt * sper;     // float4 per tile: ns * 16 / 4
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            const int i = k * 256 + tid;
+            if (i < stotal) {
+                const int ti = i >= sper;
+                g.sc[k] = ((const float4*)t.s[ti])[i - ti * sper];
+            }
+        }
+    }
+}
+CPB_DEV void stage_commit(const TileSet& t, int b0, const StageRegs& g, bool scales, u32x4* lw, float* ls) {
+    const int per = t.nsp * 64, total = t.nt * per, tid = threadIdx.x;
+#pragma unroll
+    for (int k = 0; k < kStageBatch; k++) {
+        const int i = b0 + k * 256 + tid;
+        if (i < total) lw[i] = g.r[k];
+    }
+    if (scales) {
+        const int stotal = t.nt * t.nsp * 8;
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            const int i = k * 256 + tid;
+            if (i < stotal) ((float4*)ls)[i] = g.sc[k];
+        }
+    }
+}
+// copy the tiles' stream to LDS; `between` runs while the first batch is in
+// flight.  The scales (nt * nsp * 8 float4) come with the first batch: at
+// most 512 float4, which d <= 4096 (qkv: 2 tiles, nsp <= 32) and n_head <= 128
+// (o-proj: 1 tile, nsp <= 64) keep.
+template <class F>
+CPB_DEV void stage_tiles(const TileSet& t, u32x4* lw, float* ls, F between) {
+    StageRegs g;
+    stage_issue(t, 0, g, true);
+    between();
+    stage_commit(t, 0, g, true, lw, ls);
+    const int total = t.nt * t.nsp * 64;
+    for (int b0 = kStageBatch * 256; b0 < total; b0 += kStageBatch * 256) {
+        stage_issue(t, b0, g, false);
+        stage_commit(t, b0, g, false, lw, ls);
+    }
+}
+
+// The chain of this lane over one 8-row tile staged in LDS (codes lw, scales
+// ls), activations in LDS (xl: dwords, 8 per block; sl: scales; both padded
+// to q8c_nbp blocks with zeros).  Returns the row's dot_q8_i8 in lane 0 of
+// the row's group of 8.
+CPB_DEV float q8c_dot(const u32x4* lw, const float* ls, int nbp, const uint32_t* xl, const float* sl) {
     const int lane = threadIdx.x & 63, r = lane >> 3, h = (lane >> 2) & 1, j = lane & 3;
-    const int8_t* wt = w + (size_t)tile * nb * 256 + r * 32 + 4 * j;
-    const float* st = s + (size_t)tile * nb * 8 + r;
-    const int nbe = nb & ~1;
+    const int nsp = nbp / 4;
+    const float* lsl = ls + r * 2 + h;
     float acc = 0.0f;
 #pragma unroll 4
-    for (int b = h; b < nbe; b += 2) {
-        const uint32_t w0 = *(const uint32_t*)(wt + (size_t)b * 256), w1 = *(const uint32_t*)(wt + (size_t)b * 256 + 16);
-        const int t = sdot4(w1, xl[b * 8 + 4 + j], sdot4(w0, xl[b * 8 + j], 0));
-        acc = fmaf((float)t, st[(size_t)b * 8] * sl[b], acc);
-    }
-    if ((nb & 1) && h == 0) {
-        const int b = nb - 1;
-        const uint32_t w0 = *(const uint32_t*)(wt + (size_t)b * 256), w1 = *(const uint32_t*)(wt + (size_t)b * 256 + 16);
-        const int t = sdot4(w1, xl[b * 8 + 4 + j], sdot4(w0, xl[b * 8 + j], 0));
-        acc = fmaf((float)t, st[(size_t)b * 8] * sl[b], acc);
-    }
-    const float v = acc + __shfl_xor(acc, 4);            // v_j = acc0_j + acc1_j
-    const float v01 = v + __shfl_xor(v, 1);              // j = 0, 1: v0 + v1; j = 2, 3: v2 + v3
-    const int g = lane & ~7;
-    return __shfl(v01, g) + __shfl(v01, g + 2);
-}
-
-// activations (xq as dwords, scales) into LDS
-CPB_DEV void stage_act(const int8_t* xq, const float* xsb, int nb, uint32_t* xl, float* sl) {
-    for (int i = threadIdx.x; i < nb * 8; i += blockDim.x) xl[i] = ((const uint32_t*)xq)[i];
-    for (int i = threadIdx.x; i < nb; i += blockDim.x) sl[i] = xsb[i];
-    __syncthreads();
-}
-
-// ---- rmsnorm + Q8 of x ----
-__global__ __launch_bounds__(256) void k_attn_norm(AttnArgs a) {
-    extern __shared__ __align__(16) unsigned char smem[];
-    float* xs = (float*)smem;
-    float* xnl = xs + a.d;
-    float* scratch = xnl + a.d;
-    norm_into(a.x, a.L.norm, a.d, a.eps, 0, 0, 1, xs, xnl, scratch);
-    const int l = threadIdx.x & 31;
-    for (int bk = threadIdx.x >> 5; bk < a.nb; bk += blockDim.x >> 5) {
-        const float v = xnl[bk * 32 + l];
-        float m = fabsf(v);
+    for (int sp = 0; sp < nsp; sp++) {
+        const u32x4 w = lw[sp * 64 + lane];
 #pragma unroll
-        for (int s2 = 16; s2 >= 1; s2 >>= 1) m = fmaxf(m, __shfl_xor(m, s2));
-        const float sc = fmaxf(1e-12f, m) / 127.0f;
-        a.xq[bk * 32 + l] = (int8_t)q8_round(v, sc);
-        if (l == 0) a.xsb[bk] = sc;
+        for (int t = 0; t < 2; t++) {
+            const int b = 2 * (2 * sp + t) + h;
+            const int dot = sdot4(w[2 * t + 1], xl[b * 8 + 4 + j], sdot4(w[2 * t], xl[b * 8 + j], 0));
+            acc = fmaf((float)dot, lsl[(2 * sp + t) * 16] * sl[b], acc);
+        }
+    }
+    // lanes 0-3 of each group of 8: v_j = acc0_j + acc1_j (lane + 4: row_ror by 12)
+    const float v = acc + dppf<0x12C>(acc);
+    const float v01 = v + dppf<0xB1>(v);                 // lane 0: v0 + v1, lane 2: v2 + v3
+    return v01 + dppf<0x4E>(v01);                        // lane 0 of the group: (v0 + v1) + (v2 + v3)
+}
+
+// rmsnorm of x (gpt-oss: 16 fp32 chains over x[16m + q], :710-726) and Q8
+// per 32 (qblock32 :691-699) into LDS: xl dwords / sl scales, padded with
+// zeros to nbp blocks.  xs / ws: x and the norm weights, already in LDS (the
+// barrier at entry publishes them); red: 17 floats.
+CPB_DEV void attn_norm_q8(int d, int nb, int nbp, float eps, const float* xs, const float* ws, float* red, uint32_t* xl,
+                          float* sl, int8_t* gxq, float* gxsb) {
+    const int tid = threadIdx.x;
+    __syncthreads();
+    if (tid < 16) {
+        float acc = 0.0f;
+        const int n16 = d / 16;
+        int m = 0;
+        for (; m + 8 <= n16; m += 8) {
+            float t[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) t[u] = xs[(m + u) * 16 + tid];
+#pragma unroll
+            for (int u = 0; u < 8; u++) acc = fmaf(t[u], t[u], acc);
+        }
+        for (; m < n16; m++) { const float t = xs[m * 16 + tid]; acc = fmaf(t, t, acc); }
+        red[tid] = acc;                                   // chain q = 4v + l
+    }
+    __syncthreads();
+    if (tid == 0) {
+        float L[4];
+        for (int l = 0; l < 4; l++) L[l] = (red[l] + red[4 + l]) + (red[8 + l] + red[12 + l]);
+        float sq = (L[0] + L[1]) + (L[2] + L[3]);
+        for (int i = d - d % 16; i < d; i++) sq += xs[i] * xs[i];
+        red[16] = 1.0f / sqrtf(sq / (float)d + eps);
+    }
+    __syncthreads();
+    const float inv = red[16];
+    // Q8: 4 lanes per block, 8 values each (bytes 8q .. 8q + 7 = dwords 2q, 2q + 1)
+    for (int e = tid; e < nbp * 4; e += 256) {
+        const int bk = e >> 2, q = e & 3;
+        if (bk < nb) {
+            const int o4 = bk * 8 + 2 * q;
+            const float4 x0 = ((const float4*)xs)[o4], x1 = ((const float4*)xs)[o4 + 1];
+            const float4 w0 = ((const float4*)ws)[o4], w1 = ((const float4*)ws)[o4 + 1];
+            const float v[8] = {x0.x * inv * w0.x, x0.y * inv * w0.y, x0.z * inv * w0.z, x0.w * inv * w0.w,
+                                x1.x * inv * w1.x, x1.y * inv * w1.y, x1.z * inv * w1.z, x1.w * inv * w1.w};
+            float m = 0.0f;
+#pragma unroll
+            for (int u = 0; u < 8; u++) m = fmaxf(m, fabsf(v[u]));
+            m = fmaxf(m, dppf<0xB1>(m));
+            m = fmaxf(m, dppf<0x4E>(m));
+            const float sc = fmaxf(1e-12f, m) / 127.0f;
+            uint32_t wd[2] = {0u, 0u};
+#pragma unroll
+            for (int u = 0; u < 8; u++) wd[u >> 2] |= (uint32_t)(uint8_t)q8_round(v[u], sc) << (8 * (u & 3));
+            xl[bk * 8 + 2 * q] = wd[0];
+            xl[bk * 8 + 2 * q + 1] = wd[1];
+            if (q == 0) sl[bk] = sc;
+            if (gxq) {
+                ((uint2*)gxq)[bk * 4 + q] = make_uint2(wd[0], wd[1]);
+                if (q == 0) gxsb[bk] = sc;
+            }
+        } else {
+            xl[bk * 8 + 2 * q] = 0u;
+            xl[bk * 8 + 2 * q + 1] = 0u;
+            if (q == 0) sl[bk] = 0.0f;
+        }
     }
 }
 
-// ---- q / k / v rows + bias + RoPE + cache ----
-// one wavefront per 8 rows {i, 32 + i} (i in [4g, 4g + 4)) of one head, so
-// each RoPE pair is in the wave; grid: (nh + 2 nkv) * 8.
-__global__ __launch_bounds__(64) void k_attn_qkv(AttnArgs a) {
+// ---- rmsnorm + Q8 of x, q / k / v rows + bias + RoPE + cache ----
+// 256 threads, two 8-row tiles of one head: rows 8k + [0, 8) (wave 0) and
+// 32 + 8k + [0, 8) (wave 1), so each RoPE pair (i, 32 + i) is in the
+// workgroup; grid (nh + 2 nkv) * 4.  Every workgroup normalises x itself
+// (the reference's order, rmsnorm_quant_par :730-738) while its weight loads
+// are in flight.
+__global__ __launch_bounds__(256) void k_attn_qkv(AttnArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
-    uint32_t* xl = (uint32_t*)smem;
-    float* sl = (float*)(xl + a.nb * 8);
-    __shared__ float hv[8];
-    stage_act(a.xq, a.xsb, a.nb, xl, sl);
-    const int head = blockIdx.x >> 3, g = blockIdx.x & 7;
-    const int lane = threadIdx.x, r = lane >> 3;                 // tile row r: head row i or 32 + i
-    const int hrow = (r < 4 ? 4 * g + r : 32 + 4 * g + (r - 4));
-    int kind, hh;                                                // 0 q, 1 k, 2 v
+    const int nbp = q8c_nbp(a.nb), nsp = nbp / 4, ns = nbp / 2;
+    u32x4* lw = (u32x4*)smem;                         // [2][nsp * 64]
+    float* ls = (float*)(lw + 2 * nsp * 64);          // [2][ns * 16]
+    float* xs = ls + 2 * ns * 16;                     // [d]
+    float* ws = xs + a.d;                             // [d]
+    float* red = ws + a.d;                            // [64]
+    uint32_t* xl = (uint32_t*)(red + 64);             // [nbp * 8]
+    float* sl = (float*)(xl + nbp * 8);               // [nbp]
+    __shared__ float hv[16];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    // x and the norm weights first: the norm waits for them, not for the tiles
+    float4 xr[4], wr[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int i4 = (tid + k * 256) * 4 < a.d ? tid + k * 256 : 0;
+        xr[k] = ((const float4*)a.x)[i4];
+        wr[k] = ((const float4*)a.L.norm)[i4];
+    }
+    const int head = blockIdx.x >> 2, k = blockIdx.x & 3;
+    int kind, hh;                                     // 0 q, 1 k, 2 v
     if (head < a.nh) { kind = 0; hh = head; }
     else if (head < a.nh + a.nkv) { kind = 1; hh = head - a.nh; }
     else { kind = 2; hh = head - a.nh - a.nkv; }
-    const int8_t* W = kind == 0 ? a.L.wq : kind == 1 ? a.L.wk : a.L.wv;
+    const u32x4* W = kind == 0 ? a.L.wq : kind == 1 ? a.L.wk : a.L.wv;
     const float* S = kind == 0 ? a.L.sq : kind == 1 ? a.L.sk : a.L.sv;
     const float* B = kind == 0 ? a.L.bq : kind == 1 ? a.L.bk : a.L.bv;
-    const int row = hh * kAttnHd + hrow;
-    // the 8 lanes of tile row r read head row `row` from its own 8-row tile
-    const int tile = row >> 3, tr = row & 7;
-    float v;
+    const int tile0 = hh * 8 + k, tile1 = hh * 8 + 4 + k;
+    // bias of this lane's row and the RoPE entries of pair 8k + tid, also up front
+    const float bias = B[(wave ? tile1 : tile0) * 8 + ((lane >> 3) & 7)];
+    const int ri = 8 * k + (tid & 7);
+    const float rc = a.rope[((size_t)a.pos * 32 + ri) * 2], rs = a.rope[((size_t)a.pos * 32 + ri) * 2 + 1];
+    TileSet ts;
+    ts.w[0] = W + (size_t)tile0 * nsp * 64;
+    ts.w[1] = W + (size_t)tile1 * nsp * 64;
+    ts.s[0] = S + (size_t)tile0 * ns * 16;
+    ts.s[1] = S + (size_t)tile1 * ns * 16;
+    ts.nt = 2;
+    ts.nsp = nsp;
     {
-        const int h = (lane >> 2) & 1, j = lane & 3;
-        const int8_t* wt = W + (size_t)tile * a.nb * 256 + tr * 32 + 4 * j;
-        const float* st = S + (size_t)tile * a.nb * 8 + tr;
-        const int nb = a.nb, nbe = nb & ~1;
-        float acc = 0.0f;
-#pragma unroll 4
-        for (int b = h; b < nbe; b += 2) {
-            const uint32_t w0 = *(const uint32_t*)(wt + (size_t)b * 256), w1 = *(const uint32_t*)(wt + (size_t)b * 256 + 16);
-            const int t = sdot4(w1, xl[b * 8 + 4 + j], sdot4(w0, xl[b * 8 + j], 0));
-            acc = fmaf((float)t, st[(size_t)b * 8] * sl[b], acc);
+        StageRegs g;
+        stage_issue(ts, 0, g, true);
+#pragma unroll
+        for (int k4 = 0; k4 < 4; k4++)
+            if ((tid + k4 * 256) * 4 < a.d) {
+                ((float4*)xs)[tid + k4 * 256] = xr[k4];
+                ((float4*)ws)[tid + k4 * 256] = wr[k4];
+            }
+        attn_norm_q8(a.d, a.nb, nbp, a.eps, xs, ws, red, xl, sl, blockIdx.x == 0 ? a.xq : nullptr, a.xsb);
+        stage_commit(ts, 0, g, true, lw, ls);
+        for (int b0 = kStageBatch * 256; b0 < 2 * nsp * 64; b0 += kStageBatch * 256) {
+            stage_issue(ts, b0, g, false);
+            stage_commit(ts, b0, g, false, lw, ls);
         }
-        if ((nb & 1) && h == 0) {
-            const int b = nb - 1;
-            const uint32_t w0 = *(const uint32_t*)(wt + (size_t)b * 256), w1 = *(const uint32_t*)(wt + (size_t)b * 256 + 16);
-            const int t = sdot4(w1, xl[b * 8 + 4 + j], sdot4(w0, xl[b * 8 + j], 0));
-            acc = fmaf((float)t, st[(size_t)b * 8] * sl[b], acc);
-        }
-        const float vv = acc + __shfl_xor(acc, 4);
-        const float v01 = vv + __shfl_xor(vv, 1);
-        const int gl = lane & ~7;
-        v = __shfl(v01, gl) + __shfl(v01, gl + 2);
     }
-    v = v + B[row];                                          // :786-793 dot + bias
-    if ((lane & 7) == 0) hv[r] = v;
     __syncthreads();
-    if (lane >= 4) return;
-    // RoPE pair (i, 32 + i), i = 4g + lane (rope_yarn :578-590); v unrotated
-    const int i = 4 * g + lane;
-    float lo = hv[lane], hi = hv[4 + lane];
+    if (wave < 2) {
+        const float v = q8c_dot(lw + wave * nsp * 64, ls + wave * ns * 16, nbp, xl, sl);
+        if ((lane & 7) == 0) {
+            const int row = (wave ? tile1 : tile0) * 8 + (lane >> 3);
+            hv[wave * 8 + (lane >> 3)] = v + bias;        // :786-793 dot + bias (row)
+            (void)row;
+        }
+    }
+    __syncthreads();
+    if (tid >= 8) return;
+    // RoPE pair (i, 32 + i), i = 8k + tid (rope_yarn :578-590); v unrotated
+    const int i = 8 * k + tid;
+    float lo = hv[tid], hi = hv[8 + tid];
     if (kind != 2) {
-        const float c = a.rope[((size_t)a.pos * 32 + i) * 2], s = a.rope[((size_t)a.pos * 32 + i) * 2 + 1];
+        const float c = rc, s = rs;
         const float nlo = lo * c - hi * s, nhi = hi * c + lo * s;
         lo = nlo;
         hi = nhi;
@@ -203,102 +379,223 @@ __global__ __launch_bounds__(64) void k_attn_qkv(AttnArgs a) {
         a.q[hh * kAttnHd + i] = lo;
         a.q[hh * kAttnHd + 32 + i] = hi;
     } else {
-        float* dst = (kind == 1 ? a.kc : a.vc) + ((size_t)a.pos * a.nkv + hh) * kAttnHd;
+        float* dst = (kind == 1 ? a.kc : a.vc) + ((size_t)hh * a.max_seq + a.pos) * kAttnHd;
         dst[i] = lo;
         dst[32 + i] = hi;
     }
 }
 
-// ---- per q-head: scores, softmax with the sink, weighted v, Q8 ----
-__global__ __launch_bounds__(256) void k_attn_core(AttnArgs a) {
-    extern __shared__ __align__(16) unsigned char smem[];
-    float* sc = (float*)smem;                                    // [n]
-    __shared__ float qs[kAttnHd];
-    __shared__ float red[256];
-    __shared__ float part[4][kAttnHd];
-    const int h = blockIdx.x, tid = threadIdx.x;
-    const int kvh = h / (a.nh / a.nkv);
-    const int n = a.pos - a.start + 1;
-    if (tid < kAttnHd) qs[tid] = a.q[h * kAttnHd + tid];
-    __syncthreads();
-    // scores (:810-820): lane-parallel fmas in 4 x 4 accumulators over steps of 16
-    for (int t = tid; t < n; t += blockDim.x) {
-        const float4* kp = (const float4*)(a.kc + ((size_t)(a.start + t) * a.nkv + kvh) * kAttnHd);
-        float acc[4][4] = {{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
+// ---- attention of one kv-head's q-heads over one chunk of positions ----
+// grid (nkv, nsplit), chunks of 128 positions (a window of 128 is one
+// chunk); wave w runs q-heads w and w + 4 of the group, lane l positions l
+// and l + 64.  With several chunks each workgroup leaves (max, sum, weighted
+// v) per head and the last to arrive for its kv-head merges them with the
+// sink; then the heads' outputs are quantised (qblock32 :691-699).
+__device__ __forceinline__ float score64(const float* kr, const float4 (&qv)[16]) {
+    // :810-820: 4 x 4 fma accumulators over steps of 16, then the fixed tree
+    float4 kk[16];
 #pragma unroll
-        for (int jj = 0; jj < 4; jj++)
+    for (int i = 0; i < 16; i++) kk[i] = *(const float4*)&kr[4 * i];
+    float acc[4][4] = {{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
 #pragma unroll
-            for (int m = 0; m < 4; m++) {
-                const float4 kv = kp[jj * 4 + m];
-                const float* qv = qs + jj * 16 + 4 * m;
-                acc[m][0] = fmaf(kv.x, qv[0], acc[m][0]);
-                acc[m][1] = fmaf(kv.y, qv[1], acc[m][1]);
-                acc[m][2] = fmaf(kv.z, qv[2], acc[m][2]);
-                acc[m][3] = fmaf(kv.w, qv[3], acc[m][3]);
-            }
-        float s4[4];
+    for (int jj = 0; jj < 4; jj++)
 #pragma unroll
-        for (int l = 0; l < 4; l++) s4[l] = (acc[0][l] + acc[1][l]) + (acc[2][l] + acc[3][l]);
-        sc[t] = ((s4[0] + s4[1]) + (s4[2] + s4[3])) * 0.125f;   // 1 / sqrt(64)
-    }
-    __syncthreads();
-    // max over the sink and the scores
-    const float sink = a.L.sinks[h];
-    float m = sink;
-    for (int t = tid; t < n; t += blockDim.x) m = fmaxf(m, sc[t]);
-    red[tid] = m;
-    __syncthreads();
-    for (int s2 = 128; s2 >= 1; s2 >>= 1) {
-        if (tid < s2) red[tid] = fmaxf(red[tid], red[tid + s2]);
-        __syncthreads();
-    }
-    const float mx = red[0];
-    __syncthreads();
-    // weights and their sum (fixed-order tree), sink term first
-    float ps = 0.0f;
-    for (int t = tid; t < n; t += blockDim.x) {
-        const float e = expf(sc[t] - mx);
-        sc[t] = e;
-        ps += e;
-    }
-    red[tid] = ps;
-    __syncthreads();
-    for (int s2 = 128; s2 >= 1; s2 >>= 1) {
-        if (tid < s2) red[tid] += red[tid + s2];
-        __syncthreads();
-    }
-    const float den = expf(sink - mx) + red[0];
-    // ao[u] = sum_t e_t v_t[u] / den: 4 position groups per dimension
-    const int u = tid & 63, grp = tid >> 6;
-    float acc = 0.0f;
-    for (int t = grp; t < n; t += 4) acc = fmaf(a.vc[((size_t)(a.start + t) * a.nkv + kvh) * kAttnHd + u], sc[t], acc);
-    part[grp][u] = acc;
-    __syncthreads();
-    if (tid >= 64) return;
-    const float o = ((part[0][u] + part[1][u]) + (part[2][u] + part[3][u])) * (1.0f / den);
-    a.ao[h * kAttnHd + u] = o;
-    // qblock32 (:691-699) of the head's two blocks
-    float mb = fabsf(o);
+        for (int m = 0; m < 4; m++) {
+            const float4 kv = kk[jj * 4 + m];
+            const float4 q4 = qv[jj * 4 + m];
+            acc[m][0] = fmaf(kv.x, q4.x, acc[m][0]);
+            acc[m][1] = fmaf(kv.y, q4.y, acc[m][1]);
+            acc[m][2] = fmaf(kv.z, q4.z, acc[m][2]);
+            acc[m][3] = fmaf(kv.w, q4.w, acc[m][3]);
+        }
+    float s4[4];
 #pragma unroll
-    for (int s2 = 16; s2 >= 1; s2 >>= 1) mb = fmaxf(mb, __shfl_xor(mb, s2));
-    const float scq = fmaxf(1e-12f, mb) / 127.0f;
-    a.aq[h * kAttnHd + u] = (int8_t)q8_round(o, scq);
-    if ((u & 31) == 0) a.asb[h * 2 + (u >> 5)] = scq;
+    for (int l = 0; l < 4; l++) s4[l] = (acc[0][l] + acc[1][l]) + (acc[2][l] + acc[3][l]);
+    return ((s4[0] + s4[1]) + (s4[2] + s4[3])) * 0.125f;     // 1 / sqrt(64)
 }
 
-// ---- x[r] += wo[r] . ao + bo[r] (:837) ----
-__global__ __launch_bounds__(64) void k_attn_oproj(AttnArgs a) {
-    extern __shared__ __align__(16) unsigned char smem[];
-    uint32_t* xl = (uint32_t*)smem;
-    float* sl = (float*)(xl + a.nbo * 8);
-    stage_act(a.aq, a.asb, a.nbo, xl, sl);
-    const int tile = blockIdx.x;
-    const float v = q8_tile_dot(a.L.wo, a.L.so, tile, a.nbo, xl, sl);
-    const int lane = threadIdx.x;
-    if ((lane & 7) == 0) {
-        const int row = tile * 8 + (lane >> 3);
-        a.x[row] += v + a.L.bo[row];
+CPB_DEV void wave_sync_lds() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__global__ __launch_bounds__(256) void k_attn_core(AttnArgs a) {
+    __shared__ __align__(16) float ks[kAttnChunk][68];
+    __shared__ __align__(16) float vs[kAttnHd][kAttnChunk + 4];    // transposed: [dimension][position]
+    __shared__ __align__(16) float qs[kAttnMaxGroup][kAttnHd];
+    __shared__ __align__(16) float es[kAttnMaxGroup][kAttnChunk];
+    __shared__ int last;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int kvh = blockIdx.x, split = blockIdx.y, R = a.nh / a.nkv;
+    const int p0 = a.start + split * kAttnChunk;
+    const int cnt = min(kAttnChunk, a.pos + 1 - p0);
+    const float* kb = a.kc + ((size_t)kvh * a.max_seq + p0) * kAttnHd;
+    const float* vb = a.vc + ((size_t)kvh * a.max_seq + p0) * kAttnHd;
+    constexpr int kIt = kAttnChunk * 16 / 256;
+    float sinkr[2];
+#pragma unroll
+    for (int t = 0; t < 2; t++) sinkr[t] = (wave + 4 * t < R) ? a.L.sinks[kvh * R + wave + 4 * t] : 0.0f;
+    {
+        float4 kr[kIt], vr[kIt];
+        float2 qr;
+#pragma unroll
+        for (int it = 0; it < kIt; it++) {
+            const int e = it * 256 + tid, p = e >> 4, c = e & 15;
+            const int pc = p < cnt ? p : 0;               // rows past the chunk: loaded, not stored
+            kr[it] = *(const float4*)(kb + pc * kAttnHd + c * 4);
+            vr[it] = *(const float4*)(vb + pc * kAttnHd + c * 4);
+        }
+        const int qe = (2 * tid < R * kAttnHd) ? 2 * tid : 0;
+        qr = *(const float2*)(a.q + kvh * R * kAttnHd + qe);
+        if (2 * tid < R * kAttnHd) *(float2*)(&qs[0][0] + 2 * tid) = qr;
+#pragma unroll
+        for (int it = 0; it < kIt; it++) {
+            const int e = it * 256 + tid, p = e >> 4, c = e & 15;
+            if (p < cnt) {
+                *(float4*)&ks[p][c * 4] = kr[it];
+                vs[c * 4][p] = vr[it].x;
+                vs[c * 4 + 1][p] = vr[it].y;
+                vs[c * 4 + 2][p] = vr[it].z;
+                vs[c * 4 + 3][p] = vr[it].w;
+            }
+        }
     }
+    __syncthreads();
+    for (int hl = wave, t = 0; hl < R; hl += 4, t++) {
+        const int h = kvh * R + hl;
+        float4 qv[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) qv[i] = *(const float4*)&qs[hl][4 * i];
+        const float s0 = lane < cnt ? score64(ks[lane], qv) : -INFINITY;
+        const float s1 = lane + 64 < cnt ? score64(ks[lane + 64], qv) : -INFINITY;
+        float m = wave_max_f32(fmaxf(s0, s1));
+        if (a.nsplit == 1) m = fmaxf(m, sinkr[t]);       // one chunk: the sink joins the max here
+        const float e0 = lane < cnt ? expf(s0 - m) : 0.0f;
+        const float e1 = lane + 64 < cnt ? expf(s1 - m) : 0.0f;
+        const float sum = wave_sum_f32(e0 + e1);
+        es[hl][lane] = e0;
+        es[hl][lane + 64] = e1;
+        wave_sync_lds();
+        // weighted v, dimension lane: 4 positions per pair of 16-byte reads
+        float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        int p = 0;
+        for (; p + 4 <= cnt; p += 4) {
+            const float4 vv = *(const float4*)&vs[lane][p];
+            const float4 ee = *(const float4*)&es[hl][p];
+            o[0] = fmaf(vv.x, ee.x, o[0]);
+            o[1] = fmaf(vv.y, ee.y, o[1]);
+            o[2] = fmaf(vv.z, ee.z, o[2]);
+            o[3] = fmaf(vv.w, ee.w, o[3]);
+        }
+        for (; p < cnt; p++) o[0] = fmaf(vs[lane][p], es[hl][p], o[0]);
+        const float ov = (o[0] + o[1]) + (o[2] + o[3]);
+        if (a.nsplit == 1) {
+            // softmax with the sink in the denominator, then Q8 of the head
+            const float val = ov / (expf(sinkr[t] - m) + sum);
+            a.ao[h * kAttnHd + lane] = val;
+            const float mb = half_max_f32(fabsf(val));
+            const float scq = fmaxf(1e-12f, mb) / 127.0f;
+            a.aq[h * kAttnHd + lane] = (int8_t)q8_round(val, scq);
+            if ((lane & 31) == 0) a.asb[h * 2 + (lane >> 5)] = scq;
+        } else {
+            // coherent (write-through) stores: read by another workgroup of this launch
+            float* pp = a.part + ((size_t)h * a.nsplit + split) * 66;
+            st_dev(pp + 2 + lane, ov);
+            if (lane == 0) {
+                st_dev(pp, m);
+                st_dev(pp + 1, sum);
+            }
+        }
+    }
+    if (a.nsplit == 1) return;
+    // arrival: the last workgroup of this kv-head merges.  Each wave waits for
+    // its stores to complete before the barrier; the counter is then bumped.
+    drain_memory();
+    __syncthreads();
+    if (tid == 0) {
+        const int prev = __hip_atomic_fetch_add(a.count + kvh, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last = prev == a.nsplit - 1;
+        if (last) __hip_atomic_store(a.count + kvh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!last) return;
+    // the chunks' partials: coherent loads (they bypass this CU's and this
+    // XCD's caches, which may hold older values)
+    for (int hl = wave, t = 0; hl < R; hl += 4, t++) {
+        const int h = kvh * R + hl;
+        const float* pp = a.part + (size_t)h * a.nsplit * 66;
+        const float sink = sinkr[t];
+        float M = sink;
+        for (int i0 = 0; i0 < a.nsplit; i0 += 64)
+            if (i0 + lane < a.nsplit) M = fmaxf(M, ld_dev(pp + (i0 + lane) * 66));
+        M = wave_max_f32(M);
+        float den = 0.0f, acc = 0.0f;
+        for (int i0 = 0; i0 < a.nsplit; i0 += 64) {
+            const int i = i0 + lane;
+            const float f = i < a.nsplit ? expf(ld_dev(pp + i * 66) - M) : 0.0f;
+            if (i < a.nsplit) den = fmaf(ld_dev(pp + i * 66 + 1), f, den);
+            es[hl][lane] = f;
+            wave_sync_lds();
+            // weighted merge of the chunks' values, dimension lane
+            float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            const int n = min(64, a.nsplit - i0);
+            int c = 0;
+            for (; c + 4 <= n; c += 4) {
+#pragma unroll
+                for (int q = 0; q < 4; q++) o[q] = fmaf(ld_dev(pp + (i0 + c + q) * 66 + 2 + lane), es[hl][c + q], o[q]);
+            }
+            for (; c < n; c++) o[0] = fmaf(ld_dev(pp + (i0 + c) * 66 + 2 + lane), es[hl][c], o[0]);
+            acc += (o[0] + o[1]) + (o[2] + o[3]);
+            wave_sync_lds();
+        }
+        den = wave_sum_f32(den);
+        den += expf(sink - M);
+        const float val = acc / den;
+        a.ao[h * kAttnHd + lane] = val;
+        const float mb = half_max_f32(fabsf(val));
+        const float scq = fmaxf(1e-12f, mb) / 127.0f;
+        a.aq[h * kAttnHd + lane] = (int8_t)q8_round(val, scq);
+        if ((lane & 31) == 0) a.asb[h * 2 + (lane >> 5)] = scq;
+    }
+}
+
+// ---- x[r] += wo[r] . ao + bo[r] (:837), one 8-row tile per workgroup ----
+__global__ __launch_bounds__(256) void k_attn_oproj(AttnArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int nbp = q8c_nbp(a.nbo), nsp = nbp / 4, ns = nbp / 2;
+    u32x4* lw = (u32x4*)smem;                         // [nsp * 64]
+    float* ls = (float*)(lw + nsp * 64);              // [ns * 16]
+    uint32_t* xl = (uint32_t*)(ls + ns * 16);         // [nbp * 8]
+    float* sl = (float*)(xl + nbp * 8);               // [nbp]
+    const int tile = blockIdx.x, tid = threadIdx.x;
+    // activations, bias and the residual rows first (nbo <= 256: 8 dwords a thread)
+    uint32_t ar[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const int i = tid + k * 256;
+        ar[k] = i < a.nbo * 8 ? ((const uint32_t*)a.aq)[i] : 0u;
+    }
+    const float as = tid < a.nbo ? a.asb[tid] : 0.0f;
+    const int row = tile * 8 + ((tid >> 3) & 7);
+    const float bo = a.L.bo[row], xo = a.x[row];
+    TileSet ts;
+    ts.w[0] = ts.w[1] = a.L.wo + (size_t)tile * nsp * 64;
+    ts.s[0] = ts.s[1] = a.L.so + (size_t)tile * ns * 16;
+    ts.nt = 1;
+    ts.nsp = nsp;
+    stage_tiles(ts, lw, ls, [&] {
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const int i = tid + k * 256;
+            if (i < nbp * 8) xl[i] = ar[k];
+        }
+        if (tid < nbp) sl[tid] = as;
+    });
+    __syncthreads();
+    if (tid >= 64) return;
+    const float v = q8c_dot(lw, ls, nbp, xl, sl);
+    if ((tid & 7) == 0) a.x[row] = xo + (v + bo);
 }
 
 }  // namespace cpb
@@ -314,6 +611,9 @@ struct cpb_attn {
     std::vector<bool> loaded;
     float *kc = nullptr, *vc = nullptr, *rope = nullptr, *x = nullptr;
     int8_t *xq = nullptr, *aq = nullptr;
+    float* part = nullptr;
+    int* count = nullptr;
+    int max_split = 1;
     float *xsb = nullptr, *q = nullptr, *ao = nullptr, *asb = nullptr;
 };
 
@@ -333,6 +633,10 @@ int attn_check(const cpb_attn_cfg* c) {
     if (c->d <= 0 || c->d % 32 || c->d > 4096) return fail(CPB_EINVAL, "d=%d must be a multiple of 32, <= 4096", c->d);
     if (c->n_head <= 0 || c->n_head_kv <= 0 || c->n_head % c->n_head_kv)
         return fail(CPB_EINVAL, "n_head=%d must be a positive multiple of n_head_kv=%d", c->n_head, c->n_head_kv);
+    if (c->n_head / c->n_head_kv > cpb::kAttnMaxGroup)
+        return fail(CPB_EINVAL, "n_head / n_head_kv = %d: at most %d q-heads per kv-head", c->n_head / c->n_head_kv,
+                    cpb::kAttnMaxGroup);
+    if (c->n_head > 128) return fail(CPB_EINVAL, "n_head=%d: at most 128", c->n_head);
     if (c->n_layer <= 0 || c->max_seq <= 0 || c->max_seq > 8192) return fail(CPB_EINVAL, "bad n_layer / max_seq (<= 8192)");
     if (c->sliding_window < 1) return fail(CPB_EINVAL, "sliding_window must be >= 1");
     return 0;
@@ -374,7 +678,7 @@ void cpb_attn_destroy(cpb_attn_t* h) {
     if (h->stream) hipStreamSynchronize(h->stream);
     for (void* p : h->layer_mem)
         if (p) hipFree(p);
-    void* bufs[] = {h->kc, h->vc, h->rope, h->x, h->xq, h->aq, h->xsb, h->q, h->ao, h->asb};
+    void* bufs[] = {h->kc, h->vc, h->rope, h->x, h->xq, h->aq, h->xsb, h->q, h->ao, h->asb, h->part, h->count};
     for (void* p : bufs)
         if (p) hipFree(p);
     if (h->own) hipStreamDestroy(h->own);
@@ -392,6 +696,7 @@ int cpb_attn_create(const cpb_attn_cfg* cfg, int device, cpb_attn_t** out) {
     cpb_attn_t* h = new cpb_attn_t();
     h->cfg = *cfg;
     h->device = device;
+    h->max_split = (cfg->max_seq + cpb::kAttnChunk - 1) / cpb::kAttnChunk;
     h->layers.resize(cfg->n_layer);
     h->layer_mem.assign(cfg->n_layer, nullptr);
     h->loaded.assign(cfg->n_layer, false);
@@ -408,12 +713,24 @@ int cpb_attn_create(const cpb_attn_cfg* cfg, int device, cpb_attn_t** out) {
     if ((r = dm((void**)&h->kc, cache)) || (r = dm((void**)&h->vc, cache)) ||
         (r = dm((void**)&h->rope, (size_t)cfg->max_seq * 64 * 4)) || (r = dm((void**)&h->x, d * 4)) ||
         (r = dm((void**)&h->xq, d)) || (r = dm((void**)&h->xsb, d / 32 * 4)) || (r = dm((void**)&h->q, nq * 4)) ||
-        (r = dm((void**)&h->ao, nq * 4)) || (r = dm((void**)&h->aq, nq)) || (r = dm((void**)&h->asb, nq / 32 * 4)))
+        (r = dm((void**)&h->ao, nq * 4)) || (r = dm((void**)&h->aq, nq)) || (r = dm((void**)&h->asb, nq / 32 * 4)) ||
+        (r = dm((void**)&h->part, (size_t)cfg->n_head * h->max_split * 66 * 4)) ||
+        (r = dm((void**)&h->count, (size_t)cfg->n_head_kv * 4)))
         return bail(r);
+    // LDS beyond 64 KiB per workgroup (d = 4096: 110 KiB for k_attn_qkv) is opted into
+    {
+        const int nbp = cpb::q8c_nbp(cfg->d / 32), nbpo = cpb::q8c_nbp(cfg->n_head * 2);
+        const int lq = 2 * (nbp / 4) * 1024 + 2 * (nbp / 2) * 64 + 4 * (2 * cfg->d + 64) + nbp * 36;
+        const int lo = (nbpo / 4) * 1024 + (nbpo / 2) * 64 + nbpo * 36;
+        if (hipFuncSetAttribute((const void*)cpb::k_attn_qkv, hipFuncAttributeMaxDynamicSharedMemorySize, lq) != hipSuccess ||
+            hipFuncSetAttribute((const void*)cpb::k_attn_oproj, hipFuncAttributeMaxDynamicSharedMemorySize, lo) != hipSuccess)
+            return bail(fail(CPB_ENODEV, "LDS attribute (%d / %d bytes) refused", lq, lo));
+    }
     std::vector<float> tab;
     rope_table(64, cfg->max_seq, cfg->rope_base, tab);
     if (hipMemcpy(h->rope, tab.data(), tab.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
         hipMemsetAsync(h->kc, 0, cache, h->stream) != hipSuccess || hipMemsetAsync(h->vc, 0, cache, h->stream) != hipSuccess ||
+        hipMemsetAsync(h->count, 0, (size_t)cfg->n_head_kv * 4, h->stream) != hipSuccess ||
         hipStreamSynchronize(h->stream) != hipSuccess)
         return bail(fail(CPB_ENODEV, "attention init copies failed"));
     *out = h;
@@ -436,9 +753,10 @@ int cpb_attn_load_layer(cpb_attn_t* h, int layer, const float* attn_norm, const 
     const size_t mats[4][2] = {{nq, d}, {nkv, d}, {nkv, d}, {d, nq}};
     size_t off[4][2], o = 0;
     for (int m = 0; m < 4; m++) {
-        off[m][0] = o; o += (mats[m][0] * mats[m][1] + 255) / 256 * 256;
-        off[m][1] = o; o += (mats[m][0] * (mats[m][1] / 32) * 4 + 255) / 256 * 256;
+        off[m][0] = o; o += (cpb::q8c_code_bytes((int)mats[m][0], (int)mats[m][1]) + 255) / 256 * 256;
+        off[m][1] = o; o += (cpb::q8c_scale_bytes((int)mats[m][0], (int)mats[m][1]) + 255) / 256 * 256;
     }
+    const size_t wbytes = o;
     const size_t vec[6] = {d, nq, nkv, nkv, d, (size_t)c.n_head};      // norm, bq, bk, bv, bo, sinks
     size_t voff[6];
     for (int k = 0; k < 6; k++) { voff[k] = o; o += (vec[k] * 4 + 255) / 256 * 256; }
@@ -447,13 +765,14 @@ int cpb_attn_load_layer(cpb_attn_t* h, int layer, const float* attn_norm, const 
     h->layer_mem[layer] = base;
     const uint16_t* srcs[4] = {wq, wk, wv, wo};
     uint16_t* staging = nullptr;
-    hipError_t e = hipMalloc((void**)&staging, nq * d * 2 > d * nq * 2 ? nq * d * 2 : d * nq * 2);
+    hipError_t e = hipMalloc((void**)&staging, nq * d * 2);
+    if (e == hipSuccess) e = hipMemsetAsync(base, 0, wbytes, h->stream);     // block padding
     for (int m = 0; m < 4 && e == hipSuccess; m++) {
         const size_t n = mats[m][0] * mats[m][1];
         e = hipMemcpyAsync(staging, srcs[m], n * 2, hipMemcpyHostToDevice, h->stream);
         if (e == hipSuccess) {
-            hipLaunchKernelGGL(cpb::k_q8_tiles, dim3(4096), dim3(256), 0, h->stream, staging, (int)mats[m][0],
-                               (int)mats[m][1], (int8_t*)(base + off[m][0]), (float*)(base + off[m][1]));
+            hipLaunchKernelGGL(cpb::k_q8c_quant, dim3(4096), dim3(256), 0, h->stream, staging, (int)mats[m][0],
+                               (int)mats[m][1], (cpb::u32x4*)(base + off[m][0]), (float*)(base + off[m][1]));
             e = hipGetLastError();
         }
         if (e == hipSuccess) e = hipStreamSynchronize(h->stream);
@@ -463,10 +782,10 @@ int cpb_attn_load_layer(cpb_attn_t* h, int layer, const float* attn_norm, const 
     for (int k = 0; k < 6 && e == hipSuccess; k++) e = hipMemcpy(base + voff[k], vsrc[k], vec[k] * 4, hipMemcpyHostToDevice);
     if (e != hipSuccess) return fail(CPB_ENODEV, "attention layer load: %s", hipGetErrorString(e));
     cpb::AttnLayerDev& L = h->layers[layer];
-    L.wq = (const int8_t*)(base + off[0][0]); L.sq = (const float*)(base + off[0][1]);
-    L.wk = (const int8_t*)(base + off[1][0]); L.sk = (const float*)(base + off[1][1]);
-    L.wv = (const int8_t*)(base + off[2][0]); L.sv = (const float*)(base + off[2][1]);
-    L.wo = (const int8_t*)(base + off[3][0]); L.so = (const float*)(base + off[3][1]);
+    L.wq = (const cpb::u32x4*)(base + off[0][0]); L.sq = (const float*)(base + off[0][1]);
+    L.wk = (const cpb::u32x4*)(base + off[1][0]); L.sk = (const float*)(base + off[1][1]);
+    L.wv = (const cpb::u32x4*)(base + off[2][0]); L.sv = (const float*)(base + off[2][1]);
+    L.wo = (const cpb::u32x4*)(base + off[3][0]); L.so = (const float*)(base + off[3][1]);
     L.norm = (const float*)(base + voff[0]); L.bq = (const float*)(base + voff[1]);
     L.bk = (const float*)(base + voff[2]); L.bv = (const float*)(base + voff[3]);
     L.bo = (const float*)(base + voff[4]); L.sinks = (const float*)(base + voff[5]);
@@ -481,6 +800,7 @@ static int attn_launch(cpb_attn_t* h, int layer, int pos, float* dx) {
     a.pos = pos; a.max_seq = c.max_seq; a.eps = c.rms_eps;
     // :797 sliding window on layers 0, 2, ... ((il + 1) % 2 != 0)
     a.start = ((layer + 1) % 2 != 0) ? (pos - (c.sliding_window - 1) > 0 ? pos - (c.sliding_window - 1) : 0) : 0;
+    a.nsplit = (pos - a.start + 1 + cpb::kAttnChunk - 1) / cpb::kAttnChunk;
     a.L = h->layers[layer];
     a.x = dx;
     const size_t lc = (size_t)c.max_seq * c.n_head_kv * 64;
@@ -488,10 +808,15 @@ static int attn_launch(cpb_attn_t* h, int layer, int pos, float* dx) {
     a.vc = h->vc + (size_t)layer * lc;
     a.rope = h->rope;
     a.xq = h->xq; a.xsb = h->xsb; a.q = h->q; a.ao = h->ao; a.aq = h->aq; a.asb = h->asb;
-    cpb::launch(cpb::k_attn_norm, dim3(1), dim3(256), sizeof(float) * (2 * c.d + 64), h->stream, a);
-    cpb::launch(cpb::k_attn_qkv, dim3((c.n_head + 2 * c.n_head_kv) * 8), dim3(64), (size_t)a.nb * 36, h->stream, a);
-    cpb::launch(cpb::k_attn_core, dim3(c.n_head), dim3(256), (size_t)(pos - a.start + 1) * 4, h->stream, a);
-    cpb::launch(cpb::k_attn_oproj, dim3(c.d / 8), dim3(64), (size_t)a.nbo * 36, h->stream, a);
+    a.part = h->part; a.count = h->count;
+    const int nbp = cpb::q8c_nbp(a.nb), nbpo = cpb::q8c_nbp(a.nbo);
+    // LDS: two tiles' codes (nbp / 4 step pairs x 1 KiB) and scales (nbp / 2 x 64 B), x, xn, activations
+    const size_t lds_qkv = (size_t)2 * (nbp / 4) * 1024 + (size_t)2 * (nbp / 2) * 64 + sizeof(float) * (2 * c.d + 64) +
+                           (size_t)nbp * 36;     // codes, scales, x, norm weights, 64, activations
+    const size_t lds_o = (size_t)(nbpo / 4) * 1024 + (size_t)(nbpo / 2) * 64 + (size_t)nbpo * 36;
+    cpb::launch(cpb::k_attn_qkv, dim3((c.n_head + 2 * c.n_head_kv) * 4), dim3(256), lds_qkv, h->stream, a);
+    cpb::launch(cpb::k_attn_core, dim3(c.n_head_kv, a.nsplit), dim3(256), 0, h->stream, a);
+    cpb::launch(cpb::k_attn_oproj, dim3(c.d / 8), dim3(256), lds_o, h->stream, a);
     return hipGetLastError() == hipSuccess ? 0 : fail(CPB_ENODEV, "attention launch failed");
 }
 
@@ -523,8 +848,11 @@ int cpb_attn_forward(cpb_attn_t* h, int layer, int pos, float* x, cpb_attn_trace
         r |= cp(tr->xq, h->xq, c.d);
         r |= cp(tr->xsb, h->xsb, c.d / 32 * 4);
         r |= cp(tr->q, h->q, nq * 4);
-        r |= cp(tr->k, h->kc + (size_t)layer * lc + (size_t)pos * nkv, nkv * 4);
-        r |= cp(tr->v, h->vc + (size_t)layer * lc + (size_t)pos * nkv, nkv * 4);
+        // cache rows of pos: one 256-byte row per kv-head ([nkv][max_seq][64])
+        if (tr->k) HIP_OK_A(hipMemcpy2DAsync(tr->k, 256, h->kc + (size_t)layer * lc + (size_t)pos * 64,
+                                             (size_t)c.max_seq * 256, 256, c.n_head_kv, hipMemcpyDeviceToHost, h->stream));
+        if (tr->v) HIP_OK_A(hipMemcpy2DAsync(tr->v, 256, h->vc + (size_t)layer * lc + (size_t)pos * 64,
+                                             (size_t)c.max_seq * 256, 256, c.n_head_kv, hipMemcpyDeviceToHost, h->stream));
         r |= cp(tr->ao, h->ao, nq * 4);
         r |= cp(tr->aq, h->aq, nq);
         r |= cp(tr->asb, h->asb, nq / 32 * 4);

@@ -163,9 +163,38 @@ float orc_q8_row_dot(const int8_t* q, const float* s, const int8_t* xq, const fl
  * Q4 screen values and exact Q8 logits; xq / xsb: the quantised activations.
  * The Q4 rows are quantised here (OpenMP over rows), the Q8 rows only for the
  * candidates. */
+/* Q4Mat of every row (OpenMP over rows): nib [V][d/2], sc [V][d/32] -- the
+ * reference's load-time quantisation (:237-300), for orc_head_pre. */
+void orc_q4_quant_rows(const uint16_t* w, int V, int d, uint8_t* nib, uint16_t* sc) {
+    int nth = orc_get_threads();
+    #pragma omp parallel for schedule(static) num_threads(nth)
+    for (int r = 0; r < V; r++)
+        orc_q4_quant_row(w + (size_t)r * d, d, nib + (size_t)r * (d / 2), sc + (size_t)r * (d / 32));
+}
+
+static void head_impl(const uint16_t* w, const uint8_t* pre_nib, const uint16_t* pre_sc, int V, int d,
+                      const float* x, const float* norm_w, float eps, int nt, int cand, int32_t* cand_ids,
+                      float* cand_screen, float* cand_logits, int8_t* xq_out, float* xsb_out, int32_t* chosen);
+
 void orc_head(const uint16_t* w, int V, int d, const float* x, const float* norm_w, float eps, int nt, int cand,
               int32_t* cand_ids, float* cand_screen, float* cand_logits, int8_t* xq_out, float* xsb_out,
               int32_t* chosen) {
+    head_impl(w, NULL, NULL, V, d, x, norm_w, eps, nt, cand, cand_ids, cand_screen, cand_logits, xq_out, xsb_out,
+              chosen);
+}
+
+/* orc_head with the Q4 rows already quantised (orc_q4_quant_rows): the
+ * per-token work of the reference's head. */
+void orc_head_pre(const uint16_t* w, const uint8_t* nib, const uint16_t* sc, int V, int d, const float* x,
+                  const float* norm_w, float eps, int nt, int cand, int32_t* cand_ids, float* cand_screen,
+                  float* cand_logits, int8_t* xq_out, float* xsb_out, int32_t* chosen) {
+    head_impl(w, nib, sc, V, d, x, norm_w, eps, nt, cand, cand_ids, cand_screen, cand_logits, xq_out, xsb_out,
+              chosen);
+}
+
+static void head_impl(const uint16_t* w, const uint8_t* pre_nib, const uint16_t* pre_sc, int V, int d,
+                      const float* x, const float* norm_w, float eps, int nt, int cand, int32_t* cand_ids,
+                      float* cand_screen, float* cand_logits, int8_t* xq_out, float* xsb_out, int32_t* chosen) {
     int nb = d / 32, nq = V / 4;
     float* xn = (float*)malloc(sizeof(float) * d);
     int8_t* xq = (int8_t*)malloc(d);
@@ -177,10 +206,14 @@ void orc_head(const uint16_t* w, int V, int d, const float* x, const float* norm
     int nth = orc_get_threads();
     #pragma omp parallel for schedule(static) num_threads(nth)
     for (int r = 0; r < V; r++) {
-        uint8_t nib[4096];
-        uint16_t sc[256];
-        orc_q4_quant_row(w + (size_t)r * d, d, nib, sc);
-        screen[r] = orc_q4_row_dot(nib, sc, xq, xsb, nb);
+        if (pre_nib) {
+            screen[r] = orc_q4_row_dot(pre_nib + (size_t)r * (d / 2), pre_sc + (size_t)r * nb, xq, xsb, nb);
+        } else {
+            uint8_t nib[4096];
+            uint16_t sc[256];
+            orc_q4_quant_row(w + (size_t)r * d, d, nib, sc);
+            screen[r] = orc_q4_row_dot(nib, sc, xq, xsb, nb);
+        }
     }
     /* per worker: top-cand of its quads [nq*wid/nt, nq*(wid+1)/nt), insertion
      * with strict comparisons (an equal later value goes behind) */

@@ -114,6 +114,10 @@ float orc_q8_row_dot(const int8_t* q, const float* s, const int8_t* xq, const fl
 void  orc_head(const uint16_t* w, int V, int d, const float* x, const float* norm_w, float eps, int nt, int cand,
                int32_t* cand_ids, float* cand_screen, float* cand_logits, int8_t* xq_out, float* xsb_out,
                int32_t* chosen);
+void  orc_q4_quant_rows(const uint16_t* w, int V, int d, uint8_t* nib, uint16_t* sc);
+void  orc_head_pre(const uint16_t* w, const uint8_t* nib, const uint16_t* sc, int V, int d, const float* x,
+                   const float* norm_w, float eps, int nt, int cand, int32_t* cand_ids, float* cand_screen,
+                   float* cand_logits, int8_t* xq_out, float* xsb_out, int32_t* chosen);
 
 /* ---- attention block, decode (attn.c; engine_gpt2.rs:535-590, 772-843) ---- */
 typedef struct orc_attn_layer_t {

@@ -86,6 +86,9 @@ def lib() -> C.CDLL:
         L.orc_q8_row_dot.argtypes = [i8p, f32p, i8p, f32p, C.c_int]
         L.orc_head.argtypes = [u16p, C.c_int, C.c_int, f32p, f32p, C.c_float, C.c_int, C.c_int, i32p, f32p, f32p,
                                i8p, f32p, i32p]
+        L.orc_q4_quant_rows.argtypes = [u16p, C.c_int, C.c_int, u8p, u16p]
+        L.orc_head_pre.argtypes = [u16p, u8p, u16p, C.c_int, C.c_int, f32p, f32p, C.c_float, C.c_int, C.c_int, i32p,
+                                   f32p, f32p, i8p, f32p, i32p]
         L.orc_set_threads.argtypes = [C.c_int]
         L.orc_get_threads.restype = C.c_int
         _LIB = L
@@ -295,9 +298,19 @@ def q8_row_dot(q, s, xq, xsb):
     return np.float32(lib().orc_q8_row_dot(_p(q, i8p), _p(s, f32p), _p(xq, i8p), _p(xsb, f32p), q.size))
 
 
-def head(w_bf16, x, norm_w, eps, nt=12, cand=8):
+def q4_quant_rows(w_bf16):
+    """Q4Mat of every row of [V][d] bf16: (nib [V][d/2], sc [V][d/32])."""
+    w = np.ascontiguousarray(w_bf16, np.uint16)
+    V, d = w.shape
+    nib = np.empty((V, d // 2), np.uint8); sc = np.empty((V, d // 32), np.uint16)
+    lib().orc_q4_quant_rows(_p(w, u16p), V, d, _p(nib, u8p), _p(sc, u16p))
+    return nib, sc
+
+
+def head(w_bf16, x, norm_w, eps, nt=12, cand=8, pre=None):
     """engine_gpt2.rs:937-1002 (greedy).  Returns dict: chosen, cand_ids,
-    cand_screen, cand_logits, xq, xsb."""
+    cand_screen, cand_logits, xq, xsb.  pre: (nib, sc) of q4_quant_rows, or
+    None to quantise the Q4 rows inside the call."""
     w = np.ascontiguousarray(w_bf16, np.uint16)
     V, d = w.shape
     x = np.ascontiguousarray(x, np.float32); norm_w = np.ascontiguousarray(norm_w, np.float32)
@@ -305,6 +318,14 @@ def head(w_bf16, x, norm_w, eps, nt=12, cand=8):
            "cand_logits": np.zeros(nt * cand, np.float32), "xq": np.zeros(d, np.int8),
            "xsb": np.zeros(d // 32, np.float32)}
     ch = C.c_int32()
+    if pre is not None:
+        nib, sc = (np.ascontiguousarray(pre[0], np.uint8), np.ascontiguousarray(pre[1], np.uint16))
+        assert nib.shape == (V, d // 2) and sc.shape == (V, d // 32)
+        lib().orc_head_pre(_p(w, u16p), _p(nib, u8p), _p(sc, u16p), V, d, _p(x, f32p), _p(norm_w, f32p), float(eps),
+                           nt, cand, _p(out["cand_ids"], i32p), _p(out["cand_screen"], f32p),
+                           _p(out["cand_logits"], f32p), _p(out["xq"], i8p), _p(out["xsb"], f32p), C.byref(ch))
+        out["chosen"] = int(ch.value)
+        return out
     lib().orc_head(_p(w, u16p), V, d, _p(x, f32p), _p(norm_w, f32p), float(eps), nt, cand,
                    _p(out["cand_ids"], i32p), _p(out["cand_screen"], f32p), _p(out["cand_logits"], f32p),
                    _p(out["xq"], i8p), _p(out["xsb"], f32p), C.byref(ch))

@@ -180,3 +180,20 @@ def test_head_candidates_and_greedy():
     logits = np.array([O.q8_row_dot(*O.q8_quant_row(w[r]), xq, xsb) for r in ids], np.float32)
     assert np.array_equal(out["cand_logits"], logits)
     assert out["chosen"] == ids[int(np.argmax(logits))]       # first maximum
+
+
+def test_head_prequantised_rows_agree():
+    # the load-time Q4 quantisation split off (orc_head_pre) gives the same head
+    r = np.random.default_rng(11)
+    V, d = 512, 96
+    w = r.integers(0, 0x7F00, (V, d), dtype=np.uint16) ^ (r.integers(0, 2, (V, d), dtype=np.uint16) << 15)
+    x = r.standard_normal(d).astype(np.float32)
+    nw = np.ones(d, np.float32)
+    a = O.head(w, x, nw, 1e-5)
+    pre = O.q4_quant_rows(w)
+    for row in (0, 17, V - 1):
+        nib, sc = O.q4_quant_row(w[row])
+        assert np.array_equal(pre[0][row], nib) and np.array_equal(pre[1][row], sc)
+    b = O.head(w, x, nw, 1e-5, pre=pre)
+    for k in a:
+        assert np.array_equal(np.asarray(a[k]), np.asarray(b[k])), k
