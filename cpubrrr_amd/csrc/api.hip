@@ -148,7 +148,6 @@ struct cpb_moe {
     // staging for raw GGUF bytes at load time
     uint8_t* staging = nullptr;
     size_t staging_size = 0;
-    unsigned long long* d_stamps = nullptr;   // probe builds (CPB_DECODE_STAMPS): phase timestamps
     // grouped (n_tok > 1) MXFP4 path: per-token and per-pair scratch
     bool grouped = false;
     float *g_inv = nullptr, *g_xn = nullptr, *g_xsb = nullptr, *g_logits = nullptr, *g_wts = nullptr, *g_hsb = nullptr, *g_dnout = nullptr;
@@ -371,8 +370,6 @@ int layer_token(cpb_moe_t* h, const DecodeBufs& B, int layer, float* dx, int app
     ra.qk = h->mx ? 0 : 1;
     ra.xn = B.xn; ra.xq = B.xq; ra.ximg = B.ximg; ra.xsb = B.xsb; ra.xsum = B.xsum;
     ra.lstar = B.lstar; ra.lbound = B.lbound;
-    unsigned long long* stamps = h->d_stamps ? h->d_stamps + (size_t)(layer % 60) * 16384 : nullptr;
-    ra.stamps = stamps;
     // the route launch publishes certified logits; the gate/up kernel
     // selects at its start (no cross-workgroup hand-off inside a launch)
     {
@@ -384,7 +381,6 @@ int layer_token(cpb_moe_t* h, const DecodeBufs& B, int layer, float* dx, int app
         g.w = L.gu; g.gate_b = L.gate_b; g.up_b = L.up_b;
         g.ximg = B.ximg; g.xsb = B.xsb;
         g.ids = B.ids;
-        g.stamps = stamps;
         {
             g.sel.lstar = B.lstar; g.sel.lbound = B.lbound; g.sel.router_w = L.router_w; g.sel.router_b = L.router_b;
             g.sel.xn = B.xn; g.sel.ne = c.n_expert; g.sel.k = c.top_k; g.sel.d = c.d;
@@ -398,7 +394,7 @@ int layer_token(cpb_moe_t* h, const DecodeBufs& B, int layer, float* dx, int app
         dn.w = L.dn; dn.down_b = L.down_b; dn.himg = B.himg; dn.hsb = B.hsb;
         dn.ids = B.ids; dn.wts = B.wts;
         dn.d = c.d; dn.dff = c.d_ff; dn.nbf = h->nbf; dn.nparts = h->parts_dn; dn.top_k = c.top_k;
-        dn.x = dx; dn.dn = h->t_dn; dn.dn_sums = h->t_dn_sums; dn.stamps = stamps;
+        dn.x = dx; dn.dn = h->t_dn; dn.dn_sums = h->t_dn_sums;
         {
             Timer tm(h, 1, timed);
             if (cpb::launch_gateup_mx(g, trace, h->stream)) return fail(CPB_ENODEV, "gate/up launch failed");
@@ -419,7 +415,6 @@ int layer_token(cpb_moe_t* h, const DecodeBufs& B, int layer, float* dx, int app
         k.d = c.d; k.dff = c.d_ff; k.top_k = c.top_k;
         k.hbuf = B.hbuf; k.hq = B.hq; k.hs = B.hsb; k.hsum = B.hsum; k.x = dx;
         k.gu_out = h->t_gu; k.gu_sums = h->t_gu_sums; k.dn_out = h->t_dn; k.dn_sums = h->t_dn_sums;
-        k.stamps = stamps;
         {
             Timer tm(h, 1, timed);
             if (cpb::launch_gateup_kq(k, trace, h->stream)) return fail(CPB_ENODEV, "k-quant gate/up launch failed");
@@ -495,9 +490,6 @@ int cpb_moe_create(const cpb_moe_cfg* cfg, int device, cpb_moe_t** out) {
         if (!h->mx && ((r = dmalloc(&h->g_xsum, T * nb)) || (r = dmalloc(&h->g_hsum, np * nbf)) || (r = dmalloc(&h->g_hbuf, np * ff))))
             return bail(r);
     }
-#ifdef CPB_DECODE_STAMPS
-    if ((r = dmalloc(&h->d_stamps, ((size_t)1 << 20) + 4096))) return bail(r);
-#endif
     if (hipMemsetAsync(h->b.fallback, 0, sizeof(int32_t), h->stream) != hipSuccess ||
         hipStreamSynchronize(h->stream) != hipSuccess)
         return bail(fail(CPB_ENODEV, "init memset failed"));
@@ -857,17 +849,6 @@ void cpb_moe_destroy(cpb_moe_t* h) {
     hipSetDevice(h->device);
     if (h->stream) hipStreamSynchronize(h->stream);
     clear_graphs(h);
-#ifdef CPB_DECODE_STAMPS
-    if (h->d_stamps) {
-        const char* path = getenv("CPB_DECODE_STAMPS_FILE");
-        size_t n = ((size_t)1 << 20) + 4096;
-        std::vector<unsigned long long> st(n);
-        hipMemcpy(st.data(), h->d_stamps, n * 8, hipMemcpyDeviceToHost);
-        FILE* f = path ? fopen(path, "wb") : nullptr;
-        if (f) { fwrite(st.data(), 8, n, f); fclose(f); }
-        hipFree(h->d_stamps);
-    }
-#endif
     void* gbufs[] = {h->g_xsum, h->g_hsum, h->g_hbuf,
                      h->g_inv, h->g_xn, h->g_xsb, h->g_logits, h->g_wts, h->g_hsb, h->g_dnout, h->g_xq, h->g_hq, h->g_ximg,
                      h->g_himg, h->g_lstar, h->g_lbound, h->g_ids, h->g_fallback, h->g_sorted, h->g_ntiles, h->g_tiles,

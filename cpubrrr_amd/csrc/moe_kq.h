@@ -38,7 +38,6 @@ struct KqArgs {
     int32_t* gu_sums;        // [top_k][2][dff][d/256][2]  (sumi, mint)
     float* dn_out;           // [top_k][d]
     int32_t* dn_sums;        // [top_k][d][dff/256][nsum]  nsum = 2 (Q4_K: sumi, mint) or 1 (Q6_K)
-    unsigned long long* stamps;  // probe builds (CPB_DECODE_STAMPS) only: per-workgroup phase clocks
 };
 
 // bytes of the stream layouts

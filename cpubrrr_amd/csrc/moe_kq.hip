@@ -128,8 +128,6 @@ __global__ __launch_bounds__(1024) void k_gateup_kq(KqArgs a) {
     const int lane = threadIdx.x & 63, q = uniform((int)(threadIdx.x >> 6));
     const int nth = blockDim.x;
     const int ei = blockIdx.x / T, t = blockIdx.x % T;
-    RSTAMP_DECL;
-    RSTAMP(0);
     int8_t* xl = (int8_t*)smem;                                  // [nsb][kXsPad]
     int32_t* xsl = (int32_t*)(smem + nsb * kXsPad);              // [nsb * 8]
     float* ysl = (float*)(xsl + nsb * 8);                        // [nsb]
@@ -158,15 +156,13 @@ __global__ __launch_bounds__(1024) void k_gateup_kq(KqArgs a) {
         if (ranked) select_rank_wg(a.sel, smem, blockIdx.x == 0 ? a.sel.logits : nullptr, pre);
         // ids only; workgroup 0 publishes the softmax weights once its
         // weight loads are in flight
-        if (q == 0) select_topk_wave(a.sel, smem, &ssel, false, a.stamps ? a.stamps + 12288 + (size_t)blockIdx.x * 4 : nullptr,
-                                     nullptr, ranked, true);
+        if (q == 0) select_topk_wave(a.sel, smem, &ssel, false, nullptr, ranked, true);
         __syncthreads();
         e = uniform(ssel.ids[ei]);
     } else {
         e = uniform(a.ids[ei]);
     }
 
-    RSTAMP(1);
     // weights: this lane's (row, superblock); idle lanes (s >= nsb) read superblock 0
     const int s = 2 * q + (lane >> 5), r = lane & 31;
     const bool live = s < nsb;
@@ -191,10 +187,7 @@ __global__ __launch_bounds__(1024) void k_gateup_kq(KqArgs a) {
         int32_t* so = TRACE ? a.gu_sums + ((((size_t)ei * 2 + isup) * a.dff + row) * nsb + s) * 2 : nullptr;
         part[s * 32 + r] = q4k_term<TRACE>(u, xl + s * kXsPad, xsl + s * 8, ysl[s], so);
     }
-    RSTAMP(2);
     __syncthreads();
-    RSTAMP(3);
-    RSTAMP_FLUSH_TO(a.stamps ? a.stamps + 2048 + (size_t)blockIdx.x * 8 : nullptr);
     if (threadIdx.x >= 32) return;
     float v = 0.0f;                                              // sumf, superblocks in order
     for (int k = 0; k < nsb; k++) v += part[k * 32 + r];
@@ -223,8 +216,6 @@ __global__ __launch_bounds__(1024) void k_down_kq(KqArgs a) {
     float* vv = part + nsbf * 64;                                 // [64]
     float4* hst = (float4*)(((size_t)(vv + 64) + 15) & ~(size_t)15);   // [K*dff/32][8] h chunks (one-chunk case)
 
-    RSTAMP_DECL;
-    RSTAMP(0);
     int es[8];
 #pragma unroll
     for (int k = 0; k < 8; k++) es[k] = uniform(a.ids[k < K ? k : 0]);
@@ -285,9 +276,7 @@ __global__ __launch_bounds__(1024) void k_down_kq(KqArgs a) {
             chunk_max(c);
         }
     }
-    RSTAMP(1);
     __syncthreads();
-    RSTAMP(2);
     // pass 2: scale per 256 (amax seeded 1e-12), round, sums per 32 and 16
     for (int c = threadIdx.x; c < nch; c += nth) {
         const int blk = c / 8;
@@ -336,10 +325,7 @@ __global__ __launch_bounds__(1024) void k_down_kq(KqArgs a) {
             tv = q6k_term<TRACE>(u, xs, h16 + (ei * nsbf + q) * 16, ys, so);
         part[q * 64 + lane] = tv;
     }
-    RSTAMP(3);
     __syncthreads();
-    RSTAMP(4);
-    RSTAMP_FLUSH_TO(a.stamps ? a.stamps + 8192 + (size_t)blockIdx.x * 8 : nullptr);
     if (q != 0) return;
     float v = 0.0f;
     for (int k = 0; k < nsbf; k++) v += part[k * 64 + lane];

@@ -20,7 +20,6 @@ struct GateUpArgs {
     int8_t* hq;              // [top_k][dff]
     uint8_t* himg;           // [top_k][dff/32][64] fp8 image of hq (mx_dev.h)
     float* hsb;              // [top_k][dff/32]
-    unsigned long long* stamps;  // probe builds (CPB_DECODE_STAMPS) only
     // trace (TRACE instantiation only)
     float* gu;               // [top_k][2][dff]
     int32_t* gu_sums;        // [top_k][2][dff][nb]
@@ -36,7 +35,6 @@ struct DownArgs {
     const float* wts;
     int d, dff, nbf, nparts, top_k;
     float* x;                // [d] residual, updated in place
-    unsigned long long* stamps;  // probe builds (CPB_DECODE_STAMPS) only
     float* dn;               // trace [top_k][d]
     int32_t* dn_sums;        // trace [top_k][d][nbf]
 };

@@ -58,8 +58,6 @@ __global__ __launch_bounds__(128 * kMaxParts) __attribute__((amdgpu_waves_per_eu
     // the selection's fields arrive in a second kernarg round trip)
     asm volatile("" ::"s"(a.sel.lstar), "s"(a.sel.lbound), "s"(a.sel.ne), "s"(a.sel.k), "s"(a.ximg), "s"(a.xsb),
                  "s"(a.nb), "s"(a.w));
-    RSTAMP_DECL;
-    RSTAMP(0);
     SelectPre pre{0.0, 0.0};
     if (a.sel.lstar && w == 0) pre = select_preload(a.sel);
     float* red = (float*)smem;                                 // [kTilesPerWG][W][64]
@@ -87,9 +85,8 @@ __global__ __launch_bounds__(128 * kMaxParts) __attribute__((amdgpu_waves_per_eu
         // ids only; workgroup 0 publishes the softmax weights once its weight
         // loads are in flight
         if (w == 0)
-            select_topk_wave(a.sel, smem, &ssel, false, a.stamps ? a.stamps + 4096 + (size_t)blockIdx.x * 4 : nullptr, &pre,
+            select_topk_wave(a.sel, smem, &ssel, false, &pre,
                              false, true);
-        RSTAMP(5);
         // barrier on LDS only (s_barrier without a wait for the activation loads)
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         // a plain LDS read: merged with the global read below into one flat
@@ -98,7 +95,6 @@ __global__ __launch_bounds__(128 * kMaxParts) __attribute__((amdgpu_waves_per_eu
     } else {
         e = a.ids[ei];
     }
-    RSTAMP(1);
     // both tiles' sub-parts requested back to back (a missing second tile of
     // an odd tile count reads the first again; its result is dropped)
     u32x4 wv[kTilesPerWG][1 + kSubUnits];
@@ -121,10 +117,8 @@ __global__ __launch_bounds__(128 * kMaxParts) __attribute__((amdgpu_waves_per_eu
         if (TRACE && t < tiles) so = a.gu_sums + (((size_t)(ei * 2 + isup) * a.dff + t * 32 + (lane & 31)) * a.nb + blk0);
         red[(j * W + w) * 64 + lane] = part_dot_sub_mfma<TRACE>(wv[j], ub, xw, xsc, so, blk0, a.nb);
     }
-    RSTAMP(2);
     __syncthreads();
     if (w >= kTilesPerWG || tw >= tiles) return;
-    RSTAMP(3);
     const int t = tw, row = t * 32 + (lane & 31);
     float pr[2 * kMaxParts];
 #pragma unroll
@@ -166,8 +160,6 @@ __global__ __launch_bounds__(128 * kMaxParts) __attribute__((amdgpu_waves_per_eu
         if (TRACE) a.h[(size_t)ei * a.dff + row] = h;
     }
     if (lane == 0) a.hsb[(size_t)ei * (a.dff / 32) + t] = sc;
-    RSTAMP(4);
-    RSTAMP_FLUSH_TO(a.stamps ? a.stamps + 1024 + (size_t)blockIdx.x * 8 : nullptr);
 }
 
 // top_k in {1, 2, 4}: one tile of 64 / top_k rows x top_k slots.
@@ -180,8 +172,6 @@ __global__ __launch_bounds__(128 * kMaxParts) void k_down_mx(DownArgs a) {
     const int ub = kSubUnits * hh;
     const int tiles = a.d / RT, t = blockIdx.x;
     const int ei = lane / RT, rr = lane % RT, row = t * RT + rr;
-    RSTAMP_DECL;
-    RSTAMP(0);
     float* red = (float*)smem;                                 // [W][64]
     float* vv = red + W * 64;                                  // [64]
     const int blk0 = q * kBlkPerPart;
@@ -213,13 +203,8 @@ __global__ __launch_bounds__(128 * kMaxParts) void k_down_mx(DownArgs a) {
         }
     }
     const int e = ei == 0 ? es[0] : ei == 1 ? es[1] : ei == 2 ? es[2] : es[3];
-#ifdef CPB_DECODE_STAMPS
-    asm volatile("" ::"v"(e));
-#endif
-    RSTAMP(4);
     u32x4 wv[1 + kSubUnits];
     load_sub(a.w + (((((size_t)e * tiles + t) * P + q) * kUnits) * RT) + rr, RT, ub, wv);
-    RSTAMP(5);
     float dnb_pf = 0.0f, x_pf = 0.0f, w_pf[4];
     if (w == 0) {
         if (a.down_b) dnb_pf = a.down_b[(size_t)e * a.d + row];
@@ -230,11 +215,9 @@ __global__ __launch_bounds__(128 * kMaxParts) void k_down_mx(DownArgs a) {
     int32_t* so = nullptr;
     if (TRACE) so = a.dn_sums + (((size_t)ei * a.d + row) * a.nbf + blk0);
     const float acc = part_dot_sub_mfma4<TRACE>(wv, ub, xa, xsc, so, blk0, a.nbf);
-    RSTAMP(1);
     red[w * 64 + lane] = acc;
     __syncthreads();
     if (w != 0) return;
-    RSTAMP(2);
     float pr[2 * kMaxParts];
 #pragma unroll
     for (int p = 0; p < 2 * kMaxParts; p++) pr[p] = p < W ? red[p * 64 + lane] : 0.0f;
@@ -254,8 +237,6 @@ __global__ __launch_bounds__(128 * kMaxParts) void k_down_mx(DownArgs a) {
             if (k < K) s += w_pf[k] * vv[k * RT + lane];
         a.x[row] = s;
     }
-    RSTAMP(3);
-    RSTAMP_FLUSH_TO(a.stamps ? a.stamps + 8192 + (size_t)blockIdx.x * 8 : nullptr);
 }
 
 // Any top_k <= 8: 16-row tiles, expert slots four at a time (one pass for
@@ -273,8 +254,6 @@ __global__ __launch_bounds__(128 * kMaxParts) void k_down_mx_slots(DownArgs a) {
     const int ub = kSubUnits * hh;
     const int tiles = a.d / RT, t = blockIdx.x;
     const int gi = lane / RT, rr = lane % RT, row = t * RT + rr;
-    RSTAMP_DECL;
-    RSTAMP(0);
     float* red = (float*)smem;                                 // [NP][W][64]
     float* vv = red + NP * W * 64;                             // [NP][64]
     const int blk0 = q * kBlkPerPart;
@@ -320,23 +299,16 @@ __global__ __launch_bounds__(128 * kMaxParts) void k_down_mx_slots(DownArgs a) {
 #pragma unroll
         for (int k = 1; k < 8; k++)
             if (slot == k) e = es[k];
-#ifdef CPB_DECODE_STAMPS
-        asm volatile("" ::"v"(e));
-#endif
-        if (pass == 0) RSTAMP(4);
         u32x4 wv[1 + kSubUnits];
         load_sub(a.w + (((((size_t)e * tiles + t) * P + q) * kUnits) * RT) + rr, RT, ub, wv);
-        if (pass == 0) RSTAMP(5);
         if (w == 0 && a.down_b && slot < K) dnb_pf[pass] = a.down_b[(size_t)e * a.d + row];
         int32_t* so = nullptr;
         if (TRACE && slot < K) so = a.dn_sums + (((size_t)slot * a.d + row) * a.nbf + blk0);
         const float acc = part_dot_sub_mfma4<TRACE>(wv, ub, xa, xsc, so, blk0, a.nbf);
         red[(pass * W + w) * 64 + lane] = acc;
     }
-    RSTAMP(1);
     __syncthreads();
     if (w != 0) return;
-    RSTAMP(2);
     for (int pass = 0; pass < NP; pass++) {
         float pr[2 * kMaxParts];
 #pragma unroll
@@ -359,8 +331,6 @@ __global__ __launch_bounds__(128 * kMaxParts) void k_down_mx_slots(DownArgs a) {
             if (k < K) s += w_pf[k] * vv[(k / SP) * 64 + (k % SP) * RT + lane];
         a.x[row] = s;
     }
-    RSTAMP(3);
-    RSTAMP_FLUSH_TO(a.stamps ? a.stamps + 8192 + (size_t)blockIdx.x * 8 : nullptr);
 }
 
 // ---- load-time re-layout from native GGUF MXFP4 rows (17-byte blocks) ----

@@ -21,7 +21,6 @@ struct RouteArgs {
     int32_t* xsum;           // [d/32] (qk == 1)
     double* lstar;           // [ne] fp64 logit (route_dev.h)
     double* lbound;          // [ne] bound on |reference serial fp32 logit - lstar|
-    unsigned long long* stamps;  // probe builds (CPB_DECODE_STAMPS) only: [ne][16] phase clocks
 };
 
 // Routing: expert e's certified logit (lstar / lbound) and the activation

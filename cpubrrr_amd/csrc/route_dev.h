@@ -109,19 +109,6 @@ CPB_DEV void norm_into(const float* __restrict__ xg, const float* __restrict__ n
 }
 
 
-#ifdef CPB_DECODE_STAMPS
-// timestamps kept in registers and written once at the end: a global store
-// per stamp would make every later vmcnt wait include its completion
-#define RSTAMP_DECL unsigned long long rst_[8] = {0, 0, 0, 0, 0, 0, 0, 0}
-#define RSTAMP(i) do { rst_[i] = wall_clock64(); } while (0)
-#define RSTAMP_FLUSH_TO(p_) do { if (threadIdx.x == 0 && (p_)) for (int i_ = 0; i_ < 8; i_++) (p_)[i_] = rst_[i_]; } while (0)
-#define RSTAMP_FLUSH RSTAMP_FLUSH_TO(a.stamps ? a.stamps + (size_t)e * 16 : nullptr)
-#else
-#define RSTAMP_DECL do { } while (0)
-#define RSTAMP(i) do { } while (0)
-#define RSTAMP_FLUSH do { } while (0)
-#define RSTAMP_FLUSH_TO(p_) do { } while (0)
-#endif
 
 // ---- wavefront DPP helpers on doubles (no LDS round trips) ----
 // v from the DPP source lane; lanes whose source is out of the row, or whose
@@ -284,8 +271,6 @@ CPB_DEV void route_expert(const RouteArgs& a, int e, int NEg, unsigned char* sme
     float* xl = (float*)smem;                                  // transposed (gpt-oss) or plain (Qwen) x
     double* dred = (double*)(smem + route_lds_bytes(d) - sizeof(double) * 64 - 64);   // [64]
     float* sinv = (float*)(dred + 64);
-    RSTAMP_DECL;
-    RSTAMP(0);
 
     const int j0 = et * kRouteC;
     const bool act = et >= 0 && j0 < d;
@@ -323,7 +308,6 @@ CPB_DEV void route_expert(const RouteArgs& a, int e, int NEg, unsigned char* sme
         qx = ld_dev(a.x + j);
         if (use_g) qg = a.norm_w[j];
     }
-    RSTAMP(1);
 
     // ---- x into LDS for the sum of squares ----
     const int S = route_xt_stride(d);
@@ -346,7 +330,6 @@ CPB_DEV void route_expert(const RouteArgs& a, int e, int NEg, unsigned char* sme
         }
     }
     __syncthreads();
-    RSTAMP(3);
     if (wv == 0) {
         if (a.apply_norm && a.norm == 0) {
             // lane q streams its row: the next group's reads are issued before
@@ -400,7 +383,6 @@ CPB_DEV void route_expert(const RouteArgs& a, int e, int NEg, unsigned char* sme
             for (int k = 0; k < nt; k++) tot += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ps), k));
             if (lane == 0) *sinv = 1.0f / sqrtf(tot / (float)d + a.eps);
         }
-        RSTAMP(6);
     } else {
         // ---- router logit, unscaled, beside the sum-of-squares chain ----
         LogitThread lt;
@@ -409,16 +391,13 @@ CPB_DEV void route_expert(const RouteArgs& a, int e, int NEg, unsigned char* sme
     }
     __syncthreads();
     const float inv = a.apply_norm ? *sinv : 1.0f;
-    RSTAMP(2);
     if (tid == 0) {
         double ls = 0.0, lb = 0.0;
         logit_final(dred, nws, d, b, inv, &ls, &lb);
         st_dev(a.lstar + e, ls);
         st_dev(a.lbound + e, lb);
-        RSTAMP(4);
     }
     if (wv == 0) {
-        RSTAMP_FLUSH;
         return;
     }
 

@@ -272,11 +272,6 @@ CPB_DEV void wave_lds_order() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"
 // ranking that truncation made wrong cannot pass it, and then the exact path
 // (the reference's serial logits) decides.  Softmax over the k in the
 // reference's order.  Writes *out (LDS) from lanes < K.
-#ifdef CPB_DECODE_STAMPS
-#define SSTAMP(i) do { if (st && (threadIdx.x & 63) == 0) st[i] = wall_clock64(); } while (0)
-#else
-#define SSTAMP(i) do { } while (0)
-#endif
 // The intervals of a <= 64-expert selection, one per lane, loaded ahead (a
 // caller issues these before its other loads so that the selection does not
 // wait for them: a wave's loads complete in order).
@@ -370,10 +365,9 @@ CPB_DEV void select_rank_wg(const SelectIn& s, unsigned char* lds, float* logits
 CPB_DEV void select_publish(const SelectIn& s, const Selection* out);
 template <int EXACT_CAND = 1, int EXACT_CHUNK = 1>
 CPB_DEV void select_topk_wave(const SelectIn& s, unsigned char* lds, Selection* out, bool publish_logits = false,
-                              unsigned long long* st = nullptr, const SelectPre* pre = nullptr, bool ranked = false,
+                              const SelectPre* pre = nullptr, bool ranked = false,
                               bool defer = false) {
     const int lane = threadIdx.x & 63;
-    SSTAMP(0);
     const int NE = s.ne, K = s.k;
     double lv[4] = {0.0, 0.0, 0.0, 0.0}, bv[4] = {0.0, 0.0, 0.0, 0.0};
     float lf[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -397,7 +391,6 @@ CPB_DEV void select_topk_wave(const SelectIn& s, unsigned char* lds, Selection* 
             my_l = sLf[lane];
             my_lo = sLo[lane];
         }
-        SSTAMP(1);
         bad = __any(lane < K && !(my_lo > later));
         wave_lds_order();
         if (bad) {
@@ -421,7 +414,6 @@ CPB_DEV void select_topk_wave(const SelectIn& s, unsigned char* lds, Selection* 
         const uint32_t key = valid ? ((float_key(lf[0]) & 0xFFFFFF00u) | (uint32_t)(255 - lane)) : 0u;
         const float lo = f32_down(lv[0] - bv[0]);
         const float hi = valid ? f32_up(lv[0] + bv[0]) : -__builtin_inff();
-        SSTAMP(1);
         uint32_t* skey = (uint32_t*)lds;                  // [64]
         int* sE = (int*)(skey + 64);                      // [8] by rank
         float* sLf = (float*)(sE + 8);                    // [8]
@@ -471,7 +463,6 @@ CPB_DEV void select_topk_wave(const SelectIn& s, unsigned char* lds, Selection* 
         lo[j] = f32_down(lv[j] - bv[j]);
         hi[j] = e < NE ? f32_up(lv[j] + bv[j]) : -__builtin_inff();
     }
-    SSTAMP(1);
     float my_lo = 0.0f, my_hi = -__builtin_inff();
     for (int i = 0; i < K; i++) {
         const uint32_t m = wave_max_u32(max(max(key[0], key[1]), max(key[2], key[3])));
@@ -498,7 +489,6 @@ CPB_DEV void select_topk_wave(const SelectIn& s, unsigned char* lds, Selection* 
     }
     bad = __any(lane < K && !(my_lo > later));
     }
-    SSTAMP(2);
     if (bad) {
         double* sL = (double*)lds;
         double* sH = sL + NE;
@@ -528,7 +518,6 @@ CPB_DEV void select_topk_wave(const SelectIn& s, unsigned char* lds, Selection* 
                 if (e < NE) s.logits[e] = lf[j];
             }
         }
-        SSTAMP(3);
         return;
     }
     // softmax over the k selected, reference order: ex_i = exp(l_i - l_0)
@@ -544,7 +533,6 @@ CPB_DEV void select_topk_wave(const SelectIn& s, unsigned char* lds, Selection* 
         out->wts[lane] = wt;
     }
     if (lane == 0) out->fallback = bad ? 1 : 0;
-    SSTAMP(3);
     // trace outputs and the routed ids / weights for later launches (by one
     // workgroup, or by this one when it alone selects for its token)
     if (publish_logits) {
