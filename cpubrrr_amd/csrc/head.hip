@@ -20,6 +20,7 @@
 #include <cfloat>
 #include <cstdio>
 #include <mutex>
+#include <vector>
 
 #include "cpb_head.h"
 #include "cpb_internal.h"
@@ -30,6 +31,8 @@ namespace cpb {
 
 constexpr int kHeadRT = 64;          // rows per stream tile
 constexpr int kHeadMaxCand = 16;
+constexpr int kHeadMaxSlices = 32;
+constexpr int kHeadGroupRows = 4 * 64;    // rows of one screen workgroup (4 tiles)
 
 CPB_DEV float bf16f(uint32_t v) { return __uint_as_float(v << 16); }
 // engine_gpt2.rs:303-307: round to nearest even into the top 16 bits
@@ -55,7 +58,70 @@ struct HeadDev {
     float* cand_screen;
     float* cand_logits;
     int32_t* chosen;       // [1]
+    // per worker slice: the rows' tiles and where their candidates go
+    const int32_t* wtab;   // [nt][2]: first screen workgroup (256 rows), base offset into candv / candi
+    float* candv;          // per (worker, workgroup): its best n_cand screen values in the slice
+    int32_t* candi;        //   and their rows (INT32_MAX: none)
+    int32_t* count;        // [1] arrivals of the refine workgroups (0 between launches)
 };
+
+// rows of worker slice w: [4 nq w / nt, 4 nq (w + 1) / nt) (head_worker's quads)
+CPB_DEV_HOST_INLINE int slice_r0(long nq, int nt, int w) { return (int)(4 * (nq * w / nt)); }
+
+// ---- cross-lane helpers on DPP + readlane ----
+template <int CTRL>
+CPB_DEV float dpp_fh(float v) { return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false)); }
+template <int CTRL>
+CPB_DEV int dpp_ih(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false); }
+
+// (value, index) order of the screen: larger value first, then lower index
+CPB_DEV bool better(float v, int i, float w, int j) { return v > w || (v == w && i < j); }
+template <int CTRL>
+CPB_DEV void best_step(float& v, int& i) {
+    const float ov = dpp_fh<CTRL>(v);
+    const int oi = dpp_ih<CTRL>(i);
+    if (better(ov, oi, v, i)) { v = ov; i = oi; }
+}
+// the best (value, index) of the wave, in every lane
+CPB_DEV void wave_best(float& v, int& i) {
+    best_step<0xB1>(v, i);       // lane ^ 1
+    best_step<0x4E>(v, i);       // lane ^ 2
+    best_step<0x141>(v, i);      // mirror within 8
+    best_step<0x140>(v, i);      // mirror within 16
+    float bv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    int bi = __builtin_amdgcn_readlane(i, 0);
+#pragma unroll
+    for (int r = 16; r < 64; r += 16) {
+        const float rv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), r));
+        const int ri = __builtin_amdgcn_readlane(i, r);
+        if (better(rv, ri, bv, bi)) { bv = rv; bi = ri; }
+    }
+    v = bv;
+    i = bi;
+}
+
+// rank of this lane's (value, index) among the wave's 64 (the number of
+// better entries; sentinels (-inf, INT32_MAX) are below every entry).  sv /
+// si: this wave's 64-entry LDS scratch.
+CPB_DEV int wave_rank(float v, int i, float* sv, int* si) {
+    const int lane = threadIdx.x & 63;
+    sv[lane] = v;
+    si[lane] = i;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    int rank = 0;
+#pragma unroll 4
+    for (int q = 0; q < 16; q++) {
+        const float4 ov = ((const float4*)sv)[q];
+        const int4 oi = ((const int4*)si)[q];
+        rank += better(ov.x, oi.x, v, i) + better(ov.y, oi.y, v, i) + better(ov.z, oi.z, v, i) + better(ov.w, oi.w, v, i);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    return rank;
+}
 
 // ---- load time: Q4Mat + Q8Mat rows from bf16, one thread per (row, block) ----
 __global__ void k_head_quant(const uint16_t* __restrict__ w, int V, int Vpad, int d, u32x4* __restrict__ q4,
@@ -126,173 +192,290 @@ __global__ __launch_bounds__(256) void k_head_norm(HeadDev a) {
     float* xnl = xs + d;
     float* scratch = xnl + d;
     norm_into(a.x, a.norm_w, d, a.eps, 0, 0, 1, xs, xnl, scratch);
-    const int l = tid & 31;
-    for (int bk = tid >> 5; bk < a.nb; bk += blockDim.x >> 5) {
-        const float v = xnl[bk * 32 + l];
-        float m = fabsf(v);
+    // 4 lanes per block, 8 consecutive values each (lane q: elements 8q .. 8q + 7)
+    for (int e = tid; e < a.nb * 4; e += blockDim.x) {
+        const int bk = e >> 2, q = e & 3;
+        float v[8];
+        float m = 0.0f;
 #pragma unroll
-        for (int s2 = 16; s2 >= 1; s2 >>= 1) m = fmaxf(m, __shfl_xor(m, s2));
+        for (int u = 0; u < 8; u++) {
+            v[u] = xnl[bk * 32 + 8 * q + u];
+            m = fmaxf(m, fabsf(v[u]));
+        }
+        m = fmaxf(m, dpp_fh<0xB1>(m));
+        m = fmaxf(m, dpp_fh<0x4E>(m));
         const float sc = fmaxf(1e-12f, m) / 127.0f;
-        const int q = q8_round(v, sc);
-        a.xq[bk * 32 + l] = (int8_t)q;
-        if (l == 0) a.xsb[bk] = sc;
-        // lane part j of the screen dot = elements 4j..4j+3 and 16+4j..16+4j+3
-        int s = q;
-        s += __shfl_xor(s, 1);
-        s += __shfl_xor(s, 2);
-        s += __shfl_xor(s, 16);
-        if (l < 16 && (l & 3) == 0) a.xs8[bk * 4 + (l >> 2)] = s;
+        uint32_t wd[2] = {0u, 0u};
+        int slo = 0, shi = 0;
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int qv = q8_round(v[u], sc);
+            wd[u >> 2] |= (uint32_t)(uint8_t)qv << (8 * (u & 3));
+            if (u < 4) slo += qv; else shi += qv;
+        }
+        ((uint2*)a.xq)[bk * 4 + q] = make_uint2(wd[0], wd[1]);
+        if (q == 0) a.xsb[bk] = sc;
+        // lane part j of the screen dot = elements 4j..4j+3 and 16+4j..16+4j+3:
+        // j = 0, 1 from lanes 0 and 2 (low / high four), j = 2, 3 from lanes 1 and 3
+        const int plo = slo + dpp_ih<0x4E>(slo), phi = shi + dpp_ih<0x4E>(shi);
+        if (q < 2) {
+            a.xs8[bk * 4 + 2 * q] = plo;
+            a.xs8[bk * 4 + 2 * q + 1] = phi;
+        }
     }
 }
 
 // ---- Q4 screen of every row (dot4_q4_i8, :314-342): one lane per row ----
 __global__ __launch_bounds__(256) void k_head_screen(HeadDev a) {
     extern __shared__ __align__(16) unsigned char smem[];
-    const int nb = a.nb, tid = threadIdx.x, lane = tid & 63;
+    const int nb = a.nb, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     uint32_t* xl = (uint32_t*)smem;                    // xq as dwords [nb][8]
     float* xsl = (float*)(xl + nb * 8);                // [nb]
     int32_t* x8 = (int32_t*)(xsl + nb);                // [nb][4]
+    __shared__ __align__(16) float rsv[4][64];
+    __shared__ __align__(16) int rsi[4][64];
+    __shared__ float lv[kHeadMaxSlices][4][kHeadMaxCand];
+    __shared__ int li[kHeadMaxSlices][4][kHeadMaxCand];
     for (int i = tid; i < nb * 8; i += blockDim.x) xl[i] = ((const uint32_t*)a.xq)[i];
     for (int i = tid; i < nb; i += blockDim.x) xsl[i] = a.xsb[i];
     for (int i = tid; i < nb * 4; i += blockDim.x) x8[i] = a.xs8[i];
     __syncthreads();
-    const int tile = blockIdx.x * (blockDim.x >> 6) + (tid >> 6);
-    if (tile * kHeadRT >= a.Vpad) return;
-    const u32x4* wp = a.q4 + (size_t)tile * nb * kHeadRT + lane;
-    const uint16_t* sp = a.q4s + (size_t)tile * nb * kHeadRT + lane;
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const int tile = blockIdx.x * 4 + wave;
+    const bool live = tile * kHeadRT < a.Vpad;
+    float val = -INFINITY;
+    const int row = tile * kHeadRT + lane;
+    if (live) {
+        const u32x4* wp = a.q4 + (size_t)tile * nb * kHeadRT + lane;
+        const uint16_t* sp = a.q4s + (size_t)tile * nb * kHeadRT + lane;
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll 6
-    for (int b = 0; b < nb; b++) {
-        const u32x4 w = __builtin_nontemporal_load(wp + (size_t)b * kHeadRT);
-        const float sv = bf16f(sp[(size_t)b * kHeadRT]) * xsl[b];
+        for (int b = 0; b < nb; b++) {
+            const u32x4 w = __builtin_nontemporal_load(wp + (size_t)b * kHeadRT);
+            const float sv = bf16f(sp[(size_t)b * kHeadRT]) * xsl[b];
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            int t = sdot4(w[j] & 0x0F0F0F0Fu, xl[b * 8 + j], 0);
-            t = sdot4((w[j] >> 4) & 0x0F0F0F0Fu, xl[b * 8 + 4 + j], t);
-            t -= 8 * x8[b * 4 + j];                    // codes are KVI4[c] = c - 8
-            acc[j] = fmaf((float)t, sv, acc[j]);
+            for (int j = 0; j < 4; j++) {
+                int t = sdot4(w[j] & 0x0F0F0F0Fu, xl[b * 8 + j], 0);
+                t = sdot4((w[j] >> 4) & 0x0F0F0F0Fu, xl[b * 8 + 4 + j], t);
+                t -= 8 * x8[b * 4 + j];                    // codes are KVI4[c] = c - 8
+                acc[j] = fmaf((float)t, sv, acc[j]);
+            }
         }
+        val = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+        a.screen[row] = val;
     }
-    a.screen[tile * kHeadRT + lane] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
-}
-
-// (value, index) order of the screen: larger value first, then lower index
-CPB_DEV bool better(float v, int i, float w, int j) { return v > w || (v == w && i < j); }
-
-// ---- per worker slice: the n_cand best rows (the reference's insertion) ----
-// grid: n_slices workgroups of 1024 threads.
-__global__ __launch_bounds__(1024) void k_head_topk(HeadDev a) {
-    __shared__ float wv[16];
-    __shared__ int wi[16], wt[16];
-    __shared__ int win_tid;
-    const int wid = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv_id = tid >> 6;
+    // the workgroup's best n_cand rows in each worker slice it meets (a slice's
+    // best n_cand are among its row groups' best n_cand): per tile by rank,
+    // then the four tiles' lists by rank again
     const long nq = a.V / 4;
-    const int r0 = (int)(4 * (nq * wid / a.nt)), r1 = (int)(4 * (nq * (wid + 1) / a.nt));
     const int C = a.nc;
-    float lv[kHeadMaxCand];
-    int li[kHeadMaxCand];
-#pragma unroll
-    for (int k = 0; k < kHeadMaxCand; k++) { lv[k] = -FLT_MAX; li[k] = 0; }
-    // rows visited in increasing order per thread: an equal later value stays behind
-    for (int r = r0 + tid; r < r1; r += blockDim.x) {
-        const float v = a.screen[r];
-        if (v > lv[C - 1]) {
-            lv[C - 1] = v;
-            li[C - 1] = r;
-#pragma unroll
-            for (int p = kHeadMaxCand - 1; p > 0; p--)
-                if (p < C && lv[p - 1] < lv[p]) {
-                    const float tv = lv[p]; lv[p] = lv[p - 1]; lv[p - 1] = tv;
-                    const int ti = li[p]; li[p] = li[p - 1]; li[p - 1] = ti;
-                }
-        }
+    const int glo = blockIdx.x * 4 * kHeadRT, ghi = min(glo + 4 * kHeadRT, a.V) - 1;
+    int wa = (int)((long)(glo / 4) * a.nt / nq);
+    while (wa > 0 && slice_r0(nq, a.nt, wa) > glo) wa--;
+    while (wa + 1 < a.nt && slice_r0(nq, a.nt, wa + 1) <= glo) wa++;
+    int wb = wa;
+    while (wb + 1 < a.nt && slice_r0(nq, a.nt, wb + 1) <= ghi) wb++;
+    for (int w = wa; w <= wb; w++) {
+        const int r0 = slice_r0(nq, a.nt, w), r1 = slice_r0(nq, a.nt, w + 1);
+        // head_worker inserts only values above its initial -FLT_MAX
+        const bool in = live && row >= r0 && row < r1 && row < a.V && val > -FLT_MAX;
+        const float v = in ? val : -INFINITY;
+        const int i = in ? row : INT32_MAX;
+        const int rank = wave_rank(v, i, rsv[wave], rsi[wave]);
+        if (in && rank < C) { lv[w - wa][wave][rank] = v; li[w - wa][wave][rank] = i; }
+        const int n_in = __builtin_popcountll(__ballot(in));
+        if (lane >= n_in && lane < C) { lv[w - wa][wave][lane] = -INFINITY; li[w - wa][wave][lane] = INT32_MAX; }
     }
-    // merge: C rounds of a block-wide best over each thread's next entry
-    int ptr = 0;
-    for (int k = 0; k < C; k++) {
-        float v = -FLT_MAX;
-        int i = 0x7fffffff;
-#pragma unroll
-        for (int p = 0; p < kHeadMaxCand; p++)
-            if (p == ptr) { v = lv[p]; i = li[p]; }
-        // an exhausted thread (ptr == C) offers nothing
-        if (ptr >= C) { v = -FLT_MAX; i = 0x7fffffff; }
-        int t = tid;
-#pragma unroll
-        for (int s2 = 32; s2 >= 1; s2 >>= 1) {
-            const float ov = __shfl_xor(v, s2);
-            const int oi = __shfl_xor(i, s2), ot = __shfl_xor(t, s2);
-            if (better(ov, oi, v, i) || (ov == v && oi == i && ot < t)) { v = ov; i = oi; t = ot; }
-        }
-        if (lane == 0) { wv[wv_id] = v; wi[wv_id] = i; wt[wv_id] = t; }
-        __syncthreads();
-        if (tid == 0) {
-            float bv = wv[0];
-            int bi = wi[0], bt = wt[0];
-            for (int q = 1; q < (int)(blockDim.x >> 6); q++)
-                if (better(wv[q], wi[q], bv, bi) || (wv[q] == bv && wi[q] == bi && wt[q] < bt)) {
-                    bv = wv[q]; bi = wi[q]; bt = wt[q];
-                }
-            // an empty slice keeps the reference's initial entries (-FLT_MAX, row 0)
-            a.cand_ids[wid * C + k] = bi == 0x7fffffff ? 0 : bi;
-            a.cand_screen[wid * C + k] = bv;
-            win_tid = bt;
-        }
-        __syncthreads();
-        if (tid == win_tid) ptr++;
-        __syncthreads();
+    __syncthreads();
+    for (int w = wa + wave; w <= wb; w += 4) {
+        const int r0 = slice_r0(nq, a.nt, w), r1 = slice_r0(nq, a.nt, w + 1);
+        if (r0 == r1) continue;
+        const bool has = lane < 4 * C;
+        const float v = has ? lv[w - wa][lane / C][lane % C] : -INFINITY;
+        const int i = has ? li[w - wa][lane / C][lane % C] : INT32_MAX;
+        const int rank = wave_rank(v, i, rsv[wave], rsi[wave]);
+        const size_t slot = (size_t)a.wtab[2 * w + 1] + (size_t)(blockIdx.x - a.wtab[2 * w]) * C;
+        const bool real = i != INT32_MAX;
+        if (real && rank < C) { a.candv[slot + rank] = v; a.candi[slot + rank] = i; }
+        const int n_real = __builtin_popcountll(__ballot(real));
+        if (lane >= n_real && lane < C) { a.candv[slot + lane] = -INFINITY; a.candi[slot + lane] = INT32_MAX; }
     }
 }
 
-// ---- exact Q8 logits of the candidates (dot_q8_i8, :169-191) + greedy ----
-// 8 lanes per candidate: chain (accumulator h = even / odd blocks, lane part j)
+// ---- per worker slice: merge the tiles' candidates into the n_cand best
+// (the reference's insertion keeps the n_cand largest values, equal values in
+// row order), their exact Q8 logits (dot_q8_i8, :169-191), then the greedy
+// choice over all workers' candidates in worker / rank order (:128-134) by the
+// last workgroup to finish.  grid: n_slices workgroups of 1024 threads.
+constexpr int kRefineWaves = 16;
 __global__ __launch_bounds__(1024) void k_head_refine(HeadDev a) {
-    __shared__ float lg[1024 / 8];
-    const int tid = threadIdx.x, nc = a.nt * a.nc, nb = a.nb;
-    const int c = tid >> 3, h = (tid >> 2) & 1, j = tid & 3;
-    if (c < nc) {
-        const int row = a.cand_ids[c];
-        const int8_t* q = a.q8 + (size_t)row * a.d;
-        const float* s = a.q8s + (size_t)row * nb;
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int C = a.nc, nb = a.nb, d = a.d;
+    u32x4* rows = (u32x4*)smem;                        // [C][d / 16] candidate rows' Q8 codes
+    float* rs = (float*)(rows + (size_t)C * (d / 16)); // [C][nb] their scales
+    uint32_t* xl = (uint32_t*)(rs + C * nb);           // xq as dwords [nb][8]
+    float* xsl = (float*)(xl + nb * 8);                // [nb]
+    __shared__ float wv[kRefineWaves][kHeadMaxCand];
+    __shared__ int wi[kRefineWaves][kHeadMaxCand];
+    __shared__ float wv2[4][kHeadMaxCand];
+    __shared__ int wi2[4][kHeadMaxCand];
+    __shared__ __align__(16) float rsv[kRefineWaves][64];
+    __shared__ __align__(16) int rsi[kRefineWaves][64];
+    __shared__ int cid[kHeadMaxCand];
+    __shared__ float lgs[128];
+    __shared__ int ids_s[128];
+    __shared__ int last;
+    const int w = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (int i = tid; i < nb * 8; i += 1024) xl[i] = ((const uint32_t*)a.xq)[i];
+    for (int i = tid; i < nb; i += 1024) xsl[i] = a.xsb[i];
+    const long nq = a.V / 4;
+    const int r0 = slice_r0(nq, a.nt, w), r1 = slice_r0(nq, a.nt, w + 1);
+    const int M = r0 == r1 ? 0 : ((r1 - 1) / kHeadGroupRows - a.wtab[2 * w] + 1) * C;
+    const float* cv = a.candv + a.wtab[2 * w + 1];
+    const int* ci = a.candi + a.wtab[2 * w + 1];
+    // each wave: chunks of 64 entries by rank, folded into a running best n_cand
+    {
+        const int nchunk = (M + 63) / 64;
+        float runv = -INFINITY;
+        int runi = INT32_MAX;                 // lane k < C: the wave's k-th best so far
+        for (int ch = wave; ch < nchunk; ch += kRefineWaves) {
+            const int e = ch * 64 + lane;
+            const float v = e < M ? cv[e] : -INFINITY;
+            const int i = e < M ? ci[e] : INT32_MAX;
+            const int rank = wave_rank(v, i, rsv[wave], rsi[wave]);
+            // lanes C .. 2C - 1: this chunk's best n_cand, then rank the 2C
+            float mv = lane < C ? runv : -INFINITY;
+            int mi = lane < C ? runi : INT32_MAX;
+            rsv[wave][lane] = -INFINITY;
+            rsi[wave][lane] = INT32_MAX;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            if (i != INT32_MAX && rank < C) { rsv[wave][C + rank] = v; rsi[wave][C + rank] = i; }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            if (lane >= C && lane < 2 * C) { mv = rsv[wave][lane]; mi = rsi[wave][lane]; }
+            const int r2 = wave_rank(mv, mi, rsv[wave], rsi[wave]);
+            rsv[wave][lane] = -INFINITY;
+            rsi[wave][lane] = INT32_MAX;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            if (mi != INT32_MAX && r2 < C) { rsv[wave][r2] = mv; rsi[wave][r2] = mi; }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            runv = rsv[wave][lane];
+            runi = rsi[wave][lane];
+        }
+        if (lane < C) { wv[wave][lane] = runv; wi[wave][lane] = runi; }
+    }
+    __syncthreads();
+    // waves 0-3: the n_cand best of four waves' lists each
+    if (wave < 4) {
+        const float v = lane < 4 * C ? wv[4 * wave + lane / C][lane % C] : -INFINITY;
+        const int i = lane < 4 * C ? wi[4 * wave + lane / C][lane % C] : INT32_MAX;
+        const int rank = wave_rank(v, i, rsv[wave], rsi[wave]);
+        if (i != INT32_MAX && rank < C) { wv2[wave][rank] = v; wi2[wave][rank] = i; }
+        const int n_real = __builtin_popcountll(__ballot(i != INT32_MAX));
+        if (lane >= n_real && lane < C) { wv2[wave][lane] = -INFINITY; wi2[wave][lane] = INT32_MAX; }
+    }
+    __syncthreads();
+    // wave 0: the n_cand best of those four
+    if (wave == 0) {
+        const float v = lane < 4 * C ? wv2[lane / C][lane % C] : -INFINITY;
+        const int i = lane < 4 * C ? wi2[lane / C][lane % C] : INT32_MAX;
+        const int rank = wave_rank(v, i, rsv[0], rsi[0]);
+        const bool real = i != INT32_MAX;
+        if (real && rank < C) {
+            cid[rank] = i;
+            st_dev(a.cand_ids + w * C + rank, i);
+            st_dev(a.cand_screen + w * C + rank, v);
+        }
+        const int n_real = __builtin_popcountll(__ballot(real));
+        // fewer than n_cand rows: the reference's initial entries (-FLT_MAX, row 0)
+        if (lane >= n_real && lane < C) {
+            cid[lane] = 0;
+            st_dev(a.cand_ids + w * C + lane, 0);
+            st_dev(a.cand_screen + w * C + lane, -FLT_MAX);
+        }
+    }
+    __syncthreads();
+    // the candidates' Q8 rows and scales into LDS, every load in flight at once
+    {
+        const int per = d / 16;
+        for (int e = tid; e < C * per; e += 1024) {
+            const int c = e / per, o = e - c * per;
+            rows[e] = *((const u32x4*)(a.q8 + (size_t)cid[c] * d) + o);
+        }
+        for (int e = tid; e < C * nb; e += 1024) {
+            const int c = e / nb, o = e - c * nb;
+            rs[e] = a.q8s[(size_t)cid[c] * nb + o];
+        }
+    }
+    __syncthreads();
+    // exact Q8 logits: 8 lanes per candidate, lane (h, j) runs the reference's
+    // chain j of the even (h = 0) or odd (h = 1) blocks
+    if (tid < C * 8) {
+        const int c = tid >> 3, h = (tid >> 2) & 1, j = tid & 3;
+        const uint32_t* q = (const uint32_t*)(rows + (size_t)c * (d / 16));
+        const float* sc = rs + c * nb;
         const int nbe = nb & ~1;
         float acc = 0.0f;
         auto blk = [&](int b) {
-            const uint32_t w0 = *(const uint32_t*)(q + b * 32 + 4 * j), w1 = *(const uint32_t*)(q + b * 32 + 16 + 4 * j);
-            const uint32_t x0 = *(const uint32_t*)(a.xq + b * 32 + 4 * j), x1 = *(const uint32_t*)(a.xq + b * 32 + 16 + 4 * j);
-            const int t = sdot4(w1, x1, sdot4(w0, x0, 0));
-            acc = fmaf((float)t, s[b] * a.xsb[b], acc);
+            const int t = sdot4(q[b * 8 + 4 + j], xl[b * 8 + 4 + j], sdot4(q[b * 8 + j], xl[b * 8 + j], 0));
+            acc = fmaf((float)t, sc[b] * xsl[b], acc);
         };
+#pragma unroll 4
         for (int b = h; b < nbe; b += 2) blk(b);
         if ((nb & 1) && h == 0) blk(nb - 1);       // an odd last block goes into the first accumulator
-        // v_j = acc0_j + acc1_j, then (v0 + v1) + (v2 + v3)
-        const float v = acc + __shfl_xor(acc, 4);
-        const float v01 = v + __shfl_xor(v, 1);     // lanes j = 0, 1 -> v0 + v1; j = 2, 3 -> v2 + v3
-        const float tot = __shfl(v01, (tid & ~7)) + __shfl(v01, (tid & ~7) + 2);
-        if ((tid & 7) == 0) {
-            lg[c] = tot;
-            a.cand_logits[c] = tot;
-        }
+        // lanes 0-3 of each group of 8: v_j = acc0_j + acc1_j (lane + 4: row_ror by 12),
+        // then lane 0: (v0 + v1) + (v2 + v3)
+        const float v = acc + dpp_fh<0x12C>(acc);
+        const float v01 = v + dpp_fh<0xB1>(v);
+        const float tot = v01 + dpp_fh<0x4E>(v01);
+        if ((tid & 7) == 0) st_dev(a.cand_logits + w * C + c, tot);
+    }
+    // arrival: the last workgroup takes the greedy choice
+    drain_memory();
+    __syncthreads();
+    if (tid == 0) {
+        const int prev = __hip_atomic_fetch_add(a.count, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last = prev == a.nt - 1;
+        if (last) __hip_atomic_store(a.count, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!last) return;
+    const int nc = a.nt * C;
+    if (tid < nc) {
+        lgs[tid] = ld_dev(a.cand_logits + tid);
+        ids_s[tid] = ld_dev(a.cand_ids + tid);
     }
     __syncthreads();
     if (tid == 0) {
         float best = -FLT_MAX;
         int bi = 0;
         for (int k = 0; k < nc; k++)
-            if (lg[k] > best) { best = lg[k]; bi = a.cand_ids[k]; }
+            if (lgs[k] > best) { best = lgs[k]; bi = ids_s[k]; }
         *a.chosen = bi;
     }
 }
 
+// LDS of k_head_refine: candidate rows and scales, activations
+inline size_t head_refine_lds(int d, int nc) { return (size_t)nc * d + (size_t)nc * (d / 32) * 4 + (size_t)(d / 32) * 36; }
+
 }  // namespace cpb
 
 using cpb::fail;
+
+constexpr int kHeadBufs = 16;
 
 struct cpb_head {
     cpb_head_cfg cfg{};
     int device = 0;
     hipStream_t own = nullptr, stream = nullptr;
     cpb::HeadDev a{};
-    void* base[12] = {};
+    void* base[16] = {};
     bool loaded = false;
 };
 
@@ -355,10 +538,23 @@ int cpb_head_create(const cpb_head_cfg* cfg, int device, cpb_head_t** out) {
     a.d = cfg->d; a.nb = cfg->d / 32; a.V = cfg->n_vocab; a.Vpad = (int)vpad(cfg);
     a.nt = cfg->n_slices; a.nc = cfg->n_cand; a.eps = cfg->rms_eps;
     const size_t nb = a.nb, nc = (size_t)a.nt * a.nc;
-    const size_t sizes[12] = {(size_t)a.Vpad * nb * 16, (size_t)a.Vpad * nb * 2, (size_t)a.V * a.d, (size_t)a.V * nb * 4,
-                              (size_t)a.d * 4, (size_t)a.d * 4, (size_t)a.d + nb * 4 + nb * 16, (size_t)a.Vpad * 4,
-                              nc * 4, nc * 4, nc * 4, 4};
-    for (int i = 0; i < 12; i++) {
+    // worker slices: first tile and candidate offset of each
+    std::vector<int32_t> wtab(2 * a.nt);
+    size_t ncand = 0;
+    {
+        const long nq = a.V / 4;
+        for (int w = 0; w < a.nt; w++) {
+            const int r0 = cpb::slice_r0(nq, a.nt, w), r1 = cpb::slice_r0(nq, a.nt, w + 1);
+            wtab[2 * w] = r0 / cpb::kHeadGroupRows;
+            wtab[2 * w + 1] = (int32_t)ncand;
+            if (r1 > r0) ncand += (size_t)((r1 - 1) / cpb::kHeadGroupRows - r0 / cpb::kHeadGroupRows + 1) * a.nc;
+        }
+    }
+    const size_t sizes[kHeadBufs] = {(size_t)a.Vpad * nb * 16, (size_t)a.Vpad * nb * 2, (size_t)a.V * a.d,
+                                     (size_t)a.V * nb * 4, (size_t)a.d * 4, (size_t)a.d * 4,
+                                     (size_t)a.d + nb * 4 + nb * 16, (size_t)a.Vpad * 4, nc * 4, nc * 4, nc * 4, 4,
+                                     wtab.size() * 4, ncand * 4, ncand * 4, 4};
+    for (int i = 0; i < kHeadBufs; i++) {
         hipError_t e = hipMalloc(&h->base[i], sizes[i]);
         if (e != hipSuccess) return bail(fail(CPB_ENOMEM, "hipMalloc(%zu): %s", sizes[i], hipGetErrorString(e)));
     }
@@ -376,6 +572,16 @@ int cpb_head_create(const cpb_head_cfg* cfg, int device, cpb_head_t** out) {
     a.cand_screen = (float*)h->base[9];
     a.cand_logits = (float*)h->base[10];
     a.chosen = (int32_t*)h->base[11];
+    a.wtab = (const int32_t*)h->base[12];
+    a.candv = (float*)h->base[13];
+    a.candi = (int32_t*)h->base[14];
+    a.count = (int32_t*)h->base[15];
+    if (hipFuncSetAttribute((const void*)cpb::k_head_refine, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)cpb::head_refine_lds(a.d, a.nc)) != hipSuccess)
+        return bail(fail(CPB_ENODEV, "LDS attribute refused"));
+    if (hipMemcpy(h->base[12], wtab.data(), wtab.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemset(a.count, 0, 4) != hipSuccess)
+        return bail(fail(CPB_ENODEV, "head init copies failed"));
     *out = h;
     return 0;
 }
@@ -401,13 +607,15 @@ int cpb_head_load(cpb_head_t* h, const uint16_t* out_w, const float* out_norm) {
     return 0;
 }
 
-static int head_launch(cpb_head_t* h) {
-    const cpb::HeadDev& a = h->a;
+// x: the hidden state (device), chosen: where the token goes (device)
+static int head_launch(cpb_head_t* h, const float* x, int32_t* chosen) {
+    cpb::HeadDev a = h->a;
+    a.x = x;
+    a.chosen = chosen;
     cpb::launch(cpb::k_head_norm, dim3(1), dim3(256), sizeof(float) * (2 * a.d + 64), h->stream, a);
     const int tiles = a.Vpad / cpb::kHeadRT;
     cpb::launch(cpb::k_head_screen, dim3((tiles + 3) / 4), dim3(256), (size_t)a.nb * (32 + 4 + 16), h->stream, a);
-    cpb::launch(cpb::k_head_topk, dim3(a.nt), dim3(1024), 0, h->stream, a);
-    cpb::launch(cpb::k_head_refine, dim3(1), dim3(1024), 0, h->stream, a);
+    cpb::launch(cpb::k_head_refine, dim3(a.nt), dim3(1024), cpb::head_refine_lds(a.d, a.nc), h->stream, a);
     return hipGetLastError() == hipSuccess ? 0 : fail(CPB_ENODEV, "head launch failed");
 }
 
@@ -415,10 +623,7 @@ int cpb_head_forward_device(cpb_head_t* h, const float* d_x, int32_t* d_chosen) 
     if (!h || !d_x || !d_chosen) return fail(CPB_EINVAL, "NULL argument");
     if (!h->loaded) return fail(CPB_ESTATE, "head not loaded");
     HIP_OK_H(hipSetDevice(h->device));
-    HIP_OK_H(hipMemcpyAsync((void*)h->a.x, d_x, (size_t)h->a.d * 4, hipMemcpyDeviceToDevice, h->stream));
-    if (int r = head_launch(h)) return r;
-    HIP_OK_H(hipMemcpyAsync(d_chosen, h->a.chosen, 4, hipMemcpyDeviceToDevice, h->stream));
-    return 0;
+    return head_launch(h, d_x, d_chosen);
 }
 
 int cpb_head_forward(cpb_head_t* h, const float* x, int32_t* chosen, cpb_head_trace* tr) {
@@ -427,7 +632,7 @@ int cpb_head_forward(cpb_head_t* h, const float* x, int32_t* chosen, cpb_head_tr
     HIP_OK_H(hipSetDevice(h->device));
     const cpb::HeadDev& a = h->a;
     HIP_OK_H(hipMemcpyAsync((void*)a.x, x, (size_t)a.d * 4, hipMemcpyHostToDevice, h->stream));
-    if (int r = head_launch(h)) return r;
+    if (int r = head_launch(h, a.x, a.chosen)) return r;
     HIP_OK_H(hipMemcpyAsync(chosen, a.chosen, 4, hipMemcpyDeviceToHost, h->stream));
     if (tr) {
         const size_t nc = (size_t)a.nt * a.nc;
