@@ -100,27 +100,33 @@ CPB_DEV void wave_best(float& v, int& i) {
     i = bi;
 }
 
+// 64-bit key ordered as better(): the value's bits made monotonic (-0 as +0,
+// as the float comparisons treat them), then the complement of the index
+CPB_DEV uint64_t rank_key(float v, int i) {
+    uint32_t u = v == 0.0f ? 0u : __float_as_uint(v);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((uint64_t)u << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)i);
+}
 // rank of this lane's (value, index) among the wave's 64 (the number of
-// better entries; sentinels (-inf, INT32_MAX) are below every entry).  sv /
-// si: this wave's 64-entry LDS scratch.
-CPB_DEV int wave_rank(float v, int i, float* sv, int* si) {
+// better entries; sentinels (-inf, INT32_MAX) are below every entry).  sk:
+// this wave's 64-entry LDS scratch.
+CPB_DEV int wave_rank(float v, int i, uint64_t* sk) {
     const int lane = threadIdx.x & 63;
-    sv[lane] = v;
-    si[lane] = i;
+    const uint64_t k = rank_key(v, i);
+    sk[lane] = k;
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    int rank = 0;
-#pragma unroll 4
-    for (int q = 0; q < 16; q++) {
-        const float4 ov = ((const float4*)sv)[q];
-        const int4 oi = ((const int4*)si)[q];
-        rank += better(ov.x, oi.x, v, i) + better(ov.y, oi.y, v, i) + better(ov.z, oi.z, v, i) + better(ov.w, oi.w, v, i);
+    int r[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int q = 0; q < 32; q++) {
+        const ulonglong2 o = ((const ulonglong2*)sk)[q];
+        r[q & 3] += (o.x > k) + (o.y > k);
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    return rank;
+    return (r[0] + r[1]) + (r[2] + r[3]);
 }
 
 // ---- load time: Q4Mat + Q8Mat rows from bf16, one thread per (row, block) ----
@@ -232,8 +238,7 @@ __global__ __launch_bounds__(256) void k_head_screen(HeadDev a) {
     uint32_t* xl = (uint32_t*)smem;                    // xq as dwords [nb][8]
     float* xsl = (float*)(xl + nb * 8);                // [nb]
     int32_t* x8 = (int32_t*)(xsl + nb);                // [nb][4]
-    __shared__ __align__(16) float rsv[4][64];
-    __shared__ __align__(16) int rsi[4][64];
+    __shared__ __align__(16) uint64_t rsk[4][64];
     __shared__ float lv[kHeadMaxSlices][4][kHeadMaxCand];
     __shared__ int li[kHeadMaxSlices][4][kHeadMaxCand];
     for (int i = tid; i < nb * 8; i += blockDim.x) xl[i] = ((const uint32_t*)a.xq)[i];
@@ -280,7 +285,7 @@ __global__ __launch_bounds__(256) void k_head_screen(HeadDev a) {
         const bool in = live && row >= r0 && row < r1 && row < a.V && val > -FLT_MAX;
         const float v = in ? val : -INFINITY;
         const int i = in ? row : INT32_MAX;
-        const int rank = wave_rank(v, i, rsv[wave], rsi[wave]);
+        const int rank = wave_rank(v, i, rsk[wave]);
         if (in && rank < C) { lv[w - wa][wave][rank] = v; li[w - wa][wave][rank] = i; }
         const int n_in = __builtin_popcountll(__ballot(in));
         if (lane >= n_in && lane < C) { lv[w - wa][wave][lane] = -INFINITY; li[w - wa][wave][lane] = INT32_MAX; }
@@ -292,7 +297,7 @@ __global__ __launch_bounds__(256) void k_head_screen(HeadDev a) {
         const bool has = lane < 4 * C;
         const float v = has ? lv[w - wa][lane / C][lane % C] : -INFINITY;
         const int i = has ? li[w - wa][lane / C][lane % C] : INT32_MAX;
-        const int rank = wave_rank(v, i, rsv[wave], rsi[wave]);
+        const int rank = wave_rank(v, i, rsk[wave]);
         const size_t slot = (size_t)a.wtab[2 * w + 1] + (size_t)(blockIdx.x - a.wtab[2 * w]) * C;
         const bool real = i != INT32_MAX;
         if (real && rank < C) { a.candv[slot + rank] = v; a.candi[slot + rank] = i; }
@@ -320,6 +325,7 @@ __global__ __launch_bounds__(1024) void k_head_refine(HeadDev a) {
     __shared__ int wi2[4][kHeadMaxCand];
     __shared__ __align__(16) float rsv[kRefineWaves][64];
     __shared__ __align__(16) int rsi[kRefineWaves][64];
+    __shared__ __align__(16) uint64_t rsk[kRefineWaves][64];
     __shared__ int cid[kHeadMaxCand];
     __shared__ float lgs[128];
     __shared__ int ids_s[128];
@@ -341,7 +347,7 @@ __global__ __launch_bounds__(1024) void k_head_refine(HeadDev a) {
             const int e = ch * 64 + lane;
             const float v = e < M ? cv[e] : -INFINITY;
             const int i = e < M ? ci[e] : INT32_MAX;
-            const int rank = wave_rank(v, i, rsv[wave], rsi[wave]);
+            const int rank = wave_rank(v, i, rsk[wave]);
             // lanes C .. 2C - 1: this chunk's best n_cand, then rank the 2C
             float mv = lane < C ? runv : -INFINITY;
             int mi = lane < C ? runi : INT32_MAX;
@@ -355,7 +361,7 @@ __global__ __launch_bounds__(1024) void k_head_refine(HeadDev a) {
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
             if (lane >= C && lane < 2 * C) { mv = rsv[wave][lane]; mi = rsi[wave][lane]; }
-            const int r2 = wave_rank(mv, mi, rsv[wave], rsi[wave]);
+            const int r2 = wave_rank(mv, mi, rsk[wave]);
             rsv[wave][lane] = -INFINITY;
             rsi[wave][lane] = INT32_MAX;
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -375,7 +381,7 @@ __global__ __launch_bounds__(1024) void k_head_refine(HeadDev a) {
     if (wave < 4) {
         const float v = lane < 4 * C ? wv[4 * wave + lane / C][lane % C] : -INFINITY;
         const int i = lane < 4 * C ? wi[4 * wave + lane / C][lane % C] : INT32_MAX;
-        const int rank = wave_rank(v, i, rsv[wave], rsi[wave]);
+        const int rank = wave_rank(v, i, rsk[wave]);
         if (i != INT32_MAX && rank < C) { wv2[wave][rank] = v; wi2[wave][rank] = i; }
         const int n_real = __builtin_popcountll(__ballot(i != INT32_MAX));
         if (lane >= n_real && lane < C) { wv2[wave][lane] = -INFINITY; wi2[wave][lane] = INT32_MAX; }
@@ -385,7 +391,7 @@ __global__ __launch_bounds__(1024) void k_head_refine(HeadDev a) {
     if (wave == 0) {
         const float v = lane < 4 * C ? wv2[lane / C][lane % C] : -INFINITY;
         const int i = lane < 4 * C ? wi2[lane / C][lane % C] : INT32_MAX;
-        const int rank = wave_rank(v, i, rsv[0], rsi[0]);
+        const int rank = wave_rank(v, i, rsk[0]);
         const bool real = i != INT32_MAX;
         if (real && rank < C) {
             cid[rank] = i;
