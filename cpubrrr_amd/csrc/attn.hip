@@ -228,69 +228,89 @@ CPB_DEV float q8c_dot(const u32x4* lw, const float* ls, int nbp, const uint32_t*
     return v01 + dppf<0x4E>(v01);                        // lane 0 of the group: (v0 + v1) + (v2 + v3)
 }
 
-// rmsnorm of x (gpt-oss: 16 fp32 chains over x[16m + q], :710-726) and Q8
-// per 32 (qblock32 :691-699) into LDS: xl dwords / sl scales, padded with
-// zeros to nbp blocks.  xs / ws: x and the norm weights, already in LDS (the
-// barrier at entry publishes them); red: 17 floats.
-CPB_DEV void attn_norm_q8(int d, int nb, int nbp, float eps, const float* xs, const float* ws, float* red, uint32_t* xl,
-                          float* sl, int8_t* gxq, float* gxsb) {
-    const int tid = threadIdx.x;
-    __syncthreads();
-    if (tid < 16) {
-        float acc = 0.0f;
-        const int n16 = d / 16;
-        int m = 0;
-        for (; m + 8 <= n16; m += 8) {
-            float t[8];
+// rmsnorm of x (gpt-oss: 16 fp32 chains, chain q over x[16m + q],
+// :710-726) and Q8 per 32 (qblock32 :691-699) into LDS (xl dwords / sl
+// scales, padded with zeros to nbp blocks).  xr / wr: this thread's float4
+// slots tid + 256k of x and of the norm weights, in registers.  xt: LDS for a
+// transposed copy (chain q's elements contiguous, row stride attn_xt_stride);
+// red: 17 floats.
+CPB_DEV_HOST_INLINE int attn_xt_stride(int d) {
+    int S = (d / 16 + 3) & ~3;
+    return S + ((68 - S % 64) % 64);                  // = 4 (mod 64): 16 lanes' 16-byte reads hit distinct banks
+}
+CPB_DEV void attn_norm_q8(const float4 (&xr)[4], const float4 (&wr)[4], int d, int nb, int nbp, float eps, float* xt,
+                          float* red, uint32_t* xl, float* sl, int8_t* gxq, float* gxsb) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int n16 = d / 16, S = attn_xt_stride(d);
 #pragma unroll
-            for (int u = 0; u < 8; u++) t[u] = xs[(m + u) * 16 + tid];
+    for (int k = 0; k < 4; k++) {
+        const int i = tid + k * 256;
+        if (i * 4 < d) {
+            const float xv[4] = {xr[k].x, xr[k].y, xr[k].z, xr[k].w};
 #pragma unroll
-            for (int u = 0; u < 8; u++) acc = fmaf(t[u], t[u], acc);
+            for (int c = 0; c < 4; c++) {
+                const int e = 4 * i + c;
+                xt[(e & 15) * S + (e >> 4)] = xv[c];
+            }
         }
-        for (; m < n16; m++) { const float t = xs[m * 16 + tid]; acc = fmaf(t, t, acc); }
-        red[tid] = acc;                                   // chain q = 4v + l
     }
+    // zero padding past d / 16: fma(0, 0, acc) leaves acc (>= 0) unchanged
+    for (int e = tid; e < 16 * (S - n16); e += 256) xt[(e & 15) * S + n16 + (e >> 4)] = 0.0f;
     __syncthreads();
-    if (tid == 0) {
+    if (tid < 64) {
+        float acc = 0.0f;
+        if (lane < 16) {
+            const float4* row = (const float4*)(xt + lane * S);
+            for (int j0 = 0; j0 < S / 4; j0 += 16) {
+                float4 t[16];
+#pragma unroll
+                for (int u = 0; u < 16; u++) t[u] = j0 + u < S / 4 ? row[j0 + u] : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+                for (int u = 0; u < 16; u++) {
+                    acc = fmaf(t[u].x, t[u].x, acc);
+                    acc = fmaf(t[u].y, t[u].y, acc);
+                    acc = fmaf(t[u].z, t[u].z, acc);
+                    acc = fmaf(t[u].w, t[u].w, acc);
+                }
+            }
+        }
+        // chain q = 4v + l -> acc[v][l]; L[l] = (a0 + a1) + (a2 + a3); s = (L0 + L1) + (L2 + L3)
+        float c16[16];
+#pragma unroll
+        for (int q = 0; q < 16; q++) c16[q] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), q));
         float L[4];
-        for (int l = 0; l < 4; l++) L[l] = (red[l] + red[4 + l]) + (red[8 + l] + red[12 + l]);
-        float sq = (L[0] + L[1]) + (L[2] + L[3]);
-        for (int i = d - d % 16; i < d; i++) sq += xs[i] * xs[i];
-        red[16] = 1.0f / sqrtf(sq / (float)d + eps);
+#pragma unroll
+        for (int l = 0; l < 4; l++) L[l] = (c16[l] + c16[4 + l]) + (c16[8 + l] + c16[12 + l]);
+        const float sq = (L[0] + L[1]) + (L[2] + L[3]);
+        if (lane == 0) red[16] = 1.0f / sqrtf(sq / (float)d + eps);
     }
     __syncthreads();
     const float inv = red[16];
-    // Q8: 4 lanes per block, 8 values each (bytes 8q .. 8q + 7 = dwords 2q, 2q + 1)
-    for (int e = tid; e < nbp * 4; e += 256) {
-        const int bk = e >> 2, q = e & 3;
-        if (bk < nb) {
-            const int o4 = bk * 8 + 2 * q;
-            const float4 x0 = ((const float4*)xs)[o4], x1 = ((const float4*)xs)[o4 + 1];
-            const float4 w0 = ((const float4*)ws)[o4], w1 = ((const float4*)ws)[o4 + 1];
-            const float v[8] = {x0.x * inv * w0.x, x0.y * inv * w0.y, x0.z * inv * w0.z, x0.w * inv * w0.w,
-                                x1.x * inv * w1.x, x1.y * inv * w1.y, x1.z * inv * w1.z, x1.w * inv * w1.w};
-            float m = 0.0f;
+    // Q8 from registers: slot i = 4 elements, a 32-block = 8 consecutive slots (lanes)
 #pragma unroll
-            for (int u = 0; u < 8; u++) m = fmaxf(m, fabsf(v[u]));
+    for (int k = 0; k < 4; k++) {
+        const int i = tid + k * 256;
+        if (i * 4 < d) {
+            const float v[4] = {xr[k].x * inv * wr[k].x, xr[k].y * inv * wr[k].y, xr[k].z * inv * wr[k].z,
+                                xr[k].w * inv * wr[k].w};
+            float m = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
             m = fmaxf(m, dppf<0xB1>(m));
             m = fmaxf(m, dppf<0x4E>(m));
+            m = fmaxf(m, dppf<0x141>(m));            // the other quad of the 8
             const float sc = fmaxf(1e-12f, m) / 127.0f;
-            uint32_t wd[2] = {0u, 0u};
+            uint32_t wd = 0u;
 #pragma unroll
-            for (int u = 0; u < 8; u++) wd[u >> 2] |= (uint32_t)(uint8_t)q8_round(v[u], sc) << (8 * (u & 3));
-            xl[bk * 8 + 2 * q] = wd[0];
-            xl[bk * 8 + 2 * q + 1] = wd[1];
-            if (q == 0) sl[bk] = sc;
+            for (int u = 0; u < 4; u++) wd |= (uint32_t)(uint8_t)q8_round(v[u], sc) << (8 * u);
+            xl[i] = wd;
+            if ((i & 7) == 0) sl[i >> 3] = sc;
             if (gxq) {
-                ((uint2*)gxq)[bk * 4 + q] = make_uint2(wd[0], wd[1]);
-                if (q == 0) gxsb[bk] = sc;
+                ((uint32_t*)gxq)[i] = wd;
+                if ((i & 7) == 0) gxsb[i >> 3] = sc;
             }
-        } else {
-            xl[bk * 8 + 2 * q] = 0u;
-            xl[bk * 8 + 2 * q + 1] = 0u;
-            if (q == 0) sl[bk] = 0.0f;
         }
     }
+    for (int i = d / 4 + tid; i < nbp * 8; i += 256) xl[i] = 0u;
+    for (int bk = nb + tid; bk < nbp; bk += 256) sl[bk] = 0.0f;
 }
 
 // ---- rmsnorm + Q8 of x, q / k / v rows + bias + RoPE + cache ----
@@ -304,9 +324,8 @@ __global__ __launch_bounds__(256) void k_attn_qkv(AttnArgs a) {
     const int nbp = q8c_nbp(a.nb), nsp = nbp / 4, ns = nbp / 2;
     u32x4* lw = (u32x4*)smem;                         // [2][nsp * 64]
     float* ls = (float*)(lw + 2 * nsp * 64);          // [2][ns * 16]
-    float* xs = ls + 2 * ns * 16;                     // [d]
-    float* ws = xs + a.d;                             // [d]
-    float* red = ws + a.d;                            // [64]
+    float* xt = ls + 2 * ns * 16;                     // [16][attn_xt_stride(d)] transposed x
+    float* red = xt + 16 * attn_xt_stride(a.d);       // [64]
     uint32_t* xl = (uint32_t*)(red + 64);             // [nbp * 8]
     float* sl = (float*)(xl + nbp * 8);               // [nbp]
     __shared__ float hv[16];
@@ -342,13 +361,7 @@ __global__ __launch_bounds__(256) void k_attn_qkv(AttnArgs a) {
     {
         StageRegs g;
         stage_issue(ts, 0, g, true);
-#pragma unroll
-        for (int k4 = 0; k4 < 4; k4++)
-            if ((tid + k4 * 256) * 4 < a.d) {
-                ((float4*)xs)[tid + k4 * 256] = xr[k4];
-                ((float4*)ws)[tid + k4 * 256] = wr[k4];
-            }
-        attn_norm_q8(a.d, a.nb, nbp, a.eps, xs, ws, red, xl, sl, blockIdx.x == 0 ? a.xq : nullptr, a.xsb);
+        attn_norm_q8(xr, wr, a.d, a.nb, nbp, a.eps, xt, red, xl, sl, blockIdx.x == 0 ? a.xq : nullptr, a.xsb);
         stage_commit(ts, 0, g, true, lw, ls);
         for (int b0 = kStageBatch * 256; b0 < 2 * nsp * 64; b0 += kStageBatch * 256) {
             stage_issue(ts, b0, g, false);
@@ -462,8 +475,12 @@ __global__ __launch_bounds__(256) void k_attn_core(AttnArgs a) {
         }
     }
     __syncthreads();
-    for (int hl = wave, t = 0; hl < R; hl += 4, t++) {
-        const int h = kvh * R + hl;
+    // wave w: q-heads w and w + 4 of the group (the second absent when R <= 4)
+    float mv[2] = {0.0f, 0.0f}, sv[2] = {0.0f, 0.0f};
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+        const int hl = wave + 4 * t;
+        if (hl >= R) break;
         float4 qv[16];
 #pragma unroll
         for (int i = 0; i < 16; i++) qv[i] = *(const float4*)&qs[hl][4 * i];
@@ -473,38 +490,52 @@ __global__ __launch_bounds__(256) void k_attn_core(AttnArgs a) {
         if (a.nsplit == 1) m = fmaxf(m, sinkr[t]);       // one chunk: the sink joins the max here
         const float e0 = lane < cnt ? expf(s0 - m) : 0.0f;
         const float e1 = lane + 64 < cnt ? expf(s1 - m) : 0.0f;
-        const float sum = wave_sum_f32(e0 + e1);
+        sv[t] = wave_sum_f32(e0 + e1);
+        mv[t] = m;
         es[hl][lane] = e0;
         es[hl][lane + 64] = e1;
-        wave_sync_lds();
-        // weighted v, dimension lane: 4 positions per pair of 16-byte reads
-        float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    wave_sync_lds();
+    if (wave < R) {
+        // weighted v, dimension lane, both heads over one read of each 4 positions
+        const int h0 = wave, h1 = wave + 4 < R ? wave + 4 : wave;
+        float o0[4] = {0.0f, 0.0f, 0.0f, 0.0f}, o1[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         int p = 0;
+#pragma unroll 4
         for (; p + 4 <= cnt; p += 4) {
             const float4 vv = *(const float4*)&vs[lane][p];
-            const float4 ee = *(const float4*)&es[hl][p];
-            o[0] = fmaf(vv.x, ee.x, o[0]);
-            o[1] = fmaf(vv.y, ee.y, o[1]);
-            o[2] = fmaf(vv.z, ee.z, o[2]);
-            o[3] = fmaf(vv.w, ee.w, o[3]);
+            const float4 e0 = *(const float4*)&es[h0][p], e1 = *(const float4*)&es[h1][p];
+            o0[0] = fmaf(vv.x, e0.x, o0[0]); o0[1] = fmaf(vv.y, e0.y, o0[1]);
+            o0[2] = fmaf(vv.z, e0.z, o0[2]); o0[3] = fmaf(vv.w, e0.w, o0[3]);
+            o1[0] = fmaf(vv.x, e1.x, o1[0]); o1[1] = fmaf(vv.y, e1.y, o1[1]);
+            o1[2] = fmaf(vv.z, e1.z, o1[2]); o1[3] = fmaf(vv.w, e1.w, o1[3]);
         }
-        for (; p < cnt; p++) o[0] = fmaf(vs[lane][p], es[hl][p], o[0]);
-        const float ov = (o[0] + o[1]) + (o[2] + o[3]);
-        if (a.nsplit == 1) {
-            // softmax with the sink in the denominator, then Q8 of the head
-            const float val = ov / (expf(sinkr[t] - m) + sum);
-            a.ao[h * kAttnHd + lane] = val;
-            const float mb = half_max_f32(fabsf(val));
-            const float scq = fmaxf(1e-12f, mb) / 127.0f;
-            a.aq[h * kAttnHd + lane] = (int8_t)q8_round(val, scq);
-            if ((lane & 31) == 0) a.asb[h * 2 + (lane >> 5)] = scq;
-        } else {
-            // coherent (write-through) stores: read by another workgroup of this launch
-            float* pp = a.part + ((size_t)h * a.nsplit + split) * 66;
-            st_dev(pp + 2 + lane, ov);
-            if (lane == 0) {
-                st_dev(pp, m);
-                st_dev(pp + 1, sum);
+        for (; p < cnt; p++) {
+            o0[0] = fmaf(vs[lane][p], es[h0][p], o0[0]);
+            o1[0] = fmaf(vs[lane][p], es[h1][p], o1[0]);
+        }
+        const float ovs[2] = {(o0[0] + o0[1]) + (o0[2] + o0[3]), (o1[0] + o1[1]) + (o1[2] + o1[3])};
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            if (wave + 4 * t >= R) break;
+            const int h = kvh * R + wave + 4 * t;
+            const float ov = ovs[t];
+            if (a.nsplit == 1) {
+                // softmax with the sink in the denominator, then Q8 of the head
+                const float val = ov / (expf(sinkr[t] - mv[t]) + sv[t]);
+                a.ao[h * kAttnHd + lane] = val;
+                const float mb = half_max_f32(fabsf(val));
+                const float scq = fmaxf(1e-12f, mb) / 127.0f;
+                a.aq[h * kAttnHd + lane] = (int8_t)q8_round(val, scq);
+                if ((lane & 31) == 0) a.asb[h * 2 + (lane >> 5)] = scq;
+            } else {
+                // coherent (write-through) stores: read by another workgroup of this launch
+                float* pp = a.part + ((size_t)h * a.nsplit + split) * 66;
+                st_dev(pp + 2 + lane, ov);
+                if (lane == 0) {
+                    st_dev(pp, mv[t]);
+                    st_dev(pp + 1, sv[t]);
+                }
             }
         }
     }
@@ -720,7 +751,7 @@ int cpb_attn_create(const cpb_attn_cfg* cfg, int device, cpb_attn_t** out) {
     // LDS beyond 64 KiB per workgroup (d = 4096: 110 KiB for k_attn_qkv) is opted into
     {
         const int nbp = cpb::q8c_nbp(cfg->d / 32), nbpo = cpb::q8c_nbp(cfg->n_head * 2);
-        const int lq = 2 * (nbp / 4) * 1024 + 2 * (nbp / 2) * 64 + 4 * (2 * cfg->d + 64) + nbp * 36;
+        const int lq = 2 * (nbp / 4) * 1024 + 2 * (nbp / 2) * 64 + 4 * (16 * cpb::attn_xt_stride(cfg->d) + 64) + nbp * 36;
         const int lo = (nbpo / 4) * 1024 + (nbpo / 2) * 64 + nbpo * 36;
         if (hipFuncSetAttribute((const void*)cpb::k_attn_qkv, hipFuncAttributeMaxDynamicSharedMemorySize, lq) != hipSuccess ||
             hipFuncSetAttribute((const void*)cpb::k_attn_oproj, hipFuncAttributeMaxDynamicSharedMemorySize, lo) != hipSuccess)
@@ -811,8 +842,8 @@ static int attn_launch(cpb_attn_t* h, int layer, int pos, float* dx) {
     a.part = h->part; a.count = h->count;
     const int nbp = cpb::q8c_nbp(a.nb), nbpo = cpb::q8c_nbp(a.nbo);
     // LDS: two tiles' codes (nbp / 4 step pairs x 1 KiB) and scales (nbp / 2 x 64 B), x, xn, activations
-    const size_t lds_qkv = (size_t)2 * (nbp / 4) * 1024 + (size_t)2 * (nbp / 2) * 64 + sizeof(float) * (2 * c.d + 64) +
-                           (size_t)nbp * 36;     // codes, scales, x, norm weights, 64, activations
+    const size_t lds_qkv = (size_t)2 * (nbp / 4) * 1024 + (size_t)2 * (nbp / 2) * 64 +
+                           sizeof(float) * (16 * cpb::attn_xt_stride(c.d) + 64) + (size_t)nbp * 36;   // codes, scales, x^T, 64, activations
     const size_t lds_o = (size_t)(nbpo / 4) * 1024 + (size_t)(nbpo / 2) * 64 + (size_t)nbpo * 36;
     cpb::launch(cpb::k_attn_qkv, dim3((c.n_head + 2 * c.n_head_kv) * 4), dim3(256), lds_qkv, h->stream, a);
     cpb::launch(cpb::k_attn_core, dim3(c.n_head_kv, a.nsplit), dim3(256), 0, h->stream, a);
