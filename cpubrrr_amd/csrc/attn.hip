@@ -490,31 +490,62 @@ __global__ __launch_bounds__(256) void k_attn_core(AttnArgs a) {
         if (a.nsplit == 1) m = fmaxf(m, sinkr[t]);       // one chunk: the sink joins the max here
         const float e0 = lane < cnt ? expf(s0 - m) : 0.0f;
         const float e1 = lane + 64 < cnt ? expf(s1 - m) : 0.0f;
-        sv[t] = wave_sum_f32(e0 + e1);
+        if (a.nsplit > 1) sv[t] = wave_sum_f32(e0 + e1);
         mv[t] = m;
         es[hl][lane] = e0;
         es[hl][lane + 64] = e1;
     }
     wave_sync_lds();
     if (wave < R) {
-        // weighted v, dimension lane, both heads over one read of each 4 positions
         const int h0 = wave, h1 = wave + 4 < R ? wave + 4 : wave;
-        float o0[4] = {0.0f, 0.0f, 0.0f, 0.0f}, o1[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        int p = 0;
+        float ovs[2], dens[2] = {1.0f, 1.0f};
+        if (a.nsplit == 1) {
+            // the reference's order (:823-831): den = exp(sink - mx), then += e in
+            // position order; per dimension one fma chain over the positions; ao
+            // = acc * (1 / den)
+            float acc0 = 0.0f, acc1 = 0.0f, d0 = expf(sinkr[0] - mv[0]), d1 = expf(sinkr[1] - mv[1]);
+            int p = 0;
+#pragma unroll 2
+            for (; p + 4 <= cnt; p += 4) {
+                const float4 vv = *(const float4*)&vs[lane][p];
+                const float4 e0 = *(const float4*)&es[h0][p], e1 = *(const float4*)&es[h1][p];
+                acc0 = fmaf(vv.x, e0.x, acc0); acc0 = fmaf(vv.y, e0.y, acc0);
+                acc0 = fmaf(vv.z, e0.z, acc0); acc0 = fmaf(vv.w, e0.w, acc0);
+                acc1 = fmaf(vv.x, e1.x, acc1); acc1 = fmaf(vv.y, e1.y, acc1);
+                acc1 = fmaf(vv.z, e1.z, acc1); acc1 = fmaf(vv.w, e1.w, acc1);
+                d0 += e0.x; d0 += e0.y; d0 += e0.z; d0 += e0.w;
+                d1 += e1.x; d1 += e1.y; d1 += e1.z; d1 += e1.w;
+            }
+            for (; p < cnt; p++) {
+                acc0 = fmaf(vs[lane][p], es[h0][p], acc0);
+                acc1 = fmaf(vs[lane][p], es[h1][p], acc1);
+                d0 += es[h0][p];
+                d1 += es[h1][p];
+            }
+            ovs[0] = acc0;
+            ovs[1] = acc1;
+            dens[0] = d0;
+            dens[1] = d1;
+        } else {
+            // one chunk of several: 4 position chains, merged below with the sink
+            float o0[4] = {0.0f, 0.0f, 0.0f, 0.0f}, o1[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            int p = 0;
 #pragma unroll 4
-        for (; p + 4 <= cnt; p += 4) {
-            const float4 vv = *(const float4*)&vs[lane][p];
-            const float4 e0 = *(const float4*)&es[h0][p], e1 = *(const float4*)&es[h1][p];
-            o0[0] = fmaf(vv.x, e0.x, o0[0]); o0[1] = fmaf(vv.y, e0.y, o0[1]);
-            o0[2] = fmaf(vv.z, e0.z, o0[2]); o0[3] = fmaf(vv.w, e0.w, o0[3]);
-            o1[0] = fmaf(vv.x, e1.x, o1[0]); o1[1] = fmaf(vv.y, e1.y, o1[1]);
-            o1[2] = fmaf(vv.z, e1.z, o1[2]); o1[3] = fmaf(vv.w, e1.w, o1[3]);
+            for (; p + 4 <= cnt; p += 4) {
+                const float4 vv = *(const float4*)&vs[lane][p];
+                const float4 e0 = *(const float4*)&es[h0][p], e1 = *(const float4*)&es[h1][p];
+                o0[0] = fmaf(vv.x, e0.x, o0[0]); o0[1] = fmaf(vv.y, e0.y, o0[1]);
+                o0[2] = fmaf(vv.z, e0.z, o0[2]); o0[3] = fmaf(vv.w, e0.w, o0[3]);
+                o1[0] = fmaf(vv.x, e1.x, o1[0]); o1[1] = fmaf(vv.y, e1.y, o1[1]);
+                o1[2] = fmaf(vv.z, e1.z, o1[2]); o1[3] = fmaf(vv.w, e1.w, o1[3]);
+            }
+            for (; p < cnt; p++) {
+                o0[0] = fmaf(vs[lane][p], es[h0][p], o0[0]);
+                o1[0] = fmaf(vs[lane][p], es[h1][p], o1[0]);
+            }
+            ovs[0] = (o0[0] + o0[1]) + (o0[2] + o0[3]);
+            ovs[1] = (o1[0] + o1[1]) + (o1[2] + o1[3]);
         }
-        for (; p < cnt; p++) {
-            o0[0] = fmaf(vs[lane][p], es[h0][p], o0[0]);
-            o1[0] = fmaf(vs[lane][p], es[h1][p], o1[0]);
-        }
-        const float ovs[2] = {(o0[0] + o0[1]) + (o0[2] + o0[3]), (o1[0] + o1[1]) + (o1[2] + o1[3])};
 #pragma unroll
         for (int t = 0; t < 2; t++) {
             if (wave + 4 * t >= R) break;
@@ -522,7 +553,7 @@ __global__ __launch_bounds__(256) void k_attn_core(AttnArgs a) {
             const float ov = ovs[t];
             if (a.nsplit == 1) {
                 // softmax with the sink in the denominator, then Q8 of the head
-                const float val = ov / (expf(sinkr[t] - mv[t]) + sv[t]);
+                const float val = ov * (1.0f / dens[t]);
                 a.ao[h * kAttnHd + lane] = val;
                 const float mb = half_max_f32(fabsf(val));
                 const float scq = fmaxf(1e-12f, mb) / 127.0f;
@@ -582,7 +613,7 @@ __global__ __launch_bounds__(256) void k_attn_core(AttnArgs a) {
         }
         den = wave_sum_f32(den);
         den += expf(sink - M);
-        const float val = acc / den;
+        const float val = acc * (1.0f / den);
         a.ao[h * kAttnHd + lane] = val;
         const float mb = half_max_f32(fabsf(val));
         const float scq = fmaxf(1e-12f, mb) / 127.0f;
