@@ -65,6 +65,10 @@ CONFIGS = {
                  "at position 1024 with the KV cache filled, Q8 projections",
             d=2880, dff=0, ne=0, k=0, layers=24, per_step=24, zipf=None, norm=True, family="attn", n_head=64,
             n_head_kv=8, swa=128, pos=1024),
+    8: dict(name="config8: gpt-oss-20b whole decode step on the GPU: 24 x (attention at position 1024 + MoE, Zipf(1.1) "
+                 "router bias) + two-stage LM head, one captured graph per token",
+            d=2880, dff=2880, ne=32, k=4, layers=24, per_step=24, zipf=1.1, norm=True, family="step", n_head=64,
+            n_head_kv=8, swa=128, pos=1024, vocab=201088),
 }
 for _c in CONFIGS.values():
     _c.setdefault("family", "gptoss")
@@ -322,6 +326,148 @@ def bench_attn(args, c) -> int:
     return 0
 
 
+def bench_step(args, c) -> int:
+    """config 8: one token through 24 x (attention + MoE) and the head, the
+    whole step captured as one graph (the library's launches land in the
+    caller's graph); value = bytes the step reads / time."""
+    import numpy as np
+    import torch
+
+    from cpubrrr_amd import Attention, LmHead, MoeBlock, MoeConfig, synth
+
+    d, nl, pos, V = c["d"], c["layers"], c["pos"], c["vocab"]
+    torch.cuda.set_device(0)
+    t0 = time.perf_counter()
+    at = Attention(d, c["n_head"], c["n_head_kv"], nl, max_seq=pos + 1, sliding_window=c["swa"], rope_base=150000.0,
+                   rms_eps=1e-5)
+    cfg = MoeConfig.gptoss(d=d, n_expert=c["ne"], top_k=c["k"], d_ff=c["dff"], n_layer=nl)
+    moe = MoeBlock(cfg)
+    host_attn0 = host_moe0 = None
+    for l in range(nl):
+        A = synth.attn_layer(d, c["n_head"], c["n_head_kv"], 64, seed=0, layer=l, swa=c["swa"])
+        at.load_layer(l, A)
+        M = synth.gptoss_layer(d, c["dff"], c["ne"], c["k"], seed=0, layer=l, zipf=c["zipf"])
+        moe.load_layer(l, M)
+        if l == 0:
+            host_attn0, host_moe0 = A, M
+        del A, M
+    r = np.random.default_rng(0)
+    w32 = (r.standard_normal((V, d)) * 0.02).astype(np.float32)
+    w_out = ((w32.view(np.uint32).astype(np.uint64) + 0x7FFF + ((w32.view(np.uint32) >> 16) & 1)) >> 16).astype(np.uint16)
+    del w32
+    n_out = np.ones(d, np.float32)
+    hd = LmHead(d, V)
+    hd.load(w_out, n_out)
+    log(f"loaded {nl} attention + MoE layers and the head in {time.perf_counter() - t0:.1f} s")
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
+    for h in (at, moe, hd):
+        h.set_stream(stream.cuda_stream)
+    x = torch.from_numpy(synth.token(d, 0, 7)).to("cuda:0")
+    ch = torch.zeros(1, dtype=torch.int32, device="cuda:0")
+    # the cache: positions 0 .. pos-1 through the attention layers
+    for p in range(pos):
+        for l in range(nl):
+            at.forward_device(l, p, x.data_ptr())
+        x.mul_(0.5)
+    torch.cuda.synchronize()
+    x0 = torch.from_numpy(synth.token(d, 0, 8)).to("cuda:0")
+    xs = x0.clone()
+    torch.cuda.synchronize()
+
+    def token_step():
+        for l in range(nl):
+            at.forward_device(l, pos, xs.data_ptr())
+            moe.forward_device(l, 1, xs.data_ptr(), 1, True)
+        hd.forward_device(xs.data_ptr(), ch.data_ptr())
+
+    token_step()                           # eager once (the MoE layers' buffers exist before capture)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        token_step()
+    for _ in range(args.warmup):
+        xs.copy_(x0)
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(args.steps):
+        xs.copy_(x0)
+        g.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    assert torch.isfinite(xs).all().item()
+    moe_b = layer_bytes(dict(c, family="gptoss"))["total"] * nl
+    ab = attn_bytes(c)["per_token"]
+    nb = d // 32
+    head_b = V * nb * 18 + 96 * (d + nb * 4)
+    total = moe_b + ab + head_b
+    gbs = total / (ms * 1e-3) / 1e9
+    out = {"metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+           "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "dtype": "int8 x MXFP4 / Q8 / Q4 (fp32 softmax, routing)", "data": "synthetic",
+           "config": {"workload": c["name"], "d": d, "layers": nl, "pos": pos, "n_expert": c["ne"], "top_k": c["k"],
+                      "n_vocab": V},
+           "tok_per_s": round(1e3 / ms, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+           "bytes_per_token": {"moe": moe_b, "attention": ab, "head": head_b},
+           # the reference's own end-to-end decode figure, on its hardware (context, not the same metric)
+           "reference_published": {"value": 90.1, "unit": "tok/s", "hardware": "Apple M4 Max CPU",
+                                   "source": "README.md:19 (BASELINE.md section 1)"},
+           "roofline": {"bound": "hbm", "kernel": "whole decode step (24 x 6 kernels + 3)", "achieved": round(gbs, 1),
+                        "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                        "bytes_per_launch": total}}
+    for h in (hd, moe, at):
+        h.close()
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline_step(host_attn0, host_moe0, w_out, n_out, c, args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def cpu_baseline_step(A, M, w_out, n_out, c, budget_s: float) -> dict:
+    """The oracle's decode step at the same shapes: attention (single-threaded
+    C) and MoE (C, OpenMP) of one layer per step of the sample, scaled to the
+    24 layers, plus the head on pre-quantised rows."""
+    import numpy as np
+    from oracle import oracle as O
+
+    info = _host_info()
+    threads = info["usable"]
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        threads = min(threads, int(os.environ["OMP_NUM_THREADS"]))
+    O.set_threads(threads)
+    pos, nkv = c["pos"], c["n_head_kv"]
+    Lq = dict(A)
+    for n in ("q", "k", "v", "o"):
+        Lq["w" + n], Lq["s" + n] = O.q8_rows(A["w" + n])
+    tab = O.rope_table(64, pos + 1, 150000.0)
+    r = np.random.default_rng(1)
+    kc = r.standard_normal((pos + 1, nkv, 64)).astype(np.float32)
+    vc = r.standard_normal((pos + 1, nkv, 64)).astype(np.float32)
+    x = r.standard_normal(c["d"]).astype(np.float32)
+    pre = O.q4_quant_rows(w_out)
+    n, t_layers, t_head = 0, 0.0, 0.0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < budget_s or n < 2:
+        t1 = time.perf_counter()
+        xa, _ = O.attn_layer(Lq, n % 2, pos, x, kc, vc, tab)
+        xm, _ = O.gptoss_moe(M, xa, True)
+        t2 = time.perf_counter()
+        O.head(w_out, xm, n_out, 1e-5, pre=pre)
+        t3 = time.perf_counter()
+        t_layers += t2 - t1
+        t_head += t3 - t2
+        n += 1
+    per_tok = t_layers / n * c["layers"] + t_head / n
+    return {"value": round(1.0 / per_tok, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"{n} (attention + MoE layer + head) evaluations in {t_layers + t_head:.1f} s on {threads} threads "
+                      f"(attention single-threaded); {t_layers / n * 1e3:.1f} ms per layer, {t_head / n * 1e3:.1f} ms "
+                      f"head, scaled to {c['layers']} layers + head",
+            "ms_per_token": round(per_tok * 1e3, 2)}
+
+
 def cpu_baseline_attn(L, c, budget_s: float) -> dict:
     """The oracle's attention step (single-threaded C, the reference's fp32
     order) at the same shape and position, on random cache contents."""
@@ -396,6 +542,8 @@ def main() -> int:
         return bench_head(args, c)
     if c["family"] == "attn":
         return bench_attn(args, c)
+    if c["family"] == "step":
+        return bench_step(args, c)
     d, dff, ne, k, nl = c["d"], c["dff"], c["ne"], c["k"], c["layers"]
     qwen = c["family"] == "qwen"
     if qwen:
