@@ -3,7 +3,7 @@
     python bench.py [--config 1] [--steps K] [--warmup W] [--gpus 1]
 
 A step is one decode token through the workload's MoE layers with all
-inputs resident in HBM.  Workloads (BASELINE.json configs, synthetic data):
+inputs resident in HBM.  Workloads (synthetic data):
   0  gpt-oss-20b single MoE layer (rotating 8 distinct layer copies so the
      256 MB Infinity Cache cannot hold the active experts)
   1  gpt-oss-20b 24-layer MoE stack, Zipf(1.1) router bias   (default)
@@ -11,10 +11,12 @@ inputs resident in HBM.  Workloads (synthetic data):
   3  Qwen3-30B-A3B 48-layer MoE stack: Q4_K gate/up, Q6_K down, top-8 of 128
   4  gpt-oss-20b layer, 512-token prefill: tokens grouped by expert, expert
      GEMMs on the matrix cores (8 rotating layer copies)
-  5  Qwen3-30B-A3B layer, 512-token prefill on the int8 matrix cores (not a
-     BASELINE config; the batched k-quant path beside config 4)
-  6  gpt-oss two-stage LM head, 201088 x 2880 (not a BASELINE config): Q4
+  5  Qwen3-30B-A3B layer, 512-token prefill on the int8 matrix cores (the
+     batched k-quant path beside config 4)
+  6  gpt-oss two-stage LM head, 201088 x 2880: Q4
      screen of every row, exact Q8 refine of 96 candidates, greedy
+  7  gpt-oss-20b attention, 24 layers, one token at position 1024
+  8  gpt-oss-20b whole decode step: 24 x (attention + MoE) + head, one graph
 Prints one JSON line: value = expert-weight GB/s (algorithmic bytes of the
 active experts + biases + router per token / time), plus tok/s, the roofline
 of the dominant kernel (gate/up) and the CPU baseline (the oracle on the
@@ -414,7 +416,7 @@ def bench_step(args, c) -> int:
            "bytes_per_token": {"moe": moe_b, "attention": ab, "head": head_b},
            # the reference's own end-to-end decode figure, on its hardware (context, not the same metric)
            "reference_published": {"value": 90.1, "unit": "tok/s", "hardware": "Apple M4 Max CPU",
-                                   "source": "README.md:19 (BASELINE.md section 1)"},
+                                   "source": "the reference's README.md:19"},
            "roofline": {"bound": "hbm", "kernel": "whole decode step (24 x 6 kernels + 3)", "achieved": round(gbs, 1),
                         "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
                         "bytes_per_launch": total}}

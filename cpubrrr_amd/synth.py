@@ -1,8 +1,8 @@
-"""Synthetic workloads of the BASELINE configs, generated through the C ABI
+"""Synthetic workloads of the bench configs, generated through the C ABI
 (cpb_synth_*) so the host here, the GPU box and every test produce identical
 bytes from (seed, layer).
 
-Distributions (BASELINE.json configs):
+Distributions:
   MXFP4 codes uniform over 16 values, e8m0 = 127 + U{-6..-3};
   expert biases N(0, 0.01); router N(0, 0.02), bias 0 (config 0) or
   Zipf(1.1) over a seeded expert permutation (stacks); input x N(0, 1);
@@ -91,7 +91,7 @@ def qwen_layer(d: int, dff: int, ne: int, k: int, seed: int = 0, layer: int = 0,
 
 
 def token(d: int, seed: int = 0, index: int = 0) -> np.ndarray:
-    """fp32 N(0,1) activation (BASELINE: input after RMSNorm for config 0)."""
+    """fp32 N(0,1) activation (config 0 feeds it as the input after RMSNorm)."""
     return normal(d, 1.0, seed, 1_000_000 + index)
 
 

@@ -1,6 +1,6 @@
 /* cpb_synth.h -- deterministic synthetic weights and activations.
  *
- * Generates the BASELINE workloads' tensors from (seed, stream) so that the
+ * Generates the bench workloads' tensors from (seed, stream) so that the
  * host here, the GPU box and every test produce identical bytes.  Counter
  * based (splitmix64 finaliser of key + index), so any slice can be generated
  * independently and in parallel.  Host-only; no GPU calls.
@@ -23,7 +23,7 @@ extern "C" {
 uint64_t cpb_synth_u64(uint64_t seed, uint64_t stream, uint64_t i);
 
 /* MXFP4 GGUF blocks: nblocks x 17 bytes; e8m0 byte = e_lo + U{0..e_span-1},
- * nibbles uniform over all 16 codes.  (e_lo=121, e_span=4
+ * nibbles uniform over all 16 codes.  (bench config 0: e_lo=121, e_span=4
  * i.e. exponent uniform in [-6,-3].) */
 void cpb_synth_mxfp4(uint8_t* out, size_t nblocks, int e_lo, int e_span, uint64_t seed, uint64_t stream);
 

@@ -86,7 +86,7 @@ typedef struct orc_gptoss_layer {
 } orc_gptoss_layer;
 
 /* engine_gpt2.rs:845-923: x <- x + sum_ei w_ei * (down_e(hq_ei) + down_b_e).
- * apply_norm=0 feeds x itself as xn (input already normed). */
+ * apply_norm=0 feeds x itself as xn (config 0 of the bench: input already normed). */
 void orc_gptoss_moe(const orc_gptoss_layer* L, float* x, int apply_norm, orc_trace* tr);
 
 typedef struct orc_qwen_layer {

@@ -1,4 +1,4 @@
-"""GPU parity at the BASELINE configs' own sizes.
+"""GPU parity at the bench configs' own sizes.
 
 - config 2 shape: d = 2880, 128 experts, top-4, Zipf(1.1) router bias, with
   the norm (two layers of the 36-layer stack), traced against the oracle;

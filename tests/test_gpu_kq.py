@@ -88,7 +88,7 @@ def test_qwen_q4k_down(gpu):
 
 
 def test_qwen_config3_layer(gpu):
-    # BASELINE config 3 layer shape: d 2048, 128 experts, top-8, d_ff 768
+    # bench config 3 layer shape: d 2048, 128 experts, top-8, d_ff 768
     for layer in (0, 5):
         run_qwen(2048, 768, 128, 8, seed=0, layer=layer)
 

@@ -4,7 +4,7 @@ Bit-exact: xn, xq, xsb (Q8 activation bytes and scales), expert ids, int32
 block sums of gate/up and (given the same hq) of down.  To tolerance: router
 logits (within the serial-sum bound), softmax weights, gate/up outputs, hq/hsb
 (SwiGLU goes through expf) and the layer output (max-abs <= 1e-3 * RMS of the
-FFN output, BASELINE north_star).
+FFN output).
 """
 import numpy as np
 import pytest
@@ -74,7 +74,7 @@ def test_small_shapes(gpu):
 
 
 def test_config0_layer(gpu):
-    # gpt-oss-20b layer, seed 0, input already normed
+    # bench config 0: gpt-oss-20b layer, seed 0, input already normed
     run_case(2880, 2880, 32, 4, seed=0, apply_norm=False)
 
 
