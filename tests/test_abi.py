@@ -84,3 +84,48 @@ def test_synth_deterministic():
     assert abs(p.sum() - 1) < 1e-5 and np.allclose(np.sort(p)[::-1], (np.arange(1, 33) ** -1.1) / (np.arange(1, 33) ** -1.1).sum(), rtol=1e-5)
     for v in (0.0, 1.0, -2.5, 65504.0, 1e-5, 3e-8, 0.1, 7e4):
         assert L.lib().cpb_f32_to_half(v) == np.float16(v).view(np.uint16)
+
+
+@pytest.mark.parametrize("mut", [
+    dict(head_dim=128), dict(d=2880 + 16), dict(d=8192), dict(n_head_kv=3), dict(n_head=0),
+    dict(n_head=64, n_head_kv=4), dict(n_layer=0), dict(max_seq=0), dict(max_seq=1 << 14), dict(sliding_window=0),
+])
+def test_attention_bad_configs_rejected(mut):
+    # checked before any device is touched (GPU or not)
+    base = dict(d=2880, n_head=64, n_head_kv=8, head_dim=64, n_layer=2, max_seq=64, sliding_window=128,
+                rope_base=150000.0, rms_eps=1e-5)
+    base.update(mut)
+    c = L.AttnCfg(**base)
+    h = C.c_void_p()
+    assert L.lib().cpb_attn_create(C.byref(c), 0, C.byref(h)) == L.CPB_EINVAL, mut
+    assert not h.value
+
+
+@pytest.mark.parametrize("mut", [
+    dict(d=100), dict(d=8192), dict(n_vocab=1001), dict(n_vocab=0), dict(n_slices=0), dict(n_slices=33),
+    dict(n_cand=0), dict(n_cand=17), dict(n_slices=32, n_cand=8),
+])
+def test_head_bad_configs_rejected(mut):
+    base = dict(d=2880, n_vocab=4096, n_slices=12, n_cand=8, rms_eps=1e-5)
+    base.update(mut)
+    c = L.HeadCfg(**base)
+    h = C.c_void_p()
+    assert L.lib().cpb_head_create(C.byref(c), 0, C.byref(h)) == L.CPB_EINVAL, mut
+    assert not h.value
+    n = C.c_size_t()
+    assert L.lib().cpb_head_bytes(C.byref(c), C.byref(n)) == L.CPB_EINVAL
+
+
+def test_attention_and_head_null_args():
+    lib = L.lib()
+    assert lib.cpb_attn_create(None, 0, None) == L.CPB_EINVAL
+    assert lib.cpb_attn_forward(None, 0, 0, None, None) == L.CPB_EINVAL
+    assert lib.cpb_attn_forward_device(None, 0, 0, None) == L.CPB_EINVAL
+    assert lib.cpb_attn_reset(None) == L.CPB_EINVAL
+    assert lib.cpb_attn_sync(None) == L.CPB_EINVAL
+    lib.cpb_attn_destroy(None)
+    assert lib.cpb_head_create(None, 0, None) == L.CPB_EINVAL
+    assert lib.cpb_head_forward(None, None, None, None) == L.CPB_EINVAL
+    assert lib.cpb_head_forward_device(None, None, None) == L.CPB_EINVAL
+    assert lib.cpb_head_sync(None) == L.CPB_EINVAL
+    lib.cpb_head_destroy(None)
