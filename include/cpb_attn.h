@@ -62,6 +62,12 @@ int  cpb_attn_forward(cpb_attn_t* h, int layer, int pos, float* x, cpb_attn_trac
 int  cpb_attn_forward_device(cpb_attn_t* h, int layer, int pos, float* d_x);
 /* Forget every cached position (a new sequence). */
 int  cpb_attn_reset(cpb_attn_t* h);
+/* Calls on one handle run in order on its stream (set_stream waits for the
+ * old stream's work).  Two calls that overlap -- the same handle driven from
+ * two streams at once -- race on its scratch, the cache and the arrival
+ * counters.  Launches of cpb_attn_forward_device may be captured into a
+ * caller's graph (they record no memset); the position is part of what is
+ * captured. */
 int  cpb_attn_set_stream(cpb_attn_t* h, void* stream);
 int  cpb_attn_sync(cpb_attn_t* h);
 void cpb_attn_destroy(cpb_attn_t* h);

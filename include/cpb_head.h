@@ -49,6 +49,9 @@ int  cpb_head_load(cpb_head_t* h, const uint16_t* out_w, const float* out_norm);
 int  cpb_head_forward(cpb_head_t* h, const float* x, int32_t* chosen, cpb_head_trace* trace);
 /* Device x [d] and device *chosen, asynchronous on the handle's stream. */
 int  cpb_head_forward_device(cpb_head_t* h, const float* d_x, int32_t* d_chosen);
+/* Calls on one handle run in order on its stream (set_stream waits for the
+ * old stream's work).  Two calls that overlap -- the same handle driven from
+ * two streams at once -- race on its scratch and its arrival counter. */
 int  cpb_head_set_stream(cpb_head_t* h, void* stream);
 int  cpb_head_sync(cpb_head_t* h);
 void cpb_head_destroy(cpb_head_t* h);
