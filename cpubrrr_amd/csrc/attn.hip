@@ -8,19 +8,23 @@
 //   k_attn_qkv   rmsnorm (16-lane sum of squares) + Q8 per 32 of x, then the
 //                q / k / v rows: the reference's Q8 dot (8 fp32 chains per
 //                row, one lane each), bias, RoPE from the table, cache write;
-//   k_attn_core  per (kv-head, chunk of 64 positions): scores of the group's
-//                q-heads, chunk max / sum / weighted v; the last workgroup of
-//                a kv-head merges the chunks with the sink and quantises;
+//   k_attn_core  per (kv-head, chunk of 128 positions): scores of the group's
+//                q-heads, softmax weights, weighted v; a window of 128 is one
+//                chunk and finishes in the workgroup in the reference's order,
+//                longer spans leave per-chunk (max, sum, weighted v) that the
+//                last workgroup of the kv-head merges with the sink; then Q8
+//                of the heads' outputs;
 //   k_attn_oproj x[r] += wo[r] . ao + bo[r].
 // The projections, RoPE and the cache rows are the reference's operations in
 // its order (bit for bit given the same RoPE table, which the host computes
-// once with the reference's formula); the softmax is merged over chunks
-// (flash-decoding) and goes through expf, so the heads' outputs match to
+// once with the reference's formula); the softmax goes through expf (and,
+// past one chunk, a merge over chunks), so the heads' outputs match to
 // tolerance.
 //
-// Weights: the chain-major Q8 stream described at q8c_dot, built on the GPU
-// at load time from the bf16 tensors.  KV cache: [layer][kv-head][position]
-// [64] fp32, so a chunk of positions of one head is one contiguous 16 KiB run.
+// Weights: the chain-major Q8 stream described before q8c_dot, built on the
+// GPU at load time from the bf16 tensors.  KV cache: [layer][kv-head]
+// [position][64] fp32, so a chunk of positions of one head is one contiguous
+// 32 KiB run.
 #include <hip/hip_runtime.h>
 
 #include <cfloat>
