@@ -15,6 +15,15 @@
 // row-major (only the few candidate rows are read).  The screen is a
 // bandwidth-bound GEMV over 4.5 bits per weight (~326 MB for gpt-oss's
 // 201088 x 2880 head), one lane per row.
+//
+// Kernels per token: k_head_norm (rmsnorm + Q8 of the hidden state);
+// k_head_screen (every row's screen value; each 256-row workgroup also leaves
+// its best n_cand rows in every worker slice it meets); k_head_refine (one
+// workgroup per worker slice: the slice's best n_cand from those lists, their
+// exact Q8 logits; the last workgroup to finish takes the greedy choice).
+// A slice's best n_cand by the reference's insertion (strict comparisons) are
+// its n_cand largest values, equal values in row order; every selection here
+// ranks by that order.
 #include <hip/hip_runtime.h>
 
 #include <cfloat>
