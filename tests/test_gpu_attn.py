@@ -117,3 +117,9 @@ def test_errors():
     with pytest.raises(RuntimeError):
         Attention(256, 8, 3, 1)                   # n_head not a multiple of n_head_kv
     assert Lb.CPB_EINVAL == -22
+
+
+def test_long_context_merge():
+    # a full-causal layer past several 128-position chunks (the chunk merge with
+    # the sink, a partial last chunk), GQA 4 q-heads per kv-head
+    check_seq(256, 8, 2, 4, 560, layers=(1,), seed=9, max_seq=576)

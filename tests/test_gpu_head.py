@@ -61,3 +61,14 @@ def test_head_ties(gpu):
 def test_head_gptoss_shape(gpu):
     # gpt-oss output.weight: 201088 x 2880
     run(201088, 2880, 4, full_screen=False)
+
+
+def test_head_edge_shapes(gpu):
+    # fewer row quads than workers: empty slices keep the reference's initial
+    # entries (-FLT_MAX, row 0); a vocabulary that ends mid-tile and mid
+    # workgroup; the largest worker x candidate product; one worker
+    run(16, 64, 5, nt=12, cand=8)
+    run(4, 32, 6, nt=3, cand=2)
+    run(1000, 96, 7, nt=8, cand=16)
+    run(2052, 128, 8, nt=1, cand=16)
+    run(300, 64, 9, nt=32, cand=4, dup=True)
