@@ -587,36 +587,40 @@ __global__ __launch_bounds__(256) void k_attn_core(AttnArgs a) {
     __syncthreads();
     if (!last) return;
     // the chunks' partials: coherent loads (they bypass this CU's and this
-    // XCD's caches, which may hold older values)
-    for (int hl = wave, t = 0; hl < R; hl += 4, t++) {
+    // XCD's caches, which may hold older values), for both of the wave's heads
+    // and the first kMergeRegs chunks all requested before any is used (one
+    // round trip; nsplit <= max_seq / 128 <= 64)
+    constexpr int kMergeRegs = 16;
+    float mi[2], lsum[2], ov[2][kMergeRegs];
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+        const int hl = wave + 4 * t;
+        const bool hv_ = hl < R;
+        const float* pp = a.part + (size_t)(kvh * R + (hv_ ? hl : 0)) * a.nsplit * 66;
+        const bool ok = hv_ && lane < a.nsplit;
+        mi[t] = ok ? ld_dev(pp + lane * 66) : -INFINITY;
+        lsum[t] = ok ? ld_dev(pp + lane * 66 + 1) : 0.0f;
+#pragma unroll
+        for (int c = 0; c < kMergeRegs; c++) ov[t][c] = (hv_ && c < a.nsplit) ? ld_dev(pp + c * 66 + 2 + lane) : 0.0f;
+    }
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+        const int hl = wave + 4 * t;
+        if (hl >= R) break;
         const int h = kvh * R + hl;
         const float* pp = a.part + (size_t)h * a.nsplit * 66;
         const float sink = sinkr[t];
-        float M = sink;
-        for (int i0 = 0; i0 < a.nsplit; i0 += 64)
-            if (i0 + lane < a.nsplit) M = fmaxf(M, ld_dev(pp + (i0 + lane) * 66));
-        M = wave_max_f32(M);
-        float den = 0.0f, acc = 0.0f;
-        for (int i0 = 0; i0 < a.nsplit; i0 += 64) {
-            const int i = i0 + lane;
-            const float f = i < a.nsplit ? expf(ld_dev(pp + i * 66) - M) : 0.0f;
-            if (i < a.nsplit) den = fmaf(ld_dev(pp + i * 66 + 1), f, den);
-            es[hl][lane] = f;
-            wave_sync_lds();
-            // weighted merge of the chunks' values, dimension lane
-            float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-            const int n = min(64, a.nsplit - i0);
-            int c = 0;
-            for (; c + 4 <= n; c += 4) {
+        const float M = wave_max_f32(fmaxf(mi[t], sink));
+        const float f = lane < a.nsplit ? expf(mi[t] - M) : 0.0f;
+        const float den = wave_sum_f32(lane < a.nsplit ? lsum[t] * f : 0.0f) + expf(sink - M);
+        es[hl][lane] = f;
+        wave_sync_lds();
+        // weighted merge of the chunks' values, dimension lane
+        float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                for (int q = 0; q < 4; q++) o[q] = fmaf(ld_dev(pp + (i0 + c + q) * 66 + 2 + lane), es[hl][c + q], o[q]);
-            }
-            for (; c < n; c++) o[0] = fmaf(ld_dev(pp + (i0 + c) * 66 + 2 + lane), es[hl][c], o[0]);
-            acc += (o[0] + o[1]) + (o[2] + o[3]);
-            wave_sync_lds();
-        }
-        den = wave_sum_f32(den);
-        den += expf(sink - M);
+        for (int c = 0; c < kMergeRegs; c++) o[c & 3] = fmaf(ov[t][c], es[hl][c], o[c & 3]);
+        for (int c = kMergeRegs; c < a.nsplit; c++) o[c & 3] = fmaf(ld_dev(pp + c * 66 + 2 + lane), es[hl][c], o[c & 3]);
+        const float acc = (o[0] + o[1]) + (o[2] + o[3]);
         const float val = acc * (1.0f / den);
         a.ao[h * kAttnHd + lane] = val;
         const float mb = half_max_f32(fabsf(val));
