@@ -36,10 +36,10 @@ sys.path.insert(0, str(ROOT))
 
 # HBM bytes per dispatch of the roofline kernel, from rocprofv3 FETCH_SIZE /
 # WRITE_SIZE runs scaled by a 1 GiB copy (profiles/hbm_traffic_config1_phased.md,
-# profiles/hbm_traffic_config3_qwen.md);
+# profiles/hbm_traffic_config3_qwen.md, profiles/hbm_traffic_config6_head.md);
 # None where not yet measured.
 MEASURED_TRAFFIC = {"k_gateup_mx": 35_815_144, "k_gateup_kq": 14_404_042,
-                    "k_gateup_grouped": 484_748_900}
+                    "k_gateup_grouped": 484_748_900, "head": 327_526_064}
 
 METRIC = "expert-weight GB/s (% HBM peak) + MoE-layer tok/s, gpt-oss-20b shape, 1 GPU"
 HBM_PEAK_GBS = 8000.0
@@ -136,6 +136,21 @@ def batched_result(c, args, ms, n_tok, kt) -> dict:
     }
 
 
+def calib_copy(args) -> None:
+    """A copy kernel of known size: its FETCH_SIZE / WRITE_SIZE give the
+    counter-to-bytes factor for the kernels of the same run."""
+    if not args.calib_copy_mib:
+        return
+    import torch
+    n = args.calib_copy_mib * (1 << 20) // 4
+    src = torch.empty(n, dtype=torch.float32, device="cuda:0").uniform_()
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+
+
 def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
@@ -221,6 +236,7 @@ def bench_head(args, c) -> int:
     stream = torch.cuda.Stream()
     torch.cuda.set_stream(stream)
     hd.set_stream(stream.cuda_stream)
+    calib_copy(args)
     x = torch.from_numpy((r.standard_normal(d) * 3).astype(np.float32)).to("cuda:0")
     ch = torch.zeros(1, dtype=torch.int32, device="cuda:0")
     for _ in range(args.warmup):
@@ -243,7 +259,8 @@ def bench_head(args, c) -> int:
            "config": {"workload": c["name"], "d": d, "n_vocab": V, "n_slices": 12, "n_cand": 8},
            "tok_per_s": round(1e3 / ms, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
            "roofline": {"bound": "hbm", "kernel": "whole head (norm, screen, top-k, refine)", "achieved": round(gbs, 1),
-                        "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                        "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                        "traffic": MEASURED_TRAFFIC["head"] if (d, V) == (2880, 201088) else None,
                         "bytes_per_launch": screen_bytes + refine_bytes}}
     hd.close()
     if not args.no_cpu:
@@ -287,6 +304,7 @@ def bench_attn(args, c) -> int:
     stream = torch.cuda.Stream()
     torch.cuda.set_stream(stream)
     at.set_stream(stream.cuda_stream)
+    calib_copy(args)
     x = torch.from_numpy(synth.token(d, 0, 7)).to("cuda:0")
     # fill the cache: positions 0 .. pos-1 through every layer
     for p in range(pos):
@@ -579,16 +597,7 @@ def main() -> int:
         x = torch.from_numpy(np.stack([synth.token(d, 0, i) for i in range(n_tok)])).to(dev)
     else:
         x = torch.from_numpy(synth.token(d, 0, 0)).to(dev)
-    if args.calib_copy_mib:
-        # a copy kernel of known size: its FETCH_SIZE / WRITE_SIZE give the
-        # counter-to-bytes factor for the kernels above
-        n = args.calib_copy_mib * (1 << 20) // 4
-        src = torch.empty(n, dtype=torch.float32, device=dev).uniform_()
-        dst = torch.empty_like(src)
-        torch.cuda.synchronize()
-        dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
+    calib_copy(args)
 
     def step(i):
         if c["per_step"] == nl:
