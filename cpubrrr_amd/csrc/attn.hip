@@ -74,7 +74,8 @@ CPB_DEV float half_max_f32(float v) {
 // scale(b) * xscale(b).  Lane 8r + c of a wave runs chain c of tile row r.
 // Per 8-row tile the codes are stored by pairs of chain steps: entry (tile,
 // sp) is 64 lanes x 16 bytes, lane l's 16 bytes = (lo, hi) of its chain at
-// steps 2sp and 2sp + 1 (step s = block 2s + h).  Scales: [tile][s][r][h].
+// steps 2sp and 2sp + 1 (step s = block 2s + h).  Scales: [tile][sp][r][h][2]
+// (one float2 per lane and step pair).
 // Blocks are padded to a multiple of 4 with zero codes and zero scales
 // (their products are +0 and leave every chain unchanged).
 CPB_DEV_HOST_INLINE int q8c_nbp(int nb) { return (nb + 3) & ~3; }
@@ -107,8 +108,11 @@ struct AttnArgs {
 
 // ---- load time: Q8Mat::from_bf16 (:476-489) into the chain-major stream ----
 // one thread per (row, block); the stream must be zeroed beforehand (padding)
+// pair_tiles: within each 64-row head, tile j holds rows 4j..4j+3 (slots 0-3)
+// and 32+4j..32+4j+3 (slots 4-7), so a RoPE pair (i, 32 + i) shares a tile;
+// otherwise tile t holds rows 8t..8t+7.
 __global__ void k_q8c_quant(const uint16_t* __restrict__ w, int rows, int cols, u32x4* __restrict__ q,
-                            float* __restrict__ s) {
+                            float* __restrict__ s, int pair_tiles) {
     const int nb = cols / 32, nbp = q8c_nbp(nb), nsp = nbp / 4, ns = nbp / 2;
     const size_t total = (size_t)rows * nb;
     for (size_t idx = blockIdx.x * (size_t)blockDim.x + threadIdx.x; idx < total; idx += (size_t)gridDim.x * blockDim.x) {
@@ -127,8 +131,11 @@ __global__ void k_q8c_quant(const uint16_t* __restrict__ w, int rows, int cols, 
             r = r < -127.0f ? -127.0f : r > 127.0f ? 127.0f : r;
             wd[i >> 2] |= (uint32_t)(uint8_t)(int8_t)r << (8 * (i & 3));
         }
-        const int tile = row >> 3, r = row & 7, h = b & 1, st = b >> 1, sp = st >> 1, k = st & 1;
-        s[(((size_t)tile * ns + st) * 8 + r) * 2 + h] = sc;
+        const int i64 = row & 63;
+        const int tile = pair_tiles ? (row >> 6) * 8 + ((i64 & 31) >> 2) : row >> 3;
+        const int r = pair_tiles ? (i64 & 3) + ((i64 >> 5) << 2) : row & 7;
+        const int h = b & 1, st = b >> 1, sp = st >> 1, k = st & 1;
+        s[((((size_t)tile * nsp + sp) * 8 + r) * 2 + h) * 2 + k] = sc;
         uint32_t* base = (uint32_t*)(q + ((size_t)tile * nsp + sp) * 64 + r * 8 + h * 4);
 #pragma unroll
         for (int j = 0; j < 4; j++) {
@@ -138,93 +145,95 @@ __global__ void k_q8c_quant(const uint16_t* __restrict__ w, int rows, int cols, 
     }
 }
 
+// LDS writes of this wave visible to its own later reads
+CPB_DEV void wave_sync_lds() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // ---- staging of 8-row tiles into LDS ----
-// A workgroup copies the codes and scales of its (one or two) tiles to LDS
-// with every thread's 16-byte loads issued before any is waited for, so the
-// whole tile stream is in flight at once; the chains then run from LDS.
-constexpr int kStageBatch = 16;       // 16-byte loads per thread per batch (x 256 threads)
+// A workgroup copies the codes and scales of its consecutive tiles (at most
+// kMaxTiles) to LDS with every thread's 16-byte loads issued before any is
+// waited for, so the whole tile stream is in flight at once; the chains then
+// run from LDS.  The loads are unconditional buffer loads (an offset past the
+// tiles reads zeros): with a branch around each, the compiler could not count
+// them, and any use of data loaded before them (x for the norm, the
+// activations) waited for nearly the whole stream.
+constexpr int kMaxTiles = 3;
+// 16-byte code loads and float4 scale loads per thread (x 256 threads): qkv,
+// 3 tiles at d <= 4096; o-projection, 1 tile at n_head <= 128
+constexpr int kQkvLoads = 24, kQkvScales = 3, kOprojLoads = 16, kOprojScales = 2;
 struct TileSet {
-    const u32x4* w[2];
-    const float* s[2];
+    const u32x4* w;                   // first tile's codes (the tiles follow it)
+    const float* s;                   // first tile's scales
     int nt, nsp;                      // tiles, step pairs per tile
 };
+template <int NL, int NS>
 struct StageRegs {
-    u32x4 r[kStageBatch];
-    float4 sc[2];
+    u32x4 r[NL];
+    float4 sc[NS];
 };
-CPB_DEV void stage_issue(const TileSet& t, int b0, StageRegs& g, bool scales) {
-    const int per = t.nsp * 64, total = t.nt * per, tid = threadIdx.x;
+template <int NL, int NS>
+CPB_DEV void stage_issue(const TileSet& t, StageRegs<NL, NS>& g) {
+    const int total = t.nt * t.nsp * 64, tid = threadIdx.x;
+    const __amdgpu_buffer_rsrc_t rw = buf_rsrc(t.w, (uint32_t)total * 16);
 #pragma unroll
-    for (int k = 0; k < kStageBatch; k++) {
-        const int i = b0 + k * 256 + tid;
-        if (i < total) {
-            const int ti = i >= per;
-            g.r[k] = __builtin_nontemporal_load(t.w[ti] + (i - ti * per));
-        }
-    }
-    if (scales) {
-        const int sper = t.nsp * 2 * 4, stotal = t.nt * sper;     // float4 per tile: ns * 16 / 4
+    for (int k = 0; k < NL; k++)
+        g.r[k] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, (uint32_t)(k * 256 + tid) * 16, 0, 2));
+    const int stotal = t.nt * t.nsp * 8;                  // float4: ns * 16 / 4 per tile
+    const __amdgpu_buffer_rsrc_t rs = buf_rsrc(t.s, (uint32_t)stotal * 16);
 #pragma unroll
-        for (int k = 0; k < 2; k++) {
-            const int i = k * 256 + tid;
-            if (i < stotal) {
-                const int ti = i >= sper;
-                g.sc[k] = ((const float4*)t.s[ti])[i - ti * sper];
-            }
-        }
-    }
+    for (int k = 0; k < NS; k++)
+        g.sc[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rs, (uint32_t)(k * 256 + tid) * 16, 0, 0));
 }
-CPB_DEV void stage_commit(const TileSet& t, int b0, const StageRegs& g, bool scales, u32x4* lw, float* ls) {
-    const int per = t.nsp * 64, total = t.nt * per, tid = threadIdx.x;
+template <int NL, int NS>
+CPB_DEV void stage_commit(const TileSet& t, const StageRegs<NL, NS>& g, u32x4* lw, float* ls) {
+    const int total = t.nt * t.nsp * 64, tid = threadIdx.x;
 #pragma unroll
-    for (int k = 0; k < kStageBatch; k++) {
-        const int i = b0 + k * 256 + tid;
+    for (int k = 0; k < NL; k++) {
+        const int i = k * 256 + tid;
         if (i < total) lw[i] = g.r[k];
     }
-    if (scales) {
-        const int stotal = t.nt * t.nsp * 8;
+    const int stotal = t.nt * t.nsp * 8;
 #pragma unroll
-        for (int k = 0; k < 2; k++) {
-            const int i = k * 256 + tid;
-            if (i < stotal) ((float4*)ls)[i] = g.sc[k];
-        }
-    }
-}
-// copy the tiles' stream to LDS; `between` runs while the first batch is in
-// flight.  The scales (nt * nsp * 8 float4) come with the first batch: at
-// most 512 float4, which d <= 4096 (qkv: 2 tiles, nsp <= 32) and n_head <= 128
-// (o-proj: 1 tile, nsp <= 64) keep.
-template <class F>
-CPB_DEV void stage_tiles(const TileSet& t, u32x4* lw, float* ls, F between) {
-    StageRegs g;
-    stage_issue(t, 0, g, true);
-    between();
-    stage_commit(t, 0, g, true, lw, ls);
-    const int total = t.nt * t.nsp * 64;
-    for (int b0 = kStageBatch * 256; b0 < total; b0 += kStageBatch * 256) {
-        stage_issue(t, b0, g, false);
-        stage_commit(t, b0, g, false, lw, ls);
+    for (int k = 0; k < NS; k++) {
+        const int i = k * 256 + tid;
+        if (i < stotal) ((float4*)ls)[i] = g.sc[k];
     }
 }
 
+// Activations in LDS in the chains' order too: dword i of the Q8 row (block
+// b = i / 8, word w = i % 8: bytes 4j..4j+3 of the block for w = j, 16+4j..
+// for w = 4 + j) goes to entry (sp = b / 4, h = b % 2, j) component 2t + w / 4
+// (t = (b / 2) % 2), so a lane reads its step pair's four dwords at once;
+// the block scales as float2 per (sp, h): blocks 4sp + h and 4sp + 2 + h.
+CPB_DEV_HOST_INLINE int xc_index(int i) {
+    const int b = i >> 3, w = i & 7;
+    return ((((b >> 2) * 2 + (b & 1)) * 4 + (w & 3)) * 4) + ((b >> 1) & 1) * 2 + (w >> 2);
+}
+CPB_DEV_HOST_INLINE int xs_index(int b) { return ((b >> 2) * 2 + (b & 1)) * 2 + ((b >> 1) & 1); }
+
 // The chain of this lane over one 8-row tile staged in LDS (codes lw, scales
-// ls), activations in LDS (xl: dwords, 8 per block; sl: scales; both padded
-// to q8c_nbp blocks with zeros).  Returns the row's dot_q8_i8 in lane 0 of
-// the row's group of 8.
+// ls), activations in LDS (xl: dwords in xc_index order; sl: scales in
+// xs_index order; both padded to q8c_nbp blocks with zeros).  Returns the
+// row's dot_q8_i8 in lane 0 of the row's group of 8.
 CPB_DEV float q8c_dot(const u32x4* lw, const float* ls, int nbp, const uint32_t* xl, const float* sl) {
     const int lane = threadIdx.x & 63, r = lane >> 3, h = (lane >> 2) & 1, j = lane & 3;
     const int nsp = nbp / 4;
-    const float* lsl = ls + r * 2 + h;
+    const float2* wsc = (const float2*)ls + r * 2 + h;           // [sp][8][2] float2
+    const u32x4* xc = (const u32x4*)xl + h * 4 + j;              // [sp][2][4] u32x4
+    const float2* xsc = (const float2*)sl + h;                   // [sp][2] float2
     float acc = 0.0f;
 #pragma unroll 4
     for (int sp = 0; sp < nsp; sp++) {
-        const u32x4 w = lw[sp * 64 + lane];
-#pragma unroll
-        for (int t = 0; t < 2; t++) {
-            const int b = 2 * (2 * sp + t) + h;
-            const int dot = sdot4(w[2 * t + 1], xl[b * 8 + 4 + j], sdot4(w[2 * t], xl[b * 8 + j], 0));
-            acc = fmaf((float)dot, lsl[(2 * sp + t) * 16] * sl[b], acc);
-        }
+        const u32x4 w = lw[sp * 64 + lane], xa = xc[sp * 8];
+        const float2 ws = wsc[sp * 16], xs = xsc[sp * 2];
+        // steps 2sp (block 4sp + h) and 2sp + 1 (block 4sp + 2 + h)
+        const int d0 = sdot4(w[1], xa[1], sdot4(w[0], xa[0], 0));
+        acc = fmaf((float)d0, ws.x * xs.x, acc);
+        const int d1 = sdot4(w[3], xa[3], sdot4(w[2], xa[2], 0));
+        acc = fmaf((float)d1, ws.y * xs.y, acc);
     }
     // lanes 0-3 of each group of 8: v_j = acc0_j + acc1_j (lane + 4: row_ror by 12)
     const float v = acc + dppf<0x12C>(acc);
@@ -236,12 +245,10 @@ CPB_DEV float q8c_dot(const u32x4* lw, const float* ls, int nbp, const uint32_t*
 // :710-726) and Q8 per 32 (qblock32 :691-699) into LDS (xl dwords / sl
 // scales, padded with zeros to nbp blocks).  xr / wr: this thread's float4
 // slots tid + 256k of x and of the norm weights, in registers.  xt: LDS for a
-// transposed copy (chain q's elements contiguous, row stride attn_xt_stride);
-// red: 17 floats.
-CPB_DEV_HOST_INLINE int attn_xt_stride(int d) {
-    int S = (d / 16 + 3) & ~3;
-    return S + ((68 - S % 64) % 64);                  // = 4 (mod 64): 16 lanes' 16-byte reads hit distinct banks
-}
+// transposed copy (chain q's elements contiguous, row stride attn_xt_stride,
+// zero padded so that whole 32-value groups can be read; the chain's one-group
+// look-ahead past the last row lands in red); red: 64 floats.
+CPB_DEV_HOST_INLINE int attn_xt_stride(int d) { return (d / 16 + 32 + 63) / 64 * 64 + 4; }   // = 4 (mod 64): distinct banks
 CPB_DEV void attn_norm_q8(const float4 (&xr)[4], const float4 (&wr)[4], int d, int nb, int nbp, float eps, float* xt,
                           float* red, uint32_t* xl, float* sl, int8_t* gxq, float* gxsb) {
     const int tid = threadIdx.x, lane = tid & 63;
@@ -262,22 +269,24 @@ CPB_DEV void attn_norm_q8(const float4 (&xr)[4], const float4 (&wr)[4], int d, i
     for (int e = tid; e < 16 * (S - n16); e += 256) xt[(e & 15) * S + n16 + (e >> 4)] = 0.0f;
     __syncthreads();
     if (tid < 64) {
+        // lane q (mod 16) streams row q: the next group's reads are issued
+        // before the current group's fmas
         float acc = 0.0f;
-        if (lane < 16) {
-            const float4* row = (const float4*)(xt + lane * S);
-            for (int j0 = 0; j0 < S / 4; j0 += 16) {
-                float4 t[16];
-#pragma unroll
-                for (int u = 0; u < 16; u++) t[u] = j0 + u < S / 4 ? row[j0 + u] : make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-                for (int u = 0; u < 16; u++) {
-                    acc = fmaf(t[u].x, t[u].x, acc);
-                    acc = fmaf(t[u].y, t[u].y, acc);
-                    acc = fmaf(t[u].z, t[u].z, acc);
-                    acc = fmaf(t[u].w, t[u].w, acc);
-                }
-            }
+        uint32_t ra = lds_addr(xt + (lane & 15) * S);
+        f32x4 ga[8], gb[8];                           // ping-pong groups of 32 values
+        lds_read8(ga, ra);
+        for (int m = 0;; m += 64) {
+            lds_read8(gb, ra + 128);
+            lds_wait_older8(ga);
+            acc = sumsq_chain(ga, acc);
+            if (m + 32 >= n16) break;
+            lds_read8(ga, ra + 256);
+            lds_wait_older8(gb);
+            acc = sumsq_chain(gb, acc);
+            if (m + 64 >= n16) break;
+            ra += 256;
         }
+        lds_wait_all();
         // chain q = 4v + l -> acc[v][l]; L[l] = (a0 + a1) + (a2 + a3); s = (L0 + L1) + (L2 + L3)
         float c16[16];
 #pragma unroll
@@ -290,49 +299,89 @@ CPB_DEV void attn_norm_q8(const float4 (&xr)[4], const float4 (&wr)[4], int d, i
     }
     __syncthreads();
     const float inv = red[16];
-    // Q8 from registers: slot i = 4 elements, a 32-block = 8 consecutive slots (lanes)
+    // Q8 from registers: slot i = 4 elements, a 32-block = 8 consecutive slots
+    // (lanes).  The four slots of a thread are computed side by side (a slot
+    // past d holds x[0..3]: computed, not stored; d % 32 == 0 keeps a block's
+    // eight slots all inside or all past d), one rarely taken branch for the
+    // exact rounding path.
+    float v[4][4], sc[4], rs[4], r[4][4];
+    bool near = false;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        v[k][0] = xr[k].x * inv * wr[k].x;
+        v[k][1] = xr[k].y * inv * wr[k].y;
+        v[k][2] = xr[k].z * inv * wr[k].z;
+        v[k][3] = xr[k].w * inv * wr[k].w;
+        float m = fmaxf(fmaxf(fabsf(v[k][0]), fabsf(v[k][1])), fmaxf(fabsf(v[k][2]), fabsf(v[k][3])));
+        m = fmaxf(m, dppf<0xB1>(m));
+        m = fmaxf(m, dppf<0x4E>(m));
+        m = fmaxf(m, dppf<0x141>(m));                // the other quad of the 8
+        sc[k] = fmaxf(1e-12f, m) / 127.0f;
+        rs[k] = __builtin_amdgcn_rcpf(sc[k]);
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const float y = v[k][u] * rs[k];
+            r[k][u] = __builtin_rintf(y);
+            near = near || q8_near_half(y);
+        }
+    }
+    if (near) {
+        // the exact quotients of all 16 side by side (no branch per value)
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const float ex = roundf(v[k][u] / sc[k]);
+                r[k][u] = q8_near_half(v[k][u] * rs[k]) ? ex : r[k][u];
+            }
+    }
 #pragma unroll
     for (int k = 0; k < 4; k++) {
         const int i = tid + k * 256;
-        if (i * 4 < d) {
-            const float v[4] = {xr[k].x * inv * wr[k].x, xr[k].y * inv * wr[k].y, xr[k].z * inv * wr[k].z,
-                                xr[k].w * inv * wr[k].w};
-            float m = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-            m = fmaxf(m, dppf<0xB1>(m));
-            m = fmaxf(m, dppf<0x4E>(m));
-            m = fmaxf(m, dppf<0x141>(m));            // the other quad of the 8
-            const float sc = fmaxf(1e-12f, m) / 127.0f;
-            uint32_t wd = 0u;
+        uint32_t wd = 0u;
 #pragma unroll
-            for (int u = 0; u < 4; u++) wd |= (uint32_t)(uint8_t)q8_round(v[u], sc) << (8 * u);
-            xl[i] = wd;
-            if ((i & 7) == 0) sl[i >> 3] = sc;
+        for (int u = 0; u < 4; u++) wd |= (uint32_t)(uint8_t)q8_clamp(r[k][u]) << (8 * u);
+        if (i * 4 < d) {
+            xl[xc_index(i)] = wd;
+            if ((i & 7) == 0) sl[xs_index(i >> 3)] = sc[k];
             if (gxq) {
                 ((uint32_t*)gxq)[i] = wd;
-                if ((i & 7) == 0) gxsb[i >> 3] = sc;
+                if ((i & 7) == 0) gxsb[i >> 3] = sc[k];
             }
         }
     }
-    for (int i = d / 4 + tid; i < nbp * 8; i += 256) xl[i] = 0u;
-    for (int bk = nb + tid; bk < nbp; bk += 256) sl[bk] = 0.0f;
+    for (int i = d / 4 + tid; i < nbp * 8; i += 256) xl[xc_index(i)] = 0u;
+    for (int bk = nb + tid; bk < nbp; bk += 256) sl[xs_index(bk)] = 0.0f;
 }
 
 // ---- rmsnorm + Q8 of x, q / k / v rows + bias + RoPE + cache ----
-// 256 threads, two 8-row tiles of one head: rows 8k + [0, 8) (wave 0) and
-// 32 + 8k + [0, 8) (wave 1), so each RoPE pair (i, 32 + i) is in the
-// workgroup; grid (nh + 2 nkv) * 4.  Every workgroup normalises x itself
-// (the reference's order, rmsnorm_quant_par :730-738) while its weight loads
-// are in flight.
+// The q, k and v streams are one sequence of T = (nh + 2 nkv) * 8 tiles
+// (q heads, then k heads, then v heads; tile j of a head holds rows 4j..4j+3
+// and 32+4j..32+4j+3, so each RoPE pair (i, 32 + i) is in one tile).
+// Workgroup g of G takes tiles [g T / G, (g + 1) T / G) (at most kMaxTiles),
+// with G = min(256, T) where that allows: one workgroup per CU, none of them
+// streaming twice the bytes of another.  256 threads; wave w runs tile w's
+// chains.  Every workgroup normalises x itself (the reference's order,
+// rmsnorm_quant_par :730-738) while its weight loads are in flight.
+CPB_DEV_HOST_INLINE size_t qkv_lds_bytes(int d) {
+    const int nbp = q8c_nbp(d / 32);
+    // tiles' codes and scales, transposed x, red, activation dwords and scales
+    return (size_t)kMaxTiles * ((nbp / 4) * 1024 + (nbp / 2) * 64) + sizeof(float) * (16 * attn_xt_stride(d) + 64) + (size_t)nbp * 36;
+}
+CPB_DEV_HOST_INLINE int qkv_groups(int tiles) {
+    const int g = tiles < 256 ? tiles : 256;
+    return g * kMaxTiles >= tiles ? g : (tiles + kMaxTiles - 1) / kMaxTiles;
+}
 __global__ __launch_bounds__(256) void k_attn_qkv(AttnArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     const int nbp = q8c_nbp(a.nb), nsp = nbp / 4, ns = nbp / 2;
-    u32x4* lw = (u32x4*)smem;                         // [2][nsp * 64]
-    float* ls = (float*)(lw + 2 * nsp * 64);          // [2][ns * 16]
-    float* xt = ls + 2 * ns * 16;                     // [16][attn_xt_stride(d)] transposed x
+    u32x4* lw = (u32x4*)smem;                         // [kMaxTiles][nsp * 64]
+    float* ls = (float*)(lw + kMaxTiles * nsp * 64);  // [kMaxTiles][ns * 16]
+    float* xt = ls + kMaxTiles * ns * 16;             // [16][attn_xt_stride(d)] transposed x
     float* red = xt + 16 * attn_xt_stride(a.d);       // [64]
     uint32_t* xl = (uint32_t*)(red + 64);             // [nbp * 8]
     float* sl = (float*)(xl + nbp * 8);               // [nbp]
-    __shared__ float hv[16];
+    __shared__ float hv[kMaxTiles][8];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     // x and the norm weights first: the norm waits for them, not for the tiles
     float4 xr[4], wr[4];
@@ -342,53 +391,46 @@ __global__ __launch_bounds__(256) void k_attn_qkv(AttnArgs a) {
         xr[k] = ((const float4*)a.x)[i4];
         wr[k] = ((const float4*)a.L.norm)[i4];
     }
-    const int head = blockIdx.x >> 2, k = blockIdx.x & 3;
-    int kind, hh;                                     // 0 q, 1 k, 2 v
+    const int T = (a.nh + 2 * a.nkv) * 8, G = gridDim.x;
+    const int t0 = (int)((long long)blockIdx.x * T / G), nt = (int)((long long)(blockIdx.x + 1) * T / G) - t0;
+    // this wave's tile: head, kind (0 q, 1 k, 2 v), the row of this lane's
+    // slot r = lane / 8, its bias, and (lanes 0-3) the RoPE entries of pair
+    // i = 4j + lane, all requested up front
+    const int tw = t0 + (wave < nt ? wave : 0), head = tw >> 3, j = tw & 7;
+    int kind, hh;
     if (head < a.nh) { kind = 0; hh = head; }
     else if (head < a.nh + a.nkv) { kind = 1; hh = head - a.nh; }
     else { kind = 2; hh = head - a.nh - a.nkv; }
-    const u32x4* W = kind == 0 ? a.L.wq : kind == 1 ? a.L.wk : a.L.wv;
-    const float* S = kind == 0 ? a.L.sq : kind == 1 ? a.L.sk : a.L.sv;
     const float* B = kind == 0 ? a.L.bq : kind == 1 ? a.L.bk : a.L.bv;
-    const int tile0 = hh * 8 + k, tile1 = hh * 8 + 4 + k;
-    // bias of this lane's row and the RoPE entries of pair 8k + tid, also up front
-    const float bias = B[(wave ? tile1 : tile0) * 8 + ((lane >> 3) & 7)];
-    const int ri = 8 * k + (tid & 7);
+    const int r = lane >> 3, rrow = (r < 4 ? 4 * j + r : 32 + 4 * j + r - 4);
+    const float bias = B[hh * kAttnHd + rrow];
+    const int ri = 4 * j + (lane & 3);
     const float rc = a.rope[((size_t)a.pos * 32 + ri) * 2], rs = a.rope[((size_t)a.pos * 32 + ri) * 2 + 1];
     TileSet ts;
-    ts.w[0] = W + (size_t)tile0 * nsp * 64;
-    ts.w[1] = W + (size_t)tile1 * nsp * 64;
-    ts.s[0] = S + (size_t)tile0 * ns * 16;
-    ts.s[1] = S + (size_t)tile1 * ns * 16;
-    ts.nt = 2;
+    ts.w = a.L.wq + (size_t)t0 * nsp * 64;
+    ts.s = a.L.sq + (size_t)t0 * ns * 16;
+    ts.nt = nt;
     ts.nsp = nsp;
+    // every wave's x requests go out before any wave's weight requests (an
+    // execution barrier, no memory wait): x then lands ahead of the stream
+    __builtin_amdgcn_s_barrier();
     {
-        StageRegs g;
-        stage_issue(ts, 0, g, true);
+        StageRegs<kQkvLoads, kQkvScales> g;
+        stage_issue(ts, g);
         attn_norm_q8(xr, wr, a.d, a.nb, nbp, a.eps, xt, red, xl, sl, blockIdx.x == 0 ? a.xq : nullptr, a.xsb);
-        stage_commit(ts, 0, g, true, lw, ls);
-        for (int b0 = kStageBatch * 256; b0 < 2 * nsp * 64; b0 += kStageBatch * 256) {
-            stage_issue(ts, b0, g, false);
-            stage_commit(ts, b0, g, false, lw, ls);
-        }
+        stage_commit(ts, g, lw, ls);
     }
     __syncthreads();
-    if (wave < 2) {
-        const float v = q8c_dot(lw + wave * nsp * 64, ls + wave * ns * 16, nbp, xl, sl);
-        if ((lane & 7) == 0) {
-            const int row = (wave ? tile1 : tile0) * 8 + (lane >> 3);
-            hv[wave * 8 + (lane >> 3)] = v + bias;        // :786-793 dot + bias (row)
-            (void)row;
-        }
-    }
-    __syncthreads();
-    if (tid >= 8) return;
-    // RoPE pair (i, 32 + i), i = 8k + tid (rope_yarn :578-590); v unrotated
-    const int i = 8 * k + tid;
-    float lo = hv[tid], hi = hv[8 + tid];
+    if (wave >= nt) return;
+    const float v = q8c_dot(lw + wave * nsp * 64, ls + wave * ns * 16, nbp, xl, sl);
+    if ((lane & 7) == 0) hv[wave][r] = v + bias;      // :786-793 dot + bias (row)
+    wave_sync_lds();
+    if (lane >= 4) return;
+    // RoPE pair (i, 32 + i), i = 4j + lane (rope_yarn :578-590); v unrotated
+    const int i = 4 * j + lane;
+    float lo = hv[wave][lane], hi = hv[wave][lane + 4];
     if (kind != 2) {
-        const float c = rc, s = rs;
-        const float nlo = lo * c - hi * s, nhi = hi * c + lo * s;
+        const float nlo = lo * rc - hi * rs, nhi = hi * rc + lo * rs;
         lo = nlo;
         hi = nhi;
     }
@@ -404,8 +446,8 @@ __global__ __launch_bounds__(256) void k_attn_qkv(AttnArgs a) {
 
 // ---- attention of one kv-head's q-heads over one chunk of positions ----
 // grid (nkv, nsplit), chunks of 128 positions (a window of 128 is one
-// chunk); wave w runs q-heads w and w + 4 of the group, lane l positions l
-// and l + 64.  With several chunks each workgroup leaves (max, sum, weighted
+// chunk); 512 threads, wave w runs q-head w of the group (two waves per SIMD
+// hide each other's latencies), lane l positions l and l + 64.  With several chunks each workgroup leaves (max, sum, weighted
 // v) per head and the last to arrive for its kv-head merges them with the
 // sink; then the heads' outputs are quantised (qblock32 :691-699).
 __device__ __forceinline__ float score64(const float* kr, const float4 (&qv)[16]) {
@@ -431,13 +473,8 @@ __device__ __forceinline__ float score64(const float* kr, const float4 (&qv)[16]
     return ((s4[0] + s4[1]) + (s4[2] + s4[3])) * 0.125f;     // 1 / sqrt(64)
 }
 
-CPB_DEV void wave_sync_lds() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
 
-__global__ __launch_bounds__(256) void k_attn_core(AttnArgs a) {
+__global__ __launch_bounds__(512) void k_attn_core(AttnArgs a) {
     __shared__ __align__(16) float ks[kAttnChunk][68];
     __shared__ __align__(16) float vs[kAttnHd][kAttnChunk + 4];    // transposed: [dimension][position]
     __shared__ __align__(16) float qs[kAttnMaxGroup][kAttnHd];
@@ -449,26 +486,24 @@ __global__ __launch_bounds__(256) void k_attn_core(AttnArgs a) {
     const int cnt = min(kAttnChunk, a.pos + 1 - p0);
     const float* kb = a.kc + ((size_t)kvh * a.max_seq + p0) * kAttnHd;
     const float* vb = a.vc + ((size_t)kvh * a.max_seq + p0) * kAttnHd;
-    constexpr int kIt = kAttnChunk * 16 / 256;
-    float sinkr[2];
-#pragma unroll
-    for (int t = 0; t < 2; t++) sinkr[t] = (wave + 4 * t < R) ? a.L.sinks[kvh * R + wave + 4 * t] : 0.0f;
+    constexpr int kIt = kAttnChunk * 16 / 512;
+    const bool live = wave < R;                       // wave w runs q-head w of the group
+    const int h = kvh * R + (live ? wave : 0);
+    const float sink = a.L.sinks[h];
     {
         float4 kr[kIt], vr[kIt];
-        float2 qr;
 #pragma unroll
         for (int it = 0; it < kIt; it++) {
-            const int e = it * 256 + tid, p = e >> 4, c = e & 15;
+            const int e = it * 512 + tid, p = e >> 4, c = e & 15;
             const int pc = p < cnt ? p : 0;               // rows past the chunk: loaded, not stored
             kr[it] = *(const float4*)(kb + pc * kAttnHd + c * 4);
             vr[it] = *(const float4*)(vb + pc * kAttnHd + c * 4);
         }
-        const int qe = (2 * tid < R * kAttnHd) ? 2 * tid : 0;
-        qr = *(const float2*)(a.q + kvh * R * kAttnHd + qe);
-        if (2 * tid < R * kAttnHd) *(float2*)(&qs[0][0] + 2 * tid) = qr;
+        const float qv = a.q[kvh * R * kAttnHd + (tid < R * kAttnHd ? tid : 0)];
+        if (tid < R * kAttnHd) (&qs[0][0])[tid] = qv;
 #pragma unroll
         for (int it = 0; it < kIt; it++) {
-            const int e = it * 256 + tid, p = e >> 4, c = e & 15;
+            const int e = it * 512 + tid, p = e >> 4, c = e & 15;
             if (p < cnt) {
                 *(float4*)&ks[p][c * 4] = kr[it];
                 vs[c * 4][p] = vr[it].x;
@@ -479,98 +514,74 @@ __global__ __launch_bounds__(256) void k_attn_core(AttnArgs a) {
         }
     }
     __syncthreads();
-    // wave w: q-heads w and w + 4 of the group (the second absent when R <= 4)
-    float mv[2] = {0.0f, 0.0f}, sv[2] = {0.0f, 0.0f};
-#pragma unroll
-    for (int t = 0; t < 2; t++) {
-        const int hl = wave + 4 * t;
-        if (hl >= R) break;
+    float mv = 0.0f, sv = 0.0f, ov = 0.0f, den = 1.0f;
+    if (live) {
+        // scores of positions lane and lane + 64, softmax weights
         float4 qv[16];
 #pragma unroll
-        for (int i = 0; i < 16; i++) qv[i] = *(const float4*)&qs[hl][4 * i];
+        for (int i = 0; i < 16; i++) qv[i] = *(const float4*)&qs[wave][4 * i];
         const float s0 = lane < cnt ? score64(ks[lane], qv) : -INFINITY;
         const float s1 = lane + 64 < cnt ? score64(ks[lane + 64], qv) : -INFINITY;
         float m = wave_max_f32(fmaxf(s0, s1));
-        if (a.nsplit == 1) m = fmaxf(m, sinkr[t]);       // one chunk: the sink joins the max here
+        if (a.nsplit == 1) m = fmaxf(m, sink);            // one chunk: the sink joins the max here
         const float e0 = lane < cnt ? expf(s0 - m) : 0.0f;
         const float e1 = lane + 64 < cnt ? expf(s1 - m) : 0.0f;
-        if (a.nsplit > 1) sv[t] = wave_sum_f32(e0 + e1);
-        mv[t] = m;
-        es[hl][lane] = e0;
-        es[hl][lane + 64] = e1;
-    }
-    wave_sync_lds();
-    if (wave < R) {
-        const int h0 = wave, h1 = wave + 4 < R ? wave + 4 : wave;
-        float ovs[2], dens[2] = {1.0f, 1.0f};
+        if (a.nsplit > 1) sv = wave_sum_f32(e0 + e1);
+        mv = m;
+        es[wave][lane] = e0;
+        es[wave][lane + 64] = e1;
+        wave_sync_lds();
+        const float* vrow = vs[lane];
+        const float* er = es[wave];
         if (a.nsplit == 1) {
             // the reference's order (:823-831): den = exp(sink - mx), then += e in
             // position order; per dimension one fma chain over the positions; ao
             // = acc * (1 / den)
-            float acc0 = 0.0f, acc1 = 0.0f, d0 = expf(sinkr[0] - mv[0]), d1 = expf(sinkr[1] - mv[1]);
-            int p = 0;
-#pragma unroll 2
-            for (; p + 4 <= cnt; p += 4) {
-                const float4 vv = *(const float4*)&vs[lane][p];
-                const float4 e0 = *(const float4*)&es[h0][p], e1 = *(const float4*)&es[h1][p];
-                acc0 = fmaf(vv.x, e0.x, acc0); acc0 = fmaf(vv.y, e0.y, acc0);
-                acc0 = fmaf(vv.z, e0.z, acc0); acc0 = fmaf(vv.w, e0.w, acc0);
-                acc1 = fmaf(vv.x, e1.x, acc1); acc1 = fmaf(vv.y, e1.y, acc1);
-                acc1 = fmaf(vv.z, e1.z, acc1); acc1 = fmaf(vv.w, e1.w, acc1);
-                d0 += e0.x; d0 += e0.y; d0 += e0.z; d0 += e0.w;
-                d1 += e1.x; d1 += e1.y; d1 += e1.z; d1 += e1.w;
-            }
-            for (; p < cnt; p++) {
-                acc0 = fmaf(vs[lane][p], es[h0][p], acc0);
-                acc1 = fmaf(vs[lane][p], es[h1][p], acc1);
-                d0 += es[h0][p];
-                d1 += es[h1][p];
-            }
-            ovs[0] = acc0;
-            ovs[1] = acc1;
-            dens[0] = d0;
-            dens[1] = d1;
-        } else {
-            // one chunk of several: 4 position chains, merged below with the sink
-            float o0[4] = {0.0f, 0.0f, 0.0f, 0.0f}, o1[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            float acc = 0.0f, d0 = expf(sink - m);
             int p = 0;
 #pragma unroll 4
             for (; p + 4 <= cnt; p += 4) {
-                const float4 vv = *(const float4*)&vs[lane][p];
-                const float4 e0 = *(const float4*)&es[h0][p], e1 = *(const float4*)&es[h1][p];
-                o0[0] = fmaf(vv.x, e0.x, o0[0]); o0[1] = fmaf(vv.y, e0.y, o0[1]);
-                o0[2] = fmaf(vv.z, e0.z, o0[2]); o0[3] = fmaf(vv.w, e0.w, o0[3]);
-                o1[0] = fmaf(vv.x, e1.x, o1[0]); o1[1] = fmaf(vv.y, e1.y, o1[1]);
-                o1[2] = fmaf(vv.z, e1.z, o1[2]); o1[3] = fmaf(vv.w, e1.w, o1[3]);
+                const float4 vv = *(const float4*)&vrow[p];
+                const float4 e4 = *(const float4*)&er[p];
+                acc = fmaf(vv.x, e4.x, acc); acc = fmaf(vv.y, e4.y, acc);
+                acc = fmaf(vv.z, e4.z, acc); acc = fmaf(vv.w, e4.w, acc);
+                d0 += e4.x; d0 += e4.y; d0 += e4.z; d0 += e4.w;
             }
             for (; p < cnt; p++) {
-                o0[0] = fmaf(vs[lane][p], es[h0][p], o0[0]);
-                o1[0] = fmaf(vs[lane][p], es[h1][p], o1[0]);
+                acc = fmaf(vrow[p], er[p], acc);
+                d0 += er[p];
             }
-            ovs[0] = (o0[0] + o0[1]) + (o0[2] + o0[3]);
-            ovs[1] = (o1[0] + o1[1]) + (o1[2] + o1[3]);
+            ov = acc;
+            den = d0;
+        } else {
+            // one chunk of several: 4 position chains, merged below with the sink
+            float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            int p = 0;
+#pragma unroll 4
+            for (; p + 4 <= cnt; p += 4) {
+                const float4 vv = *(const float4*)&vrow[p];
+                const float4 e4 = *(const float4*)&er[p];
+                o[0] = fmaf(vv.x, e4.x, o[0]); o[1] = fmaf(vv.y, e4.y, o[1]);
+                o[2] = fmaf(vv.z, e4.z, o[2]); o[3] = fmaf(vv.w, e4.w, o[3]);
+            }
+            for (; p < cnt; p++) o[0] = fmaf(vrow[p], er[p], o[0]);
+            ov = (o[0] + o[1]) + (o[2] + o[3]);
         }
-#pragma unroll
-        for (int t = 0; t < 2; t++) {
-            if (wave + 4 * t >= R) break;
-            const int h = kvh * R + wave + 4 * t;
-            const float ov = ovs[t];
-            if (a.nsplit == 1) {
-                // softmax with the sink in the denominator, then Q8 of the head
-                const float val = ov * (1.0f / dens[t]);
-                a.ao[h * kAttnHd + lane] = val;
-                const float mb = half_max_f32(fabsf(val));
-                const float scq = fmaxf(1e-12f, mb) / 127.0f;
-                a.aq[h * kAttnHd + lane] = (int8_t)q8_round(val, scq);
-                if ((lane & 31) == 0) a.asb[h * 2 + (lane >> 5)] = scq;
-            } else {
-                // coherent (write-through) stores: read by another workgroup of this launch
-                float* pp = a.part + ((size_t)h * a.nsplit + split) * 66;
-                st_dev(pp + 2 + lane, ov);
-                if (lane == 0) {
-                    st_dev(pp, mv[t]);
-                    st_dev(pp + 1, sv[t]);
-                }
+        if (a.nsplit == 1) {
+            // softmax with the sink in the denominator, then Q8 of the head
+            const float val = ov * (1.0f / den);
+            a.ao[h * kAttnHd + lane] = val;
+            const float mb = half_max_f32(fabsf(val));
+            const float scq = fmaxf(1e-12f, mb) / 127.0f;
+            a.aq[h * kAttnHd + lane] = (int8_t)q8_round(val, scq);
+            if ((lane & 31) == 0) a.asb[h * 2 + (lane >> 5)] = scq;
+        } else {
+            // coherent (write-through) stores: read by another workgroup of this launch
+            float* pp = a.part + ((size_t)h * a.nsplit + split) * 66;
+            st_dev(pp + 2 + lane, ov);
+            if (lane == 0) {
+                st_dev(pp, mv);
+                st_dev(pp + 1, sv);
             }
         }
     }
@@ -585,49 +596,36 @@ __global__ __launch_bounds__(256) void k_attn_core(AttnArgs a) {
         if (last) __hip_atomic_store(a.count + kvh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
-    if (!last) return;
-    // the chunks' partials: coherent loads (they bypass this CU's and this
-    // XCD's caches, which may hold older values), for both of the wave's heads
-    // and the first kMergeRegs chunks all requested before any is used (one
-    // round trip; nsplit <= max_seq / 128 <= 64)
+    if (!last || !live) return;
+    // the chunks' partials of this wave's head: coherent loads (they bypass
+    // this CU's and this XCD's caches, which may hold older values), the first
+    // kMergeRegs chunks all requested before any is used (one round trip;
+    // nsplit <= max_seq / 128 <= 64)
     constexpr int kMergeRegs = 16;
-    float mi[2], lsum[2], ov[2][kMergeRegs];
+    const float* pp = a.part + (size_t)h * a.nsplit * 66;
+    const bool ok = lane < a.nsplit;
+    const float mi = ok ? ld_dev(pp + lane * 66) : -INFINITY;
+    const float lsum = ok ? ld_dev(pp + lane * 66 + 1) : 0.0f;
+    float ovc[kMergeRegs];
 #pragma unroll
-    for (int t = 0; t < 2; t++) {
-        const int hl = wave + 4 * t;
-        const bool hv_ = hl < R;
-        const float* pp = a.part + (size_t)(kvh * R + (hv_ ? hl : 0)) * a.nsplit * 66;
-        const bool ok = hv_ && lane < a.nsplit;
-        mi[t] = ok ? ld_dev(pp + lane * 66) : -INFINITY;
-        lsum[t] = ok ? ld_dev(pp + lane * 66 + 1) : 0.0f;
+    for (int c = 0; c < kMergeRegs; c++) ovc[c] = c < a.nsplit ? ld_dev(pp + c * 66 + 2 + lane) : 0.0f;
+    const float M = wave_max_f32(fmaxf(mi, sink));
+    const float f = ok ? expf(mi - M) : 0.0f;
+    const float dsum = wave_sum_f32(ok ? lsum * f : 0.0f) + expf(sink - M);
+    es[wave][lane] = f;
+    wave_sync_lds();
+    // weighted merge of the chunks' values, dimension lane
+    float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int c = 0; c < kMergeRegs; c++) ov[t][c] = (hv_ && c < a.nsplit) ? ld_dev(pp + c * 66 + 2 + lane) : 0.0f;
-    }
-#pragma unroll
-    for (int t = 0; t < 2; t++) {
-        const int hl = wave + 4 * t;
-        if (hl >= R) break;
-        const int h = kvh * R + hl;
-        const float* pp = a.part + (size_t)h * a.nsplit * 66;
-        const float sink = sinkr[t];
-        const float M = wave_max_f32(fmaxf(mi[t], sink));
-        const float f = lane < a.nsplit ? expf(mi[t] - M) : 0.0f;
-        const float den = wave_sum_f32(lane < a.nsplit ? lsum[t] * f : 0.0f) + expf(sink - M);
-        es[hl][lane] = f;
-        wave_sync_lds();
-        // weighted merge of the chunks' values, dimension lane
-        float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int c = 0; c < kMergeRegs; c++) o[c & 3] = fmaf(ov[t][c], es[hl][c], o[c & 3]);
-        for (int c = kMergeRegs; c < a.nsplit; c++) o[c & 3] = fmaf(ld_dev(pp + c * 66 + 2 + lane), es[hl][c], o[c & 3]);
-        const float acc = (o[0] + o[1]) + (o[2] + o[3]);
-        const float val = acc * (1.0f / den);
-        a.ao[h * kAttnHd + lane] = val;
-        const float mb = half_max_f32(fabsf(val));
-        const float scq = fmaxf(1e-12f, mb) / 127.0f;
-        a.aq[h * kAttnHd + lane] = (int8_t)q8_round(val, scq);
-        if ((lane & 31) == 0) a.asb[h * 2 + (lane >> 5)] = scq;
-    }
+    for (int c = 0; c < kMergeRegs; c++) o[c & 3] = fmaf(ovc[c], es[wave][c], o[c & 3]);
+    for (int c = kMergeRegs; c < a.nsplit; c++) o[c & 3] = fmaf(ld_dev(pp + c * 66 + 2 + lane), es[wave][c], o[c & 3]);
+    const float acc = (o[0] + o[1]) + (o[2] + o[3]);
+    const float val = acc * (1.0f / dsum);
+    a.ao[h * kAttnHd + lane] = val;
+    const float mb = half_max_f32(fabsf(val));
+    const float scq = fmaxf(1e-12f, mb) / 127.0f;
+    a.aq[h * kAttnHd + lane] = (int8_t)q8_round(val, scq);
+    if ((lane & 31) == 0) a.asb[h * 2 + (lane >> 5)] = scq;
 }
 
 // ---- x[r] += wo[r] . ao + bo[r] (:837), one 8-row tile per workgroup ----
@@ -650,18 +648,21 @@ __global__ __launch_bounds__(256) void k_attn_oproj(AttnArgs a) {
     const int row = tile * 8 + ((tid >> 3) & 7);
     const float bo = a.L.bo[row], xo = a.x[row];
     TileSet ts;
-    ts.w[0] = ts.w[1] = a.L.wo + (size_t)tile * nsp * 64;
-    ts.s[0] = ts.s[1] = a.L.so + (size_t)tile * ns * 16;
+    ts.w = a.L.wo + (size_t)tile * nsp * 64;
+    ts.s = a.L.so + (size_t)tile * ns * 16;
     ts.nt = 1;
     ts.nsp = nsp;
-    stage_tiles(ts, lw, ls, [&] {
+    {
+        StageRegs<kOprojLoads, kOprojScales> g;
+        stage_issue(ts, g);
 #pragma unroll
         for (int k = 0; k < 8; k++) {
             const int i = tid + k * 256;
-            if (i < nbp * 8) xl[i] = ar[k];
+            if (i < nbp * 8) xl[xc_index(i)] = ar[k];
         }
-        if (tid < nbp) sl[tid] = as;
-    });
+        if (tid < nbp) sl[xs_index(tid)] = as;
+        stage_commit(ts, g, lw, ls);
+    }
     __syncthreads();
     if (tid >= 64) return;
     const float v = q8c_dot(lw, ls, nbp, xl, sl);
@@ -744,14 +745,15 @@ extern "C" {
 
 void cpb_attn_destroy(cpb_attn_t* h) {
     if (!h) return;
-    hipSetDevice(h->device);
-    if (h->stream) hipStreamSynchronize(h->stream);
+    // teardown: errors here have no caller to report to
+    (void)hipSetDevice(h->device);
+    if (h->stream) (void)hipStreamSynchronize(h->stream);
     for (void* p : h->layer_mem)
-        if (p) hipFree(p);
+        if (p) (void)hipFree(p);
     void* bufs[] = {h->kc, h->vc, h->rope, h->x, h->xq, h->aq, h->xsb, h->q, h->ao, h->asb, h->part, h->count};
     for (void* p : bufs)
-        if (p) hipFree(p);
-    if (h->own) hipStreamDestroy(h->own);
+        if (p) (void)hipFree(p);
+    if (h->own) (void)hipStreamDestroy(h->own);
     delete h;
 }
 
@@ -787,10 +789,10 @@ int cpb_attn_create(const cpb_attn_cfg* cfg, int device, cpb_attn_t** out) {
         (r = dm((void**)&h->part, (size_t)cfg->n_head * h->max_split * 66 * 4)) ||
         (r = dm((void**)&h->count, (size_t)cfg->n_head_kv * 4)))
         return bail(r);
-    // LDS beyond 64 KiB per workgroup (d = 4096: 110 KiB for k_attn_qkv) is opted into
+    // LDS beyond 64 KiB per workgroup (d = 4096: 136 KiB for k_attn_qkv) is opted into
     {
         const int nbp = cpb::q8c_nbp(cfg->d / 32), nbpo = cpb::q8c_nbp(cfg->n_head * 2);
-        const int lq = 2 * (nbp / 4) * 1024 + 2 * (nbp / 2) * 64 + 4 * (16 * cpb::attn_xt_stride(cfg->d) + 64) + nbp * 36;
+        const int lq = (int)cpb::qkv_lds_bytes(cfg->d);
         const int lo = (nbpo / 4) * 1024 + (nbpo / 2) * 64 + nbpo * 36;
         if (hipFuncSetAttribute((const void*)cpb::k_attn_qkv, hipFuncAttributeMaxDynamicSharedMemorySize, lq) != hipSuccess ||
             hipFuncSetAttribute((const void*)cpb::k_attn_oproj, hipFuncAttributeMaxDynamicSharedMemorySize, lo) != hipSuccess)
@@ -817,15 +819,16 @@ int cpb_attn_load_layer(cpb_attn_t* h, int layer, const float* attn_norm, const 
         return fail(CPB_EINVAL, "NULL tensor");
     HIP_OK_A(hipSetDevice(h->device));
     HIP_OK_A(hipStreamSynchronize(h->stream));
-    if (h->layer_mem[layer]) { hipFree(h->layer_mem[layer]); h->layer_mem[layer] = nullptr; h->loaded[layer] = false; }
+    if (h->layer_mem[layer]) { (void)hipFree(h->layer_mem[layer]); h->layer_mem[layer] = nullptr; h->loaded[layer] = false; }
     const size_t d = c.d, nq = (size_t)c.n_head * 64, nkv = (size_t)c.n_head_kv * 64;
-    // one allocation: four Q8 streams + scales, then the fp32 vectors
+    // one allocation: the four Q8 code streams back to back (q, k, v form one
+    // sequence of tiles for k_attn_qkv), then their scales, then the fp32 vectors
     const size_t mats[4][2] = {{nq, d}, {nkv, d}, {nkv, d}, {d, nq}};
     size_t off[4][2], o = 0;
-    for (int m = 0; m < 4; m++) {
-        off[m][0] = o; o += (cpb::q8c_code_bytes((int)mats[m][0], (int)mats[m][1]) + 255) / 256 * 256;
-        off[m][1] = o; o += (cpb::q8c_scale_bytes((int)mats[m][0], (int)mats[m][1]) + 255) / 256 * 256;
-    }
+    for (int m = 0; m < 4; m++) { off[m][0] = o; o += cpb::q8c_code_bytes((int)mats[m][0], (int)mats[m][1]); }
+    o = (o + 255) / 256 * 256;
+    for (int m = 0; m < 4; m++) { off[m][1] = o; o += cpb::q8c_scale_bytes((int)mats[m][0], (int)mats[m][1]); }
+    o = (o + 255) / 256 * 256;
     const size_t wbytes = o;
     const size_t vec[6] = {d, nq, nkv, nkv, d, (size_t)c.n_head};      // norm, bq, bk, bv, bo, sinks
     size_t voff[6];
@@ -842,12 +845,12 @@ int cpb_attn_load_layer(cpb_attn_t* h, int layer, const float* attn_norm, const 
         e = hipMemcpyAsync(staging, srcs[m], n * 2, hipMemcpyHostToDevice, h->stream);
         if (e == hipSuccess) {
             hipLaunchKernelGGL(cpb::k_q8c_quant, dim3(4096), dim3(256), 0, h->stream, staging, (int)mats[m][0],
-                               (int)mats[m][1], (cpb::u32x4*)(base + off[m][0]), (float*)(base + off[m][1]));
+                               (int)mats[m][1], (cpb::u32x4*)(base + off[m][0]), (float*)(base + off[m][1]), m < 3 ? 1 : 0);
             e = hipGetLastError();
         }
         if (e == hipSuccess) e = hipStreamSynchronize(h->stream);
     }
-    if (staging) hipFree(staging);
+    if (staging) (void)hipFree(staging);
     const float* vsrc[6] = {attn_norm, bq, bk, bv, bo, sinks};
     for (int k = 0; k < 6 && e == hipSuccess; k++) e = hipMemcpy(base + voff[k], vsrc[k], vec[k] * 4, hipMemcpyHostToDevice);
     if (e != hipSuccess) return fail(CPB_ENODEV, "attention layer load: %s", hipGetErrorString(e));
@@ -879,13 +882,11 @@ static int attn_launch(cpb_attn_t* h, int layer, int pos, float* dx) {
     a.rope = h->rope;
     a.xq = h->xq; a.xsb = h->xsb; a.q = h->q; a.ao = h->ao; a.aq = h->aq; a.asb = h->asb;
     a.part = h->part; a.count = h->count;
-    const int nbp = cpb::q8c_nbp(a.nb), nbpo = cpb::q8c_nbp(a.nbo);
-    // LDS: two tiles' codes (nbp / 4 step pairs x 1 KiB) and scales (nbp / 2 x 64 B), x, xn, activations
-    const size_t lds_qkv = (size_t)2 * (nbp / 4) * 1024 + (size_t)2 * (nbp / 2) * 64 +
-                           sizeof(float) * (16 * cpb::attn_xt_stride(c.d) + 64) + (size_t)nbp * 36;   // codes, scales, x^T, 64, activations
+    const int nbpo = cpb::q8c_nbp(a.nbo);
     const size_t lds_o = (size_t)(nbpo / 4) * 1024 + (size_t)(nbpo / 2) * 64 + (size_t)nbpo * 36;
-    cpb::launch(cpb::k_attn_qkv, dim3((c.n_head + 2 * c.n_head_kv) * 4), dim3(256), lds_qkv, h->stream, a);
-    cpb::launch(cpb::k_attn_core, dim3(c.n_head_kv, a.nsplit), dim3(256), 0, h->stream, a);
+    cpb::launch(cpb::k_attn_qkv, dim3(cpb::qkv_groups((c.n_head + 2 * c.n_head_kv) * 8)), dim3(256), cpb::qkv_lds_bytes(c.d),
+                h->stream, a);
+    cpb::launch(cpb::k_attn_core, dim3(c.n_head_kv, a.nsplit), dim3(512), 0, h->stream, a);
     cpb::launch(cpb::k_attn_oproj, dim3(c.d / 8), dim3(256), lds_o, h->stream, a);
     return hipGetLastError() == hipSuccess ? 0 : fail(CPB_ENODEV, "attention launch failed");
 }

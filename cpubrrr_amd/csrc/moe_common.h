@@ -61,12 +61,13 @@ CPB_DEV float e8m0_scale(uint32_t e, float xsb) { return e == 0 ? 0.0f : ldexpf(
 
 // Q8 round: (v / sc).round() in the reference's fp32 (quotient correctly
 // rounded, then half away from zero), clamped to +-127.  The quotient from
-// the hardware reciprocal, v * rcp(sc), is within a few ulp (< 2^-16 for
-// |v / sc| <= 128) of the exact one; unless it lies within 2^-10 of a
-// half-integer both round to the same integer (and round-to-nearest-even of
-// it agrees with half-away-from-zero), and only there (about one value in a
-// thousand) the IEEE division decides.
-CPB_DEV bool q8_near_half(float y) { return fabsf(__builtin_amdgcn_fractf(fabsf(y)) - 0.5f) < 0x1p-10f; }
+// the hardware reciprocal, y = v * rcp(sc), lies within 2^-15 of the IEEE
+// one for |v / sc| <= 128 (rcp within 1 ulp, the product rounded once: a
+// relative error below 1.5 * 2^-23, plus half an ulp of the IEEE quotient).
+// Unless y lies within 2^-13 of a half-integer, both round to the same
+// integer (and round-to-nearest-even of y agrees with half-away-from-zero);
+// only there (about one value in four thousand) the IEEE quotient decides.
+CPB_DEV bool q8_near_half(float y) { return fabsf(__builtin_amdgcn_fractf(fabsf(y)) - 0.5f) < 0x1p-13f; }
 CPB_DEV int8_t q8_clamp(float r) { return (int8_t)(int)fminf(fmaxf(r, -127.0f), 127.0f); }
 CPB_DEV int8_t q8_round(float v, float sc) {
     const float y = v * __builtin_amdgcn_rcpf(sc);
