@@ -171,7 +171,7 @@ struct TileSet {
 };
 template <int NL, int NS>
 struct StageRegs {
-    u32x4 r[NL];
+    u32x4 r[NL > 0 ? NL : 1];
     float4 sc[NS];
 };
 template <int NL, int NS>
@@ -217,23 +217,77 @@ CPB_DEV_HOST_INLINE int xs_index(int b) { return ((b >> 2) * 2 + (b & 1)) * 2 + 
 // The chain of this lane over one 8-row tile staged in LDS (codes lw, scales
 // ls), activations in LDS (xl: dwords in xc_index order; sl: scales in
 // xs_index order; both padded to q8c_nbp blocks with zeros).  Returns the
-// row's dot_q8_i8 in lane 0 of the row's group of 8.
+// row's dot_q8_i8 in lane 0 of the row's group of 8.  NSP > 0: the step-pair
+// count is NSP (== nbp / 4) and the chain is unrolled whole, so the LDS reads
+// are scheduled ahead of the fmas that wait for them; NSP == 0: any count.
+struct Q8cOps {
+    u32x4 w, xa;
+    float2 ws, xs;
+};
+CPB_DEV Q8cOps q8c_load(const u32x4* lw, const float2* wsc, const u32x4* xc, const float2* xsc, int sp, int lane) {
+    return Q8cOps{lw[sp * 64 + lane], xc[sp * 8], wsc[sp * 16], xsc[sp * 2]};
+}
+CPB_DEV void q8c_fma(const Q8cOps& o, float& acc) {
+    // steps 2sp (block 4sp + h) and 2sp + 1 (block 4sp + 2 + h)
+    const int d0 = sdot4(o.w[1], o.xa[1], sdot4(o.w[0], o.xa[0], 0));
+    acc = fmaf((float)d0, o.ws.x * o.xs.x, acc);
+    const int d1 = sdot4(o.w[3], o.xa[3], sdot4(o.w[2], o.xa[2], 0));
+    acc = fmaf((float)d1, o.ws.y * o.xs.y, acc);
+}
+// The same chain with this lane's codes in registers (wreg[sp]: its 16 bytes
+// of step pair sp, loaded in step order): step pair sp waits for its own load
+// only, so the chain runs while the later codes are still arriving.
+template <int NSP>
+CPB_DEV float q8c_dot_regs(const u32x4 (&wreg)[NSP], const float* ls, const uint32_t* xl, const float* sl) {
+    const int lane = threadIdx.x & 63, r = lane >> 3, h = (lane >> 2) & 1, j = lane & 3;
+    const float2* wsc = (const float2*)ls + r * 2 + h;
+    const u32x4* xc = (const u32x4*)xl + h * 4 + j;
+    const float2* xsc = (const float2*)sl + h;
+    float acc = 0.0f;
+    constexpr int kAhead = NSP < 3 ? NSP : 3;
+    Q8cOps ring[kAhead];
+#pragma unroll
+    for (int i = 0; i < kAhead; i++) ring[i] = Q8cOps{u32x4{}, xc[i * 8], wsc[i * 16], xsc[i * 2]};
+#pragma unroll
+    for (int sp = 0; sp < NSP; sp++) {
+        Q8cOps cur = ring[sp % kAhead];
+        cur.w = wreg[sp];
+        if (sp + kAhead < NSP)
+            ring[sp % kAhead] = Q8cOps{u32x4{}, xc[(sp + kAhead) * 8], wsc[(sp + kAhead) * 16], xsc[(sp + kAhead) * 2]};
+        q8c_fma(cur, acc);
+        // steps stay in load order (the integer dots do not depend on acc, and
+        // hoisting later ones would wait for later loads)
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    const float v = acc + dppf<0x12C>(acc);
+    const float v01 = v + dppf<0xB1>(v);
+    return v01 + dppf<0x4E>(v01);
+}
+
+template <int NSP>
 CPB_DEV float q8c_dot(const u32x4* lw, const float* ls, int nbp, const uint32_t* xl, const float* sl) {
     const int lane = threadIdx.x & 63, r = lane >> 3, h = (lane >> 2) & 1, j = lane & 3;
-    const int nsp = nbp / 4;
     const float2* wsc = (const float2*)ls + r * 2 + h;           // [sp][8][2] float2
     const u32x4* xc = (const u32x4*)xl + h * 4 + j;              // [sp][2][4] u32x4
     const float2* xsc = (const float2*)sl + h;                   // [sp][2] float2
     float acc = 0.0f;
+    if constexpr (NSP > 0) {
+        // a ring of the next kAhead step pairs' operands: step sp + kAhead is
+        // requested before step sp's fmas
+        constexpr int kAhead = NSP < 6 ? NSP : 6;
+        Q8cOps ring[kAhead];
+#pragma unroll
+        for (int i = 0; i < kAhead; i++) ring[i] = q8c_load(lw, wsc, xc, xsc, i, lane);
+#pragma unroll
+        for (int sp = 0; sp < NSP; sp++) {
+            const Q8cOps cur = ring[sp % kAhead];
+            if (sp + kAhead < NSP) ring[sp % kAhead] = q8c_load(lw, wsc, xc, xsc, sp + kAhead, lane);
+            q8c_fma(cur, acc);
+        }
+    } else {
+        const int nsp = nbp / 4;
 #pragma unroll 4
-    for (int sp = 0; sp < nsp; sp++) {
-        const u32x4 w = lw[sp * 64 + lane], xa = xc[sp * 8];
-        const float2 ws = wsc[sp * 16], xs = xsc[sp * 2];
-        // steps 2sp (block 4sp + h) and 2sp + 1 (block 4sp + 2 + h)
-        const int d0 = sdot4(w[1], xa[1], sdot4(w[0], xa[0], 0));
-        acc = fmaf((float)d0, ws.x * xs.x, acc);
-        const int d1 = sdot4(w[3], xa[3], sdot4(w[2], xa[2], 0));
-        acc = fmaf((float)d1, ws.y * xs.y, acc);
+        for (int sp = 0; sp < nsp; sp++) q8c_fma(q8c_load(lw, wsc, xc, xsc, sp, lane), acc);
     }
     // lanes 0-3 of each group of 8: v_j = acc0_j + acc1_j (lane + 4: row_ror by 12)
     const float v = acc + dppf<0x12C>(acc);
@@ -372,6 +426,7 @@ CPB_DEV_HOST_INLINE int qkv_groups(int tiles) {
     const int g = tiles < 256 ? tiles : 256;
     return g * kMaxTiles >= tiles ? g : (tiles + kMaxTiles - 1) / kMaxTiles;
 }
+template <int NSP>
 __global__ __launch_bounds__(256) void k_attn_qkv(AttnArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     const int nbp = q8c_nbp(a.nb), nsp = nbp / 4, ns = nbp / 2;
@@ -414,7 +469,27 @@ __global__ __launch_bounds__(256) void k_attn_qkv(AttnArgs a) {
     // every wave's x requests go out before any wave's weight requests (an
     // execution barrier, no memory wait): x then lands ahead of the stream
     __builtin_amdgcn_s_barrier();
-    {
+    u32x4 wreg[NSP > 0 ? NSP : 1];
+    if constexpr (NSP > 0) {
+        // the scales through LDS (requested first), each wave's own tile's
+        // codes straight into its registers: unconditional loads (a wave past
+        // the workgroup's tiles reads zeros from an empty range), so every
+        // wait below is counted exactly
+        StageRegs<0, kQkvScales> g;
+        stage_issue(ts, g);
+        const __amdgpu_buffer_rsrc_t rw =
+            buf_rsrc(a.L.wq + (size_t)(t0 + (wave < nt ? wave : 0)) * NSP * 64, wave < nt ? (uint32_t)NSP * 64 * 16 : 0u);
+        // the first half before the norm, the rest once its registers are free
+        constexpr int kEarly = NSP / 2;
+#pragma unroll
+        for (int sp = 0; sp < kEarly; sp++)
+            wreg[sp] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, (uint32_t)(sp * 64 + lane) * 16, 0, 2));
+        attn_norm_q8(xr, wr, a.d, a.nb, nbp, a.eps, xt, red, xl, sl, blockIdx.x == 0 ? a.xq : nullptr, a.xsb);
+#pragma unroll
+        for (int sp = kEarly; sp < NSP; sp++)
+            wreg[sp] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, (uint32_t)(sp * 64 + lane) * 16, 0, 2));
+        stage_commit(ts, g, lw, ls);
+    } else {
         StageRegs<kQkvLoads, kQkvScales> g;
         stage_issue(ts, g);
         attn_norm_q8(xr, wr, a.d, a.nb, nbp, a.eps, xt, red, xl, sl, blockIdx.x == 0 ? a.xq : nullptr, a.xsb);
@@ -422,7 +497,9 @@ __global__ __launch_bounds__(256) void k_attn_qkv(AttnArgs a) {
     }
     __syncthreads();
     if (wave >= nt) return;
-    const float v = q8c_dot(lw + wave * nsp * 64, ls + wave * ns * 16, nbp, xl, sl);
+    float v;
+    if constexpr (NSP > 0) v = q8c_dot_regs<NSP>(wreg, ls + wave * ns * 16, xl, sl);
+    else v = q8c_dot<NSP>(lw + wave * nsp * 64, ls + wave * ns * 16, nbp, xl, sl);
     if ((lane & 7) == 0) hv[wave][r] = v + bias;      // :786-793 dot + bias (row)
     wave_sync_lds();
     if (lane >= 4) return;
@@ -629,6 +706,7 @@ __global__ __launch_bounds__(512) void k_attn_core(AttnArgs a) {
 }
 
 // ---- x[r] += wo[r] . ao + bo[r] (:837), one 8-row tile per workgroup ----
+template <int NSP>
 __global__ __launch_bounds__(256) void k_attn_oproj(AttnArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     const int nbp = q8c_nbp(a.nbo), nsp = nbp / 4, ns = nbp / 2;
@@ -665,9 +743,17 @@ __global__ __launch_bounds__(256) void k_attn_oproj(AttnArgs a) {
     }
     __syncthreads();
     if (tid >= 64) return;
-    const float v = q8c_dot(lw, ls, nbp, xl, sl);
+    const float v = q8c_dot<NSP>(lw, ls, nbp, xl, sl);
     if ((tid & 7) == 0) a.x[row] = xo + (v + bo);
 }
+
+// Step-pair counts with a whole-chain unrolled instantiation: q / k / v at
+// d = 2880 (90 blocks padded to 92) and the o-projection at 64 heads (128
+// blocks); other shapes take the generic loop.
+constexpr int kQkvNsp = 23, kOprojNsp = 32;
+typedef void (*AttnKernel)(AttnArgs);
+inline AttnKernel qkv_kernel(int nsp) { return nsp == kQkvNsp ? k_attn_qkv<kQkvNsp> : k_attn_qkv<0>; }
+inline AttnKernel oproj_kernel(int nsp) { return nsp == kOprojNsp ? k_attn_oproj<kOprojNsp> : k_attn_oproj<0>; }
 
 }  // namespace cpb
 
@@ -794,8 +880,8 @@ int cpb_attn_create(const cpb_attn_cfg* cfg, int device, cpb_attn_t** out) {
         const int nbp = cpb::q8c_nbp(cfg->d / 32), nbpo = cpb::q8c_nbp(cfg->n_head * 2);
         const int lq = (int)cpb::qkv_lds_bytes(cfg->d);
         const int lo = (nbpo / 4) * 1024 + (nbpo / 2) * 64 + nbpo * 36;
-        if (hipFuncSetAttribute((const void*)cpb::k_attn_qkv, hipFuncAttributeMaxDynamicSharedMemorySize, lq) != hipSuccess ||
-            hipFuncSetAttribute((const void*)cpb::k_attn_oproj, hipFuncAttributeMaxDynamicSharedMemorySize, lo) != hipSuccess)
+        if (hipFuncSetAttribute((const void*)cpb::qkv_kernel(nbp / 4), hipFuncAttributeMaxDynamicSharedMemorySize, lq) != hipSuccess ||
+            hipFuncSetAttribute((const void*)cpb::oproj_kernel(nbpo / 4), hipFuncAttributeMaxDynamicSharedMemorySize, lo) != hipSuccess)
             return bail(fail(CPB_ENODEV, "LDS attribute (%d / %d bytes) refused", lq, lo));
     }
     std::vector<float> tab;
@@ -884,10 +970,10 @@ static int attn_launch(cpb_attn_t* h, int layer, int pos, float* dx) {
     a.part = h->part; a.count = h->count;
     const int nbpo = cpb::q8c_nbp(a.nbo);
     const size_t lds_o = (size_t)(nbpo / 4) * 1024 + (size_t)(nbpo / 2) * 64 + (size_t)nbpo * 36;
-    cpb::launch(cpb::k_attn_qkv, dim3(cpb::qkv_groups((c.n_head + 2 * c.n_head_kv) * 8)), dim3(256), cpb::qkv_lds_bytes(c.d),
+    cpb::launch(cpb::qkv_kernel(cpb::q8c_nbp(a.nb) / 4), dim3(cpb::qkv_groups((c.n_head + 2 * c.n_head_kv) * 8)), dim3(256), cpb::qkv_lds_bytes(c.d),
                 h->stream, a);
     cpb::launch(cpb::k_attn_core, dim3(c.n_head_kv, a.nsplit), dim3(512), 0, h->stream, a);
-    cpb::launch(cpb::k_attn_oproj, dim3(c.d / 8), dim3(256), lds_o, h->stream, a);
+    cpb::launch(cpb::oproj_kernel(nbpo / 4), dim3(c.d / 8), dim3(256), lds_o, h->stream, a);
     return hipGetLastError() == hipSuccess ? 0 : fail(CPB_ENODEV, "attention launch failed");
 }
 
