@@ -218,6 +218,8 @@ int check_cfg(const cpb_moe_cfg* c) {
     if (c->norm != CPB_NORM_GPTOSS && c->norm != CPB_NORM_QWEN) return fail(CPB_EINVAL, "bad norm %d", c->norm);
     if (c->norm == CPB_NORM_QWEN && (c->norm_nt < 1 || c->norm_nt > 64))
         return fail(CPB_EINVAL, "norm_nt must be in [1,64]");
+    if (c->norm == CPB_NORM_QWEN && c->d < 16 * c->norm_nt)
+        return fail(CPB_EINVAL, "norm_nt=%d: slices of d=%d shorter than 16 elements", c->norm_nt, c->d);
     return 0;
 }
 
@@ -247,7 +249,7 @@ int scratch_address(int device, unsigned char** out) {
 
 int ensure_staging(cpb_moe_t* h, size_t n) {
     if (h->staging_size >= n) return 0;
-    if (h->staging) hipFree(h->staging);
+    if (h->staging) (void)hipFree(h->staging);
     h->staging = nullptr;
     h->staging_size = 0;
     if (int r = dmalloc(&h->staging, n)) return r;
@@ -287,7 +289,7 @@ ParamSlots param_slots(const cpb_moe_cfg& c) {
 }
 
 void free_layer(LayerDev& L) {
-    hipFree(L.gu); hipFree(L.up); hipFree(L.dn);
+    (void)hipFree(L.gu); (void)hipFree(L.up); (void)hipFree(L.dn);
     L = LayerDev{};
 }
 
@@ -318,7 +320,7 @@ struct Timer {
 // Q4_K's {sumi, mint} and Q6_K's {sumi}, since the type is per layer.
 void free_trace(cpb_moe_t* h) {
     void* p[] = {h->t_gu, h->t_h, h->t_dn, h->t_gu_sums, h->t_dn_sums};
-    for (void* q : p) if (q) hipFree(q);
+    for (void* q : p) if (q) (void)hipFree(q);
     h->t_gu = h->t_h = h->t_dn = nullptr;
     h->t_gu_sums = h->t_dn_sums = nullptr;
 }
@@ -339,7 +341,7 @@ int ensure_trace(cpb_moe_t* h) {
 }
 
 void clear_graphs(cpb_moe_t* h) {
-    for (auto& g : h->graphs) hipGraphExecDestroy(g.second.first);
+    for (auto& g : h->graphs) (void)hipGraphExecDestroy(g.second.first);
     h->graphs.clear();
 }
 
@@ -352,8 +354,8 @@ void evict_lru_graph(cpb_moe_t* h) {
         if (it->second.second < old->second.second) old = it;
     // the graph may still be executing on the stream: destroying an exec
     // that is in flight is not allowed
-    hipStreamSynchronize(h->stream);
-    hipGraphExecDestroy(old->second.first);
+    (void)hipStreamSynchronize(h->stream);
+    (void)hipGraphExecDestroy(old->second.first);
     h->graphs.erase(old);
 }
 
@@ -664,11 +666,11 @@ int cpb_moe_forward_device(cpb_moe_t* h, int layer0, int n_layers, float* d_x, i
         int r = launch_direct(h, layer0, n_layers, d_x, n_tok, apply_norm);
         hipGraph_t g = nullptr;
         hipError_t ec = hipStreamEndCapture(h->stream, &g);
-        if (r) { if (g) hipGraphDestroy(g); return r; }
+        if (r) { if (g) (void)hipGraphDestroy(g); return r; }
         if (ec != hipSuccess) return fail(CPB_ENODEV, "graph capture failed: %s", hipGetErrorString(ec));
         hipGraphExec_t ge = nullptr;
         ec = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
-        hipGraphDestroy(g);
+        (void)hipGraphDestroy(g);
         if (ec != hipSuccess) return fail(CPB_ENODEV, "graph instantiate failed: %s", hipGetErrorString(ec));
         it = h->graphs.emplace(key, std::make_pair(ge, 0ull)).first;
     }
@@ -717,7 +719,7 @@ int cpb_moe_grouped_sums(cpb_moe_t* h, int layer, float* x, int n_tok, int apply
                              : np * d * (c.d_ff / 256) * (h->layers[layer].down_type == CPB_GGUF_Q4_K ? 2 : 1);
     int32_t *dgu = nullptr, *ddn = nullptr;
     int r;
-    if ((r = dmalloc(&dgu, ngu)) || (r = dmalloc(&ddn, ndn))) { hipFree(dgu); return r; }
+    if ((r = dmalloc(&dgu, ngu)) || (r = dmalloc(&ddn, ndn))) { (void)hipFree(dgu); return r; }
     r = 0;
     if (hipMemcpyAsync(h->x, x, n_tok * d * sizeof(float), hipMemcpyHostToDevice, h->stream) != hipSuccess) r = CPB_ENODEV;
     if (!r) r = layer_grouped(h, layer, h->x, n_tok, apply_norm, dgu, ddn);
@@ -726,8 +728,8 @@ int cpb_moe_grouped_sums(cpb_moe_t* h, int layer, float* x, int n_tok, int apply
                hipMemcpyAsync(dn_sums, ddn, ndn * 4, hipMemcpyDeviceToHost, h->stream) != hipSuccess ||
                hipStreamSynchronize(h->stream) != hipSuccess))
         r = fail(CPB_ENODEV, "grouped sums copy failed");
-    hipFree(dgu);
-    hipFree(ddn);
+    (void)hipFree(dgu);
+    (void)hipFree(ddn);
     return r;
 }
 
@@ -806,7 +808,7 @@ int cpb_moe_set_stream(cpb_moe_t* h, void* stream) {
     HIP_OK(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
     hipError_t e = hipEventRecord(ev, h->stream);
     if (e == hipSuccess) e = hipStreamWaitEvent(ns, ev, 0);
-    hipEventDestroy(ev);
+    (void)hipEventDestroy(ev);
     if (e != hipSuccess) return fail(CPB_ENODEV, "stream switch: %s", hipGetErrorString(e));
     h->stream = ns;
     return 0;
@@ -846,21 +848,21 @@ int cpb_moe_kernel_times(cpb_moe_t* h, double ms[3], long n[3]) {
 
 void cpb_moe_destroy(cpb_moe_t* h) {
     if (!h) return;
-    hipSetDevice(h->device);
-    if (h->stream) hipStreamSynchronize(h->stream);
+    (void)hipSetDevice(h->device);
+    if (h->stream) (void)hipStreamSynchronize(h->stream);
     clear_graphs(h);
     void* gbufs[] = {h->g_xsum, h->g_hsum, h->g_hbuf,
                      h->g_inv, h->g_xn, h->g_xsb, h->g_logits, h->g_wts, h->g_hsb, h->g_dnout, h->g_xq, h->g_hq, h->g_ximg,
                      h->g_himg, h->g_lstar, h->g_lbound, h->g_ids, h->g_fallback, h->g_sorted, h->g_ntiles, h->g_tiles,
                      h->d_special};
-    for (void* p : gbufs) hipFree(p);
+    for (void* p : gbufs) (void)hipFree(p);
     for (auto& L : h->layers) free_layer(L);
     void* bufs[] = {h->params, h->x, h->dec_base, h->t_gu, h->t_h,
                     h->t_dn, h->t_gu_sums, h->t_dn_sums, h->staging};
-    for (void* p : bufs) if (p) hipFree(p);
-    for (auto& u : h->ev_used) { hipEventDestroy(u.second.first); hipEventDestroy(u.second.second); }
-    for (auto e : h->ev_pool) hipEventDestroy(e);
-    if (h->own) hipStreamDestroy(h->own);
+    for (void* p : bufs) if (p) (void)hipFree(p);
+    for (auto& u : h->ev_used) { (void)hipEventDestroy(u.second.first); (void)hipEventDestroy(u.second.second); }
+    for (auto e : h->ev_pool) (void)hipEventDestroy(e);
+    if (h->own) (void)hipStreamDestroy(h->own);
     delete h;
 }
 

@@ -527,11 +527,11 @@ int cpb_head_bytes(const cpb_head_cfg* c, size_t* out) {
 
 void cpb_head_destroy(cpb_head_t* h) {
     if (!h) return;
-    hipSetDevice(h->device);
-    if (h->stream) hipStreamSynchronize(h->stream);
+    (void)hipSetDevice(h->device);
+    if (h->stream) (void)hipStreamSynchronize(h->stream);
     for (void* p : h->base)
-        if (p) hipFree(p);
-    if (h->own) hipStreamDestroy(h->own);
+        if (p) (void)hipFree(p);
+    if (h->own) (void)hipStreamDestroy(h->own);
     delete h;
 }
 
@@ -616,7 +616,7 @@ int cpb_head_load(cpb_head_t* h, const uint16_t* out_w, const float* out_norm) {
         e = hipGetLastError();
     }
     if (e == hipSuccess) e = hipStreamSynchronize(h->stream);
-    hipFree(staging);
+    (void)hipFree(staging);
     if (e != hipSuccess) return fail(CPB_ENODEV, "head load: %s", hipGetErrorString(e));
     h->loaded = true;
     return 0;

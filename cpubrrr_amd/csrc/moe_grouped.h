@@ -61,7 +61,7 @@ struct GroupedArgs {
 // token tiles of one expert and row group then run back to back on one XCD
 // and re-read that weight slice from its L2 instead of HBM.  Returns false for
 // workgroups past the last item.
-CPB_DEV inline bool grouped_item(int ntiles, int ngroups, int* tile, int* group) {
+CPB_DEV bool grouped_item(int ntiles, int ngroups, int* tile, int* group) {
     const int L = blockIdx.x, total = ntiles * ngroups;
     const int per = (total + 7) / 8;
     const int slot = L >> 3, w = (L & 7) * per + slot;

@@ -15,7 +15,7 @@ CPB_DEV_HOST_INLINE int kq_units(int type) { return type == 12 ? kQ4Units : kQ6U
 CPB_DEV_HOST_INLINE int kq_sb_bytes(int type) { return type == 12 ? 144 : 210; }
 
 // engine_qwen2.rs:40-51 converts IEEE binary16 exactly; so does the hardware.
-CPB_DEV inline float half_bits(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (uint16_t)h); }
+CPB_DEV float half_bits(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (uint16_t)h); }
 
 struct KqArgs {
     const u32x4* gu;         // gate+up stream layout (k_repack_kq_gateup)

@@ -214,7 +214,9 @@ __global__ __launch_bounds__(1024) void k_down_kq(KqArgs a) {
     float* hsl = (float*)(h16 + K * a.dff / 16);                  // [K*nsbf]
     float* part = hsl + K * nsbf;                                 // [nsbf][64]
     float* vv = part + nsbf * 64;                                 // [64]
-    float4* hst = (float4*)(((size_t)(vv + 64) + 15) & ~(size_t)15);   // [K*dff/32][8] h chunks (one-chunk case)
+    // h chunks (one-chunk case), k-major [8][K*dff/32]: consecutive threads'
+    // 16-byte accesses fall on consecutive banks
+    float4* hst = (float4*)(((size_t)(vv + 64) + 15) & ~(size_t)15);
 
     int es[8];
 #pragma unroll
@@ -266,7 +268,7 @@ __global__ __launch_bounds__(1024) void k_down_kq(KqArgs a) {
         if ((int)threadIdx.x < nch) {
             chunk_max(threadIdx.x);
 #pragma unroll
-            for (int k = 0; k < 8; k++) hst[threadIdx.x * 8 + k] = hv[k];
+            for (int k = 0; k < 8; k++) hst[k * nch + threadIdx.x] = hv[k];
         }
     } else {
         for (int c = threadIdx.x; c < nch; c += nth) {
@@ -284,22 +286,31 @@ __global__ __launch_bounds__(1024) void k_down_kq(KqArgs a) {
 #pragma unroll
         for (int k = 0; k < 8; k++) amax = fmaxf(amax, cmax[blk * 8 + k]);
         const float sc = amax / 127.0f;
-        {
-            const float4* src = one_chunk ? hst + c * 8 : (const float4*)(a.hbuf + (size_t)c * 32);
+        if (one_chunk) {
+#pragma unroll
+            for (int k = 0; k < 8; k++) hv[k] = hst[k * nch + c];
+        } else {
+            const float4* src = (const float4*)(a.hbuf + (size_t)c * 32);
 #pragma unroll
             for (int k = 0; k < 8; k++) hv[k] = src[k];
         }
         const int slot = c / (a.dff / 32), cc = c % (a.dff / 32);   // expert slot, chunk within it
         int8_t* dst = hql + slot * hstride + (cc / 8) * kXsPad + (cc % 8) * 32;
-        int s16[2] = {0, 0};
+        // the chunk's 32 bytes in two q8_round16 (one rarely taken branch per
+        // 16 values); the per-16 sums from the packed bytes (signed dot with ones)
+        float hf[32];
 #pragma unroll
         for (int k = 0; k < 8; k++) {
-            const float4 v = hv[k];
-            const int q0 = q8_round(v.x, sc), q1 = q8_round(v.y, sc), q2 = q8_round(v.z, sc), q3 = q8_round(v.w, sc);
-            s16[k / 4] += q0 + q1 + q2 + q3;
-            *(uint32_t*)(dst + 4 * k) = (uint32_t)(uint8_t)q0 | ((uint32_t)(uint8_t)q1 << 8) |
-                                        ((uint32_t)(uint8_t)q2 << 16) | ((uint32_t)(uint8_t)q3 << 24);
+            hf[4 * k] = hv[k].x; hf[4 * k + 1] = hv[k].y; hf[4 * k + 2] = hv[k].z; hf[4 * k + 3] = hv[k].w;
         }
+        uint32_t qp[8];
+        q8_round16(hf, sc, qp);
+        q8_round16(hf + 16, sc, qp + 4);
+        int s16[2] = {0, 0};
+#pragma unroll
+        for (int k = 0; k < 8; k++) s16[k / 4] = sdot4(qp[k], 0x01010101u, s16[k / 4]);
+        ((u32x4*)dst)[0] = u32x4{qp[0], qp[1], qp[2], qp[3]};
+        ((u32x4*)dst)[1] = u32x4{qp[4], qp[5], qp[6], qp[7]};
         h32[c] = s16[0] + s16[1];
         h16[2 * c] = s16[0];
         h16[2 * c + 1] = s16[1];

@@ -25,7 +25,7 @@ __global__ __launch_bounds__(320) void k_route(RouteArgs a) {
 int launch_route(const RouteArgs* a, hipStream_t s) {
     if (a->n_expert > 256 || a->n_expert < a->top_k || a->top_k > 8 || a->d % 32 != 0 || a->d > 4096)
         return -22;
-    launch(k_route, dim3(a->n_expert), dim3(route_threads(a->d)), route_lds_bytes(a->d), s, *a);
+    launch(k_route, dim3(a->n_expert), dim3(route_threads(a->d)), route_lds_bytes(a->d, route_slices(*a)), s, *a);
     return hipGetLastError() == hipSuccess ? 0 : -19;
 }
 

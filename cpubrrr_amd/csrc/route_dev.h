@@ -178,10 +178,28 @@ constexpr int kRouteC = 16;         // consecutive elements per thread in route_
 // the 16 lanes' 16-byte reads spread over the banks; the chain's one-group
 // look-ahead past the last row lands in the reduction area behind it
 CPB_DEV_HOST inline int route_xt_stride(int d) { return (d / 16 + 32 + 63) / 64 * 64 + 4; }
-CPB_DEV_HOST inline size_t route_lds_bytes(int d) {
+// Qwen: slice q of the nt serial slices in row q (the same padding and bank
+// offset for the longest slice, ceil(d / nt))
+CPB_DEV_HOST inline int route_slice_stride(int d, int nt) { return ((d + nt - 1) / nt + 32 + 63) / 64 * 64 + 4; }
+// slices of the Qwen sum of squares, 1 for the gpt-oss order
+CPB_DEV_HOST inline int route_slices(const RouteArgs& a) { return a.norm == 0 ? 1 : a.norm_nt; }
+CPB_DEV_HOST inline size_t route_lds_bytes(int d, int nt) {
     const size_t xt = sizeof(float) * 16 * (size_t)route_xt_stride(d);
-    const size_t xr = sizeof(float) * (size_t)d;
-    return (xt > xr ? xt : xr) + sizeof(double) * 64 + 64;
+    const size_t xs = sizeof(float) * (size_t)nt * route_slice_stride(d, nt);
+    return (xt > xs ? xt : xs) + sizeof(double) * 64 + 64;
+}
+// s + v*v for the 32 values of g in order, unfused (the reference's Qwen
+// slice sums are a multiply then an add)
+CPB_DEV float sumsq_serial(const f32x4 (&g)[8], float s) {
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const float p = g[u][c] * g[u][c];
+            s = s + p;
+        }
+    }
+    return s;
 }
 
 // ---- router logit from unscaled products, shared by the decode route and
@@ -269,7 +287,7 @@ CPB_DEV void route_expert(const RouteArgs& a, int e, int NEg, unsigned char* sme
     const int d = a.d;
     const int et = tid - 64, ws = wv - 1, nws = (nth >> 6) - 1;     // element thread / wave
     float* xl = (float*)smem;                                  // transposed (gpt-oss) or plain (Qwen) x
-    double* dred = (double*)(smem + route_lds_bytes(d) - sizeof(double) * 64 - 64);   // [64]
+    double* dred = (double*)(smem + route_lds_bytes(d, route_slices(a)) - sizeof(double) * 64 - 64);   // [64]
     float* sinv = (float*)(dred + 64);
 
     const int j0 = et * kRouteC;
@@ -279,22 +297,17 @@ CPB_DEV void route_expert(const RouteArgs& a, int e, int NEg, unsigned char* sme
     const __amdgpu_buffer_rsrc_t rW = buf_rsrc(a.router_w + (size_t)e * d, (uint32_t)d * 4);
     const bool use_g = a.norm_w && a.apply_norm;
     const __amdgpu_buffer_rsrc_t rg = buf_rsrc(a.norm_w, use_g ? (uint32_t)d * 4 : 0u);
+    // the raw loads; converted where used (after x is in LDS), so that the
+    // LDS copy of x waits for x only, not for the router and norm weights
     float xf[16], gf[16], wf[16];
-    u32x4 xv[4] = {};
+    u32x4 xv[4] = {}, wq[4] = {}, gq[4] = {};
     if (wv > 0) {
-        u32x4 wq[4], gq[4];
 #pragma unroll
         for (int k = 0; k < 4; k++) xv[k] = ld_dev16(rx, off + 16 * k);     // may come from this launch
 #pragma unroll
         for (int k = 0; k < 4; k++) wq[k] = __builtin_amdgcn_raw_buffer_load_b128(rW, off + 16 * k, 0, 0);
 #pragma unroll
         for (int k = 0; k < 4; k++) gq[k] = __builtin_amdgcn_raw_buffer_load_b128(rg, off + 16 * k, 0, 0);
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            xf[i] = act ? __uint_as_float(xv[i >> 2][i & 3]) : 0.0f;
-            gf[i] = use_g ? __uint_as_float(gq[i >> 2][i & 3]) : 1.0f;
-            wf[i] = act ? __uint_as_float(wq[i >> 2][i & 3]) : 0.0f;
-        }
     }
     const double b = a.router_b ? (double)a.router_b[e] : 0.0;
     // Q8 (qk == 0): element thread et quantises element et % 32 of this
@@ -315,18 +328,34 @@ CPB_DEV void route_expert(const RouteArgs& a, int e, int NEg, unsigned char* sme
         if (a.norm == 0) {
             // chain q's element m = x[16m + q] lives in element thread m,
             // register q: transposed (chain q's elements contiguous)
+            // (from the loaded registers: the writes wait for x only, not
+            // for the router and norm weights loaded beside it)
             if (act) {
 #pragma unroll
-                for (int i = 0; i < 16; i++) xl[i * S + et] = xf[i];
+                for (int i = 0; i < 16; i++) xl[i * S + et] = __uint_as_float(xv[i >> 2][i & 3]);
             }
             // zero padding past d/16: fma(0, 0, acc) leaves acc (>= 0) unchanged
             for (int c = d / 16 + et; c < S; c += nth - 64) {
 #pragma unroll
                 for (int i = 0; i < 16; i++) xl[i * S + c] = 0.0f;
             }
-        } else if (act) {
+        } else {
+            // slice q (the first d % nt slices one element longer) in row q
+            // of stride SQ; zeros past each slice: p + 0 * 0 leaves p (>= 0)
+            const int nt = a.norm_nt, base = d / nt, rem = d % nt, SQ = route_slice_stride(d, nt);
+            const int big = rem * (base + 1);                 // elements of the longer slices
+            if (act) {
+                // this thread's 16 elements start at (q, i) and cross into
+                // row q + 1 at most once (slices are >= 16 long: d >= 16 nt)
+                const int q = j0 < big ? j0 / (base + 1) : rem + (j0 - big) / base;
+                const int i = j0 - (q < rem ? q * (base + 1) : big + (q - rem) * base);
+                const int cross = base + (q < rem ? 1 : 0) - i;          // elements left in row q
+                const int a0 = q * SQ + i, a1 = (q + 1) * SQ - cross;
 #pragma unroll
-            for (int k = 0; k < 4; k++) ((u32x4*)xl)[et * 4 + k] = xv[k];
+                for (int u = 0; u < 16; u++) xl[(u < cross ? a0 : a1) + u] = __uint_as_float(xv[u >> 2][u & 3]);
+            }
+            for (int q = 0; q < nt; q++)
+                for (int i = base + (q < rem ? 1 : 0) + et; i < SQ; i += nth - 64) xl[q * SQ + i] = 0.0f;
         }
     }
     __syncthreads();
@@ -365,26 +394,38 @@ CPB_DEV void route_expert(const RouteArgs& a, int e, int NEg, unsigned char* sme
             if (lane == 0) *sinv = 1.0f / sqrtf(ssq / (float)d + a.eps);
         } else if (a.apply_norm) {
             // nt serial slices, then a serial sum of the partials (nt <= 64)
-            const int nt = a.norm_nt, base = d / nt, rem = d % nt;
+            // lane q streams row q (lanes past nt repeat row 0, unused) with
+            // the next 32 values' reads issued before the current 32 adds
+            const int nt = a.norm_nt, SQ = route_slice_stride(d, nt), nm = (d + nt - 1) / nt;
             float ps = 0.0f;
-            if (lane < nt) {
-                const int s0 = lane * base + (lane < rem ? lane : rem), sz = base + (lane < rem ? 1 : 0);
-                int i = 0;
-                for (; i + 16 <= sz; i += 16) {
-                    float t[16];
-#pragma unroll
-                    for (int u = 0; u < 16; u++) t[u] = xl[s0 + i + u];
-#pragma unroll
-                    for (int u = 0; u < 16; u++) ps += t[u] * t[u];
-                }
-                for (; i < sz; i++) { const float v = xl[s0 + i]; ps += v * v; }
+            uint32_t ra = lds_addr(xl + (lane < nt ? lane : 0) * SQ);
+            f32x4 ga[8], gb[8];
+            lds_read8(ga, ra);
+            for (int m = 0;; m += 64) {
+                lds_read8(gb, ra + 128);
+                lds_wait_older8(ga);
+                ps = sumsq_serial(ga, ps);
+                if (m + 32 >= nm) break;
+                lds_read8(ga, ra + 256);
+                lds_wait_older8(gb);
+                ps = sumsq_serial(gb, ps);
+                if (m + 64 >= nm) break;
+                ra += 256;
             }
+            lds_wait_all();
             float tot = 0.0f;
             for (int k = 0; k < nt; k++) tot += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ps), k));
             if (lane == 0) *sinv = 1.0f / sqrtf(tot / (float)d + a.eps);
         }
     } else {
         // ---- router logit, unscaled, beside the sum-of-squares chain ----
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            xf[i] = act ? __uint_as_float(xv[i >> 2][i & 3]) : 0.0f;
+            gf[i] = use_g ? __uint_as_float(gq[i >> 2][i & 3]) : 1.0f;
+            wf[i] = act ? __uint_as_float(wq[i >> 2][i & 3]) : 0.0f;
+        }
         LogitThread lt;
         logit_phase1(wf, xf, gf, lt, dred, ws);
         logit_phase2(lt, act, dred, ws);

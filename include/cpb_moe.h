@@ -59,7 +59,7 @@ typedef struct cpb_moe_cfg {
     int   router;         /* CPB_ROUTER_*                               */
     int   act;            /* CPB_ACT_*                                  */
     int   norm;           /* CPB_NORM_*                                 */
-    int   norm_nt;        /* CPB_NORM_QWEN: number of slices (reference NT = 12) */
+    int   norm_nt;        /* CPB_NORM_QWEN: number of slices (reference NT = 12), 1..64, d >= 16 * norm_nt */
     float alpha, limit;   /* SwiGLU-OAI constants (1.702, 7.0)          */
     float rms_eps;
     int   wtype_gate_up;  /* CPB_GGUF_MXFP4 or CPB_GGUF_Q4_K            */

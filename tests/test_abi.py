@@ -49,6 +49,16 @@ def test_bad_configs_rejected(mut):
     assert L.lib().cpb_moe_last_error()
 
 
+@pytest.mark.parametrize("mut", [dict(norm_nt=0), dict(norm_nt=65), dict(d=256, norm_nt=17)])
+def test_bad_qwen_norm_slices_rejected(mut):
+    # the Qwen sum of squares runs one lane per slice, each at least 16 long
+    cfg = MoeConfig.qwen3(d=256, d_ff=256, n_expert=8, top_k=2)
+    for k, v in mut.items():
+        setattr(cfg, k, v)
+    assert _create(cfg) == L.CPB_EINVAL, mut
+    assert L.lib().cpb_moe_last_error()
+
+
 def test_null_args():
     lib = L.lib()
     assert lib.cpb_moe_create(None, 0, None) == L.CPB_EINVAL
