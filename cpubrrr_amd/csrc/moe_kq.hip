@@ -215,8 +215,11 @@ __global__ __launch_bounds__(1024) void k_down_kq(KqArgs a) {
     float* part = hsl + K * nsbf;                                 // [nsbf][64]
     float* vv = part + nsbf * 64;                                 // [64]
     // h chunks (one-chunk case), k-major [8][K*dff/32]: consecutive threads'
-    // 16-byte accesses fall on consecutive banks
-    float4* hst = (float4*)(((size_t)(vv + 64) + 15) & ~(size_t)15);
+    // 16-byte accesses fall on consecutive banks.  Offset from smem (not a
+    // cast of the address), so that the compiler keeps it an LDS pointer: as
+    // a generic one its accesses were flat, counted with the weight loads,
+    // and reading them back waited for the whole weight stream.
+    float4* hst = (float4*)(smem + ((((unsigned char*)(vv + 64) - smem) + 15) & ~15));
 
     int es[8];
 #pragma unroll
