@@ -204,7 +204,6 @@ __global__ __launch_bounds__(1024) void k_down_kq(KqArgs a) {
     constexpr int U = TYPE == 12 ? kQ4Units : kQ6Units;
     const int K = a.top_k, RT = 64 / K, nsbf = a.dff / 256, T = a.d / RT;
     const int lane = threadIdx.x & 63, q = uniform((int)(threadIdx.x >> 6));
-    const int nth = blockDim.x;
     const int ei = lane / RT, rr = lane % RT, t = blockIdx.x, row = t * RT + rr;
     const int hstride = nsbf * kXsPad;                            // LDS bytes per expert slot
     int8_t* hql = (int8_t*)smem;                                  // [K][nsbf][kXsPad]
@@ -228,17 +227,18 @@ __global__ __launch_bounds__(1024) void k_down_kq(KqArgs a) {
 #pragma unroll
     for (int k = 1; k < 8; k++) if (ei == k) e = es[k];
 
-    // this thread's 32-value chunk of h first (one chunk per thread when
-    // K*dff/32 <= the block size, as for every supported shape but the
-    // largest), then the weights of (slot ei, row, superblock q): the chunk
-    // lands before the weight stream, so the Q8_K below runs while the
-    // weights are in flight (a wave's loads complete in order)
+    // this thread's 32-value chunk of h first (K * dff / 32 chunks, at most
+    // the dff / 4 threads since top_k <= 8: one chunk per thread), then the
+    // weights of (slot ei, row, superblock q): the chunk lands before the
+    // weight stream, so the Q8_K below runs while the weights are in flight
+    // (a wave's loads complete in order).  Every access below that the Q8_K
+    // makes is to LDS: a global one on any path would make the compiler wait
+    // for the weights there.
     const int nch = K * a.dff / 32;
-    const bool one_chunk = nch <= nth;
+    const int c = (int)threadIdx.x;
     float4 hv[8];
     {
-        const int c = one_chunk && (int)threadIdx.x < nch ? (int)threadIdx.x : 0;
-        const float4* src = (const float4*)(a.hbuf + (size_t)c * 32);
+        const float4* src = (const float4*)(a.hbuf + (size_t)(c < nch ? c : 0) * 32);
 #pragma unroll
         for (int k = 0; k < 8; k++) hv[k] = src[k];
     }
@@ -256,9 +256,8 @@ __global__ __launch_bounds__(1024) void k_down_kq(KqArgs a) {
     __builtin_amdgcn_sched_barrier(0);
 
     // Q8_K of hbuf (engine_qwen2.rs:288-300): chunk c = 32 values; a 256-block
-    // is 8 chunks.  Pass 1: chunk amax (the one-chunk case straight-line, so
-    // that it waits for the chunk's loads only, not the weights behind them).
-    auto chunk_max = [&](int c) {
+    // is 8 chunks.  Pass 1: chunk amax, the chunk to LDS.
+    if (c < nch) {
         float m = 0.0f;
 #pragma unroll
         for (int k = 0; k < 8; k++) {
@@ -266,37 +265,19 @@ __global__ __launch_bounds__(1024) void k_down_kq(KqArgs a) {
             m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
         }
         cmax[c] = m;
-    };
-    if (one_chunk) {
-        if ((int)threadIdx.x < nch) {
-            chunk_max(threadIdx.x);
 #pragma unroll
-            for (int k = 0; k < 8; k++) hst[k * nch + threadIdx.x] = hv[k];
-        }
-    } else {
-        for (int c = threadIdx.x; c < nch; c += nth) {
-            const float4* src = (const float4*)(a.hbuf + (size_t)c * 32);
-#pragma unroll
-            for (int k = 0; k < 8; k++) hv[k] = src[k];
-            chunk_max(c);
-        }
+        for (int k = 0; k < 8; k++) hst[k * nch + c] = hv[k];
     }
     __syncthreads();
     // pass 2: scale per 256 (amax seeded 1e-12), round, sums per 32 and 16
-    for (int c = threadIdx.x; c < nch; c += nth) {
+    if (c < nch) {
         const int blk = c / 8;
         float amax = 1e-12f;
 #pragma unroll
         for (int k = 0; k < 8; k++) amax = fmaxf(amax, cmax[blk * 8 + k]);
         const float sc = amax / 127.0f;
-        if (one_chunk) {
 #pragma unroll
-            for (int k = 0; k < 8; k++) hv[k] = hst[k * nch + c];
-        } else {
-            const float4* src = (const float4*)(a.hbuf + (size_t)c * 32);
-#pragma unroll
-            for (int k = 0; k < 8; k++) hv[k] = src[k];
-        }
+        for (int k = 0; k < 8; k++) hv[k] = hst[k * nch + c];
         const int slot = c / (a.dff / 32), cc = c % (a.dff / 32);   // expert slot, chunk within it
         int8_t* dst = hql + slot * hstride + (cc / 8) * kXsPad + (cc % 8) * 32;
         // the chunk's 32 bytes in two q8_round16 (one rarely taken branch per
@@ -434,9 +415,10 @@ int launch_gateup_kq(const KqArgs& a, bool trace, hipStream_t s) {
 
 int launch_down_kq(const KqArgs& a, bool trace, hipStream_t s) {
     const int K = a.top_k, nsbf = a.dff / 256, RT = 64 / K;
+    if (K * a.dff / 32 > 64 * nsbf) return -22;                  // one h chunk per thread (top_k <= 8)
     const size_t lds = (size_t)K * nsbf * kXsPad + (size_t)K * a.dff / 32 * 4 * 2 + (size_t)K * a.dff / 16 * 4 +
                        (size_t)K * nsbf * 4 + (size_t)nsbf * 64 * 4 + 64 * 4 +
-                       (K * a.dff / 32 <= 64 * nsbf ? (size_t)K * a.dff / 32 * 128 + 16 : 0);
+                       (size_t)K * a.dff / 32 * 128 + 16;
     const dim3 grid(a.d / RT), block(64 * nsbf);
     if (a.down_type == 12) {
         if (trace) launch((k_down_kq<12, true>), grid, block, lds, s, a);
