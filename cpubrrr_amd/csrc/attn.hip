@@ -236,7 +236,11 @@ CPB_DEV void q8c_fma(const Q8cOps& o, float& acc) {
 }
 // The same chain with this lane's codes in registers (wreg[sp]: its 16 bytes
 // of step pair sp, loaded in step order): step pair sp waits for its own load
-// only, so the chain runs while the later codes are still arriving.
+// only, so the chain runs while the later codes are still arriving.  An empty
+// volatile asm passes acc and step sp's codes through, so step sp's dots come
+// after step sp - 1's fma: as plain code the compiler hoisted later steps'
+// dots, whose operands are the later loads, and the chain waited for the
+// whole stream.
 template <int NSP>
 CPB_DEV float q8c_dot_regs(const u32x4 (&wreg)[NSP], const float* ls, const uint32_t* xl, const float* sl) {
     const int lane = threadIdx.x & 63, r = lane >> 3, h = (lane >> 2) & 1, j = lane & 3;
@@ -244,51 +248,32 @@ CPB_DEV float q8c_dot_regs(const u32x4 (&wreg)[NSP], const float* ls, const uint
     const u32x4* xc = (const u32x4*)xl + h * 4 + j;
     const float2* xsc = (const float2*)sl + h;
     float acc = 0.0f;
-    constexpr int kAhead = NSP < 3 ? NSP : 3;
-    Q8cOps ring[kAhead];
-#pragma unroll
-    for (int i = 0; i < kAhead; i++) ring[i] = Q8cOps{u32x4{}, xc[i * 8], wsc[i * 16], xsc[i * 2]};
 #pragma unroll
     for (int sp = 0; sp < NSP; sp++) {
-        Q8cOps cur = ring[sp % kAhead];
-        cur.w = wreg[sp];
-        if (sp + kAhead < NSP)
-            ring[sp % kAhead] = Q8cOps{u32x4{}, xc[(sp + kAhead) * 8], wsc[(sp + kAhead) * 16], xsc[(sp + kAhead) * 2]};
-        q8c_fma(cur, acc);
-        // steps stay in load order (the integer dots do not depend on acc, and
-        // hoisting later ones would wait for later loads)
-        __builtin_amdgcn_sched_barrier(0);
+        u32x4 w = wreg[sp];
+        asm volatile("" : "+v"(acc), "+v"(w));
+        const u32x4 xa = xc[sp * 8];
+        const float2 ws = wsc[sp * 16], xs = xsc[sp * 2];
+        // steps 2sp (block 4sp + h) and 2sp + 1 (block 4sp + 2 + h)
+        const int d0 = sdot4(w[1], xa[1], sdot4(w[0], xa[0], 0));
+        acc = fmaf((float)d0, ws.x * xs.x, acc);
+        const int d1 = sdot4(w[3], xa[3], sdot4(w[2], xa[2], 0));
+        acc = fmaf((float)d1, ws.y * xs.y, acc);
     }
     const float v = acc + dppf<0x12C>(acc);
     const float v01 = v + dppf<0xB1>(v);
     return v01 + dppf<0x4E>(v01);
 }
 
-template <int NSP>
 CPB_DEV float q8c_dot(const u32x4* lw, const float* ls, int nbp, const uint32_t* xl, const float* sl) {
     const int lane = threadIdx.x & 63, r = lane >> 3, h = (lane >> 2) & 1, j = lane & 3;
     const float2* wsc = (const float2*)ls + r * 2 + h;           // [sp][8][2] float2
     const u32x4* xc = (const u32x4*)xl + h * 4 + j;              // [sp][2][4] u32x4
     const float2* xsc = (const float2*)sl + h;                   // [sp][2] float2
     float acc = 0.0f;
-    if constexpr (NSP > 0) {
-        // a ring of the next kAhead step pairs' operands: step sp + kAhead is
-        // requested before step sp's fmas
-        constexpr int kAhead = NSP < 6 ? NSP : 6;
-        Q8cOps ring[kAhead];
-#pragma unroll
-        for (int i = 0; i < kAhead; i++) ring[i] = q8c_load(lw, wsc, xc, xsc, i, lane);
-#pragma unroll
-        for (int sp = 0; sp < NSP; sp++) {
-            const Q8cOps cur = ring[sp % kAhead];
-            if (sp + kAhead < NSP) ring[sp % kAhead] = q8c_load(lw, wsc, xc, xsc, sp + kAhead, lane);
-            q8c_fma(cur, acc);
-        }
-    } else {
-        const int nsp = nbp / 4;
+    const int nsp = nbp / 4;
 #pragma unroll 4
-        for (int sp = 0; sp < nsp; sp++) q8c_fma(q8c_load(lw, wsc, xc, xsc, sp, lane), acc);
-    }
+    for (int sp = 0; sp < nsp; sp++) q8c_fma(q8c_load(lw, wsc, xc, xsc, sp, lane), acc);
     // lanes 0-3 of each group of 8: v_j = acc0_j + acc1_j (lane + 4: row_ror by 12)
     const float v = acc + dppf<0x12C>(acc);
     const float v01 = v + dppf<0xB1>(v);                 // lane 0: v0 + v1, lane 2: v2 + v3
@@ -499,7 +484,7 @@ __global__ __launch_bounds__(256) void k_attn_qkv(AttnArgs a) {
     if (wave >= nt) return;
     float v;
     if constexpr (NSP > 0) v = q8c_dot_regs<NSP>(wreg, ls + wave * ns * 16, xl, sl);
-    else v = q8c_dot<NSP>(lw + wave * nsp * 64, ls + wave * ns * 16, nbp, xl, sl);
+    else v = q8c_dot(lw + wave * nsp * 64, ls + wave * ns * 16, nbp, xl, sl);
     if ((lane & 7) == 0) hv[wave][r] = v + bias;      // :786-793 dot + bias (row)
     wave_sync_lds();
     if (lane >= 4) return;
@@ -706,7 +691,6 @@ __global__ __launch_bounds__(512) void k_attn_core(AttnArgs a) {
 }
 
 // ---- x[r] += wo[r] . ao + bo[r] (:837), one 8-row tile per workgroup ----
-template <int NSP>
 __global__ __launch_bounds__(256) void k_attn_oproj(AttnArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     const int nbp = q8c_nbp(a.nbo), nsp = nbp / 4, ns = nbp / 2;
@@ -743,17 +727,58 @@ __global__ __launch_bounds__(256) void k_attn_oproj(AttnArgs a) {
     }
     __syncthreads();
     if (tid >= 64) return;
-    const float v = q8c_dot<NSP>(lw, ls, nbp, xl, sl);
+    const float v = q8c_dot(lw, ls, nbp, xl, sl);
     if ((tid & 7) == 0) a.x[row] = xo + (v + bo);
 }
 
-// Step-pair counts with a whole-chain unrolled instantiation: q / k / v at
+// The o-projection at 64 heads (32 step pairs): one wave per 8-row tile,
+// its codes loaded straight into registers in step order and the chain
+// consuming each step pair as it lands.  Activations and the tile's scales
+// go through LDS (the wave's own; no barrier).
+__global__ __launch_bounds__(64) void k_attn_oproj_wave(AttnArgs a) {
+    constexpr int NSP = 32, NBP = 4 * NSP, NS = 2 * NSP;
+    __shared__ __align__(16) uint32_t xl[NBP * 8];
+    __shared__ __align__(16) float sl[NBP];
+    __shared__ __align__(16) float ls[NS * 16];
+    const int tile = blockIdx.x, lane = threadIdx.x;
+    // activations (nbo = NBP blocks: 16 dwords a lane), their scales, the tile's
+    // scales, then the codes; bias and residual rows last
+    const __amdgpu_buffer_rsrc_t ra = buf_rsrc(a.aq, (uint32_t)NBP * 32);
+    const __amdgpu_buffer_rsrc_t rsb = buf_rsrc(a.asb, (uint32_t)NBP * 4);
+    const __amdgpu_buffer_rsrc_t rs = buf_rsrc(a.L.so + (size_t)tile * NS * 16, (uint32_t)NS * 64);
+    uint32_t ar[16];
+#pragma unroll
+    for (int k = 0; k < 16; k++) ar[k] = __builtin_amdgcn_raw_buffer_load_b32(ra, (uint32_t)(lane + k * 64) * 4, 0, 0);
+    float as[2];
+#pragma unroll
+    for (int k = 0; k < 2; k++) as[k] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsb, (uint32_t)(lane + k * 64) * 4, 0, 0));
+    u32x4 sc[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) sc[k] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (uint32_t)(lane + k * 64) * 16, 0, 0));
+    const __amdgpu_buffer_rsrc_t rw = buf_rsrc(a.L.wo + (size_t)tile * NSP * 64, (uint32_t)NSP * 64 * 16);
+    u32x4 wreg[NSP];
+#pragma unroll
+    for (int sp = 0; sp < NSP; sp++)
+        wreg[sp] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, (uint32_t)(sp * 64 + lane) * 16, 0, 2));
+    const int row = tile * 8 + (lane >> 3);
+    const float bo = a.L.bo[row], xo = a.x[row];
+#pragma unroll
+    for (int k = 0; k < 16; k++) xl[xc_index(lane + k * 64)] = ar[k];
+#pragma unroll
+    for (int k = 0; k < 2; k++) sl[xs_index(lane + k * 64)] = as[k];
+#pragma unroll
+    for (int k = 0; k < 4; k++) ((u32x4*)ls)[lane + k * 64] = sc[k];
+    wave_sync_lds();
+    const float v = q8c_dot_regs<NSP>(wreg, ls, xl, sl);
+    if ((lane & 7) == 0) a.x[row] = xo + (v + bo);
+}
+
+// Step-pair counts with a register-streamed instantiation: q / k / v at
 // d = 2880 (90 blocks padded to 92) and the o-projection at 64 heads (128
-// blocks); other shapes take the generic loop.
+// blocks, k_attn_oproj_wave); other shapes take the LDS-staged kernels.
 constexpr int kQkvNsp = 23, kOprojNsp = 32;
 typedef void (*AttnKernel)(AttnArgs);
 inline AttnKernel qkv_kernel(int nsp) { return nsp == kQkvNsp ? k_attn_qkv<kQkvNsp> : k_attn_qkv<0>; }
-inline AttnKernel oproj_kernel(int nsp) { return nsp == kOprojNsp ? k_attn_oproj<kOprojNsp> : k_attn_oproj<0>; }
 
 }  // namespace cpb
 
@@ -881,7 +906,7 @@ int cpb_attn_create(const cpb_attn_cfg* cfg, int device, cpb_attn_t** out) {
         const int lq = (int)cpb::qkv_lds_bytes(cfg->d);
         const int lo = (nbpo / 4) * 1024 + (nbpo / 2) * 64 + nbpo * 36;
         if (hipFuncSetAttribute((const void*)cpb::qkv_kernel(nbp / 4), hipFuncAttributeMaxDynamicSharedMemorySize, lq) != hipSuccess ||
-            hipFuncSetAttribute((const void*)cpb::oproj_kernel(nbpo / 4), hipFuncAttributeMaxDynamicSharedMemorySize, lo) != hipSuccess)
+            hipFuncSetAttribute((const void*)cpb::k_attn_oproj, hipFuncAttributeMaxDynamicSharedMemorySize, lo) != hipSuccess)
             return bail(fail(CPB_ENODEV, "LDS attribute (%d / %d bytes) refused", lq, lo));
     }
     std::vector<float> tab;
@@ -973,7 +998,8 @@ static int attn_launch(cpb_attn_t* h, int layer, int pos, float* dx) {
     cpb::launch(cpb::qkv_kernel(cpb::q8c_nbp(a.nb) / 4), dim3(cpb::qkv_groups((c.n_head + 2 * c.n_head_kv) * 8)), dim3(256), cpb::qkv_lds_bytes(c.d),
                 h->stream, a);
     cpb::launch(cpb::k_attn_core, dim3(c.n_head_kv, a.nsplit), dim3(512), 0, h->stream, a);
-    cpb::launch(cpb::oproj_kernel(nbpo / 4), dim3(c.d / 8), dim3(256), lds_o, h->stream, a);
+    if (nbpo / 4 == cpb::kOprojNsp) cpb::launch(cpb::k_attn_oproj_wave, dim3(c.d / 8), dim3(64), 0, h->stream, a);
+    else cpb::launch(cpb::k_attn_oproj, dim3(c.d / 8), dim3(256), lds_o, h->stream, a);
     return hipGetLastError() == hipSuccess ? 0 : fail(CPB_ENODEV, "attention launch failed");
 }
 
