@@ -8,13 +8,17 @@
 //   k_attn_qkv   rmsnorm (16-lane sum of squares) + Q8 per 32 of x, then the
 //                q / k / v rows: the reference's Q8 dot (8 fp32 chains per
 //                row, one lane each), bias, RoPE from the table, cache write;
+//                one workgroup per CU, 2-3 RoPE-complete 8-row tiles each;
 //   k_attn_core  per (kv-head, chunk of 128 positions): scores of the group's
 //                q-heads, softmax weights, weighted v; a window of 128 is one
 //                chunk and finishes in the workgroup in the reference's order,
 //                longer spans leave per-chunk (max, sum, weighted v) that the
 //                last workgroup of the kv-head merges with the sink; then Q8
 //                of the heads' outputs;
-//   k_attn_oproj x[r] += wo[r] . ao + bo[r].
+//   k_attn_oproj x[r] += wo[r] . ao + bo[r] (k_attn_oproj_wave at 64 heads:
+//                one wave per 8-row tile, codes in registers).
+// At the gpt-oss shapes the codes of q / k / v and of the o-projection are
+// loaded straight into registers and each chain consumes them in load order.
 // The projections, RoPE and the cache rows are the reference's operations in
 // its order (bit for bit given the same RoPE table, which the host computes
 // once with the reference's formula); the softmax goes through expf (and,
