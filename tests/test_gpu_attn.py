@@ -8,8 +8,9 @@ the order of the softmax sums differ), their Q8 codes within one step on the
 rare value that the last ulp moves across a rounding boundary, and x bit for
 bit (where a code moved, against the oracle's o-projection of the GPU's own
 codes).  Covers the sliding window of even layers, the
-full-causal odd layers, an odd block count, the gpt-oss shape, reset and
-the device entry point."""
+full-causal odd layers, an odd block count, the gpt-oss shape (register-
+streamed q / k / v and o-projection), the shape limits (d = 4096, 128 heads:
+the LDS-staged kernels at their largest), reset and the device entry point."""
 import numpy as np
 import pytest
 
@@ -123,3 +124,12 @@ def test_long_context_merge():
     # a full-causal layer past several 128-position chunks (the chunk merge with
     # the sink, a partial last chunk), GQA 4 q-heads per kv-head
     check_seq(256, 8, 2, 4, 560, layers=(1,), seed=9, max_seq=576)
+
+
+def test_shape_limits():
+    # d = 4096 and 128 q-heads (16 kv-heads): the LDS-staged q / k / v path at
+    # three tiles per workgroup (its 24 loads per thread) and the staged
+    # o-projection at 64 step pairs (16 loads per thread), full causal and
+    # window layers
+    check_seq(4096, 128, 16, 4, 6, seed=11, max_seq=8, xs=1.0)
+
