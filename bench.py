@@ -136,6 +136,22 @@ def batched_result(c, args, ms, n_tok, kt) -> dict:
     }
 
 
+def grouping_padding(blk, c, tokens) -> dict:
+    """Tile slots the grouped GEMMs compute for a batch (pairs grouped by
+    expert, 32-token tiles, the last tile of each expert padded) against the
+    (token, slot) pairs themselves.  The ids come from the per-token decode
+    path, which the grouped path matches bit for bit."""
+    import numpy as np
+    counts = np.zeros(c["ne"], np.int64)
+    for t in tokens:
+        _, tr = blk.forward(0, t, c["norm"], trace=True)
+        np.add.at(counts, tr["ids"], 1)
+    pairs = int(counts.sum())
+    tiles = int(np.ceil(counts / 32).sum())
+    return {"pairs": pairs, "experts_used": int((counts > 0).sum()), "tiles": tiles, "tile_slots": 32 * tiles,
+            "overhead": round(32 * tiles / pairs - 1, 4), "max_pairs_per_expert": int(counts.max())}
+
+
 def calib_copy(args) -> None:
     """A copy kernel of known size: its FETCH_SIZE / WRITE_SIZE give the
     counter-to-bytes factor for the kernels of the same run."""
@@ -626,6 +642,8 @@ def main() -> int:
 
     if n_tok > 1:
         out = batched_result(c, args, ms, n_tok, kt)
+        # padding of the token tiles, on the step's initial batch
+        out["padding"] = grouping_padding(blk, c, [synth.token(d, 0, i) for i in range(n_tok)])
         if not args.no_cpu:
             log("timing the CPU baseline ...")
             out["cpu_baseline"] = cpu_baseline(host_keep, c, args.cpu_seconds)
