@@ -188,16 +188,14 @@ CPB_DEV_HOST inline size_t route_lds_bytes(int d, int nt) {
     const size_t xs = sizeof(float) * (size_t)nt * route_slice_stride(d, nt);
     return (xt > xs ? xt : xs) + sizeof(double) * 64 + 64;
 }
-// s + v*v for the 32 values of g in order, unfused (the reference's Qwen
-// slice sums are a multiply then an add)
-CPB_DEV float sumsq_serial(const f32x4 (&g)[8], float s) {
+// s + p for the 32 values of g in order (the Qwen slice chain over squares
+// already rounded to fp32: the reference's multiply then add, with the
+// multiplies off the dependent chain)
+CPB_DEV float sum_serial32(const f32x4 (&g)[8], float s) {
 #pragma unroll
     for (int u = 0; u < 8; u++) {
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const float p = g[u][c] * g[u][c];
-            s = s + p;
-        }
+        for (int c = 0; c < 4; c++) s = s + g[u][c];
     }
     return s;
 }
@@ -277,8 +275,8 @@ CPB_DEV void logit_final(const double* dred, int nws, int d, double b, float inv
 // sum of squares (16 fma chains, chain q over x[16m + q],
 // engine_gpt2.rs:710-726) runs in 16 lanes of wave 0 over a transposed copy
 // (chain q's elements contiguous); the Qwen one (nt serial slices,
-// engine_qwen2.rs:457-467) over a plain copy.  Meanwhile the element waves
-// compute the router logit as the fp64 sum of the unscaled products W_j * x_j
+// engine_qwen2.rs:457-467) over the squares, in slice rows.  Meanwhile the
+// element waves compute the router logit as the fp64 sum of the unscaled products W_j * x_j
 // * g_j (scaled by the norm scale once that is known; its bound covers every
 // rounding of the reference's fp32 path, see logit_final).
 CPB_DEV_HOST_INLINE int route_threads(int d) { return 64 + (d / 16 + 63) / 64 * 64; }
@@ -340,8 +338,10 @@ CPB_DEV void route_expert(const RouteArgs& a, int e, int NEg, unsigned char* sme
                 for (int i = 0; i < 16; i++) xl[i * S + c] = 0.0f;
             }
         } else {
-            // slice q (the first d % nt slices one element longer) in row q
-            // of stride SQ; zeros past each slice: p + 0 * 0 leaves p (>= 0)
+            // the squares x_j * x_j (rounded to fp32, as the reference's
+            // multiply) of slice q (the first d % nt slices one element
+            // longer) in row q of stride SQ; zeros past each slice: p + 0
+            // leaves p (>= 0)
             const int nt = a.norm_nt, base = d / nt, rem = d % nt, SQ = route_slice_stride(d, nt);
             const int big = rem * (base + 1);                 // elements of the longer slices
             if (act) {
@@ -352,7 +352,10 @@ CPB_DEV void route_expert(const RouteArgs& a, int e, int NEg, unsigned char* sme
                 const int cross = base + (q < rem ? 1 : 0) - i;          // elements left in row q
                 const int a0 = q * SQ + i, a1 = (q + 1) * SQ - cross;
 #pragma unroll
-                for (int u = 0; u < 16; u++) xl[(u < cross ? a0 : a1) + u] = __uint_as_float(xv[u >> 2][u & 3]);
+                for (int u = 0; u < 16; u++) {
+                    const float v = __uint_as_float(xv[u >> 2][u & 3]);
+                    xl[(u < cross ? a0 : a1) + u] = v * v;
+                }
             }
             for (int q = 0; q < nt; q++)
                 for (int i = base + (q < rem ? 1 : 0) + et; i < SQ; i += nth - 64) xl[q * SQ + i] = 0.0f;
@@ -394,8 +397,9 @@ CPB_DEV void route_expert(const RouteArgs& a, int e, int NEg, unsigned char* sme
             if (lane == 0) *sinv = 1.0f / sqrtf(ssq / (float)d + a.eps);
         } else if (a.apply_norm) {
             // nt serial slices, then a serial sum of the partials (nt <= 64)
-            // lane q streams row q (lanes past nt repeat row 0, unused) with
-            // the next 32 values' reads issued before the current 32 adds
+            // lane q streams row q of squares (lanes past nt repeat row 0,
+            // unused) with the next 32 values' reads issued before the
+            // current 32 adds: one dependent add per element
             const int nt = a.norm_nt, SQ = route_slice_stride(d, nt), nm = (d + nt - 1) / nt;
             float ps = 0.0f;
             uint32_t ra = lds_addr(xl + (lane < nt ? lane : 0) * SQ);
@@ -404,11 +408,11 @@ CPB_DEV void route_expert(const RouteArgs& a, int e, int NEg, unsigned char* sme
             for (int m = 0;; m += 64) {
                 lds_read8(gb, ra + 128);
                 lds_wait_older8(ga);
-                ps = sumsq_serial(ga, ps);
+                ps = sum_serial32(ga, ps);
                 if (m + 32 >= nm) break;
                 lds_read8(ga, ra + 256);
                 lds_wait_older8(gb);
-                ps = sumsq_serial(gb, ps);
+                ps = sum_serial32(gb, ps);
                 if (m + 64 >= nm) break;
                 ra += 256;
             }
