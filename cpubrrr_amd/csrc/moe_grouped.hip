@@ -547,7 +547,9 @@ int launch_grouped_layer(const GroupedArgs& a, bool trace, hipStream_t s, const 
     } else {
         launch(k_prep_batch, dim3(nt), dim3(256), sizeof(float) * (2 * a.d + 64), s, a);
     }
-    launch(k_router_batch, dim3(a.ne, (nt + kRouteTok - 1) / kRouteTok), dim3(256), sizeof(double) * 64, s, a);
+    // one thread per kRouteC elements, whole waves (the decode route's element waves)
+    launch(k_router_batch, dim3(a.ne, (nt + kRouteTok - 1) / kRouteTok), dim3((a.d / kRouteC + 63) / 64 * 64),
+           sizeof(double) * 64, s, a);
     launch(k_select_batch, dim3(nt), dim3(64), select_lds_bytes(a.ne, a.d, kExactGroupWide), s, a);
     launch(k_group, dim3(1), dim3(1024), 0, s, a);
     if (a.kq) {
