@@ -161,7 +161,8 @@ __global__ __launch_bounds__(64) void k_select_batch(GroupedArgs a) {
 }
 
 // ---- 4. group the (token, slot) pairs by expert (stable), tile table ----
-// One workgroup of 16 waves; wave w takes a contiguous run of pairs.  Per
+// Batches whose token x expert table exceeds its LDS budget (k_group_dense
+// below handles the others).  One workgroup of 16 waves; wave w takes a contiguous run of pairs.  Per
 // 64-pair group a wave ranks its lanes among those of the same expert with one
 // ballot per distinct expert present (not per expert of the layer), keeping
 // a running per-wave count per expert in LDS; the waves' counts are then
@@ -243,6 +244,78 @@ __global__ __launch_bounds__(1024) void k_group(GroupedArgs a) {
     for (int e = w; e < ne; e += kGroupWaves) {
         const int c = cnt_l[e], nt = (c + 31) / 32;
         for (int j = lane; j < nt; j += 64) a.tiles[toff_l[e] + j] = int4{e, off_l[e] + 32 * j, min(32, c - 32 * j), 0};
+    }
+}
+
+// The same grouping from a token x expert table in LDS, for batches whose
+// table fits (n_tok * ne <= kGroupDenseMax bytes).  A token's k experts are
+// distinct, so the stable rank of pair (t, slot) among its expert's pairs is
+// the number of earlier tokens that chose that expert.  Byte M[t][e] = slot +
+// 1 of expert e in token t (0: not chosen); thread (e, part) counts column e
+// over its run of tokens, the counts are scanned expert major, part minor,
+// and the thread writes its column's pairs in token order: sorted is the
+// pair-ranking kernel's, entry for entry, with no per-expert ballots.
+constexpr int kGroupDenseMax = 128 * 1024;
+CPB_DEV_HOST_INLINE size_t group_dense_lds(int n_tok, int ne) {
+    return ((size_t)n_tok * ne + 15) / 16 * 16 + sizeof(int) * (1024 + 3 * 256);
+}
+__global__ __launch_bounds__(1024) void k_group_dense(GroupedArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int nt = a.n_tok, ne = a.ne, k = a.k, np = nt * k;
+    const size_t mb = ((size_t)nt * ne + 15) / 16 * 16;
+    uint8_t* M = smem;
+    int* cnt = (int*)(smem + mb);                         // [P][ne]
+    int* off_l = cnt + 1024;
+    int* toff_l = off_l + 256;
+    int* cnt_l = toff_l + 256;
+    for (size_t i = tid; i < mb / 16; i += 1024) ((u32x4*)M)[i] = u32x4{0, 0, 0, 0};
+    __syncthreads();
+    for (int p = tid; p < np; p += 1024) {
+        const int t = p / k;
+        M[(size_t)t * ne + a.ids[p]] = (uint8_t)(p - t * k + 1);
+    }
+    __syncthreads();
+    const int P = 1024 / ne, e = tid % ne, part = tid / ne;
+    const bool act = part < P;
+    const int tpp = (nt + P - 1) / P, t0 = act ? part * tpp : 0, t1 = act ? min(nt, t0 + tpp) : 0;
+    int c = 0;
+    for (int t = t0; t < t1; t++) c += M[(size_t)t * ne + e] != 0;
+    if (act) cnt[part * ne + e] = c;
+    __syncthreads();
+    // per expert: total, exclusive prefix over experts (counts and 32-pair tiles)
+    if (w == 0) {
+        int o = 0, to = 0;
+        for (int base = 0; base < ne; base += 64) {
+            const int ee = base + lane;
+            int ce = 0;
+            if (ee < ne)
+                for (int v = 0; v < P; v++) ce += cnt[v * ne + ee];
+            const int tl = (ce + 31) / 32;
+            int ic = ce, it = tl;
+#pragma unroll
+            for (int s2 = 1; s2 < 64; s2 <<= 1) {
+                const int uc = __shfl_up(ic, s2), ut = __shfl_up(it, s2);
+                if (lane >= s2) { ic += uc; it += ut; }
+            }
+            if (ee < ne) { off_l[ee] = o + ic - ce; toff_l[ee] = to + it - tl; cnt_l[ee] = ce; }
+            o += __shfl(ic, 63);
+            to += __shfl(it, 63);
+        }
+        if (lane == 0) *a.ntiles = to;
+    }
+    __syncthreads();
+    if (act) {
+        int r = off_l[e];
+        for (int v = 0; v < part; v++) r += cnt[v * ne + e];
+        for (int t = t0; t < t1; t++) {
+            const int sl = M[(size_t)t * ne + e];
+            if (sl) a.sorted[r++] = t * k + sl - 1;
+        }
+    }
+    for (int ee = w; ee < ne; ee += 16) {
+        const int ce = cnt_l[ee], ntl = (ce + 31) / 32;
+        for (int j = lane; j < ntl; j += 64) a.tiles[toff_l[ee] + j] = int4{ee, off_l[ee] + 32 * j, min(32, ce - 32 * j), 0};
     }
 }
 
@@ -551,7 +624,10 @@ int launch_grouped_layer(const GroupedArgs& a, bool trace, hipStream_t s, const 
     launch(k_router_batch, dim3(a.ne, (nt + kRouteTok - 1) / kRouteTok), dim3((a.d / kRouteC + 63) / 64 * 64),
            sizeof(double) * 64, s, a);
     launch(k_select_batch, dim3(nt), dim3(64), select_lds_bytes(a.ne, a.d, kExactGroupWide), s, a);
-    launch(k_group, dim3(1), dim3(1024), 0, s, a);
+    if ((size_t)a.n_tok * a.ne <= kGroupDenseMax)
+        launch(k_group_dense, dim3(1), dim3(1024), group_dense_lds(a.n_tok, a.ne), s, a);
+    else
+        launch(k_group, dim3(1), dim3(1024), 0, s, a);
     if (a.kq) {
         if (launch_kq_gemms(a, trace, s, ev)) return -19;
         launch(k_combine_batch, dim3((unsigned)std::min<size_t>(((size_t)nt * (a.d / 4) + 255) / 256, 2048)), dim3(256), 0, s, a);

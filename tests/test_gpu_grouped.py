@@ -33,6 +33,9 @@ def per_token(blk, X, apply_norm):
     (2880, 2880, 32, 4, 64, 3, True, 1.1),
     (960, 960, 32, 8, 45, 4, True, 1.1),
     (480, 480, 8, 3, 29, 5, False, None),
+    # 1100 tokens x 128 experts: past the token x expert table's LDS size,
+    # so the pairs are grouped by the ranking kernel (k_group), not k_group_dense
+    (384, 64, 128, 4, 1100, 6, True, None),
 ])
 def test_grouped_equals_per_token(gpu, d, dff, ne, k, n_tok, seed, norm, zipf):
     say(f"case grouped d={d} dff={dff} ne={ne} k={k} n_tok={n_tok} seed={seed} norm={norm} zipf={zipf}")
