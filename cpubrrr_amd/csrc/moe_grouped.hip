@@ -152,7 +152,7 @@ __global__ __launch_bounds__(64) void k_select_batch(GroupedArgs a) {
     si.xn = a.xn + (size_t)t * a.d;
     si.ne = a.ne; si.k = a.k; si.d = a.d;
     si.logits = a.logits + (size_t)t * a.ne;      // written by every workgroup: one per token
-    select_topk_wave<4, 2>(si, smem, &sel, true);
+    select_topk_wave<8, 4>(si, smem, &sel, true);
     if (lane < a.k) {
         a.ids[(size_t)t * a.k + lane] = sel.ids[lane];
         a.wts[(size_t)t * a.k + lane] = sel.wts[lane];

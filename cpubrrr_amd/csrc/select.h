@@ -49,38 +49,44 @@ struct Selection {
 // reaches the lowest lower bound of the provisional top-k, then rank those
 // exactly (descending, lowest index first).  sL / sH: LDS values and upper
 // bounds of all NE experts; sSel: LDS [K] provisional choice, overwritten;
-// pst: LDS scratch of exact_group(CAND) * exact_stride(d) floats and as many
+// pst: LDS scratch of exact_group(CAND) * exact_stride(d) floats, then NE
 // ints.  One wavefront.
 template <int CAND, int CHUNK>
 CPB_DEV void exact_reselect(double* sL, const double* sH, int* sSel, int NE, int K, const float* __restrict__ router_w,
                             const float* __restrict__ router_b, const float* __restrict__ xn, int d, float* pst) {
     const int lane = threadIdx.x & 63;
     constexpr int NG = exact_group(CAND);
-    int* sCand = (int*)(pst + NG * exact_stride(d));   // [NG]
+    int* sList = (int*)(pst + NG * exact_stride(d));   // [NE] every candidate, ascending
     // candidates: intervals reaching the lowest lower bound of the selected
     double tau = 1e300;
     for (int i = 0; i < K; i++) { const int e = sSel[i]; tau = fmin(tau, sL[e] - (sH[e] - sL[e])); }
     // the others can never reach the top k
     for (int e = lane; e < NE; e += 64)
         if (!(sH[e] >= tau)) sL[e] = -1e300;
+    // the candidates in ascending order, 64 experts per ballot
+    int nl = 0;
+    {
+        const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
+        for (int base = 0; base < NE; base += 64) {
+            const int e = base + lane;
+            const bool c = e < NE && sH[e] >= tau;
+            const uint64_t m = __ballot(c);
+            if (c) sList[nl + __popcll(m & below)] = e;
+            nl += __popcll(m);
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     const __amdgpu_buffer_rsrc_t rx = buf_rsrc(xn, (uint32_t)d * 4);
     const int stride = exact_stride(d);
     // candidates in groups of kExactGroup: the wave writes each candidate's
     // fp32 products W[j]*xn[j] to LDS (coalesced row loads), then lane c runs
     // candidate c's serial chain acc = b; acc += p_j over them
-    int e_next = 0;
-    for (;;) {
-        // the group's candidates (wave-uniform scan), their ids in LDS
-        int ng = 0;
-        for (; e_next < NE && ng < NG; e_next++) {
-            if (!(sH[e_next] >= tau)) continue;
-            if (lane == 0) sCand[ng] = e_next;
-            ng++;
-        }
-        if (ng == 0) break;
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    for (int g0 = 0; g0 < nl; g0 += NG) {
+        // the group's candidates
+        const int ng = min(NG, nl - g0);
+        const int* sCand = sList + g0;
         if constexpr (CAND == 1) {
             // one 16-byte load pair per lane in flight (few registers)
             for (int c = 0; c < ng; c++) {
@@ -182,10 +188,17 @@ CPB_DEV void exact_reselect(double* sL, const double* sH, int* sSel, int NE, int
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
-    for (int e = lane; e < NE; e += 64) {
+    // exact ranking among the candidates (every other expert is below them
+    // all, and the candidates include the k provisional choices)
+    for (int i = lane; i < nl; i += 64) {
+        const int e = sList[i];
         const double v = sL[e];
         int r = 0;
-        for (int j = 0; j < NE; j++) { const double o = sL[j]; r += (o > v) || (o == v && j < e); }
+        for (int j = 0; j < nl; j++) {
+            const int oe = sList[j];
+            const double o = sL[oe];
+            r += (o > v) || (o == v && oe < e);
+        }
         if (r < K) sSel[r] = e;
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -210,7 +223,7 @@ struct SelectIn {
 };
 // LDS bytes select_topk_wave may use (its exact fallback)
 CPB_DEV_HOST_INLINE size_t select_lds_bytes(int ne, int d, int group = kExactGroup) {
-    return sizeof(double) * 2 * ne + 64 + sizeof(float) * group * exact_stride(d) + sizeof(int) * group;
+    return sizeof(double) * 2 * ne + 64 + sizeof(float) * group * exact_stride(d) + sizeof(int) * ne;
 }
 
 // Wave-wide maximum of a 32-bit unsigned value via DPP (quad swaps, half-row
