@@ -425,21 +425,40 @@ CPB_DEV v16f grouped_parts(const WeightStream& ws, int P, unsigned char* smem, c
         const float* sl = (const float*)(st + kBlkPerPart * 32 * kSlot) + ti;
         v16f acc = {}, Dc, Dn;
         float sc_c, sc_n;
+        // activation operands two blocks ahead: buffer j & 1 holds block j's
+        // until its MFMA is issued, then takes block j + 2's
+        u32x4 xa[2][2];
+        float sa[2];
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            xa[j][0] = *(const u32x4*)(xp + j * 32 * kSlot);
+            xa[j][1] = *(const u32x4*)(xp + j * 32 * kSlot + 16);
+            sa[j] = sl[j * 32];
+        }
         {
-            const u32x4 x0 = *(const u32x4*)xp, x1 = *(const u32x4*)(xp + 16);
-            sc_c = sl[0];
-            Dc = mx_block_mfma(wv[1], x0, x1, ex[0] & 0xffu);
+            sc_c = sa[0];
+            Dc = mx_block_mfma(wv[1], xa[0][0], xa[0][1], ex[0] & 0xffu);
             wv[1] = wload(ws, qn, 1);
+            xa[0][0] = *(const u32x4*)(xp + 2 * 32 * kSlot);
+            xa[0][1] = *(const u32x4*)(xp + 2 * 32 * kSlot + 16);
+            sa[0] = sl[2 * 32];
         }
 #pragma unroll
         for (int i = 0; i < kBlkPerPart; i++) {
             if (i + 1 < kBlkPerPart) {
-                const int j = i + 1;
-                const u32x4 x0 = *(const u32x4*)(xp + j * 32 * kSlot), x1 = *(const u32x4*)(xp + j * 32 * kSlot + 16);
-                sc_n = sl[j * 32];
-                Dn = mx_block_mfma(wv[1 + j], x0, x1, (ex[j >> 2] >> (8 * (j & 3))) & 0xffu);
+                const int j = i + 1, bj = j & 1;
+                sc_n = sa[bj];
+                Dn = mx_block_mfma(wv[1 + j], xa[bj][0], xa[bj][1], (ex[j >> 2] >> (8 * (j & 3))) & 0xffu);
                 wv[1 + j] = wload(ws, qn, 1 + j);
+                if (j + 2 < kBlkPerPart) {
+                    xa[bj][0] = *(const u32x4*)(xp + (j + 2) * 32 * kSlot);
+                    xa[bj][1] = *(const u32x4*)(xp + (j + 2) * 32 * kSlot + 16);
+                    sa[bj] = sl[(j + 2) * 32];
+                }
             }
+            // keep the order as written (the scheduler would sink the reads
+            // next to their MFMA)
+            __builtin_amdgcn_sched_barrier(0);
             if (TRACE) {
                 const int b = q * kBlkPerPart + i;
                 const uint32_t eb = (ex[i >> 2] >> (8 * (i & 3))) & 0xffu;
