@@ -111,7 +111,7 @@ __global__ __launch_bounds__(256) void k_prep_batch_kq(GroupedArgs a) {
 // one workgroup per (token tile, pair of 32-row tiles) (grouped_item); wave w
 // = row tile w / 2, gate (w even) or up (w odd).
 template <bool TRACE>
-__global__ __launch_bounds__(256) void k_gateup_kq_grouped(GroupedArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_gateup_kq_grouped(GroupedArgs a) {
     __shared__ int src[32];
     __shared__ uint8_t s_sm[4][32][16];          // per wave and row: sc[8], mn[8]
     __shared__ float s_dm[4][32][2];             // d, dmin
@@ -241,7 +241,7 @@ CPB_DEV uint32_t q6_minus32(uint32_t v) {
 // one workgroup per (token tile, group of 4 row tiles of 32 rows); wave w =
 // row tile w.
 template <int TYPE, bool TRACE>
-__global__ __launch_bounds__(256) void k_down_kq_grouped(GroupedArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_down_kq_grouped(GroupedArgs a) {
     constexpr int U = TYPE == 12 ? kQ4Units : kQ6Units;
     __shared__ int src[32];
     __shared__ uint8_t s_sm[4][32][16];          // Q4_K: sc[8], mn[8]; Q6_K: int8 scales[16]
