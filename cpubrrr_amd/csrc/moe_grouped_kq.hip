@@ -135,12 +135,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     float sumf[16];
 #pragma unroll
     for (int i = 0; i < 16; i++) sumf[i] = 0.0f;
+    // the next superblock's weight units are requested before this one's
+    // products (software pipelined; one superblock of lead)
+    u32x4 nu0, nwq[4];
+    {
+        nu0 = wrow[0];
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++) nwq[jj] = wrow[(1 + 2 * jj + hb) * 32];
+    }
     for (int sb = 0; sb < nsb; sb++) {
-        const u32x4* wp = wrow + (size_t)sb * kQ4Units * 32;
-        const u32x4 u0 = wp[0];
+        const u32x4 u0 = nu0;
         u32x4 wq[4];
 #pragma unroll
-        for (int jj = 0; jj < 4; jj++) wq[jj] = wp[(1 + 2 * jj + hb) * 32];
+        for (int jj = 0; jj < 4; jj++) wq[jj] = nwq[jj];
+        if (sb + 1 < nsb) {
+            const u32x4* wp = wrow + (size_t)(sb + 1) * kQ4Units * 32;
+            nu0 = wp[0];
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) nwq[jj] = wp[(1 + 2 * jj + hb) * 32];
+        }
         u32x4 xb[8];
 #pragma unroll
         for (int j = 0; j < 8; j++)
