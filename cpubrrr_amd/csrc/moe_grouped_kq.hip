@@ -277,17 +277,46 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     float sumf[16];
 #pragma unroll
     for (int i = 0; i < 16; i++) sumf[i] = 0.0f;
-    for (int sb = 0; sb < nsbf; sb++) {
+    // this lane's weight units of a superblock: Q4_K d/dmin/scales + 4 quant
+    // units; Q6_K 4 ql + 2 qh units, the int8 scales, the fp16 d.  The next
+    // superblock's are requested before the current products (one
+    // superblock of lead).
+    auto wload = [&](int sb, u32x4 (&wu)[7], uint32_t& du) {
         const u32x4* wp = wrow + (size_t)sb * U * RT;
+        if constexpr (TYPE == 12) {
+            wu[0] = wp[0];
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) wu[1 + jj] = wp[(1 + 2 * jj + hb) * RT];
+            du = 0;
+        } else {
+#pragma unroll
+            for (int h6 = 0; h6 < 2; h6++) {
+#pragma unroll
+                for (int pp = 0; pp < 2; pp++) wu[h6 * 2 + pp] = wp[(h6 * 4 + pp * 2 + hb) * RT];
+                wu[4 + h6] = wp[(8 + h6 * 2 + hb) * RT];
+            }
+            wu[6] = wp[12 * RT];
+            du = *(const uint32_t*)(wp + 13 * RT);
+        }
+    };
+    u32x4 nwu[7];
+    uint32_t ndu;
+    wload(0, nwu, ndu);
+    for (int sb = 0; sb < nsbf; sb++) {
+        u32x4 wu[7];
+#pragma unroll
+        for (int k = 0; k < 7; k++) wu[k] = nwu[k];
+        const uint32_t du = ndu;
+        if (sb + 1 < nsbf) wload(sb + 1, nwu, ndu);
         const float ys = pair >= 0 ? a.hsb[(size_t)pair * nsbf + sb] : 0.0f;
         int acc[16], mint[16];
 #pragma unroll
         for (int i = 0; i < 16; i++) acc[i] = mint[i] = 0;
         if constexpr (TYPE == 12) {
-            const u32x4 u0 = wp[0];
+            const u32x4 u0 = wu[0];
             u32x4 wq[4];
 #pragma unroll
-            for (int jj = 0; jj < 4; jj++) wq[jj] = wp[(1 + 2 * jj + hb) * RT];
+            for (int jj = 0; jj < 4; jj++) wq[jj] = wu[1 + jj];
             u32x4 xb[8];
 #pragma unroll
             for (int j = 0; j < 8; j++)
@@ -322,15 +351,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
             }
         } else {
             // ql[128] = units 0-7, qh[64] = units 8-11, int8 scales = unit 12, d = unit 13
-            u32x4 ql[4], qh[2];
-#pragma unroll
-            for (int h6 = 0; h6 < 2; h6++) {
-#pragma unroll
-                for (int pp = 0; pp < 2; pp++) ql[h6 * 2 + pp] = wp[(h6 * 4 + pp * 2 + hb) * RT];
-                qh[h6] = wp[(8 + h6 * 2 + hb) * RT];
-            }
-            const u32x4 scu = wp[12 * RT];
-            const uint32_t du = *(const uint32_t*)(wp + 13 * RT);
+            const u32x4 ql[4] = {wu[0], wu[1], wu[2], wu[3]}, qh[2] = {wu[4], wu[5]};
+            const u32x4 scu = wu[6];
             if (hb == 0) {
                 *(u32x4*)&s_sm[w][r][0] = scu;
                 s_dm[w][r][0] = half_bits(du & 0xffffu);
