@@ -95,43 +95,59 @@ __global__ __launch_bounds__(256) void k_prep_batch(GroupedArgs a) {
 // ---- 2. router logits + bounds, workgroup = (expert, kRouteTok tokens) ----
 // The decode route's computation (logit_phase1/2/final, 16 elements per
 // thread, element wave w = elements 1024w ..), so every token's logits are
-// those of per-token decode bit for bit.
+// those of per-token decode bit for bit.  The products are formed as
+// (W_j g_j) x_j with W_j g_j in fp64 once per workgroup: W_j g_j and x_j g_j
+// are exact in fp64 (24-bit significands), so both orders give the exact
+// triple product rounded once, logit_phase1's W_j (x_j g_j) bit for bit.
+// Threads past d load zeros (their products are 0) and zero their prefix
+// term once, where logit_phase2 selects per element.
 __global__ __launch_bounds__(256) void k_router_batch(GroupedArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     const int e = blockIdx.x, d = a.d, tid = threadIdx.x, nw = blockDim.x >> 6;
+    const int lane = tid & 63, ws = tid >> 6;
     double* dred = (double*)smem;              // [64]
     const int j0 = tid * kRouteC;
     const bool act = j0 < d;
-    const uint32_t off = (uint32_t)(act ? j0 : 0) * 4;
+    const uint32_t off = act ? (uint32_t)j0 * 4 : kOffNone;
     const __amdgpu_buffer_rsrc_t rW = buf_rsrc(a.router_w + (size_t)e * d, (uint32_t)d * 4);
     const bool use_g = a.norm_w && a.apply_norm;
     const __amdgpu_buffer_rsrc_t rg = buf_rsrc(a.norm_w, use_g ? (uint32_t)d * 4 : 0u);
-    float wf[16], gf[16];
+    double wg[16];
 #pragma unroll
     for (int k = 0; k < 4; k++) {
         const u32x4 w4 = __builtin_amdgcn_raw_buffer_load_b128(rW, off + 16 * k, 0, 0);
         const u32x4 g4 = __builtin_amdgcn_raw_buffer_load_b128(rg, off + 16 * k, 0, 0);
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
-            wf[4 * k + c] = act ? __uint_as_float(w4[c]) : 0.0f;
-            gf[4 * k + c] = use_g ? __uint_as_float(g4[c]) : 1.0f;
-        }
+        for (int c = 0; c < 4; c++)
+            wg[4 * k + c] = (double)__uint_as_float(w4[c]) * (use_g ? (double)__uint_as_float(g4[c]) : 1.0);
     }
     const double b = a.router_b ? (double)a.router_b[e] : 0.0;
     for (int tt = 0; tt < kRouteTok; tt++) {
         const int t = blockIdx.y * kRouteTok + tt;
         if (t >= a.n_tok) break;
         const __amdgpu_buffer_rsrc_t rx = buf_rsrc(a.x + (size_t)t * d, (uint32_t)d * 4);
-        float xf[16];
+        double P[16];
+        double loc = 0.0, absp = 0.0;
 #pragma unroll
         for (int k = 0; k < 4; k++) {
             const u32x4 x4 = __builtin_amdgcn_raw_buffer_load_b128(rx, off + 16 * k, 0, 0);
 #pragma unroll
-            for (int c = 0; c < 4; c++) xf[4 * k + c] = act ? __uint_as_float(x4[c]) : 0.0f;
+            for (int c = 0; c < 4; c++) {
+                const int i = 4 * k + c;
+                P[i] = wg[i] * (double)__uint_as_float(x4[c]);
+                loc += P[i];
+                absp += fabs(P[i]);
+            }
         }
-        LogitThread lt;
-        logit_phase1(wf, xf, gf, lt, dred, tid >> 6);
-        logit_phase2(lt, act, dred, tid >> 6);
+        // logit_phase1 / logit_phase2 (route_dev.h), in their order
+        const double incl = wave_scan_f64(loc);
+        if (lane == 63) dred[ws] = incl;
+        double run = incl - loc, sabs = 0.0;
+#pragma unroll
+        for (int i = 0; i < 16; i++) { run += P[i]; sabs += fabs(run); }
+        const double s1 = wave_total63_f64(act ? sabs : 0.0);
+        const double s2 = wave_total63_f64(absp);
+        if (lane == 63) { dred[16 + ws] = s1; dred[32 + ws] = s2; }
         __syncthreads();
         if (tid == 0) logit_final(dred, nw, d, b, a.inv[t], a.lstar + (size_t)t * a.ne + e, a.lbound + (size_t)t * a.ne + e);
         __syncthreads();
