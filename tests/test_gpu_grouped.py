@@ -36,6 +36,8 @@ def per_token(blk, X, apply_norm):
     # 1100 tokens x 128 experts: past the token x expert table's LDS size,
     # so the pairs are grouped by the ranking kernel (k_group), not k_group_dense
     (384, 64, 128, 4, 1100, 6, True, None),
+    # 1024 x 128: the table at its largest (128 KB), still k_group_dense
+    (384, 64, 128, 4, 1024, 7, True, None),
 ])
 def test_grouped_equals_per_token(gpu, d, dff, ne, k, n_tok, seed, norm, zipf):
     say(f"case grouped d={d} dff={dff} ne={ne} k={k} n_tok={n_tok} seed={seed} norm={norm} zipf={zipf}")
