@@ -361,6 +361,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
             const u32x4 z = {0, 0, 0, 0};
+            // the superblock's activations, all eight requests in flight at once
+            u32x4 xvs[8];
+#pragma unroll
+            for (int m = 0; m < 8; m++)
+                xvs[m] = __builtin_amdgcn_raw_buffer_load_b128(
+                    rh, pair >= 0 ? (uint32_t)((size_t)pair * a.dff + sb * 256 + 32 * m + 16 * hb) : kOffNone, 0, 0);
 #pragma unroll
             for (int m = 0; m < 8; m++) {
                 // elements 32 m .. 32 m + 31 (engine_qwen2.rs:171-190): 128-half h6, quarter p
@@ -370,8 +376,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
                 u32x4 A;
 #pragma unroll
                 for (int c = 0; c < 4; c++) A[c] = q6_minus32((lq[c] & 0x0F0F0F0Fu) | ((hq2[c] & 0x03030303u) << 4));
-                const u32x4 xv = __builtin_amdgcn_raw_buffer_load_b128(
-                    rh, pair >= 0 ? (uint32_t)((size_t)pair * a.dff + sb * 256 + 32 * m + 16 * hb) : kOffNone, 0, 0);
+                const u32x4 xv = xvs[m];
                 // group 2m in the first K half, 2m + 1 in the second
                 const v16i_k D0 = mfma_i8(A, hb == 0 ? xv : z);
                 const v16i_k D1 = mfma_i8(A, hb == 1 ? xv : z);
