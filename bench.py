@@ -663,7 +663,7 @@ def main() -> int:
     out = {
         "metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+        "vs_baseline": None, "dtype": "int8" if qwen else "fp8 x fp4 (exact int8 x E2M1)", "data": "synthetic",
         "config": {"workload": c["name"], "layers_per_step": c["per_step"], "d": d, "d_ff": dff,
                    "n_expert": ne, "top_k": k, "batch": 1,
                    "weights": "Q4_K gate/up + Q6_K down (GGUF types 12/14)" if qwen else "MXFP4 (GGUF type 39)"},
