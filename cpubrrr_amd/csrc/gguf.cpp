@@ -126,6 +126,7 @@ struct cpb_gguf {
     uint32_t version = 0;
     uint64_t alignment = 32, data_start = 0;
     std::unordered_map<std::string, Meta> meta;
+    std::vector<std::string> meta_order;     // keys in file order (a repeated key keeps its first place)
     std::vector<TensorRec> tensors;
     std::unordered_map<std::string, size_t> by_name;
 };
@@ -166,7 +167,10 @@ int cpb_gguf_open(const char* path, cpb_gguf_t** out) {
         const uint32_t t = r.get<uint32_t>();
         Meta mv;
         r.value((int)t, &mv);
-        if (r.ok) g->meta[key] = mv;
+        if (r.ok) {
+            if (!g->meta.count(key)) g->meta_order.push_back(key);
+            g->meta[key] = mv;
+        }
     }
     if (!r.ok) return bail(fail(CPB_EINVAL, "%s: truncated or corrupt metadata", path));
     auto al = g->meta.find("general.alignment");
@@ -276,15 +280,15 @@ int cpb_gguf_meta_str(const cpb_gguf_t* g, const char* key, const char** out) {
     return 0;
 }
 
-// setup_model.sh's g(*suffixes): the first key equal to "<arch>.<suffix>" or
-// ending in ".<suffix>", in the file's key order for the suffix match
+// setup_model.sh:54-58 g(*suffixes): the keys in file order, the first one
+// equal to "<arch>.<suffix>" or ending in ".<suffix>" (an exact key later in
+// the file does not win over an earlier suffix match)
 static const Meta* hp(const cpb_gguf_t* g, const std::string& arch, const char* suffix) {
-    auto it = g->meta.find(arch + "." + suffix);
-    if (it != g->meta.end()) return &it->second;
-    const std::string tail = std::string(".") + suffix;
-    for (auto& kv : g->meta)
-        if (kv.first.size() > tail.size() && kv.first.compare(kv.first.size() - tail.size(), tail.size(), tail) == 0)
-            return &kv.second;
+    const std::string exact = arch + "." + suffix, tail = std::string(".") + suffix;
+    for (const std::string& k : g->meta_order) {
+        const bool ends = k.size() >= tail.size() && k.compare(k.size() - tail.size(), tail.size(), tail) == 0;
+        if (k == exact || ends) return &g->meta.find(k)->second;
+    }
     return nullptr;
 }
 
@@ -354,9 +358,10 @@ int cpb_moe_load_gguf_layer(cpb_moe_t* h, const cpb_gguf_t* g, int layer) {
     if (layer < 0 || layer >= c.n_layer) return fail(CPB_EINVAL, "layer %d out of range", layer);
     const uint64_t d = (uint64_t)c.d, ff = (uint64_t)c.d_ff, ne = (uint64_t)c.n_expert;
     char name[256];
-    auto get = [&](const char* suffix, cpb_gguf_tensor* t, bool required) -> int {
+    auto get = [&](const char* suffix, cpb_gguf_tensor* t, bool required, bool* found = nullptr) -> int {
         snprintf(name, sizeof name, "blk.%d.%s", layer, suffix);
         auto it = g->by_name.find(name);
+        if (found) *found = it != g->by_name.end();
         if (it == g->by_name.end()) {
             t->data = nullptr;
             return required ? fail(CPB_EINVAL, "tensor %s not in the file", name) : 0;
@@ -379,15 +384,17 @@ int cpb_moe_load_gguf_layer(cpb_moe_t* h, const cpb_gguf_t* g, int layer) {
         return 0;
     };
     cpb_gguf_tensor tg, tu, td, tgb, tub, tdb, trw, trb, tn;
+    bool has_norm = false;
     int r;
     if ((r = get("ffn_gate_exps.weight", &tg, true)) || (r = get("ffn_up_exps.weight", &tu, true)) ||
         (r = get("ffn_down_exps.weight", &td, true)) || (r = get("ffn_gate_inp.weight", &trw, true)) ||
-        (r = get("ffn_norm.weight", &tn, false)))
+        (r = get("ffn_norm.weight", &tn, false, &has_norm)))
         return r;
     if ((r = shape(tg, 3, d, ff, ne)) || (r = shape(tu, 3, d, ff, ne)) || (r = shape(td, 3, ff, d, ne)) ||
         (r = shape(trw, 2, d, ne, 1)) || (r = f32(trw)))
         return r;
-    if (tn.data && ((r = shape(tn, 1, d, 1, 1)) || (r = f32(tn)))) return r;
+    // a norm weight that is present must be F32 of [d] (absent: no norm weight)
+    if (has_norm && ((r = shape(tn, 1, d, 1, 1)) || (r = f32(tn)))) return r;
     const float *gb = nullptr, *ub = nullptr, *db = nullptr, *rb = nullptr;
     if (c.has_bias) {
         if ((r = get("ffn_gate_exps.bias", &tgb, true)) || (r = get("ffn_up_exps.bias", &tub, true)) ||

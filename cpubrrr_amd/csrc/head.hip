@@ -74,8 +74,12 @@ struct HeadDev {
     int32_t* count;        // [1] arrivals of the refine workgroups (0 between launches)
 };
 
-// rows of worker slice w: [4 nq w / nt, 4 nq (w + 1) / nt) (head_worker's quads)
-CPB_DEV_HOST_INLINE int slice_r0(long nq, int nt, int w) { return (int)(4 * (nq * w / nt)); }
+// rows of worker slice w: quads [nq su(w) / tu, nq su(w + 1) / tu), the
+// reference's sl() (engine_gpt2.rs:636-642) with its unit weights (wunits,
+// total_units :29-38): 5 units for workers 0-11, 2 for workers 12 and above,
+// tu = su(nt)
+CPB_DEV_HOST_INLINE long head_units(int w) { return w < 12 ? 5L * w : 60L + 2L * (w - 12); }
+CPB_DEV_HOST_INLINE int slice_r0(long nq, int nt, int w) { return (int)(4 * (nq * head_units(w) / head_units(nt))); }
 
 // ---- cross-lane helpers on DPP + readlane ----
 template <int CTRL>

@@ -8,8 +8,9 @@
  * The head (engine_gpt2.rs:937-1002): rmsnorm + Q8 of the final hidden state
  * (rmsnorm_quant_par :730-738), a Q4 screen of every vocabulary row
  * (dot4_q4_i8 :314-342 over Q4Mat :237-272) in which each of NT workers keeps
- * the top CAND rows of its contiguous slice of row quads (sl(), NT = 12,
- * CAND = 8, :21-29), then the exact Q8 logits of those NT * CAND rows
+ * the top CAND rows of its contiguous slice of row quads (sl(), NT = 12 by
+ * default, up to 32, weighted 5 units for workers 0-11 and 2 above; CAND =
+ * 8, :21-38, :636-642), then the exact Q8 logits of those NT * CAND rows
  * (dot_q8_i8 :169-191 over Q8Mat :464-494) and greedy selection over them
  * (sample_cands with temperature 0, :128-134).
  */
@@ -172,6 +173,14 @@ void orc_q4_quant_rows(const uint16_t* w, int V, int d, uint8_t* nib, uint16_t* 
         orc_q4_quant_row(w + (size_t)r * d, d, nib + (size_t)r * (d / 2), sc + (size_t)r * (d / 32));
 }
 
+/* sl() (engine_gpt2.rs:636-642) over n items, with wunits / total_units
+ * (:29-38): workers 0..11 weigh 5 units, workers 12.. weigh EW = 2 (:21-22);
+ * worker wid's slice starts at n * su(wid) / tu (integer division). */
+static long head_units(int w) { return w < 12 ? 5L * w : 60L + 2L * (w - 12); }
+long orc_head_slice_start(long n, int nt, int wid) {
+    return (long)((unsigned long long)n * (unsigned long long)head_units(wid) / (unsigned long long)head_units(nt));
+}
+
 static void head_impl(const uint16_t* w, const uint8_t* pre_nib, const uint16_t* pre_sc, int V, int d,
                       const float* x, const float* norm_w, float eps, int nt, int cand, int32_t* cand_ids,
                       float* cand_screen, float* cand_logits, int8_t* xq_out, float* xsb_out, int32_t* chosen);
@@ -215,8 +224,8 @@ static void head_impl(const uint16_t* w, const uint8_t* pre_nib, const uint16_t*
             screen[r] = orc_q4_row_dot(nib, sc, xq, xsb, nb);
         }
     }
-    /* per worker: top-cand of its quads [nq*wid/nt, nq*(wid+1)/nt), insertion
-     * with strict comparisons (an equal later value goes behind) */
+    /* per worker: top-cand of its quads sl(wid, nq) (:944), insertion with
+     * strict comparisons (an equal later value goes behind) */
     int nc = nt * cand;
     int32_t* ids = (int32_t*)malloc(sizeof(int32_t) * nc);
     float* lv = (float*)malloc(sizeof(float) * nc);
@@ -224,7 +233,7 @@ static void head_impl(const uint16_t* w, const uint8_t* pre_nib, const uint16_t*
         float* l = lv + wid * cand;
         int32_t* li = ids + wid * cand;
         for (int k = 0; k < cand; k++) { l[k] = -FLT_MAX; li[k] = 0; }
-        long qa = (long)nq * wid / nt, qb = (long)nq * (wid + 1) / nt;
+        long qa = orc_head_slice_start(nq, nt, wid), qb = orc_head_slice_start(nq, nt, wid + 1);
         for (long q = qa; q < qb; q++)
             for (int i = 0; i < 4; i++) {
                 float val = screen[q * 4 + i];

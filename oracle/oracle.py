@@ -84,6 +84,8 @@ def lib() -> C.CDLL:
         L.orc_q4_row_dot.argtypes = [u8p, u16p, i8p, f32p, C.c_int]
         L.orc_q8_row_dot.restype = C.c_float
         L.orc_q8_row_dot.argtypes = [i8p, f32p, i8p, f32p, C.c_int]
+        L.orc_head_slice_start.argtypes = [C.c_long, C.c_int, C.c_int]
+        L.orc_head_slice_start.restype = C.c_long
         L.orc_head.argtypes = [u16p, C.c_int, C.c_int, f32p, f32p, C.c_float, C.c_int, C.c_int, i32p, f32p, f32p,
                                i8p, f32p, i32p]
         L.orc_q4_quant_rows.argtypes = [u16p, C.c_int, C.c_int, u8p, u16p]
@@ -305,6 +307,11 @@ def q4_quant_rows(w_bf16):
     nib = np.empty((V, d // 2), np.uint8); sc = np.empty((V, d // 32), np.uint16)
     lib().orc_q4_quant_rows(_p(w, u16p), V, d, _p(nib, u8p), _p(sc, u16p))
     return nib, sc
+
+
+def head_slice_start(n, nt, wid):
+    """First item of worker wid's slice of n items (sl(), engine_gpt2.rs:636-642)."""
+    return int(lib().orc_head_slice_start(n, nt, wid))
 
 
 def head(w_bf16, x, norm_w, eps, nt=12, cand=8, pre=None):

@@ -17,7 +17,7 @@ T_U8, T_I8, T_U16, T_I16, T_U32, T_I32, T_F32, T_BOOL, T_STR, T_ARR, T_U64, T_I6
 _FMT = {T_U8: "<B", T_I8: "<b", T_U16: "<H", T_I16: "<h", T_U32: "<I", T_I32: "<i", T_F32: "<f", T_BOOL: "<?",
         T_U64: "<Q", T_I64: "<q", T_F64: "<d"}
 # bytes per block, elements per block
-BLOCK = {0: (4, 1), 1: (2, 1), 8: (34, 32), 12: (144, 256), 14: (210, 256), 30: (2, 1), 39: (17, 32)}
+BLOCK = {0: (4, 1), 1: (2, 1), 2: (18, 32), 8: (34, 32), 12: (144, 256), 14: (210, 256), 30: (2, 1), 39: (17, 32)}
 
 
 def _s(b: bytearray, text: str) -> None:

@@ -60,6 +60,22 @@ def test_metadata_and_hparams(tmp_path):
         assert (cfg.d, cfg.d_ff, cfg.n_expert, cfg.top_k, cfg.n_layer, cfg.has_bias) == (64, 96, 4, 2, 2, True)
 
 
+def test_hparam_suffix_match_in_file_order(tmp_path):
+    # setup_model.sh:54-58 g(): the first key in file order that equals
+    # "<arch>.<suffix>" or ends in ".<suffix>" -- an earlier key of another
+    # prefix wins over the exact key written after it
+    meta = [("general.architecture", W.T_STR, "gpt-oss"),
+            ("foo.block_count", W.T_U32, 7),
+            ("gpt-oss.block_count", W.T_U32, 2),
+            ("gpt-oss.expert_count", W.T_U32, 4),
+            ("bar.expert_count", W.T_U32, 9)]
+    p = tmp_path / "order.gguf"
+    W.write_gguf(p, meta, [("a", 0, [4], bytes(16))])
+    with GgufFile(p) as g:
+        hp = g.hparams()
+        assert hp["n_layer"] == 7 and hp["n_expert"] == 4
+
+
 def test_qwen_hparams_and_types(tmp_path):
     d, dff, ne, k = 512, 256, 8, 2
     layers = [synth.qwen_layer(d, dff, ne, k, seed=4, layer=0, down_type=14),

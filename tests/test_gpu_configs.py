@@ -2,9 +2,11 @@
 
 - config 2 shape: d = 2880, 128 experts, top-4, Zipf(1.1) router bias, with
   the norm (two layers of the 36-layer stack), traced against the oracle;
-- config 1: every layer of the 24-layer gpt-oss-20b stack traced against the
-  oracle on the GPU's own input (teacher forced), and the device stack (one
-  captured graph, as the bench runs it) bit-identical to that chain;
+- configs 1, 2 and 3: every layer of the 24-layer gpt-oss-20b, the 36-layer
+  gpt-oss-120b (128 experts) and the 48-layer Qwen3-30B-A3B stacks traced
+  against the oracle on the GPU's own input (teacher forced), and each
+  device stack (one captured graph, as the bench runs it) bit-identical to
+  that chain;
 - config 4: a 512-token Zipf-skewed prefill batch through the grouped path,
   bit-identical to per-token decode on every token, int32 block sums
   bit-identical on a sample of tokens, outputs against the oracle on a few;
@@ -32,6 +34,30 @@ def test_config2_120b_layers(gpu):
         run_case(2880, 2880, 128, 4, seed=0, layer=layer, apply_norm=True, zipf=1.1)
 
 
+def _full_stack(cfg, nl, make_layer, check, x0, teacher_every=6):
+    """Every layer traced against the oracle on the GPU's own input (teacher
+    forced), then the nl-layer device stack (one captured graph, as the bench
+    runs it) against that chain of single-layer calls, bit for bit."""
+    import torch
+    with MoeBlock(cfg) as blk:
+        x = x0.copy()
+        worst = 0.0
+        for l in range(nl):
+            L = make_layer(l)
+            blk.load_layer(l, L)
+            xo, t = blk.forward(l, x, apply_norm=True, trace=True)
+            worst = max(worst, check(L, x, xo, t, l % teacher_every == 0))
+            x = xo
+            del L
+        say(f"  per-layer worst err/rms = {worst:.3e}; running the device stack")
+        xd = torch.from_numpy(x0.copy()).to("cuda:0")
+        torch.cuda.synchronize()
+        blk.forward_device(0, nl, xd.data_ptr(), 1, True)
+        blk.sync()
+        y = xd.cpu().numpy()
+    assert np.array_equal(y.view(np.uint32), x.view(np.uint32)), "device stack != chain of single-layer calls"
+
+
 def test_config1_full_stack_vs_oracle(gpu):
     # The 24-layer chain cannot be compared end to end with a tolerance: Q8
     # quantisation is discontinuous, so a 1e-7 relative change of one
@@ -43,28 +69,35 @@ def test_config1_full_stack_vs_oracle(gpu):
     # sums bit-exact, output within 1e-3 * RMS), and the 24-layer device
     # stack (one captured graph, as the bench runs it) must equal that chain
     # of single-layer calls bit for bit.
-    import torch
     d, ne, k, nl = 2880, 32, 4, 24
     say("case config 1: 24-layer 20b stack, each layer vs the oracle")
     cfg = MoeConfig.gptoss(d=d, n_expert=ne, top_k=k, d_ff=d, n_layer=nl)
-    x0 = synth.token(d, 0, 0)
-    with MoeBlock(cfg) as blk:
-        x = x0.copy()
-        worst = 0.0
-        for l in range(nl):
-            L = synth.gptoss_layer(d, d, ne, k, seed=0, layer=l, zipf=1.1)
-            blk.load_layer(l, L)
-            xo, t = blk.forward(l, x, apply_norm=True, trace=True)
-            worst = max(worst, check_layer(L, x, True, xo, t, teacher_forced_down=(l % 6 == 0)))
-            x = xo
-            del L
-        say(f"  per-layer worst err/rms = {worst:.3e}; running the device stack")
-        xd = torch.from_numpy(x0.copy()).to("cuda:0")
-        torch.cuda.synchronize()
-        blk.forward_device(0, nl, xd.data_ptr(), 1, True)
-        blk.sync()
-        y = xd.cpu().numpy()
-    assert np.array_equal(y.view(np.uint32), x.view(np.uint32)), "device stack != chain of single-layer calls"
+    _full_stack(cfg, nl, lambda l: synth.gptoss_layer(d, d, ne, k, seed=0, layer=l, zipf=1.1),
+                lambda L, x, xo, t, tf: check_layer(L, x, True, xo, t, teacher_forced_down=tf),
+                synth.token(d, 0, 0))
+
+
+def test_config2_full_stack_vs_oracle(gpu):
+    # the gpt-oss-120b stack the bench runs: 36 layers of 128 experts
+    # (61 GB resident), Zipf(1.1) router bias, checked as config 1
+    d, ne, k, nl = 2880, 128, 4, 36
+    say("case config 2: 36-layer 120b stack, each layer vs the oracle")
+    cfg = MoeConfig.gptoss(d=d, n_expert=ne, top_k=k, d_ff=d, n_layer=nl)
+    _full_stack(cfg, nl, lambda l: synth.gptoss_layer(d, d, ne, k, seed=0, layer=l, zipf=1.1),
+                lambda L, x, xo, t, tf: check_layer(L, x, True, xo, t, teacher_forced_down=tf),
+                synth.token(d, 0, 0), teacher_every=9)
+
+
+def test_config3_full_stack_vs_oracle(gpu):
+    # the Qwen3-30B-A3B stack the bench runs: 48 layers, Q4_K gate/up, Q6_K
+    # down, top-8 of 128; every layer's ids, Q8_K bytes, superblock sums and
+    # gate/up rows bit-exact, output within 1e-3 * RMS (check_qwen)
+    d, dff, ne, k, nl = 2048, 768, 128, 8, 48
+    say("case config 3: 48-layer Qwen3 stack, each layer vs the oracle")
+    cfg = MoeConfig.qwen3(d=d, n_expert=ne, top_k=k, d_ff=dff, n_layer=nl)
+
+    _full_stack(cfg, nl, lambda l: synth.qwen_layer(d, dff, ne, k, seed=0, layer=l),
+                lambda L, x, xo, t, tf: check_qwen(L, x, True, xo, t), synth.token(d, 0, 0))
 
 
 def test_config4_512_tokens_grouped(gpu):

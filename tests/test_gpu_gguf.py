@@ -73,6 +73,15 @@ def test_gguf_type_and_shape_checks(gpu, tmp_path):
     with GgufFile(bad) as g, MoeBlock(cfg) as blk:
         with pytest.raises(L.CpbError, match="F32"):
             blk.load_gguf_layer(g, 0)
+    # a norm weight that is present in a type the reader does not handle
+    # (Q4_0), or present as F16: rejected, not read as "no norm weight"
+    t_ok = list(t)
+    t_ok[3] = ("blk.0.ffn_gate_inp.weight", 0, [d, ne], L0["router_w"].tobytes())
+    for typ, raw in ((2, bytes(d // 32 * 18)), (1, bytes(2 * d))):
+        W.write_gguf(bad, meta, t_ok + [("blk.0.ffn_norm.weight", typ, [d], raw)])
+        with GgufFile(bad) as g, MoeBlock(cfg) as blk:
+            with pytest.raises(L.CpbError, match="F32"):
+                blk.load_gguf_layer(g, 0)
     # down declared with swapped dims
     t2 = list(t)
     t2[3] = ("blk.0.ffn_gate_inp.weight", 0, [d, ne], L0["router_w"].tobytes())

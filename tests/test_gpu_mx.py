@@ -45,9 +45,28 @@ def check_layer(L, x, apply_norm, xo, t, *, teacher_forced_down=True):
     ffn_o = (xo_o - x).astype(np.float64)
     ffn_g = (xo - x).astype(np.float64)
     rms = np.sqrt((ffn_o ** 2).mean())
+    if np.count_nonzero(dq):
+        # expf (unpinned between the GPU and the host libm) put some h on the
+        # other side of a Q8 rounding boundary: one quantum of h moves every
+        # down row by up to ~1e-3 of the output RMS.  The kernels are then
+        # checked on the GPU's own hq: the oracle's down rows and combine
+        # (engine_gpt2.rs:908-922) recomputed from it
+        ffn_o = down_from_gpu_hq(L, x, t, to["wts"]).astype(np.float64) - x
     err = np.max(np.abs(ffn_g - ffn_o))
-    assert err <= 1e-3 * rms, (err, rms)
+    assert err <= 1e-3 * rms, (err, rms, np.count_nonzero(dq))
     return err / rms
+
+
+def down_from_gpu_hq(L, x, t, wts):
+    """x + sum over slots (ascending) of wts * (down row . the GPU's hq + bias)
+    in the reference's fp32 order, with the oracle's row dots."""
+    d, k = L["d"], L["k"]
+    s = np.array(x, np.float32, copy=True)
+    for ei in range(k):
+        e = int(t["ids"][ei])
+        v = np.array([O.mx_row_dot(L["down"][e * d + r], t["hq"][ei], t["hsb"][ei])[0] for r in range(d)], np.float32)
+        s = (s + np.float32(wts[ei]) * (v + L["down_b"][e])).astype(np.float32)
+    return s
 
 
 def run_case(d, dff, ne, k, seed=0, layer=0, apply_norm=False, zipf=None, n_tok=1):

@@ -98,6 +98,61 @@ def test_q4_scale_search_and_codes():
     assert np.all(nib[16:32] == 0x88) and sc[1] == 0
 
 
+def test_q4_scale_search_known_answers():
+    # Pins of engine_gpt2.rs:279-300 that do not restate its loop: blocks
+    # whose optimum the arithmetic fixes.
+    # (a) values k * d0 with k in [-8, 7] and one k = -8: the Q4_0 end
+    #     (nmax = 8, t = 16) reproduces every value exactly (error 0); no
+    #     earlier candidate rounds to d0 in bf16, so it is the unique best
+    k = rng.integers(-7, 8, 32)
+    k[5] = -8
+    vals = (k * np.float32(-0.25)).astype(np.float32)           # vmax = +2.0
+    db, idq = O.q4_scale_search(vals)
+    assert db == 0xBE80 and idq == np.float32(-4.0)             # bf16(-0.25)
+    nib, sc = O.q4_quant_row(bf16_np(vals))
+    codes = np.concatenate([nib[:16] & 15, nib[:16] >> 4])
+    assert sc[0] == 0xBE80 and np.array_equal(codes.astype(int) - 8, k)
+    # (b) symmetric end: |k| <= 7 and vmax = 7 * d0 < 0: nmax = 7 (t = 0)
+    #     gives d = +0.25 and error 0; the first exact candidate wins
+    k = rng.integers(-7, 8, 32)
+    k[9] = 7
+    vals = (k * np.float32(-0.25)).astype(np.float32)           # vmax = -1.75
+    db, idq = O.q4_scale_search(vals)
+    assert db == 0x3E80 and idq == np.float32(4.0)              # bf16(+0.25)
+    # (c) all-equal block 3.0: only nmax = 8 reconstructs it exactly
+    #     (code 0, (0 - 8) * -0.375 = 3); every other candidate's bf16 scale
+    #     leaves an error
+    db, idq = O.q4_scale_search(np.full(32, 3.0, np.float32))
+    assert db == 0xBEC0                                          # bf16(-0.375)
+    # (d) the zero block: scale 0, every code 8
+    db, idq = O.q4_scale_search(np.zeros(32, np.float32))
+    assert db == 0 and idq == 0
+    nib, sc = O.q4_quant_row(np.zeros(32, np.uint16))
+    assert sc[0] == 0 and np.all(nib == 0x88)
+
+
+def test_q4_scale_search_error_minimal_f64():
+    # The chosen scale's reconstruction error, recomputed in float64, is the
+    # least among the 17 candidates vmax / -(7 + t/16) rounded to bf16
+    # (up to the float32 rounding of the reference's own error sums).
+    for trial in range(200):
+        vals = from_bf16(bf16_np(rng.standard_normal(32).astype(np.float32) * f32(10 ** rng.uniform(-3, 1))))
+        vmax = vals[np.argmax(np.abs(vals))]
+        errs = {}
+        for t in range(17):
+            d = float(from_bf16(bf16_np(np.float32(vmax) / -np.float32(7 + t / 16))))
+            if d == 0.0:
+                continue
+            idq = float(np.float32(1.0) / np.float32(d))
+            c = np.clip(np.floor(vals.astype(np.float64) * idq + 8.5), 0, 15)
+            errs[t] = float(((vals.astype(np.float64) - (c - 8) * d) ** 2).sum())
+        db, _ = O.q4_scale_search(vals)
+        d_chosen = float(from_bf16(np.uint16(db)))
+        e_chosen = min(e for t, e in errs.items()
+                       if float(from_bf16(bf16_np(np.float32(vmax) / -np.float32(7 + t / 16)))) == d_chosen)
+        assert e_chosen <= min(errs.values()) * (1 + 1e-5) + 1e-30, trial
+
+
 def test_q8_quant_row_closed_form():
     w = bf16_np(rng.standard_normal(512).astype(np.float32) * 0.05)
     q, s = O.q8_quant_row(w)
@@ -172,7 +227,7 @@ def test_head_candidates_and_greedy():
     nq = V // 4
     ids = []
     for wid in range(nt):
-        r0, r1 = 4 * (nq * wid // nt), 4 * (nq * (wid + 1) // nt)
+        r0, r1 = 4 * O.head_slice_start(nq, nt, wid), 4 * O.head_slice_start(nq, nt, wid + 1)
         order = np.argsort(-screen[r0:r1].astype(np.float64), kind="stable")[:cand]
         ids += list(r0 + order)
     assert np.array_equal(out["cand_ids"], np.array(ids, np.int32))
@@ -180,6 +235,39 @@ def test_head_candidates_and_greedy():
     logits = np.array([O.q8_row_dot(*O.q8_quant_row(w[r]), xq, xsb) for r in ids], np.float32)
     assert np.array_equal(out["cand_logits"], logits)
     assert out["chosen"] == ids[int(np.argmax(logits))]       # first maximum
+
+
+def test_head_worker_slices_known_answers():
+    # sl() weights workers 0-11 at 5 units and workers 12+ at 2
+    # (engine_gpt2.rs:21-38, 636-642): with n equal to the total units the
+    # slice starts are the unit offsets themselves
+    assert [O.head_slice_start(68, 16, w) for w in range(17)] == \
+        [0, 5, 10, 15, 20, 25, 30, 35, 40, 45, 50, 55, 60, 62, 64, 66, 68]
+    assert [O.head_slice_start(100, 32, w) for w in range(33)] == \
+        list(range(0, 60, 5)) + list(range(60, 101, 2))
+    # gpt-oss vocabulary quads (201088 / 4 = 50272) over 16 workers (68
+    # units): 50272 * 60 / 68 = 44357.6, * 62 / 68 = 45836.2, * 66 / 68 = 48793.4
+    assert [O.head_slice_start(50272, 16, w) for w in (12, 13, 15, 16)] == [44357, 45836, 48793, 50272]
+    # up to 12 workers every slice has the same weight: n * w / nt
+    assert [O.head_slice_start(50272, 12, w) for w in (1, 5, 11)] == [50272 // 12, 50272 * 5 // 12, 50272 * 11 // 12]
+
+
+def test_head_candidates_more_than_12_workers():
+    # E-core workers (12+) get the narrower slices
+    V, d, nt, cand = 1600, 128, 20, 4
+    r = np.random.default_rng(5)
+    w = bf16_np(r.standard_normal((V, d)).astype(np.float32) * 0.02)
+    x = r.standard_normal(d).astype(np.float32)
+    out = O.head(w, x, np.ones(d, np.float32), 1e-5, nt, cand)
+    xq, xsb = out["xq"], out["xsb"]
+    screen = np.array([O.q4_row_dot(*O.q4_quant_row(w[i]), xq, xsb) for i in range(V)], np.float32)
+    units = [5 * k if k < 12 else 60 + 2 * (k - 12) for k in range(nt + 1)]
+    ids = []
+    for wid in range(nt):
+        r0, r1 = 4 * (400 * units[wid] // units[nt]), 4 * (400 * units[wid + 1] // units[nt])
+        order = np.argsort(-screen[r0:r1].astype(np.float64), kind="stable")[:cand]
+        ids += list(r0 + order)
+    assert np.array_equal(out["cand_ids"], np.array(ids, np.int32))
 
 
 def test_head_prequantised_rows_agree():
