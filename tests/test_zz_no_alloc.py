@@ -52,6 +52,52 @@ def test_noalloc_matches_forward_device_qwen(gpu):
             assert np.array_equal(want.view(np.uint32), got.view(np.uint32)), n_tok
 
 
+def test_noalloc_under_graph_capture(gpu):
+    # the entry point's purpose: a caller capturing its stream into a graph.
+    # Captured into a torch CUDA graph on the handle's stream and replayed
+    # three times, with eager work and synchronisations between the replays;
+    # every replay equals the eager call bit for bit, and the calls change
+    # the device's free memory by nothing
+    import torch
+    say("case noalloc captured in a graph, 3 replays")
+    d, ne, k, nl = 960, 16, 4, 2
+    layers = [synth.gptoss_layer(d, d, ne, k, seed=33, layer=l, zipf=1.1) for l in range(nl)]
+    X = np.stack([synth.token(d, 33, i) for i in range(3)])
+    with MoeBlock(MoeConfig.gptoss(d=d, n_expert=ne, top_k=k, d_ff=d, n_layer=nl)) as blk:
+        for l in range(nl):
+            blk.load_layer(l, layers[l])
+        s = torch.cuda.Stream()
+        blk.set_stream(s.cuda_stream)
+        want = []
+        for i in range(3):
+            a = torch.from_numpy(X[i].copy()).to("cuda:0")
+            torch.cuda.synchronize()
+            blk.forward_device_noalloc(0, nl, a.data_ptr(), 1, True)
+            blk.sync()
+            want.append(a.cpu().numpy())
+        free0 = torch.cuda.mem_get_info()[0]
+        for i in range(3):
+            a = torch.from_numpy(X[i].copy()).to("cuda:0")
+            torch.cuda.synchronize()
+            blk.forward_device_noalloc(0, nl, a.data_ptr(), 1, True)
+            blk.sync()
+        assert torch.cuda.mem_get_info()[0] == free0
+        xs = torch.from_numpy(X[0].copy()).to("cuda:0")
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            blk.forward_device_noalloc(0, nl, xs.data_ptr(), 1, True)
+        for i in (1, 0, 2):
+            xs.copy_(torch.from_numpy(X[i]).to("cuda:0"))
+            junk = torch.ones(4096, device="cuda:0") * float(i)      # eager work between replays
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            assert np.array_equal(xs.cpu().numpy().view(np.uint32), want[i].view(np.uint32)), i
+            del junk
+        blk.set_stream(None)
+
+
 def test_noalloc_rejects_shapes_beyond_scratch(gpu):
     say("case noalloc size limit")
     cfg = MoeConfig.qwen3(d=8192, n_expert=8, top_k=8, d_ff=4096)
