@@ -35,11 +35,15 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 # HBM bytes per dispatch of the roofline kernel, from rocprofv3 FETCH_SIZE /
-# WRITE_SIZE runs scaled by a 1 GiB copy (profiles/hbm_traffic_config1_phased.md,
-# profiles/hbm_traffic_config3_qwen.md, profiles/hbm_traffic_config6_head.md);
-# None where not yet measured.
+# WRITE_SIZE runs scaled by a 1 GiB copy; None where not yet measured.  The
+# bench cannot read hardware counters itself (they need a profiler run of
+# their own), so each line names the profile its figure comes from.
 MEASURED_TRAFFIC = {"k_gateup_mx": 35_815_144, "k_gateup_kq": 14_404_042,
                     "k_gateup_grouped": 484_748_900, "head": 327_526_064}
+TRAFFIC_SOURCE = {"k_gateup_mx": "profiles/hbm_traffic_config1_phased.md",
+                  "k_gateup_kq": "profiles/hbm_traffic_config3_qwen.md",
+                  "k_gateup_grouped": "profiles/mfma_hbm_config4_grouped.md",
+                  "head": "profiles/hbm_traffic_config6_head.md"}
 
 METRIC = "expert-weight GB/s (% HBM peak) + MoE-layer tok/s, gpt-oss-20b shape, 1 GPU"
 HBM_PEAK_GBS = 8000.0
@@ -172,15 +176,34 @@ def log(msg):
 
 
 def _host_info() -> dict:
-    """nproc, the cores this process may run on, and the CPU model."""
-    model = ""
+    """nproc, the cores this process may run on, and the CPU model: the
+    model name as the host reports it (a virtual machine may shorten it),
+    with the vendor, family / model / stepping numbers and lscpu's name."""
+    info = {}
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                model = line.split(":", 1)[1].strip()
+            k, _, v = line.partition(":")
+            k = k.strip()
+            if k in ("model name", "vendor_id", "cpu family", "model", "stepping") and k not in info:
+                info[k] = v.strip()
+            if line.strip() == "" and info:
                 break
     except OSError:
         pass
+    model = info.get("model name", "")
+    try:
+        import subprocess
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                ln = line.split(":", 1)[1].strip()
+                if ln and ln != model:
+                    model = f"{model} (lscpu: {ln})" if model else ln
+    except Exception:
+        pass
+    ids = ", ".join(f"{k} {info[k]}" for k in ("vendor_id", "cpu family", "model", "stepping") if k in info)
+    if ids:
+        model = f"{model} [{ids}]"
     try:
         usable = len(os.sched_getaffinity(0))
     except AttributeError:
@@ -220,7 +243,22 @@ def cpu_baseline(host_layers, c, budget_s: float) -> dict:
     n1, dt1 = run(1, budget_s / 2)
     per_layer, per_layer1 = dt / n, dt1 / n1
     tok_s = 1.0 / (per_layer * c["per_step"])
+    f64 = None
+    if c["family"] != "qwen":
+        # the second mode: scripts/ffn_reference.py's float64 dequant algorithm
+        # (scale 2^(e-128)) on the same layers and threads
+        O.set_threads(threads)
+        x = synth.token(c["d"], 0, 12345)
+        nf, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < budget_s / 2 or nf == 0:
+            x = O.gptoss_moe_f64(host_layers[nf % len(host_layers)], x, c["norm"])
+            nf += 1
+        pf = (time.perf_counter() - t0) / nf
+        f64 = {"value": round(1.0 / (pf * c["per_step"]), 3), "unit": "tok/s", "cores": threads,
+               "ms_per_layer": round(pf * 1e3, 3), "layers": nf,
+               "algorithm": "scripts/ffn_reference.py float64 dequant (2^(e-128)), weights decoded per row"}
     return {"value": round(tok_s, 3), "unit": "tok/s", "cores": threads,
+            "f64_dequant": f64,
             "kind": "port", "sample": f"{n} MoE layers ({len(host_layers)} distinct) of the same workload in "
                                        f"{dt:.1f} s on {threads} threads; {per_layer * 1e3:.2f} ms/layer, "
                                        f"{lb / per_layer / 1e9:.2f} GB/s algorithmic",
@@ -277,6 +315,7 @@ def bench_head(args, c) -> int:
            "roofline": {"bound": "hbm", "kernel": "whole head (norm, screen, top-k, refine)", "achieved": round(gbs, 1),
                         "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
                         "traffic": MEASURED_TRAFFIC["head"] if (d, V) == (2880, 201088) else None,
+                     "traffic_source": TRAFFIC_SOURCE["head"],
                         "bytes_per_launch": screen_bytes + refine_bytes}}
     hd.close()
     if not args.no_cpu:
@@ -674,6 +713,7 @@ def main() -> int:
         "roofline": {"bound": "hbm", "kernel": "k_gateup_kq" if qwen else "k_gateup_mx", "achieved": round(gu_ach, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gu_ach / HBM_PEAK_GBS, 4),
                      "traffic": MEASURED_TRAFFIC["k_gateup_kq" if qwen else "k_gateup_mx"],
+                     "traffic_source": TRAFFIC_SOURCE["k_gateup_kq" if qwen else "k_gateup_mx"],
                      "bytes_per_launch": lb["gate_up"]},
     }
     if not args.no_cpu:

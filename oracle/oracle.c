@@ -451,3 +451,86 @@ void orc_qwen_moe(const orc_qwen_layer* L, float* x, int apply_norm, orc_trace* 
     }
     free(xn); free(xq); free(hbuf); free(hq); free(hs); free(hm);
 }
+
+
+/* ---- f64 dequant reference of one gpt-oss MoE layer ----
+ * scripts/ffn_reference.py:23-62 (the spec its header recovers from
+ * llama.cpp: router logits = W x + b, top-4, softmax over the four;
+ * g = gate_e x + gate_b, u = up_e x + up_b, SwiGLU-OAI, out += w_e (down_e h
+ * + down_b)) in float64 with every weight dequantised, KV[c] * 2^(e - 128)
+ * (the script's line 28 writes 2^(e - 127) with the doubled table KV, i.e.
+ * twice the MXFP4 value; the reference engines use 2^(e - 128),
+ * engine_gpt2.rs:437).  apply_norm: an f64 rmsnorm (x / sqrt(mean x^2 +
+ * eps) * w) first, as the stacks feed it.  Ties in the top-k keep the lower
+ * index (a stable descending order).  Weights are decoded row by row on the
+ * fly (the script dequantised whole matrices at load). */
+static double mx_row_f64(const uint8_t* row, const double* v, int cols) {
+    double acc = 0.0;
+    for (int b = 0; b < cols / 32; b++) {
+        const uint8_t* blk = row + (size_t)b * 17;
+        const double sc = ldexp(1.0, (int)blk[0] - 128);
+        double s = 0.0;
+        for (int j = 0; j < 16; j++) {
+            s += (double)KVI[blk[1 + j] & 0xF] * v[b * 32 + j];
+            s += (double)KVI[blk[1 + j] >> 4] * v[b * 32 + 16 + j];
+        }
+        acc += s * sc;
+    }
+    return acc;
+}
+
+void orc_gptoss_moe_f64(const orc_gptoss_layer* L, float* x, int apply_norm) {
+    const int d = L->d, dff = L->dff, ne = L->ne, k = L->k;
+    const size_t rowb = (size_t)(d / 32) * 17, rowbf = (size_t)(dff / 32) * 17;
+    int nth = orc_get_threads();
+    (void)nth;
+    double* xn = (double*)malloc(sizeof(double) * d);
+    double* h = (double*)malloc(sizeof(double) * dff);
+    double* out = (double*)calloc((size_t)d, sizeof(double));
+    double logit[512];
+    if (apply_norm) {
+        double ss = 0.0;
+        for (int i = 0; i < d; i++) ss += (double)x[i] * (double)x[i];
+        const double inv = 1.0 / sqrt(ss / d + (double)L->eps);
+        for (int i = 0; i < d; i++) xn[i] = (double)x[i] * inv * (L->norm_w ? (double)L->norm_w[i] : 1.0);
+    } else {
+        for (int i = 0; i < d; i++) xn[i] = x[i];
+    }
+    for (int e = 0; e < ne; e++) {
+        double a = L->router_b ? (double)L->router_b[e] : 0.0;
+        for (int j = 0; j < d; j++) a += (double)L->router_w[(size_t)e * d + j] * xn[j];
+        logit[e] = a;
+    }
+    int top[8];
+    for (int i = 0; i < k; i++) {
+        int best = -1;
+        for (int e = 0; e < ne; e++) {
+            int used = 0;
+            for (int t = 0; t < i; t++) used |= top[t] == e;
+            if (!used && (best < 0 || logit[e] > logit[best])) best = e;
+        }
+        top[i] = best;
+    }
+    double w[8], wmax = logit[top[0]], wsum = 0.0;
+    for (int i = 0; i < k; i++) { w[i] = exp(logit[top[i]] - wmax); wsum += w[i]; }
+    for (int i = 0; i < k; i++) w[i] /= wsum;
+    const double alpha = L->alpha, lim = L->limit;
+    for (int i = 0; i < k; i++) {
+        const int e = top[i];
+        #pragma omp parallel for schedule(static) num_threads(nth)
+        for (int r = 0; r < dff; r++) {
+            const size_t row = (size_t)e * dff + r;
+            const double g = mx_row_f64(L->gate + row * rowb, xn, d) + (L->gate_b ? (double)L->gate_b[row] : 0.0);
+            const double u = mx_row_f64(L->up + row * rowb, xn, d) + (L->up_b ? (double)L->up_b[row] : 0.0);
+            const double xg = fmin(g, lim), yu = fmin(fmax(u, -lim), lim);
+            h[r] = (xg / (1.0 + exp(-alpha * xg))) * (yu + 1.0);
+        }
+        #pragma omp parallel for schedule(static) num_threads(nth)
+        for (int r = 0; r < d; r++) {
+            const size_t row = (size_t)e * d + r;
+            out[r] += w[i] * (mx_row_f64(L->down + row * rowbf, h, dff) + (L->down_b ? (double)L->down_b[row] : 0.0));
+        }
+    }
+    for (int i = 0; i < d; i++) x[i] = (float)((double)x[i] + out[i]);
+    free(xn); free(h); free(out);
+}

@@ -88,6 +88,9 @@ typedef struct orc_gptoss_layer {
 /* engine_gpt2.rs:845-923: x <- x + sum_ei w_ei * (down_e(hq_ei) + down_b_e).
  * apply_norm=0 feeds x itself as xn (config 0 of the bench: input already normed). */
 void orc_gptoss_moe(const orc_gptoss_layer* L, float* x, int apply_norm, orc_trace* tr);
+/* scripts/ffn_reference.py's float64 dequant algorithm (scale 2^(e-128)):
+ * the CPU baseline's second mode.  x <- x + the layer's MoE output. */
+void orc_gptoss_moe_f64(const orc_gptoss_layer* L, float* x, int apply_norm);
 
 typedef struct orc_qwen_layer {
     int d, dff, ne, k, nt;

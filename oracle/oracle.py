@@ -84,6 +84,8 @@ def lib() -> C.CDLL:
         L.orc_q4_row_dot.argtypes = [u8p, u16p, i8p, f32p, C.c_int]
         L.orc_q8_row_dot.restype = C.c_float
         L.orc_q8_row_dot.argtypes = [i8p, f32p, i8p, f32p, C.c_int]
+        L.orc_gptoss_moe_f64.argtypes = [C.c_void_p, f32p, C.c_int]
+        L.orc_gptoss_moe_f64.restype = None
         L.orc_head_slice_start.argtypes = [C.c_long, C.c_int, C.c_int]
         L.orc_head_slice_start.restype = C.c_long
         L.orc_head.argtypes = [u16p, C.c_int, C.c_int, f32p, f32p, C.c_float, C.c_int, C.c_int, i32p, f32p, f32p,
@@ -242,6 +244,21 @@ def gptoss_moe(layer: dict, x: np.ndarray, apply_norm: bool, want_sums: bool = F
     tr = _mk_trace(t)
     lib().orc_gptoss_moe(C.byref(L), _p(xo, f32p), int(bool(apply_norm)), C.byref(tr))
     return xo, t
+
+
+def gptoss_moe_f64(layer: dict, x: np.ndarray, apply_norm: bool):
+    """scripts/ffn_reference.py's float64 dequant algorithm (scale 2^(e-128))
+    on one gpt-oss layer.  Returns x + the layer's MoE output (fp32)."""
+    d, dff, ne, k = layer["d"], layer["dff"], layer["ne"], layer["k"]
+    keep = {n: np.ascontiguousarray(layer[n]) for n in
+            ("gate", "up", "down", "gate_b", "up_b", "down_b", "router_w", "router_b", "norm_w")}
+    L = GptossLayer(d, dff, ne, k, layer.get("alpha", 1.702), layer.get("limit", 7.0), layer.get("eps", 1e-5),
+                    _p(keep["gate"], u8p), _p(keep["up"], u8p), _p(keep["down"], u8p),
+                    _p(keep["gate_b"], f32p), _p(keep["up_b"], f32p), _p(keep["down_b"], f32p),
+                    _p(keep["router_w"], f32p), _p(keep["router_b"], f32p), _p(keep["norm_w"], f32p))
+    xo = np.array(x, np.float32, copy=True)
+    lib().orc_gptoss_moe_f64(C.byref(L), _p(xo, f32p), int(bool(apply_norm)))
+    return xo
 
 
 def qwen_moe(layer: dict, x: np.ndarray, apply_norm: bool, want_sums: bool = False):

@@ -346,6 +346,26 @@ def test_gptoss_layer_vs_f64(apply_norm):
         assert np.array_equal(t["dn_sums"][ei, r], R.mx_block_sums(L["down"][e * L["d"] + r], t["hq"][ei]))
 
 
+@pytest.mark.parametrize("apply_norm", [False, True])
+def test_gptoss_f64_dequant_mode_vs_numpy(apply_norm):
+    # the CPU baseline's second mode (orc_gptoss_moe_f64, C) against the
+    # numpy float64 layer of tests/f64ref.py (OCP MX decode, 2^(e-127) with
+    # the plain E2M1 table), unquantised: the same mathematics summed in
+    # another order
+    L = _small_gptoss(seed=3, zipf=1.1)
+    from cpubrrr_amd import synth
+    x = synth.token(L["d"], 3) * np.float32(2.0)
+    got = O.gptoss_moe_f64(L, x, apply_norm)
+    x64 = x.astype(np.float64)
+    if apply_norm:
+        xn = x64 / np.sqrt((x64 ** 2).mean() + 1e-5) * L["norm_w"].astype(np.float64)
+    else:
+        xn = x64
+    ref, _, _ = R.gptoss_ffn_f64(L, xn, quantize=False)
+    want = (x64 + ref).astype(np.float32)
+    assert np.max(np.abs(got.astype(np.float64) - want)) <= 1e-6 * np.abs(want).max()
+
+
 def test_qwen_layer_vs_f64():
     from cpubrrr_amd import synth
     d, dff, ne, k = 512, 256, 16, 8
