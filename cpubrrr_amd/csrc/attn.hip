@@ -912,6 +912,23 @@ int cpb_attn_create(const cpb_attn_cfg* cfg, int device, cpb_attn_t** out) {
         if (hipFuncSetAttribute((const void*)cpb::qkv_kernel(nbp / 4), hipFuncAttributeMaxDynamicSharedMemorySize, lq) != hipSuccess ||
             hipFuncSetAttribute((const void*)cpb::k_attn_oproj, hipFuncAttributeMaxDynamicSharedMemorySize, lo) != hipSuccess)
             return bail(fail(CPB_ENODEV, "LDS attribute (%d / %d bytes) refused", lq, lo));
+        // static + dynamic LDS of every kernel the forward launches within the
+        // device's per-workgroup limit (160 KiB on gfx950)
+        int lim = 0;
+        if (hipDeviceGetAttribute(&lim, hipDeviceAttributeMaxSharedMemoryPerBlock, device) != hipSuccess || lim <= 0)
+            return bail(fail(CPB_ENODEV, "LDS limit query failed"));
+        const struct { const void* f; size_t dyn; const char* name; } ks[] = {
+            {(const void*)cpb::qkv_kernel(nbp / 4), (size_t)lq, "k_attn_qkv"},
+            {(const void*)cpb::k_attn_core, 0, "k_attn_core"},
+            {(const void*)cpb::k_attn_oproj, (size_t)lo, "k_attn_oproj"},
+            {(const void*)cpb::k_attn_oproj_wave, 0, "k_attn_oproj_wave"}};
+        for (const auto& k : ks) {
+            hipFuncAttributes fa{};
+            if (hipFuncGetAttributes(&fa, k.f) != hipSuccess) return bail(fail(CPB_ENODEV, "attributes of %s", k.name));
+            if (fa.sharedSizeBytes + k.dyn > (size_t)lim)
+                return bail(fail(CPB_EINVAL, "%s needs %zu + %zu bytes of LDS, above the device's %d", k.name,
+                                 (size_t)fa.sharedSizeBytes, k.dyn, lim));
+        }
     }
     std::vector<float> tab;
     rope_table(64, cfg->max_seq, cfg->rope_base, tab);
