@@ -270,7 +270,8 @@ def cpu_baseline(host_layers, c, budget_s: float) -> dict:
 
 
 def bench_head(args, c) -> int:
-    """config 6: the LM head on one token; value = Q4 screen bytes / time."""
+    """config 6: the LM head on one token; value = screen bytes (Q4, or Q2
+    with --head-screen 2: the reference's CPBRR_HEAD2 option) / time."""
     import numpy as np
     import torch
 
@@ -290,6 +291,7 @@ def bench_head(args, c) -> int:
     stream = torch.cuda.Stream()
     torch.cuda.set_stream(stream)
     hd.set_stream(stream.cuda_stream)
+    hd.set_screen(args.head_screen)
     calib_copy(args)
     x = torch.from_numpy((r.standard_normal(d) * 3).astype(np.float32)).to("cuda:0")
     ch = torch.zeros(1, dtype=torch.int32, device="cuda:0")
@@ -304,18 +306,20 @@ def bench_head(args, c) -> int:
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / args.steps
     nb = d // 32
-    screen_bytes = V * nb * (16 + 2)                   # nibbles + bf16 scales of every row
+    q2 = args.head_screen == 2
+    screen_bytes = V * nb * ((8 if q2 else 16) + 2)    # codes + bf16 scales of every row
     refine_bytes = 96 * (d + nb * 4)
     gbs = (screen_bytes + refine_bytes) / (ms * 1e-3) / 1e9
     out = {"metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
            "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
-           "vs_baseline": None, "dtype": "int8 x Q4 / Q8", "data": "synthetic",
-           "config": {"workload": c["name"], "d": d, "n_vocab": V, "n_slices": 12, "n_cand": 8},
+           "vs_baseline": None, "dtype": "int8 x Q2 / Q8" if q2 else "int8 x Q4 / Q8", "data": "synthetic",
+           "config": {"workload": c["name"] + (" [Q2 screen]" if q2 else ""), "d": d, "n_vocab": V, "n_slices": 12,
+                      "n_cand": 8, "screen_bits": args.head_screen},
            "tok_per_s": round(1e3 / ms, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
            "roofline": {"bound": "hbm", "kernel": "whole head (norm, screen, top-k, refine)", "achieved": round(gbs, 1),
                         "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
-                        "traffic": MEASURED_TRAFFIC["head"] if (d, V) == (2880, 201088) else None,
-                     "traffic_source": TRAFFIC_SOURCE["head"],
+                        "traffic": MEASURED_TRAFFIC["head"] if (d, V) == (2880, 201088) and not q2 else None,
+                        "traffic_source": TRAFFIC_SOURCE["head"] if not q2 else None,
                         "bytes_per_launch": screen_bytes + refine_bytes}}
     hd.close()
     if not args.no_cpu:
@@ -586,7 +590,7 @@ def cpu_baseline_head(w, nw, x, budget_s: float) -> dict:
         n += 1
     per = (time.perf_counter() - t0) / n
     return {"value": round(1.0 / per, 3), "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"{n} head evaluations (Q4 rows quantised beforehand, as at the reference's load) in "
+            "sample": f"{n} head evaluations with the Q4 screen (rows quantised beforehand, as at the reference's load) in "
                       f"{per * n:.1f} s on {threads} threads; {per * 1e3:.1f} ms each",
             "ms_per_token": round(per * 1e3, 2)}
 
@@ -599,6 +603,8 @@ def main() -> int:
     ap.add_argument("--config", type=int, default=1, choices=sorted(CONFIGS))
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--head-screen", type=int, default=4, choices=[4, 2],
+                    help="config 6: the head's screen rows, Q4 (default) or Q2 (the reference's CPBRR_HEAD2)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="also run one plain device copy of this many MiB (HBM-traffic counter calibration)")
     args = ap.parse_args()

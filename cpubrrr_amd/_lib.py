@@ -105,6 +105,7 @@ SIGNATURES = {
     "cpb_head_load": (C.c_int, [C.c_void_p, C.POINTER(C.c_uint16), f32p]),
     "cpb_head_forward": (C.c_int, [C.c_void_p, f32p, i32p, C.POINTER(HeadTrace)]),
     "cpb_head_forward_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p]),
+    "cpb_head_set_screen": (C.c_int, [C.c_void_p, C.c_int]),
     "cpb_head_set_stream": (C.c_int, [C.c_void_p, C.c_void_p]),
     "cpb_head_sync": (C.c_int, [C.c_void_p]),
     "cpb_head_destroy": (None, [C.c_void_p]),

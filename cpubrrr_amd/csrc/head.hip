@@ -11,7 +11,9 @@
 //
 // HBM layout of the Q4 screen stream (built at load time from the bf16
 // weights): rows in tiles of 64, per (tile, 32-block) 64 lanes x 16 nibble
-// bytes (1 KB, one wavefront load) and 64 x bf16 scales; the Q8 rows stay
+// bytes (1 KB, one wavefront load) and 64 x bf16 scales; the Q2 stream (the
+// reference's CPBRR_HEAD2 option) the same with 8 code bytes per lane (two
+// blocks per 16-byte lane unit measured slower: fewer loads in flight); the Q8 rows stay
 // row-major (only the few candidate rows are read).  The screen is a
 // bandwidth-bound GEMV over 4.5 bits per weight (~326 MB for gpt-oss's
 // 201088 x 2880 head), one lane per row.
@@ -55,6 +57,8 @@ struct HeadDev {
     float eps;
     const u32x4* q4;       // [Vpad/64][nb][64] nibble units
     const uint16_t* q4s;   // [Vpad/64][nb][64] bf16 scales
+    const uint64_t* q2;    // [Vpad/64][nb][64] Q2 bytes (8 per row and block)
+    const uint16_t* q2s;   // [Vpad/64][nb][64] bf16 scales
     const int8_t* q8;      // [V][d]
     const float* q8s;      // [V][nb]
     const float* norm_w;   // [d]
@@ -142,9 +146,10 @@ CPB_DEV int wave_rank(float v, int i, uint64_t* sk) {
     return (r[0] + r[1]) + (r[2] + r[3]);
 }
 
-// ---- load time: Q4Mat + Q8Mat rows from bf16, one thread per (row, block) ----
+// ---- load time: Q4Mat, Q2Mat and Q8Mat rows from bf16, one thread per (row, block) ----
 __global__ void k_head_quant(const uint16_t* __restrict__ w, int V, int Vpad, int d, u32x4* __restrict__ q4,
-                             uint16_t* __restrict__ q4s, int8_t* __restrict__ q8, float* __restrict__ q8s) {
+                             uint16_t* __restrict__ q4s, uint64_t* __restrict__ q2, uint16_t* __restrict__ q2s,
+                             int8_t* __restrict__ q8, float* __restrict__ q8s) {
     const int nb = d / 32;
     const size_t total = (size_t)Vpad * nb;
     for (size_t idx = blockIdx.x * (size_t)blockDim.x + threadIdx.x; idx < total; idx += (size_t)gridDim.x * blockDim.x) {
@@ -189,6 +194,27 @@ __global__ void k_head_quant(const uint16_t* __restrict__ w, int V, int Vpad, in
         const size_t u = ((size_t)(row / kHeadRT) * nb + b) * kHeadRT + row % kHeadRT;
         q4[u] = u32x4{wd[0], wd[1], wd[2], wd[3]};
         q4s[u] = (uint16_t)best_db;
+        // Q2Mat (:366-399): scale bf16(vmax / -2), code clamp(floor(v / scale
+        // + 2.5), 0, 3); byte j holds elements j, j + 8, j + 16, j + 24
+        {
+            const uint32_t db2 = f32_to_bf16(vmax / -2.0f);
+            const float dq2 = bf16f(db2);
+            const float idq2 = dq2 != 0.0f ? 1.0f / dq2 : 0.0f;
+            uint64_t bytes = 0;
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                uint32_t byte = 0;
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    int c = (int)floorf(vals[j + 8 * k] * idq2 + 2.5f);
+                    c = c < 0 ? 0 : c > 3 ? 3 : c;
+                    byte |= (uint32_t)c << (2 * k);
+                }
+                bytes |= (uint64_t)byte << (8 * j);
+            }
+            q2[u] = bytes;
+            q2s[u] = (uint16_t)db2;
+        }
         if (row >= V) continue;
         // Q8Mat (:476-489): amax seeded 1e-12, round half away from zero
         float a8 = 1e-12f;
@@ -244,7 +270,11 @@ __global__ __launch_bounds__(256) void k_head_norm(HeadDev a) {
     }
 }
 
-// ---- Q4 screen of every row (dot4_q4_i8, :314-342): one lane per row ----
+// ---- screen of every row: one lane per row.  Q4 (dot4_q4_i8, :314-342) or
+// Q2 (dot4_q2_i8, :403-428; head2_on() at :953-957 selects it), the same
+// lane order: lane part j = elements 4j..4j+3 and 16+4j..16+4j+3, an int
+// dot per block, acc_j = fma(t_j, bf16 scale * xsb, acc_j) ----
+template <bool Q2>
 __global__ __launch_bounds__(256) void k_head_screen(HeadDev a) {
     extern __shared__ __align__(16) unsigned char smem[];
     const int nb = a.nb, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -262,7 +292,30 @@ __global__ __launch_bounds__(256) void k_head_screen(HeadDev a) {
     const bool live = tile * kHeadRT < a.Vpad;
     float val = -INFINITY;
     const int row = tile * kHeadRT + lane;
-    if (live) {
+    if (live && Q2) {
+        const uint64_t* wp = a.q2 + (size_t)tile * nb * kHeadRT + lane;
+        const uint16_t* sp = a.q2s + (size_t)tile * nb * kHeadRT + lane;
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 6
+        for (int b = 0; b < nb; b++) {
+            const uint64_t w = __builtin_nontemporal_load(wp + (size_t)b * kHeadRT);
+            const float sv = bf16f(sp[(size_t)b * kHeadRT]) * xsl[b];
+            const uint32_t w0 = (uint32_t)w, w1 = (uint32_t)(w >> 32);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                // elements 4j..4j+3: bytes 4 (j & 1) .. +3, bits 2 (j >> 1);
+                // elements 16+4j..: the same bytes, bits 4 + 2 (j >> 1)
+                const uint32_t src = (j & 1) ? w1 : w0;
+                const int sh = 2 * (j >> 1);
+                int t = sdot4((src >> sh) & 0x03030303u, xl[b * 8 + j], 0);
+                t = sdot4((src >> (sh + 4)) & 0x03030303u, xl[b * 8 + 4 + j], t);
+                t -= 2 * x8[b * 4 + j];                    // codes are KVI2[c] = c - 2
+                acc[j] = fmaf((float)t, sv, acc[j]);
+            }
+        }
+        val = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+        a.screen[row] = val;
+    } else if (live) {
         const u32x4* wp = a.q4 + (size_t)tile * nb * kHeadRT + lane;
         const uint16_t* sp = a.q4s + (size_t)tile * nb * kHeadRT + lane;
         float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -487,15 +540,16 @@ inline size_t head_refine_lds(int d, int nc) { return (size_t)nc * d + (size_t)n
 
 using cpb::fail;
 
-constexpr int kHeadBufs = 16;
+constexpr int kHeadBufs = 18;
 
 struct cpb_head {
     cpb_head_cfg cfg{};
     int device = 0;
     hipStream_t own = nullptr, stream = nullptr;
     cpb::HeadDev a{};
-    void* base[16] = {};
+    void* base[kHeadBufs] = {};
     bool loaded = false;
+    bool q2 = false;          // screen with the Q2 rows (cpb_head_set_screen)
 };
 
 namespace {
@@ -525,7 +579,7 @@ int cpb_head_bytes(const cpb_head_cfg* c, size_t* out) {
     if (int r = head_check(c)) return r;
     if (!out) return fail(CPB_EINVAL, "out is NULL");
     const size_t nb = c->d / 32;
-    *out = vpad(c) * nb * (16 + 2) + (size_t)c->n_vocab * (c->d + nb * 4);
+    *out = vpad(c) * nb * (16 + 2 + 8 + 2) + (size_t)c->n_vocab * (c->d + nb * 4);
     return 0;
 }
 
@@ -572,7 +626,8 @@ int cpb_head_create(const cpb_head_cfg* cfg, int device, cpb_head_t** out) {
     const size_t sizes[kHeadBufs] = {(size_t)a.Vpad * nb * 16, (size_t)a.Vpad * nb * 2, (size_t)a.V * a.d,
                                      (size_t)a.V * nb * 4, (size_t)a.d * 4, (size_t)a.d * 4,
                                      (size_t)a.d + nb * 4 + nb * 16, (size_t)a.Vpad * 4, nc * 4, nc * 4, nc * 4, 4,
-                                     wtab.size() * 4, ncand * 4, ncand * 4, 4};
+                                     wtab.size() * 4, ncand * 4, ncand * 4, 4, (size_t)a.Vpad * nb * 8,
+                                     (size_t)a.Vpad * nb * 2};
     for (int i = 0; i < kHeadBufs; i++) {
         hipError_t e = hipMalloc(&h->base[i], sizes[i]);
         if (e != hipSuccess) return bail(fail(CPB_ENOMEM, "hipMalloc(%zu): %s", sizes[i], hipGetErrorString(e)));
@@ -595,6 +650,8 @@ int cpb_head_create(const cpb_head_cfg* cfg, int device, cpb_head_t** out) {
     a.candv = (float*)h->base[13];
     a.candi = (int32_t*)h->base[14];
     a.count = (int32_t*)h->base[15];
+    a.q2 = (const uint64_t*)h->base[16];
+    a.q2s = (const uint16_t*)h->base[17];
     if (hipFuncSetAttribute((const void*)cpb::k_head_refine, hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)cpb::head_refine_lds(a.d, a.nc)) != hipSuccess)
         return bail(fail(CPB_ENODEV, "LDS attribute refused"));
@@ -616,7 +673,8 @@ int cpb_head_load(cpb_head_t* h, const uint16_t* out_w, const float* out_norm) {
     if (e == hipSuccess) e = hipMemcpyAsync((void*)a.norm_w, out_norm, (size_t)a.d * 4, hipMemcpyHostToDevice, h->stream);
     if (e == hipSuccess) {
         hipLaunchKernelGGL(cpb::k_head_quant, dim3(8192), dim3(256), 0, h->stream, staging, a.V, a.Vpad, a.d,
-                           (cpb::u32x4*)a.q4, (uint16_t*)a.q4s, (int8_t*)a.q8, (float*)a.q8s);
+                           (cpb::u32x4*)a.q4, (uint16_t*)a.q4s, (uint64_t*)a.q2, (uint16_t*)a.q2s, (int8_t*)a.q8,
+                           (float*)a.q8s);
         e = hipGetLastError();
     }
     if (e == hipSuccess) e = hipStreamSynchronize(h->stream);
@@ -633,7 +691,8 @@ static int head_launch(cpb_head_t* h, const float* x, int32_t* chosen) {
     a.chosen = chosen;
     cpb::launch(cpb::k_head_norm, dim3(1), dim3(256), sizeof(float) * (2 * a.d + 64), h->stream, a);
     const int tiles = a.Vpad / cpb::kHeadRT;
-    cpb::launch(cpb::k_head_screen, dim3((tiles + 3) / 4), dim3(256), (size_t)a.nb * (32 + 4 + 16), h->stream, a);
+    if (h->q2) cpb::launch(cpb::k_head_screen<true>, dim3((tiles + 3) / 4), dim3(256), (size_t)a.nb * (32 + 4 + 16), h->stream, a);
+    else cpb::launch(cpb::k_head_screen<false>, dim3((tiles + 3) / 4), dim3(256), (size_t)a.nb * (32 + 4 + 16), h->stream, a);
     cpb::launch(cpb::k_head_refine, dim3(a.nt), dim3(1024), cpb::head_refine_lds(a.d, a.nc), h->stream, a);
     return hipGetLastError() == hipSuccess ? 0 : fail(CPB_ENODEV, "head launch failed");
 }
@@ -669,6 +728,13 @@ int cpb_head_forward(cpb_head_t* h, const float* x, int32_t* chosen, cpb_head_tr
         if (r) return r;
     }
     HIP_OK_H(hipStreamSynchronize(h->stream));
+    return 0;
+}
+
+int cpb_head_set_screen(cpb_head_t* h, int bits) {
+    if (!h) return fail(CPB_EINVAL, "handle is NULL");
+    if (bits != 4 && bits != 2) return fail(CPB_EINVAL, "screen bits %d: 4 (Q4, default) or 2 (Q2)", bits);
+    h->q2 = bits == 2;
     return 0;
 }
 

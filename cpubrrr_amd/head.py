@@ -74,6 +74,10 @@ class LmHead:
         L.check(self._lib.cpb_head_forward_device(self._h, C.c_void_p(x_ptr), C.c_void_p(chosen_ptr)),
                 "cpb_head_forward_device")
 
+    def set_screen(self, bits: int) -> None:
+        """4: Q4 screen (default); 2: Q2 screen (the reference's CPBRR_HEAD2)."""
+        L.check(self._lib.cpb_head_set_screen(self._h, int(bits)), "cpb_head_set_screen")
+
     def set_stream(self, stream_ptr: int | None) -> None:
         L.check(self._lib.cpb_head_set_stream(self._h, C.c_void_p(stream_ptr or 0)), "cpb_head_set_stream")
 

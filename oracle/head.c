@@ -84,6 +84,56 @@ void orc_q4_quant_row(const uint16_t* w, int cols, uint8_t* nib, uint16_t* sc) {
     }
 }
 
+/* engine_gpt2.rs:356-399 Q2Mat::from_bf16, one row (natural layout: per
+ * 32-block 8 bytes, byte j = code(j) | code(j + 8) << 2 | code(j + 16) << 4 |
+ * code(j + 24) << 6; one bf16 scale bf16(vmax / -2), vmax the first value
+ * of largest magnitude; code = clamp(floor(v / scale + 2.5), 0, 3), value
+ * KVI2[code] = code - 2) */
+void orc_q2_quant_row(const uint16_t* w, int cols, uint8_t* nib, uint16_t* sc) {
+    for (int b = 0; b < cols / 32; b++) {
+        float vals[32], vmax = 0.0f, amax = 0.0f;
+        for (int i = 0; i < 32; i++) {
+            vals[i] = orc_bf16_to_f32(w[b * 32 + i]);
+            if (fabsf(vals[i]) > amax) { amax = fabsf(vals[i]); vmax = vals[i]; }
+        }
+        uint16_t db = orc_f32_to_bf16(vmax / -2.0f);
+        float dq = orc_bf16_to_f32(db);
+        float idq = dq != 0.0f ? 1.0f / dq : 0.0f;
+        sc[b] = db;
+        for (int j = 0; j < 8; j++) {
+            uint8_t byte = 0;
+            for (int k = 0; k < 4; k++) {
+                int c = (int)floorf(vals[j + k * 8] * idq + 2.5f);
+                c = c < 0 ? 0 : c > 3 ? 3 : c;
+                byte |= (uint8_t)(c << (2 * k));
+            }
+            nib[b * 8 + j] = byte;
+        }
+    }
+}
+
+/* engine_gpt2.rs:403-428 dot4_q2_i8, one row: as dot4_q4_i8, lane j takes
+ * elements 4j..4j+3 and 16+4j..16+4j+3 (code of element e: bits 2 (e / 8) of
+ * byte e % 8), KVI2[c] = c - 2 */
+float orc_q2_row_dot(const uint8_t* nib, const uint16_t* sc, const int8_t* xq, const float* xsb, int nb) {
+    float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int b = 0; b < nb; b++) {
+        float sv = orc_bf16_to_f32(sc[b]) * xsb[b];
+        for (int j = 0; j < 4; j++) {
+            int t = 0;
+            for (int i = 0; i < 4; i++) {
+                int e0 = 4 * j + i, e1 = 16 + 4 * j + i;
+                int c0 = (nib[b * 8 + e0 % 8] >> (2 * (e0 / 8))) & 3;
+                int c1 = (nib[b * 8 + e1 % 8] >> (2 * (e1 / 8))) & 3;
+                t += (c0 - 2) * xq[b * 32 + e0];
+                t += (c1 - 2) * xq[b * 32 + e1];
+            }
+            a[j] = fmaf((float)t, sv, a[j]);
+        }
+    }
+    return (a[0] + a[1]) + (a[2] + a[3]);
+}
+
 /* engine_gpt2.rs:466-494 Q8Mat::from_bf16, one row */
 void orc_q8_quant_row(const uint16_t* w, int cols, int8_t* q, float* s) {
     for (int b = 0; b < cols / 32; b++) {
@@ -183,13 +233,21 @@ long orc_head_slice_start(long n, int nt, int wid) {
 
 static void head_impl(const uint16_t* w, const uint8_t* pre_nib, const uint16_t* pre_sc, int V, int d,
                       const float* x, const float* norm_w, float eps, int nt, int cand, int32_t* cand_ids,
-                      float* cand_screen, float* cand_logits, int8_t* xq_out, float* xsb_out, int32_t* chosen);
+                      float* cand_screen, float* cand_logits, int8_t* xq_out, float* xsb_out, int32_t* chosen, int q2);
 
 void orc_head(const uint16_t* w, int V, int d, const float* x, const float* norm_w, float eps, int nt, int cand,
               int32_t* cand_ids, float* cand_screen, float* cand_logits, int8_t* xq_out, float* xsb_out,
               int32_t* chosen) {
     head_impl(w, NULL, NULL, V, d, x, norm_w, eps, nt, cand, cand_ids, cand_screen, cand_logits, xq_out, xsb_out,
-              chosen);
+              chosen, 0);
+}
+
+/* the head with the Q2 screen (head2_on(), engine_gpt2.rs:953-957) */
+void orc_head_q2(const uint16_t* w, int V, int d, const float* x, const float* norm_w, float eps, int nt, int cand,
+                 int32_t* cand_ids, float* cand_screen, float* cand_logits, int8_t* xq_out, float* xsb_out,
+                 int32_t* chosen) {
+    head_impl(w, NULL, NULL, V, d, x, norm_w, eps, nt, cand, cand_ids, cand_screen, cand_logits, xq_out, xsb_out,
+              chosen, 1);
 }
 
 /* orc_head with the Q4 rows already quantised (orc_q4_quant_rows): the
@@ -198,12 +256,12 @@ void orc_head_pre(const uint16_t* w, const uint8_t* nib, const uint16_t* sc, int
                   const float* norm_w, float eps, int nt, int cand, int32_t* cand_ids, float* cand_screen,
                   float* cand_logits, int8_t* xq_out, float* xsb_out, int32_t* chosen) {
     head_impl(w, nib, sc, V, d, x, norm_w, eps, nt, cand, cand_ids, cand_screen, cand_logits, xq_out, xsb_out,
-              chosen);
+              chosen, 0);
 }
 
 static void head_impl(const uint16_t* w, const uint8_t* pre_nib, const uint16_t* pre_sc, int V, int d,
                       const float* x, const float* norm_w, float eps, int nt, int cand, int32_t* cand_ids,
-                      float* cand_screen, float* cand_logits, int8_t* xq_out, float* xsb_out, int32_t* chosen) {
+                      float* cand_screen, float* cand_logits, int8_t* xq_out, float* xsb_out, int32_t* chosen, int q2) {
     int nb = d / 32, nq = V / 4;
     float* xn = (float*)malloc(sizeof(float) * d);
     int8_t* xq = (int8_t*)malloc(d);
@@ -215,7 +273,12 @@ static void head_impl(const uint16_t* w, const uint8_t* pre_nib, const uint16_t*
     int nth = orc_get_threads();
     #pragma omp parallel for schedule(static) num_threads(nth)
     for (int r = 0; r < V; r++) {
-        if (pre_nib) {
+        if (q2) {
+            uint8_t nib[2048];
+            uint16_t sc[256];
+            orc_q2_quant_row(w + (size_t)r * d, d, nib, sc);
+            screen[r] = orc_q2_row_dot(nib, sc, xq, xsb, nb);
+        } else if (pre_nib) {
             screen[r] = orc_q4_row_dot(pre_nib + (size_t)r * (d / 2), pre_sc + (size_t)r * nb, xq, xsb, nb);
         } else {
             uint8_t nib[4096];

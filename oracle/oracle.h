@@ -115,6 +115,11 @@ void  orc_q8_quant_row(const uint16_t* w, int cols, int8_t* q, float* s);
 float orc_q4_row_dot(const uint8_t* nib, const uint16_t* sc, const int8_t* xq, const float* xsb, int nb);
 float orc_q8_row_dot(const int8_t* q, const float* s, const int8_t* xq, const float* xsb, int cols);
 long  orc_head_slice_start(long n, int nt, int wid);
+void  orc_q2_quant_row(const uint16_t* w, int cols, uint8_t* nib, uint16_t* sc);
+float orc_q2_row_dot(const uint8_t* nib, const uint16_t* sc, const int8_t* xq, const float* xsb, int nb);
+void  orc_head_q2(const uint16_t* w, int V, int d, const float* x, const float* norm_w, float eps, int nt, int cand,
+                  int32_t* cand_ids, float* cand_screen, float* cand_logits, int8_t* xq_out, float* xsb_out,
+                  int32_t* chosen);
 void  orc_head(const uint16_t* w, int V, int d, const float* x, const float* norm_w, float eps, int nt, int cand,
                int32_t* cand_ids, float* cand_screen, float* cand_logits, int8_t* xq_out, float* xsb_out,
                int32_t* chosen);

@@ -86,6 +86,11 @@ def lib() -> C.CDLL:
         L.orc_q8_row_dot.argtypes = [i8p, f32p, i8p, f32p, C.c_int]
         L.orc_gptoss_moe_f64.argtypes = [C.c_void_p, f32p, C.c_int]
         L.orc_gptoss_moe_f64.restype = None
+        L.orc_q2_quant_row.argtypes = [u16p, C.c_int, u8p, u16p]
+        L.orc_q2_row_dot.restype = C.c_float
+        L.orc_q2_row_dot.argtypes = [u8p, u16p, i8p, f32p, C.c_int]
+        L.orc_head_q2.argtypes = [u16p, C.c_int, C.c_int, f32p, f32p, C.c_float, C.c_int, C.c_int, i32p, f32p, f32p,
+                                  i8p, f32p, i32p]
         L.orc_head_slice_start.argtypes = [C.c_long, C.c_int, C.c_int]
         L.orc_head_slice_start.restype = C.c_long
         L.orc_head.argtypes = [u16p, C.c_int, C.c_int, f32p, f32p, C.c_float, C.c_int, C.c_int, i32p, f32p, f32p,
@@ -298,6 +303,19 @@ def q4_quant_row(w_bf16):
     return nib, sc
 
 
+def q2_quant_row(w_bf16):
+    w = np.ascontiguousarray(w_bf16, np.uint16)
+    nib = np.empty(w.size // 4, np.uint8); sc = np.empty(w.size // 32, np.uint16)
+    lib().orc_q2_quant_row(_p(w, u16p), w.size, _p(nib, u8p), _p(sc, u16p))
+    return nib, sc
+
+
+def q2_row_dot(nib, sc, xq, xsb):
+    nib = np.ascontiguousarray(nib, np.uint8); sc = np.ascontiguousarray(sc, np.uint16)
+    xq = np.ascontiguousarray(xq, np.int8); xsb = np.ascontiguousarray(xsb, np.float32)
+    return np.float32(lib().orc_q2_row_dot(_p(nib, u8p), _p(sc, u16p), _p(xq, i8p), _p(xsb, f32p), xsb.size))
+
+
 def q8_quant_row(w_bf16):
     w = np.ascontiguousarray(w_bf16, np.uint16)
     q = np.empty(w.size, np.int8); s = np.empty(w.size // 32, np.float32)
@@ -331,10 +349,11 @@ def head_slice_start(n, nt, wid):
     return int(lib().orc_head_slice_start(n, nt, wid))
 
 
-def head(w_bf16, x, norm_w, eps, nt=12, cand=8, pre=None):
+def head(w_bf16, x, norm_w, eps, nt=12, cand=8, pre=None, q2=False):
     """engine_gpt2.rs:937-1002 (greedy).  Returns dict: chosen, cand_ids,
     cand_screen, cand_logits, xq, xsb.  pre: (nib, sc) of q4_quant_rows, or
-    None to quantise the Q4 rows inside the call."""
+    None to quantise the Q4 rows inside the call.  q2: the Q2 screen
+    (head2_on(), :953-957) instead of the Q4 one."""
     w = np.ascontiguousarray(w_bf16, np.uint16)
     V, d = w.shape
     x = np.ascontiguousarray(x, np.float32); norm_w = np.ascontiguousarray(norm_w, np.float32)
@@ -350,9 +369,10 @@ def head(w_bf16, x, norm_w, eps, nt=12, cand=8, pre=None):
                            _p(out["cand_logits"], f32p), _p(out["xq"], i8p), _p(out["xsb"], f32p), C.byref(ch))
         out["chosen"] = int(ch.value)
         return out
-    lib().orc_head(_p(w, u16p), V, d, _p(x, f32p), _p(norm_w, f32p), float(eps), nt, cand,
-                   _p(out["cand_ids"], i32p), _p(out["cand_screen"], f32p), _p(out["cand_logits"], f32p),
-                   _p(out["xq"], i8p), _p(out["xsb"], f32p), C.byref(ch))
+    fn = lib().orc_head_q2 if q2 else lib().orc_head
+    fn(_p(w, u16p), V, d, _p(x, f32p), _p(norm_w, f32p), float(eps), nt, cand,
+       _p(out["cand_ids"], i32p), _p(out["cand_screen"], f32p), _p(out["cand_logits"], f32p),
+       _p(out["xq"], i8p), _p(out["xsb"], f32p), C.byref(ch))
     out["chosen"] = int(ch.value)
     return out
 

@@ -235,6 +235,7 @@ extern "C" {
     pub fn cpb_head_load(h: *mut cpb_head_t, out_w: *const u16, out_norm: *const f32) -> c_int;
     pub fn cpb_head_forward(h: *mut cpb_head_t, x: *const f32, chosen: *mut i32, trace: *mut cpb_head_trace) -> c_int;
     pub fn cpb_head_forward_device(h: *mut cpb_head_t, d_x: *const f32, d_chosen: *mut i32) -> c_int;
+    pub fn cpb_head_set_screen(h: *mut cpb_head_t, bits: c_int) -> c_int;
     pub fn cpb_head_set_stream(h: *mut cpb_head_t, stream: *mut c_void) -> c_int;
     pub fn cpb_head_sync(h: *mut cpb_head_t) -> c_int;
     pub fn cpb_head_destroy(h: *mut cpb_head_t);

@@ -1,6 +1,6 @@
 """GPU parity of the two-stage LM head (head.hip) against the oracle
 (oracle/head.c, pinned in tests/test_oracle_head.py): Q8 activations,
-every row's Q4 screen value, the candidate set (ids in worker / rank order),
+every row's Q4 (or Q2) screen value, the candidate set (ids in worker / rank order),
 the candidates' exact Q8 logits and the greedy token, all bit for bit;
 including tied rows (lower index first) and an odd block count."""
 import numpy as np
@@ -21,8 +21,8 @@ def bf16(a):
     return (((b + 0x7FFF + ((b >> 16) & 1)) >> 16) & 0xFFFF).astype(np.uint16)
 
 
-def run(V, d, seed, nt=12, cand=8, dup=False, full_screen=True):
-    say(f"case head V={V} d={d} seed={seed} nt={nt} cand={cand} dup={dup}")
+def run(V, d, seed, nt=12, cand=8, dup=False, full_screen=True, q2=False):
+    say(f"case head V={V} d={d} seed={seed} nt={nt} cand={cand} dup={dup} q2={q2}")
     r = np.random.default_rng(seed)
     w = bf16(r.standard_normal((V, d)).astype(np.float32) * 0.02)
     if dup:
@@ -33,14 +33,17 @@ def run(V, d, seed, nt=12, cand=8, dup=False, full_screen=True):
     x = (r.standard_normal(d) * 3).astype(np.float32)
     with LmHead(d, V, 1e-5, nt, cand) as hd:
         hd.load(w, nw)
+        if q2:
+            hd.set_screen(2)
         ch, t = hd.forward(x, trace=True)
         ch2, _ = hd.forward(x)
-    o = O.head(w, x, nw, 1e-5, nt, cand)
+    o = O.head(w, x, nw, 1e-5, nt, cand, q2=q2)
     assert ch == ch2
     assert np.array_equal(t["xq"], o["xq"]) and np.array_equal(t["xsb"].view(np.uint32), o["xsb"].view(np.uint32))
     rows = range(V) if full_screen else list(range(0, V, max(1, V // 300))) + list(o["cand_ids"])
     for row in rows:
-        want = O.q4_row_dot(*O.q4_quant_row(w[row]), o["xq"], o["xsb"])
+        want = (O.q2_row_dot(*O.q2_quant_row(w[row]), o["xq"], o["xsb"]) if q2
+                else O.q4_row_dot(*O.q4_quant_row(w[row]), o["xq"], o["xsb"]))
         assert t["screen"][row].view(np.uint32) == np.float32(want).view(np.uint32), row
     assert np.array_equal(t["cand_ids"], o["cand_ids"]), (t["cand_ids"], o["cand_ids"])
     assert np.array_equal(t["cand_screen"].view(np.uint32), o["cand_screen"].view(np.uint32))
@@ -72,3 +75,13 @@ def test_head_edge_shapes(gpu):
     run(1000, 96, 7, nt=8, cand=16)
     run(2052, 128, 8, nt=1, cand=16)
     run(300, 64, 9, nt=32, cand=4, dup=True)
+
+
+def test_head_q2_screen(gpu):
+    # the reference's Q2 screen option (CPBRR_HEAD2): every row's Q2 value,
+    # the candidates and the token bit-exact, at a small shape, with ties,
+    # with 20 workers, and at gpt-oss's 201088 x 2880
+    run(4096, 512, 11, q2=True)
+    run(4096, 256, 12, dup=True, q2=True)
+    run(1000, 96, 13, nt=20, cand=4, q2=True)
+    run(201088, 2880, 14, full_screen=False, q2=True)

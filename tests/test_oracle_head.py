@@ -153,6 +153,77 @@ def test_q4_scale_search_error_minimal_f64():
         assert e_chosen <= min(errs.values()) * (1 + 1e-5) + 1e-30, trial
 
 
+def _q2_codes(nib):
+    """[nb * 8] Q2 bytes -> [nb][32] codes in element order (element e: bits
+    2 (e // 8) of byte e % 8, engine_gpt2.rs:356-399)"""
+    b = np.asarray(nib, np.uint8).reshape(-1, 8)
+    return np.concatenate([(b >> (2 * k)) & 3 for k in range(4)], axis=1)
+
+
+def test_q2_quant_known_answers():
+    # values k * d0 with k in {-2, -1, 0, 1} and vmax = -2 * d0: scale
+    # bf16(vmax / -2) = d0 exactly, every value reproduced (code k + 2)
+    k = rng.integers(-2, 2, 32)
+    k[3] = -2
+    vals = (k * np.float32(-0.5)).astype(np.float32)            # vmax = +1.0
+    nib, sc = O.q2_quant_row(bf16_np(vals))
+    assert sc[0] == 0xBF00                                        # bf16(-0.5)
+    assert np.array_equal(_q2_codes(nib)[0].astype(int) - 2, k)
+    # byte j packs elements j, j + 8, j + 16, j + 24, two bits each, low first
+    c = k + 2
+    for j in range(8):
+        assert nib[j] == c[j] | (c[j + 8] << 2) | (c[j + 16] << 4) | (c[j + 24] << 6)
+    # clamping: a value beyond the scale's range takes code 0 or 3
+    v2 = np.zeros(32, np.float32)
+    v2[0], v2[1], v2[2] = 4.0, -4.0, -9.0                         # vmax = -9 -> scale bf16(4.5) = 4.5
+    nib, sc = O.q2_quant_row(bf16_np(v2))
+    cc = _q2_codes(nib)[0]
+    # floor(4/4.5 + 2.5) = 3, floor(-4/4.5 + 2.5) = 1, floor(-2 + 2.5) = 0, zeros -> 2
+    assert sc[0] == bf16_np(np.float32(4.5)) and list(cc[:4]) == [3, 1, 0, 2]
+    # the zero block: vmax / -2 = -0.0 (bf16 0x8000), codes 2 (value 0)
+    nib, sc = O.q2_quant_row(np.zeros(32, np.uint16))
+    assert sc[0] == 0x8000 and np.all(nib == 0xAA)
+
+
+def test_q2_row_dot_lane_order():
+    d = 2880
+    xq, xsb = _xq(d)
+    w = bf16_np(rng.standard_normal(d).astype(np.float32) * 0.02)
+    nib, sc = O.q2_quant_row(w)
+    codes = _q2_codes(nib)
+    a = [f32(0)] * 4
+    for b in range(d // 32):
+        sv = from_bf16(sc[b]) * xsb[b]
+        for j in range(4):
+            e = np.concatenate([np.arange(4 * j, 4 * j + 4), np.arange(16 + 4 * j, 20 + 4 * j)])
+            t = int(((codes[b, e].astype(int) - 2) * xq[b * 32 + e]).sum())
+            a[j] = fma32(f32(t), sv, a[j])
+    want = f32(f32(a[0] + a[1]) + f32(a[2] + a[3]))
+    assert O.q2_row_dot(nib, sc, xq, xsb) == want
+    deq = ((codes.astype(np.float64) - 2) * from_bf16(sc)[:, None].astype(np.float64)).reshape(-1)
+    ref = float((deq * xq.astype(np.float64) * np.repeat(xsb, 32)).sum())
+    assert abs(float(want) - ref) <= 1e-5 * float(np.abs(deq * xq * np.repeat(xsb, 32)).sum())
+
+
+def test_head_q2_screen_candidates():
+    V, d, nt, cand = 1024, 256, 12, 8
+    w = bf16_np(rng.standard_normal((V, d)).astype(np.float32) * 0.02)
+    x = rng.standard_normal(d).astype(np.float32)
+    out = O.head(w, x, np.ones(d, np.float32), 1e-5, nt, cand, q2=True)
+    xq, xsb = out["xq"], out["xsb"]
+    screen = np.array([O.q2_row_dot(*O.q2_quant_row(w[r]), xq, xsb) for r in range(V)], np.float32)
+    ids = []
+    for wid in range(nt):
+        r0, r1 = 4 * O.head_slice_start(V // 4, nt, wid), 4 * O.head_slice_start(V // 4, nt, wid + 1)
+        order = np.argsort(-screen[r0:r1].astype(np.float64), kind="stable")[:cand]
+        ids += list(r0 + order)
+    assert np.array_equal(out["cand_ids"], np.array(ids, np.int32))
+    assert np.array_equal(out["cand_screen"], screen[ids])
+    logits = np.array([O.q8_row_dot(*O.q8_quant_row(w[r]), xq, xsb) for r in ids], np.float32)
+    assert np.array_equal(out["cand_logits"], logits)
+    assert out["chosen"] == ids[int(np.argmax(logits))]
+
+
 def test_q8_quant_row_closed_form():
     w = bf16_np(rng.standard_normal(512).astype(np.float32) * 0.05)
     q, s = O.q8_quant_row(w)
