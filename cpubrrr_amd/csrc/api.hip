@@ -120,6 +120,7 @@ struct LayerDev {
     cpb::u32x4* gu = nullptr;   // gate+up stream layout
     cpb::u32x4* up = nullptr;   // unused (kept null)
     cpb::u32x4* dn = nullptr;   // down stream
+    const uint16_t* dn_d = nullptr;   // Q6_K down: its fp16 d stream (inside the dn allocation)
     float *gate_b = nullptr, *up_b = nullptr, *down_b = nullptr;
     float *router_w = nullptr, *router_b = nullptr, *norm_w = nullptr;
     int gu_type = 0, down_type = 0;   // GGUF type ids of this layer's gate/up and down tensors
@@ -407,7 +408,7 @@ int layer_token(cpb_moe_t* h, const DecodeBufs& B, int layer, float* dx, int app
         }
     } else {
         cpb::KqArgs k{};
-        k.gu = L.gu; k.dn = L.dn; k.down_type = L.down_type;
+        k.gu = L.gu; k.dn = L.dn; k.dn_d = L.dn_d; k.down_type = L.down_type;
         k.xq = B.xq; k.xs = B.xsb; k.xsum = B.xsum; k.ids = B.ids; k.wts = B.wts;
         {
             k.sel.lstar = B.lstar; k.sel.lbound = B.lbound; k.sel.router_w = L.router_w; k.sel.router_b = L.router_b;
@@ -568,6 +569,7 @@ int cpb_moe_load_layer_typed(cpb_moe_t* h, int layer, int gate_type, int up_type
         if ((r = dmalloc((uint8_t**)&L.dn, cpb::kq_down_bytes(ne, d, ff, c.top_k, down_type)))) return r;
         if (cpb::launch_repack_kq_down(h->staging, L.dn, ne, d, ff, c.top_k, down_type, h->stream))
             return fail(CPB_ENODEV, "repack launch failed");
+        L.dn_d = cpb::kq_down_dstream(L.dn, ne, d, ff, down_type);
     }
     const ParamSlots ps = param_slots(c);
     float* base = h->params + (size_t)layer * ps.per_layer;
@@ -600,7 +602,7 @@ static int layer_grouped(cpb_moe_t* h, int layer, float* d_x, int n_tok, int app
     const LayerDev& L = h->layers[layer];
     cpb::GroupedArgs g{};
     g.norm_w = L.norm_w; g.router_w = L.router_w; g.router_b = L.router_b;
-    g.gu = L.gu; g.dn = L.dn; g.gate_b = L.gate_b; g.up_b = L.up_b; g.down_b = L.down_b;
+    g.gu = L.gu; g.dn = L.dn; g.dn_d = L.dn_d; g.gate_b = L.gate_b; g.up_b = L.up_b; g.down_b = L.down_b;
     g.n_tok = n_tok; g.d = c.d; g.dff = c.d_ff; g.ne = c.n_expert; g.k = c.top_k; g.nb = h->nb; g.nbf = h->nbf;
     g.parts_gu = h->parts_gu; g.parts_dn = h->parts_dn;
     g.norm = c.norm; g.norm_nt = c.norm_nt; g.apply_norm = apply_norm;

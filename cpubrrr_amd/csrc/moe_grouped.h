@@ -15,6 +15,7 @@ struct GroupedArgs {
     const float* router_b;
     const u32x4* gu;           // decode stream layouts (moe_mx.hip), read as MFMA operands
     const u32x4* dn;
+    const uint16_t* dn_d;      // Q6_K down: the fp16 d stream (kq_down_dstream)
     const float* gate_b;
     const float* up_b;
     const float* down_b;

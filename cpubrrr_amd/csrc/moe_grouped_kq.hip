@@ -27,7 +27,8 @@
 // Weights are read in the decode kernels' stream layouts (one copy in HBM):
 // gate/up per (expert, 16-row tile, superblock) 9 units x 32 lanes (lanes
 // 0-15 gate, 16-31 up); down per (expert, RT-row tile, superblock) U units x
-// RT lanes (RT = 64 / top_k).
+// RT lanes (RT = 64 / top_k), and for Q6_K the fp16 d of those RT rows in the
+// d stream.
 #include "moe_common.h"
 #include "moe_grouped.h"
 #include "moe_kq.h"
@@ -255,7 +256,7 @@ CPB_DEV uint32_t q6_minus32(uint32_t v) {
 // row tile w.
 template <int TYPE, bool TRACE>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_down_kq_grouped(GroupedArgs a) {
-    constexpr int U = TYPE == 12 ? kQ4Units : kQ6Units;
+    constexpr int U = TYPE == 12 ? kQ4Units : kQ6StreamUnits;   // units per superblock in the stream
     __shared__ int src[32];
     __shared__ uint8_t s_sm[4][32][16];          // Q4_K: sc[8], mn[8]; Q6_K: int8 scales[16]
     __shared__ float s_dm[4][32][2];
@@ -273,6 +274,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     const int pair = src[r];
     const int R = (live ? rt : 0) * 32 + r;                   // this lane's A row
     const u32x4* wrow = a.dn + (((size_t)e * Td + R / RT) * nsbf) * U * RT + R % RT;
+    const uint16_t* drow = TYPE == 14 ? a.dn_d + ((size_t)e * Td + R / RT) * nsbf * RT + R % RT : nullptr;
     const __amdgpu_buffer_rsrc_t rh = buf_rsrc(a.hq, (uint32_t)((size_t)a.n_tok * a.k * a.dff));
     float sumf[16];
 #pragma unroll
@@ -296,7 +298,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
                 wu[4 + h6] = wp[(8 + h6 * 2 + hb) * RT];
             }
             wu[6] = wp[12 * RT];
-            du = *(const uint32_t*)(wp + 13 * RT);
+            du = drow[(size_t)sb * RT];
         }
     };
     u32x4 nwu[7];
@@ -350,7 +352,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
                 for (int j = 0; j < 8; j++) mint[i] += (int)s_sm[w][row][8 + j] * xs8[j];
             }
         } else {
-            // ql[128] = units 0-7, qh[64] = units 8-11, int8 scales = unit 12, d = unit 13
+            // ql[128] = units 0-7, qh[64] = units 8-11, int8 scales = unit 12, d from the d stream
             const u32x4 ql[4] = {wu[0], wu[1], wu[2], wu[3]}, qh[2] = {wu[4], wu[5]};
             const u32x4 scu = wu[6];
             if (hb == 0) {

@@ -7,11 +7,16 @@
 
 namespace cpb {
 
-// 16-byte units per superblock in the stream layouts (Q4_K: 144 B = 9 units;
-// Q6_K: 210 B padded to 14, the fp16 d alone in unit 13)
+// 16-byte units per superblock in the stream layouts.  Q4_K: 144 B = 9
+// units.  Q6_K: ql, qh and the int8 scales (208 B = 13 units) in the unit
+// stream, the fp16 d in a separate stream behind it (2 B per superblock, the
+// RT rows of a (tile, superblock) contiguous), so the down stream holds
+// exactly the 210 B of each superblock.  In registers the kernels keep the d
+// as a 14th unit (kQ6Units).
 constexpr int kQ4Units = 9;
 constexpr int kQ6Units = 14;
-CPB_DEV_HOST_INLINE int kq_units(int type) { return type == 12 ? kQ4Units : kQ6Units; }
+constexpr int kQ6StreamUnits = 13;
+CPB_DEV_HOST_INLINE int kq_units(int type) { return type == 12 ? kQ4Units : kQ6StreamUnits; }
 CPB_DEV_HOST_INLINE int kq_sb_bytes(int type) { return type == 12 ? 144 : 210; }
 
 // engine_qwen2.rs:40-51 converts IEEE binary16 exactly; so does the hardware.
@@ -20,6 +25,7 @@ CPB_DEV float half_bits(uint32_t h) { return (float)__builtin_bit_cast(_Float16,
 struct KqArgs {
     const u32x4* gu;         // gate+up stream layout (k_repack_kq_gateup)
     const u32x4* dn;         // down stream layout (k_repack_kq_down)
+    const uint16_t* dn_d;    // Q6_K: the fp16 d stream behind dn (kq_down_dstream)
     int down_type;           // 12 (Q4_K) or 14 (Q6_K); gate/up are Q4_K
     const int8_t* xq;        // [d]   Q8_K activations
     const float* xs;         // [d/256]
@@ -43,6 +49,8 @@ struct KqArgs {
 // bytes of the stream layouts
 size_t kq_gateup_bytes(int ne, int dff, int d);
 size_t kq_down_bytes(int ne, int d, int dff, int top_k, int down_type);
+// the Q6_K fp16 d stream behind the units of a down stream (null for Q4_K)
+const uint16_t* kq_down_dstream(const u32x4* dn, int ne, int d, int dff, int down_type);
 // re-layout from native GGUF superblock rows (device buffers, stream s)
 int launch_repack_kq_gateup(const uint8_t* gate, const uint8_t* up, u32x4* out, int ne, int dff, int d, hipStream_t s);
 int launch_repack_kq_down(const uint8_t* down, u32x4* out, int ne, int d, int dff, int top_k, int down_type,

@@ -13,8 +13,8 @@
 // for bit.
 //
 // HBM layout ("stream layout", k_repack_kq_*): a superblock is cut into
-// 16-byte units (Q4_K: 144 B = 9 units; Q6_K: 210 B padded to 14 units, the
-// fp16 d alone in unit 13).
+// 16-byte units (Q4_K: 144 B = 9 units; Q6_K: its first 208 B = 13 units,
+// the fp16 d in a separate stream behind them, RT rows contiguous).
 //   gate/up: tile = 16 rows of gate + the same 16 rows of up of one expert;
 //            for each (expert, tile, superblock): units x 32 lanes x 16 B,
 //            lanes 0-15 gate, 16-31 up.  A wave handles two superblocks
@@ -78,7 +78,7 @@ CPB_DEV float q4k_term(const u32x4 (&u)[kQ4Units], const int8_t* xs, const int32
     return ys * d * (float)sumi - ys * dmin * (float)mint;
 }
 
-// Q6_K superblock term of one row (engine_qwen2.rs:164-200).  u: 14 units
+// Q6_K superblock term of one row (engine_qwen2.rs:164-200).  u: 14 units in registers
 // (ql[128] = u[0..7], qh[64] = u[8..11], int8 scales[16] = u[12], fp16 d in
 // u[13]); xs: 256 int8 activations; xs16: their 16 int32 sums per 16.
 // q - 32 is folded as dot(q, x) - 32 * sum(x) (an exact integer identity).
@@ -243,16 +243,14 @@ __global__ __launch_bounds__(1024) void k_down_kq(KqArgs a) {
         for (int k = 0; k < 8; k++) hv[k] = src[k];
     }
     __builtin_amdgcn_sched_barrier(0);          // the chunk's loads stay ahead of the weights'
-    const u32x4* wp = a.dn + ((((size_t)e * T + t) * nsbf + q) * U) * RT + rr;
+    constexpr int SU = TYPE == 12 ? kQ4Units : kQ6StreamUnits;   // units in the stream
+    const size_t sbi = ((size_t)e * T + t) * nsbf + q;           // (expert, tile, superblock)
+    const u32x4* wp = a.dn + sbi * SU * RT + rr;
     u32x4 u[U];
 #pragma unroll
-    for (int k = 0; k < U; k++) {
-        // Q6_K's last unit holds only the fp16 d: a 4-byte load (a partly dead
-        // 16-byte destination lets later instructions reuse its registers,
-        // which then wait for the whole weight stream)
-        if (TYPE == 14 && k == kQ6Units - 1) u[k] = u32x4{__builtin_nontemporal_load((const uint32_t*)(wp + k * RT)), 0, 0, 0};
-        else u[k] = __builtin_nontemporal_load(wp + k * RT);
-    }
+    for (int k = 0; k < SU; k++) u[k] = __builtin_nontemporal_load(wp + k * RT);
+    // Q6_K: the fp16 d from its own stream, kept as unit 13
+    if constexpr (TYPE == 14) u[kQ6Units - 1] = u32x4{(uint32_t)__builtin_nontemporal_load(a.dn_d + sbi * RT + rr), 0, 0, 0};
     __builtin_amdgcn_sched_barrier(0);
 
     // Q8_K of hbuf (engine_qwen2.rs:288-300): chunk c = 32 values; a 256-block
@@ -364,10 +362,12 @@ __global__ void k_repack_kq_down(const uint8_t* __restrict__ down, u32x4* __rest
     const int U = kq_units(type), SB = kq_sb_bytes(type);
     const size_t T = d / RT;
     const size_t total = (size_t)ne * T * nsbf * U * RT;
+    uint16_t* dstream = (uint16_t*)(out + total);     // Q6_K: the fp16 d behind the units
     for (size_t idx = blockIdx.x * (size_t)blockDim.x + threadIdx.x; idx < total; idx += (size_t)gridDim.x * blockDim.x) {
         const int rr = idx % RT;
         size_t r1 = idx / RT;
         const int uu = r1 % U; r1 /= U;
+        const size_t sbi = r1;                        // (expert, tile, superblock)
         const int s = r1 % nsbf; r1 /= nsbf;
         const size_t t = r1 % T;
         const size_t e = r1 / T;
@@ -381,13 +381,17 @@ __global__ void k_repack_kq_down(const uint8_t* __restrict__ down, u32x4* __rest
         for (int k = 0; k < 4; k++)
             w[k] = b[4 * k] | (b[4 * k + 1] << 8) | (b[4 * k + 2] << 16) | ((uint32_t)b[4 * k + 3] << 24);
         out[idx] = u32x4{w[0], w[1], w[2], w[3]};
+        if (type == 14 && uu == 0) dstream[sbi * RT + rr] = (uint16_t)(src[208] | (src[209] << 8));
     }
 }
 
 size_t kq_gateup_bytes(int ne, int dff, int d) { return (size_t)ne * 2 * dff * (d / 256) * 144; }
 size_t kq_down_bytes(int ne, int d, int dff, int top_k, int down_type) {
     (void)top_k;
-    return (size_t)ne * d * (dff / 256) * kq_units(down_type) * 16;
+    return (size_t)ne * d * (dff / 256) * kq_sb_bytes(down_type);   // Q4_K 9 units; Q6_K 13 units + d
+}
+const uint16_t* kq_down_dstream(const u32x4* dn, int ne, int d, int dff, int down_type) {
+    return down_type == 14 ? (const uint16_t*)(dn + (size_t)ne * d * (dff / 256) * kQ6StreamUnits) : nullptr;
 }
 
 int launch_repack_kq_gateup(const uint8_t* gate, const uint8_t* up, u32x4* out, int ne, int dff, int d, hipStream_t s) {
