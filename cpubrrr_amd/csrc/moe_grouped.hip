@@ -421,7 +421,8 @@ CPB_DEV u32x4 wload(const WeightStream& ws, int q, int u) {
 // TRACE writes the int32 block sums S = D * 2^(128 - e) of valid rows.
 template <bool TRACE>
 CPB_DEV v16f grouped_parts(const WeightStream& ws, int P, unsigned char* smem, const uint8_t* img, const float* sc,
-                           size_t rows, int nbk, const int* src, int lane, int32_t* tb, bool trace_ok) {
+                           size_t rows, int nbk, const int* src, int lane, int32_t* tb, bool trace_ok,
+                           float* bias_lds, float bias_v) {
     const int ti = lane & 31, hb = lane >> 5;
     u32x4 wv[kUnits];
 #pragma unroll
@@ -497,6 +498,8 @@ CPB_DEV v16f grouped_parts(const WeightStream& ws, int P, unsigned char* smem, c
             sc_c = sc_n;
         }
     }
+    // the caller's bias, loaded at its start, into LDS for its epilogue
+    if (threadIdx.x < 256) bias_lds[threadIdx.x] = bias_v;
     __syncthreads();             // callers reuse the LDS
     return tot;
 }
@@ -518,6 +521,16 @@ __global__ __launch_bounds__(512) void k_gateup_grouped(GroupedArgs a) {
     const bool live = rt < T;
     if (threadIdx.x < 32) src[threadIdx.x] = (int)threadIdx.x < cnt ? a.sorted[start + threadIdx.x] / a.k : -1;
     __syncthreads();
+    // the biases of the workgroup's 4 x (32 gate + 32 up) rows, requested now
+    // and kept in one register until the epilogue (a load issued after the
+    // GEMM would wait a full loaded-memory latency)
+    __shared__ float bias_s[256];                   // [row tile][gate 32 | up 32]
+    float bias_v = 0.0f;
+    {
+        const int t = (int)threadIdx.x, rtb = grp * 4 + (t >> 6), gu = (t >> 5) & 1;
+        const float* bp = gu ? a.up_b : a.gate_b;
+        if (t < 256 && bp && rtb < T) bias_v = bp[(size_t)e * a.dff + rtb * 32 + (t & 31)];
+    }
     const int ti = lane & 31, hb = lane >> 5;
     const bool valid = ti < cnt;
     const int pair = valid ? a.sorted[start + ti] : 0;
@@ -532,42 +545,62 @@ __global__ __launch_bounds__(512) void k_gateup_grouped(GroupedArgs a) {
     int32_t* tb = TRACE ? a.gu_sums + (((size_t)pair * 2 + isup) * a.dff + rt * 32) * nb : nullptr;
 
     const v16f tot = grouped_parts<TRACE>(ws, P, smem, a.ximg, a.xsb, (size_t)a.n_tok, nb, src, lane, tb,
-                                          valid && live);
-    // up totals to the gate wave of the same row tile (LDS reused)
-    float* xch = (float*)smem;
-    if (isup) {
+                                          valid && live, bias_s, bias_v);
+    // SwiGLU, Q8 and image of the row tile, split over its two waves: the
+    // lane's rows 8g + 4hb + c (g, c < 4) of groups g = isup and g = isup + 2
+    // are this wave's (so each wave owns whole hq words and whole 8-byte image
+    // runs); each wave hands the partner the totals of the partner's rows
+    // (LDS reused), then the block maximum is combined through LDS.
+    const int rtl = w >> 1;
+    float* xch = (float*)smem;                    // [row tile][sender][8][64]
+    float* mxs = xch + 4 * 2 * 8 * 64;            // [row tile][wave][64]
 #pragma unroll
-        for (int r = 0; r < 16; r++) xch[((w >> 1) * 16 + r) * 64 + lane] = tot[r];
+    for (int j = 0; j < 8; j++) {
+        const int r = 4 * (1 - isup) + (j & 3) + 8 * (j >> 2);        // partner's j-th row
+        xch[((rtl * 2 + isup) * 8 + j) * 64 + lane] = tot[r];
     }
     __syncthreads();
-    if (isup || !live) return;
-    float hv[16], m = 0.0f;
+    float hv[8], m = 0.0f;
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-        const int row = rt * 32 + 8 * (r >> 2) + 4 * hb + (r & 3);
-        float vg = tot[r], vu = xch[((w >> 1) * 16 + r) * 64 + lane];
-        if (a.gate_b) vg += a.gate_b[(size_t)e * a.dff + row];
-        if (a.up_b) vu += a.up_b[(size_t)e * a.dff + row];
+    for (int j = 0; j < 8; j++) {
+        const int r = 4 * isup + (j & 3) + 8 * (j >> 2);                // this wave's j-th row
+        const int rr = 8 * (r >> 2) + 4 * hb + (r & 3);                 // row within the tile
+        const float own = tot[r], oth = xch[((rtl * 2 + 1 - isup) * 8 + j) * 64 + lane];
+        float vg = isup ? oth : own, vu = isup ? own : oth;
+        if (a.gate_b) vg += bias_s[rtl * 64 + rr];
+        if (a.up_b) vu += bias_s[rtl * 64 + 32 + rr];
         const float xg = fminf(vg, a.limit);                           // engine_gpt2.rs:887-906
         const float yu = fminf(fmaxf(vu, -a.limit), a.limit);
-        hv[r] = (xg / (1.0f + expf(-a.alpha * xg))) * (yu + 1.0f);
-        m = fmaxf(m, fabsf(hv[r]));
+        hv[j] = (xg / (1.0f + expf(-a.alpha * xg))) * (yu + 1.0f);
+        m = fmaxf(m, fabsf(hv[j]));
     }
     m = fmaxf(m, __shfl_xor(m, 32));
+    mxs[(rtl * 2 + isup) * 64 + lane] = m;
+    __syncthreads();
+    m = fmaxf(m, mxs[(rtl * 2 + 1 - isup) * 64 + lane]);
     const float sc = fmaxf(1e-12f, m) / 127.0f;
-    if (!valid) return;
+    if (!valid || !live) return;
+    // hq: the lane's groups g = isup, isup + 2 as 4-byte words; image: elements
+    // e and e + 16 sit at adjacent K (2e, 2e + 1), so groups g and g + 2 fill
+    // the 8 bytes K = 16 isup + 8hb .. +7 of each half
     uint8_t* img = a.himg + ((size_t)pair * a.nbf + rt) * kImg;
+    uint32_t qw[2] = {0u, 0u}, hi[2] = {0u, 0u}, lo[2] = {0u, 0u};
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-        const int el = 8 * (r >> 2) + 4 * hb + (r & 3);
-        const int qv = q8_round(hv[r], sc);
-        a.hq[(size_t)pair * a.dff + rt * 32 + el] = (int8_t)qv;
+    for (int j = 0; j < 8; j++) {
+        const int gh = j >> 2, c = j & 3;                               // g = isup + 2 gh
+        const int qv = q8_round(hv[j], sc);
+        qw[gh] |= ((uint32_t)qv & 0xffu) << (8 * c);
         const int h = qv >> 4;
-        const int o = img_hi_off(el);
-        img[o] = (uint8_t)e4m3_small(16 * h);
-        img[o + 16] = (uint8_t)e4m3_small(qv - 16 * h);
+        const int sh = 8 * (2 * (c & 1) + gh);                          // byte 2c + gh of the run
+        hi[c >> 1] |= e4m3_small(16 * h) << sh;
+        lo[c >> 1] |= e4m3_small(qv - 16 * h) << sh;
     }
-    if (hb == 0) a.hsb[(size_t)pair * a.nbf + rt] = sc;
+    uint32_t* hqw = (uint32_t*)(a.hq + (size_t)pair * a.dff + rt * 32 + 8 * isup + 4 * hb);
+    hqw[0] = qw[0];
+    hqw[4] = qw[1];
+    *(uint2*)(img + 32 * isup + 8 * hb) = make_uint2(hi[0], hi[1]);
+    *(uint2*)(img + 32 * isup + 8 * hb + 16) = make_uint2(lo[0], lo[1]);
+    if (hb == 0 && !isup) a.hsb[(size_t)pair * a.nbf + rt] = sc;
 }
 
 // ---- 6. grouped down (+ bias) into dnout ----
@@ -590,6 +623,12 @@ __global__ __launch_bounds__(512) void k_down_grouped(GroupedArgs a) {
     const bool valid = ti < cnt;
     const int pair = valid ? a.sorted[start + ti] : 0;
     const int row_l = rt * 32 + (lane & 31);                          // this lane's A row
+    // the biases of the workgroup's 8 x 32 rows, requested now (one register
+    // until the epilogue)
+    __shared__ float bias_s[256];
+    float bias_v = 0.0f;
+    if (threadIdx.x < 256 && a.down_b && grp * 256 + (int)threadIdx.x < a.d)
+        bias_v = a.down_b[(size_t)e * a.d + grp * 256 + threadIdx.x];
     WeightStream ws;
     {
         const size_t ex_units = (size_t)Tv * P * kUnits * RTv;      // one expert's down stream
@@ -601,7 +640,7 @@ __global__ __launch_bounds__(512) void k_down_grouped(GroupedArgs a) {
     int32_t* tb = TRACE ? a.dn_sums + ((size_t)pair * a.d + rt * 32) * nbf : nullptr;
 
     const v16f tot = grouped_parts<TRACE>(ws, P, smem, a.himg, a.hsb, (size_t)a.n_tok * a.k, nbf, src, lane,
-                                          tb, valid && live);
+                                          tb, valid && live, bias_s, bias_v);
     if (!valid || !live) return;
     float* out = a.dnout + (size_t)pair * a.d + rt * 32 + 4 * hb;
 #pragma unroll
@@ -611,7 +650,7 @@ __global__ __launch_bounds__(512) void k_down_grouped(GroupedArgs a) {
 #pragma unroll
         for (int c = 0; c < 4; c++) {
             const int row = rt * 32 + 8 * g + 4 * hb + c;
-            vp[c] = tot[4 * g + c] + (a.down_b ? a.down_b[(size_t)e * a.d + row] : 0.0f);
+            vp[c] = tot[4 * g + c] + (a.down_b ? bias_s[row - grp * 256] : 0.0f);
         }
         *(float4*)(out + 8 * g) = v;
     }
