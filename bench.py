@@ -38,7 +38,7 @@ sys.path.insert(0, str(ROOT))
 # WRITE_SIZE runs scaled by a 1 GiB copy; None where not yet measured.  The
 # bench cannot read hardware counters itself (they need a profiler run of
 # their own), so each line names the profile its figure comes from.
-MEASURED_TRAFFIC = {"k_gateup_mx": 35_815_144, "k_gateup_kq": 14_404_042,
+MEASURED_TRAFFIC = {"k_gateup_mx": 35_815_144, "k_gateup_kq": 14_418_124,
                     "k_gateup_grouped": 484_748_900, "head": 327_526_064}
 TRAFFIC_SOURCE = {"k_gateup_mx": "profiles/hbm_traffic_config1_phased.md",
                   "k_gateup_kq": "profiles/hbm_traffic_config3_qwen.md",
