@@ -164,6 +164,10 @@ CPB_DEV void st_dev(T* p, T v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HI
 CPB_DEV __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(const_cast<void*>(base)), (short)0, (int)uniform(bytes), 0x00020000);
 }
+// a * b for operands that fit in 24 signed bits (the k-quant block sums and
+// scales): the full-rate 24-bit multiply (v_mul_i32_i24) in place of the
+// quarter-rate 32-bit one; the 32-bit result is exact while |a * b| < 2^31
+CPB_DEV int mul24(int a, int b) { return __mul24(a, b); }
 constexpr uint32_t kOffNone = 0x80000000u;   // a buffer offset beyond every range
 // 16-byte load with the cache policy of ld_dev (sc1: coherent across XCDs)
 CPB_DEV u32x4 ld_dev16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {

@@ -108,15 +108,64 @@ __global__ __launch_bounds__(256) void k_prep_batch_kq(GroupedArgs a) {
     }
 }
 
+// ---- the token tile's activations in LDS (gate/up, d % 1024 == 0) ----
+// Q8_K bytes of token slot ti at ti * (d + 16) (the 16-byte pad spreads the
+// 32 slots' reads over the banks), then the per-32 sums at stride
+// kq_xsum_stride(d) ints, then the per-256 scales (nsb per slot).  Written
+// once per workgroup by direct global-to-LDS loads (no staging registers);
+// padding slots read zeros.
+CPB_DEV_HOST_INLINE int kq_xsum_stride(int d) { return (d / 32 > 64 ? d / 32 : 64) + 4; }
+CPB_DEV_HOST_INLINE size_t kq_stage_bytes(int d) {
+    return (size_t)32 * (d + 16) + (size_t)32 * kq_xsum_stride(d) * 4 + (size_t)32 * (d / 256) * 4;
+}
+// the staged gate/up: d a multiple of 1024 and two workgroups' LDS per CU
+CPB_DEV_HOST_INLINE bool kq_staged(int d) { return d % 1024 == 0 && kq_stage_bytes(d) <= 76 * 1024; }
+typedef __attribute__((address_space(3))) void lds_void_k;
+CPB_DEV void stage_tile_acts(const GroupedArgs& a, const int* src, unsigned char* st) {
+    const int d = a.d, nsb = d / 256, lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int XS = kq_xsum_stride(d);
+    const __amdgpu_buffer_rsrc_t rx = buf_rsrc(a.xq, (uint32_t)((size_t)a.n_tok * d));
+    const __amdgpu_buffer_rsrc_t rs = buf_rsrc(a.xsum, (uint32_t)((size_t)a.n_tok * (d / 32) * 4));
+    const __amdgpu_buffer_rsrc_t rb = buf_rsrc(a.xsb, (uint32_t)((size_t)a.n_tok * nsb * 4));
+    // Q8_K bytes: 1 KB pieces, d / 1024 per slot
+    const int per = d / 1024;
+    for (int i = w; i < 32 * per; i += nw) {
+        const int ti = i / per, h = i % per, pr = src[ti];
+        const uint32_t off = pr >= 0 ? (uint32_t)((size_t)(pr / a.k) * d + h * 1024 + lane * 16) : kOffNone;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void_k*)(st + (size_t)ti * (d + 16) + h * 1024), 16, off, 0, 0, 0);
+    }
+    // per-32 sums: 64 ints per load, lanes past d / 32 read zeros into the pad
+    unsigned char* xsl = st + (size_t)32 * (d + 16);
+    const int sper = (d / 32 + 63) / 64;
+    for (int i = w; i < 32 * sper; i += nw) {
+        const int ti = i / sper, h = i % sper, pr = src[ti], j = h * 64 + lane;
+        const uint32_t off = pr >= 0 && j < d / 32 ? (uint32_t)(((size_t)(pr / a.k) * (d / 32) + j) * 4) : kOffNone;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_k*)(xsl + ((size_t)ti * XS + h * 64) * 4), 4, off, 0, 0, 0);
+    }
+    // per-256 scales: slot ti's nsb values contiguous
+    unsigned char* xbl = xsl + (size_t)32 * XS * 4;
+    for (int i = w; i < (32 * nsb + 63) / 64; i += nw) {
+        const int g = i * 64 + lane, ti = g / nsb, sb = g % nsb;
+        const int pr = g < 32 * nsb ? src[ti] : -1;
+        const uint32_t off = pr >= 0 ? (uint32_t)(((size_t)(pr / a.k) * nsb + sb) * 4) : kOffNone;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void_k*)(xbl + (size_t)i * 256), 4, off, 0, 0, 0);
+    }
+}
+
 // ---- gate/up (+ SiLU * up) ----
 // one workgroup per (token tile, pair of 32-row tiles) (grouped_item); wave w
 // = row tile w / 2, gate (w even) or up (w odd).
-template <bool TRACE>
+// STAGED: the tile's activations are read from LDS (stage_tile_acts), else
+// from global memory per superblock.
+template <bool TRACE, bool STAGED>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_gateup_kq_grouped(GroupedArgs a) {
+    extern __shared__ __align__(16) unsigned char kst[];
     __shared__ int src[32];
     __shared__ uint8_t s_sm[4][32][16];          // per wave and row: sc[8], mn[8]
     __shared__ float s_dm[4][32][2];             // d, dmin
-    __shared__ float xch[2][16][64];             // up results to the gate waves
+    __shared__ float xch_s[STAGED ? 1 : 2 * 16 * 64];
+    // up results to the gate waves (the staging area once the products are done)
+    float (*xch)[16][64] = (float (*)[16][64])(STAGED ? (float*)kst : xch_s);
     const int T32 = a.dff / 32, T16 = a.dff / 16, nsb = a.d / 256;
     int tile, grp;
     if (!grouped_item(uniform(*a.ntiles), (T32 + 1) / 2, &tile, &grp)) return;
@@ -127,6 +176,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     const bool live = rt < T32;
     if (threadIdx.x < 32) src[threadIdx.x] = (int)threadIdx.x < cnt ? a.sorted[start + threadIdx.x] : -1;
     __syncthreads();
+    if constexpr (STAGED) stage_tile_acts(a, src, kst);
     const int r = lane & 31, hb = lane >> 5;
     const int pair = src[r], tok = pair >= 0 ? pair / a.k : -1;        // B column / D column of this lane
     // this lane's A row: stream tile 2 rt + r / 16, lane r % 16 (+16 for up)
@@ -144,6 +194,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
 #pragma unroll
         for (int jj = 0; jj < 4; jj++) nwq[jj] = wrow[(1 + 2 * jj + hb) * 32];
     }
+    const unsigned char* xl = kst + (size_t)r * (a.d + 16) + 16 * hb;
+    const int* xsl = (const int*)(kst + (size_t)32 * (a.d + 16)) + r * kq_xsum_stride(a.d);
+    const float* xbl = (const float*)(kst + (size_t)32 * (a.d + 16) + (size_t)32 * kq_xsum_stride(a.d) * 4) + r * nsb;
+    if constexpr (STAGED) __syncthreads();       // the tile's activations landed (the barrier waits for every load)
     for (int sb = 0; sb < nsb; sb++) {
         const u32x4 u0 = nu0;
         u32x4 wq[4];
@@ -156,12 +210,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
             for (int jj = 0; jj < 4; jj++) nwq[jj] = wp[(1 + 2 * jj + hb) * 32];
         }
         u32x4 xb[8];
+        int xs8[8];
+        float ys = 0.0f;
+        if constexpr (STAGED) {
+#pragma unroll
+            for (int j = 0; j < 8; j++) xb[j] = *(const u32x4*)(xl + sb * 256 + 32 * j);
+#pragma unroll
+            for (int j = 0; j < 8; j++) xs8[j] = xsl[sb * 8 + j];
+            ys = xbl[sb];
+        } else {
 #pragma unroll
         for (int j = 0; j < 8; j++)
             xb[j] = __builtin_amdgcn_raw_buffer_load_b128(
                 rx, tok >= 0 ? (uint32_t)((size_t)tok * a.d + sb * 256 + 32 * j + 16 * hb) : kOffNone, 0, 0);
-        int xs8[8];
-        float ys = 0.0f;
         if (tok >= 0) {
 #pragma unroll
             for (int j = 0; j < 8; j++) xs8[j] = a.xsum[(size_t)tok * (a.d / 32) + sb * 8 + j];
@@ -169,6 +230,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
         } else {
 #pragma unroll
             for (int j = 0; j < 8; j++) xs8[j] = 0;
+        }
         }
         if (hb == 0) {
             unpack_q4k(u0, &s_sm[w][r][0], &s_sm[w][r][8]);
@@ -188,7 +250,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
 #pragma unroll
             for (int i = 0; i < 16; i++) {
                 const int row = d_row(i, hb);
-                sumi[i] += D0[i] * (int)s_sm[w][row][2 * jj] + D1[i] * (int)s_sm[w][row][2 * jj + 1];
+                sumi[i] += mul24(D0[i], (int)s_sm[w][row][2 * jj]) + mul24(D1[i], (int)s_sm[w][row][2 * jj + 1]);
             }
         }
 #pragma unroll
@@ -196,7 +258,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
             const int row = d_row(i, hb);
             int mint = 0;
 #pragma unroll
-            for (int j = 0; j < 8; j++) mint += (int)s_sm[w][row][8 + j] * xs8[j];
+            for (int j = 0; j < 8; j++) mint += mul24((int)s_sm[w][row][8 + j], xs8[j]);
             const float dd = s_dm[w][row][0], dmin = s_dm[w][row][1];
             sumf[i] += ys * dd * (float)sumi[i] - ys * dmin * (float)mint;      // engine_qwen2.rs:110
             if (TRACE && pair >= 0 && live) {
@@ -209,6 +271,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
+    if constexpr (STAGED) __syncthreads();       // every wave is done with the staged activations
     if (isup) {
 #pragma unroll
         for (int i = 0; i < 16; i++) xch[w >> 1][i][lane] = sumf[i];
@@ -342,14 +405,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
 #pragma unroll
                 for (int i = 0; i < 16; i++) {
                     const int row = d_row(i, hb);
-                    acc[i] += D0[i] * (int)s_sm[w][row][2 * jj] + D1[i] * (int)s_sm[w][row][2 * jj + 1];
+                    acc[i] += mul24(D0[i], (int)s_sm[w][row][2 * jj]) + mul24(D1[i], (int)s_sm[w][row][2 * jj + 1]);
                 }
             }
 #pragma unroll
             for (int i = 0; i < 16; i++) {
                 const int row = d_row(i, hb);
 #pragma unroll
-                for (int j = 0; j < 8; j++) mint[i] += (int)s_sm[w][row][8 + j] * xs8[j];
+                for (int j = 0; j < 8; j++) mint[i] += mul24((int)s_sm[w][row][8 + j], xs8[j]);
             }
         } else {
             // ql[128] = units 0-7, qh[64] = units 8-11, int8 scales = unit 12, d from the d stream
@@ -385,7 +448,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
 #pragma unroll
                 for (int i = 0; i < 16; i++) {
                     const int row = d_row(i, hb);
-                    acc[i] += D0[i] * (int)(int8_t)s_sm[w][row][2 * m] + D1[i] * (int)(int8_t)s_sm[w][row][2 * m + 1];
+                    acc[i] += mul24(D0[i], (int)(int8_t)s_sm[w][row][2 * m]) + mul24(D1[i], (int)(int8_t)s_sm[w][row][2 * m + 1]);
                 }
             }
         }
@@ -425,8 +488,9 @@ int launch_kq_gemms(const GroupedArgs& a, bool trace, hipStream_t s, const Launc
     const dim3 ggu((ngu + 7) / 8 * 8), gdn((ndn + 7) / 8 * 8);
     const int np = a.n_tok * a.k, nq = np * (a.dff / 256);
     if (ev) armed_events() = ev[0];
-    if (trace) launch(k_gateup_kq_grouped<true>, ggu, dim3(256), 0, s, a);
-    else launch(k_gateup_kq_grouped<false>, ggu, dim3(256), 0, s, a);
+    if (trace) launch(k_gateup_kq_grouped<true, false>, ggu, dim3(256), 0, s, a);
+    else if (kq_staged(a.d)) launch(k_gateup_kq_grouped<false, true>, ggu, dim3(256), kq_stage_bytes(a.d), s, a);
+    else launch(k_gateup_kq_grouped<false, false>, ggu, dim3(256), 0, s, a);
     launch(k_quant_h_batch, dim3((nq + 3) / 4), dim3(256), 0, s, a);
     if (ev) armed_events() = ev[1];
     if (a.down_type == 12) {

@@ -69,11 +69,11 @@ CPB_DEV float q4k_term(const u32x4 (&u)[kQ4Units], const int8_t* xs, const int32
             s0 = sdot4(w[i] & 0x0F0F0F0Fu, xa[i], s0);
             s1 = sdot4((w[i] >> 4) & 0x0F0F0F0Fu, xb[i], s1);
         }
-        sumi += s0 * sc[2 * jj] + s1 * sc[2 * jj + 1];
+        sumi += mul24(s0, sc[2 * jj]) + mul24(s1, sc[2 * jj + 1]);
     }
     int mint = 0;
 #pragma unroll
-    for (int j = 0; j < 8; j++) mint += mn[j] * xsum8[j];
+    for (int j = 0; j < 8; j++) mint += mul24(mn[j], xsum8[j]);
     if (TRACE) { sums[0] = sumi; sums[1] = mint; }
     return ys * d * (float)sumi - ys * dmin * (float)mint;
 }
@@ -113,7 +113,7 @@ CPB_DEV float q6k_term(const u32x4 (&u)[kQ6Units], const int8_t* xs, const int32
 #pragma unroll
     for (int g = 0; g < 16; g++) {
         const int sc = (int)(int8_t)(scw[g / 4] >> (8 * (g % 4)));
-        acc += (s[g] - 32 * xs16[g]) * sc;
+        acc += mul24(s[g] - 32 * xs16[g], sc);
     }
     if (TRACE) sums[0] = acc;
     return ys * d * (float)acc;
