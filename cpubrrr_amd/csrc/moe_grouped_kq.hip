@@ -47,6 +47,13 @@ CPB_DEV v16i_k mfma_i8(const u32x4& a, const u32x4& b) {
     const v16i_k Z = {};
     return __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, Z, 0, 0, 0);
 }
+// 32 x 32 x 16 int8 product: lanes 0-31 hold K 0-7 of their row / column,
+// lanes 32-63 K 8-15
+CPB_DEV v16i_k mfma_i8_k16(uint2 a, uint2 b) {
+    const long A = (long)(((uint64_t)a.y << 32) | a.x), B = (long)(((uint64_t)b.y << 32) | b.x);
+    const v16i_k Z = {};
+    return __builtin_amdgcn_mfma_i32_32x32x16_i8(A, B, Z, 0, 0, 0);
+}
 CPB_DEV u32x4 and4(const u32x4& v, uint32_t m) { return u32x4{v[0] & m, v[1] & m, v[2] & m, v[3] & m}; }
 CPB_DEV u32x4 shr4(const u32x4& v, int s) { return u32x4{v[0] >> s, v[1] >> s, v[2] >> s, v[3] >> s}; }
 // row of D register i for lane half hb
@@ -253,12 +260,28 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
                 sumi[i] += mul24(D0[i], (int)s_sm[w][row][2 * jj]) + mul24(D1[i], (int)s_sm[w][row][2 * jj + 1]);
             }
         }
+        // mint = sum_j mn[row][j] * xs8[tok][j] on the matrix cores: xs8 =
+        // 64 bh + bl with bl in [0, 63] and bh in [-64, 63] (|xs8| < 2^12) both
+        // int8; lanes 0-31 carry (mn, bl) in K 0-7 of the first product and
+        // lanes 32-63 (mn, bh) in K 8-15 of the second (the other half's A
+        // zero), so mint = M1 + 64 M2 exactly
+        v16i_k M1, M2;
+        {
+            const uint2 mn = *(const uint2*)&s_sm[w][r][8];
+            uint32_t bw[2] = {0u, 0u};
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const uint32_t v = (uint32_t)(hb ? (xs8[j] >> 6) : (xs8[j] & 63)) & 0xffu;
+                bw[j >> 2] |= v << (8 * (j & 3));
+            }
+            const uint2 zero = {0u, 0u}, B = {bw[0], bw[1]};
+            M1 = mfma_i8_k16(hb ? zero : mn, B);
+            M2 = mfma_i8_k16(hb ? mn : zero, B);
+        }
 #pragma unroll
         for (int i = 0; i < 16; i++) {
             const int row = d_row(i, hb);
-            int mint = 0;
-#pragma unroll
-            for (int j = 0; j < 8; j++) mint += mul24((int)s_sm[w][row][8 + j], xs8[j]);
+            const int mint = M1[i] + 64 * M2[i];
             const float dd = s_dm[w][row][0], dmin = s_dm[w][row][1];
             sumf[i] += ys * dd * (float)sumi[i] - ys * dmin * (float)mint;      // engine_qwen2.rs:110
             if (TRACE && pair >= 0 && live) {
