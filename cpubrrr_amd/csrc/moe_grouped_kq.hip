@@ -54,6 +54,15 @@ CPB_DEV v16i_k mfma_i8_k16(uint2 a, uint2 b) {
     const v16i_k Z = {};
     return __builtin_amdgcn_mfma_i32_32x32x16_i8(A, B, Z, 0, 0, 0);
 }
+// Two 16-element groups held one per lane half (lanes 0-31 group G0 as
+// dwords 0-3, lanes 32-63 group G1) into the 32 x 32 x 16 operand layout:
+// dwords 0-1 become G0 (lanes 0-31 its elements 0-7, lanes 32-63 its 8-15),
+// dwords 2-3 G1 likewise (v_permlane32_swap of dwords 0/2 and 1/3)
+CPB_DEV void groups_to_k16(u32x4& v) {
+    const auto s0 = __builtin_amdgcn_permlane32_swap(v[0], v[2], false, false);
+    const auto s1 = __builtin_amdgcn_permlane32_swap(v[1], v[3], false, false);
+    v[0] = s0[0]; v[2] = s0[1]; v[1] = s1[0]; v[3] = s1[1];
+}
 CPB_DEV u32x4 and4(const u32x4& v, uint32_t m) { return u32x4{v[0] & m, v[1] & m, v[2] & m, v[3] & m}; }
 CPB_DEV u32x4 shr4(const u32x4& v, int s) { return u32x4{v[0] >> s, v[1] >> s, v[2] >> s, v[3] >> s}; }
 // row of D register i for lane half hb
@@ -115,38 +124,42 @@ __global__ __launch_bounds__(256) void k_prep_batch_kq(GroupedArgs a) {
     }
 }
 
-// ---- the token tile's activations in LDS (gate/up, d % 1024 == 0) ----
-// Q8_K bytes of token slot ti at ti * (d + 16) (the 16-byte pad spreads the
-// 32 slots' reads over the banks), then the per-32 sums at stride
-// kq_xsum_stride(d) ints, then the per-256 scales (nsb per slot).  Written
-// once per workgroup by direct global-to-LDS loads (no staging registers);
-// padding slots read zeros.
-CPB_DEV_HOST_INLINE int kq_xsum_stride(int d) { return (d / 32 > 64 ? d / 32 : 64) + 4; }
-CPB_DEV_HOST_INLINE size_t kq_stage_bytes(int d) {
-    return (size_t)32 * (d + 16) + (size_t)32 * kq_xsum_stride(d) * 4 + (size_t)32 * (d / 256) * 4;
+// ---- a token tile's activations in LDS ----
+// For K-element rows (gate/up: the tokens' Q8_K x, K = d; down: the pairs'
+// Q8_K h, K = d_ff): slot ti's bytes at ti * kq_row_stride(K) (whole 1 KB
+// pieces plus 16 bytes, which spreads the 32 slots' reads over the banks),
+// then the per-32 sums at stride kq_sum_stride(K) ints, then the per-256
+// scales (K / 256 per slot).  Written once per workgroup by direct
+// global-to-LDS loads (no staging registers); padding slots read zeros.
+CPB_DEV_HOST_INLINE int kq_row_stride(int K) { return (K + 1023) / 1024 * 1024 + 16; }
+CPB_DEV_HOST_INLINE int kq_sum_stride(int K) { return (K / 32 > 64 ? (K / 32 + 63) / 64 * 64 : 64) + 4; }
+CPB_DEV_HOST_INLINE size_t kq_stage_bytes(int K) {
+    return (size_t)32 * kq_row_stride(K) + (size_t)32 * kq_sum_stride(K) * 4 + (size_t)32 * (K / 256) * 4;
 }
-// the staged gate/up: d a multiple of 1024 and two workgroups' LDS per CU
-CPB_DEV_HOST_INLINE bool kq_staged(int d) { return d % 1024 == 0 && kq_stage_bytes(d) <= 76 * 1024; }
+// staged when two workgroups' LDS still fit a CU
+CPB_DEV_HOST_INLINE bool kq_staged(int K) { return kq_stage_bytes(K) <= 76 * 1024; }
 typedef __attribute__((address_space(3))) void lds_void_k;
-CPB_DEV void stage_tile_acts(const GroupedArgs& a, const int* src, unsigned char* st) {
-    const int d = a.d, nsb = d / 256, lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    const int XS = kq_xsum_stride(d);
-    const __amdgpu_buffer_rsrc_t rx = buf_rsrc(a.xq, (uint32_t)((size_t)a.n_tok * d));
-    const __amdgpu_buffer_rsrc_t rs = buf_rsrc(a.xsum, (uint32_t)((size_t)a.n_tok * (d / 32) * 4));
-    const __amdgpu_buffer_rsrc_t rb = buf_rsrc(a.xsb, (uint32_t)((size_t)a.n_tok * nsb * 4));
-    // Q8_K bytes: 1 KB pieces, d / 1024 per slot
-    const int per = d / 1024;
+// row of slot ti = src[ti] / div (-1: padding); rows_total bounds the buffers
+CPB_DEV void stage_tile_acts(const int8_t* q, const int32_t* sums, const float* scales, int K, int div,
+                             size_t rows_total, const int* src, unsigned char* st) {
+    const int nsb = K / 256, lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int RS = kq_row_stride(K), XS = kq_sum_stride(K);
+    const __amdgpu_buffer_rsrc_t rx = buf_rsrc(q, (uint32_t)(rows_total * K));
+    const __amdgpu_buffer_rsrc_t rs = buf_rsrc(sums, (uint32_t)(rows_total * (K / 32) * 4));
+    const __amdgpu_buffer_rsrc_t rb = buf_rsrc(scales, (uint32_t)(rows_total * nsb * 4));
+    // bytes: 1 KB pieces, lanes past the row's end read zeros into the pad
+    const int per = (K + 1023) / 1024;
     for (int i = w; i < 32 * per; i += nw) {
-        const int ti = i / per, h = i % per, pr = src[ti];
-        const uint32_t off = pr >= 0 ? (uint32_t)((size_t)(pr / a.k) * d + h * 1024 + lane * 16) : kOffNone;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void_k*)(st + (size_t)ti * (d + 16) + h * 1024), 16, off, 0, 0, 0);
+        const int ti = i / per, h = i % per, pr = src[ti], c = h * 1024 + lane * 16;
+        const uint32_t off = pr >= 0 && c < K ? (uint32_t)((size_t)(pr / div) * K + c) : kOffNone;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void_k*)(st + (size_t)ti * RS + h * 1024), 16, off, 0, 0, 0);
     }
-    // per-32 sums: 64 ints per load, lanes past d / 32 read zeros into the pad
-    unsigned char* xsl = st + (size_t)32 * (d + 16);
-    const int sper = (d / 32 + 63) / 64;
+    // per-32 sums: 64 ints per load
+    unsigned char* xsl = st + (size_t)32 * RS;
+    const int sper = (K / 32 + 63) / 64;
     for (int i = w; i < 32 * sper; i += nw) {
         const int ti = i / sper, h = i % sper, pr = src[ti], j = h * 64 + lane;
-        const uint32_t off = pr >= 0 && j < d / 32 ? (uint32_t)(((size_t)(pr / a.k) * (d / 32) + j) * 4) : kOffNone;
+        const uint32_t off = pr >= 0 && j < K / 32 ? (uint32_t)(((size_t)(pr / div) * (K / 32) + j) * 4) : kOffNone;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_k*)(xsl + ((size_t)ti * XS + h * 64) * 4), 4, off, 0, 0, 0);
     }
     // per-256 scales: slot ti's nsb values contiguous
@@ -154,7 +167,7 @@ CPB_DEV void stage_tile_acts(const GroupedArgs& a, const int* src, unsigned char
     for (int i = w; i < (32 * nsb + 63) / 64; i += nw) {
         const int g = i * 64 + lane, ti = g / nsb, sb = g % nsb;
         const int pr = g < 32 * nsb ? src[ti] : -1;
-        const uint32_t off = pr >= 0 ? (uint32_t)(((size_t)(pr / a.k) * nsb + sb) * 4) : kOffNone;
+        const uint32_t off = pr >= 0 ? (uint32_t)(((size_t)(pr / div) * nsb + sb) * 4) : kOffNone;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void_k*)(xbl + (size_t)i * 256), 4, off, 0, 0, 0);
     }
 }
@@ -183,7 +196,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     const bool live = rt < T32;
     if (threadIdx.x < 32) src[threadIdx.x] = (int)threadIdx.x < cnt ? a.sorted[start + threadIdx.x] : -1;
     __syncthreads();
-    if constexpr (STAGED) stage_tile_acts(a, src, kst);
+    if constexpr (STAGED) stage_tile_acts(a.xq, a.xsum, a.xsb, a.d, a.k, (size_t)a.n_tok, src, kst);
     const int r = lane & 31, hb = lane >> 5;
     const int pair = src[r], tok = pair >= 0 ? pair / a.k : -1;        // B column / D column of this lane
     // this lane's A row: stream tile 2 rt + r / 16, lane r % 16 (+16 for up)
@@ -201,9 +214,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
 #pragma unroll
         for (int jj = 0; jj < 4; jj++) nwq[jj] = wrow[(1 + 2 * jj + hb) * 32];
     }
-    const unsigned char* xl = kst + (size_t)r * (a.d + 16) + 16 * hb;
-    const int* xsl = (const int*)(kst + (size_t)32 * (a.d + 16)) + r * kq_xsum_stride(a.d);
-    const float* xbl = (const float*)(kst + (size_t)32 * (a.d + 16) + (size_t)32 * kq_xsum_stride(a.d) * 4) + r * nsb;
+    const unsigned char* xl = kst + (size_t)r * kq_row_stride(a.d) + 16 * hb;
+    const int* xsl = (const int*)(kst + (size_t)32 * kq_row_stride(a.d)) + r * kq_sum_stride(a.d);
+    const float* xbl = (const float*)(kst + (size_t)32 * kq_row_stride(a.d) + (size_t)32 * kq_sum_stride(a.d) * 4) + r * nsb;
     if constexpr (STAGED) __syncthreads();       // the tile's activations landed (the barrier waits for every load)
     for (int sb = 0; sb < nsb; sb++) {
         const u32x4 u0 = nu0;
@@ -340,9 +353,12 @@ CPB_DEV uint32_t q6_minus32(uint32_t v) {
 // ---- down (Q4_K or Q6_K) into dnout ----
 // one workgroup per (token tile, group of 4 row tiles of 32 rows); wave w =
 // row tile w.
-template <int TYPE, bool TRACE>
+// STAGED: the tile's Q8_K h is read from LDS (stage_tile_acts), else from
+// global memory per superblock.
+template <int TYPE, bool TRACE, bool STAGED>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_down_kq_grouped(GroupedArgs a) {
     constexpr int U = TYPE == 12 ? kQ4Units : kQ6StreamUnits;   // units per superblock in the stream
+    extern __shared__ __align__(16) unsigned char kst[];
     __shared__ int src[32];
     __shared__ uint8_t s_sm[4][32][16];          // Q4_K: sc[8], mn[8]; Q6_K: int8 scales[16]
     __shared__ float s_dm[4][32][2];
@@ -356,6 +372,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     const bool live = rt < T32;
     if (threadIdx.x < 32) src[threadIdx.x] = (int)threadIdx.x < cnt ? a.sorted[start + threadIdx.x] : -1;
     __syncthreads();
+    if constexpr (STAGED)
+        stage_tile_acts(a.hq, a.hsum, a.hsb, a.dff, 1, (size_t)a.n_tok * a.k, src, kst);
     const int r = lane & 31, hb = lane >> 5;
     const int pair = src[r];
     const int R = (live ? rt : 0) * 32 + r;                   // this lane's A row
@@ -390,13 +408,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     u32x4 nwu[7];
     uint32_t ndu;
     wload(0, nwu, ndu);
+    const unsigned char* hl = kst + (size_t)r * kq_row_stride(a.dff) + 16 * hb;
+    const int* hsl = (const int*)(kst + (size_t)32 * kq_row_stride(a.dff)) + r * kq_sum_stride(a.dff);
+    const float* hbl =
+        (const float*)(kst + (size_t)32 * kq_row_stride(a.dff) + (size_t)32 * kq_sum_stride(a.dff) * 4) + r * nsbf;
+    if constexpr (STAGED) __syncthreads();       // the tile's h landed (the barrier waits for every load)
     for (int sb = 0; sb < nsbf; sb++) {
         u32x4 wu[7];
 #pragma unroll
         for (int k = 0; k < 7; k++) wu[k] = nwu[k];
         const uint32_t du = ndu;
         if (sb + 1 < nsbf) wload(sb + 1, nwu, ndu);
-        const float ys = pair >= 0 ? a.hsb[(size_t)pair * nsbf + sb] : 0.0f;
+        const float ys = STAGED ? hbl[sb] : pair >= 0 ? a.hsb[(size_t)pair * nsbf + sb] : 0.0f;
         int acc[16], mint[16];
 #pragma unroll
         for (int i = 0; i < 16; i++) acc[i] = mint[i] = 0;
@@ -406,13 +429,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
 #pragma unroll
             for (int jj = 0; jj < 4; jj++) wq[jj] = wu[1 + jj];
             u32x4 xb[8];
+            int xs8[8];
+            if constexpr (STAGED) {
+#pragma unroll
+                for (int j = 0; j < 8; j++) xb[j] = *(const u32x4*)(hl + sb * 256 + 32 * j);
+#pragma unroll
+                for (int j = 0; j < 8; j++) xs8[j] = hsl[sb * 8 + j];
+            } else {
 #pragma unroll
             for (int j = 0; j < 8; j++)
                 xb[j] = __builtin_amdgcn_raw_buffer_load_b128(
                     rh, pair >= 0 ? (uint32_t)((size_t)pair * a.dff + sb * 256 + 32 * j + 16 * hb) : kOffNone, 0, 0);
-            int xs8[8];
 #pragma unroll
             for (int j = 0; j < 8; j++) xs8[j] = pair >= 0 ? a.hsum[(size_t)pair * (a.dff / 32) + sb * 8 + j] : 0;
+            }
             if (hb == 0) {
                 unpack_q4k(u0, &s_sm[w][r][0], &s_sm[w][r][8]);
                 s_dm[w][r][0] = half_bits(u0[0] & 0xffffu);
@@ -448,13 +478,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            const u32x4 z = {0, 0, 0, 0};
             // the superblock's activations, all eight requests in flight at once
             u32x4 xvs[8];
 #pragma unroll
             for (int m = 0; m < 8; m++)
-                xvs[m] = __builtin_amdgcn_raw_buffer_load_b128(
-                    rh, pair >= 0 ? (uint32_t)((size_t)pair * a.dff + sb * 256 + 32 * m + 16 * hb) : kOffNone, 0, 0);
+                xvs[m] = STAGED ? *(const u32x4*)(hl + sb * 256 + 32 * m)
+                                : __builtin_amdgcn_raw_buffer_load_b128(
+                                      rh, pair >= 0 ? (uint32_t)((size_t)pair * a.dff + sb * 256 + 32 * m + 16 * hb) : kOffNone, 0, 0);
 #pragma unroll
             for (int m = 0; m < 8; m++) {
                 // elements 32 m .. 32 m + 31 (engine_qwen2.rs:171-190): 128-half h6, quarter p
@@ -464,10 +494,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
                 u32x4 A;
 #pragma unroll
                 for (int c = 0; c < 4; c++) A[c] = q6_minus32((lq[c] & 0x0F0F0F0Fu) | ((hq2[c] & 0x03030303u) << 4));
-                const u32x4 xv = xvs[m];
-                // group 2m in the first K half, 2m + 1 in the second
-                const v16i_k D0 = mfma_i8(A, hb == 0 ? xv : z);
-                const v16i_k D1 = mfma_i8(A, hb == 1 ? xv : z);
+                u32x4 xv = xvs[m];
+                // lane half hb holds group 2m + hb (weights and activations):
+                // one 32 x 32 x 16 product per group
+                groups_to_k16(A);
+                groups_to_k16(xv);
+                const v16i_k D0 = mfma_i8_k16(uint2{A[0], A[1]}, uint2{xv[0], xv[1]});
+                const v16i_k D1 = mfma_i8_k16(uint2{A[2], A[3]}, uint2{xv[2], xv[3]});
 #pragma unroll
                 for (int i = 0; i < 16; i++) {
                     const int row = d_row(i, hb);
@@ -516,12 +549,16 @@ int launch_kq_gemms(const GroupedArgs& a, bool trace, hipStream_t s, const Launc
     else launch(k_gateup_kq_grouped<false, false>, ggu, dim3(256), 0, s, a);
     launch(k_quant_h_batch, dim3((nq + 3) / 4), dim3(256), 0, s, a);
     if (ev) armed_events() = ev[1];
+    const bool sd = kq_staged(a.dff);
+    const size_t ldn = sd ? kq_stage_bytes(a.dff) : 0;
     if (a.down_type == 12) {
-        if (trace) launch(k_down_kq_grouped<12, true>, gdn, dim3(256), 0, s, a);
-        else launch(k_down_kq_grouped<12, false>, gdn, dim3(256), 0, s, a);
+        if (trace) launch(k_down_kq_grouped<12, true, false>, gdn, dim3(256), 0, s, a);
+        else if (sd) launch(k_down_kq_grouped<12, false, true>, gdn, dim3(256), ldn, s, a);
+        else launch(k_down_kq_grouped<12, false, false>, gdn, dim3(256), 0, s, a);
     } else {
-        if (trace) launch(k_down_kq_grouped<14, true>, gdn, dim3(256), 0, s, a);
-        else launch(k_down_kq_grouped<14, false>, gdn, dim3(256), 0, s, a);
+        if (trace) launch(k_down_kq_grouped<14, true, false>, gdn, dim3(256), 0, s, a);
+        else if (sd) launch(k_down_kq_grouped<14, false, true>, gdn, dim3(256), ldn, s, a);
+        else launch(k_down_kq_grouped<14, false, false>, gdn, dim3(256), 0, s, a);
     }
     return hipGetLastError() == hipSuccess ? 0 : -19;
 }
