@@ -22,7 +22,7 @@ extern "C" {
 #endif
 
 typedef struct cpb_head_cfg {
-    int   d;          /* n_embd (multiple of 32, <= 8192)                         */
+    int   d;          /* n_embd (multiple of 32, <= 4096)                         */
     int   n_vocab;    /* rows of output.weight (multiple of 4)                    */
     int   n_slices;   /* screening workers NT (reference default 12; 1..32)       */
     int   n_cand;     /* rows kept per worker CAND (reference 8; 1..16)           */
