@@ -105,7 +105,7 @@ __global__ __launch_bounds__(256) void k_router_batch(GroupedArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     const int e = blockIdx.x, d = a.d, tid = threadIdx.x, nw = blockDim.x >> 6;
     const int lane = tid & 63, ws = tid >> 6;
-    double* dred = (double*)smem;              // [64]
+    double* dreds = (double*)smem;             // [kRouteTok][64]: each token's wave partials
     const int j0 = tid * kRouteC;
     const bool act = j0 < d;
     const uint32_t off = act ? (uint32_t)j0 * 4 : kOffNone;
@@ -126,6 +126,7 @@ __global__ __launch_bounds__(256) void k_router_batch(GroupedArgs a) {
         const int t = blockIdx.y * kRouteTok + tt;
         if (t >= a.n_tok) break;
         const __amdgpu_buffer_rsrc_t rx = buf_rsrc(a.x + (size_t)t * d, (uint32_t)d * 4);
+        double* dred = dreds + tt * 64;
         double P[16];
         double loc = 0.0, absp = 0.0;
 #pragma unroll
@@ -148,10 +149,12 @@ __global__ __launch_bounds__(256) void k_router_batch(GroupedArgs a) {
         const double s1 = wave_total63_f64(act ? sabs : 0.0);
         const double s2 = wave_total63_f64(absp);
         if (lane == 63) { dred[16 + ws] = s1; dred[32 + ws] = s2; }
-        __syncthreads();
-        if (tid == 0) logit_final(dred, nw, d, b, a.inv[t], a.lstar + (size_t)t * a.ne + e, a.lbound + (size_t)t * a.ne + e);
-        __syncthreads();
     }
+    // one barrier, then the tokens' logits and bounds side by side (thread tt)
+    __syncthreads();
+    const int t = blockIdx.y * kRouteTok + tid;
+    if (tid < kRouteTok && t < a.n_tok)
+        logit_final(dreds + tid * 64, nw, d, b, a.inv[t], a.lstar + (size_t)t * a.ne + e, a.lbound + (size_t)t * a.ne + e);
 }
 
 // ---- 3. top-k + softmax, one wavefront per token (the decode kernels'
@@ -696,7 +699,7 @@ int launch_grouped_layer(const GroupedArgs& a, bool trace, hipStream_t s, const 
     }
     // one thread per kRouteC elements, whole waves (the decode route's element waves)
     launch(k_router_batch, dim3(a.ne, (nt + kRouteTok - 1) / kRouteTok), dim3((a.d / kRouteC + 63) / 64 * 64),
-           sizeof(double) * 64, s, a);
+           sizeof(double) * 64 * kRouteTok, s, a);
     launch(k_select_batch, dim3(nt), dim3(64), select_lds_bytes(a.ne, a.d, kExactGroupWide), s, a);
     if ((size_t)a.n_tok * a.ne <= kGroupDenseMax)
         launch(k_group_dense, dim3(1), dim3(1024), group_dense_lds(a.n_tok, a.ne), s, a);
