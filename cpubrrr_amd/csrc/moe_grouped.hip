@@ -298,8 +298,18 @@ __global__ __launch_bounds__(1024) void k_group_dense(GroupedArgs a) {
     const int P = 1024 / ne, e = tid % ne, part = tid / ne;
     const bool act = part < P;
     const int tpp = (nt + P - 1) / P, t0 = act ? part * tpp : 0, t1 = act ? min(nt, t0 + tpp) : 0;
+    // the run's bytes eight at a time: every read of a group issued before
+    // any is used (one at a time, each read's latency was paid in turn)
     int c = 0;
-    for (int t = t0; t < t1; t++) c += M[(size_t)t * ne + e] != 0;
+    int t = t0;
+    for (; t + 8 <= t1; t += 8) {
+        uint8_t v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = M[(size_t)(t + u) * ne + e];
+#pragma unroll
+        for (int u = 0; u < 8; u++) c += v[u] != 0;
+    }
+    for (; t < t1; t++) c += M[(size_t)t * ne + e] != 0;
     if (act) cnt[part * ne + e] = c;
     __syncthreads();
     // per expert: total, exclusive prefix over experts (counts and 32-pair tiles)
@@ -327,7 +337,16 @@ __global__ __launch_bounds__(1024) void k_group_dense(GroupedArgs a) {
     if (act) {
         int r = off_l[e];
         for (int v = 0; v < part; v++) r += cnt[v * ne + e];
-        for (int t = t0; t < t1; t++) {
+        int t = t0;
+        for (; t + 8 <= t1; t += 8) {
+            uint8_t v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) v[u] = M[(size_t)(t + u) * ne + e];
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                if (v[u]) a.sorted[r++] = (t + u) * k + v[u] - 1;
+        }
+        for (; t < t1; t++) {
             const int sl = M[(size_t)t * ne + e];
             if (sl) a.sorted[r++] = t * k + sl - 1;
         }
