@@ -48,7 +48,6 @@ typedef int v8i_g __attribute__((ext_vector_type(8)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
 constexpr int kImg = 64;          // image bytes per 32-block
-constexpr int kRouteTok = 4;      // tokens per router workgroup
 
 // exact e4m3 encodings used by the split (v = 0, an integer in [1, 15] or 16*h)
 CPB_DEV uint32_t e4m3_small(int v) {
@@ -92,73 +91,93 @@ __global__ __launch_bounds__(256) void k_prep_batch(GroupedArgs a) {
     }
 }
 
-// ---- 2. router logits + bounds, workgroup = (expert, kRouteTok tokens) ----
-// The decode route's computation (logit_phase1/2/final, 16 elements per
-// thread, element wave w = elements 1024w ..), so every token's logits are
-// those of per-token decode bit for bit.  The products are formed as
-// (W_j g_j) x_j with W_j g_j in fp64 once per workgroup: W_j g_j and x_j g_j
-// are exact in fp64 (24-bit significands), so both orders give the exact
-// triple product rounded once, logit_phase1's W_j (x_j g_j) bit for bit.
-// Threads past d load zeros (their products are 0) and zero their prefix
-// term once, where logit_phase2 selects per element.
-__global__ __launch_bounds__(256) void k_router_batch(GroupedArgs a) {
-    extern __shared__ __align__(16) unsigned char smem[];
-    const int e = blockIdx.x, d = a.d, tid = threadIdx.x, nw = blockDim.x >> 6;
-    const int lane = tid & 63, ws = tid >> 6;
-    double* dreds = (double*)smem;             // [kRouteTok][64]: each token's wave partials
-    const int j0 = tid * kRouteC;
-    const bool act = j0 < d;
-    const uint32_t off = act ? (uint32_t)j0 * 4 : kOffNone;
-    const __amdgpu_buffer_rsrc_t rW = buf_rsrc(a.router_w + (size_t)e * d, (uint32_t)d * 4);
-    const bool use_g = a.norm_w && a.apply_norm;
-    const __amdgpu_buffer_rsrc_t rg = buf_rsrc(a.norm_w, use_g ? (uint32_t)d * 4 : 0u);
-    double wg[16];
+// ---- 2. router logits, exactly: workgroup = (8 experts, 8 tokens) ----
+// Every (token, expert) logit as the reference computes it
+// (engine_gpt2.rs:849-852, engine_qwen2.rs:395-400): acc = b; acc += W[j] *
+// xn[j] for j = 0 .. d-1, fp32, each product and each sum rounded once, in
+// order.  A chain cannot be split, but a batch has n_tok * ne of them: lane
+// (tl, el) of the wave runs the chain of token 8 ty + tl and expert 8 ex + el,
+// the products one step ahead of the adds.  The 8 tokens' xn and the 8
+// experts' router rows stream through LDS in chunks of kChainChunk (the next
+// chunk requested into registers while the current one is summed).  The
+// logit goes to lstar with a zero lbound: the selection then ranks exact
+// values and never needs its exact path, and the weights are the softmax of
+// the reference's own fp32 logits.
+constexpr int kChainChunk = 128;
+constexpr int kChainStride = kChainChunk + 4;     // floats per LDS row (spreads the 8 rows over the banks)
+__global__ __launch_bounds__(64) void k_router_exact(GroupedArgs a) {
+    __shared__ __align__(16) float xs[2][8][kChainStride];
+    __shared__ __align__(16) float wsh[2][8][kChainStride];
+    const int lane = threadIdx.x, d = a.d;
+    const int tl = lane >> 3, el = lane & 7;
+    const int t = blockIdx.y * 8 + tl, e = blockIdx.x * 8 + el;
+    // staging: lane moves 16-byte pieces c = lane + 64 i (i < 4) of the
+    // 8 x 128-float chunk: row c / 32, floats 4 (c % 32) ..
+    const int nt = a.n_tok, ne = a.ne;
+    const __amdgpu_buffer_rsrc_t rx = buf_rsrc(a.xn, (uint32_t)((size_t)nt * d * 4));
+    const __amdgpu_buffer_rsrc_t rw = buf_rsrc(a.router_w, (uint32_t)((size_t)ne * d * 4));
+    auto fetch = [&](int j0, u32x4 (&xr)[4], u32x4 (&wr)[4]) {
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const u32x4 w4 = __builtin_amdgcn_raw_buffer_load_b128(rW, off + 16 * k, 0, 0);
-        const u32x4 g4 = __builtin_amdgcn_raw_buffer_load_b128(rg, off + 16 * k, 0, 0);
+        for (int i = 0; i < 4; i++) {
+            const int c = lane + 64 * i, row = c >> 5, j = j0 + 4 * (c & 31);
+            const int tt = blockIdx.y * 8 + row, ee = blockIdx.x * 8 + row;
+            xr[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, tt < nt && j < d ? (uint32_t)(((size_t)tt * d + j) * 4) : kOffNone, 0, 0);
+            wr[i] = __builtin_amdgcn_raw_buffer_load_b128(rw, ee < ne && j < d ? (uint32_t)(((size_t)ee * d + j) * 4) : kOffNone, 0, 0);
+        }
+    };
+    auto put = [&](int buf, const u32x4 (&xr)[4], const u32x4 (&wr)[4]) {
 #pragma unroll
-        for (int c = 0; c < 4; c++)
-            wg[4 * k + c] = (double)__uint_as_float(w4[c]) * (use_g ? (double)__uint_as_float(g4[c]) : 1.0);
-    }
-    const double b = a.router_b ? (double)a.router_b[e] : 0.0;
-    for (int tt = 0; tt < kRouteTok; tt++) {
-        const int t = blockIdx.y * kRouteTok + tt;
-        if (t >= a.n_tok) break;
-        const __amdgpu_buffer_rsrc_t rx = buf_rsrc(a.x + (size_t)t * d, (uint32_t)d * 4);
-        double* dred = dreds + tt * 64;
-        double P[16];
-        double loc = 0.0, absp = 0.0;
+        for (int i = 0; i < 4; i++) {
+            const int c = lane + 64 * i, row = c >> 5, f = 4 * (c & 31);
+            *(u32x4*)&xs[buf][row][f] = xr[i];
+            *(u32x4*)&wsh[buf][row][f] = wr[i];
+        }
+    };
+    float acc = (a.router_b && e < ne) ? a.router_b[e] : 0.0f;
+    u32x4 xr[4], wr[4];
+    fetch(0, xr, wr);
+    put(0, xr, wr);
+    const int nch = (d + kChainChunk - 1) / kChainChunk;
+    for (int ch = 0; ch < nch; ch++) {
+        const int buf = ch & 1;
+        if (ch + 1 < nch) fetch((ch + 1) * kChainChunk, xr, wr);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const int n = min(kChainChunk, d - ch * kChainChunk);   // a multiple of 32 (d % 32 == 0)
+        const float* xp = &xs[buf][tl][0];
+        const float* wp = &wsh[buf][el][0];
+        for (int j = 0; j < n; j += 32) {
+            f32x4 xv[8], wv[8];
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const u32x4 x4 = __builtin_amdgcn_raw_buffer_load_b128(rx, off + 16 * k, 0, 0);
+            for (int u = 0; u < 8; u++) {
+                xv[u] = *(const f32x4*)(xp + j + 4 * u);
+                wv[u] = *(const f32x4*)(wp + j + 4 * u);
+            }
 #pragma unroll
-            for (int c = 0; c < 4; c++) {
-                const int i = 4 * k + c;
-                P[i] = wg[i] * (double)__uint_as_float(x4[c]);
-                loc += P[i];
-                absp += fabs(P[i]);
+            for (int u = 0; u < 8; u++) {
+#pragma unroll
+                for (int c = 0; c < 4; c++) acc = __fadd_rn(acc, __fmul_rn(wv[u][c], xv[u][c]));
             }
         }
-        // logit_phase1 / logit_phase2 (route_dev.h), in their order
-        const double incl = wave_scan_f64(loc);
-        if (lane == 63) dred[ws] = incl;
-        double run = incl - loc, sabs = 0.0;
-#pragma unroll
-        for (int i = 0; i < 16; i++) { run += P[i]; sabs += fabs(run); }
-        const double s1 = wave_total63_f64(act ? sabs : 0.0);
-        const double s2 = wave_total63_f64(absp);
-        if (lane == 63) { dred[16 + ws] = s1; dred[32 + ws] = s2; }
+        if (ch + 1 < nch) {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            put(buf ^ 1, xr, wr);
+        }
     }
-    // one barrier, then the tokens' logits and bounds side by side (thread tt)
-    __syncthreads();
-    const int t = blockIdx.y * kRouteTok + tid;
-    if (tid < kRouteTok && t < a.n_tok)
-        logit_final(dreds + tid * 64, nw, d, b, a.inv[t], a.lstar + (size_t)t * a.ne + e, a.lbound + (size_t)t * a.ne + e);
+    if (t < nt && e < ne) {
+        a.lstar[(size_t)t * ne + e] = (double)acc;
+        a.lbound[(size_t)t * ne + e] = 0.0;
+    }
 }
 
+
 // ---- 3. top-k + softmax, one wavefront per token (the decode kernels'
-// selection, so ids and weights are per-token decode's bit for bit) ----
+// selection code; on the exact logits of k_router_exact its intervals are
+// points, so the ids are the reference's and the weights the softmax of the
+// reference's fp32 logits) ----
 __global__ __launch_bounds__(64) void k_select_batch(GroupedArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ Selection sel;
@@ -717,8 +736,7 @@ int launch_grouped_layer(const GroupedArgs& a, bool trace, hipStream_t s, const 
         launch(k_prep_batch, dim3(nt), dim3(256), sizeof(float) * (2 * a.d + 64), s, a);
     }
     // one thread per kRouteC elements, whole waves (the decode route's element waves)
-    launch(k_router_batch, dim3(a.ne, (nt + kRouteTok - 1) / kRouteTok), dim3((a.d / kRouteC + 63) / 64 * 64),
-           sizeof(double) * 64 * kRouteTok, s, a);
+    launch(k_router_exact, dim3((a.ne + 7) / 8, (nt + 7) / 8), dim3(64), 0, s, a);
     launch(k_select_batch, dim3(nt), dim3(64), select_lds_bytes(a.ne, a.d, kExactGroupWide), s, a);
     if ((size_t)a.n_tok * a.ne <= kGroupDenseMax)
         launch(k_group_dense, dim3(1), dim3(1024), group_dense_lds(a.n_tok, a.ne), s, a);

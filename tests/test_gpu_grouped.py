@@ -1,15 +1,20 @@
 """GPU parity of the grouped (n_tok > 1) MXFP4 path: tokens grouped by expert,
-expert products on the matrix cores.  The reference's batched tile path is
-bit-identical to per-token decode (engine_gpt2.rs:1120-1239); so is this one:
-every layer output and every int32 block sum is compared bit for bit with
-the per-token kernels (whose block sums tests/test_gpu_mx.py pins to the
-oracle), and the layer outputs also with the oracle to tolerance.
+expert products on the matrix cores.  The reference's batched tile path
+computes what its per-token decode computes (engine_gpt2.rs:1120-1239).
+Here the batched router evaluates the reference's own serial fp32 logits, so
+the selection and weights are the reference's (tests/grouped_ref.py), and
+the expert products are per-token decode's: every int32 block sum is
+compared bit for bit with the per-token kernels (whose block sums
+tests/test_gpu_mx.py pins to the oracle), every layer output with the
+reference's combine of those rows (within an expf ulp of the weights; most
+tokens bit for bit), and the outputs with the oracle to tolerance.
 """
 import numpy as np
 import pytest
 
 from cpubrrr_amd import MoeBlock, MoeConfig, synth
 from oracle import oracle as O
+from tests.grouped_ref import BatchCheck, grouped_expect
 
 pytestmark = pytest.mark.gpu
 
@@ -46,8 +51,12 @@ def test_grouped_equals_per_token(gpu, d, dff, ne, k, n_tok, seed, norm, zipf):
     with MoeBlock(MoeConfig.gptoss(d=d, n_expert=ne, top_k=k, d_ff=dff, max_tokens=n_tok)) as blk:
         blk.load_layer(0, L)
         Y, _ = blk.forward(0, X, apply_norm=norm)          # n_tok > 1: grouped path
-        Yt = per_token(blk, X, norm)
-    assert np.array_equal(Y.view(np.uint32), Yt.view(np.uint32)), "grouped != per-token"
+        bc = BatchCheck()
+        for i in range(n_tok):
+            _, tr = blk.forward(0, X[i], apply_norm=norm, trace=True)
+            ye, _, _ = grouped_expect(L, X[i], tr, "gptoss")
+            bc.add(Y[i], ye, X[i], i)
+        bc.done()
     # and against the oracle, to max-abs <= 1e-3 * RMS of the output
     for i in range(0, n_tok, max(1, n_tok // 5)):
         yo, _ = O.gptoss_moe(L, X[i], norm)
@@ -63,12 +72,16 @@ def test_grouped_block_sums_bit_exact(gpu):
     with MoeBlock(MoeConfig.gptoss(d=d, n_expert=ne, top_k=k, d_ff=dff, max_tokens=n_tok)) as blk:
         blk.load_layer(0, L)
         Y, gs, ds = blk.grouped_sums(0, X, apply_norm=True)
+        bc = BatchCheck()
         for t in range(n_tok):
             y, tr = blk.forward(0, X[t], apply_norm=True, trace=True)
-            assert np.array_equal(y.view(np.uint32), Y[t].view(np.uint32)), t
+            ye, _, order = grouped_expect(L, X[t], tr, "gptoss")
+            bc.add(Y[t], ye, X[t], t)
+            # grouped slot s is the reference's rank s: decode's slot order[s]
             for s in range(k):
-                assert np.array_equal(gs[t * k + s], tr["gu_sums"][s]), ("gate/up sums", t, s)
-                assert np.array_equal(ds[t * k + s], tr["dn_sums"][s]), ("down sums", t, s)
+                assert np.array_equal(gs[t * k + s], tr["gu_sums"][order[s]]), ("gate/up sums", t, s)
+                assert np.array_equal(ds[t * k + s], tr["dn_sums"][order[s]]), ("down sums", t, s)
+        bc.done()
 
 
 def test_grouped_falls_back_on_special_scales(gpu):

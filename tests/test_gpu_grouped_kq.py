@@ -9,6 +9,7 @@ import pytest
 
 from cpubrrr_amd import MoeBlock, MoeConfig, synth
 from oracle import oracle as O
+from tests.grouped_ref import BatchCheck, grouped_expect
 
 pytestmark = pytest.mark.gpu
 
@@ -34,14 +35,17 @@ def test_kq_grouped_equals_per_token(gpu, d, dff, ne, k, n_tok, seed, norm, down
         Y, _ = blk.forward(0, X, apply_norm=norm)               # n_tok > 1: grouped path
         Y2, gs, ds = blk.grouped_sums(0, X, apply_norm=norm)
         assert np.array_equal(Y.view(np.uint32), Y2.view(np.uint32))
+        bc = BatchCheck()
         for t in range(n_tok):
-            trace = t % (7 if n_tok < 200 else 61) == 0
-            y, tr = blk.forward(0, X[t], apply_norm=norm, trace=trace)
-            assert np.array_equal(y.view(np.uint32), Y[t].view(np.uint32)), ("grouped != per-token", t)
-            if trace:
+            y, tr = blk.forward(0, X[t], apply_norm=norm, trace=True)
+            ye, _, order = grouped_expect(L, X[t], tr, "qwen")
+            bc.add(Y[t], ye, X[t], t)
+            if t % (7 if n_tok < 200 else 61) == 0:
+                # grouped slot s is the reference's rank s: decode's slot order[s]
                 for s in range(k):
-                    assert np.array_equal(gs[t * k + s], tr["gu_sums"][s]), ("gate/up sums", t, s)
-                    assert np.array_equal(ds[t * k + s], tr["dn_sums"][s]), ("down sums", t, s)
+                    assert np.array_equal(gs[t * k + s], tr["gu_sums"][order[s]]), ("gate/up sums", t, s)
+                    assert np.array_equal(ds[t * k + s], tr["dn_sums"][order[s]]), ("down sums", t, s)
+        bc.done()
     for t in range(0, n_tok, max(1, n_tok // 4)):
         yo, _ = O.qwen_moe(L, X[t], norm)
         rms = np.sqrt(((yo - X[t]).astype(np.float64) ** 2).mean())
