@@ -148,7 +148,10 @@ int cpb_moe_forward_device(cpb_moe_t* h, int layer0, int n_layers, float* d_x, i
  * exceeds it get CPB_EINVAL.  Kernels are launched directly on the handle's
  * stream (no graph is captured; per-kernel timing is not recorded).  All
  * calls on one GPU share that array: calls that overlap on one GPU (from any
- * handle or thread) race.  Results equal cpb_moe_forward_device's bit for bit. */
+ * handle or thread) race.  Each token goes through the per-token decode
+ * kernels, so results equal cpb_moe_forward_device's bit for bit for n_tok = 1,
+ * and those of n_tok such calls, one token each, for n_tok > 1 (where
+ * cpb_moe_forward_device batches the tokens through the grouped path). */
 int cpb_moe_forward_device_noalloc(cpb_moe_t* h, int layer0, int n_layers, float* d_x, int n_tok,
                                    int apply_norm);
 

@@ -127,6 +127,9 @@ def test_router_tie_uses_exact_fallback(gpu):
 
 
 def test_multi_token_equals_per_token(gpu):
+    # three tokens take the grouped path: the reference's combine of the
+    # per-token expert rows with the reference's own selection and weights
+    from tests.grouped_ref import BatchCheck, grouped_expect
     say("case n_tok=3")
     d = 960
     L = synth.gptoss_layer(d, d, 16, 4, seed=4)
@@ -135,9 +138,12 @@ def test_multi_token_equals_per_token(gpu):
     with MoeBlock(cfg) as blk:
         blk.load_layer(0, L)
         Y, _ = blk.forward(0, X, apply_norm=True)
+        bc = BatchCheck()
         for i in range(3):
-            y, _ = blk.forward(0, X[i], apply_norm=True)
-            assert np.array_equal(y.view(np.uint32), Y[i].view(np.uint32))
+            _, tr = blk.forward(0, X[i], apply_norm=True, trace=True)
+            ye, _, _ = grouped_expect(L, X[i], tr, "gptoss")
+            bc.add(Y[i], ye, X[i], i)
+        bc.done()
 
 
 def test_device_stack_vs_oracle(gpu):

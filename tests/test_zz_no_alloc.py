@@ -1,7 +1,10 @@
 """The no-allocation entry point (cpb_moe_forward_device_noalloc, static
 per-GPU scratch) against cpb_moe_forward_device, bit for bit, on two calls in
 a row (the second with a smaller input), for both weight families, and its
-size limit.  Runs last: it shares one device array across handles."""
+size limit.  It runs the per-token kernels for every token, so a batch is
+compared with single-token cpb_moe_forward_device calls (a batched
+forward_device takes the grouped path).  Runs last: it shares one device
+array across handles."""
 import numpy as np
 import pytest
 
@@ -20,7 +23,8 @@ def _pair(blk, X, n_tok, nl, norm):
     a = torch.from_numpy(np.ascontiguousarray(X[:n_tok])).to("cuda:0")
     b = a.clone()
     torch.cuda.synchronize()
-    blk.forward_device(0, nl, a.data_ptr(), n_tok, norm)
+    for t in range(n_tok):                     # single-token calls
+        blk.forward_device(0, nl, a[t].data_ptr(), 1, norm)
     blk.sync()
     blk.forward_device_noalloc(0, nl, b.data_ptr(), n_tok, norm)
     blk.sync()
