@@ -386,53 +386,77 @@ CPB_DEV v16f mx_block_mfma(const u32x4& w, const u32x4& x0, const u32x4& x1, uin
 }
 
 // LDS staging of one k-part's activations for a 32-token tile: per block i
-// and token ti an 80-byte slot (64 B image + 16 B pad against bank
-// conflicts), then the 15 x 32 scales.
-constexpr int kSlot = 80;
-constexpr int kStageBytes = kBlkPerPart * 32 * kSlot + kBlkPerPart * 32 * 4;
+// and token ti a 64-byte slot whose four 16-byte chunks are XOR-swizzled by
+// the token (chunk c at position c ^ swz(ti)), then the 15 x 32 scales.  The
+// swizzle makes both the stores (16 consecutive chunks per 16 lanes) and the
+// reads (lane ti reads chunk 2hb or 2hb + 1 of slot ti) touch distinct banks
+// in every group of 8 and of 16 lanes.
+constexpr int kSlot = 64;
+constexpr int kStageBlk = 15;
+constexpr int kStageBytes = kStageBlk * 32 * kSlot + kStageBlk * 32 * 4;
+CPB_DEV_HOST_INLINE int stage_swz(int ti) { return ((ti >> 1) ^ (ti >> 2)) & 3; }
+
+// Workgroup sizes of the grouped GEMMs.  Gate/up: 4 waves, so that two
+// workgroups share a CU (LDS 2 x 65 KB, <= 256 registers per lane) and one's
+// barriers, prologue and SwiGLU epilogue overlap the other's k-part loop.
+// Down (a short epilogue): 8 waves, whose row tiles share one staged
+// activation tile.
+constexpr int kGuThreads = 256, kDnThreads = 512;
 
 // Staging of blocks [q*15, q*15+15) of the images / scales of the tile's
 // tokens (src[ti] = token or pair row, -1 for padding), split into the global
 // loads (into registers, issued early) and the LDS stores (after the wait).
-// Each thread moves up to kStageVec 16-byte chunks and one scale.
-constexpr int kStageVec = (kBlkPerPart * 32 * 4 + 511) / 512;
+// Each of the NT threads moves up to kStageVec 16-byte chunks and kStageSc
+// scales.
+template <int NT>
 struct StageRegs {
+    static constexpr int kStageVec = (kStageBlk * 32 * 4 + NT - 1) / NT;
+    static constexpr int kStageSc = (kStageBlk * 32 + NT - 1) / NT;
     u32x4 v[kStageVec];
-    uint32_t s;
+    uint32_t s[kStageSc];
 };
-CPB_DEV StageRegs stage_load(const uint8_t* img, const float* sc, size_t rows, int nbk, int q, const int* src) {
+template <int NT>
+CPB_DEV StageRegs<NT> stage_load(const uint8_t* img, const float* sc, size_t rows, int nbk, int q, const int* src) {
     const int tid = threadIdx.x;
     const __amdgpu_buffer_rsrc_t ri = buf_rsrc(img, (uint32_t)(rows * nbk * kImg));
     const __amdgpu_buffer_rsrc_t rs = buf_rsrc(sc, (uint32_t)(rows * nbk * 4));
-    StageRegs g;
+    StageRegs<NT> g;
 #pragma unroll
-    for (int k = 0; k < kStageVec; k++) {
-        const int idx = tid + 512 * k;
+    for (int k = 0; k < g.kStageVec; k++) {
+        const int idx = tid + NT * k;
         const int i = idx >> 7, ti = (idx >> 2) & 31, c = idx & 3;
         const int b = q * kBlkPerPart + i, r = src[ti];
-        const uint32_t off = (idx < kBlkPerPart * 128 && b < nbk && r >= 0) ? ((uint32_t)r * nbk + b) * kImg + c * 16
-                                                                            : kOffNone;
+        const bool ok = (i < kBlkPerPart) & (b < nbk) & (r >= 0);
+        const uint32_t off = ok ? ((uint32_t)r * nbk + b) * kImg + c * 16 : kOffNone;
         g.v[k] = __builtin_amdgcn_raw_buffer_load_b128(ri, off, 0, 0);
     }
-    {
-        const int i = tid >> 5, ti = tid & 31;
+#pragma unroll
+    for (int k = 0; k < g.kStageSc; k++) {
+        const int idx = tid + NT * k;
+        const int i = idx >> 5, ti = idx & 31;
         const int b = q * kBlkPerPart + i, r = src[ti];
-        const uint32_t off = (tid < kBlkPerPart * 32 && b < nbk && r >= 0) ? ((uint32_t)r * nbk + b) * 4 : kOffNone;
-        g.s = __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0);
+        const bool ok = (i < kBlkPerPart) & (b < nbk) & (r >= 0);
+        const uint32_t off = ok ? ((uint32_t)r * nbk + b) * 4 : kOffNone;
+        g.s[k] = __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0);
     }
     return g;
 }
-CPB_DEV void stage_store(unsigned char* st, const StageRegs& g) {
+template <int NT>
+CPB_DEV void stage_store(unsigned char* st, const StageRegs<NT>& g) {
     const int tid = threadIdx.x;
 #pragma unroll
-    for (int k = 0; k < kStageVec; k++) {
-        const int idx = tid + 512 * k;
-        if (idx < kBlkPerPart * 128) {
+    for (int k = 0; k < g.kStageVec; k++) {
+        const int idx = tid + NT * k;
+        if (idx < kStageBlk * 128) {
             const int i = idx >> 7, ti = (idx >> 2) & 31, c = idx & 3;
-            *(u32x4*)(st + (i * 32 + ti) * kSlot + c * 16) = g.v[k];
+            *(u32x4*)(st + (i * 32 + ti) * kSlot + ((c ^ stage_swz(ti)) << 4)) = g.v[k];
         }
     }
-    if (tid < kBlkPerPart * 32) ((uint32_t*)(st + kBlkPerPart * 32 * kSlot))[tid] = g.s;
+#pragma unroll
+    for (int k = 0; k < g.kStageSc; k++) {
+        const int idx = tid + NT * k;
+        if (idx < kStageBlk * 32) ((uint32_t*)(st + kStageBlk * 32 * kSlot))[idx] = g.s[k];
+    }
 }
 
 // Weight operand of one k-part for the lane's row: unit u (0 = the e8m0
@@ -460,15 +484,17 @@ CPB_DEV u32x4 wload(const WeightStream& ws, int q, int u) {
 // current one is multiplied, and one barrier per k-part suffices (buffer q & 1
 // is rewritten two iterations after it was read, past the next barrier).
 // TRACE writes the int32 block sums S = D * 2^(128 - e) of valid rows.
-template <bool TRACE>
+template <bool TRACE, int NT>
 CPB_DEV v16f grouped_parts(const WeightStream& ws, int P, unsigned char* smem, const uint8_t* img, const float* sc,
                            size_t rows, int nbk, const int* src, int lane, int32_t* tb, bool trace_ok,
-                           float* bias_lds, float bias_v) {
+                           float* bias_lds, float bias_v, int nbias) {
     const int ti = lane & 31, hb = lane >> 5;
+    // the lane's two 16-byte chunks (2hb, 2hb + 1) of its token's slot
+    const int o0 = ((2 * hb) ^ stage_swz(ti)) << 4, o1 = ((2 * hb + 1) ^ stage_swz(ti)) << 4;
     u32x4 wv[kUnits];
 #pragma unroll
     for (int u = 0; u < kUnits; u++) wv[u] = wload(ws, 0, u);
-    StageRegs g = stage_load(img, sc, rows, nbk, 0, src);
+    StageRegs<NT> g = stage_load<NT>(img, sc, rows, nbk, 0, src);
     v16f tot = {};
     for (int q = 0; q < P; q++) {
         unsigned char* st = smem + (q & 1) * kStageBytes;
@@ -478,9 +504,9 @@ CPB_DEV v16f grouped_parts(const WeightStream& ws, int P, unsigned char* smem, c
         const int qn = q + 1 < P ? q + 1 : 0x7fff;
         const u32x4 ex = wv[0];
         wv[0] = wload(ws, qn, 0);
-        if (q + 1 < P) g = stage_load(img, sc, rows, nbk, q + 1, src);
-        const unsigned char* xp = st + ti * kSlot + hb * 32;
-        const float* sl = (const float*)(st + kBlkPerPart * 32 * kSlot) + ti;
+        if (q + 1 < P) g = stage_load<NT>(img, sc, rows, nbk, q + 1, src);
+        const unsigned char* xp = st + ti * kSlot;
+        const float* sl = (const float*)(st + kStageBlk * 32 * kSlot) + ti;
         v16f acc = {}, Dc, Dn;
         float sc_c, sc_n;
         // activation operands two blocks ahead: buffer j & 1 holds block j's
@@ -489,16 +515,16 @@ CPB_DEV v16f grouped_parts(const WeightStream& ws, int P, unsigned char* smem, c
         float sa[2];
 #pragma unroll
         for (int j = 0; j < 2; j++) {
-            xa[j][0] = *(const u32x4*)(xp + j * 32 * kSlot);
-            xa[j][1] = *(const u32x4*)(xp + j * 32 * kSlot + 16);
+            xa[j][0] = *(const u32x4*)(xp + j * 32 * kSlot + o0);
+            xa[j][1] = *(const u32x4*)(xp + j * 32 * kSlot + o1);
             sa[j] = sl[j * 32];
         }
         {
             sc_c = sa[0];
             Dc = mx_block_mfma(wv[1], xa[0][0], xa[0][1], ex[0] & 0xffu);
             wv[1] = wload(ws, qn, 1);
-            xa[0][0] = *(const u32x4*)(xp + 2 * 32 * kSlot);
-            xa[0][1] = *(const u32x4*)(xp + 2 * 32 * kSlot + 16);
+            xa[0][0] = *(const u32x4*)(xp + 2 * 32 * kSlot + o0);
+            xa[0][1] = *(const u32x4*)(xp + 2 * 32 * kSlot + o1);
             sa[0] = sl[2 * 32];
         }
 #pragma unroll
@@ -509,8 +535,8 @@ CPB_DEV v16f grouped_parts(const WeightStream& ws, int P, unsigned char* smem, c
                 Dn = mx_block_mfma(wv[1 + j], xa[bj][0], xa[bj][1], (ex[j >> 2] >> (8 * (j & 3))) & 0xffu);
                 wv[1 + j] = wload(ws, qn, 1 + j);
                 if (j + 2 < kBlkPerPart) {
-                    xa[bj][0] = *(const u32x4*)(xp + (j + 2) * 32 * kSlot);
-                    xa[bj][1] = *(const u32x4*)(xp + (j + 2) * 32 * kSlot + 16);
+                    xa[bj][0] = *(const u32x4*)(xp + (j + 2) * 32 * kSlot + o0);
+                    xa[bj][1] = *(const u32x4*)(xp + (j + 2) * 32 * kSlot + o1);
                     sa[bj] = sl[(j + 2) * 32];
                 }
             }
@@ -540,37 +566,37 @@ CPB_DEV v16f grouped_parts(const WeightStream& ws, int P, unsigned char* smem, c
         }
     }
     // the caller's bias, loaded at its start, into LDS for its epilogue
-    if (threadIdx.x < 256) bias_lds[threadIdx.x] = bias_v;
+    if (threadIdx.x < nbias) bias_lds[threadIdx.x] = bias_v;
     __syncthreads();             // callers reuse the LDS
     return tot;
 }
 
 // ---- 5. grouped gate/up + SwiGLU-OAI + Q8 (+ image of h) ----
-// one workgroup per (token tile, group of 4 row tiles) (grouped_item); 8
+// one workgroup per (token tile, group of 2 row tiles) (grouped_item); 4
 // waves: wave w = row tile w/2 of the group, gate (w even) or up (w odd).
 template <bool TRACE>
-__global__ __launch_bounds__(512) void k_gateup_grouped(GroupedArgs a) {
+__global__ __launch_bounds__(kGuThreads) __attribute__((amdgpu_waves_per_eu(2))) void k_gateup_grouped(GroupedArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ int src[32];
     const int T = a.dff / 32, P = a.parts_gu, nb = a.nb;
     int tile, grp;
-    if (!grouped_item(uniform(*a.ntiles), (T + 3) / 4, &tile, &grp)) return;
+    if (!grouped_item(uniform(*a.ntiles), (T + 1) / 2, &tile, &grp)) return;
     const int4 tl = a.tiles[tile];
     const int e = uniform(tl.x), start = uniform(tl.y), cnt = uniform(tl.z);
     const int lane = threadIdx.x & 63, w = uniform((int)(threadIdx.x >> 6));
-    const int rt = grp * 4 + (w >> 1), isup = w & 1;
+    const int rt = grp * 2 + (w >> 1), isup = w & 1;
     const bool live = rt < T;
     if (threadIdx.x < 32) src[threadIdx.x] = (int)threadIdx.x < cnt ? a.sorted[start + threadIdx.x] / a.k : -1;
     __syncthreads();
-    // the biases of the workgroup's 4 x (32 gate + 32 up) rows, requested now
+    // the biases of the workgroup's 2 x (32 gate + 32 up) rows, requested now
     // and kept in one register until the epilogue (a load issued after the
     // GEMM would wait a full loaded-memory latency)
-    __shared__ float bias_s[256];                   // [row tile][gate 32 | up 32]
+    __shared__ float bias_s[128];                   // [row tile][gate 32 | up 32]
     float bias_v = 0.0f;
     {
-        const int t = (int)threadIdx.x, rtb = grp * 4 + (t >> 6), gu = (t >> 5) & 1;
+        const int t = (int)threadIdx.x, rtb = grp * 2 + (t >> 6), gu = (t >> 5) & 1;
         const float* bp = gu ? a.up_b : a.gate_b;
-        if (t < 256 && bp && rtb < T) bias_v = bp[(size_t)e * a.dff + rtb * 32 + (t & 31)];
+        if (t < 128 && bp && rtb < T) bias_v = bp[(size_t)e * a.dff + rtb * 32 + (t & 31)];
     }
     const int ti = lane & 31, hb = lane >> 5;
     const bool valid = ti < cnt;
@@ -585,8 +611,8 @@ __global__ __launch_bounds__(512) void k_gateup_grouped(GroupedArgs a) {
     }
     int32_t* tb = TRACE ? a.gu_sums + (((size_t)pair * 2 + isup) * a.dff + rt * 32) * nb : nullptr;
 
-    const v16f tot = grouped_parts<TRACE>(ws, P, smem, a.ximg, a.xsb, (size_t)a.n_tok, nb, src, lane, tb,
-                                          valid && live, bias_s, bias_v);
+    const v16f tot = grouped_parts<TRACE, kGuThreads>(ws, P, smem, a.ximg, a.xsb, (size_t)a.n_tok, nb, src, lane, tb,
+                                          valid && live, bias_s, bias_v, 128);
     // SwiGLU, Q8 and image of the row tile, split over its two waves: the
     // lane's rows 8g + 4hb + c (g, c < 4) of groups g = isup and g = isup + 2
     // are this wave's (so each wave owns whole hq words and whole 8-byte image
@@ -594,7 +620,7 @@ __global__ __launch_bounds__(512) void k_gateup_grouped(GroupedArgs a) {
     // (LDS reused), then the block maximum is combined through LDS.
     const int rtl = w >> 1;
     float* xch = (float*)smem;                    // [row tile][sender][8][64]
-    float* mxs = xch + 4 * 2 * 8 * 64;            // [row tile][wave][64]
+    float* mxs = xch + 2 * 2 * 8 * 64;            // [row tile][wave][64]
 #pragma unroll
     for (int j = 0; j < 8; j++) {
         const int r = 4 * (1 - isup) + (j & 3) + 8 * (j >> 2);        // partner's j-th row
@@ -647,7 +673,7 @@ __global__ __launch_bounds__(512) void k_gateup_grouped(GroupedArgs a) {
 // ---- 6. grouped down (+ bias) into dnout ----
 // one workgroup per (token tile, group of 8 row tiles of 32 rows) (grouped_item).
 template <bool TRACE>
-__global__ __launch_bounds__(512) void k_down_grouped(GroupedArgs a) {
+__global__ __launch_bounds__(kDnThreads) void k_down_grouped(GroupedArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ int src[32];
     int tile, grp;
@@ -680,8 +706,8 @@ __global__ __launch_bounds__(512) void k_down_grouped(GroupedArgs a) {
     }
     int32_t* tb = TRACE ? a.dn_sums + ((size_t)pair * a.d + rt * 32) * nbf : nullptr;
 
-    const v16f tot = grouped_parts<TRACE>(ws, P, smem, a.himg, a.hsb, (size_t)a.n_tok * a.k, nbf, src, lane,
-                                          tb, valid && live, bias_s, bias_v);
+    const v16f tot = grouped_parts<TRACE, kDnThreads>(ws, P, smem, a.himg, a.hsb, (size_t)a.n_tok * a.k, nbf, src, lane,
+                                          tb, valid && live, bias_s, bias_v, 256);
     if (!valid || !live) return;
     float* out = a.dnout + (size_t)pair * a.d + rt * 32 + 4 * hb;
 #pragma unroll
@@ -749,15 +775,15 @@ int launch_grouped_layer(const GroupedArgs& a, bool trace, hipStream_t s, const 
     }
     // one workgroup per (token tile, row group), dealt out by grouped_item:
     // 8 slots per XCD round, enough for the largest tile count
-    const int ngu = a.max_tiles * ((a.dff / 32 + 3) / 4), ndn = a.max_tiles * ((a.d / 32 + 7) / 8);
+    const int ngu = a.max_tiles * ((a.dff / 32 + 1) / 2), ndn = a.max_tiles * ((a.d / 32 + 7) / 8);
     const dim3 ggu((ngu + 7) / 8 * 8), gdn((ndn + 7) / 8 * 8);
-    const size_t lds = 2 * kStageBytes;        // two staging buffers (>= the 16 KB epilogue exchange)
+    const size_t lds = 2 * kStageBytes;        // two staging buffers (>= the 8 KB epilogue exchange)
     if (ev) armed_events() = ev[0];
-    if (trace) launch(k_gateup_grouped<true>, ggu, dim3(512), lds, s, a);
-    else launch(k_gateup_grouped<false>, ggu, dim3(512), lds, s, a);
+    if (trace) launch(k_gateup_grouped<true>, ggu, dim3(kGuThreads), lds, s, a);
+    else launch(k_gateup_grouped<false>, ggu, dim3(kGuThreads), lds, s, a);
     if (ev) armed_events() = ev[1];
-    if (trace) launch(k_down_grouped<true>, gdn, dim3(512), lds, s, a);
-    else launch(k_down_grouped<false>, gdn, dim3(512), lds, s, a);
+    if (trace) launch(k_down_grouped<true>, gdn, dim3(kDnThreads), lds, s, a);
+    else launch(k_down_grouped<false>, gdn, dim3(kDnThreads), lds, s, a);
     launch(k_combine_batch, dim3((unsigned)std::min<size_t>(((size_t)nt * (a.d / 4) + 255) / 256, 2048)), dim3(256), 0, s, a);
     return hipGetLastError() == hipSuccess ? 0 : -19;
 }
