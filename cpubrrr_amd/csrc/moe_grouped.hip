@@ -415,29 +415,44 @@ struct StageRegs {
     u32x4 v[kStageVec];
     uint32_t s[kStageSc];
 };
+// Thread tid's k-th chunk is (block i0 + k NT/128, token ti, chunk c) and its
+// k-th scale (block j0 + k NT/32, token tid & 31): the token does not depend
+// on k, so the offsets of k-part q are one base (set once; kOffNone for a
+// padding token, which stays out of range) plus constants.
+struct StagePlan {
+    __amdgpu_buffer_rsrc_t ri, rs;
+    uint32_t vbase, sbase;         // bytes: chunk k = 0 / scale k = 0 of k-part 0
+    int i0, j0;
+};
 template <int NT>
-CPB_DEV StageRegs<NT> stage_load(const uint8_t* img, const float* sc, size_t rows, int nbk, int q, const int* src) {
+CPB_DEV StagePlan stage_plan(const uint8_t* img, const float* sc, size_t rows, int nbk, const int* src) {
     const int tid = threadIdx.x;
-    const __amdgpu_buffer_rsrc_t ri = buf_rsrc(img, (uint32_t)(rows * nbk * kImg));
-    const __amdgpu_buffer_rsrc_t rs = buf_rsrc(sc, (uint32_t)(rows * nbk * 4));
+    StagePlan p;
+    p.ri = buf_rsrc(img, (uint32_t)(rows * nbk * kImg));
+    p.rs = buf_rsrc(sc, (uint32_t)(rows * nbk * 4));
+    p.i0 = tid >> 7;
+    p.j0 = (tid >> 5) & (NT / 32 - 1);
+    const int r = src[(tid >> 2) & 31], rsc = src[tid & 31];
+    p.vbase = r >= 0 ? ((uint32_t)r * nbk + p.i0) * kImg + (tid & 3) * 16 : kOffNone;
+    p.sbase = rsc >= 0 ? ((uint32_t)rsc * nbk + p.j0) * 4 : kOffNone;
+    return p;
+}
+template <int NT>
+CPB_DEV StageRegs<NT> stage_load(const StagePlan& p, int nbk, int q) {
     StageRegs<NT> g;
+    // blocks of this k-part that exist: [q*15, min(q*15 + 15, nbk))
+    const int lim = min(kBlkPerPart, nbk - q * kBlkPerPart);
 #pragma unroll
     for (int k = 0; k < g.kStageVec; k++) {
-        const int idx = tid + NT * k;
-        const int i = idx >> 7, ti = (idx >> 2) & 31, c = idx & 3;
-        const int b = q * kBlkPerPart + i, r = src[ti];
-        const bool ok = (i < kBlkPerPart) & (b < nbk) & (r >= 0);
-        const uint32_t off = ok ? ((uint32_t)r * nbk + b) * kImg + c * 16 : kOffNone;
-        g.v[k] = __builtin_amdgcn_raw_buffer_load_b128(ri, off, 0, 0);
+        const int i = p.i0 + k * (NT / 128);
+        const uint32_t off = i < lim ? p.vbase + (uint32_t)(q * kBlkPerPart + k * (NT / 128)) * kImg : kOffNone;
+        g.v[k] = __builtin_amdgcn_raw_buffer_load_b128(p.ri, off, 0, 0);
     }
 #pragma unroll
     for (int k = 0; k < g.kStageSc; k++) {
-        const int idx = tid + NT * k;
-        const int i = idx >> 5, ti = idx & 31;
-        const int b = q * kBlkPerPart + i, r = src[ti];
-        const bool ok = (i < kBlkPerPart) & (b < nbk) & (r >= 0);
-        const uint32_t off = ok ? ((uint32_t)r * nbk + b) * 4 : kOffNone;
-        g.s[k] = __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0);
+        const int i = p.j0 + k * (NT / 32);
+        const uint32_t off = i < lim ? p.sbase + (uint32_t)(q * kBlkPerPart + k * (NT / 32)) * 4 : kOffNone;
+        g.s[k] = __builtin_amdgcn_raw_buffer_load_b32(p.rs, off, 0, 0);
     }
     return g;
 }
@@ -494,7 +509,8 @@ CPB_DEV v16f grouped_parts(const WeightStream& ws, int P, unsigned char* smem, c
     u32x4 wv[kUnits];
 #pragma unroll
     for (int u = 0; u < kUnits; u++) wv[u] = wload(ws, 0, u);
-    StageRegs<NT> g = stage_load<NT>(img, sc, rows, nbk, 0, src);
+    const StagePlan plan = stage_plan<NT>(img, sc, rows, nbk, src);
+    StageRegs<NT> g = stage_load<NT>(plan, nbk, 0);
     v16f tot = {};
     for (int q = 0; q < P; q++) {
         unsigned char* st = smem + (q & 1) * kStageBytes;
@@ -504,7 +520,7 @@ CPB_DEV v16f grouped_parts(const WeightStream& ws, int P, unsigned char* smem, c
         const int qn = q + 1 < P ? q + 1 : 0x7fff;
         const u32x4 ex = wv[0];
         wv[0] = wload(ws, qn, 0);
-        if (q + 1 < P) g = stage_load<NT>(img, sc, rows, nbk, q + 1, src);
+        if (q + 1 < P) g = stage_load<NT>(plan, nbk, q + 1);
         const unsigned char* xp = st + ti * kSlot;
         const float* sl = (const float*)(st + kStageBlk * 32 * kSlot) + ti;
         v16f acc = {}, Dc, Dn;
