@@ -39,10 +39,12 @@ sys.path.insert(0, str(ROOT))
 # bench cannot read hardware counters itself (they need a profiler run of
 # their own), so each line names the profile its figure comes from.
 MEASURED_TRAFFIC = {"k_gateup_mx": 35_815_144, "k_gateup_kq": 14_418_124,
-                    "k_gateup_grouped": 484_748_900, "head": 327_526_064}
+                    "k_gateup_grouped": 537_580_042, "k_gateup_kq_grouped": 282_813_378,
+                    "head": 327_526_064}
 TRAFFIC_SOURCE = {"k_gateup_mx": "profiles/hbm_traffic_config1_phased.md",
                   "k_gateup_kq": "profiles/hbm_traffic_config3_qwen.md",
                   "k_gateup_grouped": "profiles/mfma_hbm_config4_grouped.md",
+                  "k_gateup_kq_grouped": "profiles/mfma_hbm_config4_grouped.md",
                   "head": "profiles/hbm_traffic_config6_head.md"}
 
 METRIC = "expert-weight GB/s (% HBM peak) + MoE-layer tok/s, gpt-oss-20b shape, 1 GPU"
@@ -132,7 +134,8 @@ def batched_result(c, args, ms, n_tok, kt) -> dict:
         "kernels_us": {"gate_up_gemm": round(gu_us, 2), "down_gemm": round(dn_us, 2)},
         "roofline": {"bound": "hbm", "kernel": kern, "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": MEASURED_TRAFFIC.get(kern), "bytes_per_launch": gu_w,
+                     "traffic": MEASURED_TRAFFIC.get(kern), "traffic_source": TRAFFIC_SOURCE.get(kern),
+                     "bytes_per_launch": gu_w,
                      "mfma_int8_equiv": {"achieved": round(gu_tops, 2), "peak": MFMA_FP8_PEAK_TOPS,
                                          "unit": "TOP/s", "frac": round(gu_tops / MFMA_FP8_PEAK_TOPS, 5)}},
         "mfma": {"achieved": round(tops, 2), "peak": MFMA_FP8_PEAK_TOPS, "unit": "TOP/s (useful int8-equivalent, whole layer)",
