@@ -393,7 +393,7 @@ CPB_DEV v16f mx_block_mfma(const u32x4& w, const u32x4& x0, const u32x4& x1, uin
 // in every group of 8 and of 16 lanes.
 constexpr int kSlot = 64;
 constexpr int kStageBlk = 15;
-constexpr int kStageBytes = kStageBlk * 32 * kSlot + kStageBlk * 32 * 4;
+constexpr int kStageBytes = kStageBlk * 32 * kSlot + 512 * 4;
 CPB_DEV_HOST_INLINE int stage_swz(int ti) { return ((ti >> 1) ^ (ti >> 2)) & 3; }
 
 // Workgroup sizes of the grouped GEMMs.  Gate/up: 4 waves, so that two
@@ -402,6 +402,7 @@ CPB_DEV_HOST_INLINE int stage_swz(int ti) { return ((ti >> 1) ^ (ti >> 2)) & 3; 
 // Down (a short epilogue): 8 waves, whose row tiles share one staged
 // activation tile.
 constexpr int kGuThreads = 256, kDnThreads = 512;
+constexpr bool kGuDma = true;            // gate/up activations staged by direct global-to-LDS loads
 
 // Staging of blocks [q*15, q*15+15) of the images / scales of the tile's
 // tokens (src[ti] = token or pair row, -1 for padding), split into the global
@@ -474,6 +475,54 @@ CPB_DEV void stage_store(unsigned char* st, const StageRegs<NT>& g) {
     }
 }
 
+// Direct global-to-LDS staging of k-part q (no staging registers): each
+// wavefront instruction writes 1 KB of LDS, lane L at byte 16 L, so lane L
+// fetches the chunk the swizzled layout puts there (token h*16 + L/4 of the
+// block, chunk (L & 3) ^ swz(token)); the scales take 8 instructions of 64
+// (the last half past block 14 reads nothing).
+typedef __attribute__((address_space(3))) void lds_void_g;
+struct DmaPlan {
+    __amdgpu_buffer_rsrc_t ri, rs;
+    uint32_t vbase0, vbase1, sbase;  // bytes: block 0 of the lane's chunk in token half 0 / 1, its scale
+};
+CPB_DEV DmaPlan dma_plan(const uint8_t* img, const float* sc, size_t rows, int nbk, const int* src) {
+    const int L = threadIdx.x & 63;
+    DmaPlan p;
+    p.ri = buf_rsrc(img, (uint32_t)(rows * nbk * kImg));
+    p.rs = buf_rsrc(sc, (uint32_t)(rows * nbk * 4));
+    const int t0 = L >> 2, t1 = 16 + (L >> 2), r0 = src[t0], r1 = src[t1];
+    p.vbase0 = r0 >= 0 ? (uint32_t)r0 * nbk * kImg + (uint32_t)(((L & 3) ^ stage_swz(t0)) << 4) : kOffNone;
+    p.vbase1 = r1 >= 0 ? (uint32_t)r1 * nbk * kImg + (uint32_t)(((L & 3) ^ stage_swz(t1)) << 4) : kOffNone;
+    const int rs_ = src[L & 31];
+    p.sbase = rs_ >= 0 ? (uint32_t)rs_ * nbk * 4 : kOffNone;
+    return p;
+}
+template <int NT>
+CPB_DEV void stage_dma(const DmaPlan& p, int nbk, int q, unsigned char* st) {
+    const int w = threadIdx.x >> 6, L = threadIdx.x & 63;
+    const int lim = min(kBlkPerPart, nbk - q * kBlkPerPart);
+#pragma unroll
+    for (int k = 0; k < (2 * kBlkPerPart + NT / 64 - 1) / (NT / 64); k++) {
+        const int m = w + k * (NT / 64), i = m >> 1, h = m & 1;
+        if (m < 2 * kBlkPerPart) {
+            const uint32_t off = i < lim ? (h ? p.vbase1 : p.vbase0) + (uint32_t)(q * kBlkPerPart + i) * kImg : kOffNone;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(p.ri, (lds_void_g*)(st + (i * 32 + h * 16) * kSlot), 16, off, 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < (8 + NT / 64 - 1) / (NT / 64); k++) {
+        const int n = w + k * (NT / 64), i = 2 * n + (L >> 5);
+        if (n < 8) {
+            const uint32_t off = i < lim ? p.sbase + (uint32_t)(q * kBlkPerPart + i) * 4 : kOffNone;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(p.rs, (lds_void_g*)(st + kStageBlk * 32 * kSlot + n * 256), 4, off, 0, 0, 0);
+        }
+    }
+}
+// the two staging buffers of the DMA-staged GEMMs, as separate objects so
+// that the compiler can tell the buffer being filled from the one being read
+__shared__ __align__(16) unsigned char g_stage0[kStageBytes];
+__shared__ __align__(16) unsigned char g_stage1[kStageBytes];
+
 // Weight operand of one k-part for the lane's row: unit u (0 = the e8m0
 // bytes, 1..15 = blocks) sits at byte off + u * ustride of the expert's
 // stream; rs covers the expert's whole stream (out-of-range offsets read 0).
@@ -499,7 +548,7 @@ CPB_DEV u32x4 wload(const WeightStream& ws, int q, int u) {
 // current one is multiplied, and one barrier per k-part suffices (buffer q & 1
 // is rewritten two iterations after it was read, past the next barrier).
 // TRACE writes the int32 block sums S = D * 2^(128 - e) of valid rows.
-template <bool TRACE, int NT>
+template <bool TRACE, int NT, bool DMA>
 CPB_DEV v16f grouped_parts(const WeightStream& ws, int P, unsigned char* smem, const uint8_t* img, const float* sc,
                            size_t rows, int nbk, const int* src, int lane, int32_t* tb, bool trace_ok,
                            float* bias_lds, float bias_v, int nbias) {
@@ -509,18 +558,29 @@ CPB_DEV v16f grouped_parts(const WeightStream& ws, int P, unsigned char* smem, c
     u32x4 wv[kUnits];
 #pragma unroll
     for (int u = 0; u < kUnits; u++) wv[u] = wload(ws, 0, u);
-    const StagePlan plan = stage_plan<NT>(img, sc, rows, nbk, src);
-    StageRegs<NT> g = stage_load<NT>(plan, nbk, 0);
+    StagePlan plan;
+    StageRegs<NT> g;
+    DmaPlan dp;
+    if constexpr (DMA) {
+        dp = dma_plan(img, sc, rows, nbk, src);
+        stage_dma<NT>(dp, nbk, 0, g_stage0);
+    } else {
+        plan = stage_plan<NT>(img, sc, rows, nbk, src);
+        g = stage_load<NT>(plan, nbk, 0);
+    }
     v16f tot = {};
-    for (int q = 0; q < P; q++) {
-        unsigned char* st = smem + (q & 1) * kStageBytes;
-        stage_store(st, g);
+    // k-part q on the activations staged in st; the next k-part's go to nx
+    auto kpart = [&](int q, unsigned char* st, unsigned char* nx) {
+        if constexpr (!DMA) stage_store(st, g);
         __syncthreads();
         // past the last k-part the refills read out of range (zeros, no traffic)
         const int qn = q + 1 < P ? q + 1 : 0x7fff;
         const u32x4 ex = wv[0];
         wv[0] = wload(ws, qn, 0);
-        if (q + 1 < P) g = stage_load<NT>(plan, nbk, q + 1);
+        if (q + 1 < P) {
+            if constexpr (DMA) stage_dma<NT>(dp, nbk, q + 1, nx);
+            else g = stage_load<NT>(plan, nbk, q + 1);
+        }
         const unsigned char* xp = st + ti * kSlot;
         const float* sl = (const float*)(st + kStageBlk * 32 * kSlot) + ti;
         v16f acc = {}, Dc, Dn;
@@ -580,6 +640,11 @@ CPB_DEV v16f grouped_parts(const WeightStream& ws, int P, unsigned char* smem, c
             Dc = Dn;
             sc_c = sc_n;
         }
+    };
+    if constexpr (DMA) {
+        for (int q = 0; q < P; q++) kpart(q, (q & 1) ? g_stage1 : g_stage0, (q & 1) ? g_stage0 : g_stage1);
+    } else {
+        for (int q = 0; q < P; q++) kpart(q, smem + (q & 1) * kStageBytes, nullptr);
     }
     // the caller's bias, loaded at its start, into LDS for its epilogue
     if (threadIdx.x < nbias) bias_lds[threadIdx.x] = bias_v;
@@ -627,7 +692,7 @@ __global__ __launch_bounds__(kGuThreads) __attribute__((amdgpu_waves_per_eu(2)))
     }
     int32_t* tb = TRACE ? a.gu_sums + (((size_t)pair * 2 + isup) * a.dff + rt * 32) * nb : nullptr;
 
-    const v16f tot = grouped_parts<TRACE, kGuThreads>(ws, P, smem, a.ximg, a.xsb, (size_t)a.n_tok, nb, src, lane, tb,
+    const v16f tot = grouped_parts<TRACE, kGuThreads, kGuDma>(ws, P, smem, a.ximg, a.xsb, (size_t)a.n_tok, nb, src, lane, tb,
                                           valid && live, bias_s, bias_v, 128);
     // SwiGLU, Q8 and image of the row tile, split over its two waves: the
     // lane's rows 8g + 4hb + c (g, c < 4) of groups g = isup and g = isup + 2
@@ -635,7 +700,7 @@ __global__ __launch_bounds__(kGuThreads) __attribute__((amdgpu_waves_per_eu(2)))
     // runs); each wave hands the partner the totals of the partner's rows
     // (LDS reused), then the block maximum is combined through LDS.
     const int rtl = w >> 1;
-    float* xch = (float*)smem;                    // [row tile][sender][8][64]
+    float* xch = (float*)(kGuDma ? g_stage0 : smem);      // [row tile][sender][8][64]
     float* mxs = xch + 2 * 2 * 8 * 64;            // [row tile][wave][64]
 #pragma unroll
     for (int j = 0; j < 8; j++) {
@@ -722,7 +787,7 @@ __global__ __launch_bounds__(kDnThreads) void k_down_grouped(GroupedArgs a) {
     }
     int32_t* tb = TRACE ? a.dn_sums + ((size_t)pair * a.d + rt * 32) * nbf : nullptr;
 
-    const v16f tot = grouped_parts<TRACE, kDnThreads>(ws, P, smem, a.himg, a.hsb, (size_t)a.n_tok * a.k, nbf, src, lane,
+    const v16f tot = grouped_parts<TRACE, kDnThreads, false>(ws, P, smem, a.himg, a.hsb, (size_t)a.n_tok * a.k, nbf, src, lane,
                                           tb, valid && live, bias_s, bias_v, 256);
     if (!valid || !live) return;
     float* out = a.dnout + (size_t)pair * a.d + rt * 32 + 4 * hb;
@@ -795,8 +860,8 @@ int launch_grouped_layer(const GroupedArgs& a, bool trace, hipStream_t s, const 
     const dim3 ggu((ngu + 7) / 8 * 8), gdn((ndn + 7) / 8 * 8);
     const size_t lds = 2 * kStageBytes;        // two staging buffers (>= the 8 KB epilogue exchange)
     if (ev) armed_events() = ev[0];
-    if (trace) launch(k_gateup_grouped<true>, ggu, dim3(kGuThreads), lds, s, a);
-    else launch(k_gateup_grouped<false>, ggu, dim3(kGuThreads), lds, s, a);
+    if (trace) launch(k_gateup_grouped<true>, ggu, dim3(kGuThreads), kGuDma ? 0 : lds, s, a);
+    else launch(k_gateup_grouped<false>, ggu, dim3(kGuThreads), kGuDma ? 0 : lds, s, a);
     if (ev) armed_events() = ev[1];
     if (trace) launch(k_down_grouped<true>, gdn, dim3(kDnThreads), lds, s, a);
     else launch(k_down_grouped<false>, gdn, dim3(kDnThreads), lds, s, a);
