@@ -387,10 +387,10 @@ CPB_DEV v16f mx_block_mfma(const u32x4& w, const u32x4& x0, const u32x4& x1, uin
 
 // LDS staging of one k-part's activations for a 32-token tile: per block i
 // and token ti a 64-byte slot whose four 16-byte chunks are XOR-swizzled by
-// the token (chunk c at position c ^ swz(ti)), then the 15 x 32 scales.  The
-// swizzle makes both the stores (16 consecutive chunks per 16 lanes) and the
-// reads (lane ti reads chunk 2hb or 2hb + 1 of slot ti) touch distinct banks
-// in every group of 8 and of 16 lanes.
+// the token (chunk c at position c ^ swz(ti)), then room for 512 scales (15 x
+// 32 used).  The swizzle puts the reads (lane ti reads chunk 2hb or 2hb + 1 of
+// slot ti) on distinct banks in every group of 8 and of 16 lanes (80-byte
+// padded slots had 2.75 M conflict cycles per gate/up launch).
 constexpr int kSlot = 64;
 constexpr int kStageBlk = 15;
 constexpr int kStageBytes = kStageBlk * 32 * kSlot + 512 * 4;
@@ -402,78 +402,7 @@ CPB_DEV_HOST_INLINE int stage_swz(int ti) { return ((ti >> 1) ^ (ti >> 2)) & 3; 
 // Down (a short epilogue): 8 waves, whose row tiles share one staged
 // activation tile.
 constexpr int kGuThreads = 256, kDnThreads = 512;
-constexpr bool kGuDma = true;            // gate/up activations staged by direct global-to-LDS loads
 
-// Staging of blocks [q*15, q*15+15) of the images / scales of the tile's
-// tokens (src[ti] = token or pair row, -1 for padding), split into the global
-// loads (into registers, issued early) and the LDS stores (after the wait).
-// Each of the NT threads moves up to kStageVec 16-byte chunks and kStageSc
-// scales.
-template <int NT>
-struct StageRegs {
-    static constexpr int kStageVec = (kStageBlk * 32 * 4 + NT - 1) / NT;
-    static constexpr int kStageSc = (kStageBlk * 32 + NT - 1) / NT;
-    u32x4 v[kStageVec];
-    uint32_t s[kStageSc];
-};
-// Thread tid's k-th chunk is (block i0 + k NT/128, token ti, chunk c) and its
-// k-th scale (block j0 + k NT/32, token tid & 31): the token does not depend
-// on k, so the offsets of k-part q are one base (set once; kOffNone for a
-// padding token, which stays out of range) plus constants.
-struct StagePlan {
-    __amdgpu_buffer_rsrc_t ri, rs;
-    uint32_t vbase, sbase;         // bytes: chunk k = 0 / scale k = 0 of k-part 0
-    int i0, j0;
-};
-template <int NT>
-CPB_DEV StagePlan stage_plan(const uint8_t* img, const float* sc, size_t rows, int nbk, const int* src) {
-    const int tid = threadIdx.x;
-    StagePlan p;
-    p.ri = buf_rsrc(img, (uint32_t)(rows * nbk * kImg));
-    p.rs = buf_rsrc(sc, (uint32_t)(rows * nbk * 4));
-    p.i0 = tid >> 7;
-    p.j0 = (tid >> 5) & (NT / 32 - 1);
-    const int r = src[(tid >> 2) & 31], rsc = src[tid & 31];
-    p.vbase = r >= 0 ? ((uint32_t)r * nbk + p.i0) * kImg + (tid & 3) * 16 : kOffNone;
-    p.sbase = rsc >= 0 ? ((uint32_t)rsc * nbk + p.j0) * 4 : kOffNone;
-    return p;
-}
-template <int NT>
-CPB_DEV StageRegs<NT> stage_load(const StagePlan& p, int nbk, int q) {
-    StageRegs<NT> g;
-    // blocks of this k-part that exist: [q*15, min(q*15 + 15, nbk))
-    const int lim = min(kBlkPerPart, nbk - q * kBlkPerPart);
-#pragma unroll
-    for (int k = 0; k < g.kStageVec; k++) {
-        const int i = p.i0 + k * (NT / 128);
-        const uint32_t off = i < lim ? p.vbase + (uint32_t)(q * kBlkPerPart + k * (NT / 128)) * kImg : kOffNone;
-        g.v[k] = __builtin_amdgcn_raw_buffer_load_b128(p.ri, off, 0, 0);
-    }
-#pragma unroll
-    for (int k = 0; k < g.kStageSc; k++) {
-        const int i = p.j0 + k * (NT / 32);
-        const uint32_t off = i < lim ? p.sbase + (uint32_t)(q * kBlkPerPart + k * (NT / 32)) * 4 : kOffNone;
-        g.s[k] = __builtin_amdgcn_raw_buffer_load_b32(p.rs, off, 0, 0);
-    }
-    return g;
-}
-template <int NT>
-CPB_DEV void stage_store(unsigned char* st, const StageRegs<NT>& g) {
-    const int tid = threadIdx.x;
-#pragma unroll
-    for (int k = 0; k < g.kStageVec; k++) {
-        const int idx = tid + NT * k;
-        if (idx < kStageBlk * 128) {
-            const int i = idx >> 7, ti = (idx >> 2) & 31, c = idx & 3;
-            *(u32x4*)(st + (i * 32 + ti) * kSlot + ((c ^ stage_swz(ti)) << 4)) = g.v[k];
-        }
-    }
-#pragma unroll
-    for (int k = 0; k < g.kStageSc; k++) {
-        const int idx = tid + NT * k;
-        if (idx < kStageBlk * 32) ((uint32_t*)(st + kStageBlk * 32 * kSlot))[idx] = g.s[k];
-    }
-}
 
 // Direct global-to-LDS staging of k-part q (no staging registers): each
 // wavefront instruction writes 1 KB of LDS, lane L at byte 16 L, so lane L
@@ -544,12 +473,13 @@ CPB_DEV u32x4 wload(const WeightStream& ws, int q, int u) {
 // side; each weight register is refilled with the next k-part's unit right
 // after its MFMA has been issued (one k-part of lead time, 16 units of
 // registers instead of 32).  Two LDS staging buffers alternate for the
-// activations: the next k-part's are requested (into registers) before the
-// current one is multiplied, and one barrier per k-part suffices (buffer q & 1
-// is rewritten two iterations after it was read, past the next barrier).
+// activations: right after the barrier that opens k-part q, the direct loads
+// of k-part q + 1 go into the other buffer (every wave has finished reading it
+// in k-part q - 1), so one barrier per k-part suffices; the barrier's release
+// fence makes each wave wait for its own direct loads first.
 // TRACE writes the int32 block sums S = D * 2^(128 - e) of valid rows.
-template <bool TRACE, int NT, bool DMA>
-CPB_DEV v16f grouped_parts(const WeightStream& ws, int P, unsigned char* smem, const uint8_t* img, const float* sc,
+template <bool TRACE, int NT>
+CPB_DEV v16f grouped_parts(const WeightStream& ws, int P, const uint8_t* img, const float* sc,
                            size_t rows, int nbk, const int* src, int lane, int32_t* tb, bool trace_ok,
                            float* bias_lds, float bias_v, int nbias) {
     const int ti = lane & 31, hb = lane >> 5;
@@ -558,29 +488,17 @@ CPB_DEV v16f grouped_parts(const WeightStream& ws, int P, unsigned char* smem, c
     u32x4 wv[kUnits];
 #pragma unroll
     for (int u = 0; u < kUnits; u++) wv[u] = wload(ws, 0, u);
-    StagePlan plan;
-    StageRegs<NT> g;
-    DmaPlan dp;
-    if constexpr (DMA) {
-        dp = dma_plan(img, sc, rows, nbk, src);
-        stage_dma<NT>(dp, nbk, 0, g_stage0);
-    } else {
-        plan = stage_plan<NT>(img, sc, rows, nbk, src);
-        g = stage_load<NT>(plan, nbk, 0);
-    }
+    const DmaPlan dp = dma_plan(img, sc, rows, nbk, src);
+    stage_dma<NT>(dp, nbk, 0, g_stage0);
     v16f tot = {};
     // k-part q on the activations staged in st; the next k-part's go to nx
     auto kpart = [&](int q, unsigned char* st, unsigned char* nx) {
-        if constexpr (!DMA) stage_store(st, g);
-        __syncthreads();
+        __syncthreads();                     // k-part q's activations have landed
         // past the last k-part the refills read out of range (zeros, no traffic)
         const int qn = q + 1 < P ? q + 1 : 0x7fff;
         const u32x4 ex = wv[0];
         wv[0] = wload(ws, qn, 0);
-        if (q + 1 < P) {
-            if constexpr (DMA) stage_dma<NT>(dp, nbk, q + 1, nx);
-            else g = stage_load<NT>(plan, nbk, q + 1);
-        }
+        if (q + 1 < P) stage_dma<NT>(dp, nbk, q + 1, nx);
         const unsigned char* xp = st + ti * kSlot;
         const float* sl = (const float*)(st + kStageBlk * 32 * kSlot) + ti;
         v16f acc = {}, Dc, Dn;
@@ -641,11 +559,7 @@ CPB_DEV v16f grouped_parts(const WeightStream& ws, int P, unsigned char* smem, c
             sc_c = sc_n;
         }
     };
-    if constexpr (DMA) {
-        for (int q = 0; q < P; q++) kpart(q, (q & 1) ? g_stage1 : g_stage0, (q & 1) ? g_stage0 : g_stage1);
-    } else {
-        for (int q = 0; q < P; q++) kpart(q, smem + (q & 1) * kStageBytes, nullptr);
-    }
+    for (int q = 0; q < P; q++) kpart(q, (q & 1) ? g_stage1 : g_stage0, (q & 1) ? g_stage0 : g_stage1);
     // the caller's bias, loaded at its start, into LDS for its epilogue
     if (threadIdx.x < nbias) bias_lds[threadIdx.x] = bias_v;
     __syncthreads();             // callers reuse the LDS
@@ -657,7 +571,6 @@ CPB_DEV v16f grouped_parts(const WeightStream& ws, int P, unsigned char* smem, c
 // waves: wave w = row tile w/2 of the group, gate (w even) or up (w odd).
 template <bool TRACE>
 __global__ __launch_bounds__(kGuThreads) __attribute__((amdgpu_waves_per_eu(2))) void k_gateup_grouped(GroupedArgs a) {
-    extern __shared__ __align__(16) unsigned char smem[];
     __shared__ int src[32];
     const int T = a.dff / 32, P = a.parts_gu, nb = a.nb;
     int tile, grp;
@@ -692,7 +605,7 @@ __global__ __launch_bounds__(kGuThreads) __attribute__((amdgpu_waves_per_eu(2)))
     }
     int32_t* tb = TRACE ? a.gu_sums + (((size_t)pair * 2 + isup) * a.dff + rt * 32) * nb : nullptr;
 
-    const v16f tot = grouped_parts<TRACE, kGuThreads, kGuDma>(ws, P, smem, a.ximg, a.xsb, (size_t)a.n_tok, nb, src, lane, tb,
+    const v16f tot = grouped_parts<TRACE, kGuThreads>(ws, P, a.ximg, a.xsb, (size_t)a.n_tok, nb, src, lane, tb,
                                           valid && live, bias_s, bias_v, 128);
     // SwiGLU, Q8 and image of the row tile, split over its two waves: the
     // lane's rows 8g + 4hb + c (g, c < 4) of groups g = isup and g = isup + 2
@@ -700,7 +613,7 @@ __global__ __launch_bounds__(kGuThreads) __attribute__((amdgpu_waves_per_eu(2)))
     // runs); each wave hands the partner the totals of the partner's rows
     // (LDS reused), then the block maximum is combined through LDS.
     const int rtl = w >> 1;
-    float* xch = (float*)(kGuDma ? g_stage0 : smem);      // [row tile][sender][8][64]
+    float* xch = (float*)g_stage0;                // [row tile][sender][8][64]
     float* mxs = xch + 2 * 2 * 8 * 64;            // [row tile][wave][64]
 #pragma unroll
     for (int j = 0; j < 8; j++) {
@@ -755,7 +668,6 @@ __global__ __launch_bounds__(kGuThreads) __attribute__((amdgpu_waves_per_eu(2)))
 // one workgroup per (token tile, group of 8 row tiles of 32 rows) (grouped_item).
 template <bool TRACE>
 __global__ __launch_bounds__(kDnThreads) void k_down_grouped(GroupedArgs a) {
-    extern __shared__ __align__(16) unsigned char smem[];
     __shared__ int src[32];
     int tile, grp;
     if (!grouped_item(uniform(*a.ntiles), (a.d / 32 + 7) / 8, &tile, &grp)) return;
@@ -787,7 +699,7 @@ __global__ __launch_bounds__(kDnThreads) void k_down_grouped(GroupedArgs a) {
     }
     int32_t* tb = TRACE ? a.dn_sums + ((size_t)pair * a.d + rt * 32) * nbf : nullptr;
 
-    const v16f tot = grouped_parts<TRACE, kDnThreads, false>(ws, P, smem, a.himg, a.hsb, (size_t)a.n_tok * a.k, nbf, src, lane,
+    const v16f tot = grouped_parts<TRACE, kDnThreads>(ws, P, a.himg, a.hsb, (size_t)a.n_tok * a.k, nbf, src, lane,
                                           tb, valid && live, bias_s, bias_v, 256);
     if (!valid || !live) return;
     float* out = a.dnout + (size_t)pair * a.d + rt * 32 + 4 * hb;
@@ -858,13 +770,12 @@ int launch_grouped_layer(const GroupedArgs& a, bool trace, hipStream_t s, const 
     // 8 slots per XCD round, enough for the largest tile count
     const int ngu = a.max_tiles * ((a.dff / 32 + 1) / 2), ndn = a.max_tiles * ((a.d / 32 + 7) / 8);
     const dim3 ggu((ngu + 7) / 8 * 8), gdn((ndn + 7) / 8 * 8);
-    const size_t lds = 2 * kStageBytes;        // two staging buffers (>= the 8 KB epilogue exchange)
     if (ev) armed_events() = ev[0];
-    if (trace) launch(k_gateup_grouped<true>, ggu, dim3(kGuThreads), kGuDma ? 0 : lds, s, a);
-    else launch(k_gateup_grouped<false>, ggu, dim3(kGuThreads), kGuDma ? 0 : lds, s, a);
+    if (trace) launch(k_gateup_grouped<true>, ggu, dim3(kGuThreads), 0, s, a);
+    else launch(k_gateup_grouped<false>, ggu, dim3(kGuThreads), 0, s, a);
     if (ev) armed_events() = ev[1];
-    if (trace) launch(k_down_grouped<true>, gdn, dim3(kDnThreads), lds, s, a);
-    else launch(k_down_grouped<false>, gdn, dim3(kDnThreads), lds, s, a);
+    if (trace) launch(k_down_grouped<true>, gdn, dim3(kDnThreads), 0, s, a);
+    else launch(k_down_grouped<false>, gdn, dim3(kDnThreads), 0, s, a);
     launch(k_combine_batch, dim3((unsigned)std::min<size_t>(((size_t)nt * (a.d / 4) + 255) / 256, 2048)), dim3(256), 0, s, a);
     return hipGetLastError() == hipSuccess ? 0 : -19;
 }
