@@ -645,16 +645,48 @@ __global__ __launch_bounds__(kGuThreads) __attribute__((amdgpu_waves_per_eu(2)))
     // e and e + 16 sit at adjacent K (2e, 2e + 1), so groups g and g + 2 fill
     // the 8 bytes K = 16 isup + 8hb .. +7 of each half
     uint8_t* img = a.himg + ((size_t)pair * a.nbf + rt) * kImg;
-    uint32_t qw[2] = {0u, 0u}, hi[2] = {0u, 0u}, lo[2] = {0u, 0u};
+    // Q8 of the 8 values (the exact division only when some lane's quotient
+    // lies near a rounding tie), then the bytes: qw[gh] byte c = value
+    // j = 4 gh + c; the image run's byte 2 (c & 1) + gh of word c >> 1 holds
+    // value j's 16h (hi) and l (lo) as e4m3, whose hardware conversion is
+    // exact for these integers (|16h| <= 128, 0 <= l <= 15)
+    int qv[8];
+    {
+        const float rs = __builtin_amdgcn_rcpf(sc);
+        float r[8];
+        bool near = false;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float y = hv[j] * rs;
+            r[j] = __builtin_rintf(y);
+            near = near || q8_near_half(y);
+        }
+        if (near) {
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                if (q8_near_half(hv[j] * rs)) r[j] = roundf(hv[j] / sc);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j++) qv[j] = q8_clamp(r[j]);
+    }
+    uint32_t qw[2] = {0u, 0u}, hi[2], lo[2];
+#pragma unroll
+    for (int j = 0; j < 8; j++) qw[j >> 2] |= ((uint32_t)qv[j] & 0xffu) << (8 * (j & 3));
+    float fh[8], fl[8];
 #pragma unroll
     for (int j = 0; j < 8; j++) {
-        const int gh = j >> 2, c = j & 3;                               // g = isup + 2 gh
-        const int qv = q8_round(hv[j], sc);
-        qw[gh] |= ((uint32_t)qv & 0xffu) << (8 * c);
-        const int h = qv >> 4;
-        const int sh = 8 * (2 * (c & 1) + gh);                          // byte 2c + gh of the run
-        hi[c >> 1] |= e4m3_small(16 * h) << sh;
-        lo[c >> 1] |= e4m3_small(qv - 16 * h) << sh;
+        const int h = qv[j] >> 4;
+        fh[j] = (float)(16 * h);
+        fl[j] = (float)(qv[j] - 16 * h);
+    }
+#pragma unroll
+    for (int w2 = 0; w2 < 2; w2++) {
+        // word w2: bytes (c = 2 w2, gh 0), (c = 2 w2, gh 1), (c = 2 w2 + 1, gh 0), (c = 2 w2 + 1, gh 1)
+        const int c0 = 2 * w2, c1 = 2 * w2 + 1;
+        hi[w2] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(fh[c1], fh[4 + c1],
+                                                            __builtin_amdgcn_cvt_pk_fp8_f32(fh[c0], fh[4 + c0], 0, false), true);
+        lo[w2] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(fl[c1], fl[4 + c1],
+                                                            __builtin_amdgcn_cvt_pk_fp8_f32(fl[c0], fl[4 + c0], 0, false), true);
     }
     uint32_t* hqw = (uint32_t*)(a.hq + (size_t)pair * a.dff + rt * 32 + 8 * isup + 4 * hb);
     hqw[0] = qw[0];
