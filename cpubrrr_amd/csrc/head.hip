@@ -299,7 +299,7 @@ __global__ __launch_bounds__(256) void k_head_screen(HeadDev a) {
 #pragma unroll 6
         for (int b = 0; b < nb; b++) {
             const uint64_t w = __builtin_nontemporal_load(wp + (size_t)b * kHeadRT);
-            const float sv = bf16f(sp[(size_t)b * kHeadRT]) * xsl[b];
+            const float sv = bf16f(__builtin_nontemporal_load(sp + (size_t)b * kHeadRT)) * xsl[b];
             const uint32_t w0 = (uint32_t)w, w1 = (uint32_t)(w >> 32);
 #pragma unroll
             for (int j = 0; j < 4; j++) {
@@ -322,7 +322,7 @@ __global__ __launch_bounds__(256) void k_head_screen(HeadDev a) {
 #pragma unroll 6
         for (int b = 0; b < nb; b++) {
             const u32x4 w = __builtin_nontemporal_load(wp + (size_t)b * kHeadRT);
-            const float sv = bf16f(sp[(size_t)b * kHeadRT]) * xsl[b];
+            const float sv = bf16f(__builtin_nontemporal_load(sp + (size_t)b * kHeadRT)) * xsl[b];
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 int t = sdot4(w[j] & 0x0F0F0F0Fu, xl[b * 8 + j], 0);
