@@ -274,6 +274,7 @@ __global__ __launch_bounds__(256) void k_head_norm(HeadDev a) {
 // Q2 (dot4_q2_i8, :403-428; head2_on() at :953-957 selects it), the same
 // lane order: lane part j = elements 4j..4j+3 and 16+4j..16+4j+3, an int
 // dot per block, acc_j = fma(t_j, bf16 scale * xsb, acc_j) ----
+constexpr int kScreenRing = 6;
 template <bool Q2>
 __global__ __launch_bounds__(256) void k_head_screen(HeadDev a) {
     extern __shared__ __align__(16) unsigned char smem[];
@@ -284,55 +285,99 @@ __global__ __launch_bounds__(256) void k_head_screen(HeadDev a) {
     __shared__ __align__(16) uint64_t rsk[4][64];
     __shared__ float lv[kHeadMaxSlices][4][kHeadMaxCand];
     __shared__ int li[kHeadMaxSlices][4][kHeadMaxCand];
-    for (int i = tid; i < nb * 8; i += blockDim.x) xl[i] = ((const uint32_t*)a.xq)[i];
-    for (int i = tid; i < nb; i += blockDim.x) xsl[i] = a.xsb[i];
-    for (int i = tid; i < nb * 4; i += blockDim.x) x8[i] = a.xs8[i];
-    __syncthreads();
     const int tile = blockIdx.x * 4 + wave;
     const bool live = tile * kHeadRT < a.Vpad;
     float val = -INFINITY;
     const int row = tile * kHeadRT + lane;
-    if (live && Q2) {
-        const uint64_t* wp = a.q2 + (size_t)tile * nb * kHeadRT + lane;
-        const uint16_t* sp = a.q2s + (size_t)tile * nb * kHeadRT + lane;
+    // Each lane streams its row's blocks through a ring of kScreenRing
+    // loads: block b's codes and scale are requested kScreenRing blocks
+    // before they are used, so the loads in flight never drain between
+    // groups.  Buffer loads over the tile's streams: requests past the last
+    // block fall outside the resource and fetch nothing; a wave past the last
+    // tile gets empty resources.  The ring's first loads go out before x is
+    // staged in LDS (they do not need it).
+    {
+        const size_t tb = live ? (size_t)tile * nb * kHeadRT : 0;
+        const uint32_t nr = live ? (uint32_t)(nb * kHeadRT) : 0u;
+        const __amdgpu_buffer_rsrc_t rw = Q2 ? buf_rsrc(a.q2 + tb, nr * 8) : buf_rsrc(a.q4 + tb, nr * 16);
+        const __amdgpu_buffer_rsrc_t rsc = buf_rsrc((Q2 ? a.q2s : a.q4s) + tb, nr * 2);
+        constexpr uint32_t ub = Q2 ? 8 : 16;                 // code bytes per lane and block
+        const uint32_t wo = (uint32_t)lane * ub, so = (uint32_t)lane * 2;
+        auto ldw = [&](int b) -> u32x4 {
+            if constexpr (Q2) {
+                const uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rw, wo, b * kHeadRT * (int)ub, 2));
+                return u32x4{v.x, v.y, 0u, 0u};
+            } else {
+                return __builtin_amdgcn_raw_buffer_load_b128(rw, wo, b * kHeadRT * (int)ub, 2);
+            }
+        };
+        // lane offsets in fixed registers, the block's offset in a scalar one
+        // (scales held as 32-bit values: 16-bit ones were packed in pairs
+        // across the loop, which waited for both loads)
+        auto lds = [&](int b) -> uint32_t { return __builtin_amdgcn_raw_buffer_load_b16(rsc, so, b * kHeadRT * 2, 2); };
         float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 6
-        for (int b = 0; b < nb; b++) {
-            const uint64_t w = __builtin_nontemporal_load(wp + (size_t)b * kHeadRT);
-            const float sv = bf16f(__builtin_nontemporal_load(sp + (size_t)b * kHeadRT)) * xsl[b];
-            const uint32_t w0 = (uint32_t)w, w1 = (uint32_t)(w >> 32);
+        u32x4 wq[kScreenRing];
+        uint32_t sq[kScreenRing];
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                // elements 4j..4j+3: bytes 4 (j & 1) .. +3, bits 2 (j >> 1);
-                // elements 16+4j..: the same bytes, bits 4 + 2 (j >> 1)
-                const uint32_t src = (j & 1) ? w1 : w0;
-                const int sh = 2 * (j >> 1);
-                int t = sdot4((src >> sh) & 0x03030303u, xl[b * 8 + j], 0);
-                t = sdot4((src >> (sh + 4)) & 0x03030303u, xl[b * 8 + 4 + j], t);
-                t -= 2 * x8[b * 4 + j];                    // codes are KVI2[c] = c - 2
-                acc[j] = fmaf((float)t, sv, acc[j]);
+        for (int k = 0; k < kScreenRing; k++) {
+            wq[k] = ldw(k);
+            sq[k] = lds(k);
+            __builtin_amdgcn_sched_barrier(0);          // the loop's order, for exact waits
+        }
+        for (int i = tid; i < nb * 8; i += blockDim.x) xl[i] = ((const uint32_t*)a.xq)[i];
+        for (int i = tid; i < nb; i += blockDim.x) xsl[i] = a.xsb[i];
+        for (int i = tid; i < nb * 4; i += blockDim.x) x8[i] = a.xs8[i];
+        __syncthreads();
+        auto block = [&](int b, const u32x4& w, float sv) {
+            if constexpr (Q2) {
+                const uint32_t w0 = w[0], w1 = w[1];
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    // elements 4j..4j+3: bytes 4 (j & 1) .. +3, bits 2 (j >> 1);
+                    // elements 16+4j..: the same bytes, bits 4 + 2 (j >> 1)
+                    const uint32_t src = (j & 1) ? w1 : w0;
+                    const int sh = 2 * (j >> 1);
+                    int t = sdot4((src >> sh) & 0x03030303u, xl[b * 8 + j], 0);
+                    t = sdot4((src >> (sh + 4)) & 0x03030303u, xl[b * 8 + 4 + j], t);
+                    t -= 2 * x8[b * 4 + j];                    // codes are KVI2[c] = c - 2
+                    acc[j] = fmaf((float)t, sv, acc[j]);
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    int t = sdot4(w[j] & 0x0F0F0F0Fu, xl[b * 8 + j], 0);
+                    t = sdot4((w[j] >> 4) & 0x0F0F0F0Fu, xl[b * 8 + 4 + j], t);
+                    t -= 8 * x8[b * 4 + j];                    // codes are KVI4[c] = c - 8
+                    acc[j] = fmaf((float)t, sv, acc[j]);
+                }
+            }
+        };
+        // whole groups with no branch inside (a branch there made the
+        // compiler wait for every load in flight at each block), then the
+        // last nb % kScreenRing blocks from the ring
+        const int nfull = nb - nb % kScreenRing;
+        for (int b0 = 0; b0 < nfull; b0 += kScreenRing) {
+#pragma unroll
+            for (int k = 0; k < kScreenRing; k++) {
+                const int b = b0 + k;
+                block(b, wq[k], bf16f(sq[k]) * xsl[b]);
+                // the refill after the block's last use of its registers, so
+                // that it lands in the same ones (a refill issued before the
+                // use left the loop rotating copies that waited for every
+                // load), and kept there
+                __builtin_amdgcn_sched_barrier(0);
+                wq[k] = ldw(b + kScreenRing);
+                sq[k] = lds(b + kScreenRing);
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
-        val = (acc[0] + acc[1]) + (acc[2] + acc[3]);
-        a.screen[row] = val;
-    } else if (live) {
-        const u32x4* wp = a.q4 + (size_t)tile * nb * kHeadRT + lane;
-        const uint16_t* sp = a.q4s + (size_t)tile * nb * kHeadRT + lane;
-        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 6
-        for (int b = 0; b < nb; b++) {
-            const u32x4 w = __builtin_nontemporal_load(wp + (size_t)b * kHeadRT);
-            const float sv = bf16f(__builtin_nontemporal_load(sp + (size_t)b * kHeadRT)) * xsl[b];
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                int t = sdot4(w[j] & 0x0F0F0F0Fu, xl[b * 8 + j], 0);
-                t = sdot4((w[j] >> 4) & 0x0F0F0F0Fu, xl[b * 8 + 4 + j], t);
-                t -= 8 * x8[b * 4 + j];                    // codes are KVI4[c] = c - 8
-                acc[j] = fmaf((float)t, sv, acc[j]);
-            }
+        for (int k = 0; k < kScreenRing - 1; k++)
+            if (nfull + k < nb) block(nfull + k, wq[k], bf16f(sq[k]) * xsl[nfull + k]);
+        if (live) {
+            val = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+            a.screen[row] = val;
         }
-        val = (acc[0] + acc[1]) + (acc[2] + acc[3]);
-        a.screen[row] = val;
     }
     // the workgroup's best n_cand rows in each worker slice it meets (a slice's
     // best n_cand are among its row groups' best n_cand): per tile by rank,
