@@ -70,16 +70,13 @@ CPB_DEV int d_row(int i, int hb) { return 8 * (i >> 2) + 4 * hb + (i & 3); }
 
 // Q4_K scale / min bytes of one superblock header (unit 0: d, dmin, 12
 // packed bytes; engine_qwen2.rs:57-74 get_scale_min_k4)
-CPB_DEV void unpack_q4k(const u32x4& u0, uint8_t* sc, uint8_t* mn) {
+CPB_DEV u32x4 unpack_q4k(const u32x4& u0) {
+    // sc[0..7] in words 0-1, mn[0..7] in words 2-3: bytes j < 4 are the low
+    // six bits of bytes j of q[0..3] / q[4..7]; bytes 4 + j take the low /
+    // high nibble of q[8 + j] and, as bits 4-5, the top two bits of byte j
     const uint32_t q03 = u0[1], q47 = u0[2], q811 = u0[3];
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        sc[j] = (q03 >> (8 * j)) & 63;
-        mn[j] = (q47 >> (8 * j)) & 63;
-        const uint32_t qj4 = (q811 >> (8 * j)) & 0xff;
-        sc[4 + j] = (qj4 & 0xf) | (((q03 >> (8 * j + 6)) & 3) << 4);
-        mn[4 + j] = (qj4 >> 4) | (((q47 >> (8 * j + 6)) & 3) << 4);
-    }
+    return u32x4{q03 & 0x3F3F3F3Fu, (q811 & 0x0F0F0F0Fu) | ((q03 >> 2) & 0x30303030u), q47 & 0x3F3F3F3Fu,
+                 ((q811 >> 4) & 0x0F0F0F0Fu) | ((q47 >> 2) & 0x30303030u)};
 }
 
 // ---- per token: rmsnorm + Q8_K per 256 (engine_qwen2.rs:287-300, the
@@ -181,7 +178,7 @@ template <bool TRACE, bool STAGED>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_gateup_kq_grouped(GroupedArgs a) {
     extern __shared__ __align__(16) unsigned char kst[];
     __shared__ int src[32];
-    __shared__ uint8_t s_sm[4][32][16];          // per wave and row: sc[8], mn[8]
+    __shared__ __align__(16) uint8_t s_sm[4][32][16];          // per wave and row: sc[8], mn[8]
     __shared__ float s_dm[4][32][2];             // d, dmin
     __shared__ float xch_s[STAGED ? 1 : 2 * 16 * 64];
     // up results to the gate waves (the staging area once the products are done)
@@ -253,7 +250,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
         }
         }
         if (hb == 0) {
-            unpack_q4k(u0, &s_sm[w][r][0], &s_sm[w][r][8]);
+            *(u32x4*)&s_sm[w][r][0] = unpack_q4k(u0);
             s_dm[w][r][0] = half_bits(u0[0] & 0xffffu);
             s_dm[w][r][1] = half_bits(u0[0] >> 16);
         }
@@ -360,7 +357,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     constexpr int U = TYPE == 12 ? kQ4Units : kQ6StreamUnits;   // units per superblock in the stream
     extern __shared__ __align__(16) unsigned char kst[];
     __shared__ int src[32];
-    __shared__ uint8_t s_sm[4][32][16];          // Q4_K: sc[8], mn[8]; Q6_K: int8 scales[16]
+    __shared__ __align__(16) uint8_t s_sm[4][32][16];          // Q4_K: sc[8], mn[8]; Q6_K: int8 scales[16]
     __shared__ float s_dm[4][32][2];
     const int nsbf = a.dff / 256, RT = 64 / a.k, Td = a.d / RT, T32 = a.d / 32;
     int tile, grp;
@@ -444,7 +441,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
             for (int j = 0; j < 8; j++) xs8[j] = pair >= 0 ? a.hsum[(size_t)pair * (a.dff / 32) + sb * 8 + j] : 0;
             }
             if (hb == 0) {
-                unpack_q4k(u0, &s_sm[w][r][0], &s_sm[w][r][8]);
+                *(u32x4*)&s_sm[w][r][0] = unpack_q4k(u0);
                 s_dm[w][r][0] = half_bits(u0[0] & 0xffffu);
                 s_dm[w][r][1] = half_bits(u0[0] >> 16);
             }
