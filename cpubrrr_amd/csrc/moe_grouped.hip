@@ -378,11 +378,24 @@ __global__ __launch_bounds__(1024) void k_group_dense(GroupedArgs a) {
 
 // One block of the grouped product: A = 16 raw code bytes (both K halves),
 // B = the 32-byte half-image, hardware scale = the block's e8m0 byte.
-CPB_DEV v16f mx_block_mfma(const u32x4& w, const u32x4& x0, const u32x4& x1, uint32_t e) {
+// SEL: which byte of the word ew is the block's e8m0 (the instruction's
+// scale operand select), so four blocks share one scale register
+template <int SEL>
+CPB_DEV v16f mx_block_mfma(const u32x4& w, const u32x4& x0, const u32x4& x1, uint32_t ew) {
     const v8i_g A = {(int)w[0], (int)w[1], (int)w[2], (int)w[3], 0, 0, 0, 0};
     const v8i_g B = {(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3], (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
     const v16f Z = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(A, B, Z, 4, 0, 0, (int)e, 0, 127);
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(A, B, Z, 4, 0, SEL, (int)ew, 0, 127);
+}
+// the same with the byte index a value that is constant once the caller's
+// loop is unrolled
+CPB_DEV v16f mx_block_mfma_b(const u32x4& w, const u32x4& x0, const u32x4& x1, uint32_t ew, int sel) {
+    switch (sel & 3) {
+        case 0: return mx_block_mfma<0>(w, x0, x1, ew);
+        case 1: return mx_block_mfma<1>(w, x0, x1, ew);
+        case 2: return mx_block_mfma<2>(w, x0, x1, ew);
+        default: return mx_block_mfma<3>(w, x0, x1, ew);
+    }
 }
 
 // LDS staging of one k-part's activations for a 32-token tile: per block i
@@ -428,7 +441,9 @@ CPB_DEV DmaPlan dma_plan(const uint8_t* img, const float* sc, size_t rows, int n
 }
 template <int NT>
 CPB_DEV void stage_dma(const DmaPlan& p, int nbk, int q, unsigned char* st) {
-    const int w = threadIdx.x >> 6, L = threadIdx.x & 63;
+    // the wave index as a scalar: every condition and LDS address below is
+    // then scalar work
+    const int w = uniform((int)(threadIdx.x >> 6)), L = threadIdx.x & 63;
     const int lim = min(kBlkPerPart, nbk - q * kBlkPerPart);
 #pragma unroll
     for (int k = 0; k < (2 * kBlkPerPart + NT / 64 - 1) / (NT / 64); k++) {
@@ -515,7 +530,7 @@ CPB_DEV v16f grouped_parts(const WeightStream& ws, int P, const uint8_t* img, co
         }
         {
             sc_c = sa[0];
-            Dc = mx_block_mfma(wv[1], xa[0][0], xa[0][1], ex[0] & 0xffu);
+            Dc = mx_block_mfma<0>(wv[1], xa[0][0], xa[0][1], ex[0]);
             wv[1] = wload(ws, qn, 1);
             xa[0][0] = *(const u32x4*)(xp + 2 * 32 * kSlot + o0);
             xa[0][1] = *(const u32x4*)(xp + 2 * 32 * kSlot + o1);
@@ -526,7 +541,7 @@ CPB_DEV v16f grouped_parts(const WeightStream& ws, int P, const uint8_t* img, co
             if (i + 1 < kBlkPerPart) {
                 const int j = i + 1, bj = j & 1;
                 sc_n = sa[bj];
-                Dn = mx_block_mfma(wv[1 + j], xa[bj][0], xa[bj][1], (ex[j >> 2] >> (8 * (j & 3))) & 0xffu);
+                Dn = mx_block_mfma_b(wv[1 + j], xa[bj][0], xa[bj][1], ex[j >> 2], j);
                 wv[1 + j] = wload(ws, qn, 1 + j);
                 if (j + 2 < kBlkPerPart) {
                     xa[bj][0] = *(const u32x4*)(xp + (j + 2) * 32 * kSlot + o0);
