@@ -39,7 +39,7 @@ sys.path.insert(0, str(ROOT))
 # bench cannot read hardware counters itself (they need a profiler run of
 # their own), so each line names the profile its figure comes from.
 MEASURED_TRAFFIC = {"k_gateup_mx": 35_815_144, "k_gateup_kq": 14_418_124,
-                    "k_gateup_grouped": 537_580_042, "k_gateup_kq_grouped": 282_813_378,
+                    "k_gateup_grouped": 532_770_153, "k_gateup_kq_grouped": 282_353_586,
                     "head": 327_526_064}
 TRAFFIC_SOURCE = {"k_gateup_mx": "profiles/hbm_traffic_config1_phased.md",
                   "k_gateup_kq": "profiles/hbm_traffic_config3_qwen.md",
