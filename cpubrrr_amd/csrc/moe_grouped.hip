@@ -49,18 +49,6 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 
 constexpr int kImg = 64;          // image bytes per 32-block
 
-// exact e4m3 encodings used by the split (v = 0, an integer in [1, 15] or 16*h)
-CPB_DEV uint32_t e4m3_small(int v) {
-    if (v == 0) return 0;
-    const uint32_t s = v < 0 ? 0x80u : 0u;
-    const uint32_t a = (uint32_t)(v < 0 ? -v : v);
-    const int E = 31 - __builtin_clz(a);
-    const uint32_t m = E >= 3 ? (a >> (E - 3)) & 7u : (a << (3 - E)) & 7u;
-    return s | ((uint32_t)(E + 7) << 3) | m;
-}
-CPB_DEV int k_of_elem(int e) { return e < 16 ? 2 * e : 2 * (e - 16) + 1; }
-// byte offsets of element e's two image bytes within its block
-CPB_DEV int img_hi_off(int e) { const int K = k_of_elem(e); return (K >> 4) * 32 + (K & 15); }
 
 // ---- 1. per token: rmsnorm, Q8 per 32, fp8 image ----
 __global__ __launch_bounds__(256) void k_prep_batch(GroupedArgs a) {
@@ -71,23 +59,58 @@ __global__ __launch_bounds__(256) void k_prep_batch(GroupedArgs a) {
     float* scratch = xnl + d;
     norm_into(a.x + (size_t)t * d, a.norm_w, d, a.eps, a.norm, a.norm_nt, a.apply_norm, xs, xnl, scratch);
     if (tid == 0) a.inv[t] = a.apply_norm ? scratch[16] : 1.0f;
-    // Q8 per 32-block (engine_gpt2.rs:691-699): 32 lanes per block
-    const int l = tid & 31;
-    for (int bk = tid >> 5; bk < a.nb; bk += nth >> 5) {
-        const float v = xnl[bk * 32 + l];
-        float m = fabsf(v);
+    // Q8 per 32-block (engine_gpt2.rs:691-699), one thread per block (no
+    // cross-lane reductions on the token's critical path): the block's
+    // maximum, its 32 codes (the exact division only near a rounding tie),
+    // then xn, xq, the scale and the 64-byte image as 16-byte stores.
+    // Image byte K of a half (K < 16: first 16 bytes, 16h; the next 16: l;
+    // then the same for K 16..31) holds element K / 2 (K even) or
+    // 16 + (K - 1) / 2 (K odd), so dword w of a part packs elements 2w,
+    // 16 + 2w, 2w + 1, 17 + 2w (+ 8 for the second part); their e4m3 codes
+    // come from the hardware conversion, exact for these integers.
+    for (int bk = tid; bk < a.nb; bk += nth) {
+        float v[32];
 #pragma unroll
-        for (int s2 = 16; s2 >= 1; s2 >>= 1) m = fmaxf(m, __shfl_xor(m, s2));
+        for (int i = 0; i < 8; i++) {
+            const float4 f = ((const float4*)(xnl + bk * 32))[i];
+            v[4 * i] = f.x; v[4 * i + 1] = f.y; v[4 * i + 2] = f.z; v[4 * i + 3] = f.w;
+        }
+        float m = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 32; i++) m = fmaxf(m, fabsf(v[i]));
         const float sc = fmaxf(1e-12f, m) / 127.0f;
-        const int q = q8_round(v, sc);
-        a.xn[(size_t)t * d + bk * 32 + l] = v;
-        a.xq[(size_t)t * d + bk * 32 + l] = (int8_t)q;
-        if (l == 0) a.xsb[(size_t)t * a.nb + bk] = sc;
-        const int h = q >> 4;
-        uint8_t* img = a.ximg + ((size_t)t * a.nb + bk) * kImg;
-        const int o = img_hi_off(l);
-        img[o] = (uint8_t)e4m3_small(16 * h);
-        img[o + 16] = (uint8_t)e4m3_small(q - 16 * h);
+        uint32_t qw[8];
+        q8_round16(v, sc, qw);
+        q8_round16(v + 16, sc, qw + 4);
+        float4* xo = (float4*)(a.xn + (size_t)t * d + bk * 32);
+#pragma unroll
+        for (int i = 0; i < 8; i++) xo[i] = float4{v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]};
+        u32x4* qo = (u32x4*)(a.xq + (size_t)t * d + bk * 32);
+        qo[0] = u32x4{qw[0], qw[1], qw[2], qw[3]};
+        qo[1] = u32x4{qw[4], qw[5], qw[6], qw[7]};
+        a.xsb[(size_t)t * a.nb + bk] = sc;
+        float fh[32], fl[32];
+#pragma unroll
+        for (int e = 0; e < 32; e++) {
+            const int q = (int)(int8_t)((qw[e >> 2] >> (8 * (e & 3))) & 0xffu), h = q >> 4;
+            fh[e] = (float)(16 * h);
+            fl[e] = (float)(q - 16 * h);
+        }
+        uint32_t im[16];
+#pragma unroll
+        for (int pt = 0; pt < 2; pt++) {
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                const int e0 = 8 * pt + 2 * w;
+                im[8 * pt + w] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(
+                    fh[e0 + 1], fh[e0 + 17], __builtin_amdgcn_cvt_pk_fp8_f32(fh[e0], fh[e0 + 16], 0, false), true);
+                im[8 * pt + 4 + w] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(
+                    fl[e0 + 1], fl[e0 + 17], __builtin_amdgcn_cvt_pk_fp8_f32(fl[e0], fl[e0 + 16], 0, false), true);
+            }
+        }
+        u32x4* io = (u32x4*)(a.ximg + ((size_t)t * a.nb + bk) * kImg);
+#pragma unroll
+        for (int i = 0; i < 4; i++) io[i] = u32x4{im[4 * i], im[4 * i + 1], im[4 * i + 2], im[4 * i + 3]};
     }
 }
 
