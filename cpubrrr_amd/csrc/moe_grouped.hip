@@ -59,58 +59,78 @@ __global__ __launch_bounds__(256) void k_prep_batch(GroupedArgs a) {
     float* scratch = xnl + d;
     norm_into(a.x + (size_t)t * d, a.norm_w, d, a.eps, a.norm, a.norm_nt, a.apply_norm, xs, xnl, scratch);
     if (tid == 0) a.inv[t] = a.apply_norm ? scratch[16] : 1.0f;
-    // Q8 per 32-block (engine_gpt2.rs:691-699), one thread per block (no
-    // cross-lane reductions on the token's critical path): the block's
-    // maximum, its 32 codes (the exact division only near a rounding tie),
-    // then xn, xq, the scale and the 64-byte image as 16-byte stores.
-    // Image byte K of a half (K < 16: first 16 bytes, 16h; the next 16: l;
-    // then the same for K 16..31) holds element K / 2 (K even) or
-    // 16 + (K - 1) / 2 (K odd), so dword w of a part packs elements 2w,
-    // 16 + 2w, 2w + 1, 17 + 2w (+ 8 for the second part); their e4m3 codes
-    // come from the hardware conversion, exact for these integers.
-    for (int bk = tid; bk < a.nb; bk += nth) {
-        float v[32];
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const float4 f = ((const float4*)(xnl + bk * 32))[i];
-            v[4 * i] = f.x; v[4 * i + 1] = f.y; v[4 * i + 2] = f.z; v[4 * i + 3] = f.w;
-        }
+    // Q8 per 32-block (engine_gpt2.rs:691-699), four threads per block:
+    // thread c owns elements 8p + 4h .. +3 and 16 + 8p + 4h .. +3 (p = c >> 1,
+    // h = c & 1), so its share of xq is two whole dwords and its share of the
+    // 64-byte image two whole 8-byte runs.  Image byte K of a part (K < 16:
+    // bytes 0-15, 16h; bytes 16-31, l; then the same for K 16..31 at 32-63)
+    // holds element K / 2 (K even) or 16 + (K - 1) / 2 (K odd): dword w of part
+    // p packs elements 8p + 2w, 8p + 2w + 16, 8p + 2w + 1, 8p + 2w + 17.  The
+    // e4m3 codes come from the hardware conversion, exact for these integers;
+    // the block maximum from two lane exchanges; the exact division only
+    // near a rounding tie.
+    for (int i = tid; i < a.nb * 4; i += nth) {
+        const int bk = i >> 2, c = i & 3, p = c >> 1, h = c & 1;
+        const int e0 = 8 * p + 4 * h;
+        const float4 f0 = ((const float4*)(xnl + bk * 32 + e0))[0];
+        const float4 f1 = ((const float4*)(xnl + bk * 32 + 16 + e0))[0];
+        const float v[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
         float m = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 32; i++) m = fmaxf(m, fabsf(v[i]));
+        for (int k = 0; k < 8; k++) m = fmaxf(m, fabsf(v[k]));
+        m = fmaxf(m, __shfl_xor(m, 1));
+        m = fmaxf(m, __shfl_xor(m, 2));
         const float sc = fmaxf(1e-12f, m) / 127.0f;
-        uint32_t qw[8];
-        q8_round16(v, sc, qw);
-        q8_round16(v + 16, sc, qw + 4);
-        float4* xo = (float4*)(a.xn + (size_t)t * d + bk * 32);
+        int q[8];
+        {
+            const float rs = __builtin_amdgcn_rcpf(sc);
+            float r[8];
+            bool near = false;
 #pragma unroll
-        for (int i = 0; i < 8; i++) xo[i] = float4{v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]};
-        u32x4* qo = (u32x4*)(a.xq + (size_t)t * d + bk * 32);
-        qo[0] = u32x4{qw[0], qw[1], qw[2], qw[3]};
-        qo[1] = u32x4{qw[4], qw[5], qw[6], qw[7]};
-        a.xsb[(size_t)t * a.nb + bk] = sc;
-        float fh[32], fl[32];
-#pragma unroll
-        for (int e = 0; e < 32; e++) {
-            const int q = (int)(int8_t)((qw[e >> 2] >> (8 * (e & 3))) & 0xffu), h = q >> 4;
-            fh[e] = (float)(16 * h);
-            fl[e] = (float)(q - 16 * h);
-        }
-        uint32_t im[16];
-#pragma unroll
-        for (int pt = 0; pt < 2; pt++) {
-#pragma unroll
-            for (int w = 0; w < 4; w++) {
-                const int e0 = 8 * pt + 2 * w;
-                im[8 * pt + w] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(
-                    fh[e0 + 1], fh[e0 + 17], __builtin_amdgcn_cvt_pk_fp8_f32(fh[e0], fh[e0 + 16], 0, false), true);
-                im[8 * pt + 4 + w] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(
-                    fl[e0 + 1], fl[e0 + 17], __builtin_amdgcn_cvt_pk_fp8_f32(fl[e0], fl[e0 + 16], 0, false), true);
+            for (int k = 0; k < 8; k++) {
+                const float y = v[k] * rs;
+                r[k] = __builtin_rintf(y);
+                near = near || q8_near_half(y);
             }
-        }
-        u32x4* io = (u32x4*)(a.ximg + ((size_t)t * a.nb + bk) * kImg);
+            if (near) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) io[i] = u32x4{im[4 * i], im[4 * i + 1], im[4 * i + 2], im[4 * i + 3]};
+                for (int k = 0; k < 8; k++)
+                    if (q8_near_half(v[k] * rs)) r[k] = roundf(v[k] / sc);
+            }
+#pragma unroll
+            for (int k = 0; k < 8; k++) q[k] = q8_clamp(r[k]);
+        }
+        uint32_t qw[2] = {0u, 0u};
+#pragma unroll
+        for (int k = 0; k < 8; k++) qw[k >> 2] |= ((uint32_t)q[k] & 0xffu) << (8 * (k & 3));
+        float* xo = a.xn + (size_t)t * d + bk * 32;
+        *(float4*)(xo + e0) = f0;
+        *(float4*)(xo + 16 + e0) = f1;
+        uint32_t* qo = (uint32_t*)(a.xq + (size_t)t * d + bk * 32);
+        qo[e0 >> 2] = qw[0];
+        qo[(16 + e0) >> 2] = qw[1];
+        if (c == 0) a.xsb[(size_t)t * a.nb + bk] = sc;
+        // elements e0 + j (k = j) and 16 + e0 + j (k = 4 + j), j < 4: dwords
+        // w = 2h and 2h + 1 of part p pack (e0 + 2(w - 2h), its +16, +1, +17)
+        float fh[8], fl[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const int hh = q[k] >> 4;
+            fh[k] = (float)(16 * hh);
+            fl[k] = (float)(q[k] - 16 * hh);
+        }
+        uint32_t hi[2], lo[2];
+#pragma unroll
+        for (int w = 0; w < 2; w++) {
+            const int j = 2 * w;             // elements e0 + j, 16 + e0 + j, e0 + j + 1, 16 + e0 + j + 1
+            hi[w] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(fh[j + 1], fh[4 + j + 1],
+                                                               __builtin_amdgcn_cvt_pk_fp8_f32(fh[j], fh[4 + j], 0, false), true);
+            lo[w] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(fl[j + 1], fl[4 + j + 1],
+                                                               __builtin_amdgcn_cvt_pk_fp8_f32(fl[j], fl[4 + j], 0, false), true);
+        }
+        uint8_t* img = a.ximg + ((size_t)t * a.nb + bk) * kImg + 32 * p + 8 * h;
+        *(uint2*)img = make_uint2(hi[0], hi[1]);
+        *(uint2*)(img + 16) = make_uint2(lo[0], lo[1]);
     }
 }
 
