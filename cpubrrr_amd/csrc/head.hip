@@ -250,11 +250,28 @@ __global__ __launch_bounds__(256) void k_head_norm(HeadDev a) {
         m = fmaxf(m, dpp_fh<0xB1>(m));
         m = fmaxf(m, dpp_fh<0x4E>(m));
         const float sc = fmaxf(1e-12f, m) / 127.0f;
+        // q8_round of the 8 values, the exact division only near a tie
+        float r[8];
+        {
+            const float rs = __builtin_amdgcn_rcpf(sc);
+            bool near = false;
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const float y = v[u] * rs;
+                r[u] = __builtin_rintf(y);
+                near = near || q8_near_half(y);
+            }
+            if (near) {
+#pragma unroll
+                for (int u = 0; u < 8; u++)
+                    if (q8_near_half(v[u] * rs)) r[u] = roundf(v[u] / sc);
+            }
+        }
         uint32_t wd[2] = {0u, 0u};
         int slo = 0, shi = 0;
 #pragma unroll
         for (int u = 0; u < 8; u++) {
-            const int qv = q8_round(v[u], sc);
+            const int qv = q8_clamp(r[u]);
             wd[u >> 2] |= (uint32_t)(uint8_t)qv << (8 * (u & 3));
             if (u < 4) slo += qv; else shi += qv;
         }
