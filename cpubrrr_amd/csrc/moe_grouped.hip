@@ -235,187 +235,62 @@ __global__ __launch_bounds__(64) void k_select_batch(GroupedArgs a) {
     si.logits = a.logits + (size_t)t * a.ne;      // written by every workgroup: one per token
     select_topk_wave<8, 4>(si, smem, &sel, true);
     if (lane < a.k) {
-        a.ids[(size_t)t * a.k + lane] = sel.ids[lane];
+        const int e = sel.ids[lane];
+        a.ids[(size_t)t * a.k + lane] = e;
         a.wts[(size_t)t * a.k + lane] = sel.wts[lane];
     }
     if (lane == 0) a.fallback[t] = sel.fallback;
 }
 
-// ---- 4. group the (token, slot) pairs by expert (stable), tile table ----
-// Batches whose token x expert table exceeds its LDS budget (k_group_dense
-// below handles the others).  One workgroup of 16 waves; wave w takes a contiguous run of pairs.  Per
-// 64-pair group a wave ranks its lanes among those of the same expert with one
-// ballot per distinct expert present (not per expert of the layer), keeping
-// a running per-wave count per expert in LDS; the waves' counts are then
-// scanned (expert major, wave minor), so the order is stable: by expert, then
-// by pair index.  Pair ranks stay in registers (np <= kGroupMax).
-constexpr int kGroupWaves = 16, kGroupMax = kGroupWaves * 64 * 16;
-__global__ __launch_bounds__(1024) void k_group(GroupedArgs a) {
-    __shared__ int wcnt[kGroupWaves][256];
-    __shared__ int off_l[256], toff_l[256], cnt_l[256];
+// ---- 4. grouping by expert ----
+// One workgroup: each pair takes its place among its expert's pairs from an
+// LDS counter (arrival order: any order serves, a pair's outputs do not
+// depend on its tile or on the other pairs there), then the exclusive prefix
+// of the counts (pairs and 32-pair tiles), each pair written at its expert's
+// offset + its place, and the tile list.
+constexpr int kScanPer = 16;                   // pairs per thread held in registers
+__global__ __launch_bounds__(1024) void k_group_scan(GroupedArgs a) {
+    __shared__ int cnt_l[256], off_l[256], toff_l[256];
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const int np = a.n_tok * a.k, ne = a.ne;
-    const uint64_t lt = lane ? (~0ull >> (64 - lane)) : 0ull;
-    for (int i = tid; i < kGroupWaves * 256; i += blockDim.x) (&wcnt[0][0])[i] = 0;
-    const int per = (np + kGroupWaves * 64 - 1) / (kGroupWaves * 64) * 64;     // pairs per wave, whole groups
-    const int p0 = w * per;
-    // this lane's pairs (up to 16 groups) and experts
-    int ex[16], rk[16];
+    for (int e = tid; e < ne; e += blockDim.x) cnt_l[e] = 0;
+    // every pair's expert requested before the first wait
+    int ex[kScanPer], rk[kScanPer];
 #pragma unroll
-    for (int g = 0; g < 16; g++) {
-        const int p = p0 + 64 * g + lane;
-        ex[g] = (64 * g < per && p < np) ? a.ids[p] : -1;
+    for (int u = 0; u < kScanPer; u++) {
+        const int p = tid + u * 1024;
+        ex[u] = p < np ? a.ids[p] : -1;
     }
     __syncthreads();
 #pragma unroll
-    for (int g = 0; g < 16; g++) {
-        rk[g] = 0;
-        if (64 * g >= per) continue;
-        uint64_t active = __ballot(ex[g] >= 0);
-        while (active) {
-            const int leader = __builtin_ctzll(active);
-            const int e0 = __builtin_amdgcn_readlane(ex[g], leader);
-            const uint64_t m = __ballot(ex[g] == e0);
-            const int base = wcnt[w][e0];
-            if (ex[g] == e0) rk[g] = base + __popcll(m & lt);
-            __builtin_amdgcn_wave_barrier();
-            if (lane == leader) wcnt[w][e0] = base + __popcll(m);
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            active &= ~m;
-        }
-    }
+    for (int u = 0; u < kScanPer; u++)
+        rk[u] = ex[u] >= 0 ? __hip_atomic_fetch_add(cnt_l + ex[u], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) : 0;
     __syncthreads();
-    // per expert: total, exclusive prefix over experts (counts and 32-pair tiles)
     if (w == 0) {
         int o = 0, to = 0;
         for (int base = 0; base < ne; base += 64) {
             const int e = base + lane;
-            int c = 0;
-            if (e < ne)
-                for (int v = 0; v < kGroupWaves; v++) c += wcnt[v][e];
-            const int t = (c + 31) / 32;
-            int ic = c, it = t;
+            const int c = e < ne ? cnt_l[e] : 0;
+            const int tl = (c + 31) / 32;
+            int ic = c, it = tl;
 #pragma unroll
             for (int s2 = 1; s2 < 64; s2 <<= 1) {
                 const int uc = __shfl_up(ic, s2), ut = __shfl_up(it, s2);
                 if (lane >= s2) { ic += uc; it += ut; }
             }
-            if (e < ne) { off_l[e] = o + ic - c; toff_l[e] = to + it - t; cnt_l[e] = c; }
+            if (e < ne) { off_l[e] = o + ic - c; toff_l[e] = to + it - tl; }
             o += __shfl(ic, 63);
             to += __shfl(it, 63);
         }
         if (lane == 0) *a.ntiles = to;
     }
     __syncthreads();
-    // wave offsets within each expert: in place, expert-parallel
-    for (int e = tid; e < ne; e += blockDim.x) {
-        int run = off_l[e];
-        for (int v = 0; v < kGroupWaves; v++) {
-            const int c = wcnt[v][e];
-            wcnt[v][e] = run;
-            run += c;
-        }
-    }
-    __syncthreads();
 #pragma unroll
-    for (int g = 0; g < 16; g++)
-        if (ex[g] >= 0) a.sorted[wcnt[w][ex[g]] + rk[g]] = p0 + 64 * g + lane;
-    for (int e = w; e < ne; e += kGroupWaves) {
+    for (int u = 0; u < kScanPer; u++)
+        if (ex[u] >= 0) a.sorted[off_l[ex[u]] + rk[u]] = tid + u * 1024;
+    for (int e = w; e < ne; e += 16) {
         const int c = cnt_l[e], nt = (c + 31) / 32;
         for (int j = lane; j < nt; j += 64) a.tiles[toff_l[e] + j] = int4{e, off_l[e] + 32 * j, min(32, c - 32 * j), 0};
-    }
-}
-
-// The same grouping from a token x expert table in LDS, for batches whose
-// table fits (n_tok * ne <= kGroupDenseMax bytes).  A token's k experts are
-// distinct, so the stable rank of pair (t, slot) among its expert's pairs is
-// the number of earlier tokens that chose that expert.  Byte M[t][e] = slot +
-// 1 of expert e in token t (0: not chosen); thread (e, part) counts column e
-// over its run of tokens, the counts are scanned expert major, part minor,
-// and the thread writes its column's pairs in token order: sorted is the
-// pair-ranking kernel's, entry for entry, with no per-expert ballots.
-constexpr int kGroupDenseMax = 128 * 1024;
-CPB_DEV_HOST_INLINE size_t group_dense_lds(int n_tok, int ne) {
-    return ((size_t)n_tok * ne + 15) / 16 * 16 + sizeof(int) * (1024 + 3 * 256);
-}
-__global__ __launch_bounds__(1024) void k_group_dense(GroupedArgs a) {
-    extern __shared__ __align__(16) unsigned char smem[];
-    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
-    const int nt = a.n_tok, ne = a.ne, k = a.k, np = nt * k;
-    const size_t mb = ((size_t)nt * ne + 15) / 16 * 16;
-    uint8_t* M = smem;
-    int* cnt = (int*)(smem + mb);                         // [P][ne]
-    int* off_l = cnt + 1024;
-    int* toff_l = off_l + 256;
-    int* cnt_l = toff_l + 256;
-    for (size_t i = tid; i < mb / 16; i += 1024) ((u32x4*)M)[i] = u32x4{0, 0, 0, 0};
-    __syncthreads();
-    for (int p = tid; p < np; p += 1024) {
-        const int t = p / k;
-        M[(size_t)t * ne + a.ids[p]] = (uint8_t)(p - t * k + 1);
-    }
-    __syncthreads();
-    const int P = 1024 / ne, e = tid % ne, part = tid / ne;
-    const bool act = part < P;
-    const int tpp = (nt + P - 1) / P, t0 = act ? part * tpp : 0, t1 = act ? min(nt, t0 + tpp) : 0;
-    // the run's bytes eight at a time: every read of a group issued before
-    // any is used (one at a time, each read's latency was paid in turn)
-    int c = 0;
-    int t = t0;
-    for (; t + 8 <= t1; t += 8) {
-        uint8_t v[8];
-#pragma unroll
-        for (int u = 0; u < 8; u++) v[u] = M[(size_t)(t + u) * ne + e];
-#pragma unroll
-        for (int u = 0; u < 8; u++) c += v[u] != 0;
-    }
-    for (; t < t1; t++) c += M[(size_t)t * ne + e] != 0;
-    if (act) cnt[part * ne + e] = c;
-    __syncthreads();
-    // per expert: total, exclusive prefix over experts (counts and 32-pair tiles)
-    if (w == 0) {
-        int o = 0, to = 0;
-        for (int base = 0; base < ne; base += 64) {
-            const int ee = base + lane;
-            int ce = 0;
-            if (ee < ne)
-                for (int v = 0; v < P; v++) ce += cnt[v * ne + ee];
-            const int tl = (ce + 31) / 32;
-            int ic = ce, it = tl;
-#pragma unroll
-            for (int s2 = 1; s2 < 64; s2 <<= 1) {
-                const int uc = __shfl_up(ic, s2), ut = __shfl_up(it, s2);
-                if (lane >= s2) { ic += uc; it += ut; }
-            }
-            if (ee < ne) { off_l[ee] = o + ic - ce; toff_l[ee] = to + it - tl; cnt_l[ee] = ce; }
-            o += __shfl(ic, 63);
-            to += __shfl(it, 63);
-        }
-        if (lane == 0) *a.ntiles = to;
-    }
-    __syncthreads();
-    if (act) {
-        int r = off_l[e];
-        for (int v = 0; v < part; v++) r += cnt[v * ne + e];
-        int t = t0;
-        for (; t + 8 <= t1; t += 8) {
-            uint8_t v[8];
-#pragma unroll
-            for (int u = 0; u < 8; u++) v[u] = M[(size_t)(t + u) * ne + e];
-#pragma unroll
-            for (int u = 0; u < 8; u++)
-                if (v[u]) a.sorted[r++] = (t + u) * k + v[u] - 1;
-        }
-        for (; t < t1; t++) {
-            const int sl = M[(size_t)t * ne + e];
-            if (sl) a.sorted[r++] = t * k + sl - 1;
-        }
-    }
-    for (int ee = w; ee < ne; ee += 16) {
-        const int ce = cnt_l[ee], ntl = (ce + 31) / 32;
-        for (int j = lane; j < ntl; j += 64) a.tiles[toff_l[ee] + j] = int4{ee, off_l[ee] + 32 * j, min(32, ce - 32 * j), 0};
     }
 }
 
@@ -847,10 +722,7 @@ int launch_grouped_layer(const GroupedArgs& a, bool trace, hipStream_t s, const 
     // one thread per kRouteC elements, whole waves (the decode route's element waves)
     launch(k_router_exact, dim3((a.ne + 7) / 8, (nt + 7) / 8), dim3(64), 0, s, a);
     launch(k_select_batch, dim3(nt), dim3(64), select_lds_bytes(a.ne, a.d, kExactGroupWide), s, a);
-    if ((size_t)a.n_tok * a.ne <= kGroupDenseMax)
-        launch(k_group_dense, dim3(1), dim3(1024), group_dense_lds(a.n_tok, a.ne), s, a);
-    else
-        launch(k_group, dim3(1), dim3(1024), 0, s, a);
+    launch(k_group_scan, dim3(1), dim3(1024), 0, s, a);
     if (a.kq) {
         if (launch_kq_gemms(a, trace, s, ev)) return -19;
         launch(k_combine_batch, dim3((unsigned)std::min<size_t>(((size_t)nt * (a.d / 4) + 255) / 256, 2048)), dim3(256), 0, s, a);
