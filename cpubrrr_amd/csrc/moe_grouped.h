@@ -37,7 +37,7 @@ struct GroupedArgs {
     int32_t* ids;              // [n_tok][k]
     float* wts;                // [n_tok][k]
     int32_t* fallback;         // [n_tok]
-    int32_t* sorted;           // [n_tok*k] pair ids (t*k + slot), grouped by expert, stable
+    int32_t* sorted;           // [n_tok*k] pair ids (t*k + slot), grouped by expert (any order within one)
     int4* tiles;               // [max_tiles] {expert, first sorted index, count, 0}
     int32_t* ntiles;           // [1]
     int8_t* hq;                // [n_tok*k][dff]
