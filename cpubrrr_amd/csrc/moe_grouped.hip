@@ -249,6 +249,8 @@ __global__ __launch_bounds__(64) void k_select_batch(GroupedArgs a) {
 // of the counts (pairs and 32-pair tiles), each pair written at its expert's
 // offset + its place, and the tile list.
 constexpr int kScanPer = 16;                   // pairs per thread held in registers
+// One workgroup; the caller's config check bounds n_expert <= 256 (the LDS
+// tables) and n_tok * k <= 16384 = kScanPer * 1024 (the pairs per thread).
 __global__ __launch_bounds__(1024) void k_group_scan(GroupedArgs a) {
     __shared__ int cnt_l[256], off_l[256], toff_l[256];
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
