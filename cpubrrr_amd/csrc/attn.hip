@@ -155,6 +155,13 @@ CPB_DEV void wave_sync_lds() {
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
+// workgroup barrier ordering LDS only: unlike __syncthreads, no wait for the
+// wave's outstanding global loads (the weight stream stays in flight)
+CPB_DEV void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
 
 // ---- staging of 8-row tiles into LDS ----
 // A workgroup copies the codes and scales of its consecutive tiles (at most
@@ -292,12 +299,13 @@ CPB_DEV float q8c_dot(const u32x4* lw, const float* ls, int nbp, const uint32_t*
 // zero padded so that whole 32-value groups can be read; the chain's one-group
 // look-ahead past the last row lands in red); red: 64 floats.
 CPB_DEV_HOST_INLINE int attn_xt_stride(int d) { return (d / 16 + 32 + 63) / 64 * 64 + 4; }   // = 4 (mod 64): distinct banks
-CPB_DEV void attn_norm_q8(const float4 (&xr)[4], const float4 (&wr)[4], int d, int nb, int nbp, float eps, float* xt,
+template <int KS>
+CPB_DEV void attn_norm_q8(const float4 (&xr)[KS], const float4 (&wr)[KS], int d, int nb, int nbp, float eps, float* xt,
                           float* red, uint32_t* xl, float* sl, int8_t* gxq, float* gxsb) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int n16 = d / 16, S = attn_xt_stride(d);
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
+    for (int k = 0; k < KS; k++) {
         const int i = tid + k * 256;
         if (i * 4 < d) {
             const float xv[4] = {xr[k].x, xr[k].y, xr[k].z, xr[k].w};
@@ -310,7 +318,7 @@ CPB_DEV void attn_norm_q8(const float4 (&xr)[4], const float4 (&wr)[4], int d, i
     }
     // zero padding past d / 16: fma(0, 0, acc) leaves acc (>= 0) unchanged
     for (int e = tid; e < 16 * (S - n16); e += 256) xt[(e & 15) * S + n16 + (e >> 4)] = 0.0f;
-    __syncthreads();
+    lds_barrier();
     if (tid < 64) {
         // lane q (mod 16) streams row q: the next group's reads are issued
         // before the current group's fmas
@@ -340,17 +348,17 @@ CPB_DEV void attn_norm_q8(const float4 (&xr)[4], const float4 (&wr)[4], int d, i
         const float sq = (L[0] + L[1]) + (L[2] + L[3]);
         if (lane == 0) red[16] = 1.0f / sqrtf(sq / (float)d + eps);
     }
-    __syncthreads();
+    lds_barrier();
     const float inv = red[16];
     // Q8 from registers: slot i = 4 elements, a 32-block = 8 consecutive slots
-    // (lanes).  The four slots of a thread are computed side by side (a slot
+    // (lanes).  The KS slots of a thread are computed side by side (a slot
     // past d holds x[0..3]: computed, not stored; d % 32 == 0 keeps a block's
     // eight slots all inside or all past d), one rarely taken branch for the
     // exact rounding path.
-    float v[4][4], sc[4], rs[4], r[4][4];
+    float v[KS][4], sc[KS], rs[KS], r[KS][4];
     bool near = false;
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
+    for (int k = 0; k < KS; k++) {
         v[k][0] = xr[k].x * inv * wr[k].x;
         v[k][1] = xr[k].y * inv * wr[k].y;
         v[k][2] = xr[k].z * inv * wr[k].z;
@@ -371,7 +379,7 @@ CPB_DEV void attn_norm_q8(const float4 (&xr)[4], const float4 (&wr)[4], int d, i
     if (near) {
         // the exact quotients of all 16 side by side (no branch per value)
 #pragma unroll
-        for (int k = 0; k < 4; k++)
+        for (int k = 0; k < KS; k++)
 #pragma unroll
             for (int u = 0; u < 4; u++) {
                 const float ex = roundf(v[k][u] / sc[k]);
@@ -379,7 +387,7 @@ CPB_DEV void attn_norm_q8(const float4 (&xr)[4], const float4 (&wr)[4], int d, i
             }
     }
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
+    for (int k = 0; k < KS; k++) {
         const int i = tid + k * 256;
         uint32_t wd = 0u;
 #pragma unroll
@@ -428,9 +436,12 @@ __global__ __launch_bounds__(256) void k_attn_qkv(AttnArgs a) {
     __shared__ float hv[kMaxTiles][8];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     // x and the norm weights first: the norm waits for them, not for the tiles
-    float4 xr[4], wr[4];
+    // x in float4 slots tid + 256k: 3 per thread cover d <= 3072 (every
+    // register-streamed shape: nbp = 92 blocks at most), 4 cover d <= 4096
+    constexpr int KS = NSP > 0 ? 3 : 4;
+    float4 xr[KS], wr[KS];
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
+    for (int k = 0; k < KS; k++) {
         const int i4 = (tid + k * 256) * 4 < a.d ? tid + k * 256 : 0;
         xr[k] = ((const float4*)a.x)[i4];
         wr[k] = ((const float4*)a.L.norm)[i4];
@@ -468,7 +479,9 @@ __global__ __launch_bounds__(256) void k_attn_qkv(AttnArgs a) {
         stage_issue(ts, g);
         const __amdgpu_buffer_rsrc_t rw =
             buf_rsrc(a.L.wq + (size_t)(t0 + (wave < nt ? wave : 0)) * NSP * 64, wave < nt ? (uint32_t)NSP * 64 * 16 : 0u);
-        // the first half before the norm, the rest once its registers are free
+        // half the codes before the norm, the rest after it (all of them up
+        // front, or the rest as soon as x has landed, delays x and the norm
+        // behind the other workgroups' streams: both measured slower)
         constexpr int kEarly = NSP / 2;
 #pragma unroll
         for (int sp = 0; sp < kEarly; sp++)
@@ -484,7 +497,7 @@ __global__ __launch_bounds__(256) void k_attn_qkv(AttnArgs a) {
         attn_norm_q8(xr, wr, a.d, a.nb, nbp, a.eps, xt, red, xl, sl, blockIdx.x == 0 ? a.xq : nullptr, a.xsb);
         stage_commit(ts, g, lw, ls);
     }
-    __syncthreads();
+    lds_barrier();
     if (wave >= nt) return;
     float v;
     if constexpr (NSP > 0) v = q8c_dot_regs<NSP>(wreg, ls + wave * ns * 16, xl, sl);
