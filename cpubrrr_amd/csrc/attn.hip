@@ -618,6 +618,36 @@ __global__ __launch_bounds__(512) void k_attn_core(AttnArgs a) {
             // = acc * (1 / den)
             float acc = 0.0f, d0 = expf(sink - m);
             int p = 0;
+            if (cnt == kAttnChunk) {
+                // a whole chunk: groups of 16 positions, the next group's LDS
+                // reads issued before this group's chain steps
+                float4 vv[2][4], ee[2][4];
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    vv[0][u] = *(const float4*)&vrow[4 * u];
+                    ee[0][u] = *(const float4*)&er[4 * u];
+                }
+#pragma unroll
+                for (int g = 0; g < kAttnChunk / 16; g++) {
+                    const int b = g & 1;
+                    if (g + 1 < kAttnChunk / 16) {
+#pragma unroll
+                        for (int u = 0; u < 4; u++) {
+                            vv[b ^ 1][u] = *(const float4*)&vrow[16 * (g + 1) + 4 * u];
+                            ee[b ^ 1][u] = *(const float4*)&er[16 * (g + 1) + 4 * u];
+                        }
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int u = 0; u < 4; u++) {
+                        const float4 v4 = vv[b][u], e4 = ee[b][u];
+                        acc = fmaf(v4.x, e4.x, acc); acc = fmaf(v4.y, e4.y, acc);
+                        acc = fmaf(v4.z, e4.z, acc); acc = fmaf(v4.w, e4.w, acc);
+                        d0 += e4.x; d0 += e4.y; d0 += e4.z; d0 += e4.w;
+                    }
+                }
+                p = kAttnChunk;
+            }
 #pragma unroll 4
             for (; p + 4 <= cnt; p += 4) {
                 const float4 vv = *(const float4*)&vrow[p];
@@ -636,6 +666,33 @@ __global__ __launch_bounds__(512) void k_attn_core(AttnArgs a) {
             // one chunk of several: 4 position chains, merged below with the sink
             float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
             int p = 0;
+            if (cnt == kAttnChunk) {
+                float4 vv[2][4], ee[2][4];
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    vv[0][u] = *(const float4*)&vrow[4 * u];
+                    ee[0][u] = *(const float4*)&er[4 * u];
+                }
+#pragma unroll
+                for (int g = 0; g < kAttnChunk / 16; g++) {
+                    const int b = g & 1;
+                    if (g + 1 < kAttnChunk / 16) {
+#pragma unroll
+                        for (int u = 0; u < 4; u++) {
+                            vv[b ^ 1][u] = *(const float4*)&vrow[16 * (g + 1) + 4 * u];
+                            ee[b ^ 1][u] = *(const float4*)&er[16 * (g + 1) + 4 * u];
+                        }
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int u = 0; u < 4; u++) {
+                        const float4 v4 = vv[b][u], e4 = ee[b][u];
+                        o[0] = fmaf(v4.x, e4.x, o[0]); o[1] = fmaf(v4.y, e4.y, o[1]);
+                        o[2] = fmaf(v4.z, e4.z, o[2]); o[3] = fmaf(v4.w, e4.w, o[3]);
+                    }
+                }
+                p = kAttnChunk;
+            }
 #pragma unroll 4
             for (; p + 4 <= cnt; p += 4) {
                 const float4 vv = *(const float4*)&vrow[p];
