@@ -556,7 +556,6 @@ __device__ __forceinline__ float score64(const float* kr, const float4 (&qv)[16]
 __global__ __launch_bounds__(512) void k_attn_core(AttnArgs a) {
     __shared__ __align__(16) float ks[kAttnChunk][68];
     __shared__ __align__(16) float vs[kAttnHd][kAttnChunk + 4];    // transposed: [dimension][position]
-    __shared__ __align__(16) float qs[kAttnMaxGroup][kAttnHd];
     __shared__ __align__(16) float es[kAttnMaxGroup][kAttnChunk];
     __shared__ int last;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -578,8 +577,6 @@ __global__ __launch_bounds__(512) void k_attn_core(AttnArgs a) {
             kr[it] = *(const float4*)(kb + pc * kAttnHd + c * 4);
             vr[it] = *(const float4*)(vb + pc * kAttnHd + c * 4);
         }
-        const float qv = a.q[kvh * R * kAttnHd + (tid < R * kAttnHd ? tid : 0)];
-        if (tid < R * kAttnHd) (&qs[0][0])[tid] = qv;
 #pragma unroll
         for (int it = 0; it < kIt; it++) {
             const int e = it * 512 + tid, p = e >> 4, c = e & 15;
@@ -596,9 +593,14 @@ __global__ __launch_bounds__(512) void k_attn_core(AttnArgs a) {
     float mv = 0.0f, sv = 0.0f, ov = 0.0f, den = 1.0f;
     if (live) {
         // scores of positions lane and lane + 64, softmax weights
+        // the head's q is uniform over the wave: scalar loads (constant
+        // address space: q is not written during this launch), used as the
+        // scalar operand of the score fmas, so the LDS serves only the K rows
+        typedef __attribute__((address_space(4))) const float cfloat;
+        cfloat* qc = (cfloat*)(a.q + (size_t)uniform(h) * kAttnHd);
         float4 qv[16];
 #pragma unroll
-        for (int i = 0; i < 16; i++) qv[i] = *(const float4*)&qs[wave][4 * i];
+        for (int i = 0; i < 16; i++) qv[i] = make_float4(qc[4 * i], qc[4 * i + 1], qc[4 * i + 2], qc[4 * i + 3]);
         const float s0 = lane < cnt ? score64(ks[lane], qv) : -INFINITY;
         const float s1 = lane + 64 < cnt ? score64(ks[lane + 64], qv) : -INFINITY;
         float m = wave_max_f32(fmaxf(s0, s1));
