@@ -565,6 +565,7 @@ __global__ __launch_bounds__(512) void k_attn_core(AttnArgs a) {
     const float* kb = a.kc + ((size_t)kvh * a.max_seq + p0) * kAttnHd;
     const float* vb = a.vc + ((size_t)kvh * a.max_seq + p0) * kAttnHd;
     constexpr int kIt = kAttnChunk * 16 / 512;
+    static_assert(kIt * 512 == kAttnChunk * 16, "every LDS row of the chunk is written");
     const bool live = wave < R;                       // wave w runs q-head w of the group
     const int h = kvh * R + (live ? wave : 0);
     const float sink = a.L.sinks[h];
@@ -573,20 +574,20 @@ __global__ __launch_bounds__(512) void k_attn_core(AttnArgs a) {
 #pragma unroll
         for (int it = 0; it < kIt; it++) {
             const int e = it * 512 + tid, p = e >> 4, c = e & 15;
-            const int pc = p < cnt ? p : 0;               // rows past the chunk: loaded, not stored
+            // rows past the chunk take row 0 (stored, never read): no branch
+            // around the stores, so the loads are not sunk into one each
+            const int pc = p < cnt ? p : 0;
             kr[it] = *(const float4*)(kb + pc * kAttnHd + c * 4);
             vr[it] = *(const float4*)(vb + pc * kAttnHd + c * 4);
         }
 #pragma unroll
         for (int it = 0; it < kIt; it++) {
             const int e = it * 512 + tid, p = e >> 4, c = e & 15;
-            if (p < cnt) {
-                *(float4*)&ks[p][c * 4] = kr[it];
-                vs[c * 4][p] = vr[it].x;
-                vs[c * 4 + 1][p] = vr[it].y;
-                vs[c * 4 + 2][p] = vr[it].z;
-                vs[c * 4 + 3][p] = vr[it].w;
-            }
+            *(float4*)&ks[p][c * 4] = kr[it];
+            vs[c * 4][p] = vr[it].x;
+            vs[c * 4 + 1][p] = vr[it].y;
+            vs[c * 4 + 2][p] = vr[it].z;
+            vs[c * 4 + 3][p] = vr[it].w;
         }
     }
     __syncthreads();
